@@ -1,0 +1,196 @@
+// C ABI of libdynconv.so (declared in include/dynconv.h).
+//
+// Every entry point validates its arguments on the host before touching the
+// HIP runtime and returns a dc_status; nothing here allocates, synchronises
+// or throws.  The only process-wide state is the once-initialised device
+// probe below.
+#include <mutex>
+
+#include "../../include/dynconv.h"
+#include "dc_launch.h"
+
+namespace {
+
+constexpr int64_t kI32Max = 2147483647;
+
+int device_status() {
+  static std::once_flag once;
+  static int status = DC_OK;
+  std::call_once(once, [] {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) status = DC_ERR_DEVICE;
+  });
+  return status;
+}
+
+bool dtype_ok(int dt) { return dt == DC_DTYPE_BF16 || dt == DC_DTYPE_FP16 || dt == DC_DTYPE_FP32; }
+
+bool aligned_to(const void* p, int a) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Shared size checks: positive, indexable with int32 rows/channels and int64
+// element offsets.
+int check_btd(int64_t B, int64_t T, int64_t D, int64_t W) {
+  if (B <= 0 || T <= 0 || D <= 0 || W <= 0) return DC_ERR_SHAPE;
+  if (T > kI32Max || D > kI32Max || B > kI32Max || B * T > kI32Max) return DC_ERR_SHAPE;
+  if (W > DC_MAX_W) return DC_ERR_UNSUPPORTED;
+  return DC_OK;
+}
+
+int check_headwise(int64_t B, int64_t T, int64_t D, int64_t H, int64_t W, int dtype) {
+  if (!dtype_ok(dtype)) return DC_ERR_DTYPE;
+  int s = check_btd(B, T, D, W);
+  if (s != DC_OK) return s;
+  if (H <= 0 || D % H != 0) return DC_ERR_SHAPE;
+  return DC_OK;
+}
+
+int check_lowrank(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, bool has_static) {
+  if (!dtype_ok(dtype)) return DC_ERR_DTYPE;
+  int s = check_btd(B, T, D, W);
+  if (s != DC_OK) return s;
+  if (R <= 0) return DC_ERR_SHAPE;
+  if (R + (has_static ? 1 : 0) > DC_MAX_R) return DC_ERR_UNSUPPORTED;
+  if (W * D > kI32Max) return DC_ERR_SHAPE;
+  return DC_OK;
+}
+
+int launch_status(hipError_t e) { return e == hipSuccess ? DC_OK : DC_ERR_LAUNCH; }
+
+}  // namespace
+
+extern "C" {
+
+int dc_abi_version(void) { return DC_ABI_VERSION; }
+
+const char* dc_status_string(int status) {
+  switch (status) {
+    case DC_OK: return "ok";
+    case DC_ERR_NULL: return "a required pointer is NULL (or static_w/dstatic_w disagree)";
+    case DC_ERR_SHAPE: return "invalid shape (non-positive size, D % H != 0, or size too large)";
+    case DC_ERR_DTYPE: return "unsupported dtype";
+    case DC_ERR_UNSUPPORTED: return "unsupported configuration (W or rank above the library maximum)";
+    case DC_ERR_WORKSPACE: return "workspace missing or smaller than the size query";
+    case DC_ERR_ALIGN: return "pointer not aligned to its element size";
+    case DC_ERR_DEVICE: return "no HIP device available";
+    case DC_ERR_LAUNCH: return "kernel launch failed";
+    default: return "unknown dynconv status";
+  }
+}
+
+int dc_headwise_fwd(const void* x, const void* weight, const void* static_w, void* y, int64_t B, int64_t T,
+                    int64_t D, int64_t H, int64_t W, int dtype, int residual, void* stream) {
+  int s = check_headwise(B, T, D, H, W, dtype);
+  if (s != DC_OK) return s;
+  if (!x || !weight || !y) return DC_ERR_NULL;
+  const int es = dc::dtype_size(dtype);
+  if (!aligned_to(x, es) || !aligned_to(weight, es) || !aligned_to(static_w, es) || !aligned_to(y, es))
+    return DC_ERR_ALIGN;
+  if ((s = device_status()) != DC_OK) return s;
+  dc::HwProblem p{};
+  p.x = x; p.weight = weight; p.static_w = static_w; p.y = y;
+  p.B = B; p.T = T; p.D = D; p.H = H; p.W = W;
+  p.dtype = dtype; p.residual = residual ? 1 : 0; p.stream = (hipStream_t)stream;
+  return launch_status(dc::hw_fwd(p));
+}
+
+int64_t dc_headwise_bwd_ws_bytes(int64_t B, int64_t T, int64_t D, int64_t H, int64_t W, int dtype,
+                                 int has_static) {
+  int s = check_headwise(B, T, D, H, W, dtype);
+  if (s != DC_OK) return s;
+  // The fast path needs 16-byte aligned tensors; size for it whenever the
+  // shape allows it (torch allocations are 256-byte aligned).  A generic-path
+  // call never needs more than the fast path's count.
+  static const char kAligned[16] __attribute__((aligned(256))) = {0};
+  dc::HwProblem p{};
+  p.x = p.weight = p.dy = kAligned;
+  p.dx = p.dweight = p.y = (void*)kAligned;
+  p.static_w = has_static ? kAligned : nullptr;
+  p.B = B; p.T = T; p.D = D; p.H = H; p.W = W; p.dtype = dtype;
+  int64_t fast = dc::hw_bwd_ws_bytes(p);
+  p.x = kAligned + 2;  // force the generic sizing, take the larger of the two
+  int64_t gen = dc::hw_bwd_ws_bytes(p);
+  return fast > gen ? fast : gen;
+}
+
+int dc_headwise_bwd(const void* x, const void* weight, const void* static_w, const void* dy, void* dx,
+                    void* dweight, void* dstatic_w, void* workspace, int64_t ws_bytes, int64_t B, int64_t T,
+                    int64_t D, int64_t H, int64_t W, int dtype, int residual, void* stream) {
+  int s = check_headwise(B, T, D, H, W, dtype);
+  if (s != DC_OK) return s;
+  if (!x || !weight || !dy || !dx || !dweight) return DC_ERR_NULL;
+  if ((static_w == nullptr) != (dstatic_w == nullptr)) return DC_ERR_NULL;
+  const int es = dc::dtype_size(dtype);
+  if (!aligned_to(x, es) || !aligned_to(weight, es) || !aligned_to(static_w, es) || !aligned_to(dy, es) ||
+      !aligned_to(dx, es) || !aligned_to(dweight, es) || !aligned_to(dstatic_w, es))
+    return DC_ERR_ALIGN;
+  const int64_t need = dc_headwise_bwd_ws_bytes(B, T, D, H, W, dtype, static_w != nullptr);
+  if (need < 0) return (int)need;
+  if (need > 0 && (workspace == nullptr || ws_bytes < need || !aligned_to(workspace, 4))) return DC_ERR_WORKSPACE;
+  if ((s = device_status()) != DC_OK) return s;
+  dc::HwProblem p{};
+  p.x = x; p.weight = weight; p.static_w = static_w; p.dy = dy;
+  p.dx = dx; p.dweight = dweight; p.dstatic_w = dstatic_w; p.ws = (float*)workspace;
+  p.B = B; p.T = T; p.D = D; p.H = H; p.W = W;
+  p.dtype = dtype; p.residual = residual ? 1 : 0; p.stream = (hipStream_t)stream;
+  return launch_status(dc::hw_bwd(p));
+}
+
+int dc_lowrank_fwd(const void* x, const void* z, const void* U, const void* static_w, void* y, int64_t B,
+                   int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int residual, void* stream) {
+  int s = check_lowrank(B, T, D, R, W, dtype, static_w != nullptr);
+  if (s != DC_OK) return s;
+  if (!x || !z || !U || !y) return DC_ERR_NULL;
+  const int es = dc::dtype_size(dtype);
+  if (!aligned_to(x, es) || !aligned_to(z, es) || !aligned_to(U, es) || !aligned_to(static_w, es) ||
+      !aligned_to(y, es))
+    return DC_ERR_ALIGN;
+  if ((s = device_status()) != DC_OK) return s;
+  dc::LrProblem p{};
+  p.x = x; p.z = z; p.U = U; p.static_w = static_w; p.y = y;
+  p.B = B; p.T = T; p.D = D; p.R = R; p.W = W;
+  p.dtype = dtype; p.residual = residual ? 1 : 0; p.stream = (hipStream_t)stream;
+  return launch_status(dc::lr_fwd(p));
+}
+
+int64_t dc_lowrank_bwd_ws_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype,
+                                int has_static) {
+  int s = check_lowrank(B, T, D, R, W, dtype, has_static != 0);
+  if (s != DC_OK) return s;
+  static const char kAligned[16] __attribute__((aligned(256))) = {0};
+  dc::LrProblem p{};
+  p.x = p.z = p.U = p.dy = kAligned;
+  p.y = p.dx = p.dz = p.dU = (void*)kAligned;
+  p.static_w = has_static ? kAligned : nullptr;
+  p.dstatic_w = has_static ? (void*)kAligned : nullptr;
+  p.B = B; p.T = T; p.D = D; p.R = R; p.W = W; p.dtype = dtype;
+  int64_t fast = dc::lr_bwd_ws_bytes(p);
+  p.x = kAligned + 2;
+  int64_t gen = dc::lr_bwd_ws_bytes(p);
+  return fast > gen ? fast : gen;
+}
+
+int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* static_w, const void* dy, void* dx,
+                   void* dz, void* dU, void* dstatic_w, void* workspace, int64_t ws_bytes, int64_t B, int64_t T,
+                   int64_t D, int64_t R, int64_t W, int dtype, int residual, void* stream) {
+  int s = check_lowrank(B, T, D, R, W, dtype, static_w != nullptr);
+  if (s != DC_OK) return s;
+  if (!x || !z || !U || !dy || !dx || !dz || !dU) return DC_ERR_NULL;
+  if ((static_w == nullptr) != (dstatic_w == nullptr)) return DC_ERR_NULL;
+  const int es = dc::dtype_size(dtype);
+  if (!aligned_to(x, es) || !aligned_to(z, es) || !aligned_to(U, es) || !aligned_to(static_w, es) ||
+      !aligned_to(dy, es) || !aligned_to(dx, es) || !aligned_to(dz, es) || !aligned_to(dU, es) ||
+      !aligned_to(dstatic_w, es))
+    return DC_ERR_ALIGN;
+  const int64_t need = dc_lowrank_bwd_ws_bytes(B, T, D, R, W, dtype, static_w != nullptr);
+  if (need < 0) return (int)need;
+  if (need > 0 && (workspace == nullptr || ws_bytes < need || !aligned_to(workspace, 4))) return DC_ERR_WORKSPACE;
+  if ((s = device_status()) != DC_OK) return s;
+  dc::LrProblem p{};
+  p.x = x; p.z = z; p.U = U; p.static_w = static_w; p.dy = dy;
+  p.dx = dx; p.dz = dz; p.dU = dU; p.dstatic_w = dstatic_w; p.ws = (float*)workspace;
+  p.B = B; p.T = T; p.D = D; p.R = R; p.W = W;
+  p.dtype = dtype; p.residual = residual ? 1 : 0; p.stream = (hipStream_t)stream;
+  return launch_status(dc::lr_bwd(p));
+}
+
+}  // extern "C"

@@ -1,0 +1,68 @@
+// Internal host-side launch interface between the C ABI (capi.cpp) and the
+// kernel translation units.  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dc {
+
+enum DType { kBF16 = 0, kFP16 = 1, kFP32 = 2 };
+
+inline int dtype_size(int dt) { return dt == kFP32 ? 4 : 2; }
+
+// ---------------------------------------------------------------- headwise
+struct HwProblem {
+  const void* x;
+  const void* weight;
+  const void* static_w;  // may be null
+  const void* dy;        // bwd only
+  void* y;               // fwd output
+  void* dx;
+  void* dweight;
+  void* dstatic_w;       // may be null
+  float* ws;             // bwd partials (may be null when no static filter)
+  int64_t B, T, D, H, W;
+  int dtype;
+  int residual;
+  hipStream_t stream;
+};
+
+// Shape/alignment test for the vectorised kernels.  Pure host logic.
+bool hw_fast_ok(const HwProblem& p, bool bwd);
+// Bytes of fp32 partials the backward needs (0 without a static filter).
+int64_t hw_bwd_ws_bytes(const HwProblem& p);
+hipError_t hw_fwd(const HwProblem& p);
+hipError_t hw_bwd(const HwProblem& p);
+
+// ----------------------------------------------------------------- lowrank
+struct LrProblem {
+  const void* x;
+  const void* z;
+  const void* U;
+  const void* static_w;  // may be null: then the kernel rank is R, else R + 1
+  const void* dy;
+  void* y;
+  void* dx;
+  void* dz;
+  void* dU;
+  void* dstatic_w;
+  float* ws;
+  int64_t B, T, D, R, W;  // R = dynamic rank (z.shape[-1])
+  int dtype;
+  int residual;
+  hipStream_t stream;
+};
+
+bool lr_mfma_ok(const LrProblem& p, bool bwd);
+int64_t lr_bwd_ws_bytes(const LrProblem& p);
+hipError_t lr_fwd(const LrProblem& p);
+hipError_t lr_bwd(const LrProblem& p);
+
+// ------------------------------------------------------------------ shared
+// out[c] = (T) sum_{p < P} part[p * pstride + c] for c < C, summed in a fixed
+// order (deterministic).
+hipError_t reduce_partials(const float* part, int64_t pstride, int P, int64_t C, void* out, int dtype,
+                           hipStream_t stream);
+
+}  // namespace dc

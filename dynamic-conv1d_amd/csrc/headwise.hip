@@ -1,0 +1,256 @@
+// Headwise dynamic causal short convolution: host planning, generic kernels.
+//
+// The vectorised kernels live in headwise_fast.h and are instantiated per
+// (dtype, direction) in headwise_fast_*.hip so they compile in parallel.
+#include "headwise_fast.h"
+
+namespace dc {
+
+extern template hipError_t dispatch_fast<bf16, false>(const HwProblem&, const HwPlan&);
+extern template hipError_t dispatch_fast<bf16, true>(const HwProblem&, const HwPlan&);
+extern template hipError_t dispatch_fast<fp16, false>(const HwProblem&, const HwPlan&);
+extern template hipError_t dispatch_fast<fp16, true>(const HwProblem&, const HwPlan&);
+extern template hipError_t dispatch_fast<float, false>(const HwProblem&, const HwPlan&);
+extern template hipError_t dispatch_fast<float, true>(const HwProblem&, const HwPlan&);
+
+// ------------------------------------------------------------ generic path
+// Any D, any head size dividing D, any W <= DC_MAX_W, element alignment only.
+// One thread per output element; used for shapes the vector path rejects and
+// as an independent second implementation in the tests.
+template <typename T>
+__global__ __launch_bounds__(256) void hw_fwd_generic(const T* __restrict__ x, const T* __restrict__ wt,
+                                                      const T* __restrict__ sw, T* __restrict__ y, int64_t BT,
+                                                      int Tn, int D, int H, int hs, int W, int residual) {
+  const int64_t n = BT * D;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = i / D;
+    const int d = (int)(i - row * D);
+    const int t = (int)(row % Tn);
+    const int h = d / hs;
+    float acc = 0.f;
+    for (int k = 0; k < W && k <= t; ++k) {
+      float tap = (float)wt[(row * H + h) * W + k];
+      if (sw) tap += (float)sw[(int64_t)k * D + d];
+      acc = fmaf(tap, (float)x[(row - k) * D + d], acc);
+    }
+    if (residual) acc += (float)x[i];
+    y[i] = (T)acc;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void hw_bwd_dx_generic(const T* __restrict__ wt, const T* __restrict__ sw,
+                                                         const T* __restrict__ dy, T* __restrict__ dx,
+                                                         int64_t BT, int Tn, int D, int H, int hs, int W,
+                                                         int residual) {
+  const int64_t n = BT * D;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = i / D;
+    const int d = (int)(i - row * D);
+    const int t = (int)(row % Tn);
+    const int h = d / hs;
+    float acc = 0.f;
+    for (int k = 0; k < W && t + k < Tn; ++k) {
+      float tap = (float)wt[((row + k) * H + h) * W + k];
+      if (sw) tap += (float)sw[(int64_t)k * D + d];
+      acc = fmaf((float)dy[(row + k) * D + d], tap, acc);
+    }
+    if (residual) acc += (float)dy[i];
+    dx[i] = (T)acc;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void hw_bwd_dw_generic(const T* __restrict__ x, const T* __restrict__ dy,
+                                                         T* __restrict__ dwt, int64_t BT, int Tn, int D, int H,
+                                                         int hs, int W) {
+  const int64_t n = BT * H;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = i / H;
+    const int h = (int)(i - row * H);
+    const int t = (int)(row % Tn);
+    for (int k = 0; k < W; ++k) {
+      float acc = 0.f;
+      if (k <= t) {
+        const T* dyr = dy + row * D + (int64_t)h * hs;
+        const T* xr = x + (row - k) * D + (int64_t)h * hs;
+        for (int c = 0; c < hs; ++c) acc = fmaf((float)dyr[c], (float)xr[c], acc);
+      }
+      dwt[i * W + k] = (T)acc;
+    }
+  }
+}
+
+// dstatic partials: grid (ceil(W*D/256), P); partial p covers rows
+// [p*rows_per, (p+1)*rows_per) of the flattened B*T axis.
+template <typename T>
+__global__ __launch_bounds__(256) void hw_bwd_dsw_generic(const T* __restrict__ x, const T* __restrict__ dy,
+                                                          float* __restrict__ part, int64_t BT, int Tn, int D,
+                                                          int W, int64_t rows_per) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= (int64_t)W * D) return;
+  const int k = (int)(c / D);
+  const int d = (int)(c - (int64_t)k * D);
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per;
+  const int64_t r1 = min(r0 + rows_per, BT);
+  float acc = 0.f;
+  for (int64_t row = r0; row < r1; ++row) {
+    const int t = (int)(row % Tn);
+    if (t >= k) acc = fmaf((float)dy[row * D + d], (float)x[(row - k) * D + d], acc);
+  }
+  part[(int64_t)blockIdx.y * W * D + c] = acc;
+}
+
+// --------------------------------------------------------------- host side
+namespace {
+
+constexpr int kMaxFastW = 8;
+
+int ilog2(int64_t v) {
+  int r = 0;
+  while ((int64_t(1) << r) < v) ++r;
+  return r;
+}
+
+int unroll_of(int W) { return W >= 4 ? W : W * (4 / W); }
+
+bool aligned(const void* p, int a) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Run length: aim for ~8 wavefronts per CU over 256 CUs (2048), at least one
+// unrolled chunk, a multiple of the unroll.
+int choose_seg(int64_t B, int64_t T, int64_t nvg, int W, int target_waves) {
+  const int u = unroll_of(W);
+  int64_t seg = (B * T * nvg + target_waves - 1) / target_waves;
+  if (seg < 16) seg = 16;
+  seg = (seg + u - 1) / u * u;
+  if (seg > T) seg = (T + u - 1) / u * u;
+  return (int)seg;
+}
+
+HwPlan make_plan(const HwProblem& p, bool bwd) {
+  const int VEC = 16 / dtype_size(p.dtype);
+  const int64_t hs = p.D / p.H;
+  HwPlan pl;
+  HwArgs& a = pl.a;
+  a.Tn = (int)p.T;
+  a.D = (int)p.D;
+  a.H = (int)p.H;
+  a.hs_shift = ilog2(hs);
+  a.nvc = (int)(p.D / VEC);
+  a.nvg = (a.nvc + 63) / 64;
+  a.seg = choose_seg(p.B, p.T, a.nvg, (int)p.W, bwd ? 2048 : 4096);
+  a.nspb = (int)((p.T + a.seg - 1) / a.seg);
+  a.nseg = (int)(p.B * a.nspb);
+  const int nsg = (a.nseg + 3) / 4;
+  a.nblk = nsg * a.nvg;
+  a.lph = hs > VEC ? (int)(hs / VEC) : 1;
+  a.residual = p.residual;
+  a.has_static = p.static_w != nullptr;
+  pl.nblk = a.nblk;
+  pl.P = nsg;
+  return pl;
+}
+
+unsigned generic_grid(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  if (g > 65536) g = 65536;
+  return (unsigned)(g < 1 ? 1 : g);
+}
+
+template <typename T>
+hipError_t fwd_generic(const HwProblem& p) {
+  const int64_t BT = p.B * p.T;
+  hw_fwd_generic<T><<<generic_grid(BT * p.D), 256, 0, p.stream>>>(
+      (const T*)p.x, (const T*)p.weight, (const T*)p.static_w, (T*)p.y, BT, (int)p.T, (int)p.D, (int)p.H,
+      (int)(p.D / p.H), (int)p.W, p.residual);
+  return hipGetLastError();
+}
+
+int generic_partials(int64_t BT) {
+  int64_t P = (BT + 255) / 256;
+  return (int)(P > 64 ? 64 : (P < 1 ? 1 : P));
+}
+
+template <typename T>
+hipError_t bwd_generic(const HwProblem& p) {
+  const int64_t BT = p.B * p.T;
+  const int hs = (int)(p.D / p.H);
+  hw_bwd_dx_generic<T><<<generic_grid(BT * p.D), 256, 0, p.stream>>>(
+      (const T*)p.weight, (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, BT, (int)p.T, (int)p.D, (int)p.H, hs,
+      (int)p.W, p.residual);
+  hw_bwd_dw_generic<T><<<generic_grid(BT * p.H), 256, 0, p.stream>>>(
+      (const T*)p.x, (const T*)p.dy, (T*)p.dweight, BT, (int)p.T, (int)p.D, (int)p.H, hs, (int)p.W);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !p.static_w) return e;
+  const int P = generic_partials(BT);
+  const int64_t rows_per = (BT + P - 1) / P;
+  dim3 grid((unsigned)((p.W * p.D + 255) / 256), (unsigned)P);
+  hw_bwd_dsw_generic<T><<<grid, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.dy, p.ws, BT, (int)p.T, (int)p.D,
+                                                    (int)p.W, rows_per);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return reduce_partials(p.ws, p.W * p.D, P, p.W * p.D, p.dstatic_w, p.dtype, p.stream);
+}
+
+}  // namespace
+
+bool hw_fast_ok(const HwProblem& p, bool bwd) {
+  const int es = dtype_size(p.dtype);
+  const int VEC = 16 / es;
+  const int64_t hs = p.D / p.H;
+  if (p.W < 1 || p.W > kMaxFastW) return false;
+  if (p.D % VEC != 0) return false;
+  if ((hs & (hs - 1)) != 0) return false;  // power-of-two head size
+  if (hs > 64 * VEC) return false;         // a head must fit in one wavefront
+  if (!aligned(p.x, 16) || !aligned(p.static_w, 16)) return false;
+  // weight rows start at multiples of NHL*W elements; require that alignment.
+  const int64_t nwe_bytes = (hs < VEC ? VEC / hs : 1) * p.W * es;
+  const int wa = (nwe_bytes % 16 == 0) ? 16 : (nwe_bytes % 8 == 0) ? 8 : (nwe_bytes % 4 == 0) ? 4 : 2;
+  if (!aligned(p.weight, wa)) return false;
+  if (!bwd) return aligned(p.y, 16);
+  return aligned(p.dy, 16) && aligned(p.dx, 16) && aligned(p.dweight, wa);
+}
+
+int64_t hw_bwd_ws_bytes(const HwProblem& p) {
+  if (!p.static_w) return 0;
+  int P;
+  if (hw_fast_ok(p, true))
+    P = make_plan(p, true).P;
+  else
+    P = generic_partials(p.B * p.T);
+  return (int64_t)P * p.W * p.D * (int64_t)sizeof(float);
+}
+
+hipError_t hw_fwd(const HwProblem& p) {
+  if (hw_fast_ok(p, false)) {
+    const HwPlan pl = make_plan(p, false);
+    switch (p.dtype) {
+      case kBF16: return dispatch_fast<bf16, false>(p, pl);
+      case kFP16: return dispatch_fast<fp16, false>(p, pl);
+      default: return dispatch_fast<float, false>(p, pl);
+    }
+  }
+  switch (p.dtype) {
+    case kBF16: return fwd_generic<bf16>(p);
+    case kFP16: return fwd_generic<fp16>(p);
+    default: return fwd_generic<float>(p);
+  }
+}
+
+hipError_t hw_bwd(const HwProblem& p) {
+  if (hw_fast_ok(p, true)) {
+    const HwPlan pl = make_plan(p, true);
+    switch (p.dtype) {
+      case kBF16: return dispatch_fast<bf16, true>(p, pl);
+      case kFP16: return dispatch_fast<fp16, true>(p, pl);
+      default: return dispatch_fast<float, true>(p, pl);
+    }
+  }
+  switch (p.dtype) {
+    case kBF16: return bwd_generic<bf16>(p);
+    case kFP16: return bwd_generic<fp16>(p);
+    default: return bwd_generic<float>(p);
+  }
+}
+
+}  // namespace dc

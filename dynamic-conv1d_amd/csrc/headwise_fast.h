@@ -1,0 +1,366 @@
+// Headwise dynamic causal short convolution, forward and backward, for gfx950.
+//
+//   y[b,t,d] = sum_{k<W} (w[b,t,d/hs,k] + sw[k,d]) * x[b,t-k,d]  (+ x[b,t,d])
+//
+// Reference kernels: headwise.py:24-91 (causal_conv1d_fwd_kernel) and
+// headwise.py:105-215 (causal_conv1d_bwd_kernel).
+//
+// Design (fast path).  The convolution is depthwise: a channel's window never
+// mixes with another channel's, so the W-1 row halo of a channel lives in the
+// registers of the lane that owns it.  A lane owns VEC = 16/sizeof(T)
+// channels (one 128-bit load per row) and walks a run of `seg` consecutive
+// rows of one sequence, keeping the last W rows of x (forward) or the W open
+// dx accumulators (backward) in a register ring whose slot for row t is
+// (t - t0) mod W.  The row loop is unrolled by a multiple of W so every ring
+// index is a compile-time constant.  Each row costs exactly one 128-bit load
+// of x (and dy), one contiguous load of the lane's NHL*W weights, and one
+// 128-bit store: the HBM traffic is the algorithmic traffic plus a W-1 row
+// halo per run.  64 lanes of a wavefront cover 64*VEC consecutive channels
+// (a 1 KiB contiguous row segment per load instruction); a 256-thread
+// workgroup stacks 4 wavefronts on 4 consecutive runs of the same channels,
+// so a run's halo rows were just read by the wavefront above it.
+//
+// Backward.  dx uses the scatter form: the row-t terms dy[t]*(w[t,k]+sw[k])
+// are added into the open accumulator of row t-k; row t-W+1 is complete
+// after step t and is stored.  dweight sums dy[t]*x[t-k] over the head's
+// channels: in-lane when head_size <= VEC, then a butterfly over the
+// head_size/VEC lanes of the head.  dstatic_w partial sums stay in registers
+// for the whole run, are added across the 4 wavefronts of the workgroup in
+// LDS in a fixed order, and one fp32 partial per workgroup is summed by
+// reduce_partials (no atomics: bitwise deterministic).
+#pragma once
+
+#include "dc_common.h"
+#include "dc_launch.h"
+
+namespace dc {
+
+template <typename T> struct VecOf { static constexpr int value = 16 / (int)sizeof(T); };
+
+struct HwArgs {
+  int Tn;        // sequence length
+  int D;         // channels
+  int H;         // heads
+  int hs_shift;  // log2(head_size)
+  int nvc;       // D / VEC lane columns
+  int nvg;       // ceil(nvc / 64) wavefront column groups
+  int seg;       // rows per run
+  int nspb;      // runs per sequence = ceil(T / seg)
+  int nseg;      // B * nspb
+  int nblk;      // grid size
+  int lph;       // lanes per head (head_size / VEC when > 1, else 1)
+  int residual;
+  int has_static;
+};
+
+// Rows per unrolled chunk: a multiple of W, at least 4.
+template <int W> struct Unroll { static constexpr int value = (W >= 4) ? W : W * (4 / W); };
+
+template <int W>
+__device__ __forceinline__ constexpr int ring(int u, int k) {
+  return ((u - k) % W + W) % W;
+}
+
+// ------------------------------------------------------------------ forward
+template <typename T, int W, int HSV, int U, bool GUARD>
+__device__ __forceinline__ void hw_fwd_rows(int tc, int t1, const T* __restrict__ xp, const T* __restrict__ wp,
+                                            T* __restrict__ yp, int64_t D, int64_t wrs,
+                                            float (&xr)[W][VecOf<T>::value],
+                                            const float (&swf)[W][VecOf<T>::value], int residual) {
+  constexpr int VEC = VecOf<T>::value;
+  constexpr int NWE = (VEC / HSV) * W;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int t = tc + u;
+    if (GUARD && t >= t1) break;
+    const int p = u % W;
+    load_vals<T, VEC>(xp + (int64_t)t * D, xr[p]);
+    float wv[NWE];
+    load_vals<T, NWE>(wp + (int64_t)t * wrs, wv);
+    float acc[VEC];
+    zero_vals<VEC>(acc);
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const int q = ring<W>(u, k);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) acc[j] = fmaf(wv[(j / HSV) * W + k] + swf[k][j], xr[q][j], acc[j]);
+    }
+    if (residual) {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) acc[j] += xr[p][j];
+    }
+    store_vals<T, VEC>(yp + (int64_t)t * D, acc);
+  }
+}
+
+template <typename T, int W, int HSV>
+__global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, const T* __restrict__ wt,
+                                                   const T* __restrict__ sw, T* __restrict__ y, HwArgs a) {
+  constexpr int VEC = VecOf<T>::value;
+  constexpr int U = Unroll<W>::value;
+  const int lb = xcd_remap(blockIdx.x, a.nblk);
+  const int vg = lb % a.nvg, sgp = lb / a.nvg;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int vc = vg * 64 + lane;
+  const int s = sgp * 4 + wave;
+  if (s >= a.nseg || vc >= a.nvc) return;
+  const int b = s / a.nspb;
+  const int t0 = (s - b * a.nspb) * a.seg;
+  const int t1 = min(t0 + a.seg, a.Tn);
+  const int d0 = vc * VEC;
+  const int h0 = d0 >> a.hs_shift;
+  const int64_t row0 = (int64_t)b * a.Tn;
+  const int64_t D = a.D;
+  const int64_t wrs = (int64_t)a.H * W;
+  const T* xp = x + row0 * D + d0;
+  const T* wp = wt + (row0 * a.H + h0) * W;
+  T* yp = y + row0 * D + d0;
+
+  float swf[W][VEC];
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+    if (a.has_static)
+      load_vals<T, VEC>(sw + (int64_t)k * D + d0, swf[k]);
+    else
+      zero_vals<VEC>(swf[k]);
+  }
+  float xr[W][VEC];
+  zero_vals<VEC>(xr[0]);
+#pragma unroll
+  for (int i = 1; i < W; ++i) {
+    const int t = t0 - i;
+    if (t >= 0)
+      load_vals<T, VEC>(xp + (int64_t)t * D, xr[W - i]);
+    else
+      zero_vals<VEC>(xr[W - i]);
+  }
+  for (int tc = t0; tc < t1; tc += U) {
+    if (tc + U <= t1)
+      hw_fwd_rows<T, W, HSV, U, false>(tc, t1, xp, wp, yp, D, wrs, xr, swf, a.residual);
+    else
+      hw_fwd_rows<T, W, HSV, U, true>(tc, t1, xp, wp, yp, D, wrs, xr, swf, a.residual);
+  }
+}
+
+// ----------------------------------------------------------------- backward
+template <typename T, int W, int HSV, bool HAS_STATIC, int U, bool GUARD>
+__device__ __forceinline__ void hw_bwd_rows(int tc, int tend, int t0, int t1, int Tn, const T* __restrict__ xp,
+                                            const T* __restrict__ wp, const T* __restrict__ dyp,
+                                            T* __restrict__ dxp, T* __restrict__ dwp, int64_t D, int64_t wrs,
+                                            float (&xr)[W][VecOf<T>::value],
+                                            float (&dxa)[W][VecOf<T>::value],
+                                            float (&dsw)[W][VecOf<T>::value],
+                                            const float (&swf)[W][VecOf<T>::value], int residual, int lph,
+                                            bool leader) {
+  constexpr int VEC = VecOf<T>::value;
+  constexpr int NHL = VEC / HSV;
+  constexpr int NWE = NHL * W;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int t = tc + u;
+    if (GUARD && t >= tend) break;
+    const int p = u % W;
+    const bool main_row = t < t1;
+    float dyv[VEC], wv[NWE];
+    if (t < Tn) {
+      load_vals<T, VEC>(dyp + (int64_t)t * D, dyv);
+      load_vals<T, NWE>(wp + (int64_t)t * wrs, wv);
+    } else {
+      zero_vals<VEC>(dyv);
+      zero_vals<NWE>(wv);
+    }
+    if (main_row) load_vals<T, VEC>(xp + (int64_t)t * D, xr[p]);
+
+    // dx[t-k] += dy[t] * (w[t, h, k] + sw[k]); row t opens with its k = 0 term.
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const float v = dyv[j] * (wv[(j / HSV) * W] + swf[0][j]);
+      dxa[p][j] = residual ? v + dyv[j] : v;
+    }
+#pragma unroll
+    for (int k = 1; k < W; ++k) {
+      const int q = ring<W>(u, k);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) dxa[q][j] = fmaf(dyv[j], wv[(j / HSV) * W + k] + swf[k][j], dxa[q][j]);
+    }
+
+    if (main_row) {
+      float dwv[NWE];
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        const int q = ring<W>(u, k);
+        float pr[VEC];
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) pr[j] = dyv[j] * xr[q][j];
+        if (HAS_STATIC) {
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) dsw[k][j] += pr[j];
+        }
+#pragma unroll
+        for (int hh = 0; hh < NHL; ++hh) {
+          float sacc = 0.f;
+#pragma unroll
+          for (int j = 0; j < HSV; ++j) sacc += pr[hh * HSV + j];
+          dwv[hh * W + k] = sacc;
+        }
+      }
+      if (lph > 1) {
+#pragma unroll
+        for (int k = 0; k < NWE; ++k) dwv[k] = group_sum(dwv[k], lph);
+      }
+      if (leader) store_vals<T, NWE>(dwp + (int64_t)t * wrs, dwv);
+    }
+
+    const int tdone = t - (W - 1);
+    if (tdone >= t0 && tdone < t1) store_vals<T, VEC>(dxp + (int64_t)tdone * D, dxa[(u + 1) % W]);
+  }
+}
+
+template <typename T, int W, int HSV, bool HAS_STATIC>
+__global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, const T* __restrict__ wt,
+                                                   const T* __restrict__ sw, const T* __restrict__ dy,
+                                                   T* __restrict__ dx, T* __restrict__ dwt,
+                                                   float* __restrict__ part, HwArgs a) {
+  constexpr int VEC = VecOf<T>::value;
+  constexpr int U = Unroll<W>::value;
+  const int lb = xcd_remap(blockIdx.x, a.nblk);
+  const int vg = lb % a.nvg, sgp = lb / a.nvg;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int vc = vg * 64 + lane;
+  const int s = sgp * 4 + wave;
+  const bool active = (s < a.nseg) && (vc < a.nvc);
+
+  float dsw[W][VEC];
+#pragma unroll
+  for (int k = 0; k < W; ++k) zero_vals<VEC>(dsw[k]);
+
+  // Lanes of a head are aligned groups of `lph` consecutive columns and a
+  // wavefront of one run holds whole heads, so every lane of a group shares
+  // `active`; inactive lanes never take part in a shuffle.
+  if (active) {
+    const int b = s / a.nspb;
+    const int t0 = (s - b * a.nspb) * a.seg;
+    const int t1 = min(t0 + a.seg, a.Tn);
+    const int d0 = vc * VEC;
+    const int h0 = d0 >> a.hs_shift;
+    const int64_t row0 = (int64_t)b * a.Tn;
+    const int64_t D = a.D;
+    const int64_t wrs = (int64_t)a.H * W;
+    const T* xp = x + row0 * D + d0;
+    const T* wp = wt + (row0 * a.H + h0) * W;
+    const T* dyp = dy + row0 * D + d0;
+    T* dxp = dx + row0 * D + d0;
+    T* dwp = dwt + (row0 * a.H + h0) * W;
+    const bool leader = (vc & (a.lph - 1)) == 0;
+
+    float swf[W][VEC];
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      if (HAS_STATIC)
+        load_vals<T, VEC>(sw + (int64_t)k * D + d0, swf[k]);
+      else
+        zero_vals<VEC>(swf[k]);
+    }
+    float xr[W][VEC], dxa[W][VEC];
+#pragma unroll
+    for (int k = 0; k < W; ++k) zero_vals<VEC>(dxa[k]);
+    zero_vals<VEC>(xr[0]);
+#pragma unroll
+    for (int i = 1; i < W; ++i) {
+      const int t = t0 - i;
+      if (t >= 0)
+        load_vals<T, VEC>(xp + (int64_t)t * D, xr[W - i]);
+      else
+        zero_vals<VEC>(xr[W - i]);
+    }
+    const int tend = t1 + W - 1;
+    for (int tc = t0; tc < tend; tc += U) {
+      if (tc + U <= tend)
+        hw_bwd_rows<T, W, HSV, HAS_STATIC, U, false>(tc, tend, t0, t1, a.Tn, xp, wp, dyp, dxp, dwp, D, wrs, xr,
+                                                     dxa, dsw, swf, a.residual, a.lph, leader);
+      else
+        hw_bwd_rows<T, W, HSV, HAS_STATIC, U, true>(tc, tend, t0, t1, a.Tn, xp, wp, dyp, dxp, dwp, D, wrs, xr,
+                                                    dxa, dsw, swf, a.residual, a.lph, leader);
+    }
+  }
+
+  if (HAS_STATIC) {
+    // Workgroup sum of the 4 wavefronts' dstatic partials, in wave order.
+    constexpr int COLS = 64 * VEC;
+    __shared__ float red[4][W][COLS];
+#pragma unroll
+    for (int k = 0; k < W; ++k)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) red[wave][k][lane * VEC + j] = dsw[k][j];
+    __syncthreads();
+    const int64_t D = a.D;
+    for (int e = threadIdx.x; e < W * COLS; e += 256) {
+      const int k = e / COLS, c = e - k * COLS;
+      const int64_t d = (int64_t)vg * COLS + c;
+      if (d < D) {
+        const float v = ((red[0][k][c] + red[1][k][c]) + red[2][k][c]) + red[3][k][c];
+        part[((int64_t)sgp * W + k) * D + d] = v;
+      }
+    }
+  }
+}
+
+// Launch geometry shared by the host planner and the dispatchers.
+struct HwPlan {
+  HwArgs a;
+  int nblk;
+  int P;  // partial count (bwd)
+};
+
+template <typename T, int W, int HSV>
+hipError_t launch_fwd_fast(const HwProblem& p, const HwPlan& pl) {
+  hw_fwd_fast<T, W, HSV><<<pl.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.weight, (const T*)p.static_w,
+                                                         (T*)p.y, pl.a);
+  return hipGetLastError();
+}
+
+template <typename T, int W, int HSV>
+hipError_t launch_bwd_fast(const HwProblem& p, const HwPlan& pl) {
+  if (p.static_w) {
+    hw_bwd_fast<T, W, HSV, true><<<pl.nblk, 256, 0, p.stream>>>(
+        (const T*)p.x, (const T*)p.weight, (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, (T*)p.dweight, p.ws,
+        pl.a);
+  } else {
+    hw_bwd_fast<T, W, HSV, false><<<pl.nblk, 256, 0, p.stream>>>(
+        (const T*)p.x, (const T*)p.weight, nullptr, (const T*)p.dy, (T*)p.dx, (T*)p.dweight, nullptr, pl.a);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !p.static_w) return e;
+  return reduce_partials(p.ws, p.W * p.D, pl.P, p.W * p.D, p.dstatic_w, p.dtype, p.stream);
+}
+
+// Dispatch on (W, HSV) for one element type.
+template <typename T, bool BWD>
+hipError_t dispatch_fast(const HwProblem& p, const HwPlan& pl) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const int64_t hs = p.D / p.H;
+  const int hsv = (int)(hs < VEC ? hs : VEC);
+#define DC_HW_CASE(WW, HH)                                                                  \
+  if (p.W == WW && hsv == HH) {                                                             \
+    if constexpr (BWD) return launch_bwd_fast<T, WW, HH>(p, pl);                         \
+    else return launch_fwd_fast<T, WW, HH>(p, pl);                                          \
+  }
+#define DC_HW_W(WW)                        \
+  DC_HW_CASE(WW, 1)                        \
+  DC_HW_CASE(WW, 2)                        \
+  DC_HW_CASE(WW, 4)                        \
+  if constexpr (VEC == 8) { DC_HW_CASE(WW, 8) }
+  DC_HW_W(1)
+  DC_HW_W(2)
+  DC_HW_W(3)
+  DC_HW_W(4)
+  DC_HW_W(5)
+  DC_HW_W(6)
+  DC_HW_W(7)
+  DC_HW_W(8)
+#undef DC_HW_W
+#undef DC_HW_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace dc

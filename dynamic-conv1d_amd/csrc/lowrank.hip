@@ -1,0 +1,209 @@
+// Lowrank dynamic causal short convolution: generic kernels and host dispatch.
+//
+//   Kw[b,t,k,d] = sum_r z[b,t,r] * U[r, k*D+d]   (+ static_w[k,d])
+//   y[b,t,d]    = sum_{k<W} Kw[b,t,k,d] * x[b,t-k,d]  (+ x[b,t,d])
+//
+// Reference: lowrank.py:24-67 (forward), 87-140 (dU/dz), 159-205 (dx),
+// 214-299 (autograd glue).  The static filter is the reference's extra rank
+// with z == 1 and U row = static_w (lowrank.py:223-225); here it is an
+// implicit rank R of the kernel, so no padded z or concatenated U is built.
+//
+// This file holds the one-thread-per-output kernels used for fp32 and for
+// shapes the MFMA path (lowrank_mfma.hip) does not take, plus the dispatch.
+#include "dc_common.h"
+#include "dc_launch.h"
+
+namespace dc {
+
+template <typename T>
+__device__ __forceinline__ float zrank(const T* __restrict__ z, int64_t row, int R, int r) {
+  return r < R ? (float)z[row * R + r] : 1.0f;
+}
+
+template <typename T>
+__device__ __forceinline__ float urank(const T* __restrict__ U, const T* __restrict__ sw, int R, int64_t WD,
+                                       int r, int64_t col) {
+  return r < R ? (float)U[(int64_t)r * WD + col] : (float)sw[col];
+}
+
+// Per-token tap weight Kw[row, k, d] in fp32: sum over dynamic ranks, then
+// the static filter (reference.py:29-31 order).
+template <typename T>
+__device__ __forceinline__ float lr_tap(const T* __restrict__ z, const T* __restrict__ U,
+                                        const T* __restrict__ sw, int64_t row, int R, int64_t WD, int64_t col) {
+  float w = 0.f;
+  for (int r = 0; r < R; ++r) w = fmaf((float)z[row * R + r], (float)U[(int64_t)r * WD + col], w);
+  if (sw) w += (float)sw[col];
+  return w;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void lr_fwd_generic(const T* __restrict__ x, const T* __restrict__ z,
+                                                      const T* __restrict__ U, const T* __restrict__ sw,
+                                                      T* __restrict__ y, int64_t BT, int Tn, int D, int R, int W,
+                                                      int residual) {
+  const int64_t n = BT * D;
+  const int64_t WD = (int64_t)W * D;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = i / D;
+    const int d = (int)(i - row * D);
+    const int t = (int)(row % Tn);
+    float acc = 0.f;
+    for (int k = 0; k < W && k <= t; ++k)
+      acc = fmaf(lr_tap(z, U, sw, row, R, WD, (int64_t)k * D + d), (float)x[(row - k) * D + d], acc);
+    if (residual) acc += (float)x[i];
+    y[i] = (T)acc;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void lr_bwd_dx_generic(const T* __restrict__ z, const T* __restrict__ U,
+                                                         const T* __restrict__ sw, const T* __restrict__ dy,
+                                                         T* __restrict__ dx, int64_t BT, int Tn, int D, int R,
+                                                         int W, int residual) {
+  const int64_t n = BT * D;
+  const int64_t WD = (int64_t)W * D;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = i / D;
+    const int d = (int)(i - row * D);
+    const int t = (int)(row % Tn);
+    float acc = 0.f;
+    for (int k = 0; k < W && t + k < Tn; ++k)
+      acc = fmaf((float)dy[(row + k) * D + d], lr_tap(z, U, sw, row + k, R, WD, (int64_t)k * D + d), acc);
+    if (residual) acc += (float)dy[i];
+    dx[i] = (T)acc;
+  }
+}
+
+// dz[row, r] = sum_{k, d} dy[row, d] * x[row-k, d] * U[r, k*D+d]; one
+// workgroup per row, tree reduction in LDS.
+template <typename T>
+__global__ __launch_bounds__(256) void lr_bwd_dz_generic(const T* __restrict__ x, const T* __restrict__ U,
+                                                         const T* __restrict__ dy, T* __restrict__ dz, int Tn,
+                                                         int D, int R, int W) {
+  __shared__ float red[256];
+  const int64_t row = blockIdx.x;
+  const int t = (int)(row % Tn);
+  const int64_t WD = (int64_t)W * D;
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.f;
+    for (int k = 0; k < W && k <= t; ++k) {
+      const T* xr = x + (row - k) * D;
+      const T* ur = U + (int64_t)r * WD + (int64_t)k * D;
+      for (int d = threadIdx.x; d < D; d += 256)
+        acc = fmaf((float)dy[row * D + d] * (float)xr[d], (float)ur[d], acc);
+    }
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+      if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) dz[row * R + r] = (T)red[0];
+    __syncthreads();
+  }
+}
+
+// dU (and dstatic as kernel rank R) partials: grid (ceil(RK*W*D/256), P).
+template <typename T>
+__global__ __launch_bounds__(256) void lr_bwd_du_generic(const T* __restrict__ x, const T* __restrict__ z,
+                                                         const T* __restrict__ dy, float* __restrict__ part,
+                                                         int64_t BT, int Tn, int D, int R, int RK, int W,
+                                                         int64_t rows_per) {
+  const int64_t WD = (int64_t)W * D;
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= (int64_t)RK * WD) return;
+  const int r = (int)(c / WD);
+  const int64_t col = c - (int64_t)r * WD;
+  const int k = (int)(col / D);
+  const int d = (int)(col - (int64_t)k * D);
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per;
+  const int64_t r1 = min(r0 + rows_per, BT);
+  float acc = 0.f;
+  for (int64_t row = r0; row < r1; ++row) {
+    const int t = (int)(row % Tn);
+    if (t >= k) acc = fmaf(zrank(z, row, R, r), (float)dy[row * D + d] * (float)x[(row - k) * D + d], acc);
+  }
+  part[(int64_t)blockIdx.y * RK * WD + c] = acc;
+}
+
+// ------------------------------------------------------------------- host
+namespace {
+
+unsigned generic_grid(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  if (g > 65536) g = 65536;
+  return (unsigned)(g < 1 ? 1 : g);
+}
+
+int generic_partials(int64_t BT) {
+  int64_t P = (BT + 255) / 256;
+  return (int)(P > 64 ? 64 : (P < 1 ? 1 : P));
+}
+
+template <typename T>
+hipError_t fwd_generic(const LrProblem& p) {
+  const int64_t BT = p.B * p.T;
+  lr_fwd_generic<T><<<generic_grid(BT * p.D), 256, 0, p.stream>>>(
+      (const T*)p.x, (const T*)p.z, (const T*)p.U, (const T*)p.static_w, (T*)p.y, BT, (int)p.T, (int)p.D,
+      (int)p.R, (int)p.W, p.residual);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t bwd_generic(const LrProblem& p) {
+  const int64_t BT = p.B * p.T;
+  const int RK = (int)p.R + (p.static_w ? 1 : 0);
+  const int64_t WD = p.W * p.D;
+  lr_bwd_dx_generic<T><<<generic_grid(BT * p.D), 256, 0, p.stream>>>(
+      (const T*)p.z, (const T*)p.U, (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, BT, (int)p.T, (int)p.D,
+      (int)p.R, (int)p.W, p.residual);
+  lr_bwd_dz_generic<T><<<(unsigned)BT, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.U, (const T*)p.dy,
+                                                           (T*)p.dz, (int)p.T, (int)p.D, (int)p.R, (int)p.W);
+  const int P = generic_partials(BT);
+  const int64_t rows_per = (BT + P - 1) / P;
+  dim3 grid((unsigned)((RK * WD + 255) / 256), (unsigned)P);
+  lr_bwd_du_generic<T><<<grid, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.dy, p.ws, BT,
+                                                   (int)p.T, (int)p.D, (int)p.R, RK, (int)p.W, rows_per);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  e = reduce_partials(p.ws, RK * WD, P, p.R * WD, p.dU, p.dtype, p.stream);
+  if (e != hipSuccess || !p.static_w) return e;
+  return reduce_partials(p.ws + p.R * WD, RK * WD, P, WD, p.dstatic_w, p.dtype, p.stream);
+}
+
+}  // namespace
+
+// Provided by lowrank_mfma.hip.
+bool lr_mfma_ok_impl(const LrProblem& p, bool bwd);
+int64_t lr_mfma_ws_bytes(const LrProblem& p);
+hipError_t lr_mfma_fwd(const LrProblem& p);
+hipError_t lr_mfma_bwd(const LrProblem& p);
+
+bool lr_mfma_ok(const LrProblem& p, bool bwd) { return lr_mfma_ok_impl(p, bwd); }
+
+int64_t lr_bwd_ws_bytes(const LrProblem& p) {
+  if (lr_mfma_ok(p, true)) return lr_mfma_ws_bytes(p);
+  const int64_t RK = p.R + (p.static_w ? 1 : 0);
+  return (int64_t)generic_partials(p.B * p.T) * RK * p.W * p.D * (int64_t)sizeof(float);
+}
+
+hipError_t lr_fwd(const LrProblem& p) {
+  if (lr_mfma_ok(p, false)) return lr_mfma_fwd(p);
+  switch (p.dtype) {
+    case kBF16: return fwd_generic<bf16>(p);
+    case kFP16: return fwd_generic<fp16>(p);
+    default: return fwd_generic<float>(p);
+  }
+}
+
+hipError_t lr_bwd(const LrProblem& p) {
+  if (lr_mfma_ok(p, true)) return lr_mfma_bwd(p);
+  switch (p.dtype) {
+    case kBF16: return bwd_generic<bf16>(p);
+    case kFP16: return bwd_generic<fp16>(p);
+    default: return bwd_generic<float>(p);
+  }
+}
+
+}  // namespace dc

@@ -1,0 +1,86 @@
+"""ctypes binding of libdynconv.so (C ABI declared in include/dynconv.h).
+
+The library is loaded lazily after `import torch`, so it binds to the HIP
+runtime torch has already mapped (both carry SONAME libamdhip64.so.7).
+There is no fallback: if the library is missing or a call fails, a
+RuntimeError is raised.
+"""
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdynconv.so")
+ABI_VERSION = 1
+
+DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+_c_vp = ctypes.c_void_p
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+
+# name -> (restype, argtypes); mirrors include/dynconv.h.
+SIGNATURES = {
+    "dc_abi_version": (_c_int, []),
+    "dc_status_string": (ctypes.c_char_p, [_c_int]),
+    "dc_headwise_fwd": (_c_int, [_c_vp] * 4 + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
+    "dc_headwise_bwd_ws_bytes": (_c_i64, [_c_i64] * 5 + [_c_int, _c_int]),
+    "dc_headwise_bwd": (_c_int, [_c_vp] * 8 + [_c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
+    "dc_lowrank_fwd": (_c_int, [_c_vp] * 5 + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
+    "dc_lowrank_bwd_ws_bytes": (_c_i64, [_c_i64] * 5 + [_c_int, _c_int]),
+    "dc_lowrank_bwd": (_c_int, [_c_vp] * 10 + [_c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load(path: str = LIB_PATH):
+    """Load (once) and return the ctypes handle of libdynconv.so."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"libdynconv.so not found at {path}; build it with "
+                "`python dynamic-conv1d_amd/build.py` (or __graft_entry__.build())"
+            )
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = lib.dc_abi_version()
+        if ver != ABI_VERSION:
+            raise RuntimeError(f"libdynconv.so ABI version {ver}, expected {ABI_VERSION}")
+        _lib = lib
+    return _lib
+
+
+def status_string(status: int) -> str:
+    return load().dc_status_string(status).decode()
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"dynconv {what} failed: {status_string(status)} (status {status})")
+
+
+def ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return DTYPE_CODES[dt]
+    except KeyError:
+        raise AssertionError(f"unsupported dtype {dt}; expected one of bfloat16, float16, float32") from None

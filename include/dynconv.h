@@ -1,0 +1,119 @@
+/*
+ * dynconv.h -- C ABI of libdynconv.so, the MI355X (gfx950) implementation of
+ * the dynamic short-convolution kernels.
+ *
+ * The reference drives its kernels from Python through Triton launches; each
+ * entry point below replaces the launch(es) and host-side tensor plumbing of
+ * one autograd direction:
+ *
+ *   dc_headwise_fwd   <- headwise.py:219-254  (_HeadwiseDynamicConvolutionFn.forward,
+ *                                              causal_conv1d_fwd_kernel launch 234-248)
+ *   dc_headwise_bwd   <- headwise.py:256-309  (.backward, causal_conv1d_bwd_kernel
+ *                                              launch 283-300, dstatic fp32 accumulate
+ *                                              and cast 270-275, 304-305)
+ *   dc_lowrank_fwd    <- lowrank.py:214-249   (_LowrankDynamicConvolutionFn.forward,
+ *                                              static-as-rank fusion 223-225, launch 230-242)
+ *   dc_lowrank_bwd    <- lowrank.py:251-299   (.backward, launches 266-292, dU cast and
+ *                                              static split 294-299)
+ *
+ * Conventions
+ *   - Every tensor pointer is a DEVICE pointer to a contiguous row-major array:
+ *       x, y, dy, dx        [B, T, D]
+ *       weight, dweight     [B, T, H, W]        (headwise; head_size = D / H)
+ *       z, dz               [B, T, R]           (lowrank; R = dynamic rank, without static)
+ *       U, dU               [R, W * D]          (tap k occupies columns k*D .. k*D+D-1)
+ *       static_w, dstatic_w [W, D]              (may be NULL: no static filter)
+ *     All tensors of one call share `dtype`.
+ *   - Sizes are int64.  Returns DC_OK (0) or a negative dc_status.
+ *   - Arguments are validated before any HIP call; nothing is launched on error.
+ *   - No call allocates device memory, synchronises, or throws.  Scratch for
+ *     the deterministic cross-workgroup reductions of the backward passes is a
+ *     caller-provided workspace of at least *_bwd_ws_bytes(...) bytes
+ *     (256-byte aligned); its contents on entry do not matter.
+ *   - Kernels are enqueued on `stream` (a hipStream_t; NULL = default stream)
+ *     of the current HIP device.  Calls are safe from any host thread.
+ *   - Results are deterministic: the same inputs give bitwise-identical
+ *     outputs run to run (no floating-point atomics).
+ */
+#ifndef DYNCONV_H_
+#define DYNCONV_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DC_ABI_VERSION 1
+
+/* Largest convolution width and (kernel) rank accepted. */
+#define DC_MAX_W 8
+#define DC_MAX_R 64
+
+typedef enum dc_dtype {
+  DC_DTYPE_BF16 = 0,
+  DC_DTYPE_FP16 = 1,
+  DC_DTYPE_FP32 = 2
+} dc_dtype;
+
+typedef enum dc_status {
+  DC_OK = 0,
+  DC_ERR_NULL = -1,        /* a required pointer is NULL                          */
+  DC_ERR_SHAPE = -2,       /* a size <= 0, D % H != 0, or a size too large         */
+  DC_ERR_DTYPE = -3,       /* dtype is not a dc_dtype                              */
+  DC_ERR_UNSUPPORTED = -4, /* W > DC_MAX_W, R(+1) > DC_MAX_R, head_size too large  */
+  DC_ERR_WORKSPACE = -5,   /* workspace NULL or smaller than the size query        */
+  DC_ERR_ALIGN = -6,       /* a pointer is not aligned to its element size          */
+  DC_ERR_DEVICE = -7,      /* no HIP device available                               */
+  DC_ERR_LAUNCH = -8       /* the HIP runtime rejected a kernel launch              */
+} dc_status;
+
+/* DC_ABI_VERSION of the loaded library. */
+int dc_abi_version(void);
+
+/* Static, human-readable text for a dc_status value. */
+const char* dc_status_string(int status);
+
+/* y = headwise dynamic convolution of x (+ x if residual != 0).
+ * Replaces headwise.py:219-254.  static_w may be NULL. */
+int dc_headwise_fwd(const void* x, const void* weight, const void* static_w, void* y,
+                    int64_t B, int64_t T, int64_t D, int64_t H, int64_t W,
+                    int dtype, int residual, void* stream);
+
+/* Workspace bytes needed by dc_headwise_bwd for these sizes (>= 0), or a
+ * negative dc_status for invalid sizes. */
+int64_t dc_headwise_bwd_ws_bytes(int64_t B, int64_t T, int64_t D, int64_t H, int64_t W,
+                                 int dtype, int has_static);
+
+/* dx, dweight and (when static_w != NULL) dstatic_w from dy.
+ * Replaces headwise.py:256-309.  static_w and dstatic_w are both NULL or both set. */
+int dc_headwise_bwd(const void* x, const void* weight, const void* static_w, const void* dy,
+                    void* dx, void* dweight, void* dstatic_w,
+                    void* workspace, int64_t ws_bytes,
+                    int64_t B, int64_t T, int64_t D, int64_t H, int64_t W,
+                    int dtype, int residual, void* stream);
+
+/* y = lowrank dynamic convolution; the per-token weights z @ U (+ static_w as an
+ * implicit extra rank with z == 1) are formed on chip and never written out.
+ * Replaces lowrank.py:214-249.  R is the dynamic rank (z.shape[-1]). */
+int dc_lowrank_fwd(const void* x, const void* z, const void* U, const void* static_w, void* y,
+                   int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
+                   int dtype, int residual, void* stream);
+
+/* Workspace bytes needed by dc_lowrank_bwd, or a negative dc_status. */
+int64_t dc_lowrank_bwd_ws_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
+                                int dtype, int has_static);
+
+/* dx, dz, dU and (when static_w != NULL) dstatic_w from dy, in one pass over
+ * x and dy.  Replaces lowrank.py:251-299. */
+int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* static_w,
+                   const void* dy, void* dx, void* dz, void* dU, void* dstatic_w,
+                   void* workspace, int64_t ws_bytes,
+                   int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
+                   int dtype, int residual, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DYNCONV_H_ */
