@@ -17,9 +17,12 @@ constexpr int pow2_align(int bytes) {
   return (bytes % 16 == 0) ? 16 : (bytes % 8 == 0) ? 8 : (bytes % 4 == 0) ? 4 : 2;
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 template <int A> struct Unit;
-template <> struct Unit<16> { typedef uint4 type; };
-template <> struct Unit<8> { typedef uint2 type; };
+template <> struct Unit<16> { typedef u32x4 type; };
+template <> struct Unit<8> { typedef u32x2 type; };
 template <> struct Unit<4> { typedef uint32_t type; };
 template <> struct Unit<2> { typedef uint16_t type; };
 
