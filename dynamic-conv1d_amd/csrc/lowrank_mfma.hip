@@ -199,6 +199,273 @@ __global__ __launch_bounds__(256) void lr_fwd_mfma(const T* __restrict__ x_, con
   }
 }
 
+
+// ---------------------------------------------------------------- backward
+//
+// One pass over x and dy produces dx, dz, dU and dstatic_w (reference:
+// lowrank.py:87-140 and 159-205, two kernels that both read dy).
+//
+// Tile: a wavefront owns 16 rows x 64 channels; lane l = 16q + n owns rows
+// 4q..4q+3 and the channel quartet 4n..4n+3 (64-bit loads, 128 contiguous
+// bytes per row across the 16 lanes of a row group).  With
+// G_k[t, d] = bf16(dy[t, d] * x[t-k, d]) (the reference also rounds this
+// product to bf16 before its dot products, lowrank.py:128):
+//   * dU[r, kD+d] += sum_t z_eff[t, r] G_k[t, d]: MFMA with K = the 16 rows.
+//     For each j the lane's four G values of column 4n+j are exactly the
+//     B operand (rows 4q..4q+3 of column n); A is z_eff transposed.
+//   * dz[t, r] += sum_d G_k[t, d] U_eff[r, kD+d]: needs K = channels.  The
+//     same packed G registers fed as the *A* operand of an MFMA against the
+//     16x16 identity return G transposed (lane now holds one row and four
+//     channels 4(4q+i)+j), which is the A operand of the dz MFMA.  All
+//     values are bf16-exact, so the transpose is exact.
+//   * dx[t, d] = sum_k dy[t+k, d] Kw[t+k, k, d] (+ dy): the tap weights of
+//     rows 4q..4q+3+W-1 come from NB = ceil((W+3)/4) MFMA row blocks (A rows
+//     shifted by 4), so every lane has the look-ahead rows it needs without
+//     cross-lane traffic; dy rows 4q..4q+W+2 are read from L1.
+// A workgroup is 4 wavefronts on 4 adjacent 64-channel chunks of the same
+// rows.  dz partial sums over the 256 channels are added in LDS per tile in
+// wave order and written as one fp32 partial per 256-channel group; dU
+// accumulates in registers over the wavefront's run of tiles and is written
+// as one fp32 partial per run.  reduce_partials sums both deterministically.
+
+struct LrBwdArgs {
+  int Tn, D, R, RK, residual;
+  int nch;    // ceil(D / 64) channel chunks
+  int ncg;    // ceil(nch / 4) chunk groups: one workgroup column
+  int seg;    // tiles per run
+  int nspb;   // runs per sequence
+  int nseg;   // B * nspb
+  int nblk;   // ncg * nseg
+  int64_t BT;
+};
+
+__device__ __forceinline__ uint32_t elem16x2(const u32x2& v, int j) {
+  const uint32_t w = v[j >> 1];
+  return (j & 1) ? (w >> 16) : (w & 0xFFFFu);
+}
+
+template <typename T, int W, int RC>
+__global__ __launch_bounds__(256) void lr_bwd_mfma(const T* __restrict__ x_, const T* __restrict__ z_,
+                                                   const T* __restrict__ U_, const T* __restrict__ sw_,
+                                                   const T* __restrict__ dy_, T* __restrict__ dx_,
+                                                   float* __restrict__ part_dz, float* __restrict__ part_du,
+                                                   LrBwdArgs a) {
+  constexpr int NB = (W + 6) / 4;  // MFMA row blocks for the dx look-ahead
+  constexpr int NR = W + 3;        // rows of x (4q-W+1 ..) and dy (4q ..) per lane
+  const uint16_t* __restrict__ x = reinterpret_cast<const uint16_t*>(x_);
+  const uint16_t* __restrict__ z = reinterpret_cast<const uint16_t*>(z_);
+  const uint16_t* __restrict__ U = reinterpret_cast<const uint16_t*>(U_);
+  const uint16_t* __restrict__ sw = reinterpret_cast<const uint16_t*>(sw_);
+  const uint16_t* __restrict__ dy = reinterpret_cast<const uint16_t*>(dy_);
+  uint16_t* __restrict__ dx = reinterpret_cast<uint16_t*>(dx_);
+  __shared__ float dzred[2][4][RC * 256];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane >> 4, n = lane & 15;
+  const int lb = xcd_remap(blockIdx.x, a.nblk);
+  const int cg = lb % a.ncg, sg = lb / a.ncg;
+  const int chunk = cg * 4 + wave;
+  const int D = a.D;
+  const int d0 = chunk * 64;
+  const bool chv = d0 + 4 * n < D;           // lane quartet inside D (D % 16 == 0)
+  const bool grpv = d0 + 16 * q < D;         // lane's 16-channel dz group inside D
+  const int64_t WD = (int64_t)W * D;
+  const int b = sg / a.nspb;
+  const int ntile = (a.Tn + 15) >> 4;
+  const int tile0 = (sg - b * a.nspb) * a.seg;
+  const int tile1 = min(tile0 + a.seg, ntile);
+  const int64_t row0 = (int64_t)b * a.Tn;
+
+  // Identity as the B operand: lane (q, n) gives rows 4q..4q+3 of column n.
+  u32x2 ident;
+  {
+    const uint32_t one = Mma16<T>::kOne;
+    uint32_t e[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) e[kk] = (4 * q + kk == n) ? one : 0u;
+    ident[0] = e[0] | (e[1] << 16);
+    ident[1] = e[2] | (e[3] << 16);
+  }
+
+  f32x4 du[W][RC][4];
+#pragma unroll
+  for (int k = 0; k < W; ++k)
+#pragma unroll
+    for (int c = 0; c < RC; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) du[k][c][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int tile = tile0; tile < tile1; ++tile) {
+    const int t0 = tile * 16;
+    // ---- operand loads
+    u32x2 xr[NR], dyr[NR];
+#pragma unroll
+    for (int m = 0; m < NR; ++m) {
+      const int tx = t0 + 4 * q - (W - 1) + m;
+      const int td = t0 + 4 * q + m;
+      xr[m] = (chv && tx >= 0 && tx < a.Tn) ? *reinterpret_cast<const u32x2*>(x + (row0 + tx) * D + d0 + 4 * n)
+                                            : u32x2{0u, 0u};
+      dyr[m] = (chv && td < a.Tn) ? *reinterpret_cast<const u32x2*>(dy + (row0 + td) * D + d0 + 4 * n)
+                                  : u32x2{0u, 0u};
+    }
+    // z_eff rows as the A operand of the tap-weight MFMAs (row blocks shifted by 4).
+    u32x2 zA[NB][RC];
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) {
+      const int t = t0 + 4 * bb + n;
+#pragma unroll
+      for (int c = 0; c < RC; ++c) {
+        uint32_t e[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) e[kk] = t < a.Tn ? zbits<T>(z, row0 + t, a.R, a.RK, 16 * c + 4 * q + kk) : 0u;
+        zA[bb][c][0] = e[0] | (e[1] << 16);
+        zA[bb][c][1] = e[2] | (e[3] << 16);
+      }
+    }
+    // z_eff transposed as the A operand of the dU MFMA: rank n, rows 4q..4q+3.
+    u32x2 zT[RC];
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+      uint32_t e[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int t = t0 + 4 * q + kk;
+        e[kk] = t < a.Tn ? zbits<T>(z, row0 + t, a.R, a.RK, 16 * c + n) : 0u;
+      }
+      zT[c][0] = e[0] | (e[1] << 16);
+      zT[c][1] = e[2] | (e[3] << 16);
+    }
+
+    float dxa[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dxa[i][j] = 0.f;
+    f32x4 dz[RC];
+#pragma unroll
+    for (int c = 0; c < RC; ++c) dz[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      // U_eff operands of tap k (L1-resident: 64 channels x W x RK per wavefront).
+      u32x2 uw[RC][4];  // tap weights (B): ranks 16c+4q+kk, column 4n+j
+      u32x2 uz[RC][4];  // dz (B): rank 16c+n, channels 16q + 4kk + j
+#pragma unroll
+      for (int c = 0; c < RC; ++c) {
+        u32x2 rows[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const int r = 16 * c + 4 * q + kk;
+          const uint16_t* src = nullptr;
+          if (chv && r < a.R) src = U + (int64_t)r * WD + (int64_t)k * D + d0 + 4 * n;
+          else if (chv && r < a.RK) src = sw + (int64_t)k * D + d0 + 4 * n;
+          rows[kk] = src ? *reinterpret_cast<const u32x2*>(src) : u32x2{0u, 0u};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          uw[c][j][0] = elem16x2(rows[0], j) | (elem16x2(rows[1], j) << 16);
+          uw[c][j][1] = elem16x2(rows[2], j) | (elem16x2(rows[3], j) << 16);
+        }
+        const int r = 16 * c + n;
+        const uint16_t* src = nullptr;
+        if (grpv && r < a.R) src = U + (int64_t)r * WD + (int64_t)k * D + d0 + 16 * q;
+        else if (grpv && r < a.RK) src = sw + (int64_t)k * D + d0 + 16 * q;
+        const u32x4 v0 = src ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 v1 = src ? *reinterpret_cast<const u32x4*>(src + 8) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          uz[c][j][0] = elem16(v0, j) | (elem16(v0, 4 + j) << 16);
+          uz[c][j][1] = elem16(v1, j) | (elem16(v1, 4 + j) << 16);
+        }
+      }
+      // dx += dy[4q+i+k] * Kw[4q+i+k, k]: tap weights of the row blocks that hold rows k..k+3.
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) {
+          if (4 * bb > 3 + k || 4 * bb + 3 < k) continue;
+          f32x4 wk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < RC; ++c) wk = Mma16<T>::run(zA[bb][c], uw[c][j], wk);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int tr = i + k;  // row offset of dy / Kw in the lane window
+            if (tr >= 4 * bb && tr < 4 * bb + 4)
+              dxa[i][j] = fmaf(Mma16<T>::to_f(elem16x2(dyr[tr], j)), wk[tr - 4 * bb], dxa[i][j]);
+          }
+        }
+      }
+      // G_k = bf16(dy * x_shift), packed per column j as rows 4q..4q+3.
+      u32x2 g[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t e[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          e[i] = f2bits<T>(Mma16<T>::to_f(elem16x2(dyr[i], j)) * Mma16<T>::to_f(elem16x2(xr[i - k + W - 1], j)));
+        g[j][0] = e[0] | (e[1] << 16);
+        g[j][1] = e[2] | (e[3] << 16);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // dU (K = rows); exact transpose of G_j; dz (K = channels).
+#pragma unroll
+        for (int c = 0; c < RC; ++c) du[k][c][j] = Mma16<T>::run(zT[c], g[j], du[k][c][j]);
+        const f32x4 tr = Mma16<T>::run(g[j], ident, f32x4{0.f, 0.f, 0.f, 0.f});
+        u32x2 ga;
+        ga[0] = f2bits<T>(tr[0]) | (f2bits<T>(tr[1]) << 16);
+        ga[1] = f2bits<T>(tr[2]) | (f2bits<T>(tr[3]) << 16);
+#pragma unroll
+        for (int c = 0; c < RC; ++c) dz[c] = Mma16<T>::run(ga, uz[c][j], dz[c]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- dx rows 4q..4q+3 (+ residual dy)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = t0 + 4 * q + i;
+      if (chv && t < a.Tn) {
+        u32x2 o;
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = a.residual ? dxa[i][j] + Mma16<T>::to_f(elem16x2(dyr[i], j)) : dxa[i][j];
+        o[0] = f2bits<T>(v[0]) | (f2bits<T>(v[1]) << 16);
+        o[1] = f2bits<T>(v[2]) | (f2bits<T>(v[3]) << 16);
+        *reinterpret_cast<u32x2*>(dx + (row0 + t) * D + d0 + 4 * n) = o;
+      }
+    }
+    // ---- dz: sum the 4 chunk wavefronts of this tile in LDS, one partial per group
+    const int par = tile & 1;
+#pragma unroll
+    for (int c = 0; c < RC; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dzred[par][wave][c * 256 + (4 * q + i) * 16 + n] = dz[c][i];
+    __syncthreads();
+    for (int e = threadIdx.x; e < RC * 256; e += 256) {
+      const int c = e >> 8, rem = e & 255, rr = rem >> 4, nn = rem & 15;
+      const int r = 16 * c + nn;
+      const int t = t0 + rr;
+      const float v = ((dzred[par][0][e] + dzred[par][1][e]) + dzred[par][2][e]) + dzred[par][3][e];
+      if (r < a.R && t < a.Tn) part_dz[((int64_t)cg * a.BT + row0 + t) * a.R + r] = v;
+    }
+  }
+
+  // ---- dU partial of this run: rows r < RK of U_eff, the wavefront's 64 columns per tap
+#pragma unroll
+  for (int k = 0; k < W; ++k)
+#pragma unroll
+    for (int c = 0; c < RC; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * c + 4 * q + i;
+          const int d = d0 + 4 * n + j;
+          if (r < a.RK && chv) part_du[((int64_t)sg * a.RK + r) * WD + (int64_t)k * D + d] = du[k][c][j][i];
+        }
+}
+
 // ------------------------------------------------------------------- host
 namespace {
 
@@ -247,24 +514,99 @@ hipError_t dispatch_fwd(const LrProblem& p) {
   return hipErrorInvalidValue;
 }
 
+LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
+  LrBwdArgs a;
+  a.Tn = (int)p.T;
+  a.D = (int)p.D;
+  a.R = (int)p.R;
+  a.RK = (int)p.R + (p.static_w ? 1 : 0);
+  a.residual = p.residual;
+  a.nch = (int)((p.D + 63) / 64);
+  a.ncg = (a.nch + 3) / 4;
+  const int64_t ntile = (p.T + 15) / 16;
+  int64_t seg = (p.B * ntile * a.ncg * 4 + target_waves - 1) / target_waves;
+  if (seg < 1) seg = 1;
+  if (seg > ntile) seg = ntile;
+  a.seg = (int)seg;
+  a.nspb = (int)((ntile + seg - 1) / seg);
+  a.nseg = (int)(p.B * a.nspb);
+  a.nblk = a.nseg * a.ncg;
+  a.BT = p.B * p.T;
+  return a;
+}
+
+constexpr int kBwdTargetWaves = 2048;
+
+// Workspace: [dz partials: ncg x BT x R fp32][dU partials: nseg x RK x W*D fp32], 256-byte aligned.
+struct BwdWs {
+  int64_t dz_off, du_off, total;
+};
+BwdWs bwd_ws(const LrProblem& p, const LrBwdArgs& a) {
+  BwdWs w;
+  const int64_t dz = (int64_t)a.ncg * a.BT * a.R * 4;
+  w.dz_off = 0;
+  w.du_off = (dz + 255) / 256 * 256;
+  w.total = w.du_off + (int64_t)a.nseg * a.RK * p.W * p.D * 4;
+  return w;
+}
+
+template <typename T, int W, int RC>
+hipError_t launch_bwd(const LrProblem& p) {
+  const LrBwdArgs a = make_bwd_args(p, kBwdTargetWaves);
+  const BwdWs w = bwd_ws(p, a);
+  float* pdz = (float*)((char*)p.ws + w.dz_off);
+  float* pdu = (float*)((char*)p.ws + w.du_off);
+  lr_bwd_mfma<T, W, RC><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.U,
+                                                       (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, pdz, pdu, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t WD = p.W * p.D, RKWD = (int64_t)a.RK * WD;
+  e = reduce_partials(pdu, RKWD, a.nseg, p.R * WD, p.dU, p.dtype, p.stream);
+  if (e == hipSuccess && p.static_w)
+    e = reduce_partials(pdu + p.R * WD, RKWD, a.nseg, WD, p.dstatic_w, p.dtype, p.stream);
+  if (e == hipSuccess) e = reduce_partials(pdz, a.BT * a.R, a.ncg, a.BT * a.R, p.dz, p.dtype, p.stream);
+  return e;
+}
+
+template <typename T>
+hipError_t dispatch_bwd(const LrProblem& p) {
+  const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
+#define DC_LR_CASE(WW, CC) \
+  if (p.W == WW && rc == CC) return launch_bwd<T, WW, CC>(p);
+  DC_LR_CASE(1, 1) DC_LR_CASE(1, 2) DC_LR_CASE(1, 3) DC_LR_CASE(1, 4)
+  DC_LR_CASE(2, 1) DC_LR_CASE(2, 2) DC_LR_CASE(2, 3) DC_LR_CASE(2, 4)
+  DC_LR_CASE(3, 1) DC_LR_CASE(3, 2)
+  DC_LR_CASE(4, 1) DC_LR_CASE(4, 2)
+  DC_LR_CASE(5, 1) DC_LR_CASE(6, 1) DC_LR_CASE(7, 1) DC_LR_CASE(8, 1)
+#undef DC_LR_CASE
+  return hipErrorInvalidValue;
+}
+
+bool aligned8(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
+
 }  // namespace
 
 bool lr_mfma_ok_impl(const LrProblem& p, bool bwd) {
-  if (bwd) return false;  // backward: lowrank.hip kernels
   if (p.dtype != kBF16 && p.dtype != kFP16) return false;
   if (p.W < 1 || p.W > 8) return false;
-  if (p.D % 8 != 0) return false;
   const int64_t rc = (p.R + (p.static_w ? 1 : 0) + 15) / 16;
-  if (rc > 4 || p.W * rc > 8) return false;  // staged operands: W*RC*4 KiB of LDS, at most 32 KiB
-  return aligned16(p.x) && aligned16(p.U) && aligned16(p.static_w) && aligned16(p.y);
+  if (rc > 4 || p.W * rc > 8) return false;  // staged operands / accumulators bound W*RC
+  if (!bwd) {
+    if (p.D % 8 != 0) return false;
+    return aligned16(p.x) && aligned16(p.U) && aligned16(p.static_w) && aligned16(p.y);
+  }
+  if (p.D % 16 != 0) return false;
+  return aligned8(p.x) && aligned8(p.dy) && aligned8(p.dx) && aligned16(p.U) && aligned16(p.static_w);
 }
 
-int64_t lr_mfma_ws_bytes(const LrProblem&) { return 0; }
+int64_t lr_mfma_ws_bytes(const LrProblem& p) { return bwd_ws(p, make_bwd_args(p, kBwdTargetWaves)).total; }
 
 hipError_t lr_mfma_fwd(const LrProblem& p) {
   return p.dtype == kBF16 ? dispatch_fwd<bf16>(p) : dispatch_fwd<fp16>(p);
 }
 
-hipError_t lr_mfma_bwd(const LrProblem&) { return hipErrorInvalidValue; }
+hipError_t lr_mfma_bwd(const LrProblem& p) {
+  return p.dtype == kBF16 ? dispatch_bwd<bf16>(p) : dispatch_bwd<fp16>(p);
+}
 
 }  // namespace dc
