@@ -15,9 +15,11 @@ synthetic (BASELINE.json distributions, CPU generator seed 0) and resident in
 HBM before timing.
 
 Also reported:
-  breakdown    per configuration and direction, the C-ABI call timed alone
-               with HIP events after a 512 MiB cache flush (median of reps),
-               plus configs[4] (lowrank QKV, 3 calls) at its own shape;
+  breakdown    per configuration and direction, the average C-ABI launch
+               sequence: back-to-back launches rotating over enough
+               independent input sets that each launch's data is out of the
+               256 MB MALL, between one pair of HIP events; plus configs[4]
+               (lowrank QKV, 3 calls) at its own shape;
   roofline     the dominant launch (headwise hs1 backward) against 8 TB/s;
   cpu_baseline the CPU oracle (fp32 restatement of reference.py) on configs[0]
                on this host's cores.
@@ -117,68 +119,93 @@ def cpu_baseline(torch):
     }
 
 
-class AbiTimer:
-    """Times one C-ABI launch sequence with HIP events on torch's current stream after a cache flush."""
-
-    def __init__(self, torch, dev):
-        self.torch = torch
-        self.flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
-
-    def time(self, launch, reps):
-        torch = self.torch
-        ts = []
-        for _ in range(reps):
-            self.flush.fill_(1.0)  # ~0.1 ms of GPU work: the host enqueues the launch before the GPU gets there
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            launch()
-            e.record()
-            e.synchronize()
-            ts.append(s.elapsed_time(e) * 1e3)  # us
-        return statistics.median(ts), ts
+MALL_BYTES = 256 << 20
 
 
-def abi_launchers(c, args, dy, torch):
-    """Direct C-ABI fwd and bwd launches with preallocated outputs (no autograd, no allocation)."""
+def n_sets(c):
+    """Independent input/output sets to rotate so each launch finds its data out of the 256 MB MALL."""
+    fb, _ = alg_bytes(c)
+    return max(2, math.ceil(4 * MALL_BYTES / fb))
+
+
+def abi_sets(c, torch, dev):
+    """`n_sets(c)` sets of bf16 inputs (device-generated, BASELINE scales) with preallocated outputs."""
+    from dynconv import _capi
+
+    lib = _capi.load()
+    B, T, D, W = c["B"], c["T"], c["D"], c["W"]
+    bf = torch.bfloat16
+    sets = []
+    for _ in range(n_sets(c)):
+        d = {"x": torch.randn(B, T, D, device=dev).to(bf), "dy": torch.randn(B, T, D, device=dev).to(bf)}
+        d["sw"] = ((torch.rand(W, D, device=dev) * 2 - 1) / math.sqrt(W)).to(bf) if c["static"] else None
+        if c["kind"] == "hw":
+            d["w"] = (torch.randn(B, T, c["H"], W, device=dev) / math.sqrt(W)).to(bf)
+            d["dw"] = torch.empty_like(d["w"])
+            nws = lib.dc_headwise_bwd_ws_bytes(B, T, D, c["H"], W, 0, int(c["static"]))
+        else:
+            rk = c["R"] + (1 if c["static"] else 0)
+            d["z"] = torch.randn(B, T, c["R"], device=dev).to(bf)
+            d["U"] = (torch.randn(c["R"], W * D, device=dev) / math.sqrt(rk * W)).to(bf)
+            d["dz"], d["dU"] = torch.empty_like(d["z"]), torch.empty_like(d["U"])
+            nws = lib.dc_lowrank_bwd_ws_bytes(B, T, D, c["R"], W, 0, int(c["static"]))
+        d["y"], d["dx"] = torch.empty_like(d["x"]), torch.empty_like(d["x"])
+        d["dsw"] = torch.empty_like(d["sw"]) if c["static"] else None
+        d["nws"] = nws
+        d["ws"] = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
+        sets.append(d)
+    return sets
+
+
+def abi_launchers(c, sets, torch):
+    """Direct C-ABI forward / backward launches on set i (no autograd, no allocation)."""
     from dynconv import _capi
 
     lib = _capi.load()
     st = torch.cuda.current_stream().cuda_stream
     B, T, D, W = c["B"], c["T"], c["D"], c["W"]
-    x = args[0].detach()
-    sw = args[-1].detach() if args[-1] is not None else None
-    y = torch.empty_like(x)
-    dx = torch.empty_like(x)
     p = _capi.ptr
     res = int(c["residual"])
     if c["kind"] == "hw":
-        w = args[1].detach()
-        dw = torch.empty_like(w)
-        dsw = torch.empty_like(sw) if sw is not None else None
-        nws = lib.dc_headwise_bwd_ws_bytes(B, T, D, c["H"], W, 0, int(sw is not None))
-        ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=x.device)
+        H = c["H"]
 
-        def fwd():
-            _capi.check(lib.dc_headwise_fwd(p(x), p(w), p(sw), p(y), B, T, D, c["H"], W, 0, res, st), "fwd")
+        def fwd(i):
+            d = sets[i]
+            _capi.check(lib.dc_headwise_fwd(p(d["x"]), p(d["w"]), p(d["sw"]), p(d["y"]), B, T, D, H, W, 0, res, st),
+                        "fwd")
 
-        def bwd():
-            _capi.check(lib.dc_headwise_bwd(p(x), p(w), p(sw), p(dy), p(dx), p(dw), p(dsw), p(ws), nws,
-                                            B, T, D, c["H"], W, 0, res, st), "bwd")
+        def bwd(i):
+            d = sets[i]
+            _capi.check(lib.dc_headwise_bwd(p(d["x"]), p(d["w"]), p(d["sw"]), p(d["dy"]), p(d["dx"]), p(d["dw"]),
+                                            p(d["dsw"]), p(d["ws"]), d["nws"], B, T, D, H, W, 0, res, st), "bwd")
     else:
-        z, U = args[1].detach(), args[2].detach()
-        dz, dU = torch.empty_like(z), torch.empty_like(U)
-        dsw = torch.empty_like(sw) if sw is not None else None
         R = c["R"]
-        nws = lib.dc_lowrank_bwd_ws_bytes(B, T, D, R, W, 0, int(sw is not None))
-        ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=x.device)
 
-        def fwd():
-            _capi.check(lib.dc_lowrank_fwd(p(x), p(z), p(U), p(sw), p(y), B, T, D, R, W, 0, res, st), "fwd")
+        def fwd(i):
+            d = sets[i]
+            _capi.check(lib.dc_lowrank_fwd(p(d["x"]), p(d["z"]), p(d["U"]), p(d["sw"]), p(d["y"]),
+                                           B, T, D, R, W, 0, res, st), "fwd")
 
-        def bwd():
-            _capi.check(lib.dc_lowrank_bwd(p(x), p(z), p(U), p(sw), p(dy), p(dx), p(dz), p(dU), p(dsw), p(ws), nws,
+        def bwd(i):
+            d = sets[i]
+            _capi.check(lib.dc_lowrank_bwd(p(d["x"]), p(d["z"]), p(d["U"]), p(d["sw"]), p(d["dy"]), p(d["dx"]),
+                                           p(d["dz"]), p(d["dU"]), p(d["dsw"]), p(d["ws"]), d["nws"],
                                            B, T, D, R, W, 0, res, st), "bwd")
     return fwd, bwd
+
+
+def time_launches(torch, launch, nsets, reps):
+    """Average duration of one launch sequence: `reps` back-to-back launches rotating over `nsets`
+    input sets between one pair of HIP events on torch's current stream (the launch stream)."""
+    launch(0)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(reps):
+        launch(i % nsets)
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) * 1e3 / reps  # us
 
 
 def main():
@@ -186,7 +213,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--reps", type=int, default=30, help="reps per breakdown measurement")
+    ap.add_argument("--reps", type=int, default=40, help="launches per breakdown measurement")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip configs[4] (lowrank QKV) in the breakdown")
     args = ap.parse_args()
@@ -244,17 +271,19 @@ def main():
     print(f"[bench] {args.steps} steps: {ms_per_step:.4f} ms/step (events), wall {wall * 1e3 / args.steps:.4f} ms/step",
           file=sys.stderr, flush=True)
 
-    # per-config, per-direction launch timings (C ABI, events, flushed caches)
-    timer = AbiTimer(torch, dev)
+    # per-config, per-direction launch timings (C ABI, rotating cold input sets, HIP events)
+    del data
+    torch.cuda.empty_cache()
     breakdown = {}
     roofline = None
-    for name in data:
+    names = STEP + ([] if args.no_extra else list(EXTRA))
+    for name in names:
         c = CONFIGS.get(name) or EXTRA[name]
-        a, dy = data[name]
-        fwd, bwd = abi_launchers(c, a, dy, torch)
+        sets = abi_sets(c, torch, dev)
+        fwd, bwd = abi_launchers(c, sets, torch)
         calls = c.get("calls", 1)
-        f_us, _ = timer.time(fwd, args.reps)
-        b_us, b_all = timer.time(bwd, args.reps)
+        f_us = time_launches(torch, fwd, len(sets), args.reps)
+        b_us = time_launches(torch, bwd, len(sets), args.reps)
         fb, bb = alg_bytes(c)
         fb_us = f_us + b_us
         gbs = (fb + bb) / (fb_us * 1e-6) / 1e9
@@ -271,11 +300,13 @@ def main():
         if name == "hw_hs1":
             ach = bb / (b_us * 1e-6) / 1e9
             roofline = {
-                "kernel": "headwise backward, head_size 1 (hw_bwd_fast<bf16,4,1,static> + reduce_partials)",
+                "kernel": "headwise backward, head_size 1: hw_bwd_fast<bf16,W4,HSV1,static> + reduce_partials",
                 "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / PEAK_GBS, 4), "traffic": None,
-                "alg_bytes_per_launch": bb, "avg_launch_us": round(statistics.mean(b_all), 2),
+                "alg_bytes_per_launch": bb, "avg_launch_us": round(b_us, 2),
             }
+        del sets, fwd, bwd
+        torch.cuda.empty_cache()
 
     out = {
         "metric": METRIC,

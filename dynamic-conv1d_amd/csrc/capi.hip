@@ -6,7 +6,7 @@
 // probe below.
 #include <mutex>
 
-#include "../../include/dynconv.h"
+#include "dynconv.h"
 #include "dc_launch.h"
 
 namespace {

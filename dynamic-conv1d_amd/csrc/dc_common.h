@@ -58,6 +58,34 @@ __device__ __forceinline__ void store_vals(T* __restrict__ p, const float* in) {
   for (int i = 0; i < NU; ++i) q[i] = u[i];
 }
 
+// N elements of T held as raw load units (no conversion): used to keep
+// prefetched rows in flight while the previous rows are being computed.
+template <typename T, int N>
+struct Raw {
+  static constexpr int BYTES = N * (int)sizeof(T);
+  static constexpr int A = pow2_align(BYTES);
+  typedef typename Unit<A>::type U;
+  static constexpr int NU = BYTES / A;
+  U u[NU];
+  __device__ __forceinline__ void load(const T* __restrict__ p) {
+    const U* q = reinterpret_cast<const U*>(p);
+#pragma unroll
+    for (int i = 0; i < NU; ++i) u[i] = q[i];
+  }
+  __device__ __forceinline__ void zero() { __builtin_memset(u, 0, sizeof(u)); }
+  __device__ __forceinline__ float get(int i) const {
+    T e[N];
+    __builtin_memcpy(e, u, BYTES);
+    return (float)e[i];
+  }
+  __device__ __forceinline__ void to_float(float* out) const {
+    T e[N];
+    __builtin_memcpy(e, u, BYTES);
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = (float)e[i];
+  }
+};
+
 template <int N>
 __device__ __forceinline__ void zero_vals(float* v) {
 #pragma unroll
@@ -76,9 +104,22 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblk) {
   return (xcd < r) ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
 }
 
-// Sum over aligned groups of `n` lanes (n a power of two, 1..64).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of `n` lanes (n a power of two, 1..64), leaving the
+// group sum in every lane of the group.  Groups up to 16 lanes use DPP
+// (quad_perm xor 1, xor 2, row_half_mirror, row_mirror: each pairs a lane
+// with one of the other half of its group); 32 and 64 use ds_bpermute.
 __device__ __forceinline__ float group_sum(float v, int n) {
-  for (int m = 1; m < n; m <<= 1) v += __shfl_xor(v, m);
+  if (n >= 2) v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  if (n >= 4) v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  if (n >= 8) v += dpp_f<0x141>(v);  // row_half_mirror
+  if (n >= 16) v += dpp_f<0x140>(v); // row_mirror
+  if (n >= 32) v += __shfl_xor(v, 16);
+  if (n >= 64) v += __shfl_xor(v, 32);
   return v;
 }
 

@@ -116,8 +116,10 @@ int unroll_of(int W) { return W >= 4 ? W : W * (4 / W); }
 
 bool aligned(const void* p, int a) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-// Run length: aim for ~8 wavefronts per CU over 256 CUs (2048), at least one
-// unrolled chunk, a multiple of the unroll.
+// Run length: aim for `target_waves` wavefronts in total (1024 = one per
+// SIMD of the 256 CUs: with the next chunk always in flight, fewer and longer
+// runs measured faster than more, shorter ones), at least 16 rows, a
+// multiple of the unroll.
 int choose_seg(int64_t B, int64_t T, int64_t nvg, int W, int target_waves) {
   const int u = unroll_of(W);
   int64_t seg = (B * T * nvg + target_waves - 1) / target_waves;
@@ -138,7 +140,7 @@ HwPlan make_plan(const HwProblem& p, bool bwd) {
   a.hs_shift = ilog2(hs);
   a.nvc = (int)(p.D / VEC);
   a.nvg = (a.nvc + 63) / 64;
-  a.seg = choose_seg(p.B, p.T, a.nvg, (int)p.W, bwd ? 2048 : 4096);
+  a.seg = choose_seg(p.B, p.T, a.nvg, (int)p.W, 1024);
   a.nspb = (int)((p.T + a.seg - 1) / a.seg);
   a.nseg = (int)(p.B * a.nspb);
   const int nsg = (a.nseg + 3) / 4;

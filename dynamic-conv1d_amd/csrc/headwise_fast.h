@@ -62,42 +62,14 @@ __device__ __forceinline__ constexpr int ring(int u, int k) {
 }
 
 // ------------------------------------------------------------------ forward
-template <typename T, int W, int HSV, int U, bool GUARD>
-__device__ __forceinline__ void hw_fwd_rows(int tc, int t1, const T* __restrict__ xp, const T* __restrict__ wp,
-                                            T* __restrict__ yp, int64_t D, int64_t wrs,
-                                            float (&xr)[W][VecOf<T>::value],
-                                            const float (&swf)[W][VecOf<T>::value], int residual) {
-  constexpr int VEC = VecOf<T>::value;
-  constexpr int NWE = (VEC / HSV) * W;
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int t = tc + u;
-    if (GUARD && t >= t1) break;
-    const int p = u % W;
-    load_vals<T, VEC>(xp + (int64_t)t * D, xr[p]);
-    float wv[NWE];
-    load_vals<T, NWE>(wp + (int64_t)t * wrs, wv);
-    float acc[VEC];
-    zero_vals<VEC>(acc);
-#pragma unroll
-    for (int k = 0; k < W; ++k) {
-      const int q = ring<W>(u, k);
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) acc[j] = fmaf(wv[(j / HSV) * W + k] + swf[k][j], xr[q][j], acc[j]);
-    }
-    if (residual) {
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) acc[j] += xr[p][j];
-    }
-    store_vals<T, VEC>(yp + (int64_t)t * D, acc);
-  }
-}
-
 template <typename T, int W, int HSV>
 __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, const T* __restrict__ wt,
                                                    const T* __restrict__ sw, T* __restrict__ y, HwArgs a) {
   constexpr int VEC = VecOf<T>::value;
+  constexpr int NWE = (VEC / HSV) * W;
   constexpr int U = Unroll<W>::value;
+  typedef Raw<T, VEC> XR;
+  typedef Raw<T, NWE> WR;
   const int lb = xcd_remap(blockIdx.x, a.nblk);
   const int vg = lb % a.nvg, sgp = lb / a.nvg;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -116,113 +88,89 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
   const T* wp = wt + (row0 * a.H + h0) * W;
   T* yp = y + row0 * D + d0;
 
-  float swf[W][VEC];
+  XR swr[W];
 #pragma unroll
   for (int k = 0; k < W; ++k) {
     if (a.has_static)
-      load_vals<T, VEC>(sw + (int64_t)k * D + d0, swf[k]);
+      swr[k].load(sw + (int64_t)k * D + d0);
     else
-      zero_vals<VEC>(swf[k]);
+      swr[k].zero();
   }
-  float xr[W][VEC];
-  zero_vals<VEC>(xr[0]);
+  // x ring: row t lives in slot (t - t0) mod W.
+  XR xr[W];
+  xr[0].zero();
 #pragma unroll
   for (int i = 1; i < W; ++i) {
     const int t = t0 - i;
     if (t >= 0)
-      load_vals<T, VEC>(xp + (int64_t)t * D, xr[W - i]);
+      xr[W - i].load(xp + (int64_t)t * D);
     else
-      zero_vals<VEC>(xr[W - i]);
+      xr[W - i].zero();
+  }
+  // Rows of the current chunk and, in flight meanwhile, of the next one.
+  XR xc[U], xn[U];
+  WR wc[U], wn[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int t = t0 + u;
+    if (t < t1) {
+      xc[u].load(xp + (int64_t)t * D);
+      wc[u].load(wp + (int64_t)t * wrs);
+    }
   }
   for (int tc = t0; tc < t1; tc += U) {
-    if (tc + U <= t1)
-      hw_fwd_rows<T, W, HSV, U, false>(tc, t1, xp, wp, yp, D, wrs, xr, swf, a.residual);
-    else
-      hw_fwd_rows<T, W, HSV, U, true>(tc, t1, xp, wp, yp, D, wrs, xr, swf, a.residual);
+    if (tc + U < t1) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int t = tc + U + u;
+        if (t < t1) {
+          xn[u].load(xp + (int64_t)t * D);
+          wn[u].load(wp + (int64_t)t * wrs);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = tc + u;
+      if (t < t1) {
+        const int p = u % W;
+        xr[p] = xc[u];
+        float acc[VEC];
+        zero_vals<VEC>(acc);
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          const int q = ring<W>(u, k);
+#pragma unroll
+          for (int j = 0; j < VEC; ++j)
+            acc[j] = fmaf(wc[u].get((j / HSV) * W + k) + swr[k].get(j), xr[q].get(j), acc[j]);
+        }
+        if (a.residual) {
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) acc[j] += xr[p].get(j);
+        }
+        store_vals<T, VEC>(yp + (int64_t)t * D, acc);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      xc[u] = xn[u];
+      wc[u] = wn[u];
+    }
   }
 }
 
 // ----------------------------------------------------------------- backward
-template <typename T, int W, int HSV, bool HAS_STATIC, int U, bool GUARD>
-__device__ __forceinline__ void hw_bwd_rows(int tc, int tend, int t0, int t1, int Tn, const T* __restrict__ xp,
-                                            const T* __restrict__ wp, const T* __restrict__ dyp,
-                                            T* __restrict__ dxp, T* __restrict__ dwp, int64_t D, int64_t wrs,
-                                            float (&xr)[W][VecOf<T>::value],
-                                            float (&dxa)[W][VecOf<T>::value],
-                                            float (&dsw)[W][VecOf<T>::value],
-                                            const float (&swf)[W][VecOf<T>::value], int residual, int lph,
-                                            bool leader) {
-  constexpr int VEC = VecOf<T>::value;
-  constexpr int NHL = VEC / HSV;
-  constexpr int NWE = NHL * W;
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int t = tc + u;
-    if (GUARD && t >= tend) break;
-    const int p = u % W;
-    const bool main_row = t < t1;
-    float dyv[VEC], wv[NWE];
-    if (t < Tn) {
-      load_vals<T, VEC>(dyp + (int64_t)t * D, dyv);
-      load_vals<T, NWE>(wp + (int64_t)t * wrs, wv);
-    } else {
-      zero_vals<VEC>(dyv);
-      zero_vals<NWE>(wv);
-    }
-    if (main_row) load_vals<T, VEC>(xp + (int64_t)t * D, xr[p]);
-
-    // dx[t-k] += dy[t] * (w[t, h, k] + sw[k]); row t opens with its k = 0 term.
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      const float v = dyv[j] * (wv[(j / HSV) * W] + swf[0][j]);
-      dxa[p][j] = residual ? v + dyv[j] : v;
-    }
-#pragma unroll
-    for (int k = 1; k < W; ++k) {
-      const int q = ring<W>(u, k);
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) dxa[q][j] = fmaf(dyv[j], wv[(j / HSV) * W + k] + swf[k][j], dxa[q][j]);
-    }
-
-    if (main_row) {
-      float dwv[NWE];
-#pragma unroll
-      for (int k = 0; k < W; ++k) {
-        const int q = ring<W>(u, k);
-        float pr[VEC];
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) pr[j] = dyv[j] * xr[q][j];
-        if (HAS_STATIC) {
-#pragma unroll
-          for (int j = 0; j < VEC; ++j) dsw[k][j] += pr[j];
-        }
-#pragma unroll
-        for (int hh = 0; hh < NHL; ++hh) {
-          float sacc = 0.f;
-#pragma unroll
-          for (int j = 0; j < HSV; ++j) sacc += pr[hh * HSV + j];
-          dwv[hh * W + k] = sacc;
-        }
-      }
-      if (lph > 1) {
-#pragma unroll
-        for (int k = 0; k < NWE; ++k) dwv[k] = group_sum(dwv[k], lph);
-      }
-      if (leader) store_vals<T, NWE>(dwp + (int64_t)t * wrs, dwv);
-    }
-
-    const int tdone = t - (W - 1);
-    if (tdone >= t0 && tdone < t1) store_vals<T, VEC>(dxp + (int64_t)tdone * D, dxa[(u + 1) % W]);
-  }
-}
-
 template <typename T, int W, int HSV, bool HAS_STATIC>
 __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, const T* __restrict__ wt,
                                                    const T* __restrict__ sw, const T* __restrict__ dy,
                                                    T* __restrict__ dx, T* __restrict__ dwt,
                                                    float* __restrict__ part, HwArgs a) {
   constexpr int VEC = VecOf<T>::value;
+  constexpr int NHL = VEC / HSV;
+  constexpr int NWE = NHL * W;
   constexpr int U = Unroll<W>::value;
+  typedef Raw<T, VEC> XR;
+  typedef Raw<T, NWE> WR;
   const int lb = xcd_remap(blockIdx.x, a.nblk);
   const int vg = lb % a.nvg, sgp = lb / a.nvg;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -241,6 +189,8 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
     const int b = s / a.nspb;
     const int t0 = (s - b * a.nspb) * a.seg;
     const int t1 = min(t0 + a.seg, a.Tn);
+    const int tend = t1 + W - 1;        // steps t0 .. tend-1: dx of row t needs dy, w of rows t .. t+W-1
+    const int tload = min(tend, a.Tn);  // dy / w rows that exist
     const int d0 = vc * VEC;
     const int h0 = d0 >> a.hs_shift;
     const int64_t row0 = (int64_t)b * a.Tn;
@@ -252,35 +202,116 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
     T* dxp = dx + row0 * D + d0;
     T* dwp = dwt + (row0 * a.H + h0) * W;
     const bool leader = (vc & (a.lph - 1)) == 0;
+    const int residual = a.residual, lph = a.lph;
 
-    float swf[W][VEC];
+    XR swr[W];
 #pragma unroll
     for (int k = 0; k < W; ++k) {
       if (HAS_STATIC)
-        load_vals<T, VEC>(sw + (int64_t)k * D + d0, swf[k]);
+        swr[k].load(sw + (int64_t)k * D + d0);
       else
-        zero_vals<VEC>(swf[k]);
+        swr[k].zero();
     }
-    float xr[W][VEC], dxa[W][VEC];
+    XR xr[W];
+    float dxa[W][VEC];
 #pragma unroll
     for (int k = 0; k < W; ++k) zero_vals<VEC>(dxa[k]);
-    zero_vals<VEC>(xr[0]);
+    xr[0].zero();
 #pragma unroll
     for (int i = 1; i < W; ++i) {
       const int t = t0 - i;
       if (t >= 0)
-        load_vals<T, VEC>(xp + (int64_t)t * D, xr[W - i]);
+        xr[W - i].load(xp + (int64_t)t * D);
       else
-        zero_vals<VEC>(xr[W - i]);
+        xr[W - i].zero();
     }
-    const int tend = t1 + W - 1;
+    XR dyc[U], dyn[U], xc[U], xn[U];
+    WR wc[U], wn[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = t0 + u;
+      if (t < tload) {
+        dyc[u].load(dyp + (int64_t)t * D);
+        wc[u].load(wp + (int64_t)t * wrs);
+      } else {
+        dyc[u].zero();
+        wc[u].zero();
+      }
+      if (t < t1) xc[u].load(xp + (int64_t)t * D);
+    }
     for (int tc = t0; tc < tend; tc += U) {
-      if (tc + U <= tend)
-        hw_bwd_rows<T, W, HSV, HAS_STATIC, U, false>(tc, tend, t0, t1, a.Tn, xp, wp, dyp, dxp, dwp, D, wrs, xr,
-                                                     dxa, dsw, swf, a.residual, a.lph, leader);
-      else
-        hw_bwd_rows<T, W, HSV, HAS_STATIC, U, true>(tc, tend, t0, t1, a.Tn, xp, wp, dyp, dxp, dwp, D, wrs, xr,
-                                                    dxa, dsw, swf, a.residual, a.lph, leader);
+      if (tc + U < tend) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int t = tc + U + u;
+          if (t < tload) {
+            dyn[u].load(dyp + (int64_t)t * D);
+            wn[u].load(wp + (int64_t)t * wrs);
+          } else {
+            dyn[u].zero();
+            wn[u].zero();
+          }
+          if (t < t1) xn[u].load(xp + (int64_t)t * D);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int t = tc + u;
+        if (t < tend) {
+          const int p = u % W;
+          const bool main_row = t < t1;
+          float dyv[VEC];
+          dyc[u].to_float(dyv);
+          // dx[t-k] += dy[t] * (w[t, h, k] + sw[k]); row t opens with its k = 0 term.
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) {
+            const float v = dyv[j] * (wc[u].get((j / HSV) * W) + swr[0].get(j));
+            dxa[p][j] = residual ? v + dyv[j] : v;
+          }
+#pragma unroll
+          for (int k = 1; k < W; ++k) {
+            const int q = ring<W>(u, k);
+#pragma unroll
+            for (int j = 0; j < VEC; ++j)
+              dxa[q][j] = fmaf(dyv[j], wc[u].get((j / HSV) * W + k) + swr[k].get(j), dxa[q][j]);
+          }
+          if (main_row) {
+            xr[p] = xc[u];
+            float dwv[NWE];
+#pragma unroll
+            for (int k = 0; k < W; ++k) {
+              const int q = ring<W>(u, k);
+              float pr[VEC];
+#pragma unroll
+              for (int j = 0; j < VEC; ++j) pr[j] = dyv[j] * xr[q].get(j);
+              if (HAS_STATIC) {
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) dsw[k][j] += pr[j];
+              }
+#pragma unroll
+              for (int hh = 0; hh < NHL; ++hh) {
+                float sacc = 0.f;
+#pragma unroll
+                for (int j = 0; j < HSV; ++j) sacc += pr[hh * HSV + j];
+                dwv[hh * W + k] = sacc;
+              }
+            }
+            if (lph > 1) {
+#pragma unroll
+              for (int k = 0; k < NWE; ++k) dwv[k] = group_sum(dwv[k], lph);
+            }
+            if (leader) store_vals<T, NWE>(dwp + (int64_t)t * wrs, dwv);
+          }
+          const int tdone = t - (W - 1);
+          if (tdone >= t0 && tdone < t1) store_vals<T, VEC>(dxp + (int64_t)tdone * D, dxa[(u + 1) % W]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        dyc[u] = dyn[u];
+        wc[u] = wn[u];
+        xc[u] = xn[u];
+      }
     }
   }
 

@@ -47,6 +47,12 @@ template <> struct Mma16<fp16> {
   }
 };
 
+// 16-bit element j (0..3) of a 64-bit quartet, in the low half of a word.
+__device__ __forceinline__ uint32_t elem16x2(const u32x2& v, int j) {
+  const uint32_t w = v[j >> 1];
+  return (j & 1) ? (w >> 16) : (w & 0xFFFFu);
+}
+
 // 16-bit element j (0..7) of a 128-bit row piece, in the low half of a word.
 __device__ __forceinline__ uint32_t elem16(const u32x4& v, int j) {
   const uint32_t w = v[j >> 1];
@@ -56,6 +62,23 @@ __device__ __forceinline__ uint32_t elem16(const u32x4& v, int j) {
 template <typename T>
 __device__ __forceinline__ uint32_t f2bits(float f) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (T)f);
+}
+
+template <typename T> struct Pair16;
+template <> struct Pair16<bf16> { typedef __bf16 type __attribute__((ext_vector_type(2))); };
+template <> struct Pair16<fp16> { typedef _Float16 type __attribute__((ext_vector_type(2))); };
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two floats rounded to nearest-even into one word (a in the low half): v_cvt_pk_{bf16,f16}_f32.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, typename Pair16<T>::type));
+}
+// Element j (0..3) of a 64-bit quartet as float.
+template <typename T>
+__device__ __forceinline__ float q4f(const u32x2& v, int j) {
+  return Mma16<T>::to_f(elem16x2(v, j));
 }
 
 struct LrArgs {
@@ -239,25 +262,87 @@ struct LrBwdArgs {
   int64_t BT;
 };
 
-__device__ __forceinline__ uint32_t elem16x2(const u32x2& v, int j) {
-  const uint32_t w = v[j >> 1];
-  return (j & 1) ? (w >> 16) : (w & 0xFFFFu);
+
+// Packed U_eff operands of one wavefront's 64-channel chunk, staged once in
+// LDS (the chunk never changes across the run): for tap k, rank chunk c and
+// column j, lane (q, n) reads
+//   uw: ranks 16c+4q..16c+4q+3 of channel 4n+j  (B operand of the tap weights)
+//   uz: rank 16c+n of channels 16q+j, 16q+4+j, 16q+8+j, 16q+12+j  (B operand of dz)
+// Slot ((k*RC + c)*4 + j)*2 + {0: uw, 1: uz}, 64 lanes x 8 bytes each.
+template <int W, int RC>
+__device__ __forceinline__ void stage_uops(u32x2* __restrict__ lds, const uint16_t* __restrict__ U,
+                                           const uint16_t* __restrict__ sw, int R, int RK, int D, int d0, int q,
+                                           int n, int lane) {
+  const int64_t WD = (int64_t)W * D;
+  const bool chv = d0 + 4 * n < D, grpv = d0 + 16 * q < D;
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+      u32x2 rows[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int r = 16 * c + 4 * q + kk;
+        const uint16_t* src = nullptr;
+        if (chv && r < R) src = U + (int64_t)r * WD + (int64_t)k * D + d0 + 4 * n;
+        else if (chv && r < RK) src = sw + (int64_t)k * D + d0 + 4 * n;
+        rows[kk] = src ? *reinterpret_cast<const u32x2*>(src) : u32x2{0u, 0u};
+      }
+      const int r = 16 * c + n;
+      const uint16_t* src = nullptr;
+      if (grpv && r < R) src = U + (int64_t)r * WD + (int64_t)k * D + d0 + 16 * q;
+      else if (grpv && r < RK) src = sw + (int64_t)k * D + d0 + 16 * q;
+      const u32x4 v0 = src ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
+      const u32x4 v1 = src ? *reinterpret_cast<const u32x4*>(src + 8) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u32x2 uw, uz;
+        uw[0] = elem16x2(rows[0], j) | (elem16x2(rows[1], j) << 16);
+        uw[1] = elem16x2(rows[2], j) | (elem16x2(rows[3], j) << 16);
+        uz[0] = elem16(v0, j) | (elem16(v0, 4 + j) << 16);
+        uz[1] = elem16(v1, j) | (elem16(v1, 4 + j) << 16);
+        const int slot = ((k * RC + c) * 4 + j) * 2;
+        lds[slot * 64 + lane] = uw;
+        lds[(slot + 1) * 64 + lane] = uz;
+      }
+    }
+  }
 }
 
+// Raw buffer resources.  A descriptor covers one sequence ([T, C] elements);
+// the hardware returns 0 for loads and drops stores whose VGPR byte offset is
+// >= the range, which handles rows before 0 (negative offsets wrap to large
+// unsigned values), rows past T and channels past D (lane offset kOobLane)
+// without branches or clamped addresses.  The host only takes this path when
+// one sequence spans at most kMaxSeqBytes, so no offset can wrap back into range.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kOobLane = 0x60000000;
+constexpr int64_t kMaxSeqBytes = int64_t(1) << 29;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x2 bload64(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0); }
+__device__ __forceinline__ uint32_t bload16(rsrc_t r, int off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+__device__ __forceinline__ void bstore64(u32x2 v, rsrc_t r, int off) { __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 0); }
+
 template <typename T, int W, int RC>
-__global__ __launch_bounds__(256) void lr_bwd_mfma(const T* __restrict__ x_, const T* __restrict__ z_,
-                                                   const T* __restrict__ U_, const T* __restrict__ sw_,
-                                                   const T* __restrict__ dy_, T* __restrict__ dx_,
-                                                   float* __restrict__ part_dz, float* __restrict__ part_du,
-                                                   LrBwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W * RC <= 4 ? 2 : 1, 8))) void lr_bwd_mfma(
+    const T* __restrict__ x_, const T* __restrict__ z_, const T* __restrict__ U_, const T* __restrict__ sw_,
+    const T* __restrict__ dy_, T* __restrict__ dx_, float* __restrict__ part_dz, float* __restrict__ part_du,
+    LrBwdArgs a) {
   constexpr int NB = (W + 6) / 4;  // MFMA row blocks for the dx look-ahead
-  constexpr int NR = W + 3;        // rows of x (4q-W+1 ..) and dy (4q ..) per lane
+  constexpr int NR = W + 3;        // x rows 4q-W+1 .. 4q+3 and dy rows 4q .. 4q+W+2 per lane
+  constexpr int NSLOT = W * RC * 4 * 2;
   const uint16_t* __restrict__ x = reinterpret_cast<const uint16_t*>(x_);
   const uint16_t* __restrict__ z = reinterpret_cast<const uint16_t*>(z_);
   const uint16_t* __restrict__ U = reinterpret_cast<const uint16_t*>(U_);
   const uint16_t* __restrict__ sw = reinterpret_cast<const uint16_t*>(sw_);
   const uint16_t* __restrict__ dy = reinterpret_cast<const uint16_t*>(dy_);
   uint16_t* __restrict__ dx = reinterpret_cast<uint16_t*>(dx_);
+  __shared__ u32x2 uops[4][NSLOT * 64];
   __shared__ float dzred[2][4][RC * 256];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -265,16 +350,28 @@ __global__ __launch_bounds__(256) void lr_bwd_mfma(const T* __restrict__ x_, con
   const int lb = xcd_remap(blockIdx.x, a.nblk);
   const int cg = lb % a.ncg, sg = lb / a.ncg;
   const int chunk = cg * 4 + wave;
-  const int D = a.D;
+  const int D = a.D, Tn = a.Tn;
   const int d0 = chunk * 64;
-  const bool chv = d0 + 4 * n < D;           // lane quartet inside D (D % 16 == 0)
-  const bool grpv = d0 + 16 * q < D;         // lane's 16-channel dz group inside D
+  const bool chv = d0 + 4 * n < D;  // lane quartet inside D (D % 16 == 0)
+  const int col = d0 + 4 * n;
   const int64_t WD = (int64_t)W * D;
   const int b = sg / a.nspb;
-  const int ntile = (a.Tn + 15) >> 4;
+  const int ntile = (Tn + 15) >> 4;
   const int tile0 = (sg - b * a.nspb) * a.seg;
   const int tile1 = min(tile0 + a.seg, ntile);
-  const int64_t row0 = (int64_t)b * a.Tn;
+  const int64_t row0 = (int64_t)b * Tn;
+  const int R = a.R, RK = a.RK;
+  const bool zvec = (R & 3) == 0;
+  u32x2* __restrict__ myops = uops[wave];
+  const int rowb = D * 2;
+  const int64_t seqb = (int64_t)Tn * rowb;
+  const rsrc_t rx = make_rsrc(x + row0 * D, seqb);
+  const rsrc_t rdy = make_rsrc(dy + row0 * D, seqb);
+  const rsrc_t rdx = make_rsrc(dx + row0 * D, seqb);
+  const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 2);
+  const int lane_off = chv ? (4 * q * D + col) * 2 : kOobLane;  // byte offset of the lane's row 4q quartet
+
+  stage_uops<W, RC>(myops, U, sw, R, RK, D, d0, q, n, lane);
 
   // Identity as the B operand: lane (q, n) gives rows 4q..4q+3 of column n.
   u32x2 ident;
@@ -297,44 +394,52 @@ __global__ __launch_bounds__(256) void lr_bwd_mfma(const T* __restrict__ x_, con
 
   for (int tile = tile0; tile < tile1; ++tile) {
     const int t0 = tile * 16;
-    // ---- operand loads
+    // ---- tile inputs (buffer loads: out-of-range rows / channels read as 0)
+    const int toff = t0 * rowb;
     u32x2 xr[NR], dyr[NR];
 #pragma unroll
     for (int m = 0; m < NR; ++m) {
-      const int tx = t0 + 4 * q - (W - 1) + m;
-      const int td = t0 + 4 * q + m;
-      xr[m] = (chv && tx >= 0 && tx < a.Tn) ? *reinterpret_cast<const u32x2*>(x + (row0 + tx) * D + d0 + 4 * n)
-                                            : u32x2{0u, 0u};
-      dyr[m] = (chv && td < a.Tn) ? *reinterpret_cast<const u32x2*>(dy + (row0 + td) * D + d0 + 4 * n)
-                                  : u32x2{0u, 0u};
+      xr[m] = bload64(rx, lane_off + toff + (m - (W - 1)) * rowb);
+      dyr[m] = bload64(rdy, lane_off + toff + m * rowb);
     }
-    // z_eff rows as the A operand of the tap-weight MFMAs (row blocks shifted by 4).
+    // z_eff rows t0+4bb+n, ranks 16c+4q..+3: A operand of the tap-weight MFMA.
     u32x2 zA[NB][RC];
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb) {
       const int t = t0 + 4 * bb + n;
 #pragma unroll
       for (int c = 0; c < RC; ++c) {
-        uint32_t e[4];
+        const int r0 = 16 * c + 4 * q;
+        if (zvec && r0 + 3 < R) {  // 4 dynamic ranks, 8-byte aligned (R % 4 == 0)
+          zA[bb][c] = bload64(rz, (t * R + r0) * 2);
+        } else {
+          uint32_t e[4];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) e[kk] = t < a.Tn ? zbits<T>(z, row0 + t, a.R, a.RK, 16 * c + 4 * q + kk) : 0u;
-        zA[bb][c][0] = e[0] | (e[1] << 16);
-        zA[bb][c][1] = e[2] | (e[3] << 16);
+          for (int kk = 0; kk < 4; ++kk) {
+            const int r = r0 + kk;
+            const uint32_t v = bload16(rz, (t * R + min(r, R - 1)) * 2);
+            e[kk] = r < R ? v : ((r < RK && t < Tn) ? (uint32_t)Mma16<T>::kOne : 0u);
+          }
+          zA[bb][c][0] = e[0] | (e[1] << 16);
+          zA[bb][c][1] = e[2] | (e[3] << 16);
+        }
       }
     }
-    // z_eff transposed as the A operand of the dU MFMA: rank n, rows 4q..4q+3.
+    // z_eff transposed (rank n, rows 4q..4q+3), the A operand of the dU MFMA,
+    // from row block 0 through the exact identity transpose.
     u32x2 zT[RC];
 #pragma unroll
     for (int c = 0; c < RC; ++c) {
-      uint32_t e[4];
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int t = t0 + 4 * q + kk;
-        e[kk] = t < a.Tn ? zbits<T>(z, row0 + t, a.R, a.RK, 16 * c + n) : 0u;
-      }
-      zT[c][0] = e[0] | (e[1] << 16);
-      zT[c][1] = e[2] | (e[3] << 16);
+      const f32x4 tz = Mma16<T>::run(zA[0][c], ident, f32x4{0.f, 0.f, 0.f, 0.f});
+      zT[c][0] = pack2<T>(tz[0], tz[1]);
+      zT[c][1] = pack2<T>(tz[2], tz[3]);
     }
+
+    float dyf[NR][4];
+#pragma unroll
+    for (int m = 0; m < NR; ++m)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dyf[m][j] = q4f<T>(dyr[m], j);
 
     float dxa[4][4];
 #pragma unroll
@@ -347,93 +452,49 @@ __global__ __launch_bounds__(256) void lr_bwd_mfma(const T* __restrict__ x_, con
 
 #pragma unroll
     for (int k = 0; k < W; ++k) {
-      // U_eff operands of tap k (L1-resident: 64 channels x W x RK per wavefront).
-      u32x2 uw[RC][4];  // tap weights (B): ranks 16c+4q+kk, column 4n+j
-      u32x2 uz[RC][4];  // dz (B): rank 16c+n, channels 16q + 4kk + j
-#pragma unroll
-      for (int c = 0; c < RC; ++c) {
-        u32x2 rows[4];
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const int r = 16 * c + 4 * q + kk;
-          const uint16_t* src = nullptr;
-          if (chv && r < a.R) src = U + (int64_t)r * WD + (int64_t)k * D + d0 + 4 * n;
-          else if (chv && r < a.RK) src = sw + (int64_t)k * D + d0 + 4 * n;
-          rows[kk] = src ? *reinterpret_cast<const u32x2*>(src) : u32x2{0u, 0u};
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          uw[c][j][0] = elem16x2(rows[0], j) | (elem16x2(rows[1], j) << 16);
-          uw[c][j][1] = elem16x2(rows[2], j) | (elem16x2(rows[3], j) << 16);
-        }
-        const int r = 16 * c + n;
-        const uint16_t* src = nullptr;
-        if (grpv && r < a.R) src = U + (int64_t)r * WD + (int64_t)k * D + d0 + 16 * q;
-        else if (grpv && r < a.RK) src = sw + (int64_t)k * D + d0 + 16 * q;
-        const u32x4 v0 = src ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
-        const u32x4 v1 = src ? *reinterpret_cast<const u32x4*>(src + 8) : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          uz[c][j][0] = elem16(v0, j) | (elem16(v0, 4 + j) << 16);
-          uz[c][j][1] = elem16(v1, j) | (elem16(v1, 4 + j) << 16);
-        }
-      }
-      // dx += dy[4q+i+k] * Kw[4q+i+k, k]: tap weights of the row blocks that hold rows k..k+3.
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
+        // dx += dy[4q+i+k] * Kw[4q+i+k, k]: tap weights of the row blocks that hold rows k..k+3.
 #pragma unroll
         for (int bb = 0; bb < NB; ++bb) {
           if (4 * bb > 3 + k || 4 * bb + 3 < k) continue;
           f32x4 wk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int c = 0; c < RC; ++c) wk = Mma16<T>::run(zA[bb][c], uw[c][j], wk);
+          for (int c = 0; c < RC; ++c)
+            wk = Mma16<T>::run(zA[bb][c], myops[(((k * RC + c) * 4 + j) * 2) * 64 + lane], wk);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int tr = i + k;  // row offset of dy / Kw in the lane window
-            if (tr >= 4 * bb && tr < 4 * bb + 4)
-              dxa[i][j] = fmaf(Mma16<T>::to_f(elem16x2(dyr[tr], j)), wk[tr - 4 * bb], dxa[i][j]);
+            if (tr >= 4 * bb && tr < 4 * bb + 4) dxa[i][j] = fmaf(dyf[tr][j], wk[tr - 4 * bb], dxa[i][j]);
           }
         }
-      }
-      // G_k = bf16(dy * x_shift), packed per column j as rows 4q..4q+3.
-      u32x2 g[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t e[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          e[i] = f2bits<T>(Mma16<T>::to_f(elem16x2(dyr[i], j)) * Mma16<T>::to_f(elem16x2(xr[i - k + W - 1], j)));
-        g[j][0] = e[0] | (e[1] << 16);
-        g[j][1] = e[2] | (e[3] << 16);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
+        // G_k = bf16(dy * x_shift) of column j, rows 4q..4q+3: the B operand of dU.
+        u32x2 g;
+        g[0] = pack2<T>(dyf[0][j] * q4f<T>(xr[0 - k + W - 1], j), dyf[1][j] * q4f<T>(xr[1 - k + W - 1], j));
+        g[1] = pack2<T>(dyf[2][j] * q4f<T>(xr[2 - k + W - 1], j), dyf[3][j] * q4f<T>(xr[3 - k + W - 1], j));
         // dU (K = rows); exact transpose of G_j; dz (K = channels).
 #pragma unroll
-        for (int c = 0; c < RC; ++c) du[k][c][j] = Mma16<T>::run(zT[c], g[j], du[k][c][j]);
-        const f32x4 tr = Mma16<T>::run(g[j], ident, f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int c = 0; c < RC; ++c) du[k][c][j] = Mma16<T>::run(zT[c], g, du[k][c][j]);
+        const f32x4 tr = Mma16<T>::run(g, ident, f32x4{0.f, 0.f, 0.f, 0.f});
         u32x2 ga;
-        ga[0] = f2bits<T>(tr[0]) | (f2bits<T>(tr[1]) << 16);
-        ga[1] = f2bits<T>(tr[2]) | (f2bits<T>(tr[3]) << 16);
+        ga[0] = pack2<T>(tr[0], tr[1]);
+        ga[1] = pack2<T>(tr[2], tr[3]);
 #pragma unroll
-        for (int c = 0; c < RC; ++c) dz[c] = Mma16<T>::run(ga, uz[c][j], dz[c]);
+        for (int c = 0; c < RC; ++c)
+          dz[c] = Mma16<T>::run(ga, myops[(((k * RC + c) * 4 + j) * 2 + 1) * 64 + lane], dz[c]);
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- dx rows 4q..4q+3 (+ residual dy)
+    // ---- dx rows 4q..4q+3 (+ residual dy); out-of-range stores are dropped
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int t = t0 + 4 * q + i;
-      if (chv && t < a.Tn) {
-        u32x2 o;
-        float v[4];
+      float v[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = a.residual ? dxa[i][j] + Mma16<T>::to_f(elem16x2(dyr[i], j)) : dxa[i][j];
-        o[0] = f2bits<T>(v[0]) | (f2bits<T>(v[1]) << 16);
-        o[1] = f2bits<T>(v[2]) | (f2bits<T>(v[3]) << 16);
-        *reinterpret_cast<u32x2*>(dx + (row0 + t) * D + d0 + 4 * n) = o;
-      }
+      for (int j = 0; j < 4; ++j) v[j] = a.residual ? dxa[i][j] + dyf[i][j] : dxa[i][j];
+      u32x2 o;
+      o[0] = pack2<T>(v[0], v[1]);
+      o[1] = pack2<T>(v[2], v[3]);
+      bstore64(o, rdx, lane_off + toff + i * rowb);
     }
     // ---- dz: sum the 4 chunk wavefronts of this tile in LDS, one partial per group
     const int par = tile & 1;
@@ -447,7 +508,7 @@ __global__ __launch_bounds__(256) void lr_bwd_mfma(const T* __restrict__ x_, con
       const int r = 16 * c + nn;
       const int t = t0 + rr;
       const float v = ((dzred[par][0][e] + dzred[par][1][e]) + dzred[par][2][e]) + dzred[par][3][e];
-      if (r < a.R && t < a.Tn) part_dz[((int64_t)cg * a.BT + row0 + t) * a.R + r] = v;
+      if (r < R && t < Tn) part_dz[((int64_t)cg * a.BT + row0 + t) * R + r] = v;
     }
   }
 
@@ -461,8 +522,7 @@ __global__ __launch_bounds__(256) void lr_bwd_mfma(const T* __restrict__ x_, con
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = 16 * c + 4 * q + i;
-          const int d = d0 + 4 * n + j;
-          if (r < a.RK && chv) part_du[((int64_t)sg * a.RK + r) * WD + (int64_t)k * D + d] = du[k][c][j][i];
+          if (r < RK && chv) part_du[((int64_t)sg * RK + r) * WD + (int64_t)k * D + col + j] = du[k][c][j][i];
         }
 }
 
@@ -596,6 +656,7 @@ bool lr_mfma_ok_impl(const LrProblem& p, bool bwd) {
     return aligned16(p.x) && aligned16(p.U) && aligned16(p.static_w) && aligned16(p.y);
   }
   if (p.D % 16 != 0) return false;
+  if (p.T * p.D * 2 > kMaxSeqBytes) return false;  // buffer-offset range of one sequence
   return aligned8(p.x) && aligned8(p.dy) && aligned8(p.dx) && aligned16(p.U) && aligned16(p.static_w);
 }
 
