@@ -122,6 +122,20 @@ def cpu_baseline(torch):
 MALL_BYTES = 256 << 20
 
 
+def measured_traffic(kernel_key):
+    """HBM bytes per dispatch of a kernel from the committed rocprofv3 counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            kernels = json.load(f)["kernels"]
+    except (OSError, ValueError, KeyError):
+        return None
+    for name, t in kernels.items():
+        if kernel_key in name:
+            return round(t["read_bytes"] + t["write_bytes"])
+    return None
+
+
 def n_sets(c):
     """Independent input/output sets to rotate so each launch finds its data out of the 256 MB MALL."""
     fb, _ = alg_bytes(c)
@@ -302,7 +316,8 @@ def main():
             roofline = {
                 "kernel": "headwise backward, head_size 1: hw_bwd_fast<bf16,W4,HSV1,static> + reduce_partials",
                 "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_GBS, 4), "traffic": None,
+                "frac": round(ach / PEAK_GBS, 4), "traffic": measured_traffic("hw_bwd_fastIDF16bLi4ELi1ELb1"),
+                "traffic_source": "profiles/bench_hbm_traffic.md (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
                 "alg_bytes_per_launch": bb, "avg_launch_us": round(b_us, 2),
             }
         del sets, fwd, bwd

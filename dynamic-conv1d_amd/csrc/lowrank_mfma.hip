@@ -329,7 +329,7 @@ __device__ __forceinline__ uint32_t bload16(rsrc_t r, int off) {
 __device__ __forceinline__ void bstore64(u32x2 v, rsrc_t r, int off) { __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 0); }
 
 template <typename T, int W, int RC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W * RC <= 4 ? 2 : 1, 8))) void lr_bwd_mfma(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W * RC <= 4 && RC <= 2 ? 2 : 1, 8))) void lr_bwd_mfma(
     const T* __restrict__ x_, const T* __restrict__ z_, const T* __restrict__ U_, const T* __restrict__ sw_,
     const T* __restrict__ dy_, T* __restrict__ dx_, float* __restrict__ part_dz, float* __restrict__ part_du,
     LrBwdArgs a) {
