@@ -65,4 +65,14 @@ hipError_t lr_bwd(const LrProblem& p);
 hipError_t reduce_partials(const float* part, int64_t pstride, int P, int64_t C, void* out, int dtype,
                            hipStream_t stream);
 
+// Up to three such reductions in one launch (jobs with C <= 0 are skipped).
+struct PartialReduce {
+  const float* part;
+  int64_t pstride;
+  int P;
+  int64_t C;
+  void* out;
+};
+hipError_t reduce_partials_multi(const PartialReduce* r, int n, int dtype, hipStream_t stream);
+
 }  // namespace dc

@@ -167,9 +167,11 @@ hipError_t bwd_generic(const LrProblem& p) {
                                                    (int)p.T, (int)p.D, (int)p.R, RK, (int)p.W, rows_per);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  e = reduce_partials(p.ws, RK * WD, P, p.R * WD, p.dU, p.dtype, p.stream);
-  if (e != hipSuccess || !p.static_w) return e;
-  return reduce_partials(p.ws + p.R * WD, RK * WD, P, WD, p.dstatic_w, p.dtype, p.stream);
+  const PartialReduce jobs[2] = {
+      {p.ws, RK * WD, P, p.R * WD, p.dU},
+      {p.ws + p.R * WD, RK * WD, P, p.static_w ? WD : 0, p.dstatic_w},
+  };
+  return reduce_partials_multi(jobs, 2, p.dtype, p.stream);
 }
 
 }  // namespace

@@ -47,6 +47,23 @@ template <> struct Mma16<fp16> {
   }
 };
 
+// v_mfma_f32_16x16x32 (gfx950): lane l gives A[l%16][8(l/16)..+7] and B[8(l/16)..+7][l%16].
+typedef __bf16 b16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+template <typename T> struct Mma32;
+template <> struct Mma32<bf16> {
+  __device__ static __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b16x8, a), __builtin_bit_cast(b16x8, b), c, 0, 0,
+                                                   0);
+  }
+};
+template <> struct Mma32<fp16> {
+  __device__ static __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h16x8, a), __builtin_bit_cast(h16x8, b), c, 0, 0,
+                                                  0);
+  }
+};
+
 // 16-bit element j (0..3) of a 64-bit quartet, in the low half of a word.
 __device__ __forceinline__ uint32_t elem16x2(const u32x2& v, int j) {
   const uint32_t w = v[j >> 1];
@@ -263,18 +280,21 @@ struct LrBwdArgs {
 };
 
 
-// Packed U_eff operands of one wavefront's 64-channel chunk, staged once in
-// LDS (the chunk never changes across the run): for tap k, rank chunk c and
-// column j, lane (q, n) reads
-//   uw: ranks 16c+4q..16c+4q+3 of channel 4n+j  (B operand of the tap weights)
-//   uz: rank 16c+n of channels 16q+j, 16q+4+j, 16q+8+j, 16q+12+j  (B operand of dz)
-// Slot ((k*RC + c)*4 + j)*2 + {0: uw, 1: uz}, 64 lanes x 8 bytes each.
-template <int W, int RC>
-__device__ __forceinline__ void stage_uops(u32x2* __restrict__ lds, const uint16_t* __restrict__ U,
+// U_eff operands of one wavefront's 64-channel chunk, staged once per run (the
+// chunk never changes across it): the dz operands always in LDS, the tap-weight
+// operands in registers when W*RC <= 4 (UWREG) and in LDS otherwise.  For tap k
+// and rank chunk c, lane (q, n) reads
+//   uw[j] (j = 0..3): ranks 16c+4q..16c+4q+3 of channel 4n+j, packed (B operand
+//                     of the 16x16x16 tap-weight MFMA);
+//   uz[s] (s = 0, 1): rank 16c+n, channels 32s+8q..32s+8q+7 as they lie in U
+//                     (B operand of the 16x16x32 dz MFMA).
+template <int W, int RC, bool UWREG>
+__device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds, u32x2 (&uw_reg)[UWREG ? W * RC * 4 : 1],
+                                           u32x4* __restrict__ uz_lds, const uint16_t* __restrict__ U,
                                            const uint16_t* __restrict__ sw, int R, int RK, int D, int d0, int q,
                                            int n, int lane) {
   const int64_t WD = (int64_t)W * D;
-  const bool chv = d0 + 4 * n < D, grpv = d0 + 16 * q < D;
+  const bool chv = d0 + 4 * n < D;
 #pragma unroll
   for (int k = 0; k < W; ++k) {
 #pragma unroll
@@ -288,22 +308,24 @@ __device__ __forceinline__ void stage_uops(u32x2* __restrict__ lds, const uint16
         else if (chv && r < RK) src = sw + (int64_t)k * D + d0 + 4 * n;
         rows[kk] = src ? *reinterpret_cast<const u32x2*>(src) : u32x2{0u, 0u};
       }
-      const int r = 16 * c + n;
-      const uint16_t* src = nullptr;
-      if (grpv && r < R) src = U + (int64_t)r * WD + (int64_t)k * D + d0 + 16 * q;
-      else if (grpv && r < RK) src = sw + (int64_t)k * D + d0 + 16 * q;
-      const u32x4 v0 = src ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
-      const u32x4 v1 = src ? *reinterpret_cast<const u32x4*>(src + 8) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        u32x2 uw, uz;
+        u32x2 uw;
         uw[0] = elem16x2(rows[0], j) | (elem16x2(rows[1], j) << 16);
         uw[1] = elem16x2(rows[2], j) | (elem16x2(rows[3], j) << 16);
-        uz[0] = elem16(v0, j) | (elem16(v0, 4 + j) << 16);
-        uz[1] = elem16(v1, j) | (elem16(v1, 4 + j) << 16);
-        const int slot = ((k * RC + c) * 4 + j) * 2;
-        lds[slot * 64 + lane] = uw;
-        lds[(slot + 1) * 64 + lane] = uz;
+        if constexpr (UWREG)
+          uw_reg[(k * RC + c) * 4 + j] = uw;
+        else
+          uw_lds[((k * RC + c) * 4 + j) * 64 + lane] = uw;
+      }
+      const int r = 16 * c + n;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int dd = d0 + 32 * s2 + 8 * q;  // multiple of 8; D % 16 == 0, so dd < D means dd + 8 <= D
+        const uint16_t* src = nullptr;
+        if (dd < D && r < R) src = U + (int64_t)r * WD + (int64_t)k * D + dd;
+        else if (dd < D && r < RK) src = sw + (int64_t)k * D + dd;
+        uz_lds[((k * RC + c) * 2 + s2) * 64 + lane] = src ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
       }
     }
   }
@@ -329,21 +351,29 @@ __device__ __forceinline__ uint32_t bload16(rsrc_t r, int off) {
 __device__ __forceinline__ void bstore64(u32x2 v, rsrc_t r, int off) { __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 0); }
 
 template <typename T, int W, int RC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W * RC <= 4 && RC <= 2 ? 2 : 1, 8))) void lr_bwd_mfma(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && RC == 1 ? 2 : 1, 8))) void lr_bwd_mfma(
     const T* __restrict__ x_, const T* __restrict__ z_, const T* __restrict__ U_, const T* __restrict__ sw_,
     const T* __restrict__ dy_, T* __restrict__ dx_, float* __restrict__ part_dz, float* __restrict__ part_du,
     LrBwdArgs a) {
   constexpr int NB = (W + 6) / 4;  // MFMA row blocks for the dx look-ahead
   constexpr int NR = W + 3;        // x rows 4q-W+1 .. 4q+3 and dy rows 4q .. 4q+W+2 per lane
-  constexpr int NSLOT = W * RC * 4 * 2;
+  constexpr bool UWREG = W * RC <= 4;   // tap-weight operands in registers
+  constexpr int NUW = W * RC * 4;  // packed tap-weight operands per lane
+  constexpr int NUZ = W * RC * 2;  // dz operands per lane
+  constexpr int GROW = 72;         // G tile row pitch (64 channels + 8 pad: conflict-free reads)
   const uint16_t* __restrict__ x = reinterpret_cast<const uint16_t*>(x_);
   const uint16_t* __restrict__ z = reinterpret_cast<const uint16_t*>(z_);
   const uint16_t* __restrict__ U = reinterpret_cast<const uint16_t*>(U_);
   const uint16_t* __restrict__ sw = reinterpret_cast<const uint16_t*>(sw_);
   const uint16_t* __restrict__ dy = reinterpret_cast<const uint16_t*>(dy_);
   uint16_t* __restrict__ dx = reinterpret_cast<uint16_t*>(dx_);
-  __shared__ u32x2 uops[4][NSLOT * 64];
-  __shared__ float dzred[2][4][RC * 256];
+  __shared__ u32x2 uw_lds[4][UWREG ? 1 : NUW * 64];
+  __shared__ u32x4 uz_lds[4][NUZ * 64];
+  __shared__ __attribute__((aligned(16))) uint16_t gtile[4][16 * GROW];
+  // dz partial sums of the workgroup's 4 chunks, gathered for DZB tiles and
+  // reduced once per batch (double-buffered: one barrier per batch).
+  constexpr int DZB = (UWREG && RC == 1) ? 4 : 1;
+  __shared__ float dzred[2][4][DZB][RC * 256];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, n = lane & 15;
@@ -362,7 +392,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W * RC <= 4
   const int64_t row0 = (int64_t)b * Tn;
   const int R = a.R, RK = a.RK;
   const bool zvec = (R & 3) == 0;
-  u32x2* __restrict__ myops = uops[wave];
+  u32x2* __restrict__ my_uw = uw_lds[wave];
+  u32x4* __restrict__ my_uz = uz_lds[wave];
+  uint16_t* __restrict__ my_g = gtile[wave];
   const int rowb = D * 2;
   const int64_t seqb = (int64_t)Tn * rowb;
   const rsrc_t rx = make_rsrc(x + row0 * D, seqb);
@@ -371,7 +403,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W * RC <= 4
   const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 2);
   const int lane_off = chv ? (4 * q * D + col) * 2 : kOobLane;  // byte offset of the lane's row 4q quartet
 
-  stage_uops<W, RC>(myops, U, sw, R, RK, D, d0, q, n, lane);
+  u32x2 uw_reg[UWREG ? NUW : 1];
+  stage_uops<W, RC, UWREG>(my_uw, uw_reg, my_uz, U, sw, R, RK, D, d0, q, n, lane);
 
   // Identity as the B operand: lane (q, n) gives rows 4q..4q+3 of column n.
   u32x2 ident;
@@ -452,6 +485,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W * RC <= 4
 
 #pragma unroll
     for (int k = 0; k < W; ++k) {
+      // G_k = bf16(dy * x_shift) for rows 4q..4q+3, channels 4n..4n+3 (fp32 products).
+      float gf[4][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gf[i][j] = dyf[i][j] * q4f<T>(xr[i - k + W - 1], j);
+      // Row-major copy of the G tile in this wavefront's LDS, read back below as
+      // the transposed (channel-contiguous) A operand of the dz MFMA.
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        u32x2 w;
+        w[0] = pack2<T>(gf[i][0], gf[i][1]);
+        w[1] = pack2<T>(gf[i][2], gf[i][3]);
+        *reinterpret_cast<u32x2*>(my_g + (4 * q + i) * GROW + 4 * n) = w;
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         // dx += dy[4q+i+k] * Kw[4q+i+k, k]: tap weights of the row blocks that hold rows k..k+3.
@@ -461,27 +509,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W * RC <= 4
           f32x4 wk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int c = 0; c < RC; ++c)
-            wk = Mma16<T>::run(zA[bb][c], myops[(((k * RC + c) * 4 + j) * 2) * 64 + lane], wk);
+            wk = Mma16<T>::run(zA[bb][c], UWREG ? uw_reg[UWREG ? (k * RC + c) * 4 + j : 0]
+                                                : my_uw[((k * RC + c) * 4 + j) * 64 + lane], wk);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int tr = i + k;  // row offset of dy / Kw in the lane window
             if (tr >= 4 * bb && tr < 4 * bb + 4) dxa[i][j] = fmaf(dyf[tr][j], wk[tr - 4 * bb], dxa[i][j]);
           }
         }
-        // G_k = bf16(dy * x_shift) of column j, rows 4q..4q+3: the B operand of dU.
+        // dU (K = rows): column j of G, rows 4q..4q+3, is the B operand as it lies.
         u32x2 g;
-        g[0] = pack2<T>(dyf[0][j] * q4f<T>(xr[0 - k + W - 1], j), dyf[1][j] * q4f<T>(xr[1 - k + W - 1], j));
-        g[1] = pack2<T>(dyf[2][j] * q4f<T>(xr[2 - k + W - 1], j), dyf[3][j] * q4f<T>(xr[3 - k + W - 1], j));
-        // dU (K = rows); exact transpose of G_j; dz (K = channels).
+        g[0] = pack2<T>(gf[0][j], gf[1][j]);
+        g[1] = pack2<T>(gf[2][j], gf[3][j]);
 #pragma unroll
         for (int c = 0; c < RC; ++c) du[k][c][j] = Mma16<T>::run(zT[c], g, du[k][c][j]);
-        const f32x4 tr = Mma16<T>::run(g, ident, f32x4{0.f, 0.f, 0.f, 0.f});
-        u32x2 ga;
-        ga[0] = pack2<T>(tr[0], tr[1]);
-        ga[1] = pack2<T>(tr[2], tr[3]);
+      }
+      // dz (K = 32 channels): A = G row n (this lane: row = lane % 16), channels 32s+8q..+7.
 #pragma unroll
-        for (int c = 0; c < RC; ++c)
-          dz[c] = Mma16<T>::run(ga, myops[(((k * RC + c) * 4 + j) * 2 + 1) * 64 + lane], dz[c]);
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const u32x4 ga = *reinterpret_cast<const u32x4*>(my_g + n * GROW + 32 * s2 + 8 * q);
+#pragma unroll
+        for (int c = 0; c < RC; ++c) dz[c] = Mma32<T>::run(ga, my_uz[((k * RC + c) * 2 + s2) * 64 + lane], dz[c]);
       }
     }
 
@@ -496,19 +544,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W * RC <= 4
       o[1] = pack2<T>(v[2], v[3]);
       bstore64(o, rdx, lane_off + toff + i * rowb);
     }
-    // ---- dz: sum the 4 chunk wavefronts of this tile in LDS, one partial per group
-    const int par = tile & 1;
+    // ---- dz: gather this wavefront's tile sums; every DZB tiles (and at the end of
+    // the run) add the 4 chunk wavefronts in wave order, one partial per group.
+    const int slot = (tile - tile0) % DZB;
+    const int buf = ((tile - tile0) / DZB) & 1;
 #pragma unroll
     for (int c = 0; c < RC; ++c)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dzred[par][wave][c * 256 + (4 * q + i) * 16 + n] = dz[c][i];
-    __syncthreads();
-    for (int e = threadIdx.x; e < RC * 256; e += 256) {
-      const int c = e >> 8, rem = e & 255, rr = rem >> 4, nn = rem & 15;
-      const int r = 16 * c + nn;
-      const int t = t0 + rr;
-      const float v = ((dzred[par][0][e] + dzred[par][1][e]) + dzred[par][2][e]) + dzred[par][3][e];
-      if (r < R && t < Tn) part_dz[((int64_t)cg * a.BT + row0 + t) * R + r] = v;
+      for (int i = 0; i < 4; ++i) dzred[buf][wave][slot][c * 256 + (4 * q + i) * 16 + n] = dz[c][i];
+    if (slot == DZB - 1 || tile == tile1 - 1) {
+      __syncthreads();
+      const int tb = t0 - slot * 16;  // first row of the batch
+      for (int e = threadIdx.x; e < (slot + 1) * RC * 256; e += 256) {
+        const int sl = e / (RC * 256), rem = e - sl * (RC * 256);
+        const int c = rem >> 8, rr = (rem >> 4) & 15, nn = rem & 15;
+        const int r = 16 * c + nn;
+        const int t = tb + sl * 16 + rr;
+        const float v = ((dzred[buf][0][sl][rem] + dzred[buf][1][sl][rem]) + dzred[buf][2][sl][rem]) +
+                        dzred[buf][3][sl][rem];
+        if (r < R && t < Tn) part_dz[((int64_t)cg * a.BT + row0 + t) * R + r] = v;
+      }
     }
   }
 
@@ -621,11 +676,12 @@ hipError_t launch_bwd(const LrProblem& p) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t WD = p.W * p.D, RKWD = (int64_t)a.RK * WD;
-  e = reduce_partials(pdu, RKWD, a.nseg, p.R * WD, p.dU, p.dtype, p.stream);
-  if (e == hipSuccess && p.static_w)
-    e = reduce_partials(pdu + p.R * WD, RKWD, a.nseg, WD, p.dstatic_w, p.dtype, p.stream);
-  if (e == hipSuccess) e = reduce_partials(pdz, a.BT * a.R, a.ncg, a.BT * a.R, p.dz, p.dtype, p.stream);
-  return e;
+  const PartialReduce jobs[3] = {
+      {pdu, RKWD, a.nseg, p.R * WD, p.dU},
+      {pdu + p.R * WD, RKWD, a.nseg, p.static_w ? WD : 0, p.dstatic_w},
+      {pdz, a.BT * a.R, a.ncg, a.BT * a.R, p.dz},
+  };
+  return reduce_partials_multi(jobs, 3, p.dtype, p.stream);
 }
 
 template <typename T>
@@ -634,7 +690,7 @@ hipError_t dispatch_bwd(const LrProblem& p) {
 #define DC_LR_CASE(WW, CC) \
   if (p.W == WW && rc == CC) return launch_bwd<T, WW, CC>(p);
   DC_LR_CASE(1, 1) DC_LR_CASE(1, 2) DC_LR_CASE(1, 3) DC_LR_CASE(1, 4)
-  DC_LR_CASE(2, 1) DC_LR_CASE(2, 2) DC_LR_CASE(2, 3) DC_LR_CASE(2, 4)
+  DC_LR_CASE(2, 1) DC_LR_CASE(2, 2) DC_LR_CASE(2, 3)
   DC_LR_CASE(3, 1) DC_LR_CASE(3, 2)
   DC_LR_CASE(4, 1) DC_LR_CASE(4, 2)
   DC_LR_CASE(5, 1) DC_LR_CASE(6, 1) DC_LR_CASE(7, 1) DC_LR_CASE(8, 1)
@@ -651,6 +707,7 @@ bool lr_mfma_ok_impl(const LrProblem& p, bool bwd) {
   if (p.W < 1 || p.W > 8) return false;
   const int64_t rc = (p.R + (p.static_w ? 1 : 0) + 15) / 16;
   if (rc > 4 || p.W * rc > 8) return false;  // staged operands / accumulators bound W*RC
+  if (bwd && rc == 4 && p.W > 1) return false;  // backward LDS (operands + dz sums) above 160 KiB
   if (!bwd) {
     if (p.D % 8 != 0) return false;
     return aligned16(p.x) && aligned16(p.U) && aligned16(p.static_w) && aligned16(p.y);

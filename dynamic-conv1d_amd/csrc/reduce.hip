@@ -1,56 +1,110 @@
 // Deterministic cross-workgroup reduction of fp32 partial sums.
 //
-// The backward kernels write one fp32 partial per workgroup for quantities
-// that sum over the batch and time axes (dstatic_w, dU) or over channel
-// groups (dz).  The reference accumulates those with relaxed fp32 atomics
-// (headwise.py:157-159, lowrank.py:136-137), so its results vary run to run;
-// here every column is summed in a fixed order, then rounded once to the
-// output dtype.
+// The backward kernels write one fp32 partial per workgroup (or per row run)
+// for quantities that sum over the batch and time axes (dstatic_w, dU) or over
+// channel groups (dz).  The reference accumulates those with relaxed fp32
+// atomics (headwise.py:157-159, lowrank.py:136-137), so its results vary run
+// to run; here every column is summed in a fixed order, then rounded once to
+// the output dtype.  Up to kMaxJobs reductions share one launch.
 #include "dc_common.h"
 #include "dc_launch.h"
 
 namespace dc {
 
-// 1024 threads: 64 columns x 16 partial lanes.  Lane pl sums partials
-// pl, pl+16, ...; the 16 lane sums are then added in index order.
+constexpr int kMaxJobs = 3;
+
+struct ReduceJob {
+  const float* part;  // partial p, column c at part[p * pstride + c]
+  int64_t pstride;
+  int64_t C;          // columns
+  void* out;          // C outputs of the launch dtype
+  int P;              // partials
+  int vec;            // 4: columns, pstride and pointers allow float4 access
+  int block0;         // first block of this job
+};
+
+struct ReduceJobs {
+  ReduceJob j[kMaxJobs];
+  int n;
+};
+
+// 256 threads = 64 column lanes x 4 partial lanes; a column lane owns 4
+// consecutive columns when `vec` (float4 loads), else 1.  Partial lane pl sums
+// partials pl, pl+4, ...; the 4 lane sums are added in index order in LDS.
 template <typename T>
-__global__ __launch_bounds__(1024) void reduce_partials_kernel(const float* __restrict__ part, int64_t pstride,
-                                                               int P, int64_t C, T* __restrict__ out) {
-  __shared__ float red[16][65];
-  const int cl = threadIdx.x & 63;
-  const int pl = threadIdx.x >> 6;
-  const int64_t c = (int64_t)blockIdx.x * 64 + cl;
-  float s = 0.f;
-  if (c < C) {
-    const float* q = part + c;
-    for (int p = pl; p < P; p += 16) s += q[(int64_t)p * pstride];
+__global__ __launch_bounds__(256) void reduce_partials_kernel(ReduceJobs jobs) {
+  __shared__ float4 red[4][64];
+  int ji = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxJobs; ++i)
+    if (i < jobs.n && (int)blockIdx.x >= jobs.j[i].block0) ji = i;
+  const ReduceJob& J = jobs.j[ji];
+  const int cl = threadIdx.x & 63, pl = threadIdx.x >> 6;
+  const int per = J.vec;  // columns per lane
+  const int64_t c0 = ((int64_t)(blockIdx.x - J.block0) * 64 + cl) * per;
+  float4 s = {0.f, 0.f, 0.f, 0.f};
+  if (c0 < J.C) {
+    const float* q = J.part + c0;
+    if (per == 4) {
+      for (int p = pl; p < J.P; p += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(q + (int64_t)p * J.pstride);
+        s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+      }
+    } else {
+      for (int p = pl; p < J.P; p += 4) s.x += q[(int64_t)p * J.pstride];
+    }
   }
   red[pl][cl] = s;
   __syncthreads();
-  if (pl == 0 && c < C) {
-    float t = 0.f;
+  if (pl == 0 && c0 < J.C) {
+    float4 t = red[0][cl];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) t += red[i][cl];
-    out[c] = (T)t;
+    for (int i = 1; i < 4; ++i) {
+      const float4 u = red[i][cl];
+      t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+    }
+    T* o = reinterpret_cast<T*>(J.out) + c0;
+    o[0] = (T)t.x;
+    if (per == 4) {
+      o[1] = (T)t.y;
+      o[2] = (T)t.z;
+      o[3] = (T)t.w;
+    }
   }
+}
+
+hipError_t reduce_partials_multi(const PartialReduce* r, int n, int dtype, hipStream_t stream) {
+  ReduceJobs jobs{};
+  int blocks = 0;
+  for (int i = 0; i < n && jobs.n < kMaxJobs; ++i) {
+    if (r[i].C <= 0) continue;
+    ReduceJob& J = jobs.j[jobs.n++];
+    J.part = r[i].part;
+    J.pstride = r[i].pstride;
+    J.C = r[i].C;
+    J.out = r[i].out;
+    J.P = r[i].P;
+    const int es = dtype_size(dtype);
+    const bool v4 = (r[i].C % 4 == 0) && (r[i].pstride % 4 == 0) &&
+                    (reinterpret_cast<uintptr_t>(r[i].part) % 16 == 0) &&
+                    (reinterpret_cast<uintptr_t>(r[i].out) % (4 * es) == 0);
+    J.vec = v4 ? 4 : 1;
+    J.block0 = blocks;
+    blocks += (int)((J.C + 64 * J.vec - 1) / (64 * J.vec));
+  }
+  if (jobs.n == 0) return hipSuccess;
+  switch (dtype) {
+    case kBF16: reduce_partials_kernel<bf16><<<blocks, 256, 0, stream>>>(jobs); break;
+    case kFP16: reduce_partials_kernel<fp16><<<blocks, 256, 0, stream>>>(jobs); break;
+    default: reduce_partials_kernel<float><<<blocks, 256, 0, stream>>>(jobs); break;
+  }
+  return hipGetLastError();
 }
 
 hipError_t reduce_partials(const float* part, int64_t pstride, int P, int64_t C, void* out, int dtype,
                            hipStream_t stream) {
-  if (C <= 0) return hipSuccess;
-  const unsigned grid = (unsigned)((C + 63) / 64);
-  switch (dtype) {
-    case kBF16:
-      reduce_partials_kernel<bf16><<<grid, 1024, 0, stream>>>(part, pstride, P, C, (bf16*)out);
-      break;
-    case kFP16:
-      reduce_partials_kernel<fp16><<<grid, 1024, 0, stream>>>(part, pstride, P, C, (fp16*)out);
-      break;
-    default:
-      reduce_partials_kernel<float><<<grid, 1024, 0, stream>>>(part, pstride, P, C, (float*)out);
-      break;
-  }
-  return hipGetLastError();
+  const PartialReduce r{part, pstride, P, C, out};
+  return reduce_partials_multi(&r, 1, dtype, stream);
 }
 
 }  // namespace dc
