@@ -33,6 +33,10 @@ COMMON = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", INCLUDE,
 ]
+# Per-file flags.  The lowrank forward lets its MFMA results land in VGPRs
+# directly (no v_accvgpr_read per result); the backward keeps the default,
+# where accumulation registers are what keeps its larger tiles in 512 registers.
+PER_FILE = {"lowrank_mfma_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def hipcc() -> str:
@@ -44,7 +48,7 @@ def hipcc() -> str:
 
 def _compile(src: str, extra: list) -> tuple:
     obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [hipcc(), *COMMON, *extra, "-c", src, "-o", obj]
+    cmd = [hipcc(), *COMMON, *PER_FILE.get(os.path.basename(src), []), *extra, "-c", src, "-o", obj]
     t0 = time.time()
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature; drop that line.

@@ -42,7 +42,10 @@ __device__ __forceinline__ void load_vals(const T* __restrict__ p, float* out) {
   for (int i = 0; i < N; ++i) out[i] = (float)e[i];
 }
 
-template <typename T, int N>
+// NT: nontemporal store (`nt`), for outputs written in whole 128-byte lines
+// that are not read again by the kernel; partial-line stores keep the default
+// policy so the L2 merges them before write-back.
+template <typename T, int N, bool NT = false>
 __device__ __forceinline__ void store_vals(T* __restrict__ p, const float* in) {
   constexpr int BYTES = N * (int)sizeof(T);
   constexpr int A = pow2_align(BYTES);
@@ -55,7 +58,12 @@ __device__ __forceinline__ void store_vals(T* __restrict__ p, const float* in) {
   __builtin_memcpy(u, e, BYTES);
   U* q = reinterpret_cast<U*>(p);
 #pragma unroll
-  for (int i = 0; i < NU; ++i) q[i] = u[i];
+  for (int i = 0; i < NU; ++i) {
+    if constexpr (NT)
+      __builtin_nontemporal_store(u[i], q + i);
+    else
+      q[i] = u[i];
+  }
 }
 
 // N elements of T held as raw load units (no conversion): used to keep
@@ -91,6 +99,12 @@ __device__ __forceinline__ void zero_vals(float* v) {
 #pragma unroll
   for (int i = 0; i < N; ++i) v[i] = 0.f;
 }
+
+// Wavefront index within the workgroup, marked wave-uniform for the compiler
+// (threadIdx.x >> 6 is, but divergence analysis cannot prove it): values
+// derived from it (run, sequence, base addresses, buffer descriptors) then
+// live in scalar registers.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // ------------------------------------------------------------- block remap
 // The command processor hands workgroup i to XCD (i % 8).  Renumber so that

@@ -149,6 +149,7 @@ HwPlan make_plan(const HwProblem& p, bool bwd) {
   a.residual = p.residual;
   a.has_static = p.static_w != nullptr;
   pl.nblk = a.nblk;
+  pl.tdw = a.nvc % 64 == 0;
   pl.P = nsg;
   return pl;
 }

@@ -24,7 +24,12 @@
 // are added into the open accumulator of row t-k; row t-W+1 is complete
 // after step t and is stored.  dweight sums dy[t]*x[t-k] over the head's
 // channels: in-lane when head_size <= VEC, then a butterfly over the
-// head_size/VEC lanes of the head.  dstatic_w partial sums stay in registers
+// head_size/VEC lanes of the head.  When a lane's dweight row piece is more
+// than 16 bytes (head_size < VEC, e.g. 64 bytes at head_size 1, W 4, bf16),
+// stores of it straight from the lanes write each 128-byte line in several
+// partial pieces, which measured ~30% below contiguous stores; the wavefront
+// then passes its dweight row through LDS and stores it as 16-byte lane
+// pieces that are contiguous across the wavefront (TDW).  dstatic_w partial sums stay in registers
 // for the whole run, are added across the 4 wavefronts of the workgroup in
 // LDS in a fixed order, and one fp32 partial per workgroup is summed by
 // reduce_partials (no atomics: bitwise deterministic).
@@ -72,7 +77,7 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
   typedef Raw<T, NWE> WR;
   const int lb = xcd_remap(blockIdx.x, a.nblk);
   const int vg = lb % a.nvg, sgp = lb / a.nvg;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = wave_id(), lane = threadIdx.x & 63;
   const int vc = vg * 64 + lane;
   const int s = sgp * 4 + wave;
   if (s >= a.nseg || vc >= a.nvc) return;
@@ -148,7 +153,7 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
 #pragma unroll
           for (int j = 0; j < VEC; ++j) acc[j] += xr[p].get(j);
         }
-        store_vals<T, VEC>(yp + (int64_t)t * D, acc);
+        store_vals<T, VEC, true>(yp + (int64_t)t * D, acc);
       }
     }
 #pragma unroll
@@ -160,10 +165,17 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
 }
 
 // ----------------------------------------------------------------- backward
-template <typename T, int W, int HSV, bool HAS_STATIC>
+// Transposed dweight store possible: 16-byte pieces, more than one per lane.
+template <typename T, int W, int HSV> struct TdwOf {
+  static constexpr int BYTES = (VecOf<T>::value / HSV) * W * (int)sizeof(T);
+  static constexpr bool value = BYTES % 16 == 0 && BYTES > 16;
+  static constexpr int NP = BYTES / 16;  // pieces per lane
+};
+
+template <typename T, int W, int HSV, bool HAS_STATIC, bool TDW>
 __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, const T* __restrict__ wt,
                                                    const T* __restrict__ sw, const T* __restrict__ dy,
-                                                   T* __restrict__ dx, T* __restrict__ dwt,
+                                                   T* __restrict__ dx, T* __restrict__ dwt_,
                                                    float* __restrict__ part, HwArgs a) {
   constexpr int VEC = VecOf<T>::value;
   constexpr int NHL = VEC / HSV;
@@ -173,10 +185,13 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
   typedef Raw<T, NWE> WR;
   const int lb = xcd_remap(blockIdx.x, a.nblk);
   const int vg = lb % a.nvg, sgp = lb / a.nvg;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = wave_id(), lane = threadIdx.x & 63;
   const int vc = vg * 64 + lane;
   const int s = sgp * 4 + wave;
   const bool active = (s < a.nseg) && (vc < a.nvc);
+  // TDW: the host guarantees nvc % 64 == 0, so `active` is wave-uniform.
+  constexpr int NP = TDW ? TdwOf<T, W, HSV>::NP : 1;
+  __shared__ u32x4 dwt[4][TDW ? NP * 64 : 1];
 
   float dsw[W][VEC];
 #pragma unroll
@@ -200,7 +215,9 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
     const T* wp = wt + (row0 * a.H + h0) * W;
     const T* dyp = dy + row0 * D + d0;
     T* dxp = dx + row0 * D + d0;
-    T* dwp = dwt + (row0 * a.H + h0) * W;
+    T* dwp = dwt_ + (row0 * a.H + h0) * W;
+    // dweight row of the wavefront's lane 0 (TDW: lanes own consecutive heads)
+    T* dwp0 = dwt_ + (row0 * a.H + (((vc - lane) * VEC) >> a.hs_shift)) * W;
     const bool leader = (vc & (a.lph - 1)) == 0;
     const int residual = a.residual, lph = a.lph;
 
@@ -300,10 +317,27 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
 #pragma unroll
               for (int k = 0; k < NWE; ++k) dwv[k] = group_sum(dwv[k], lph);
             }
-            if (leader) store_vals<T, NWE>(dwp + (int64_t)t * wrs, dwv);
+            if constexpr (TDW) {
+              // Lane l's piece j goes to slot l*NP + j; slot i*64 + l is then
+              // the wavefront's i-th contiguous 1 KiB.  One wavefront writes
+              // and reads its own slots, in order: no barrier.
+              T e[NWE];
+#pragma unroll
+              for (int i = 0; i < NWE; ++i) e[i] = (T)dwv[i];
+              u32x4 pc[NP];
+              __builtin_memcpy(pc, e, sizeof(pc));
+              u32x4* my = dwt[wave];
+#pragma unroll
+              for (int j = 0; j < NP; ++j) my[lane * NP + j] = pc[j];
+              u32x4* dst = reinterpret_cast<u32x4*>(dwp0 + (int64_t)t * wrs);
+#pragma unroll
+              for (int i = 0; i < NP; ++i) __builtin_nontemporal_store(my[i * 64 + lane], dst + i * 64 + lane);
+            } else {
+              if (leader) store_vals<T, NWE>(dwp + (int64_t)t * wrs, dwv);
+            }
           }
           const int tdone = t - (W - 1);
-          if (tdone >= t0 && tdone < t1) store_vals<T, VEC>(dxp + (int64_t)tdone * D, dxa[(u + 1) % W]);
+          if (tdone >= t0 && tdone < t1) store_vals<T, VEC, true>(dxp + (int64_t)tdone * D, dxa[(u + 1) % W]);
         }
       }
 #pragma unroll
@@ -340,7 +374,8 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
 struct HwPlan {
   HwArgs a;
   int nblk;
-  int P;  // partial count (bwd)
+  int P;     // partial count (bwd)
+  bool tdw;  // whole wavefronts (nvc % 64 == 0): transposed dweight stores allowed
 };
 
 template <typename T, int W, int HSV>
@@ -350,15 +385,27 @@ hipError_t launch_fwd_fast(const HwProblem& p, const HwPlan& pl) {
   return hipGetLastError();
 }
 
-template <typename T, int W, int HSV>
-hipError_t launch_bwd_fast(const HwProblem& p, const HwPlan& pl) {
+template <typename T, int W, int HSV, bool TDW>
+void launch_bwd_kernel(const HwProblem& p, const HwPlan& pl) {
   if (p.static_w) {
-    hw_bwd_fast<T, W, HSV, true><<<pl.nblk, 256, 0, p.stream>>>(
+    hw_bwd_fast<T, W, HSV, true, TDW><<<pl.nblk, 256, 0, p.stream>>>(
         (const T*)p.x, (const T*)p.weight, (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, (T*)p.dweight, p.ws,
         pl.a);
   } else {
-    hw_bwd_fast<T, W, HSV, false><<<pl.nblk, 256, 0, p.stream>>>(
+    hw_bwd_fast<T, W, HSV, false, TDW><<<pl.nblk, 256, 0, p.stream>>>(
         (const T*)p.x, (const T*)p.weight, nullptr, (const T*)p.dy, (T*)p.dx, (T*)p.dweight, nullptr, pl.a);
+  }
+}
+
+template <typename T, int W, int HSV>
+hipError_t launch_bwd_fast(const HwProblem& p, const HwPlan& pl) {
+  if constexpr (TdwOf<T, W, HSV>::value) {
+    if (pl.tdw)
+      launch_bwd_kernel<T, W, HSV, true>(p, pl);
+    else
+      launch_bwd_kernel<T, W, HSV, false>(p, pl);
+  } else {
+    launch_bwd_kernel<T, W, HSV, false>(p, pl);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !p.static_w) return e;

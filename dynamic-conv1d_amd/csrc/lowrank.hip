@@ -9,9 +9,9 @@
 // implicit rank R of the kernel, so no padded z or concatenated U is built.
 //
 // This file holds the one-thread-per-output kernels used for fp32 and for
-// shapes the MFMA path (lowrank_mfma.hip) does not take, plus the dispatch.
-#include "dc_common.h"
-#include "dc_launch.h"
+// shapes the MFMA path (lowrank_mfma_fwd.hip, lowrank_mfma_bwd.hip) does not
+// take, plus the dispatch.
+#include "lowrank_mfma.h"
 
 namespace dc {
 
@@ -130,6 +130,9 @@ __global__ __launch_bounds__(256) void lr_bwd_du_generic(const T* __restrict__ x
 // ------------------------------------------------------------------- host
 namespace {
 
+bool aligned_to16(const void* p) { return aligned_to(p, 16); }
+bool aligned_to8(const void* p) { return aligned_to(p, 8); }
+
 unsigned generic_grid(int64_t n) {
   int64_t g = (n + 255) / 256;
   if (g > 65536) g = 65536;
@@ -176,13 +179,23 @@ hipError_t bwd_generic(const LrProblem& p) {
 
 }  // namespace
 
-// Provided by lowrank_mfma.hip.
-bool lr_mfma_ok_impl(const LrProblem& p, bool bwd);
-int64_t lr_mfma_ws_bytes(const LrProblem& p);
-hipError_t lr_mfma_fwd(const LrProblem& p);
-hipError_t lr_mfma_bwd(const LrProblem& p);
-
-bool lr_mfma_ok(const LrProblem& p, bool bwd) { return lr_mfma_ok_impl(p, bwd); }
+// Shapes, dtypes and alignments the MFMA kernels (lowrank_mfma_{fwd,bwd}.hip) take.
+bool lr_mfma_ok(const LrProblem& p, bool bwd) {
+  if (p.dtype != kBF16 && p.dtype != kFP16) return false;
+  if (p.W < 1 || p.W > 8) return false;
+  const int64_t rc = (p.R + (p.static_w ? 1 : 0) + 15) / 16;
+  if (rc > 4 || p.W * rc > 8) return false;  // staged operands / accumulators bound W*RC
+  if (bwd && rc == 4 && p.W > 1) return false;  // backward LDS (operands + dz sums) above 160 KiB
+  // buffer-offset range of one sequence (x, y, dy, dx rows and z rows)
+  if ((p.T + kSeqSlackRows) * p.D * 2 > kMaxSeqBytes) return false;
+  if ((p.T + kSeqSlackRows) * p.R * 2 > kMaxSeqBytes) return false;
+  if (!bwd) {
+    if (p.D % 8 != 0) return false;
+    return aligned_to16(p.x) && aligned_to16(p.U) && aligned_to16(p.static_w) && aligned_to16(p.y);
+  }
+  if (p.D % 16 != 0) return false;
+  return aligned_to8(p.x) && aligned_to8(p.dy) && aligned_to8(p.dx) && aligned_to16(p.U) && aligned_to16(p.static_w);
+}
 
 int64_t lr_bwd_ws_bytes(const LrProblem& p) {
   if (lr_mfma_ok(p, true)) return lr_mfma_ws_bytes(p);

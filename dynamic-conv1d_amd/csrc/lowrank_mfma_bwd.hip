@@ -1,244 +1,7 @@
-// Lowrank dynamic convolution on gfx950 matrix cores (bf16 / fp16).
-//
-//   Kw[t, k, d] = sum_r z_eff[t, r] * U_eff[r, k*D + d]      (MFMA, fp32 accumulate)
-//   y[t, d]     = sum_k Kw[t, k, d] * x[t-k, d]  (+ x[t, d])
-//
-// z_eff / U_eff are z / U extended by the static filter as rank R with
-// z == 1 and U row = static_w (the reference's fusion, lowrank.py:223-225),
-// and by zero ranks up to a multiple of 16; neither is materialised.
-//
-// Forward tile (lr_fwd_mfma).  A wavefront owns 16 rows x 128 channels.
-// Lane l = 16*q + n owns rows 4q..4q+3 and the channel octet 8n..8n+7.
-// For each tap k the per-token weights come from eight
-// v_mfma_f32_16x16x16 (bf16|f16) products, one per j = 0..7, whose 16
-// output columns are the channels 8*col + j: the accumulator layout of the
-// 16x16 MFMA (lane l holds rows 4q..4q+3 of column n) then leaves every lane
-// holding exactly its own 8 channels for its own 4 rows, so the weights
-// multiply 128-bit rows of x in registers and are never written anywhere.
-// The B operands (U_eff, 16 ranks x 8 columns per lane) are loaded once per
-// run as 128-bit row pieces and repacked; the A operand is the lane's row
-// of z_eff.  Reference: lowrank.py:24-67 (Triton forward kernel).
-#include "dc_common.h"
-#include "dc_launch.h"
+// Lowrank backward on gfx950 matrix cores (bf16 / fp16): dx, dz, dU, dstatic_w.
+#include "lowrank_mfma.h"
 
 namespace dc {
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-template <typename T> struct Mma16;
-template <> struct Mma16<bf16> {
-  static constexpr uint16_t kOne = 0x3F80;  // 1.0
-  __device__ static __forceinline__ f32x4 run(u32x2 a, u32x2 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
-                                                      0, 0, 0);
-  }
-  __device__ static __forceinline__ float to_f(uint32_t bits) { return __uint_as_float(bits << 16); }
-};
-template <> struct Mma16<fp16> {
-  static constexpr uint16_t kOne = 0x3C00;  // 1.0
-  __device__ static __forceinline__ f32x4 run(u32x2 a, u32x2 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h16x4, a), __builtin_bit_cast(h16x4, b), c, 0,
-                                                 0, 0);
-  }
-  __device__ static __forceinline__ float to_f(uint32_t bits) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
-  }
-};
-
-// v_mfma_f32_16x16x32 (gfx950): lane l gives A[l%16][8(l/16)..+7] and B[8(l/16)..+7][l%16].
-typedef __bf16 b16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
-template <typename T> struct Mma32;
-template <> struct Mma32<bf16> {
-  __device__ static __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b16x8, a), __builtin_bit_cast(b16x8, b), c, 0, 0,
-                                                   0);
-  }
-};
-template <> struct Mma32<fp16> {
-  __device__ static __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h16x8, a), __builtin_bit_cast(h16x8, b), c, 0, 0,
-                                                  0);
-  }
-};
-
-// 16-bit element j (0..3) of a 64-bit quartet, in the low half of a word.
-__device__ __forceinline__ uint32_t elem16x2(const u32x2& v, int j) {
-  const uint32_t w = v[j >> 1];
-  return (j & 1) ? (w >> 16) : (w & 0xFFFFu);
-}
-
-// 16-bit element j (0..7) of a 128-bit row piece, in the low half of a word.
-__device__ __forceinline__ uint32_t elem16(const u32x4& v, int j) {
-  const uint32_t w = v[j >> 1];
-  return (j & 1) ? (w >> 16) : (w & 0xFFFFu);
-}
-
-template <typename T>
-__device__ __forceinline__ uint32_t f2bits(float f) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, (T)f);
-}
-
-template <typename T> struct Pair16;
-template <> struct Pair16<bf16> { typedef __bf16 type __attribute__((ext_vector_type(2))); };
-template <> struct Pair16<fp16> { typedef _Float16 type __attribute__((ext_vector_type(2))); };
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
-// Two floats rounded to nearest-even into one word (a in the low half): v_cvt_pk_{bf16,f16}_f32.
-template <typename T>
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  const f32x2 v = {a, b};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, typename Pair16<T>::type));
-}
-// Element j (0..3) of a 64-bit quartet as float.
-template <typename T>
-__device__ __forceinline__ float q4f(const u32x2& v, int j) {
-  return Mma16<T>::to_f(elem16x2(v, j));
-}
-
-struct LrArgs {
-  int Tn;          // sequence length
-  int D;           // channels
-  int R;           // dynamic rank (z.shape[-1])
-  int RK;          // kernel rank = R + has_static
-  int has_static;
-  int residual;
-  int nch;         // ceil(D / 128): 128-channel chunks, one per wavefront
-  int ncg;         // unused
-  int seg;         // 16-row tiles per run
-  int nspb;        // runs per sequence
-  int nseg;        // B * nspb
-  int nblk;        // grid size
-};
-
-// z_eff[row, r] as raw 16-bit bits (row < T checked by the caller).
-template <typename T>
-__device__ __forceinline__ uint32_t zbits(const uint16_t* __restrict__ z, int64_t row, int R, int RK, int r) {
-  if (r < R) return z[row * R + r];
-  return r < RK ? Mma16<T>::kOne : 0u;
-}
-
-// Packed B operands of one 128-channel chunk, staged once per workgroup:
-// ub[(k*RC + c)*8 + j][lane] = U_eff[16c + 4q + kk, k*D + dl + j], kk = 0..3.
-template <int W, int RC>
-__device__ __forceinline__ void stage_u(u32x2* __restrict__ lds, const uint16_t* __restrict__ U,
-                                        const uint16_t* __restrict__ sw, int R, int RK, int D, int dl, bool chv,
-                                        int q, int lane, int wave) {
-  const int64_t WD = (int64_t)W * D;
-  for (int kc = wave; kc < W * RC; kc += 4) {
-    const int k = kc / RC, c = kc - k * RC;
-    u32x4 rows[4];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int r = 16 * c + 4 * q + kk;
-      const uint16_t* src = nullptr;
-      if (chv && r < R) src = U + (int64_t)r * WD + (int64_t)k * D + dl;
-      else if (chv && r < RK) src = sw + (int64_t)k * D + dl;
-      rows[kk] = src ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      u32x2 v;
-      v[0] = elem16(rows[0], j) | (elem16(rows[1], j) << 16);
-      v[1] = elem16(rows[2], j) | (elem16(rows[3], j) << 16);
-      lds[(kc * 8 + j) * 64 + lane] = v;
-    }
-  }
-}
-
-template <typename T, int W, int RC>
-__global__ __launch_bounds__(256) void lr_fwd_mfma(const T* __restrict__ x_, const T* __restrict__ z_,
-                                                   const T* __restrict__ U_, const T* __restrict__ sw_,
-                                                   T* __restrict__ y_, LrArgs a) {
-  const uint16_t* __restrict__ x = reinterpret_cast<const uint16_t*>(x_);
-  const uint16_t* __restrict__ z = reinterpret_cast<const uint16_t*>(z_);
-  const uint16_t* __restrict__ U = reinterpret_cast<const uint16_t*>(U_);
-  const uint16_t* __restrict__ sw = reinterpret_cast<const uint16_t*>(sw_);
-  uint16_t* __restrict__ y = reinterpret_cast<uint16_t*>(y_);
-  __shared__ u32x2 ub[W * RC * 8 * 64];
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int q = lane >> 4, n = lane & 15;
-  const int lb = xcd_remap(blockIdx.x, a.nblk);
-  const int chunk = lb % a.nch, sgp = lb / a.nch;  // 4 wavefronts: one chunk, 4 consecutive runs
-  const int D = a.D;
-  const int dl = chunk * 128 + 8 * n;  // first channel of the lane's octet
-  const bool chv = dl < D;             // D % 8 == 0: octets are whole
-  stage_u<W, RC>(ub, U, sw, a.R, a.RK, D, dl, chv, q, lane, wave);
-  __syncthreads();
-
-  const int sg = sgp * 4 + wave;
-  if (sg >= a.nseg) return;
-  const int b = sg / a.nspb;
-  const int ntile = (a.Tn + 15) >> 4;
-  const int tile0 = (sg - b * a.nspb) * a.seg;
-  const int tile1 = min(tile0 + a.seg, ntile);
-
-  const int64_t row0 = (int64_t)b * a.Tn;
-  for (int tile = tile0; tile < tile1; ++tile) {
-    const int t0 = tile * 16;
-    // A operands: z_eff[t0 + n, 16c + 4q + kk].
-    u32x2 za[RC];
-    {
-      const int t = t0 + n;
-#pragma unroll
-      for (int c = 0; c < RC; ++c) {
-        uint32_t e[4];
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) e[kk] = t < a.Tn ? zbits<T>(z, row0 + t, a.R, a.RK, 16 * c + 4 * q + kk) : 0u;
-        za[c][0] = e[0] | (e[1] << 16);
-        za[c][1] = e[2] | (e[3] << 16);
-      }
-    }
-    // x rows t0 + 4q - (W-1) .. t0 + 4q + 3.
-    u32x4 xr[W + 3];
-#pragma unroll
-    for (int m = 0; m < W + 3; ++m) {
-      const int t = t0 + 4 * q - (W - 1) + m;
-      xr[m] = (chv && t >= 0 && t < a.Tn) ? *reinterpret_cast<const u32x4*>(x + (row0 + t) * D + dl)
-                                          : u32x4{0u, 0u, 0u, 0u};
-    }
-    float acc[4][8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
-#pragma unroll
-    for (int k = 0; k < W; ++k) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        f32x4 wk = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < RC; ++c) wk = Mma16<T>::run(za[c], ub[((k * RC + c) * 8 + j) * 64 + lane], wk);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          acc[i][j] = fmaf(wk[i], Mma16<T>::to_f(elem16(xr[i - k + W - 1], j)), acc[i][j]);
-      }
-      // Consume tap k's weights before issuing tap k+1's products: keeps the
-      // live accumulators at 8 x 4 instead of W x 8 x 4 (occupancy).
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (a.residual) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] += Mma16<T>::to_f(elem16(xr[i + W - 1], j));
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = t0 + 4 * q + i;
-      if (chv && t < a.Tn) {
-        u32x4 o;
-#pragma unroll
-        for (int h = 0; h < 4; ++h) o[h] = f2bits<T>(acc[i][2 * h]) | (f2bits<T>(acc[i][2 * h + 1]) << 16);
-        *reinterpret_cast<u32x4*>(y + (row0 + t) * D + dl) = o;
-      }
-    }
-  }
-}
-
 
 // ---------------------------------------------------------------- backward
 //
@@ -276,6 +39,7 @@ struct LrBwdArgs {
   int nspb;   // runs per sequence
   int nseg;   // B * nspb
   int nblk;   // ncg * nseg
+  int zvec;   // R % 4 == 0 and z 8-byte aligned: 8-byte z loads
   int64_t BT;
 };
 
@@ -331,25 +95,6 @@ __device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds, u32x2 (&u
   }
 }
 
-// Raw buffer resources.  A descriptor covers one sequence ([T, C] elements);
-// the hardware returns 0 for loads and drops stores whose VGPR byte offset is
-// >= the range, which handles rows before 0 (negative offsets wrap to large
-// unsigned values), rows past T and channels past D (lane offset kOobLane)
-// without branches or clamped addresses.  The host only takes this path when
-// one sequence spans at most kMaxSeqBytes, so no offset can wrap back into range.
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-constexpr int kOobLane = 0x60000000;
-constexpr int64_t kMaxSeqBytes = int64_t(1) << 29;
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ u32x2 bload64(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0); }
-__device__ __forceinline__ uint32_t bload16(rsrc_t r, int off) {
-  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-}
-__device__ __forceinline__ void bstore64(u32x2 v, rsrc_t r, int off) { __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 0); }
-
 template <typename T, int W, int RC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && RC == 1 ? 2 : 1, 8))) void lr_bwd_mfma(
     const T* __restrict__ x_, const T* __restrict__ z_, const T* __restrict__ U_, const T* __restrict__ sw_,
@@ -375,7 +120,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
   constexpr int DZB = (UWREG && RC == 1) ? 4 : 1;
   __shared__ float dzred[2][4][DZB][RC * 256];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int q = lane >> 4, n = lane & 15;
   const int lb = xcd_remap(blockIdx.x, a.nblk);
   const int cg = lb % a.ncg, sg = lb / a.ncg;
@@ -391,7 +136,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
   const int tile1 = min(tile0 + a.seg, ntile);
   const int64_t row0 = (int64_t)b * Tn;
   const int R = a.R, RK = a.RK;
-  const bool zvec = (R & 3) == 0;
+  const bool zvec = a.zvec;
   u32x2* __restrict__ my_uw = uw_lds[wave];
   u32x4* __restrict__ my_uz = uz_lds[wave];
   uint16_t* __restrict__ my_g = gtile[wave];
@@ -438,26 +183,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
     // z_eff rows t0+4bb+n, ranks 16c+4q..+3: A operand of the tap-weight MFMA.
     u32x2 zA[NB][RC];
 #pragma unroll
-    for (int bb = 0; bb < NB; ++bb) {
-      const int t = t0 + 4 * bb + n;
-#pragma unroll
-      for (int c = 0; c < RC; ++c) {
-        const int r0 = 16 * c + 4 * q;
-        if (zvec && r0 + 3 < R) {  // 4 dynamic ranks, 8-byte aligned (R % 4 == 0)
-          zA[bb][c] = bload64(rz, (t * R + r0) * 2);
-        } else {
-          uint32_t e[4];
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk) {
-            const int r = r0 + kk;
-            const uint32_t v = bload16(rz, (t * R + min(r, R - 1)) * 2);
-            e[kk] = r < R ? v : ((r < RK && t < Tn) ? (uint32_t)Mma16<T>::kOne : 0u);
-          }
-          zA[bb][c][0] = e[0] | (e[1] << 16);
-          zA[bb][c][1] = e[2] | (e[3] << 16);
-        }
-      }
-    }
+    for (int bb = 0; bb < NB; ++bb) load_za<T, RC>(zA[bb], rz, t0 + 4 * bb + n, R, RK, Tn, q, zvec);
     // z_eff transposed (rank n, rows 4q..4q+3), the A operand of the dU MFMA,
     // from row block 0 through the exact identity transpose.
     u32x2 zT[RC];
@@ -542,7 +268,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
       u32x2 o;
       o[0] = pack2<T>(v[0], v[1]);
       o[1] = pack2<T>(v[2], v[3]);
-      bstore64(o, rdx, lane_off + toff + i * rowb);
+      bstore64<true>(o, rdx, lane_off + toff + i * rowb);
     }
     // ---- dz: gather this wavefront's tile sums; every DZB tiles (and at the end of
     // the run) add the 4 chunk wavefronts in wave order, one partial per group.
@@ -584,51 +310,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
 // ------------------------------------------------------------------- host
 namespace {
 
-bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
-
-LrArgs make_args(const LrProblem& p, int target_waves) {
-  LrArgs a;
-  a.Tn = (int)p.T;
-  a.D = (int)p.D;
-  a.R = (int)p.R;
-  a.RK = (int)p.R + (p.static_w ? 1 : 0);
-  a.has_static = p.static_w != nullptr;
-  a.residual = p.residual;
-  a.nch = (int)((p.D + 127) / 128);
-  a.ncg = 0;
-  const int64_t ntile = (p.T + 15) / 16;
-  int64_t seg = (p.B * ntile * a.nch + target_waves - 1) / target_waves;
-  if (seg < 1) seg = 1;
-  if (seg > ntile) seg = ntile;
-  a.seg = (int)seg;
-  a.nspb = (int)((ntile + seg - 1) / seg);
-  a.nseg = (int)(p.B * a.nspb);
-  a.nblk = ((a.nseg + 3) / 4) * a.nch;
-  return a;
-}
-
-template <typename T, int W, int RC>
-hipError_t launch_fwd(const LrProblem& p) {
-  const LrArgs a = make_args(p, 2048);
-  lr_fwd_mfma<T, W, RC><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.U,
-                                                       (const T*)p.static_w, (T*)p.y, a);
-  return hipGetLastError();
-}
-
-template <typename T>
-hipError_t dispatch_fwd(const LrProblem& p) {
-  const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
-#define DC_LR_CASE(WW, CC) \
-  if (p.W == WW && rc == CC) return launch_fwd<T, WW, CC>(p);
-  DC_LR_CASE(1, 1) DC_LR_CASE(1, 2) DC_LR_CASE(1, 3) DC_LR_CASE(1, 4)
-  DC_LR_CASE(2, 1) DC_LR_CASE(2, 2) DC_LR_CASE(2, 3) DC_LR_CASE(2, 4)
-  DC_LR_CASE(3, 1) DC_LR_CASE(3, 2)
-  DC_LR_CASE(4, 1) DC_LR_CASE(4, 2)
-  DC_LR_CASE(5, 1) DC_LR_CASE(6, 1) DC_LR_CASE(7, 1) DC_LR_CASE(8, 1)
-#undef DC_LR_CASE
-  return hipErrorInvalidValue;
-}
-
 LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   LrBwdArgs a;
   a.Tn = (int)p.T;
@@ -647,6 +328,7 @@ LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   a.nseg = (int)(p.B * a.nspb);
   a.nblk = a.nseg * a.ncg;
   a.BT = p.B * p.T;
+  a.zvec = p.R % 4 == 0 && aligned_to(p.z, 8);
   return a;
 }
 
@@ -698,30 +380,10 @@ hipError_t dispatch_bwd(const LrProblem& p) {
   return hipErrorInvalidValue;
 }
 
-bool aligned8(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
 
 }  // namespace
 
-bool lr_mfma_ok_impl(const LrProblem& p, bool bwd) {
-  if (p.dtype != kBF16 && p.dtype != kFP16) return false;
-  if (p.W < 1 || p.W > 8) return false;
-  const int64_t rc = (p.R + (p.static_w ? 1 : 0) + 15) / 16;
-  if (rc > 4 || p.W * rc > 8) return false;  // staged operands / accumulators bound W*RC
-  if (bwd && rc == 4 && p.W > 1) return false;  // backward LDS (operands + dz sums) above 160 KiB
-  if (!bwd) {
-    if (p.D % 8 != 0) return false;
-    return aligned16(p.x) && aligned16(p.U) && aligned16(p.static_w) && aligned16(p.y);
-  }
-  if (p.D % 16 != 0) return false;
-  if (p.T * p.D * 2 > kMaxSeqBytes) return false;  // buffer-offset range of one sequence
-  return aligned8(p.x) && aligned8(p.dy) && aligned8(p.dx) && aligned16(p.U) && aligned16(p.static_w);
-}
-
 int64_t lr_mfma_ws_bytes(const LrProblem& p) { return bwd_ws(p, make_bwd_args(p, kBwdTargetWaves)).total; }
-
-hipError_t lr_mfma_fwd(const LrProblem& p) {
-  return p.dtype == kBF16 ? dispatch_fwd<bf16>(p) : dispatch_fwd<fp16>(p);
-}
 
 hipError_t lr_mfma_bwd(const LrProblem& p) {
   return p.dtype == kBF16 ? dispatch_bwd<bf16>(p) : dispatch_bwd<fp16>(p);

@@ -1,0 +1,205 @@
+// Lowrank forward on gfx950 matrix cores (bf16 / fp16): y from x, z, U (and static_w).
+//
+// Forward tile (lr_fwd_mfma).  A wavefront owns 16 rows x 128 channels.
+// Lane l = 16*q + n owns rows 4q..4q+3 and the channel octet 8n..8n+7.
+// For each tap k the per-token weights come from eight
+// v_mfma_f32_16x16x16 (bf16|f16) products, one per j = 0..7, whose 16
+// output columns are the channels 8*col + j: the accumulator layout of the
+// 16x16 MFMA (lane l holds rows 4q..4q+3 of column n) then leaves every lane
+// holding exactly its own 8 channels for its own 4 rows, so the weights
+// multiply 128-bit rows of x in registers and are never written anywhere.
+// The B operands (U_eff, 16 ranks x 8 columns per lane) are loaded once per
+// run as 128-bit row pieces and repacked; the A operand is the lane's row
+// of z_eff.  Reference: lowrank.py:24-67 (Triton forward kernel).
+#include "lowrank_mfma.h"
+
+namespace dc {
+
+struct LrArgs {
+  int Tn;          // sequence length
+  int D;           // channels
+  int R;           // dynamic rank (z.shape[-1])
+  int RK;          // kernel rank = R + has_static
+  int has_static;
+  int residual;
+  int nch;         // ceil(D / 128): 128-channel chunks, one per wavefront
+  int ncg;         // unused
+  int seg;         // 16-row tiles per run
+  int nspb;        // runs per sequence
+  int nseg;        // B * nspb
+  int nblk;        // grid size
+  int zvec;        // R % 4 == 0 and z 8-byte aligned: 8-byte z loads
+};
+
+// Packed B operands of one 128-channel chunk, staged once per workgroup:
+// ub[(k*RC + c)*8 + j][lane] = U_eff[16c + 4q + kk, k*D + dl + j], kk = 0..3.
+template <int W, int RC>
+__device__ __forceinline__ void stage_u(u32x2* __restrict__ lds, const uint16_t* __restrict__ U,
+                                        const uint16_t* __restrict__ sw, int R, int RK, int D, int dl, bool chv,
+                                        int q, int lane, int wave) {
+  const int64_t WD = (int64_t)W * D;
+  for (int kc = wave; kc < W * RC; kc += 4) {
+    const int k = kc / RC, c = kc - k * RC;
+    u32x4 rows[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int r = 16 * c + 4 * q + kk;
+      const uint16_t* src = nullptr;
+      if (chv && r < R) src = U + (int64_t)r * WD + (int64_t)k * D + dl;
+      else if (chv && r < RK) src = sw + (int64_t)k * D + dl;
+      rows[kk] = src ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      u32x2 v;
+      v[0] = elem16(rows[0], j) | (elem16(rows[1], j) << 16);
+      v[1] = elem16(rows[2], j) | (elem16(rows[3], j) << 16);
+      lds[(kc * 8 + j) * 64 + lane] = v;
+    }
+  }
+}
+
+template <typename T, int W, int RC>
+__global__ __launch_bounds__(256) void lr_fwd_mfma(const T* __restrict__ x_, const T* __restrict__ z_,
+                                                   const T* __restrict__ U_, const T* __restrict__ sw_,
+                                                   T* __restrict__ y_, LrArgs a) {
+  constexpr int NR = W + 3;  // x rows 4q-W+1 .. 4q+3 of a lane
+  const uint16_t* __restrict__ x = reinterpret_cast<const uint16_t*>(x_);
+  const uint16_t* __restrict__ z = reinterpret_cast<const uint16_t*>(z_);
+  const uint16_t* __restrict__ U = reinterpret_cast<const uint16_t*>(U_);
+  const uint16_t* __restrict__ sw = reinterpret_cast<const uint16_t*>(sw_);
+  uint16_t* __restrict__ y = reinterpret_cast<uint16_t*>(y_);
+  __shared__ u32x2 ub[W * RC * 8 * 64];
+
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int q = lane >> 4, n = lane & 15;
+  const int lb = xcd_remap(blockIdx.x, a.nblk);
+  const int chunk = lb % a.nch, sgp = lb / a.nch;  // 4 wavefronts: one chunk, 4 consecutive runs
+  const int D = a.D, Tn = a.Tn, R = a.R, RK = a.RK;
+  const int dl = chunk * 128 + 8 * n;  // first channel of the lane's octet
+  const bool chv = dl < D;             // D % 8 == 0: octets are whole
+  stage_u<W, RC>(ub, U, sw, R, RK, D, dl, chv, q, lane, wave);
+  __syncthreads();
+
+  const int sg = sgp * 4 + wave;
+  if (sg >= a.nseg) return;
+  const int b = sg / a.nspb;
+  const int ntile = (Tn + 15) >> 4;
+  const int tile0 = (sg - b * a.nspb) * a.seg;
+  const int tile1 = min(tile0 + a.seg, ntile);
+  const int64_t row0 = (int64_t)b * Tn;
+  const int rowb = D * 2;
+  const rsrc_t rx = make_rsrc(x + row0 * D, (int64_t)Tn * rowb);
+  const rsrc_t ry = make_rsrc(y + row0 * D, (int64_t)Tn * rowb);
+  const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 2);
+  const int lane_off = chv ? (4 * q * D + dl) * 2 : kOobLane;  // byte offset of the lane's row 4q octet
+  const bool zvec = a.zvec;
+
+  // Tile inputs (rows out of the sequence read as 0): the current tile's and,
+  // in flight while it is computed, the next one's.
+  u32x4 xc[NR], xn[NR];
+  u32x2 zc[RC], zn[RC];
+  auto load_tile = [&](int tile, u32x4(&xr)[NR], u32x2(&za)[RC]) {
+    const int toff = tile * 16 * rowb;
+#pragma unroll
+    for (int m = 0; m < NR; ++m) xr[m] = bload128(rx, lane_off + toff + (m - (W - 1)) * rowb);
+    load_za<T, RC>(za, rz, tile * 16 + n, R, RK, Tn, q, zvec);
+  };
+  if (tile0 < tile1) load_tile(tile0, xc, zc);
+  for (int tile = tile0; tile < tile1; ++tile) {
+    if (tile + 1 < tile1) load_tile(tile + 1, xn, zn);
+    float acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        f32x4 wk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < RC; ++c) wk = Mma16<T>::run(zc[c], ub[((k * RC + c) * 8 + j) * 64 + lane], wk);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[i][j] = fmaf(wk[i], Mma16<T>::to_f(elem16(xc[i - k + W - 1], j)), acc[i][j]);
+      }
+      // Consume tap k's weights before issuing tap k+1's products: keeps the
+      // live accumulators at 8 x 4 instead of W x 8 x 4 (occupancy).
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (a.residual) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] += Mma16<T>::to_f(elem16(xc[i + W - 1], j));
+    }
+    const int toff = tile * 16 * rowb;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u32x4 o;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) o[h] = pack2<T>(acc[i][2 * h], acc[i][2 * h + 1]);
+      bstore128<true>(o, ry, lane_off + toff + i * rowb);
+    }
+#pragma unroll
+    for (int m = 0; m < NR; ++m) xc[m] = xn[m];
+#pragma unroll
+    for (int c = 0; c < RC; ++c) zc[c] = zn[c];
+  }
+}
+
+// ------------------------------------------------------------------- host
+namespace {
+
+LrArgs make_args(const LrProblem& p, int target_waves) {
+  LrArgs a;
+  a.Tn = (int)p.T;
+  a.D = (int)p.D;
+  a.R = (int)p.R;
+  a.RK = (int)p.R + (p.static_w ? 1 : 0);
+  a.has_static = p.static_w != nullptr;
+  a.residual = p.residual;
+  a.nch = (int)((p.D + 127) / 128);
+  a.ncg = 0;
+  a.zvec = p.R % 4 == 0 && aligned_to(p.z, 8);
+  const int64_t ntile = (p.T + 15) / 16;
+  int64_t seg = (p.B * ntile * a.nch + target_waves - 1) / target_waves;
+  if (seg < 1) seg = 1;
+  if (seg > ntile) seg = ntile;
+  a.seg = (int)seg;
+  a.nspb = (int)((ntile + seg - 1) / seg);
+  a.nseg = (int)(p.B * a.nspb);
+  a.nblk = ((a.nseg + 3) / 4) * a.nch;
+  return a;
+}
+
+template <typename T, int W, int RC>
+hipError_t launch_fwd(const LrProblem& p) {
+  const LrArgs a = make_args(p, 2048);
+  lr_fwd_mfma<T, W, RC><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.U,
+                                                       (const T*)p.static_w, (T*)p.y, a);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t dispatch_fwd(const LrProblem& p) {
+  const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
+#define DC_LR_CASE(WW, CC) \
+  if (p.W == WW && rc == CC) return launch_fwd<T, WW, CC>(p);
+  DC_LR_CASE(1, 1) DC_LR_CASE(1, 2) DC_LR_CASE(1, 3) DC_LR_CASE(1, 4)
+  DC_LR_CASE(2, 1) DC_LR_CASE(2, 2) DC_LR_CASE(2, 3) DC_LR_CASE(2, 4)
+  DC_LR_CASE(3, 1) DC_LR_CASE(3, 2)
+  DC_LR_CASE(4, 1) DC_LR_CASE(4, 2)
+  DC_LR_CASE(5, 1) DC_LR_CASE(6, 1) DC_LR_CASE(7, 1) DC_LR_CASE(8, 1)
+#undef DC_LR_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t lr_mfma_fwd(const LrProblem& p) {
+  return p.dtype == kBF16 ? dispatch_fwd<bf16>(p) : dispatch_fwd<fp16>(p);
+}
+
+}  // namespace dc
