@@ -94,6 +94,81 @@ struct Raw {
   }
 };
 
+// ------------------------------------------------------- buffer resources
+// Raw buffer resources: the hardware checks every lane's byte offset against
+// the resource's range, returns 0 for loads and drops stores at or beyond it
+// (offsets are unsigned, so a negative offset is out of range too).  Kernels
+// use this for rows outside a sequence or run and lanes outside D, which keeps
+// loads free of branches: a load under a branch, or one whose result is used
+// at once, would make the compiler wait for every load issued before it
+// (vmcnt counts in order).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// Cache-policy operand of a buffer store: nontemporal (gfx940 family `nt` bit).
+constexpr int kNt = 2;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload128(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
+__device__ __forceinline__ u32x2 bload64(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0); }
+__device__ __forceinline__ uint32_t bload32(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
+__device__ __forceinline__ uint32_t bload16(rsrc_t r, int off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+template <bool NT>
+__device__ __forceinline__ void bstore64(u32x2 v, rsrc_t r, int off) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, NT ? kNt : 0);
+}
+template <bool NT>
+__device__ __forceinline__ void bstore128(u32x4 v, rsrc_t r, int off) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, NT ? kNt : 0);
+}
+
+// Load / store of one unit of A bytes (A = 2, 4, 8, 16) through a buffer resource.
+template <int A> struct BufUnit;
+template <> struct BufUnit<16> {
+  __device__ static __forceinline__ u32x4 load(rsrc_t r, int off) { return bload128(r, off); }
+  template <bool NT> __device__ static __forceinline__ void store(u32x4 v, rsrc_t r, int off) { bstore128<NT>(v, r, off); }
+};
+template <> struct BufUnit<8> {
+  __device__ static __forceinline__ u32x2 load(rsrc_t r, int off) { return bload64(r, off); }
+  template <bool NT> __device__ static __forceinline__ void store(u32x2 v, rsrc_t r, int off) { bstore64<NT>(v, r, off); }
+};
+template <> struct BufUnit<4> {
+  __device__ static __forceinline__ uint32_t load(rsrc_t r, int off) { return bload32(r, off); }
+  template <bool NT> __device__ static __forceinline__ void store(uint32_t v, rsrc_t r, int off) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, NT ? kNt : 0);
+  }
+};
+template <> struct BufUnit<2> {
+  __device__ static __forceinline__ uint16_t load(rsrc_t r, int off) {
+    return (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  }
+  template <bool NT> __device__ static __forceinline__ void store(uint16_t v, rsrc_t r, int off) {
+    __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, NT ? kNt : 0);
+  }
+};
+
+// Raw<T, N> through a buffer resource: unconditional loads (an out-of-range
+// offset reads 0) and stores (an out-of-range offset writes nothing).
+template <typename T, int N>
+__device__ __forceinline__ void bload_raw(Raw<T, N>& v, rsrc_t r, int off) {
+  typedef Raw<T, N> R;
+#pragma unroll
+  for (int i = 0; i < R::NU; ++i) v.u[i] = BufUnit<R::A>::load(r, off + i * R::A);
+}
+template <typename T, int N, bool NT = false>
+__device__ __forceinline__ void bstore_vals(rsrc_t r, int off, const float* in) {
+  typedef Raw<T, N> R;
+  T e[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) e[i] = (T)in[i];  // round-to-nearest-even
+  typename R::U u[R::NU];
+  __builtin_memcpy(u, e, R::BYTES);
+#pragma unroll
+  for (int i = 0; i < R::NU; ++i) BufUnit<R::A>::template store<NT>(u[i], r, off + i * R::A);
+}
+
 template <int N>
 __device__ __forceinline__ void zero_vals(float* v) {
 #pragma unroll
@@ -123,18 +198,5 @@ __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-// Sum over aligned groups of `n` lanes (n a power of two, 1..64), leaving the
-// group sum in every lane of the group.  Groups up to 16 lanes use DPP
-// (quad_perm xor 1, xor 2, row_half_mirror, row_mirror: each pairs a lane
-// with one of the other half of its group); 32 and 64 use ds_bpermute.
-__device__ __forceinline__ float group_sum(float v, int n) {
-  if (n >= 2) v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
-  if (n >= 4) v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
-  if (n >= 8) v += dpp_f<0x141>(v);  // row_half_mirror
-  if (n >= 16) v += dpp_f<0x140>(v); // row_mirror
-  if (n >= 32) v += __shfl_xor(v, 16);
-  if (n >= 64) v += __shfl_xor(v, 32);
-  return v;
-}
 
 }  // namespace dc

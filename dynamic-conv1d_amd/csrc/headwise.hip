@@ -129,6 +129,13 @@ int choose_seg(int64_t B, int64_t T, int64_t nvg, int W, int target_waves) {
   return (int)seg;
 }
 
+// Bytes of the larger of a row of x and a row of weight.
+int64_t max_row_bytes(const HwProblem& p) {
+  const int64_t es = dtype_size(p.dtype);
+  const int64_t xb = p.D * es, wb = p.H * p.W * es;
+  return xb > wb ? xb : wb;
+}
+
 HwPlan make_plan(const HwProblem& p, bool bwd) {
   const int VEC = 16 / dtype_size(p.dtype);
   const int64_t hs = p.D / p.H;
@@ -141,6 +148,10 @@ HwPlan make_plan(const HwProblem& p, bool bwd) {
   a.nvc = (int)(p.D / VEC);
   a.nvg = (a.nvc + 63) / 64;
   a.seg = choose_seg(p.B, p.T, a.nvg, (int)p.W, 1024);
+  // a run's buffer resources span (seg + kHwSlackRows) rows at most kHwRunBytes
+  const int u = unroll_of((int)p.W);
+  const int64_t seg_cap = (kHwRunBytes / max_row_bytes(p) - kHwSlackRows) / u * u;
+  if (a.seg > seg_cap) a.seg = (int)seg_cap;
   a.nspb = (int)((p.T + a.seg - 1) / a.seg);
   a.nseg = (int)(p.B * a.nspb);
   const int nsg = (a.nseg + 3) / 4;
@@ -205,6 +216,8 @@ bool hw_fast_ok(const HwProblem& p, bool bwd) {
   if (p.D % VEC != 0) return false;
   if ((hs & (hs - 1)) != 0) return false;  // power-of-two head size
   if (hs > 64 * VEC) return false;         // a head must fit in one wavefront
+  // buffer offsets: a run of at least one chunk must fit the resource range
+  if ((unroll_of((int)p.W) + kHwSlackRows) * max_row_bytes(p) > kHwRunBytes) return false;
   if (!aligned(p.x, 16) || !aligned(p.static_w, 16)) return false;
   // weight rows start at multiples of NHL*W elements; require that alignment.
   const int64_t nwe_bytes = (hs < VEC ? VEC / hs : 1) * p.W * es;

@@ -11,14 +11,22 @@
 // channels (one 128-bit load per row) and walks a run of `seg` consecutive
 // rows of one sequence, keeping the last W rows of x (forward) or the W open
 // dx accumulators (backward) in a register ring whose slot for row t is
-// (t - t0) mod W.  The row loop is unrolled by a multiple of W so every ring
-// index is a compile-time constant.  Each row costs exactly one 128-bit load
-// of x (and dy), one contiguous load of the lane's NHL*W weights, and one
-// 128-bit store: the HBM traffic is the algorithmic traffic plus a W-1 row
-// halo per run.  64 lanes of a wavefront cover 64*VEC consecutive channels
-// (a 1 KiB contiguous row segment per load instruction); a 256-thread
-// workgroup stacks 4 wavefronts on 4 consecutive runs of the same channels,
-// so a run's halo rows were just read by the wavefront above it.
+// (t - t0) mod W.  Rows are processed in chunks of U (a multiple of W), so
+// every ring index is a compile-time constant.  Each row costs exactly one
+// 128-bit load of x (and dy), one contiguous load of the lane's NHL*W
+// weights, and one 128-bit store: the HBM traffic is the algorithmic traffic
+// plus a W-1 row halo per run.  64 lanes of a wavefront cover 64*VEC
+// consecutive channels (a 1 KiB contiguous row segment per load instruction);
+// a 256-thread workgroup stacks 4 wavefronts on 4 consecutive runs of the same
+// channels, so a run's halo rows were just read by the wavefront above it.
+//
+// Memory pipeline.  All row traffic goes through buffer resources that cover
+// the run's rows (rows before 0 or past T, and lanes past D, read 0 and drop
+// stores), so no load sits under a branch.  Two chunk buffers, A and B,
+// alternate: the next chunk's loads are issued before the current chunk is
+// computed and no register is copied between them, so the compiler's waits
+// stay partial (vmcnt counts in order: a load under a branch or a copy of a
+// just-loaded register would make it wait for every load in flight).
 //
 // Backward.  dx uses the scatter form: the row-t terms dy[t]*(w[t,k]+sw[k])
 // are added into the open accumulator of row t-k; row t-W+1 is complete
@@ -29,10 +37,10 @@
 // stores of it straight from the lanes write each 128-byte line in several
 // partial pieces, which measured ~30% below contiguous stores; the wavefront
 // then passes its dweight row through LDS and stores it as 16-byte lane
-// pieces that are contiguous across the wavefront (TDW).  dstatic_w partial sums stay in registers
-// for the whole run, are added across the 4 wavefronts of the workgroup in
-// LDS in a fixed order, and one fp32 partial per workgroup is summed by
-// reduce_partials (no atomics: bitwise deterministic).
+// pieces that are contiguous across the wavefront (TDW).  dstatic_w partial
+// sums stay in registers for the whole run, are added across the 4 wavefronts
+// of the workgroup in LDS in a fixed order, and one fp32 partial per workgroup
+// is summed by reduce_partials (no atomics: bitwise deterministic).
 #pragma once
 
 #include "dc_common.h"
@@ -58,12 +66,67 @@ struct HwArgs {
   int has_static;
 };
 
-// Rows per unrolled chunk: a multiple of W, at least 4.
+// Rows per chunk: a multiple of W, at least 4.
 template <int W> struct Unroll { static constexpr int value = (W >= 4) ? W : W * (4 / W); };
 
 template <int W>
 __device__ __forceinline__ constexpr int ring(int u, int k) {
   return ((u - k) % W + W) % W;
+}
+
+// Buffer geometry of one run.  The resources start at row `base` = the run's
+// first halo row (max(t0 - (W-1), 0)) and end at T (capped at kHwRunBytes);
+// the host keeps (seg + kHwSlackRows) rows of x and of weight within
+// kHwRunBytes, so every in-range offset is below it, kHwRowOob (a row offset)
+// and kHwLaneOob (a lane offset) are out of range alone or together, and no
+// sum of offsets leaves int32.
+constexpr int kHwRunBytes = 1 << 29;
+constexpr int kHwRowOob = 1 << 29;
+constexpr int kHwLaneOob = 1 << 30;
+constexpr int kHwSlackRows = 40;
+
+struct HwRun {
+  int t0, t1;   // rows [t0, t1) of sequence b
+  int base;     // first row covered by the resources
+  int rowb;     // bytes per row of x / y / dy / dx
+  int wrowb;    // bytes per row of weight / dweight
+  int64_t xrow0, wrow0;  // element offsets of row `base` of sequence b
+  int xrec, wrec;        // resource ranges (bytes)
+  __device__ __forceinline__ HwRun(const HwArgs& a, int s, int W, int es) {
+    const int b = s / a.nspb;
+    t0 = (s - b * a.nspb) * a.seg;
+    t1 = min(t0 + a.seg, a.Tn);
+    base = max(t0 - (W - 1), 0);
+    rowb = a.D * es;
+    wrowb = a.H * W * es;
+    xrow0 = ((int64_t)b * a.Tn + base) * a.D;
+    wrow0 = ((int64_t)b * a.Tn + base) * a.H * W;
+    xrec = (int)min((int64_t)(a.Tn - base) * rowb, (int64_t)kHwRunBytes);
+    wrec = (int)min((int64_t)(a.Tn - base) * wrowb, (int64_t)kHwRunBytes);
+  }
+  // byte offset of row t, or the out-of-range row offset when !live
+  __device__ __forceinline__ int xrow(int t, bool live = true) const { return live ? (t - base) * rowb : kHwRowOob; }
+  __device__ __forceinline__ int wrow(int t, bool live = true) const { return live ? (t - base) * wrowb : kHwRowOob; }
+};
+
+// Sum over aligned groups of `n` lanes (n a power of two, 1..64), leaving the
+// group sum in every lane of the group: the DPP steps run always and are
+// selected by n (no branch); 32- and 64-lane groups add two ds_bpermute steps
+// under one wave-uniform branch.
+__device__ __forceinline__ float group_sum_sel(float v, int n) {
+  float d = dpp_f<0xB1>(v);  // quad_perm [1,0,3,2]
+  v = n >= 2 ? v + d : v;
+  d = dpp_f<0x4E>(v);        // quad_perm [2,3,0,1]
+  v = n >= 4 ? v + d : v;
+  d = dpp_f<0x141>(v);       // row_half_mirror
+  v = n >= 8 ? v + d : v;
+  d = dpp_f<0x140>(v);       // row_mirror
+  v = n >= 16 ? v + d : v;
+  if (n >= 32) {
+    v += __shfl_xor(v, 16);
+    if (n >= 64) v += __shfl_xor(v, 32);
+  }
+  return v;
 }
 
 // ------------------------------------------------------------------ forward
@@ -73,6 +136,7 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
   constexpr int VEC = VecOf<T>::value;
   constexpr int NWE = (VEC / HSV) * W;
   constexpr int U = Unroll<W>::value;
+  constexpr int ES = (int)sizeof(T);
   typedef Raw<T, VEC> XR;
   typedef Raw<T, NWE> WR;
   const int lb = xcd_remap(blockIdx.x, a.nblk);
@@ -80,87 +144,73 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
   const int wave = wave_id(), lane = threadIdx.x & 63;
   const int vc = vg * 64 + lane;
   const int s = sgp * 4 + wave;
-  if (s >= a.nseg || vc >= a.nvc) return;
-  const int b = s / a.nspb;
-  const int t0 = (s - b * a.nspb) * a.seg;
-  const int t1 = min(t0 + a.seg, a.Tn);
+  if (s >= a.nseg) return;
+  const HwRun run(a, s, W, ES);
+  const int t0 = run.t0, t1 = run.t1;
+  const bool lv = vc < a.nvc;
   const int d0 = vc * VEC;
-  const int h0 = d0 >> a.hs_shift;
-  const int64_t row0 = (int64_t)b * a.Tn;
+  const int xlo = lv ? d0 * ES : kHwLaneOob;
+  const int wlo = lv ? (d0 >> a.hs_shift) * W * ES : kHwLaneOob;
+  const rsrc_t rx = make_rsrc(x + run.xrow0, run.xrec);
+  const rsrc_t ry = make_rsrc(y + run.xrow0, run.xrec);
+  const rsrc_t rw = make_rsrc(wt + run.wrow0, run.wrec);
   const int64_t D = a.D;
-  const int64_t wrs = (int64_t)a.H * W;
-  const T* xp = x + row0 * D + d0;
-  const T* wp = wt + (row0 * a.H + h0) * W;
-  T* yp = y + row0 * D + d0;
 
   XR swr[W];
 #pragma unroll
   for (int k = 0; k < W; ++k) {
-    if (a.has_static)
+    if (a.has_static && lv)
       swr[k].load(sw + (int64_t)k * D + d0);
     else
       swr[k].zero();
   }
-  // x ring: row t lives in slot (t - t0) mod W.
+  // x ring: row t lives in slot (t - t0) mod W; rows before 0 read 0.
   XR xr[W];
   xr[0].zero();
 #pragma unroll
-  for (int i = 1; i < W; ++i) {
-    const int t = t0 - i;
-    if (t >= 0)
-      xr[W - i].load(xp + (int64_t)t * D);
-    else
-      xr[W - i].zero();
-  }
-  // Rows of the current chunk and, in flight meanwhile, of the next one.
-  XR xc[U], xn[U];
-  WR wc[U], wn[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int t = t0 + u;
-    if (t < t1) {
-      xc[u].load(xp + (int64_t)t * D);
-      wc[u].load(wp + (int64_t)t * wrs);
-    }
-  }
-  for (int tc = t0; tc < t1; tc += U) {
-    if (tc + U < t1) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int t = tc + U + u;
-        if (t < t1) {
-          xn[u].load(xp + (int64_t)t * D);
-          wn[u].load(wp + (int64_t)t * wrs);
-        }
-      }
-    }
+  for (int i = 1; i < W; ++i) bload_raw(xr[W - i], rx, xlo + run.xrow(t0 - i));
+
+  auto load_chunk = [&](int tc, XR(&xc)[U], WR(&wc)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int t = tc + u;
-      if (t < t1) {
-        const int p = u % W;
-        xr[p] = xc[u];
-        float acc[VEC];
-        zero_vals<VEC>(acc);
-#pragma unroll
-        for (int k = 0; k < W; ++k) {
-          const int q = ring<W>(u, k);
-#pragma unroll
-          for (int j = 0; j < VEC; ++j)
-            acc[j] = fmaf(wc[u].get((j / HSV) * W + k) + swr[k].get(j), xr[q].get(j), acc[j]);
-        }
-        if (a.residual) {
-#pragma unroll
-          for (int j = 0; j < VEC; ++j) acc[j] += xr[p].get(j);
-        }
-        store_vals<T, VEC, true>(yp + (int64_t)t * D, acc);
-      }
+      bload_raw(xc[u], rx, xlo + run.xrow(t, t < t1));
+      bload_raw(wc[u], rw, wlo + run.wrow(t, t < t1));
     }
+  };
+  auto compute_chunk = [&](int tc, const XR(&xc)[U], const WR(&wc)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      xc[u] = xn[u];
-      wc[u] = wn[u];
+      const int t = tc + u;
+      const int p = u % W;
+      xr[p] = xc[u];
+      float acc[VEC];
+      zero_vals<VEC>(acc);
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        const int q = ring<W>(u, k);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j)
+          acc[j] = fmaf(wc[u].get((j / HSV) * W + k) + swr[k].get(j), xr[q].get(j), acc[j]);
+      }
+      if (a.residual) {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[j] += xr[p].get(j);
+      }
+      bstore_vals<T, VEC, true>(ry, xlo + run.xrow(t, t < t1), acc);  // rows past the run: dropped
     }
+  };
+
+  XR xa[U], xb[U];
+  WR wa[U], wb[U];
+  load_chunk(t0, xa, wa);
+  for (int tc = t0; tc < t1; tc += 2 * U) {
+    load_chunk(tc + U, xb, wb);
+    __builtin_amdgcn_sched_barrier(0);  // the next chunk's loads go out before this chunk's waits
+    compute_chunk(tc, xa, wa);
+    load_chunk(tc + 2 * U, xa, wa);
+    __builtin_amdgcn_sched_barrier(0);
+    if (tc + U < t1) compute_chunk(tc + U, xb, wb);
   }
 }
 
@@ -181,6 +231,7 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
   constexpr int NHL = VEC / HSV;
   constexpr int NWE = NHL * W;
   constexpr int U = Unroll<W>::value;
+  constexpr int ES = (int)sizeof(T);
   typedef Raw<T, VEC> XR;
   typedef Raw<T, NWE> WR;
   const int lb = xcd_remap(blockIdx.x, a.nblk);
@@ -188,8 +239,7 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
   const int wave = wave_id(), lane = threadIdx.x & 63;
   const int vc = vg * 64 + lane;
   const int s = sgp * 4 + wave;
-  const bool active = (s < a.nseg) && (vc < a.nvc);
-  // TDW: the host guarantees nvc % 64 == 0, so `active` is wave-uniform.
+  // TDW: the host guarantees nvc % 64 == 0, so every lane is inside D.
   constexpr int NP = TDW ? TdwOf<T, W, HSV>::NP : 1;
   __shared__ u32x4 dwt[4][TDW ? NP * 64 : 1];
 
@@ -197,34 +247,33 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
 #pragma unroll
   for (int k = 0; k < W; ++k) zero_vals<VEC>(dsw[k]);
 
-  // Lanes of a head are aligned groups of `lph` consecutive columns and a
-  // wavefront of one run holds whole heads, so every lane of a group shares
-  // `active`; inactive lanes never take part in a shuffle.
-  if (active) {
-    const int b = s / a.nspb;
-    const int t0 = (s - b * a.nspb) * a.seg;
-    const int t1 = min(t0 + a.seg, a.Tn);
-    const int tend = t1 + W - 1;        // steps t0 .. tend-1: dx of row t needs dy, w of rows t .. t+W-1
-    const int tload = min(tend, a.Tn);  // dy / w rows that exist
+  // Lanes of a head are aligned groups of `lph` consecutive columns and D is a
+  // whole number of heads, so lanes past D form whole groups of their own.
+  if (s < a.nseg) {
+    const HwRun run(a, s, W, ES);
+    const int t0 = run.t0, t1 = run.t1;
+    const int tend = t1 + W - 1;  // steps t0 .. tend-1: dx of row t needs dy, w of rows t .. t+W-1
+    const bool lv = vc < a.nvc;
     const int d0 = vc * VEC;
-    const int h0 = d0 >> a.hs_shift;
-    const int64_t row0 = (int64_t)b * a.Tn;
+    const int xlo = lv ? d0 * ES : kHwLaneOob;
+    const int wlo = lv ? (d0 >> a.hs_shift) * W * ES : kHwLaneOob;
+    const int lph = a.lph;
+    const bool leader = (vc & (lph - 1)) == 0;
+    const int dwlo = leader ? wlo : kHwLaneOob;  // one lane of a head stores its dweight
+    // dweight byte offset of the wavefront's lane 0 (TDW: lanes own consecutive heads)
+    const int wlo0 = (((vc - lane) * VEC) >> a.hs_shift) * W * ES;
+    const rsrc_t rx = make_rsrc(x + run.xrow0, run.xrec);
+    const rsrc_t rdy = make_rsrc(dy + run.xrow0, run.xrec);
+    const rsrc_t rdx = make_rsrc(dx + run.xrow0, run.xrec);
+    const rsrc_t rw = make_rsrc(wt + run.wrow0, run.wrec);
+    const rsrc_t rdw = make_rsrc(dwt_ + run.wrow0, run.wrec);
+    const int residual = a.residual;
     const int64_t D = a.D;
-    const int64_t wrs = (int64_t)a.H * W;
-    const T* xp = x + row0 * D + d0;
-    const T* wp = wt + (row0 * a.H + h0) * W;
-    const T* dyp = dy + row0 * D + d0;
-    T* dxp = dx + row0 * D + d0;
-    T* dwp = dwt_ + (row0 * a.H + h0) * W;
-    // dweight row of the wavefront's lane 0 (TDW: lanes own consecutive heads)
-    T* dwp0 = dwt_ + (row0 * a.H + (((vc - lane) * VEC) >> a.hs_shift)) * W;
-    const bool leader = (vc & (a.lph - 1)) == 0;
-    const int residual = a.residual, lph = a.lph;
 
     XR swr[W];
 #pragma unroll
     for (int k = 0; k < W; ++k) {
-      if (HAS_STATIC)
+      if (HAS_STATIC && lv)
         swr[k].load(sw + (int64_t)k * D + d0);
       else
         swr[k].zero();
@@ -235,117 +284,100 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
     for (int k = 0; k < W; ++k) zero_vals<VEC>(dxa[k]);
     xr[0].zero();
 #pragma unroll
-    for (int i = 1; i < W; ++i) {
-      const int t = t0 - i;
-      if (t >= 0)
-        xr[W - i].load(xp + (int64_t)t * D);
-      else
-        xr[W - i].zero();
-    }
-    XR dyc[U], dyn[U], xc[U], xn[U];
-    WR wc[U], wn[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = t0 + u;
-      if (t < tload) {
-        dyc[u].load(dyp + (int64_t)t * D);
-        wc[u].load(wp + (int64_t)t * wrs);
-      } else {
-        dyc[u].zero();
-        wc[u].zero();
-      }
-      if (t < t1) xc[u].load(xp + (int64_t)t * D);
-    }
-    for (int tc = t0; tc < tend; tc += U) {
-      if (tc + U < tend) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int t = tc + U + u;
-          if (t < tload) {
-            dyn[u].load(dyp + (int64_t)t * D);
-            wn[u].load(wp + (int64_t)t * wrs);
-          } else {
-            dyn[u].zero();
-            wn[u].zero();
-          }
-          if (t < t1) xn[u].load(xp + (int64_t)t * D);
-        }
-      }
+    for (int i = 1; i < W; ++i) bload_raw(xr[W - i], rx, xlo + run.xrow(t0 - i));
+
+    struct Chunk {
+      XR dy[U], x[U];
+      WR w[U];
+    };
+    auto load_chunk = [&](int tc, Chunk& c) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int t = tc + u;
-        if (t < tend) {
-          const int p = u % W;
-          const bool main_row = t < t1;
-          float dyv[VEC];
-          dyc[u].to_float(dyv);
-          // dx[t-k] += dy[t] * (w[t, h, k] + sw[k]); row t opens with its k = 0 term.
-#pragma unroll
-          for (int j = 0; j < VEC; ++j) {
-            const float v = dyv[j] * (wc[u].get((j / HSV) * W) + swr[0].get(j));
-            dxa[p][j] = residual ? v + dyv[j] : v;
-          }
-#pragma unroll
-          for (int k = 1; k < W; ++k) {
-            const int q = ring<W>(u, k);
-#pragma unroll
-            for (int j = 0; j < VEC; ++j)
-              dxa[q][j] = fmaf(dyv[j], wc[u].get((j / HSV) * W + k) + swr[k].get(j), dxa[q][j]);
-          }
-          if (main_row) {
-            xr[p] = xc[u];
-            float dwv[NWE];
-#pragma unroll
-            for (int k = 0; k < W; ++k) {
-              const int q = ring<W>(u, k);
-              float pr[VEC];
-#pragma unroll
-              for (int j = 0; j < VEC; ++j) pr[j] = dyv[j] * xr[q].get(j);
-              if (HAS_STATIC) {
-#pragma unroll
-                for (int j = 0; j < VEC; ++j) dsw[k][j] += pr[j];
-              }
-#pragma unroll
-              for (int hh = 0; hh < NHL; ++hh) {
-                float sacc = 0.f;
-#pragma unroll
-                for (int j = 0; j < HSV; ++j) sacc += pr[hh * HSV + j];
-                dwv[hh * W + k] = sacc;
-              }
-            }
-            if (lph > 1) {
-#pragma unroll
-              for (int k = 0; k < NWE; ++k) dwv[k] = group_sum(dwv[k], lph);
-            }
-            if constexpr (TDW) {
-              // Lane l's piece j goes to slot l*NP + j; slot i*64 + l is then
-              // the wavefront's i-th contiguous 1 KiB.  One wavefront writes
-              // and reads its own slots, in order: no barrier.
-              T e[NWE];
-#pragma unroll
-              for (int i = 0; i < NWE; ++i) e[i] = (T)dwv[i];
-              u32x4 pc[NP];
-              __builtin_memcpy(pc, e, sizeof(pc));
-              u32x4* my = dwt[wave];
-#pragma unroll
-              for (int j = 0; j < NP; ++j) my[lane * NP + j] = pc[j];
-              u32x4* dst = reinterpret_cast<u32x4*>(dwp0 + (int64_t)t * wrs);
-#pragma unroll
-              for (int i = 0; i < NP; ++i) __builtin_nontemporal_store(my[i * 64 + lane], dst + i * 64 + lane);
-            } else {
-              if (leader) store_vals<T, NWE>(dwp + (int64_t)t * wrs, dwv);
-            }
-          }
-          const int tdone = t - (W - 1);
-          if (tdone >= t0 && tdone < t1) store_vals<T, VEC, true>(dxp + (int64_t)tdone * D, dxa[(u + 1) % W]);
-        }
+        bload_raw(c.dy[u], rdy, xlo + run.xrow(t, t < tend));  // rows past T read 0
+        bload_raw(c.w[u], rw, wlo + run.wrow(t, t < tend));
+        bload_raw(c.x[u], rx, xlo + run.xrow(t, t < t1));
       }
+    };
+    auto compute_chunk = [&](int tc, const Chunk& c) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        dyc[u] = dyn[u];
-        wc[u] = wn[u];
-        xc[u] = xn[u];
+        const int t = tc + u;
+        const int p = u % W;
+        float dyv[VEC];
+        c.dy[u].to_float(dyv);
+        // dx[t-k] += dy[t] * (w[t, h, k] + sw[k]); row t opens with its k = 0 term.
+        // Steps past tend read dy = w = 0 and add nothing.
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          const float v = dyv[j] * (c.w[u].get((j / HSV) * W) + swr[0].get(j));
+          dxa[p][j] = residual ? v + dyv[j] : v;
+        }
+#pragma unroll
+        for (int k = 1; k < W; ++k) {
+          const int q = ring<W>(u, k);
+#pragma unroll
+          for (int j = 0; j < VEC; ++j)
+            dxa[q][j] = fmaf(dyv[j], c.w[u].get((j / HSV) * W + k) + swr[k].get(j), dxa[q][j]);
+        }
+        if (t < t1) {  // wave-uniform; no loads below
+          xr[p] = c.x[u];
+          float dwv[NWE];
+#pragma unroll
+          for (int k = 0; k < W; ++k) {
+            const int q = ring<W>(u, k);
+            float pr[VEC];
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) pr[j] = dyv[j] * xr[q].get(j);
+            if (HAS_STATIC) {
+#pragma unroll
+              for (int j = 0; j < VEC; ++j) dsw[k][j] += pr[j];
+            }
+#pragma unroll
+            for (int hh = 0; hh < NHL; ++hh) {
+              float sacc = 0.f;
+#pragma unroll
+              for (int j = 0; j < HSV; ++j) sacc += pr[hh * HSV + j];
+              dwv[hh * W + k] = sacc;
+            }
+          }
+          if constexpr (HSV == VEC) {
+#pragma unroll
+            for (int k = 0; k < NWE; ++k) dwv[k] = group_sum_sel(dwv[k], lph);
+          }
+          if constexpr (TDW) {
+            // Lane l's piece j goes to slot l*NP + j; slot i*64 + l is then
+            // the wavefront's i-th contiguous 1 KiB.  One wavefront writes
+            // and reads its own slots, in order: no barrier.
+            T e[NWE];
+#pragma unroll
+            for (int i = 0; i < NWE; ++i) e[i] = (T)dwv[i];
+            u32x4 pc[NP];
+            __builtin_memcpy(pc, e, sizeof(pc));
+            u32x4* my = dwt[wave];
+#pragma unroll
+            for (int j = 0; j < NP; ++j) my[lane * NP + j] = pc[j];
+            const int o = wlo0 + run.wrow(t);
+#pragma unroll
+            for (int i = 0; i < NP; ++i) bstore128<true>(my[i * 64 + lane], rdw, o + (i * 64 + lane) * 16);
+          } else {
+            bstore_vals<T, NWE>(rdw, dwlo + run.wrow(t), dwv);
+          }
+        }
+        const int tdone = t - (W - 1);
+        bstore_vals<T, VEC, true>(rdx, xlo + run.xrow(tdone, tdone >= t0 && tdone < t1), dxa[(u + 1) % W]);
       }
+    };
+
+    Chunk ca, cb;
+    load_chunk(t0, ca);
+    for (int tc = t0; tc < tend; tc += 2 * U) {
+      load_chunk(tc + U, cb);
+      __builtin_amdgcn_sched_barrier(0);  // the next chunk's loads go out before this chunk's waits
+      compute_chunk(tc, ca);
+      load_chunk(tc + 2 * U, ca);
+      __builtin_amdgcn_sched_barrier(0);
+      if (tc + U < tend) compute_chunk(tc + U, cb);
     }
   }
 

@@ -91,62 +91,73 @@ __device__ __forceinline__ float q4f(const u32x2& v, int j) {
   return Mma16<T>::to_f(elem16x2(v, j));
 }
 
-// Raw buffer resources.  A descriptor covers one sequence ([T, C] elements);
-// the hardware returns 0 for loads and drops stores whose VGPR byte offset is
-// >= the range, which handles rows before 0 (negative offsets wrap to large
-// unsigned values), rows past T and channels past D (lane offset kOobLane)
-// without branches or clamped addresses.  The host takes these paths only when
-// (T + kSeqSlackRows) rows of a sequence span at most kMaxSeqBytes: every
-// offset a kernel forms (rows -7 .. T + 25, plus kOobLane) then stays below
-// 2^31, and every wrapped negative offset stays above kMaxSeqBytes.
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// Buffer resources (dc_common.h) of the lowrank kernels cover one sequence
+// ([T, C] elements): rows before 0 (negative offsets wrap to large unsigned
+// values), rows past T and channels past D (lane offset kOobLane) read 0 and
+// drop stores, without branches or clamped addresses.  The host takes these
+// paths only when (T + kSeqSlackRows) rows of a sequence span at most
+// kMaxSeqBytes: every offset a kernel forms (rows -7 .. T + 25, plus kOobLane)
+// then stays below 2^31, and every wrapped negative offset stays above
+// kMaxSeqBytes.
 constexpr int kOobLane = 0x40000000;
 constexpr int64_t kMaxSeqBytes = int64_t(1) << 29;
 constexpr int kSeqSlackRows = 32;
-// Cache-policy operand of a buffer store: nontemporal (gfx940 family `nt` bit).
-constexpr int kNt = 2;
 
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ u32x4 bload128(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
-__device__ __forceinline__ u32x2 bload64(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0); }
-__device__ __forceinline__ uint32_t bload16(rsrc_t r, int off) {
-  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-}
-template <bool NT>
-__device__ __forceinline__ void bstore64(u32x2 v, rsrc_t r, int off) {
-  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, NT ? kNt : 0);
-}
-template <bool NT>
-__device__ __forceinline__ void bstore128(u32x4 v, rsrc_t r, int off) {
-  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, NT ? kNt : 0);
-}
+// A byte offset that every buffer access of a sequence treats as out of range
+// (returns 0, touches no memory): the host guarantees a sequence's x / z
+// offsets stay below kMaxSeqBytes - kSeqSlackRows rows.
+constexpr int kOobTile = (int)kMaxSeqBytes;
 
 // A operands of a 16-row tile: z_eff[t, 16c+4q .. 16c+4q+3] for c < RC, where
-// t is the lane's row (column n of the MFMA's A).  8-byte loads when R % 4 == 0
-// (zvec) and the four ranks are dynamic; otherwise element loads, the static
-// rank R as 1 (inside the sequence) and zero ranks beyond.
-template <typename T, int RC>
-__device__ __forceinline__ void load_za(u32x2 (&za)[RC], rsrc_t rz, int t, int R, int RK, int Tn, int q, bool zvec) {
+// t is the lane's row (column n of the MFMA's A).  Split in two so the loads can
+// stay in flight: ZRaw::load issues them without branches or uses of the
+// results (vmcnt retires in order, so any use of a just-loaded value would also
+// wait for every load issued before it), ZRaw::finish forms the operands once
+// they are needed.  ZV (R % 4 == 0, z 8-byte aligned): one 8-byte load per rank
+// chunk, whose four ranks are all dynamic or all not; otherwise 2-byte element
+// loads.  Ranks >= R load nothing (out-of-range offset); finish sets the static
+// rank R (inside the sequence) to 1 and ranks beyond to 0.  `base` is the z
+// byte offset of row t, or kOobTile for a tile that does not exist.
+template <typename T, int RC, bool ZV>
+struct ZRaw {
+  u32x2 v[ZV ? RC : 1];
+  uint32_t e[ZV ? 1 : RC][4];
+
+  __device__ __forceinline__ void load(rsrc_t rz, int base, int R, int q) {
 #pragma unroll
-  for (int c = 0; c < RC; ++c) {
-    const int r0 = 16 * c + 4 * q;
-    if (zvec && r0 + 3 < R) {
-      za[c] = bload64(rz, (t * R + r0) * 2);
-    } else {
-      uint32_t e[4];
+    for (int c = 0; c < RC; ++c) {
+      const int r0 = 16 * c + 4 * q;
+      if constexpr (ZV) {
+        v[c] = bload64(rz, r0 < R ? base + r0 * 2 : kOobTile);
+      } else {
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int r = r0 + kk;
-        const uint32_t v = bload16(rz, (t * R + min(r, R - 1)) * 2);
-        e[kk] = r < R ? v : ((r < RK && t < Tn) ? (uint32_t)Mma16<T>::kOne : 0u);
+        for (int kk = 0; kk < 4; ++kk) e[c][kk] = bload16(rz, r0 + kk < R ? base + (r0 + kk) * 2 : kOobTile);
       }
-      za[c][0] = e[0] | (e[1] << 16);
-      za[c][1] = e[2] | (e[3] << 16);
     }
   }
-}
+  __device__ __forceinline__ void finish(u32x2 (&za)[RC], int t, int R, int RK, int Tn, int q) const {
+    const uint32_t one = (uint32_t)Mma16<T>::kOne;
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+      const int r0 = 16 * c + 4 * q;
+      if constexpr (ZV) {
+        // r0 == R < RK: the static rank opens this chunk
+        const uint32_t s = (r0 == R && R < RK && t < Tn) ? one : 0u;
+        za[c][0] = r0 < R ? v[c][0] : s;
+        za[c][1] = r0 < R ? v[c][1] : 0u;
+      } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const int r = r0 + kk;
+          w[kk] = r < R ? (e[c][kk] & 0xFFFFu) : ((r < RK && t < Tn) ? one : 0u);
+        }
+        za[c][0] = w[0] | (w[1] << 16);
+        za[c][1] = w[2] | (w[3] << 16);
+      }
+    }
+  }
+};
 
 inline bool aligned_to(const void* p, int a) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 

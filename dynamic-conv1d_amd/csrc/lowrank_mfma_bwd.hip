@@ -95,7 +95,7 @@ __device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds, u32x2 (&u
   }
 }
 
-template <typename T, int W, int RC>
+template <typename T, int W, int RC, bool ZV>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && RC == 1 ? 2 : 1, 8))) void lr_bwd_mfma(
     const T* __restrict__ x_, const T* __restrict__ z_, const T* __restrict__ U_, const T* __restrict__ sw_,
     const T* __restrict__ dy_, T* __restrict__ dx_, float* __restrict__ part_dz, float* __restrict__ part_du,
@@ -136,7 +136,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
   const int tile1 = min(tile0 + a.seg, ntile);
   const int64_t row0 = (int64_t)b * Tn;
   const int R = a.R, RK = a.RK;
-  const bool zvec = a.zvec;
+  typedef ZRaw<T, RC, ZV> ZR;
   u32x2* __restrict__ my_uw = uw_lds[wave];
   u32x4* __restrict__ my_uz = uz_lds[wave];
   uint16_t* __restrict__ my_g = gtile[wave];
@@ -170,20 +170,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
 #pragma unroll
       for (int j = 0; j < 4; ++j) du[k][c][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int tile = tile0; tile < tile1; ++tile) {
-    const int t0 = tile * 16;
-    // ---- tile inputs (buffer loads: out-of-range rows / channels read as 0)
-    const int toff = t0 * rowb;
+  // Tile inputs (buffer loads: out-of-range rows / channels read as 0).  Two
+  // buffers, A and B, alternate: while one tile is computed the next one's
+  // loads are in flight.  The loads are unconditional (a tile past the run
+  // reads the out-of-range offset kOobTile: 0, no memory traffic) and no
+  // register is copied, so the compiler's waits stay partial (vmcnt(N)).
+  struct TileIn {
     u32x2 xr[NR], dyr[NR];
+    ZR zr[NB];  // z_eff rows t0+4bb+n, ranks 16c+4q..+3: A operand of the tap-weight MFMA
+  };
+  auto load_tile = [&](int tile, TileIn& in) {
+    const bool live = tile < tile1;
+    const int toff = live ? tile * 16 * rowb : kOobTile;
 #pragma unroll
     for (int m = 0; m < NR; ++m) {
-      xr[m] = bload64(rx, lane_off + toff + (m - (W - 1)) * rowb);
-      dyr[m] = bload64(rdy, lane_off + toff + m * rowb);
+      in.xr[m] = bload64(rx, lane_off + toff + (m - (W - 1)) * rowb);
+      in.dyr[m] = bload64(rdy, lane_off + toff + m * rowb);
     }
-    // z_eff rows t0+4bb+n, ranks 16c+4q..+3: A operand of the tap-weight MFMA.
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) in.zr[bb].load(rz, live ? (tile * 16 + 4 * bb + n) * R * 2 : kOobTile, R, q);
+  };
+  auto compute_tile = [&](int tile, const TileIn& in) {
+    const int t0 = tile * 16;
+    const int toff = t0 * rowb;
+    const u32x2(&xr)[NR] = in.xr;
+    const u32x2(&dyr)[NR] = in.dyr;
     u32x2 zA[NB][RC];
 #pragma unroll
-    for (int bb = 0; bb < NB; ++bb) load_za<T, RC>(zA[bb], rz, t0 + 4 * bb + n, R, RK, Tn, q, zvec);
+    for (int bb = 0; bb < NB; ++bb) in.zr[bb].finish(zA[bb], t0 + 4 * bb + n, R, RK, Tn, q);
     // z_eff transposed (rank n, rows 4q..4q+3), the A operand of the dU MFMA,
     // from row block 0 through the exact identity transpose.
     u32x2 zT[RC];
@@ -291,6 +305,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
         if (r < R && t < Tn) part_dz[((int64_t)cg * a.BT + row0 + t) * R + r] = v;
       }
     }
+  };
+
+  TileIn ta, tb;
+  load_tile(tile0, ta);
+  for (int tile = tile0; tile < tile1; tile += 2) {
+    load_tile(tile + 1, tb);
+    __builtin_amdgcn_sched_barrier(0);  // issue the next tile's loads before this tile's waits
+    compute_tile(tile, ta);
+    load_tile(tile + 2, ta);
+    __builtin_amdgcn_sched_barrier(0);
+    if (tile + 1 < tile1) compute_tile(tile + 1, tb);
   }
 
   // ---- dU partial of this run: rows r < RK of U_eff, the wavefront's 64 columns per tap
@@ -353,8 +378,14 @@ hipError_t launch_bwd(const LrProblem& p) {
   const BwdWs w = bwd_ws(p, a);
   float* pdz = (float*)((char*)p.ws + w.dz_off);
   float* pdu = (float*)((char*)p.ws + w.du_off);
-  lr_bwd_mfma<T, W, RC><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.U,
-                                                       (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, pdz, pdu, a);
+  if (a.zvec)
+    lr_bwd_mfma<T, W, RC, true><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.U,
+                                                               (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, pdz,
+                                                               pdu, a);
+  else
+    lr_bwd_mfma<T, W, RC, false><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.U,
+                                                                (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, pdz,
+                                                                pdu, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t WD = p.W * p.D, RKWD = (int64_t)a.RK * WD;

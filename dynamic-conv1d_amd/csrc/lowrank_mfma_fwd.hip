@@ -28,7 +28,7 @@ struct LrArgs {
   int nspb;        // runs per sequence
   int nseg;        // B * nspb
   int nblk;        // grid size
-  int zvec;        // R % 4 == 0 and z 8-byte aligned: 8-byte z loads
+  int zvec;        // R % 4 == 0 and z 8-byte aligned: 8-byte z loads (host dispatch)
 };
 
 // Packed B operands of one 128-channel chunk, staged once per workgroup:
@@ -59,11 +59,12 @@ __device__ __forceinline__ void stage_u(u32x2* __restrict__ lds, const uint16_t*
   }
 }
 
-template <typename T, int W, int RC>
+template <typename T, int W, int RC, bool ZV>
 __global__ __launch_bounds__(256) void lr_fwd_mfma(const T* __restrict__ x_, const T* __restrict__ z_,
                                                    const T* __restrict__ U_, const T* __restrict__ sw_,
                                                    T* __restrict__ y_, LrArgs a) {
   constexpr int NR = W + 3;  // x rows 4q-W+1 .. 4q+3 of a lane
+  typedef ZRaw<T, RC, ZV> ZR;
   const uint16_t* __restrict__ x = reinterpret_cast<const uint16_t*>(x_);
   const uint16_t* __restrict__ z = reinterpret_cast<const uint16_t*>(z_);
   const uint16_t* __restrict__ U = reinterpret_cast<const uint16_t*>(U_);
@@ -93,21 +94,22 @@ __global__ __launch_bounds__(256) void lr_fwd_mfma(const T* __restrict__ x_, con
   const rsrc_t ry = make_rsrc(y + row0 * D, (int64_t)Tn * rowb);
   const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 2);
   const int lane_off = chv ? (4 * q * D + dl) * 2 : kOobLane;  // byte offset of the lane's row 4q octet
-  const bool zvec = a.zvec;
 
-  // Tile inputs (rows out of the sequence read as 0): the current tile's and,
-  // in flight while it is computed, the next one's.
-  u32x4 xc[NR], xn[NR];
-  u32x2 zc[RC], zn[RC];
-  auto load_tile = [&](int tile, u32x4(&xr)[NR], u32x2(&za)[RC]) {
-    const int toff = tile * 16 * rowb;
+  // Tile inputs (rows out of the sequence read as 0).  Two buffers, A and B,
+  // alternate: while one tile is computed the next one's loads are in flight.
+  // The loads are unconditional (a tile past the run reads the out-of-range
+  // offset kOobTile, which returns 0 and touches no memory) and no register
+  // is copied, so the compiler's waits stay partial (vmcnt(N), not vmcnt(0)).
+  auto load_tile = [&](int tile, u32x4(&xr)[NR], ZR& zr) {
+    const bool live = tile < tile1;
+    const int toff = live ? tile * 16 * rowb : kOobTile;
 #pragma unroll
     for (int m = 0; m < NR; ++m) xr[m] = bload128(rx, lane_off + toff + (m - (W - 1)) * rowb);
-    load_za<T, RC>(za, rz, tile * 16 + n, R, RK, Tn, q, zvec);
+    zr.load(rz, live ? (tile * 16 + n) * R * 2 : kOobTile, R, q);
   };
-  if (tile0 < tile1) load_tile(tile0, xc, zc);
-  for (int tile = tile0; tile < tile1; ++tile) {
-    if (tile + 1 < tile1) load_tile(tile + 1, xn, zn);
+  auto compute_tile = [&](int tile, const u32x4(&xc)[NR], const ZR& zr) {
+    u32x2 zc[RC];
+    zr.finish(zc, tile * 16 + n, R, RK, Tn, q);
     float acc[4][8];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -142,10 +144,18 @@ __global__ __launch_bounds__(256) void lr_fwd_mfma(const T* __restrict__ x_, con
       for (int h = 0; h < 4; ++h) o[h] = pack2<T>(acc[i][2 * h], acc[i][2 * h + 1]);
       bstore128<true>(o, ry, lane_off + toff + i * rowb);
     }
-#pragma unroll
-    for (int m = 0; m < NR; ++m) xc[m] = xn[m];
-#pragma unroll
-    for (int c = 0; c < RC; ++c) zc[c] = zn[c];
+  };
+
+  u32x4 xa[NR], xb[NR];
+  ZR za, zb;
+  load_tile(tile0, xa, za);
+  for (int tile = tile0; tile < tile1; tile += 2) {
+    load_tile(tile + 1, xb, zb);
+    __builtin_amdgcn_sched_barrier(0);  // issue the next tile's loads before this tile's waits
+    compute_tile(tile, xa, za);
+    load_tile(tile + 2, xa, za);
+    __builtin_amdgcn_sched_barrier(0);
+    if (tile + 1 < tile1) compute_tile(tile + 1, xb, zb);
   }
 }
 
@@ -177,8 +187,12 @@ LrArgs make_args(const LrProblem& p, int target_waves) {
 template <typename T, int W, int RC>
 hipError_t launch_fwd(const LrProblem& p) {
   const LrArgs a = make_args(p, 2048);
-  lr_fwd_mfma<T, W, RC><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.U,
-                                                       (const T*)p.static_w, (T*)p.y, a);
+  if (a.zvec)
+    lr_fwd_mfma<T, W, RC, true><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.U,
+                                                               (const T*)p.static_w, (T*)p.y, a);
+  else
+    lr_fwd_mfma<T, W, RC, false><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.U,
+                                                                (const T*)p.static_w, (T*)p.y, a);
   return hipGetLastError();
 }
 
