@@ -109,10 +109,25 @@ struct HwRun {
   __device__ __forceinline__ int wrow(int t, bool live = true) const { return live ? (t - base) * wrowb : kHwRowOob; }
 };
 
-// Sum over aligned groups of `n` lanes (n a power of two, 1..64), leaving the
-// group sum in every lane of the group: the DPP steps run always and are
-// selected by n (no branch); 32- and 64-lane groups add two ds_bpermute steps
-// under one wave-uniform branch.
+// Sum over aligned groups of N lanes (N a power of two, 1..64), leaving the
+// group sum in every lane of the group: DPP butterflies (quad_perm xor 1,
+// xor 2, row_half_mirror, row_mirror: each pairs a lane with one of the other
+// half of its group, and fuses into the add) up to 16 lanes, ds_bpermute
+// beyond.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (N >= 2) v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (N >= 4) v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  if constexpr (N >= 8) v += dpp_f<0x141>(v);  // row_half_mirror
+  if constexpr (N >= 16) v += dpp_f<0x140>(v); // row_mirror
+  if constexpr (N >= 32) v += __shfl_xor(v, 16);
+  if constexpr (N >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
+// The same for a group size n known only at run time (wave-uniform): the DPP
+// steps run always and are selected by n (no branch); 32- and 64-lane groups
+// add two ds_bpermute steps under one wave-uniform branch.
 __device__ __forceinline__ float group_sum_sel(float v, int n) {
   float d = dpp_f<0xB1>(v);  // quad_perm [1,0,3,2]
   v = n >= 2 ? v + d : v;
@@ -164,11 +179,16 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
     else
       swr[k].zero();
   }
-  // x ring: row t lives in slot (t - t0) mod W; rows before 0 read 0.
-  XR xr[W];
-  xr[0].zero();
+  // x ring (fp32, each row converted once): row t lives in slot (t - t0) mod W;
+  // rows before 0 read 0.
+  float xf[W][VEC];
+  zero_vals<VEC>(xf[0]);
 #pragma unroll
-  for (int i = 1; i < W; ++i) bload_raw(xr[W - i], rx, xlo + run.xrow(t0 - i));
+  for (int i = 1; i < W; ++i) {
+    XR h;
+    bload_raw(h, rx, xlo + run.xrow(t0 - i));
+    h.to_float(xf[W - i]);
+  }
 
   auto load_chunk = [&](int tc, XR(&xc)[U], WR(&wc)[U]) {
 #pragma unroll
@@ -183,19 +203,18 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
     for (int u = 0; u < U; ++u) {
       const int t = tc + u;
       const int p = u % W;
-      xr[p] = xc[u];
+      xc[u].to_float(xf[p]);
       float acc[VEC];
       zero_vals<VEC>(acc);
 #pragma unroll
       for (int k = 0; k < W; ++k) {
         const int q = ring<W>(u, k);
 #pragma unroll
-        for (int j = 0; j < VEC; ++j)
-          acc[j] = fmaf(wc[u].get((j / HSV) * W + k) + swr[k].get(j), xr[q].get(j), acc[j]);
+        for (int j = 0; j < VEC; ++j) acc[j] = fmaf(wc[u].get((j / HSV) * W + k) + swr[k].get(j), xf[q][j], acc[j]);
       }
       if (a.residual) {
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) acc[j] += xr[p].get(j);
+        for (int j = 0; j < VEC; ++j) acc[j] += xf[p][j];
       }
       bstore_vals<T, VEC, true>(ry, xlo + run.xrow(t, t < t1), acc);  // rows past the run: dropped
     }
@@ -222,7 +241,9 @@ template <typename T, int W, int HSV> struct TdwOf {
   static constexpr int NP = BYTES / 16;  // pieces per lane
 };
 
-template <typename T, int W, int HSV, bool HAS_STATIC, bool TDW>
+// LPH: lanes per head when known at compile time (1, 2, 4, 8), or 0 for the
+// run-time group size a.lph (head sizes of 16 lanes and more).
+template <typename T, int W, int HSV, bool HAS_STATIC, bool TDW, int LPH>
 __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, const T* __restrict__ wt,
                                                    const T* __restrict__ sw, const T* __restrict__ dy,
                                                    T* __restrict__ dx, T* __restrict__ dwt_,
@@ -257,7 +278,7 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
     const int d0 = vc * VEC;
     const int xlo = lv ? d0 * ES : kHwLaneOob;
     const int wlo = lv ? (d0 >> a.hs_shift) * W * ES : kHwLaneOob;
-    const int lph = a.lph;
+    const int lph = LPH > 0 ? LPH : a.lph;
     const bool leader = (vc & (lph - 1)) == 0;
     const int dwlo = leader ? wlo : kHwLaneOob;  // one lane of a head stores its dweight
     // dweight byte offset of the wavefront's lane 0 (TDW: lanes own consecutive heads)
@@ -278,13 +299,18 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
       else
         swr[k].zero();
     }
-    XR xr[W];
+    // x ring (fp32, each row converted once): row t in slot (t - t0) mod W.
+    float xf[W][VEC];
     float dxa[W][VEC];
 #pragma unroll
     for (int k = 0; k < W; ++k) zero_vals<VEC>(dxa[k]);
-    xr[0].zero();
+    zero_vals<VEC>(xf[0]);
 #pragma unroll
-    for (int i = 1; i < W; ++i) bload_raw(xr[W - i], rx, xlo + run.xrow(t0 - i));
+    for (int i = 1; i < W; ++i) {
+      XR h;
+      bload_raw(h, rx, xlo + run.xrow(t0 - i));
+      h.to_float(xf[W - i]);
+    }
 
     struct Chunk {
       XR dy[U], x[U];
@@ -321,14 +347,14 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
             dxa[q][j] = fmaf(dyv[j], c.w[u].get((j / HSV) * W + k) + swr[k].get(j), dxa[q][j]);
         }
         if (t < t1) {  // wave-uniform; no loads below
-          xr[p] = c.x[u];
+          c.x[u].to_float(xf[p]);
           float dwv[NWE];
 #pragma unroll
           for (int k = 0; k < W; ++k) {
             const int q = ring<W>(u, k);
             float pr[VEC];
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) pr[j] = dyv[j] * xr[q].get(j);
+            for (int j = 0; j < VEC; ++j) pr[j] = dyv[j] * xf[q][j];
             if (HAS_STATIC) {
 #pragma unroll
               for (int j = 0; j < VEC; ++j) dsw[k][j] += pr[j];
@@ -341,9 +367,12 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
               dwv[hh * W + k] = sacc;
             }
           }
-          if constexpr (HSV == VEC) {
+          if constexpr (LPH == 0) {
 #pragma unroll
             for (int k = 0; k < NWE; ++k) dwv[k] = group_sum_sel(dwv[k], lph);
+          } else if constexpr (LPH > 1) {
+#pragma unroll
+            for (int k = 0; k < NWE; ++k) dwv[k] = group_sum<LPH>(dwv[k]);
           }
           if constexpr (TDW) {
             // Lane l's piece j goes to slot l*NP + j; slot i*64 + l is then
@@ -417,14 +446,14 @@ hipError_t launch_fwd_fast(const HwProblem& p, const HwPlan& pl) {
   return hipGetLastError();
 }
 
-template <typename T, int W, int HSV, bool TDW>
+template <typename T, int W, int HSV, bool TDW, int LPH>
 void launch_bwd_kernel(const HwProblem& p, const HwPlan& pl) {
   if (p.static_w) {
-    hw_bwd_fast<T, W, HSV, true, TDW><<<pl.nblk, 256, 0, p.stream>>>(
+    hw_bwd_fast<T, W, HSV, true, TDW, LPH><<<pl.nblk, 256, 0, p.stream>>>(
         (const T*)p.x, (const T*)p.weight, (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, (T*)p.dweight, p.ws,
         pl.a);
   } else {
-    hw_bwd_fast<T, W, HSV, false, TDW><<<pl.nblk, 256, 0, p.stream>>>(
+    hw_bwd_fast<T, W, HSV, false, TDW, LPH><<<pl.nblk, 256, 0, p.stream>>>(
         (const T*)p.x, (const T*)p.weight, nullptr, (const T*)p.dy, (T*)p.dx, (T*)p.dweight, nullptr, pl.a);
   }
 }
@@ -433,11 +462,20 @@ template <typename T, int W, int HSV>
 hipError_t launch_bwd_fast(const HwProblem& p, const HwPlan& pl) {
   if constexpr (TdwOf<T, W, HSV>::value) {
     if (pl.tdw)
-      launch_bwd_kernel<T, W, HSV, true>(p, pl);
+      launch_bwd_kernel<T, W, HSV, true, 1>(p, pl);
     else
-      launch_bwd_kernel<T, W, HSV, false>(p, pl);
+      launch_bwd_kernel<T, W, HSV, false, 1>(p, pl);
+  } else if constexpr (HSV == VecOf<T>::value) {
+    // head_size >= VEC: lanes per head from the plan
+    switch (pl.a.lph) {
+      case 1: launch_bwd_kernel<T, W, HSV, false, 1>(p, pl); break;
+      case 2: launch_bwd_kernel<T, W, HSV, false, 2>(p, pl); break;
+      case 4: launch_bwd_kernel<T, W, HSV, false, 4>(p, pl); break;
+      case 8: launch_bwd_kernel<T, W, HSV, false, 8>(p, pl); break;
+      default: launch_bwd_kernel<T, W, HSV, false, 0>(p, pl); break;
+    }
   } else {
-    launch_bwd_kernel<T, W, HSV, false>(p, pl);
+    launch_bwd_kernel<T, W, HSV, false, 1>(p, pl);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !p.static_w) return e;
