@@ -46,7 +46,7 @@ struct LrBwdArgs {
 
 // U_eff operands of one wavefront's 64-channel chunk, staged once per run (the
 // chunk never changes across it): the dz operands always in LDS, the tap-weight
-// operands in registers when W*RC <= 4 (UWREG) and in LDS otherwise.  For tap k
+// operands in registers when W*RC <= 8 (UWREG) and in LDS otherwise.  For tap k
 // and rank chunk c, lane (q, n) reads
 //   uw[j] (j = 0..3): ranks 16c+4q..16c+4q+3 of channel 4n+j, packed (B operand
 //                     of the 16x16x16 tap-weight MFMA);
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
     LrBwdArgs a) {
   constexpr int NB = (W + 6) / 4;  // MFMA row blocks for the dx look-ahead
   constexpr int NR = W + 3;        // x rows 4q-W+1 .. 4q+3 and dy rows 4q .. 4q+W+2 per lane
-  constexpr bool UWREG = W * RC <= 4;   // tap-weight operands in registers
+  constexpr bool UWREG = W * RC <= 8;   // tap-weight operands in registers
   constexpr int NUW = W * RC * 4;  // packed tap-weight operands per lane
   constexpr int NUZ = W * RC * 2;  // dz operands per lane
   constexpr int GROW = 72;         // G tile row pitch (64 channels + 8 pad: conflict-free reads)
@@ -116,8 +116,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
   __shared__ u32x4 uz_lds[4][NUZ * 64];
   __shared__ __attribute__((aligned(16))) uint16_t gtile[4][16 * GROW];
   // dz partial sums of the workgroup's 4 chunks, gathered for DZB tiles and
-  // reduced once per batch (double-buffered: one barrier per batch).
-  constexpr int DZB = (UWREG && RC == 1) ? 4 : 1;
+  // reduced once per batch (double-buffered: one barrier per batch).  Two
+  // rank chunks batch too once registers already hold occupancy at one
+  // wavefront per SIMD (W >= 2); at W = 1 the smaller LDS keeps two.
+  constexpr int DZB = (UWREG && (RC == 1 || (RC == 2 && W >= 2))) ? 4 : 1;
   __shared__ float dzred[2][4][DZB][RC * 256];
 
   const int lane = threadIdx.x & 63, wave = wave_id();
