@@ -20,11 +20,15 @@ Also reported:
                independent input sets that each launch's data is out of the
                256 MB MALL, between one pair of HIP events; plus configs[4]
                (lowrank QKV, 3 calls) at its own shape;
-  roofline     the dominant launch (headwise hs1 backward) against 8 TB/s;
+  roofline     the dominant launch (headwise hs1 backward: hw_bwd_fast +
+               reduce_partials) against 8 TB/s, its duration taken with HIP
+               events around that backward call inside the timed step loop, on
+               the stream it runs on;
   cpu_baseline the CPU oracle (fp32 restatement of reference.py) on configs[0]
                on this host's cores.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+    python bench.py --calibrate-copy   # a plain 256 MiB device copy, for scaling HBM counters
 """
 
 import argparse
@@ -222,6 +226,18 @@ def time_launches(torch, launch, nsets, reps):
     return s.elapsed_time(e) * 1e3 / reps  # us
 
 
+def calibrate_copy(torch, dev, mib=256, reps=3):
+    """Plain device copies of exactly `mib` MiB: what FETCH_SIZE / WRITE_SIZE read for known traffic."""
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": n, "copies": reps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -230,6 +246,7 @@ def main():
     ap.add_argument("--reps", type=int, default=40, help="launches per breakdown measurement")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip configs[4] (lowrank QKV) in the breakdown")
+    ap.add_argument("--calibrate-copy", action="store_true", help="only run a plain 256 MiB device copy and exit")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -247,6 +264,9 @@ def main():
     dynconv.load_library()
     dev = torch.device("cuda", 0)
     print(f"[bench] device {torch.cuda.get_device_name(0)}", file=sys.stderr, flush=True)
+    if args.calibrate_copy:
+        calibrate_copy(torch, dev)
+        return
 
     data = {}
     for name in STEP + ([] if args.no_extra else list(EXTRA)):
@@ -255,7 +275,10 @@ def main():
     torch.cuda.synchronize()
     print("[bench] inputs resident", file=sys.stderr, flush=True)
 
-    def fwdbwd(name):
+    ROOF = "hw_hs1"  # the dominant launch: its backward is bracketed by events in the timed loop
+    roof_ev = []
+
+    def fwdbwd(name, timed=False):
         c = CONFIGS[name]
         a, dy = data[name]
         for t in a:
@@ -263,7 +286,15 @@ def main():
                 t.grad = None
         fn = hw if c["kind"] == "hw" else lr
         y = fn(*a, residual=c["residual"])
-        y.backward(dy)
+        if timed and name == ROOF:
+            # events on the stream the backward kernels are launched on (torch's current stream)
+            b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            b0.record()
+            y.backward(dy)
+            b1.record()
+            roof_ev.append((b0, b1))
+        else:
+            y.backward(dy)
 
     step_bytes = sum(sum(alg_bytes(CONFIGS[n])) for n in STEP)
     for _ in range(args.warmup):
@@ -275,13 +306,14 @@ def main():
     s_ev.record()
     for _ in range(args.steps):
         for n in STEP:
-            fwdbwd(n)
+            fwdbwd(n, timed=True)
     e_ev.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_total = s_ev.elapsed_time(e_ev)
     ms_per_step = ms_total / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    roof_us = statistics.mean(b0.elapsed_time(b1) for b0, b1 in roof_ev) * 1e3
     print(f"[bench] {args.steps} steps: {ms_per_step:.4f} ms/step (events), wall {wall * 1e3 / args.steps:.4f} ms/step",
           file=sys.stderr, flush=True)
 
@@ -311,14 +343,16 @@ def main():
         print(f"[bench] {name}: fwd {f_us:.1f} us ({breakdown[name]['fwd_GBs']} GB/s)  bwd {b_us:.1f} us "
               f"({breakdown[name]['bwd_GBs']} GB/s)  fwd+bwd {fb_us:.1f} us = {gbs:.0f} GB/s ({gbs / PEAK_GBS:.1%})",
               file=sys.stderr, flush=True)
-        if name == "hw_hs1":
-            ach = bb / (b_us * 1e-6) / 1e9
+        if name == ROOF:
+            ach = bb / (roof_us * 1e-6) / 1e9
             roofline = {
                 "kernel": "headwise backward, head_size 1: hw_bwd_fast<bf16,W4,HSV1,static> + reduce_partials",
                 "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / PEAK_GBS, 4), "traffic": measured_traffic("hw_bwd_fastIDF16bLi4ELi1ELb1"),
                 "traffic_source": "profiles/bench_hbm_traffic.md (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
-                "alg_bytes_per_launch": bb, "avg_launch_us": round(b_us, 2),
+                "alg_bytes_per_launch": bb, "avg_launch_us": round(roof_us, 2),
+                "timing": f"HIP events around the {ROOF} backward call in each of the {args.steps} timed steps",
+                "breakdown_launch_us": round(b_us, 2),
             }
         del sets, fwd, bwd
         torch.cuda.empty_cache()
