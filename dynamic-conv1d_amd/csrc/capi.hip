@@ -12,6 +12,7 @@
 namespace {
 
 constexpr int64_t kI32Max = 2147483647;
+static_assert(DC_MAX_GROUPS == dc::kMaxGroups, "group table size");
 
 int device_status() {
   static std::once_flag once;
@@ -149,7 +150,7 @@ int dc_lowrank_fwd(const void* x, const void* z, const void* U, const void* stat
   p.x = x; p.z = z; p.U = U; p.static_w = static_w; p.y = y;
   p.B = B; p.T = T; p.D = D; p.R = R; p.W = W;
   p.dtype = dtype; p.residual = residual ? 1 : 0; p.stream = (hipStream_t)stream;
-  return launch_status(dc::lr_fwd(p));
+  return launch_status(dc::lr_fwd(&p, 1));
 }
 
 int64_t dc_lowrank_bwd_ws_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype,
@@ -190,7 +191,86 @@ int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* stat
   p.dx = dx; p.dz = dz; p.dU = dU; p.dstatic_w = dstatic_w; p.ws = (float*)workspace;
   p.B = B; p.T = T; p.D = D; p.R = R; p.W = W;
   p.dtype = dtype; p.residual = residual ? 1 : 0; p.stream = (hipStream_t)stream;
-  return launch_status(dc::lr_bwd(p));
+  return launch_status(dc::lr_bwd(&p, 1));
+}
+
+// ------------------------------------------------------------------ grouped
+// G problems of one shape in one launch; group g reads x + g*D with rows
+// x_ld elements apart (the q / k / v slices of a fused projection) and, in the
+// backward, writes dx + g*D with rows dx_ld elements apart.
+
+int dc_lowrank_fwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z, const void* const* U,
+                           const void* const* static_w, void* const* y, int64_t B, int64_t T, int64_t D,
+                           int64_t R, int64_t W, int dtype, int residual, void* stream) {
+  if (G < 1 || G > DC_MAX_GROUPS) return DC_ERR_UNSUPPORTED;
+  int s = check_lowrank(B, T, D, R, W, dtype, static_w != nullptr);
+  if (s != DC_OK) return s;
+  if (x_ld < G * D || x_ld > kI32Max) return DC_ERR_SHAPE;
+  if (!x || !z || !U || !y) return DC_ERR_NULL;
+  const int es = dc::dtype_size(dtype);
+  if (!aligned_to(x, es)) return DC_ERR_ALIGN;
+  dc::LrProblem p[DC_MAX_GROUPS] = {};
+  for (int64_t g = 0; g < G; ++g) {
+    const void* sw = static_w ? static_w[g] : nullptr;
+    if (!z[g] || !U[g] || !y[g] || (static_w && !sw)) return DC_ERR_NULL;
+    if (!aligned_to(z[g], es) || !aligned_to(U[g], es) || !aligned_to(sw, es) || !aligned_to(y[g], es))
+      return DC_ERR_ALIGN;
+    dc::LrProblem& q = p[g];
+    q.x = (const char*)x + g * D * es; q.z = z[g]; q.U = U[g]; q.static_w = sw; q.y = y[g];
+    q.B = B; q.T = T; q.D = D; q.R = R; q.W = W; q.x_ld = x_ld;
+    q.dtype = dtype; q.residual = residual ? 1 : 0; q.stream = (hipStream_t)stream;
+  }
+  if ((s = device_status()) != DC_OK) return s;
+  return launch_status(dc::lr_fwd(p, (int)G));
+}
+
+// One group's share, rounded up to 256 bytes (each group's partials start aligned).
+static int64_t grouped_ws_share(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int has_static) {
+  const int64_t one = dc_lowrank_bwd_ws_bytes(B, T, D, R, W, dtype, has_static);
+  return one < 0 ? one : (one + 255) / 256 * 256;
+}
+
+int64_t dc_lowrank_bwd_grouped_ws_bytes(int64_t G, int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
+                                        int dtype, int has_static) {
+  if (G < 1 || G > DC_MAX_GROUPS) return DC_ERR_UNSUPPORTED;
+  const int64_t share = grouped_ws_share(B, T, D, R, W, dtype, has_static);
+  return share < 0 ? share : G * share;
+}
+
+int dc_lowrank_bwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z, const void* const* U,
+                           const void* const* static_w, const void* const* dy, void* dx, int64_t dx_ld,
+                           void* const* dz, void* const* dU, void* const* dstatic_w, void* workspace,
+                           int64_t ws_bytes, int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype,
+                           int residual, void* stream) {
+  if (G < 1 || G > DC_MAX_GROUPS) return DC_ERR_UNSUPPORTED;
+  int s = check_lowrank(B, T, D, R, W, dtype, static_w != nullptr);
+  if (s != DC_OK) return s;
+  if (x_ld < G * D || x_ld > kI32Max || dx_ld < G * D || dx_ld > kI32Max) return DC_ERR_SHAPE;
+  if (!x || !z || !U || !dy || !dx || !dz || !dU) return DC_ERR_NULL;
+  if ((static_w == nullptr) != (dstatic_w == nullptr)) return DC_ERR_NULL;
+  const int es = dc::dtype_size(dtype);
+  if (!aligned_to(x, es) || !aligned_to(dx, es)) return DC_ERR_ALIGN;
+  const int64_t share = grouped_ws_share(B, T, D, R, W, dtype, static_w != nullptr);
+  if (share < 0) return (int)share;
+  if (share > 0 && (workspace == nullptr || ws_bytes < G * share || !aligned_to(workspace, 256)))
+    return DC_ERR_WORKSPACE;
+  dc::LrProblem p[DC_MAX_GROUPS] = {};
+  for (int64_t g = 0; g < G; ++g) {
+    const void* sw = static_w ? static_w[g] : nullptr;
+    void* dsw = dstatic_w ? dstatic_w[g] : nullptr;
+    if (!z[g] || !U[g] || !dy[g] || !dz[g] || !dU[g] || (static_w && (!sw || !dsw))) return DC_ERR_NULL;
+    if (!aligned_to(z[g], es) || !aligned_to(U[g], es) || !aligned_to(sw, es) || !aligned_to(dy[g], es) ||
+        !aligned_to(dz[g], es) || !aligned_to(dU[g], es) || !aligned_to(dsw, es))
+      return DC_ERR_ALIGN;
+    dc::LrProblem& q = p[g];
+    q.x = (const char*)x + g * D * es; q.z = z[g]; q.U = U[g]; q.static_w = sw; q.dy = dy[g];
+    q.dx = (char*)dx + g * D * es; q.dz = dz[g]; q.dU = dU[g]; q.dstatic_w = dsw;
+    q.ws = share > 0 ? (float*)((char*)workspace + g * share) : nullptr;
+    q.B = B; q.T = T; q.D = D; q.R = R; q.W = W; q.x_ld = x_ld; q.dx_ld = dx_ld;
+    q.dtype = dtype; q.residual = residual ? 1 : 0; q.stream = (hipStream_t)stream;
+  }
+  if ((s = device_status()) != DC_OK) return s;
+  return launch_status(dc::lr_bwd(p, (int)G));
 }
 
 }  // extern "C"

@@ -49,15 +49,25 @@ struct LrProblem {
   void* dstatic_w;
   float* ws;
   int64_t B, T, D, R, W;  // R = dynamic rank (z.shape[-1])
+  int64_t x_ld;           // row stride of x in elements (0: D, contiguous)
+  int64_t dx_ld;          // row stride of dx in elements (0: D, contiguous)
   int dtype;
   int residual;
   hipStream_t stream;
+  int64_t xld() const { return x_ld > 0 ? x_ld : D; }
+  int64_t dxld() const { return dx_ld > 0 ? dx_ld : D; }
 };
+
+// Independent problems launched together (the q / k / v convolutions of one
+// layer): every group shares B, T, D, R, W, dtype, residual, the presence of
+// static_w and the x / dx row strides; pointers differ.  The backward's
+// workspace is G consecutive per-group workspaces.
+constexpr int kMaxGroups = 4;
 
 bool lr_mfma_ok(const LrProblem& p, bool bwd);
 int64_t lr_bwd_ws_bytes(const LrProblem& p);
-hipError_t lr_fwd(const LrProblem& p);
-hipError_t lr_bwd(const LrProblem& p);
+hipError_t lr_fwd(const LrProblem* p, int G);
+hipError_t lr_bwd(const LrProblem* p, int G);
 
 // ------------------------------------------------------------------ shared
 // out[c] = (T) sum_{p < P} part[p * pstride + c] for c < C, summed in a fixed
@@ -65,7 +75,8 @@ hipError_t lr_bwd(const LrProblem& p);
 hipError_t reduce_partials(const float* part, int64_t pstride, int P, int64_t C, void* out, int dtype,
                            hipStream_t stream);
 
-// Up to three such reductions in one launch (jobs with C <= 0 are skipped).
+// Up to kMaxReduceJobs such reductions in one launch (jobs with C <= 0 are skipped).
+constexpr int kMaxReduceJobs = 3 * kMaxGroups;
 struct PartialReduce {
   const float* part;
   int64_t pstride;

@@ -10,7 +10,8 @@
 //
 // This file holds the one-thread-per-output kernels used for fp32 and for
 // shapes the MFMA path (lowrank_mfma_fwd.hip, lowrank_mfma_bwd.hip) does not
-// take, plus the dispatch.
+// take, plus the dispatch.  x (and dx) rows may be xld (dxld) elements apart,
+// for inputs read out of a fused projection.
 #include "lowrank_mfma.h"
 
 namespace dc {
@@ -40,8 +41,8 @@ __device__ __forceinline__ float lr_tap(const T* __restrict__ z, const T* __rest
 template <typename T>
 __global__ __launch_bounds__(256) void lr_fwd_generic(const T* __restrict__ x, const T* __restrict__ z,
                                                       const T* __restrict__ U, const T* __restrict__ sw,
-                                                      T* __restrict__ y, int64_t BT, int Tn, int D, int R, int W,
-                                                      int residual) {
+                                                      T* __restrict__ y, int64_t BT, int Tn, int D, int64_t xld,
+                                                      int R, int W, int residual) {
   const int64_t n = BT * D;
   const int64_t WD = (int64_t)W * D;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
@@ -50,8 +51,8 @@ __global__ __launch_bounds__(256) void lr_fwd_generic(const T* __restrict__ x, c
     const int t = (int)(row % Tn);
     float acc = 0.f;
     for (int k = 0; k < W && k <= t; ++k)
-      acc = fmaf(lr_tap(z, U, sw, row, R, WD, (int64_t)k * D + d), (float)x[(row - k) * D + d], acc);
-    if (residual) acc += (float)x[i];
+      acc = fmaf(lr_tap(z, U, sw, row, R, WD, (int64_t)k * D + d), (float)x[(row - k) * xld + d], acc);
+    if (residual) acc += (float)x[row * xld + d];
     y[i] = (T)acc;
   }
 }
@@ -59,8 +60,8 @@ __global__ __launch_bounds__(256) void lr_fwd_generic(const T* __restrict__ x, c
 template <typename T>
 __global__ __launch_bounds__(256) void lr_bwd_dx_generic(const T* __restrict__ z, const T* __restrict__ U,
                                                          const T* __restrict__ sw, const T* __restrict__ dy,
-                                                         T* __restrict__ dx, int64_t BT, int Tn, int D, int R,
-                                                         int W, int residual) {
+                                                         T* __restrict__ dx, int64_t BT, int Tn, int D,
+                                                         int64_t dxld, int R, int W, int residual) {
   const int64_t n = BT * D;
   const int64_t WD = (int64_t)W * D;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(256) void lr_bwd_dx_generic(const T* __restrict__ z
     for (int k = 0; k < W && t + k < Tn; ++k)
       acc = fmaf((float)dy[(row + k) * D + d], lr_tap(z, U, sw, row + k, R, WD, (int64_t)k * D + d), acc);
     if (residual) acc += (float)dy[i];
-    dx[i] = (T)acc;
+    dx[row * dxld + d] = (T)acc;
   }
 }
 
@@ -80,7 +81,7 @@ __global__ __launch_bounds__(256) void lr_bwd_dx_generic(const T* __restrict__ z
 template <typename T>
 __global__ __launch_bounds__(256) void lr_bwd_dz_generic(const T* __restrict__ x, const T* __restrict__ U,
                                                          const T* __restrict__ dy, T* __restrict__ dz, int Tn,
-                                                         int D, int R, int W) {
+                                                         int D, int64_t xld, int R, int W) {
   __shared__ float red[256];
   const int64_t row = blockIdx.x;
   const int t = (int)(row % Tn);
@@ -88,7 +89,7 @@ __global__ __launch_bounds__(256) void lr_bwd_dz_generic(const T* __restrict__ x
   for (int r = 0; r < R; ++r) {
     float acc = 0.f;
     for (int k = 0; k < W && k <= t; ++k) {
-      const T* xr = x + (row - k) * D;
+      const T* xr = x + (row - k) * xld;
       const T* ur = U + (int64_t)r * WD + (int64_t)k * D;
       for (int d = threadIdx.x; d < D; d += 256)
         acc = fmaf((float)dy[row * D + d] * (float)xr[d], (float)ur[d], acc);
@@ -108,8 +109,8 @@ __global__ __launch_bounds__(256) void lr_bwd_dz_generic(const T* __restrict__ x
 template <typename T>
 __global__ __launch_bounds__(256) void lr_bwd_du_generic(const T* __restrict__ x, const T* __restrict__ z,
                                                          const T* __restrict__ dy, float* __restrict__ part,
-                                                         int64_t BT, int Tn, int D, int R, int RK, int W,
-                                                         int64_t rows_per) {
+                                                         int64_t BT, int Tn, int D, int64_t xld, int R, int RK,
+                                                         int W, int64_t rows_per) {
   const int64_t WD = (int64_t)W * D;
   const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (c >= (int64_t)RK * WD) return;
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(256) void lr_bwd_du_generic(const T* __restrict__ x
   float acc = 0.f;
   for (int64_t row = r0; row < r1; ++row) {
     const int t = (int)(row % Tn);
-    if (t >= k) acc = fmaf(zrank(z, row, R, r), (float)dy[row * D + d] * (float)x[(row - k) * D + d], acc);
+    if (t >= k) acc = fmaf(zrank(z, row, R, r), (float)dy[row * D + d] * (float)x[(row - k) * xld + d], acc);
   }
   part[(int64_t)blockIdx.y * RK * WD + c] = acc;
 }
@@ -148,7 +149,7 @@ template <typename T>
 hipError_t fwd_generic(const LrProblem& p) {
   const int64_t BT = p.B * p.T;
   lr_fwd_generic<T><<<generic_grid(BT * p.D), 256, 0, p.stream>>>(
-      (const T*)p.x, (const T*)p.z, (const T*)p.U, (const T*)p.static_w, (T*)p.y, BT, (int)p.T, (int)p.D,
+      (const T*)p.x, (const T*)p.z, (const T*)p.U, (const T*)p.static_w, (T*)p.y, BT, (int)p.T, (int)p.D, p.xld(),
       (int)p.R, (int)p.W, p.residual);
   return hipGetLastError();
 }
@@ -160,14 +161,15 @@ hipError_t bwd_generic(const LrProblem& p) {
   const int64_t WD = p.W * p.D;
   lr_bwd_dx_generic<T><<<generic_grid(BT * p.D), 256, 0, p.stream>>>(
       (const T*)p.z, (const T*)p.U, (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, BT, (int)p.T, (int)p.D,
-      (int)p.R, (int)p.W, p.residual);
+      p.dxld(), (int)p.R, (int)p.W, p.residual);
   lr_bwd_dz_generic<T><<<(unsigned)BT, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.U, (const T*)p.dy,
-                                                           (T*)p.dz, (int)p.T, (int)p.D, (int)p.R, (int)p.W);
+                                                           (T*)p.dz, (int)p.T, (int)p.D, p.xld(), (int)p.R,
+                                                           (int)p.W);
   const int P = generic_partials(BT);
   const int64_t rows_per = (BT + P - 1) / P;
   dim3 grid((unsigned)((RK * WD + 255) / 256), (unsigned)P);
   lr_bwd_du_generic<T><<<grid, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.dy, p.ws, BT,
-                                                   (int)p.T, (int)p.D, (int)p.R, RK, (int)p.W, rows_per);
+                                                   (int)p.T, (int)p.D, p.xld(), (int)p.R, RK, (int)p.W, rows_per);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const PartialReduce jobs[2] = {
@@ -187,13 +189,15 @@ bool lr_mfma_ok(const LrProblem& p, bool bwd) {
   if (rc > 4 || p.W * rc > 8) return false;  // staged operands / accumulators bound W*RC
   if (bwd && rc == 4 && p.W > 1) return false;  // backward LDS (operands + dz sums) above 160 KiB
   // buffer-offset range of one sequence (x, y, dy, dx rows and z rows)
-  if ((p.T + kSeqSlackRows) * p.D * 2 > kMaxSeqBytes) return false;
+  const int64_t ld = p.xld() > p.dxld() ? p.xld() : p.dxld();
+  if ((p.T + kSeqSlackRows) * ld * 2 > kMaxSeqBytes) return false;
   if ((p.T + kSeqSlackRows) * p.R * 2 > kMaxSeqBytes) return false;
   if (!bwd) {
-    if (p.D % 8 != 0) return false;
+    // 16-byte row pieces of x at every row: xld a multiple of 8 elements
+    if (p.D % 8 != 0 || p.xld() % 8 != 0) return false;
     return aligned_to16(p.x) && aligned_to16(p.U) && aligned_to16(p.static_w) && aligned_to16(p.y);
   }
-  if (p.D % 16 != 0) return false;
+  if (p.D % 16 != 0 || p.xld() % 4 != 0 || p.dxld() % 4 != 0) return false;
   return aligned_to8(p.x) && aligned_to8(p.dy) && aligned_to8(p.dx) && aligned_to16(p.U) && aligned_to16(p.static_w);
 }
 
@@ -203,22 +207,44 @@ int64_t lr_bwd_ws_bytes(const LrProblem& p) {
   return (int64_t)generic_partials(p.B * p.T) * RK * p.W * p.D * (int64_t)sizeof(float);
 }
 
-hipError_t lr_fwd(const LrProblem& p) {
-  if (lr_mfma_ok(p, false)) return lr_mfma_fwd(p);
-  switch (p.dtype) {
-    case kBF16: return fwd_generic<bf16>(p);
-    case kFP16: return fwd_generic<fp16>(p);
-    default: return fwd_generic<float>(p);
+namespace {
+bool all_mfma_ok(const LrProblem* p, int G, bool bwd) {
+  for (int g = 0; g < G; ++g)
+    if (!lr_mfma_ok(p[g], bwd)) return false;
+  return true;
+}
+}  // namespace
+
+// G problems of one shape (see dc_launch.h): one MFMA launch for all of them,
+// or one generic launch sequence per group.
+hipError_t lr_fwd(const LrProblem* p, int G) {
+  if (G < 1 || G > kMaxGroups) return hipErrorInvalidValue;
+  if (all_mfma_ok(p, G, false)) return lr_mfma_fwd(p, G);
+  for (int g = 0; g < G; ++g) {
+    hipError_t e;
+    switch (p[g].dtype) {
+      case kBF16: e = fwd_generic<bf16>(p[g]); break;
+      case kFP16: e = fwd_generic<fp16>(p[g]); break;
+      default: e = fwd_generic<float>(p[g]); break;
+    }
+    if (e != hipSuccess) return e;
   }
+  return hipSuccess;
 }
 
-hipError_t lr_bwd(const LrProblem& p) {
-  if (lr_mfma_ok(p, true)) return lr_mfma_bwd(p);
-  switch (p.dtype) {
-    case kBF16: return bwd_generic<bf16>(p);
-    case kFP16: return bwd_generic<fp16>(p);
-    default: return bwd_generic<float>(p);
+hipError_t lr_bwd(const LrProblem* p, int G) {
+  if (G < 1 || G > kMaxGroups) return hipErrorInvalidValue;
+  if (all_mfma_ok(p, G, true)) return lr_mfma_bwd(p, G);
+  for (int g = 0; g < G; ++g) {
+    hipError_t e;
+    switch (p[g].dtype) {
+      case kBF16: e = bwd_generic<bf16>(p[g]); break;
+      case kFP16: e = bwd_generic<fp16>(p[g]); break;
+      default: e = bwd_generic<float>(p[g]); break;
+    }
+    if (e != hipSuccess) return e;
   }
+  return hipSuccess;
 }
 
 }  // namespace dc

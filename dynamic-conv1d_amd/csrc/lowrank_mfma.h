@@ -161,9 +161,17 @@ struct ZRaw {
 
 inline bool aligned_to(const void* p, int a) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// Field f of group g's entry in a kernel-argument table, by selects on the
+// wave-uniform g (no dynamic indexing of the argument block).
+template <class S, class F>
+__device__ __forceinline__ F pick(const S (&a)[kMaxGroups], int g, F S::*f) {
+  static_assert(kMaxGroups == 4, "pick() selects among four groups");
+  return g == 0 ? a[0].*f : g == 1 ? a[1].*f : g == 2 ? a[2].*f : a[3].*f;
+}
+
 // Host entry points of the two MFMA translation units.
-hipError_t lr_mfma_fwd(const LrProblem& p);
+hipError_t lr_mfma_fwd(const LrProblem* p, int G);
 int64_t lr_mfma_ws_bytes(const LrProblem& p);
-hipError_t lr_mfma_bwd(const LrProblem& p);
+hipError_t lr_mfma_bwd(const LrProblem* p, int G);
 
 }  // namespace dc

@@ -26,10 +26,27 @@ namespace dc {
 //     shifted by 4), so every lane has the look-ahead rows it needs without
 //     cross-lane traffic; dy rows 4q..4q+W+2 are read from L1.
 // A workgroup is 4 wavefronts on 4 adjacent 64-channel chunks of the same
-// rows.  dz partial sums over the 256 channels are added in LDS per tile in
-// wave order and written as one fp32 partial per 256-channel group; dU
-// accumulates in registers over the wavefront's run of tiles and is written
-// as one fp32 partial per run.  reduce_partials sums both deterministically.
+// rows.  dz partial sums over the 256 channels are added in LDS in wave
+// order, once per batch of tiles, and written as one fp32 partial per
+// 256-channel group; dU accumulates in registers over the wavefront's run of
+// tiles and is written as one fp32 partial per run.  reduce_partials sums
+// both deterministically.
+//
+// Groups: up to kMaxGroups independent problems of one shape share a launch
+// (block index -> group); x and dx may have row strides xld, dxld > D, so the
+// q / k / v convolutions read x out of a fused [B, T, 3D] projection and write
+// dx into its gradient.
+
+struct LrBwdGroup {
+  const void* x;   // this group's first channel; rows xld elements apart
+  const void* z;
+  const void* U;
+  const void* sw;
+  const void* dy;
+  void* dx;        // this group's first channel; rows dxld elements apart
+  float* part_dz;
+  float* part_du;
+};
 
 struct LrBwdArgs {
   int Tn, D, R, RK, residual;
@@ -38,9 +55,13 @@ struct LrBwdArgs {
   int seg;    // tiles per run
   int nspb;   // runs per sequence
   int nseg;   // B * nspb
-  int nblk;   // ncg * nseg
+  int nblk;   // ncg * nseg * groups
+  int nblk1;  // ncg * nseg: blocks per group
+  int xld;    // row stride of x (elements)
+  int dxld;   // row stride of dx (elements)
   int zvec;   // R % 4 == 0 and z 8-byte aligned: 8-byte z loads
   int64_t BT;
+  LrBwdGroup grp[kMaxGroups];
 };
 
 
@@ -97,8 +118,6 @@ __device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds, u32x2 (&u
 
 template <typename T, int W, int RC, bool ZV>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && RC == 1 ? 2 : 1, 8))) void lr_bwd_mfma(
-    const T* __restrict__ x_, const T* __restrict__ z_, const T* __restrict__ U_, const T* __restrict__ sw_,
-    const T* __restrict__ dy_, T* __restrict__ dx_, float* __restrict__ part_dz, float* __restrict__ part_du,
     LrBwdArgs a) {
   constexpr int NB = (W + 6) / 4;  // MFMA row blocks for the dx look-ahead
   constexpr int NR = W + 3;        // x rows 4q-W+1 .. 4q+3 and dy rows 4q .. 4q+W+2 per lane
@@ -106,12 +125,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
   constexpr int NUW = W * RC * 4;  // packed tap-weight operands per lane
   constexpr int NUZ = W * RC * 2;  // dz operands per lane
   constexpr int GROW = 72;         // G tile row pitch (64 channels + 8 pad: conflict-free reads)
-  const uint16_t* __restrict__ x = reinterpret_cast<const uint16_t*>(x_);
-  const uint16_t* __restrict__ z = reinterpret_cast<const uint16_t*>(z_);
-  const uint16_t* __restrict__ U = reinterpret_cast<const uint16_t*>(U_);
-  const uint16_t* __restrict__ sw = reinterpret_cast<const uint16_t*>(sw_);
-  const uint16_t* __restrict__ dy = reinterpret_cast<const uint16_t*>(dy_);
-  uint16_t* __restrict__ dx = reinterpret_cast<uint16_t*>(dx_);
   __shared__ u32x2 uw_lds[4][UWREG ? 1 : NUW * 64];
   __shared__ u32x4 uz_lds[4][NUZ * 64];
   __shared__ __attribute__((aligned(16))) uint16_t gtile[4][16 * GROW];
@@ -124,7 +137,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
 
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int q = lane >> 4, n = lane & 15;
-  const int lb = xcd_remap(blockIdx.x, a.nblk);
+  const int lb0 = xcd_remap(blockIdx.x, a.nblk);
+  const int g = __builtin_amdgcn_readfirstlane(lb0 / a.nblk1);
+  const int lb = lb0 - g * a.nblk1;
+  const uint16_t* __restrict__ x = reinterpret_cast<const uint16_t*>(pick(a.grp, g, &LrBwdGroup::x));
+  const uint16_t* __restrict__ z = reinterpret_cast<const uint16_t*>(pick(a.grp, g, &LrBwdGroup::z));
+  const uint16_t* __restrict__ U = reinterpret_cast<const uint16_t*>(pick(a.grp, g, &LrBwdGroup::U));
+  const uint16_t* __restrict__ sw = reinterpret_cast<const uint16_t*>(pick(a.grp, g, &LrBwdGroup::sw));
+  const uint16_t* __restrict__ dy = reinterpret_cast<const uint16_t*>(pick(a.grp, g, &LrBwdGroup::dy));
+  uint16_t* __restrict__ dx = reinterpret_cast<uint16_t*>(pick(a.grp, g, &LrBwdGroup::dx));
+  float* __restrict__ part_dz = pick(a.grp, g, &LrBwdGroup::part_dz);
+  float* __restrict__ part_du = pick(a.grp, g, &LrBwdGroup::part_du);
   const int cg = lb % a.ncg, sg = lb / a.ncg;
   const int chunk = cg * 4 + wave;
   const int D = a.D, Tn = a.Tn;
@@ -142,13 +165,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
   u32x2* __restrict__ my_uw = uw_lds[wave];
   u32x4* __restrict__ my_uz = uz_lds[wave];
   uint16_t* __restrict__ my_g = gtile[wave];
-  const int rowb = D * 2;
-  const int64_t seqb = (int64_t)Tn * rowb;
-  const rsrc_t rx = make_rsrc(x + row0 * D, seqb);
-  const rsrc_t rdy = make_rsrc(dy + row0 * D, seqb);
-  const rsrc_t rdx = make_rsrc(dx + row0 * D, seqb);
+  const int rowb = D * 2, xrowb = a.xld * 2, dxrowb = a.dxld * 2;
+  const rsrc_t rx = make_rsrc(x + row0 * a.xld, (int64_t)Tn * xrowb);
+  const rsrc_t rdy = make_rsrc(dy + row0 * D, (int64_t)Tn * rowb);
+  const rsrc_t rdx = make_rsrc(dx + row0 * a.dxld, (int64_t)Tn * dxrowb);
   const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 2);
-  const int lane_off = chv ? (4 * q * D + col) * 2 : kOobLane;  // byte offset of the lane's row 4q quartet
+  // byte offsets of the lane's row 4q quartet in dy, x and dx
+  const int lane_off = chv ? (4 * q * D + col) * 2 : kOobLane;
+  const int xlane_off = chv ? (4 * q * a.xld + col) * 2 : kOobLane;
+  const int dxlane_off = chv ? (4 * q * a.dxld + col) * 2 : kOobLane;
 
   u32x2 uw_reg[UWREG ? NUW : 1];
   stage_uops<W, RC, UWREG>(my_uw, uw_reg, my_uz, U, sw, R, RK, D, d0, q, n, lane);
@@ -183,10 +208,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
   };
   auto load_tile = [&](int tile, TileIn& in) {
     const bool live = tile < tile1;
+    const int xtoff = live ? tile * 16 * xrowb : kOobTile;
     const int toff = live ? tile * 16 * rowb : kOobTile;
 #pragma unroll
     for (int m = 0; m < NR; ++m) {
-      in.xr[m] = bload64(rx, lane_off + toff + (m - (W - 1)) * rowb);
+      in.xr[m] = bload64(rx, xlane_off + xtoff + (m - (W - 1)) * xrowb);
       in.dyr[m] = bload64(rdy, lane_off + toff + m * rowb);
     }
 #pragma unroll
@@ -194,7 +220,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
   };
   auto compute_tile = [&](int tile, const TileIn& in) {
     const int t0 = tile * 16;
-    const int toff = t0 * rowb;
+    const int dxtoff = t0 * dxrowb;
     const u32x2(&xr)[NR] = in.xr;
     const u32x2(&dyr)[NR] = in.dyr;
     u32x2 zA[NB][RC];
@@ -284,7 +310,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
       u32x2 o;
       o[0] = pack2<T>(v[0], v[1]);
       o[1] = pack2<T>(v[2], v[3]);
-      bstore64<true>(o, rdx, lane_off + toff + i * rowb);
+      bstore64<true>(o, rdx, dxlane_off + dxtoff + i * dxrowb);
     }
     // ---- dz: gather this wavefront's tile sums; every DZB tiles (and at the end of
     // the run) add the 4 chunk wavefronts in wave order, one partial per group.
@@ -375,35 +401,44 @@ BwdWs bwd_ws(const LrProblem& p, const LrBwdArgs& a) {
 }
 
 template <typename T, int W, int RC>
-hipError_t launch_bwd(const LrProblem& p) {
-  const LrBwdArgs a = make_bwd_args(p, kBwdTargetWaves);
-  const BwdWs w = bwd_ws(p, a);
-  float* pdz = (float*)((char*)p.ws + w.dz_off);
-  float* pdu = (float*)((char*)p.ws + w.du_off);
+hipError_t launch_bwd(const LrProblem* p, int G) {
+  LrBwdArgs a = make_bwd_args(p[0], kBwdTargetWaves);
+  const BwdWs w = bwd_ws(p[0], a);
+  a.nblk1 = a.nblk;
+  a.nblk = G * a.nblk1;
+  a.xld = (int)p[0].xld();
+  a.dxld = (int)p[0].dxld();
+  for (int g = 0; g < G; ++g) {
+    float* pdz = (float*)((char*)p[g].ws + w.dz_off);
+    float* pdu = (float*)((char*)p[g].ws + w.du_off);
+    a.grp[g] = LrBwdGroup{p[g].x, p[g].z, p[g].U, p[g].static_w, p[g].dy, p[g].dx, pdz, pdu};
+    a.zvec = a.zvec && aligned_to(p[g].z, 8);
+  }
   if (a.zvec)
-    lr_bwd_mfma<T, W, RC, true><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.U,
-                                                               (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, pdz,
-                                                               pdu, a);
+    lr_bwd_mfma<T, W, RC, true><<<a.nblk, 256, 0, p[0].stream>>>(a);
   else
-    lr_bwd_mfma<T, W, RC, false><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.U,
-                                                                (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, pdz,
-                                                                pdu, a);
+    lr_bwd_mfma<T, W, RC, false><<<a.nblk, 256, 0, p[0].stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t WD = p.W * p.D, RKWD = (int64_t)a.RK * WD;
-  const PartialReduce jobs[3] = {
-      {pdu, RKWD, a.nseg, p.R * WD, p.dU},
-      {pdu + p.R * WD, RKWD, a.nseg, p.static_w ? WD : 0, p.dstatic_w},
-      {pdz, a.BT * a.R, a.ncg, a.BT * a.R, p.dz},
-  };
-  return reduce_partials_multi(jobs, 3, p.dtype, p.stream);
+  const int64_t WD = p[0].W * p[0].D, RKWD = (int64_t)a.RK * WD, R = p[0].R;
+  PartialReduce jobs[kMaxReduceJobs];
+  int nj = 0;
+  for (int g = 0; g < G; ++g) {
+    const float* pdz = a.grp[g].part_dz;
+    const float* pdu = a.grp[g].part_du;
+    jobs[nj++] = {pdu, RKWD, a.nseg, R * WD, p[g].dU};
+    jobs[nj++] = {pdu + R * WD, RKWD, a.nseg, p[g].static_w ? WD : 0, p[g].dstatic_w};
+    jobs[nj++] = {pdz, a.BT * R, a.ncg, a.BT * R, p[g].dz};
+  }
+  return reduce_partials_multi(jobs, nj, p[0].dtype, p[0].stream);
 }
 
 template <typename T>
-hipError_t dispatch_bwd(const LrProblem& p) {
+hipError_t dispatch_bwd(const LrProblem* pp, int G) {
+  const LrProblem& p = pp[0];
   const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
 #define DC_LR_CASE(WW, CC) \
-  if (p.W == WW && rc == CC) return launch_bwd<T, WW, CC>(p);
+  if (p.W == WW && rc == CC) return launch_bwd<T, WW, CC>(pp, G);
   DC_LR_CASE(1, 1) DC_LR_CASE(1, 2) DC_LR_CASE(1, 3) DC_LR_CASE(1, 4)
   DC_LR_CASE(2, 1) DC_LR_CASE(2, 2) DC_LR_CASE(2, 3)
   DC_LR_CASE(3, 1) DC_LR_CASE(3, 2)
@@ -418,8 +453,8 @@ hipError_t dispatch_bwd(const LrProblem& p) {
 
 int64_t lr_mfma_ws_bytes(const LrProblem& p) { return bwd_ws(p, make_bwd_args(p, kBwdTargetWaves)).total; }
 
-hipError_t lr_mfma_bwd(const LrProblem& p) {
-  return p.dtype == kBF16 ? dispatch_bwd<bf16>(p) : dispatch_bwd<fp16>(p);
+hipError_t lr_mfma_bwd(const LrProblem* p, int G) {
+  return p[0].dtype == kBF16 ? dispatch_bwd<bf16>(p, G) : dispatch_bwd<fp16>(p, G);
 }
 
 }  // namespace dc

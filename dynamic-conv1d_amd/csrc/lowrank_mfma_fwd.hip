@@ -11,9 +11,21 @@
 // The B operands (U_eff, 16 ranks x 8 columns per lane) are loaded once per
 // run as 128-bit row pieces and repacked; the A operand is the lane's row
 // of z_eff.  Reference: lowrank.py:24-67 (Triton forward kernel).
+//
+// Groups: up to kMaxGroups independent problems of one shape share a launch
+// (block index -> group); x may have a row stride xld > D, so the q / k / v
+// inputs are read straight out of a fused [B, T, 3D] projection.
 #include "lowrank_mfma.h"
 
 namespace dc {
+
+struct LrFwdGroup {
+  const void* x;  // this group's first channel; rows xld elements apart
+  const void* z;
+  const void* U;
+  const void* sw;
+  void* y;
+};
 
 struct LrArgs {
   int Tn;          // sequence length
@@ -27,8 +39,11 @@ struct LrArgs {
   int seg;         // 16-row tiles per run
   int nspb;        // runs per sequence
   int nseg;        // B * nspb
-  int nblk;        // grid size
+  int nblk;        // grid size (all groups)
+  int nblk1;       // blocks per group
+  int xld;         // row stride of x (elements)
   int zvec;        // R % 4 == 0 and z 8-byte aligned: 8-byte z loads (host dispatch)
+  LrFwdGroup grp[kMaxGroups];
 };
 
 // Packed B operands of one 128-channel chunk, staged once per workgroup:
@@ -60,21 +75,21 @@ __device__ __forceinline__ void stage_u(u32x2* __restrict__ lds, const uint16_t*
 }
 
 template <typename T, int W, int RC, bool ZV>
-__global__ __launch_bounds__(256) void lr_fwd_mfma(const T* __restrict__ x_, const T* __restrict__ z_,
-                                                   const T* __restrict__ U_, const T* __restrict__ sw_,
-                                                   T* __restrict__ y_, LrArgs a) {
+__global__ __launch_bounds__(256) void lr_fwd_mfma(LrArgs a) {
   constexpr int NR = W + 3;  // x rows 4q-W+1 .. 4q+3 of a lane
   typedef ZRaw<T, RC, ZV> ZR;
-  const uint16_t* __restrict__ x = reinterpret_cast<const uint16_t*>(x_);
-  const uint16_t* __restrict__ z = reinterpret_cast<const uint16_t*>(z_);
-  const uint16_t* __restrict__ U = reinterpret_cast<const uint16_t*>(U_);
-  const uint16_t* __restrict__ sw = reinterpret_cast<const uint16_t*>(sw_);
-  uint16_t* __restrict__ y = reinterpret_cast<uint16_t*>(y_);
   __shared__ u32x2 ub[W * RC * 8 * 64];
 
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int q = lane >> 4, n = lane & 15;
-  const int lb = xcd_remap(blockIdx.x, a.nblk);
+  const int lb0 = xcd_remap(blockIdx.x, a.nblk);
+  const int g = __builtin_amdgcn_readfirstlane(lb0 / a.nblk1);
+  const int lb = lb0 - g * a.nblk1;
+  const uint16_t* __restrict__ x = reinterpret_cast<const uint16_t*>(pick(a.grp, g, &LrFwdGroup::x));
+  const uint16_t* __restrict__ z = reinterpret_cast<const uint16_t*>(pick(a.grp, g, &LrFwdGroup::z));
+  const uint16_t* __restrict__ U = reinterpret_cast<const uint16_t*>(pick(a.grp, g, &LrFwdGroup::U));
+  const uint16_t* __restrict__ sw = reinterpret_cast<const uint16_t*>(pick(a.grp, g, &LrFwdGroup::sw));
+  uint16_t* __restrict__ y = reinterpret_cast<uint16_t*>(pick(a.grp, g, &LrFwdGroup::y));
   const int chunk = lb % a.nch, sgp = lb / a.nch;  // 4 wavefronts: one chunk, 4 consecutive runs
   const int D = a.D, Tn = a.Tn, R = a.R, RK = a.RK;
   const int dl = chunk * 128 + 8 * n;  // first channel of the lane's octet
@@ -89,11 +104,12 @@ __global__ __launch_bounds__(256) void lr_fwd_mfma(const T* __restrict__ x_, con
   const int tile0 = (sg - b * a.nspb) * a.seg;
   const int tile1 = min(tile0 + a.seg, ntile);
   const int64_t row0 = (int64_t)b * Tn;
-  const int rowb = D * 2;
-  const rsrc_t rx = make_rsrc(x + row0 * D, (int64_t)Tn * rowb);
+  const int rowb = D * 2, xrowb = a.xld * 2;
+  const rsrc_t rx = make_rsrc(x + row0 * a.xld, (int64_t)Tn * xrowb);
   const rsrc_t ry = make_rsrc(y + row0 * D, (int64_t)Tn * rowb);
   const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 2);
-  const int lane_off = chv ? (4 * q * D + dl) * 2 : kOobLane;  // byte offset of the lane's row 4q octet
+  const int lane_off = chv ? (4 * q * D + dl) * 2 : kOobLane;         // y byte offset of the lane's row 4q octet
+  const int xlane_off = chv ? (4 * q * a.xld + dl) * 2 : kOobLane;   // the same in x
 
   // Tile inputs (rows out of the sequence read as 0).  Two buffers, A and B,
   // alternate: while one tile is computed the next one's loads are in flight.
@@ -102,9 +118,9 @@ __global__ __launch_bounds__(256) void lr_fwd_mfma(const T* __restrict__ x_, con
   // is copied, so the compiler's waits stay partial (vmcnt(N), not vmcnt(0)).
   auto load_tile = [&](int tile, u32x4(&xr)[NR], ZR& zr) {
     const bool live = tile < tile1;
-    const int toff = live ? tile * 16 * rowb : kOobTile;
+    const int toff = live ? tile * 16 * xrowb : kOobTile;
 #pragma unroll
-    for (int m = 0; m < NR; ++m) xr[m] = bload128(rx, lane_off + toff + (m - (W - 1)) * rowb);
+    for (int m = 0; m < NR; ++m) xr[m] = bload128(rx, xlane_off + toff + (m - (W - 1)) * xrowb);
     zr.load(rz, live ? (tile * 16 + n) * R * 2 : kOobTile, R, q);
   };
   auto compute_tile = [&](int tile, const u32x4(&xc)[NR], const ZR& zr) {
@@ -185,22 +201,28 @@ LrArgs make_args(const LrProblem& p, int target_waves) {
 }
 
 template <typename T, int W, int RC>
-hipError_t launch_fwd(const LrProblem& p) {
-  const LrArgs a = make_args(p, 2048);
+hipError_t launch_fwd(const LrProblem* p, int G) {
+  LrArgs a = make_args(p[0], 2048);
+  a.nblk1 = a.nblk;
+  a.nblk = G * a.nblk1;
+  a.xld = (int)p[0].xld();
+  for (int g = 0; g < G; ++g) {
+    a.grp[g] = LrFwdGroup{p[g].x, p[g].z, p[g].U, p[g].static_w, p[g].y};
+    a.zvec = a.zvec && aligned_to(p[g].z, 8);
+  }
   if (a.zvec)
-    lr_fwd_mfma<T, W, RC, true><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.U,
-                                                               (const T*)p.static_w, (T*)p.y, a);
+    lr_fwd_mfma<T, W, RC, true><<<a.nblk, 256, 0, p[0].stream>>>(a);
   else
-    lr_fwd_mfma<T, W, RC, false><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.U,
-                                                                (const T*)p.static_w, (T*)p.y, a);
+    lr_fwd_mfma<T, W, RC, false><<<a.nblk, 256, 0, p[0].stream>>>(a);
   return hipGetLastError();
 }
 
 template <typename T>
-hipError_t dispatch_fwd(const LrProblem& p) {
+hipError_t dispatch_fwd(const LrProblem* pp, int G) {
+  const LrProblem& p = pp[0];
   const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
 #define DC_LR_CASE(WW, CC) \
-  if (p.W == WW && rc == CC) return launch_fwd<T, WW, CC>(p);
+  if (p.W == WW && rc == CC) return launch_fwd<T, WW, CC>(pp, G);
   DC_LR_CASE(1, 1) DC_LR_CASE(1, 2) DC_LR_CASE(1, 3) DC_LR_CASE(1, 4)
   DC_LR_CASE(2, 1) DC_LR_CASE(2, 2) DC_LR_CASE(2, 3) DC_LR_CASE(2, 4)
   DC_LR_CASE(3, 1) DC_LR_CASE(3, 2)
@@ -212,8 +234,8 @@ hipError_t dispatch_fwd(const LrProblem& p) {
 
 }  // namespace
 
-hipError_t lr_mfma_fwd(const LrProblem& p) {
-  return p.dtype == kBF16 ? dispatch_fwd<bf16>(p) : dispatch_fwd<fp16>(p);
+hipError_t lr_mfma_fwd(const LrProblem* p, int G) {
+  return p[0].dtype == kBF16 ? dispatch_fwd<bf16>(p, G) : dispatch_fwd<fp16>(p, G);
 }
 
 }  // namespace dc

@@ -5,13 +5,14 @@
 // channel groups (dz).  The reference accumulates those with relaxed fp32
 // atomics (headwise.py:157-159, lowrank.py:136-137), so its results vary run
 // to run; here every column is summed in a fixed order, then rounded once to
-// the output dtype.  Up to kMaxJobs reductions share one launch.
+// the output dtype.  Up to kMaxJobs reductions share one launch (three per
+// lowrank problem: dU, dstatic_w, dz; a grouped launch has up to kMaxGroups).
 #include "dc_common.h"
 #include "dc_launch.h"
 
 namespace dc {
 
-constexpr int kMaxJobs = 3;
+constexpr int kMaxJobs = kMaxReduceJobs;
 
 struct ReduceJob {
   const float* part;  // partial p, column c at part[p * pstride + c]
@@ -76,8 +77,9 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(ReduceJobs jobs) {
 hipError_t reduce_partials_multi(const PartialReduce* r, int n, int dtype, hipStream_t stream) {
   ReduceJobs jobs{};
   int blocks = 0;
-  for (int i = 0; i < n && jobs.n < kMaxJobs; ++i) {
+  for (int i = 0; i < n; ++i) {
     if (r[i].C <= 0) continue;
+    if (jobs.n == kMaxJobs) return hipErrorInvalidValue;
     ReduceJob& J = jobs.j[jobs.n++];
     J.part = r[i].part;
     J.pstride = r[i].pstride;

@@ -13,13 +13,14 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdynconv.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 _c_vp = ctypes.c_void_p
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
+_c_pp = ctypes.POINTER(ctypes.c_void_p)  # host array of device pointers
 
 # name -> (restype, argtypes); mirrors include/dynconv.h.
 SIGNATURES = {
@@ -31,6 +32,10 @@ SIGNATURES = {
     "dc_lowrank_fwd": (_c_int, [_c_vp] * 5 + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
     "dc_lowrank_bwd_ws_bytes": (_c_i64, [_c_i64] * 5 + [_c_int, _c_int]),
     "dc_lowrank_bwd": (_c_int, [_c_vp] * 10 + [_c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
+    "dc_lowrank_fwd_grouped": (_c_int, [_c_i64, _c_vp, _c_i64] + [_c_pp] * 4 + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
+    "dc_lowrank_bwd_grouped_ws_bytes": (_c_i64, [_c_i64] * 6 + [_c_int, _c_int]),
+    "dc_lowrank_bwd_grouped": (_c_int, [_c_i64, _c_vp, _c_i64] + [_c_pp] * 4 + [_c_vp, _c_i64] + [_c_pp] * 3
+                               + [_c_vp, _c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
 }
 
 _lib = None
@@ -73,6 +78,13 @@ def check(status: int, what: str) -> None:
 
 def ptr(t):
     return None if t is None else t.data_ptr()
+
+
+def ptr_array(ts):
+    """A host array of the tensors' device pointers (a `const void* const*` argument), or None."""
+    if ts is None:
+        return None
+    return (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
 
 
 def stream_of(t: torch.Tensor):

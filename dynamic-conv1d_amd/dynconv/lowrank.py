@@ -99,3 +99,123 @@ def lowrank_dynamic_convolution(
     assert U.dim() == 2 and U.shape[0] == R and U.shape[1] % x.shape[-1] == 0, "U must be [R, W*D]"
     assert x.dtype == z.dtype == U.dtype, "x, z and U must share one dtype"
     return _LowrankDynamicConvolutionFn.apply(x, z, U, static_w, residual)
+
+
+class _GroupedLowrankDynamicConvolutionFn(torch.autograd.Function):
+    """G lowrank convolutions of one shape in one launch per direction.
+
+    x is [B, T, G*D] (a fused projection, read in place: rows may be further
+    apart than G*D); group g convolves its columns g*D .. g*D+D-1.  The
+    backward writes the gradient of x as one [B, T, G*D] tensor, so the
+    README's .contiguous() copies (README.md:76-78) and the concatenation of
+    dq, dk, dv do not happen.
+    """
+
+    @staticmethod
+    def forward(ctx, x, residual, G, has_static, *params):
+        zs, Us = params[:G], params[G:2 * G]
+        sws = params[2 * G:3 * G] if has_static else None
+        B, T, C = x.shape
+        D = C // G
+        R = zs[0].shape[-1]
+        W = Us[0].shape[-1] // D
+        ys = [torch.empty(B, T, D, dtype=x.dtype, device=x.device) for _ in range(G)]
+        lib = _capi.load()
+        status = lib.dc_lowrank_fwd_grouped(
+            G, _capi.ptr(x), x.stride(1), _capi.ptr_array(zs), _capi.ptr_array(Us), _capi.ptr_array(sws),
+            _capi.ptr_array(ys), B, T, D, R, W, _capi.dtype_code(x.dtype), int(bool(residual)), _capi.stream_of(x),
+        )
+        _capi.check(status, "grouped lowrank forward")
+        ctx.save_for_backward(x, *params)
+        ctx.G, ctx.has_static, ctx.residual = G, has_static, bool(residual)
+        return tuple(ys)
+
+    @staticmethod
+    def backward(ctx, *dys):
+        x, *params = ctx.saved_tensors
+        G, has_static = ctx.G, ctx.has_static
+        zs, Us = params[:G], params[G:2 * G]
+        sws = params[2 * G:3 * G] if has_static else None
+        B, T, C = x.shape
+        D = C // G
+        R = zs[0].shape[-1]
+        W = Us[0].shape[-1] // D
+        dtype = _capi.dtype_code(x.dtype)
+        # an output that did not reach the loss has no gradient: it contributes zeros
+        dys = [torch.zeros(B, T, D, dtype=x.dtype, device=x.device) if d is None else d.to(x.dtype).contiguous()
+               for d in dys]
+        dx = torch.empty(B, T, C, dtype=x.dtype, device=x.device)
+        dzs = [torch.empty_like(z) for z in zs]
+        dUs = [torch.empty_like(U) for U in Us]
+        dsws = [torch.empty_like(s) for s in sws] if has_static else None
+        lib = _capi.load()
+        ws_bytes = lib.dc_lowrank_bwd_grouped_ws_bytes(G, B, T, D, R, W, dtype, int(has_static))
+        _capi.check(int(ws_bytes) if ws_bytes < 0 else 0, "grouped lowrank backward workspace query")
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes > 0 else None
+        status = lib.dc_lowrank_bwd_grouped(
+            G, _capi.ptr(x), x.stride(1), _capi.ptr_array(zs), _capi.ptr_array(Us), _capi.ptr_array(sws),
+            _capi.ptr_array(dys), _capi.ptr(dx), C, _capi.ptr_array(dzs), _capi.ptr_array(dUs),
+            _capi.ptr_array(dsws), _capi.ptr(ws), ws_bytes, B, T, D, R, W, dtype, int(ctx.residual),
+            _capi.stream_of(x),
+        )
+        _capi.check(status, "grouped lowrank backward")
+        return (dx, None, None, None, *dzs, *dUs, *(dsws or []))
+
+
+def lowrank_dynamic_convolution_grouped(
+    x: torch.Tensor,
+    z,
+    U,
+    static_w=None,
+    residual: bool = False,
+):
+    """G lowrank dynamic short convolutions of one shape, e.g. on the q, k and v of an attention layer.
+
+    Equivalent to
+        [lowrank_dynamic_convolution(x[..., g*D:(g+1)*D].contiguous(), z[g], U[g], static_w[g], residual)
+         for g in range(G)]
+    (README.md:57-110), computed by one launch per direction with x read in place.
+
+    Args:
+        x:          [B, T, G*D] activations, e.g. the fused q|k|v projection.  Channels must be
+                    contiguous (stride 1); rows may be further apart (a column slice of a wider tensor).
+        z:          G tensors [B, T, R], contiguous.
+        U:          G tensors [R, W*D], contiguous.
+        static_w:   None, or G tensors [W, D] fused as one extra rank each.
+        residual:   add each group's input to its output.
+
+    Returns:
+        a tuple of G tensors [B, T, D].
+
+    Per group, the preconditions of lowrank_dynamic_convolution (lowrank.py:328-337); G <= 4.
+    """
+    z, U = list(z), list(U)
+    G = len(z)
+    assert 1 <= G <= 4, "between 1 and 4 groups"
+    assert len(U) == G, "one U per group"
+    has_static = static_w is not None
+    if has_static:
+        static_w = list(static_w)
+        assert len(static_w) == G, "one static_w per group"
+    assert x.is_cuda and x.dim() == 3 and x.shape[-1] % G == 0, "x must be [B, T, G*D]"
+    if x.stride(2) != 1 or x.stride(0) != x.shape[1] * x.stride(1):
+        x = x.contiguous()
+    B, T, C = x.shape
+    D = C // G
+    R = z[0].shape[-1]
+    R_kernel = R + 1 if has_static else R
+    assert R_kernel & (R_kernel - 1) == 0, "rank R must be a power of 2. If static_w is set R+1 must be a power of 2."
+    for g in range(G):
+        assert z[g].is_cuda and z[g].is_contiguous()
+        assert U[g].is_cuda and U[g].is_contiguous()
+        assert z[g].dim() == 3 and tuple(z[g].shape) == (B, T, R), "every z must be [B, T, R]"
+        assert U[g].dim() == 2 and U[g].shape[0] == R and U[g].shape[1] % D == 0, "U must be [R, W*D]"
+        assert U[g].shape == U[0].shape, "every U must have one shape"
+        assert x.dtype == z[g].dtype == U[g].dtype, "x, z and U must share one dtype"
+        if has_static:
+            s = static_w[g]
+            assert s.is_cuda and s.is_contiguous()
+            assert s.dtype == z[g].dtype == U[g].dtype
+            assert s.shape == (U[g].shape[-1] // D, D)
+    params = z + U + (static_w if has_static else [])
+    return _GroupedLowrankDynamicConvolutionFn.apply(x, residual, G, has_static, *params)

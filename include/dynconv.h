@@ -15,6 +15,10 @@
  *                                              static-as-rank fusion 223-225, launch 230-242)
  *   dc_lowrank_bwd    <- lowrank.py:251-299   (.backward, launches 266-292, dU cast and
  *                                              static split 294-299)
+ *   dc_lowrank_fwd_grouped, dc_lowrank_bwd_grouped
+ *                     <- README.md:57-110 (the QKV usage: three lowrank_dynamic_convolution
+ *                                              calls, lowrank.py:302-338, on .contiguous()
+ *                                              slices of one fused projection)
  *
  * Conventions
  *   - Every tensor pointer is a DEVICE pointer to a contiguous row-major array:
@@ -23,7 +27,8 @@
  *       z, dz               [B, T, R]           (lowrank; R = dynamic rank, without static)
  *       U, dU               [R, W * D]          (tap k occupies columns k*D .. k*D+D-1)
  *       static_w, dstatic_w [W, D]              (may be NULL: no static filter)
- *     All tensors of one call share `dtype`.
+ *     All tensors of one call share `dtype`.  The grouped lowrank calls read x
+ *     (and write dx) as G column slices of one [B, T, x_ld] array.
  *   - Sizes are int64.  Returns DC_OK (0) or a negative dc_status.
  *   - Arguments are validated before any HIP call; nothing is launched on error.
  *   - No call allocates device memory, synchronises, or throws.  Scratch for
@@ -44,10 +49,12 @@
 extern "C" {
 #endif
 
-#define DC_ABI_VERSION 1
+#define DC_ABI_VERSION 2
 
 /* Largest convolution width and (kernel) rank accepted. */
 #define DC_MAX_W 8
+/* Largest number of problems in one grouped lowrank call. */
+#define DC_MAX_GROUPS 4
 #define DC_MAX_R 64
 
 typedef enum dc_dtype {
@@ -111,6 +118,38 @@ int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* stat
                    void* workspace, int64_t ws_bytes,
                    int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
                    int dtype, int residual, void* stream);
+
+/* G (1 .. DC_MAX_GROUPS) lowrank forwards of one shape in one launch, e.g. the
+ * q, k and v convolutions of an attention layer.  Group g reads x + g*D, whose
+ * rows are x_ld >= G*D elements apart (the column slices of a fused [B, T, G*D]
+ * projection, read in place); z, U, y are arrays of G device pointers, each a
+ * contiguous tensor as in dc_lowrank_fwd; static_w is NULL (no static filter in
+ * any group) or an array of G non-NULL pointers.  Each group's y equals what
+ * dc_lowrank_fwd computes for it.  Replaces the three calls of README.md:57-110
+ * (lowrank.py:302-338 each) and the .contiguous() copies of their inputs. */
+int dc_lowrank_fwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z,
+                           const void* const* U, const void* const* static_w, void* const* y,
+                           int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
+                           int dtype, int residual, void* stream);
+
+/* Workspace bytes needed by dc_lowrank_bwd_grouped, or a negative dc_status. */
+int64_t dc_lowrank_bwd_grouped_ws_bytes(int64_t G, int64_t B, int64_t T, int64_t D, int64_t R,
+                                        int64_t W, int dtype, int has_static);
+
+/* The G backwards of dc_lowrank_fwd_grouped in one pass: group g writes its dx
+ * into dx + g*D (rows dx_ld >= G*D elements apart: the gradient of the fused
+ * projection, written in place), and dz[g], dU[g] (and dstatic_w[g]) as
+ * dc_lowrank_bwd does; dy is an array of G contiguous [B, T, D] gradients.
+ * dstatic_w is NULL exactly when static_w is.  Per group, results are bitwise
+ * those of dc_lowrank_bwd.  Replaces README.md:57-110's three backwards
+ * (lowrank.py:251-299 each) and the concatenation of dq, dk, dv. */
+int dc_lowrank_bwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z,
+                           const void* const* U, const void* const* static_w,
+                           const void* const* dy, void* dx, int64_t dx_ld,
+                           void* const* dz, void* const* dU, void* const* dstatic_w,
+                           void* workspace, int64_t ws_bytes,
+                           int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
+                           int dtype, int residual, void* stream);
 
 #ifdef __cplusplus
 }

@@ -14,3 +14,5 @@ if _PKG_DIR not in _sys.path:
 
 from dynconv.lowrank import lowrank_dynamic_convolution  # noqa: E402,F401
 from dynconv.lowrank import _LowrankDynamicConvolutionFn  # noqa: E402,F401
+from dynconv.lowrank import lowrank_dynamic_convolution_grouped  # noqa: E402,F401
+from dynconv.modules import LowRankDynamicShortConvolution, GroupedLowRankDynamicShortConvolution  # noqa: E402,F401

@@ -35,7 +35,7 @@ def header_functions():
 
 def test_exports_every_declared_symbol(lib):
     names = header_functions()
-    assert len(names) == 8, names
+    assert len(names) == 11, names
     raw = ctypes.CDLL(_capi.LIB_PATH)
     for n in names:
         assert hasattr(raw, n), f"{n} declared in dynconv.h but not exported"
@@ -43,7 +43,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_strings(lib):
-    assert lib.dc_abi_version() == 1
+    assert lib.dc_abi_version() == 2
     for s in (OK, E_NULL, E_SHAPE, E_DTYPE, E_UNSUP, E_WS, E_ALIGN, E_DEV, E_LAUNCH):
         assert len(lib.dc_status_string(s)) > 0
     assert b"unknown" in lib.dc_status_string(-99)
@@ -116,3 +116,62 @@ def test_lowrank_validation(lib):
         assert lr_fwd(lib) == E_DEV
         st = lib.dc_lowrank_bwd(P, P, P, P, P, P, P, P, P, P, need, 2, 8, 16, 4, 4, 0, 0, None)
         assert st == E_DEV
+
+
+def arr(*ptrs):
+    """A host array of fake device pointers (a `const void* const*` argument)."""
+    return (ctypes.c_void_p * len(ptrs))(*ptrs)
+
+
+def lr_fwd_g(lib, G=3, x=P, x_ld=48, z="ok", U="ok", sw=None, y="ok", B=2, T=8, D=16, R=4, W=4, dt=0):
+    z = arr(*[P] * G) if z == "ok" else z
+    U = arr(*[P] * G) if U == "ok" else U
+    y = arr(*[P] * G) if y == "ok" else y
+    return lib.dc_lowrank_fwd_grouped(G, x, x_ld, z, U, sw, y, B, T, D, R, W, dt, 0, None)
+
+
+def test_lowrank_grouped_fwd_validation(lib):
+    no_dev = not torch.cuda.is_available()
+    assert lr_fwd_g(lib, G=0) == E_UNSUP
+    assert lr_fwd_g(lib, G=5, x_ld=80) == E_UNSUP          # > DC_MAX_GROUPS
+    assert lr_fwd_g(lib, x_ld=47) == E_SHAPE               # rows narrower than G*D
+    assert lr_fwd_g(lib, x_ld=1 << 31) == E_SHAPE
+    assert lr_fwd_g(lib, dt=9) == E_DTYPE
+    assert lr_fwd_g(lib, W=9) == E_UNSUP
+    assert lr_fwd_g(lib, x=None) == E_NULL
+    assert lr_fwd_g(lib, z=None) == E_NULL
+    assert lr_fwd_g(lib, y=arr(P, None, P)) == E_NULL      # a NULL entry
+    assert lr_fwd_g(lib, sw=arr(P, P, None)) == E_NULL      # static_w for every group or none
+    assert lr_fwd_g(lib, U=arr(P, P + 1, P)) == E_ALIGN
+    assert lr_fwd_g(lib, x=P + 1) == E_ALIGN
+    if no_dev:
+        assert lr_fwd_g(lib) == E_DEV
+        assert lr_fwd_g(lib, G=1, x_ld=16, sw=arr(P)) == E_DEV
+        assert lr_fwd_g(lib, G=4, x_ld=100, sw=arr(P, P, P, P)) == E_DEV
+
+
+def test_lowrank_grouped_bwd_validation(lib):
+    no_dev = not torch.cuda.is_available()
+    one = lib.dc_lowrank_bwd_ws_bytes(2, 8, 16, 4, 4, 0, 1)
+    need = lib.dc_lowrank_bwd_grouped_ws_bytes(3, 2, 8, 16, 4, 4, 0, 1)
+    assert need == 3 * ((one + 255) // 256 * 256)
+    assert lib.dc_lowrank_bwd_grouped_ws_bytes(0, 2, 8, 16, 4, 4, 0, 1) == E_UNSUP
+    assert lib.dc_lowrank_bwd_grouped_ws_bytes(3, 2, 8, 16, 0, 4, 0, 1) == E_SHAPE
+    g3 = arr(P, P, P)
+
+    def call(G=3, x_ld=48, dx_ld=48, sw=None, dsw=None, ws=P, nws=need, dz=g3, dy=g3):
+        return lib.dc_lowrank_bwd_grouped(G, P, x_ld, g3, g3, sw, dy, P, dx_ld, dz, g3, dsw, ws, nws,
+                                          2, 8, 16, 4, 4, 0, 0, None)
+
+    assert call(G=5) == E_UNSUP
+    assert call(dx_ld=40) == E_SHAPE
+    assert call(x_ld=40) == E_SHAPE
+    assert call(sw=g3, dsw=None) == E_NULL
+    assert call(sw=None, dsw=g3) == E_NULL
+    assert call(dz=arr(P, None, P)) == E_NULL
+    assert call(dy=None) == E_NULL
+    assert call(sw=g3, dsw=g3, ws=None) == E_WS
+    assert call(sw=g3, dsw=g3, nws=need - 256) == E_WS
+    assert call(sw=g3, dsw=g3, ws=P + 16) == E_WS           # workspace shares start 256-byte aligned
+    if no_dev:
+        assert call(sw=g3, dsw=g3) == E_DEV

@@ -1,0 +1,208 @@
+"""GPU parity of the grouped lowrank operator and the README modules.
+
+lowrank_dynamic_convolution_grouped runs G lowrank convolutions of one shape
+in one launch per direction, reading x as G column slices of one [B, T, G*D]
+tensor in place (README.md:57-110 uses three calls on .contiguous() slices of
+the fused q|k|v projection).  Checked here:
+
+* every group's y, dx slice, dz, dU and dstatic_w against the CPU oracle
+  (oracle/reference_cpu.py) on the same dtype-rounded inputs, to the
+  north-star tolerance, for 1-4 groups, with and without the static filter,
+  on the MFMA path (bf16, fp16) and the generic path (fp32), with x a column
+  slice of a wider tensor (row stride above G*D);
+* bitwise equality with G separate lowrank_dynamic_convolution calls (same
+  kernels, same reduction order per group);
+* a loss that uses only some groups' outputs (the others get zero gradients);
+* GroupedLowRankDynamicShortConvolution against G LowRankDynamicShortConvolution
+  modules holding the same parameters, and the README module against the oracle.
+"""
+
+import math
+
+import pytest
+import torch
+
+from helpers import assert_ns, gen, randn, uniform
+from oracle.reference_cpu import lowrank_dynamic_convolution_ref as lr_ref
+import lowrank as lr_mod
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+lr = lr_mod.lowrank_dynamic_convolution
+lr_grouped = lr_mod.lowrank_dynamic_convolution_grouped
+
+
+def _inputs(G, Bn, Tn, Dn, R, W, static, extra, seed):
+    """fp32 CPU inputs: x [B, T, G*D + extra] (the grouped op reads its first G*D columns), dy per group."""
+    g = gen(seed)
+    xw = randn(g, Bn, Tn, G * Dn + extra)
+    zs = [randn(g, Bn, Tn, R) for _ in range(G)]
+    Us = [randn(g, R, W * Dn, scale=1 / math.sqrt((R + int(static)) * W)) for _ in range(G)]
+    sws = [uniform(g, W, Dn, lo=-1 / math.sqrt(W), hi=1 / math.sqrt(W)) for _ in range(G)] if static else None
+    dys = [randn(g, Bn, Tn, Dn) for _ in range(G)]
+    return xw, zs, Us, sws, dys
+
+
+def _leaf(t, dtype):
+    return t.to(dtype).to(DEV).detach().requires_grad_()
+
+
+CASES = [
+    # G, B, T, D, R, W, static, extra columns, dtype
+    (3, 2, 64, 128, 15, 4, True, 64, torch.bfloat16),   # q|k|v slice of a wider tensor, static as rank 16
+    (3, 2, 80, 64, 16, 4, False, 0, torch.bfloat16),    # contiguous fused input, rank 16
+    (4, 1, 48, 64, 31, 3, True, 8, torch.bfloat16),     # four groups, two rank chunks
+    (2, 2, 33, 128, 8, 2, False, 16, torch.float16),    # odd T
+    (1, 2, 40, 48, 7, 4, True, 0, torch.bfloat16),      # one group
+    (2, 2, 24, 40, 3, 3, True, 12, torch.float32),      # fp32: generic path, D % 8 != 0
+]
+
+
+@pytest.mark.parametrize("G,Bn,Tn,Dn,R,W,static,extra,dtype", CASES)
+def test_grouped_against_oracle(G, Bn, Tn, Dn, R, W, static, extra, dtype):
+    xw, zs, Us, sws, dys = _inputs(G, Bn, Tn, Dn, R, W, static, extra, seed=G * 131 + Tn + Dn + R)
+    # kernel: x is the column slice [:, :, :G*D] of the wider device tensor
+    xw_k = xw.to(dtype).to(DEV)
+    x_k = xw_k[..., :G * Dn].detach().requires_grad_()
+    assert extra == 0 or not x_k.is_contiguous()
+    zk = [_leaf(t, dtype) for t in zs]
+    Uk = [_leaf(t, dtype) for t in Us]
+    sk = [_leaf(t, dtype) for t in sws] if static else None
+    ys = lr_grouped(x_k, zk, Uk, sk, residual=True)
+    assert len(ys) == G
+    torch.autograd.backward(ys, [d.to(dtype).to(DEV) for d in dys])
+    torch.cuda.synchronize()
+    for g in range(G):
+        xs = xw[..., g * Dn:(g + 1) * Dn].to(dtype).float().requires_grad_()
+        zr = zs[g].to(dtype).float().requires_grad_()
+        Ur = Us[g].to(dtype).float().requires_grad_()
+        sr = sws[g].to(dtype).float().requires_grad_() if static else None
+        yr = lr_ref(xs, zr, Ur, sr, residual=True)
+        yr.backward(dys[g].to(dtype).float())
+        assert_ns(ys[g], yr, dtype, f"g{g} y")
+        assert_ns(x_k.grad[..., g * Dn:(g + 1) * Dn], xs.grad, dtype, f"g{g} dx")
+        assert_ns(zk[g].grad, zr.grad, dtype, f"g{g} dz", elementwise=False)
+        assert_ns(Uk[g].grad, Ur.grad, dtype, f"g{g} dU", elementwise=False)
+        if static:
+            assert_ns(sk[g].grad, sr.grad, dtype, f"g{g} dstatic_w", elementwise=False)
+
+
+@pytest.mark.parametrize("static", [False, True])
+def test_grouped_bitwise_equals_separate_calls(static):
+    G, Bn, Tn, Dn, R, W = 3, 2, 96, 256, 15 if static else 16, 4
+    dtype = torch.bfloat16
+    xw, zs, Us, sws, dys = _inputs(G, Bn, Tn, Dn, R, W, static, 32, seed=7 + int(static))
+    xw_k = xw.to(dtype).to(DEV)
+    dyk = [d.to(dtype).to(DEV) for d in dys]
+
+    x_g = xw_k[..., :G * Dn].detach().requires_grad_()
+    zg = [_leaf(t, dtype) for t in zs]
+    Ug = [_leaf(t, dtype) for t in Us]
+    sg = [_leaf(t, dtype) for t in sws] if static else None
+    ys_g = lr_grouped(x_g, zg, Ug, sg, residual=True)
+    torch.autograd.backward(ys_g, dyk)
+
+    for g in range(G):
+        x1 = xw_k[..., g * Dn:(g + 1) * Dn].contiguous().requires_grad_()
+        z1, U1 = _leaf(zs[g], dtype), _leaf(Us[g], dtype)
+        s1 = _leaf(sws[g], dtype) if static else None
+        y1 = lr(x1, z1, U1, s1, residual=True)
+        y1.backward(dyk[g])
+        assert torch.equal(ys_g[g], y1), f"group {g}: y"
+        assert torch.equal(x_g.grad[..., g * Dn:(g + 1) * Dn], x1.grad), f"group {g}: dx"
+        assert torch.equal(zg[g].grad, z1.grad), f"group {g}: dz"
+        assert torch.equal(Ug[g].grad, U1.grad), f"group {g}: dU"
+        if static:
+            assert torch.equal(sg[g].grad, s1.grad), f"group {g}: dstatic_w"
+
+
+def test_grouped_partial_loss():
+    """Outputs that do not reach the loss contribute zero gradients."""
+    G, Bn, Tn, Dn, R, W = 3, 1, 64, 128, 15, 4
+    dtype = torch.bfloat16
+    xw, zs, Us, sws, dys = _inputs(G, Bn, Tn, Dn, R, W, True, 0, seed=3)
+    x = _leaf(xw, dtype)
+    zk = [_leaf(t, dtype) for t in zs]
+    Uk = [_leaf(t, dtype) for t in Us]
+    sk = [_leaf(t, dtype) for t in sws]
+    q, k, v = lr_grouped(x, zk, Uk, sk, residual=True)
+    (q.float() * dys[0].to(DEV)).sum().backward()
+    assert torch.count_nonzero(x.grad[..., Dn:]) == 0
+    for g in (1, 2):
+        assert torch.count_nonzero(zk[g].grad) == 0 and torch.count_nonzero(Uk[g].grad) == 0
+        assert torch.count_nonzero(sk[g].grad) == 0
+    xs = xw[..., :Dn].to(dtype).float().requires_grad_()
+    zr, Ur, sr = (t.to(dtype).float().requires_grad_() for t in (zs[0], Us[0], sws[0]))
+    yr = lr_ref(xs, zr, Ur, sr, residual=True)
+    (yr * dys[0]).sum().backward()
+    assert_ns(x.grad[..., :Dn], xs.grad, dtype, "dq")
+    assert_ns(zk[0].grad, zr.grad, dtype, "dz_q", elementwise=False)
+
+
+def test_modules_grouped_matches_separate():
+    from dynconv import GroupedLowRankDynamicShortConvolution, LowRankDynamicShortConvolution
+
+    torch.manual_seed(0)
+    Dm, R, W, G, Bn, Tn = 256, 15, 4, 3, 2, 128
+    dtype = torch.bfloat16
+    grouped = GroupedLowRankDynamicShortConvolution(Dm, R, W, groups=G).to(DEV, dtype)
+    with torch.no_grad():
+        grouped.proj_out.normal_(0, 1 / math.sqrt((R + 1) * W))  # the README initialises U to zero
+    singles = []
+    for g in range(G):
+        m = LowRankDynamicShortConvolution(Dm, R, W).to(DEV, dtype)
+        with torch.no_grad():
+            m.proj_in.weight.copy_(grouped.proj_in.weight[g * R:(g + 1) * R])
+            m.proj_out.copy_(grouped.proj_out[g])
+            m.proj_out_bias.copy_(grouped.proj_out_bias[g])
+        singles.append(m)
+    pre_z = torch.randn(Bn, Tn, Dm, device=DEV, dtype=dtype)
+    qkv = torch.randn(Bn, Tn, G * Dm, device=DEV, dtype=dtype)
+    dys = [torch.randn(Bn, Tn, Dm, device=DEV, dtype=dtype) for _ in range(G)]
+
+    x1 = qkv.clone().requires_grad_()
+    outs = grouped(x1, pre_z)
+    torch.autograd.backward(outs, dys)
+    x2 = qkv.clone().requires_grad_()
+    # README.md:99-110: split the fused projection, one module per slice
+    parts = x2.split(Dm, dim=-1)
+    outs2 = [m(p, pre_z) for m, p in zip(singles, parts)]
+    torch.autograd.backward(outs2, dys)
+    for g in range(G):
+        # proj_in differs only by GEMM shape ([*, 3R] vs [*, R]); compare to bf16 tolerance
+        assert_ns(outs[g], outs2[g], dtype, f"g{g} y")
+        assert_ns(grouped.proj_out.grad[g], singles[g].proj_out.grad, dtype, f"g{g} dU", elementwise=False)
+        assert_ns(grouped.proj_out_bias.grad[g], singles[g].proj_out_bias.grad, dtype, f"g{g} dstatic",
+                  elementwise=False)
+        assert_ns(grouped.proj_in.weight.grad[g * R:(g + 1) * R], singles[g].proj_in.weight.grad, dtype,
+                  f"g{g} dW_in", elementwise=False)
+    assert_ns(x1.grad, x2.grad, dtype, "dqkv")
+
+
+def test_readme_module_against_oracle():
+    from dynconv import LowRankDynamicShortConvolution
+
+    torch.manual_seed(1)
+    Dm, R, W, Bn, Tn = 128, 15, 4, 2, 64
+    dtype = torch.bfloat16
+    m = LowRankDynamicShortConvolution(Dm, R, W).to(DEV, dtype)
+    with torch.no_grad():
+        m.proj_out.normal_(0, 1 / math.sqrt((R + 1) * W))
+    x = torch.randn(Bn, Tn, Dm, device=DEV, dtype=dtype, requires_grad=True)
+    pre_z = torch.randn(Bn, Tn, Dm, device=DEV, dtype=dtype)
+    dy = torch.randn(Bn, Tn, Dm, device=DEV, dtype=dtype)
+    y = m(x, pre_z)
+    y.backward(dy)
+    # oracle: the same bf16 z (torch's GEMM), then the fp32 restatement of reference.py
+    z = m.proj_in(pre_z).detach()
+    xr = x.detach().float().cpu().requires_grad_()
+    zr = z.float().cpu().requires_grad_()
+    Ur = m.proj_out.detach().float().cpu().requires_grad_()
+    sr = m.proj_out_bias.detach().float().cpu().requires_grad_()
+    yr = lr_ref(xr, zr, Ur, sr, residual=True)
+    yr.backward(dy.float().cpu())
+    assert_ns(y, yr, dtype, "y")
+    assert_ns(x.grad, xr.grad, dtype, "dx")
+    assert_ns(m.proj_out.grad, Ur.grad, dtype, "dU", elementwise=False)
+    assert_ns(m.proj_out_bias.grad, sr.grad, dtype, "dstatic_w", elementwise=False)
