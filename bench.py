@@ -19,7 +19,12 @@ Also reported:
                sequence: back-to-back launches rotating over enough
                independent input sets that each launch's data is out of the
                256 MB MALL, between one pair of HIP events; plus configs[4]
-               (lowrank QKV, 3 calls) at its own shape;
+               (lowrank QKV) at its own shape, as 3 calls and as one grouped
+               call reading x out of the fused [B, T, 3D] projection;
+  qkv          configs[4] end to end through autograd (forward + backward):
+               the README's pattern (split the fused projection, .contiguous()
+               each slice, three calls; autograd concatenates dq, dk, dv)
+               against the grouped operator;
   roofline     the dominant launch (headwise hs1 backward: hw_bwd_fast +
                reduce_partials) against 8 TB/s, its duration taken with HIP
                events around that backward call inside the timed step loop, on
@@ -53,12 +58,18 @@ CONFIGS = {
     "hw_hs32": dict(kind="hw", B=4, T=4096, D=2048, H=64, W=4, static=True, residual=True),
     "lr_r16": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=4, static=False, residual=True),
 }
-EXTRA = {"lr_qkv": dict(kind="lr", B=2, T=8192, D=4096, R=31, W=4, static=True, residual=True, calls=3)}
+EXTRA = {
+    "lr_qkv": dict(kind="lr", B=2, T=8192, D=4096, R=31, W=4, static=True, residual=True, calls=3),
+    "lr_qkv_grouped": dict(kind="lrg", B=2, T=8192, D=4096, R=31, W=4, static=True, residual=True, G=3),
+}
 STEP = ["hw_hs1", "hw_hs32", "lr_r16"]
 
 
 def alg_bytes(c):
     """Algorithmic bytes (fwd, bwd) of one call: inputs read once, outputs written once."""
+    if c["kind"] == "lrg":
+        f, b = alg_bytes(dict(c, kind="lr"))
+        return c["G"] * f, c["G"] * b
     x = c["B"] * c["T"] * c["D"] * BF16
     sw = c["W"] * c["D"] * BF16 if c["static"] else 0
     if c["kind"] == "hw":
@@ -154,6 +165,25 @@ def abi_sets(c, torch, dev):
     B, T, D, W = c["B"], c["T"], c["D"], c["W"]
     bf = torch.bfloat16
     sets = []
+    if c["kind"] == "lrg":
+        G, R = c["G"], c["R"]
+        rk = R + (1 if c["static"] else 0)
+        for _ in range(n_sets(c)):
+            d = {"x": torch.randn(B, T, G * D, device=dev).to(bf)}
+            d["zs"] = [torch.randn(B, T, R, device=dev).to(bf) for _ in range(G)]
+            d["Us"] = [(torch.randn(R, W * D, device=dev) / math.sqrt(rk * W)).to(bf) for _ in range(G)]
+            d["sws"] = ([((torch.rand(W, D, device=dev) * 2 - 1) / math.sqrt(W)).to(bf) for _ in range(G)]
+                        if c["static"] else None)
+            d["ys"] = [torch.empty(B, T, D, device=dev, dtype=bf) for _ in range(G)]
+            d["dys"] = [torch.randn(B, T, D, device=dev).to(bf) for _ in range(G)]
+            d["dx"] = torch.empty_like(d["x"])
+            d["dzs"] = [torch.empty_like(z) for z in d["zs"]]
+            d["dUs"] = [torch.empty_like(u) for u in d["Us"]]
+            d["dsws"] = [torch.empty_like(s) for s in d["sws"]] if c["static"] else None
+            d["nws"] = lib.dc_lowrank_bwd_grouped_ws_bytes(G, B, T, D, R, W, 0, int(c["static"]))
+            d["ws"] = torch.empty(max(d["nws"], 1), dtype=torch.uint8, device=dev)
+            sets.append(d)
+        return sets
     for _ in range(n_sets(c)):
         d = {"x": torch.randn(B, T, D, device=dev).to(bf), "dy": torch.randn(B, T, D, device=dev).to(bf)}
         d["sw"] = ((torch.rand(W, D, device=dev) * 2 - 1) / math.sqrt(W)).to(bf) if c["static"] else None
@@ -184,6 +214,22 @@ def abi_launchers(c, sets, torch):
     B, T, D, W = c["B"], c["T"], c["D"], c["W"]
     p = _capi.ptr
     res = int(c["residual"])
+    if c["kind"] == "lrg":
+        G, R = c["G"], c["R"]
+        pa = _capi.ptr_array
+
+        def fwd(i):
+            d = sets[i]
+            _capi.check(lib.dc_lowrank_fwd_grouped(G, p(d["x"]), G * D, pa(d["zs"]), pa(d["Us"]), pa(d["sws"]),
+                                                   pa(d["ys"]), B, T, D, R, W, 0, res, st), "grouped fwd")
+
+        def bwd(i):
+            d = sets[i]
+            _capi.check(lib.dc_lowrank_bwd_grouped(G, p(d["x"]), G * D, pa(d["zs"]), pa(d["Us"]), pa(d["sws"]),
+                                                   pa(d["dys"]), p(d["dx"]), G * D, pa(d["dzs"]), pa(d["dUs"]),
+                                                   pa(d["dsws"]), p(d["ws"]), d["nws"], B, T, D, R, W, 0, res, st),
+                        "grouped bwd")
+        return fwd, bwd
     if c["kind"] == "hw":
         H = c["H"]
 
@@ -236,6 +282,50 @@ def calibrate_copy(torch, dev, mib=256, reps=3):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"calibrate_copy_bytes": n, "copies": reps}), flush=True)
+
+
+def qkv_end_to_end(torch, dev, reps=10):
+    """configs[4] through autograd: the README's split / .contiguous() / three calls vs the grouped operator."""
+    from lowrank import lowrank_dynamic_convolution as lr, lowrank_dynamic_convolution_grouped as lrg
+
+    c = EXTRA["lr_qkv_grouped"]
+    B, T, D, R, W, G = c["B"], c["T"], c["D"], c["R"], c["W"], c["G"]
+    bf = torch.bfloat16
+    qkv = torch.randn(B, T, G * D, device=dev).to(bf).requires_grad_()
+    zs = [torch.randn(B, T, R, device=dev).to(bf).requires_grad_() for _ in range(G)]
+    Us = [(torch.randn(R, W * D, device=dev) / math.sqrt((R + 1) * W)).to(bf).requires_grad_() for _ in range(G)]
+    sws = [((torch.rand(W, D, device=dev) * 2 - 1) / math.sqrt(W)).to(bf).requires_grad_() for _ in range(G)]
+    dys = [torch.randn(B, T, D, device=dev).to(bf) for _ in range(G)]
+
+    def readme():
+        outs = [lr(part.contiguous(), zs[g], Us[g], sws[g], residual=True)
+                for g, part in enumerate(qkv.split(D, dim=-1))]
+        torch.autograd.backward(outs, dys)
+
+    def grouped():
+        torch.autograd.backward(lrg(qkv, zs, Us, sws, residual=True), dys)
+
+    out = {}
+    for name, fn in (("readme_split_contiguous_3_calls", readme), ("grouped", grouped)):
+        for t in [qkv] + zs + Us + sws:
+            t.grad = None
+        fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            for t in [qkv] + zs + Us + sws:
+                t.grad = None
+            fn()
+        e.record()
+        e.synchronize()
+        out[name + "_us"] = round(s.elapsed_time(e) * 1e3 / reps, 1)
+    fb, bb = alg_bytes(c)
+    out["alg_MB"] = round((fb + bb) / 1e6, 1)
+    out["speedup"] = round(out["readme_split_contiguous_3_calls_us"] / out["grouped_us"], 3)
+    print(f"[bench] qkv end to end (fwd+bwd, autograd): README pattern {out['readme_split_contiguous_3_calls_us']} us, "
+          f"grouped {out['grouped_us']} us ({out['speedup']}x)", file=sys.stderr, flush=True)
+    return out
 
 
 def main():
@@ -357,6 +447,9 @@ def main():
         del sets, fwd, bwd
         torch.cuda.empty_cache()
 
+    qkv = None if args.no_extra else qkv_end_to_end(torch, dev)
+    torch.cuda.empty_cache()
+
     out = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -379,6 +472,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(torch),
         "breakdown": breakdown,
+        "qkv": qkv,
     }
     print(json.dumps(out), flush=True)
 
