@@ -25,12 +25,15 @@ namespace dc {
 //     rows 4q..4q+3+W-1 come from NB = ceil((W+3)/4) MFMA row blocks (A rows
 //     shifted by 4), so every lane has the look-ahead rows it needs without
 //     cross-lane traffic; dy rows 4q..4q+W+2 are read from L1.
-// A workgroup is 4 wavefronts on 4 adjacent 64-channel chunks of the same
-// rows.  dz partial sums over the 256 channels are added in LDS in wave
-// order, once per batch of tiles, and written as one fp32 partial per
+// A workgroup is NRW row runs x 4 wavefronts on 4 adjacent 64-channel chunks
+// of the same rows.  dz partial sums over the 256 channels are added in LDS in
+// wave order, once per batch of tiles, and written as one fp32 partial per
 // 256-channel group; dU accumulates in registers over the wavefront's run of
-// tiles and is written as one fp32 partial per run.  reduce_partials sums
-// both deterministically.
+// tiles, the NRW runs of a chunk are added in LDS at the end (run order), and
+// one fp32 partial per workgroup is written.  reduce_partials sums both
+// deterministically.  NRW = 2 (8 wavefronts, 2 per SIMD at 255 VGPRs) halves
+// the dU partials that are written and read back; it needs one rank chunk and
+// W <= 4 (registers for the tap operands, LDS for the run exchange).
 //
 // Groups: up to kMaxGroups independent problems of one shape share a launch
 // (block index -> group); x and dx may have row strides xld, dxld > D, so the
@@ -55,8 +58,9 @@ struct LrBwdArgs {
   int seg;    // tiles per run
   int nspb;   // runs per sequence
   int nseg;   // B * nspb
-  int nblk;   // ncg * nseg * groups
-  int nblk1;  // ncg * nseg: blocks per group
+  int npair;  // ceil(nseg / NRW) workgroup rows: one dU partial each
+  int nblk;   // ncg * npair * groups
+  int nblk1;  // ncg * npair: blocks per group
   int xld;    // row stride of x (elements)
   int dxld;   // row stride of dx (elements)
   int zvec;   // R % 4 == 0 and z 8-byte aligned: 8-byte z loads
@@ -116,26 +120,29 @@ __device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds, u32x2 (&u
   }
 }
 
-template <typename T, int W, int RC, bool ZV>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && RC == 1 ? 2 : 1, 8))) void lr_bwd_mfma(
-    LrBwdArgs a) {
+template <typename T, int W, int RC, bool ZV, int NRW>
+__global__ __launch_bounds__(256 * NRW) __attribute__((amdgpu_waves_per_eu(W <= 4 && RC == 1 ? 2 : 1, 8))) void
+lr_bwd_mfma(LrBwdArgs a) {
+  constexpr int NW = 4 * NRW;      // wavefronts per workgroup
+  static_assert(NRW == 1 || (RC == 1 && W <= 4), "two runs per workgroup: one rank chunk, W <= 4");
   constexpr int NB = (W + 6) / 4;  // MFMA row blocks for the dx look-ahead
   constexpr int NR = W + 3;        // x rows 4q-W+1 .. 4q+3 and dy rows 4q .. 4q+W+2 per lane
   constexpr bool UWREG = W * RC <= 8;   // tap-weight operands in registers
   constexpr int NUW = W * RC * 4;  // packed tap-weight operands per lane
   constexpr int NUZ = W * RC * 2;  // dz operands per lane
   constexpr int GROW = 72;         // G tile row pitch (64 channels + 8 pad: conflict-free reads)
-  __shared__ u32x2 uw_lds[4][UWREG ? 1 : NUW * 64];
-  __shared__ u32x4 uz_lds[4][NUZ * 64];
-  __shared__ __attribute__((aligned(16))) uint16_t gtile[4][16 * GROW];
+  __shared__ u32x2 uw_lds[NW][UWREG ? 1 : NUW * 64];
+  __shared__ u32x4 uz_lds[NW][NUZ * 64];
+  __shared__ __attribute__((aligned(16))) uint16_t gtile[NW][16 * GROW];
   // dz partial sums of the workgroup's 4 chunks, gathered for DZB tiles and
   // reduced once per batch (double-buffered: one barrier per batch).  Two
   // rank chunks batch too once registers already hold occupancy at one
   // wavefront per SIMD (W >= 2); at W = 1 the smaller LDS keeps two.
   constexpr int DZB = (UWREG && (RC == 1 || (RC == 2 && W >= 2))) ? 4 : 1;
-  __shared__ float dzred[2][4][DZB][RC * 256];
+  __shared__ float dzred[2][NRW][4][DZB][RC * 256];
 
   const int lane = threadIdx.x & 63, wave = wave_id();
+  const int cw = wave & 3, rw = wave >> 2;  // chunk and run of this wavefront in the workgroup
   const int q = lane >> 4, n = lane & 15;
   const int lb0 = xcd_remap(blockIdx.x, a.nblk);
   const int g = __builtin_amdgcn_readfirstlane(lb0 / a.nblk1);
@@ -148,18 +155,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
   uint16_t* __restrict__ dx = reinterpret_cast<uint16_t*>(pick(a.grp, g, &LrBwdGroup::dx));
   float* __restrict__ part_dz = pick(a.grp, g, &LrBwdGroup::part_dz);
   float* __restrict__ part_du = pick(a.grp, g, &LrBwdGroup::part_du);
-  const int cg = lb % a.ncg, sg = lb / a.ncg;
-  const int chunk = cg * 4 + wave;
+  const int cg = lb % a.ncg, sp = lb / a.ncg;
+  const int chunk = cg * 4 + cw;
   const int D = a.D, Tn = a.Tn;
   const int d0 = chunk * 64;
   const bool chv = d0 + 4 * n < D;  // lane quartet inside D (D % 16 == 0)
   const int col = d0 + 4 * n;
   const int64_t WD = (int64_t)W * D;
-  const int b = sg / a.nspb;
   const int ntile = (Tn + 15) >> 4;
-  const int tile0 = (sg - b * a.nspb) * a.seg;
-  const int tile1 = min(tile0 + a.seg, ntile);
-  const int64_t row0 = (int64_t)b * Tn;
+  // Run s of the grid: tiles [tile0, tile1) of sequence b.  A workgroup's last
+  // run can lie past nseg (odd nseg): it has no tiles.
+  struct Run {
+    int tile0, tile1;
+    int64_t row0;
+  };
+  auto run_of = [&](int s) {
+    Run r{0, 0, 0};
+    if (s < a.nseg) {
+      const int b = s / a.nspb;
+      r.tile0 = (s - b * a.nspb) * a.seg;
+      r.tile1 = min(r.tile0 + a.seg, ntile);
+      r.row0 = (int64_t)b * Tn;
+    }
+    return r;
+  };
+  Run runs[NRW];
+  int nit = 0;  // iterations of every wavefront: the longest run of the workgroup
+#pragma unroll
+  for (int i = 0; i < NRW; ++i) {
+    runs[i] = run_of(sp * NRW + i);
+    nit = max(nit, runs[i].tile1 - runs[i].tile0);
+  }
+  const Run me = rw == 0 ? runs[0] : runs[NRW - 1];
+  const int tile0 = me.tile0, tile1 = me.tile1;
+  const int64_t row0 = me.row0;
   const int R = a.R, RK = a.RK;
   typedef ZRaw<T, RC, ZV> ZR;
   u32x2* __restrict__ my_uw = uw_lds[wave];
@@ -218,9 +247,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb) in.zr[bb].load(rz, live ? (tile * 16 + 4 * bb + n) * R * 2 : kOobTile, R, q);
   };
-  auto compute_tile = [&](int tile, const TileIn& in) {
+  auto compute_tile = [&](int it, const TileIn& in) {
+    const int tile = tile0 + it;
+    const bool live = tile < tile1;
     const int t0 = tile * 16;
-    const int dxtoff = t0 * dxrowb;
+    const int dxtoff = live ? t0 * dxrowb : kOobTile;  // tiles past the run store nothing
     const u32x2(&xr)[NR] = in.xr;
     const u32x2(&dyr)[NR] = in.dyr;
     u32x2 zA[NB][RC];
@@ -312,41 +343,72 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
       o[1] = pack2<T>(v[2], v[3]);
       bstore64<true>(o, rdx, dxlane_off + dxtoff + i * dxrowb);
     }
-    // ---- dz: gather this wavefront's tile sums; every DZB tiles (and at the end of
-    // the run) add the 4 chunk wavefronts in wave order, one partial per group.
-    const int slot = (tile - tile0) % DZB;
-    const int buf = ((tile - tile0) / DZB) & 1;
+    // ---- dz: gather this wavefront's tile sums; every DZB iterations (and at the
+    // last one) add each run's 4 chunk wavefronts in wave order, one partial per group.
+    const int slot = it % DZB;
+    const int buf = (it / DZB) & 1;
 #pragma unroll
     for (int c = 0; c < RC; ++c)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dzred[buf][wave][slot][c * 256 + (4 * q + i) * 16 + n] = dz[c][i];
-    if (slot == DZB - 1 || tile == tile1 - 1) {
+      for (int i = 0; i < 4; ++i) dzred[buf][rw][cw][slot][c * 256 + (4 * q + i) * 16 + n] = dz[c][i];
+    if (slot == DZB - 1 || it == nit - 1) {
       __syncthreads();
-      const int tb = t0 - slot * 16;  // first row of the batch
-      for (int e = threadIdx.x; e < (slot + 1) * RC * 256; e += 256) {
-        const int sl = e / (RC * 256), rem = e - sl * (RC * 256);
+      constexpr int PER_RUN = RC * 256;
+      const int per_batch = (slot + 1) * PER_RUN;
+      for (int e = threadIdx.x; e < NRW * per_batch; e += 256 * NRW) {
+        const int ri = e / per_batch, e2 = e - ri * per_batch;
+        const int sl = e2 / PER_RUN, rem = e2 - sl * PER_RUN;
         const int c = rem >> 8, rr = (rem >> 4) & 15, nn = rem & 15;
         const int r = 16 * c + nn;
-        const int t = tb + sl * 16 + rr;
-        const float v = ((dzred[buf][0][sl][rem] + dzred[buf][1][sl][rem]) + dzred[buf][2][sl][rem]) +
-                        dzred[buf][3][sl][rem];
-        if (r < R && t < Tn) part_dz[((int64_t)cg * a.BT + row0 + t) * R + r] = v;
+        const Run& ru = ri == 0 ? runs[0] : runs[NRW - 1];
+        const int ti = ru.tile0 + it - slot + sl;  // the slot's tile of run ri
+        const int t = ti * 16 + rr;
+        const float v = ((dzred[buf][ri][0][sl][rem] + dzred[buf][ri][1][sl][rem]) + dzred[buf][ri][2][sl][rem]) +
+                        dzred[buf][ri][3][sl][rem];
+        if (ti < ru.tile1 && r < R && t < Tn) part_dz[((int64_t)cg * a.BT + ru.row0 + t) * R + r] = v;
       }
     }
   };
 
+  // Every wavefront of the workgroup runs nit iterations (the barriers of the
+  // dz batches are shared); tiles past its own run load and store nothing.
   TileIn ta, tb;
   load_tile(tile0, ta);
-  for (int tile = tile0; tile < tile1; tile += 2) {
-    load_tile(tile + 1, tb);
+  for (int it = 0; it < nit; it += 2) {
+    load_tile(tile0 + it + 1, tb);
     __builtin_amdgcn_sched_barrier(0);  // issue the next tile's loads before this tile's waits
-    compute_tile(tile, ta);
-    load_tile(tile + 2, ta);
+    compute_tile(it, ta);
+    load_tile(tile0 + it + 2, ta);
     __builtin_amdgcn_sched_barrier(0);
-    if (tile + 1 < tile1) compute_tile(tile + 1, tb);
+    if (it + 1 < nit) compute_tile(it + 1, tb);
   }
 
-  // ---- dU partial of this run: rows r < RK of U_eff, the wavefront's 64 columns per tap
+  if constexpr (NRW == 2) {
+    // The second run's wavefronts hand their dU sums to the first run's
+    // wavefronts of the same chunk through LDS (the dz buffers, now free).
+    float* xch = &dzred[0][0][0][0][0];
+    constexpr int NDU = W * RC * 4 * 4;  // dU floats per lane
+    static_assert(4 * NDU * 64 <= 2 * NRW * 4 * DZB * RC * 256, "dU exchange fits the dz buffers");
+    __syncthreads();
+    if (rw == 1) {
+#pragma unroll
+      for (int k = 0; k < W; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xch[((cw * W + k) * 16 + j * 4 + i) * 64 + lane] = du[k][0][j][i];
+    }
+    __syncthreads();
+    if (rw == 1) return;
+#pragma unroll
+    for (int k = 0; k < W; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) du[k][0][j][i] += xch[((cw * W + k) * 16 + j * 4 + i) * 64 + lane];
+  }
+
+  // ---- dU partial of this workgroup row: rows r < RK of U_eff, the wavefront's 64 columns per tap
 #pragma unroll
   for (int k = 0; k < W; ++k)
 #pragma unroll
@@ -356,7 +418,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W <= 4 && R
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = 16 * c + 4 * q + i;
-          if (r < RK && chv) part_du[((int64_t)sg * RK + r) * WD + (int64_t)k * D + col + j] = du[k][c][j][i];
+          if (r < RK && chv) part_du[((int64_t)sp * RK + r) * WD + (int64_t)k * D + col + j] = du[k][c][j][i];
         }
 }
 
@@ -379,7 +441,11 @@ LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   a.seg = (int)seg;
   a.nspb = (int)((ntile + seg - 1) / seg);
   a.nseg = (int)(p.B * a.nspb);
-  a.nblk = a.nseg * a.ncg;
+  // row runs per workgroup: two when one rank chunk and W <= 4 (see the kernel)
+  const int64_t rc = (p.R + (p.static_w ? 1 : 0) + 15) / 16;
+  const int nrw = (rc == 1 && p.W <= 4) ? 2 : 1;
+  a.npair = (a.nseg + nrw - 1) / nrw;
+  a.nblk = a.npair * a.ncg;
   a.BT = p.B * p.T;
   a.zvec = p.R % 4 == 0 && aligned_to(p.z, 8);
   return a;
@@ -387,7 +453,7 @@ LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
 
 constexpr int kBwdTargetWaves = 2048;
 
-// Workspace: [dz partials: ncg x BT x R fp32][dU partials: nseg x RK x W*D fp32], 256-byte aligned.
+// Workspace: [dz partials: ncg x BT x R fp32][dU partials: npair x RK x W*D fp32], 256-byte aligned.
 struct BwdWs {
   int64_t dz_off, du_off, total;
 };
@@ -396,12 +462,13 @@ BwdWs bwd_ws(const LrProblem& p, const LrBwdArgs& a) {
   const int64_t dz = (int64_t)a.ncg * a.BT * a.R * 4;
   w.dz_off = 0;
   w.du_off = (dz + 255) / 256 * 256;
-  w.total = w.du_off + (int64_t)a.nseg * a.RK * p.W * p.D * 4;
+  w.total = w.du_off + (int64_t)a.npair * a.RK * p.W * p.D * 4;
   return w;
 }
 
 template <typename T, int W, int RC>
 hipError_t launch_bwd(const LrProblem* p, int G) {
+  constexpr int NRW = (RC == 1 && W <= 4) ? 2 : 1;  // matches make_bwd_args
   LrBwdArgs a = make_bwd_args(p[0], kBwdTargetWaves);
   const BwdWs w = bwd_ws(p[0], a);
   a.nblk1 = a.nblk;
@@ -415,9 +482,9 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
     a.zvec = a.zvec && aligned_to(p[g].z, 8);
   }
   if (a.zvec)
-    lr_bwd_mfma<T, W, RC, true><<<a.nblk, 256, 0, p[0].stream>>>(a);
+    lr_bwd_mfma<T, W, RC, true, NRW><<<a.nblk, 256 * NRW, 0, p[0].stream>>>(a);
   else
-    lr_bwd_mfma<T, W, RC, false><<<a.nblk, 256, 0, p[0].stream>>>(a);
+    lr_bwd_mfma<T, W, RC, false, NRW><<<a.nblk, 256 * NRW, 0, p[0].stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t WD = p[0].W * p[0].D, RKWD = (int64_t)a.RK * WD, R = p[0].R;
@@ -426,8 +493,8 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
   for (int g = 0; g < G; ++g) {
     const float* pdz = a.grp[g].part_dz;
     const float* pdu = a.grp[g].part_du;
-    jobs[nj++] = {pdu, RKWD, a.nseg, R * WD, p[g].dU};
-    jobs[nj++] = {pdu + R * WD, RKWD, a.nseg, p[g].static_w ? WD : 0, p[g].dstatic_w};
+    jobs[nj++] = {pdu, RKWD, a.npair, R * WD, p[g].dU};
+    jobs[nj++] = {pdu + R * WD, RKWD, a.npair, p[g].static_w ? WD : 0, p[g].dstatic_w};
     jobs[nj++] = {pdz, a.BT * R, a.ncg, a.BT * R, p[g].dz};
   }
   return reduce_partials_multi(jobs, nj, p[0].dtype, p[0].stream);
