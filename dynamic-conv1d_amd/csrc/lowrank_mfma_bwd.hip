@@ -8,13 +8,14 @@ namespace dc {
 // One pass over x and dy produces dx, dz, dU and dstatic_w (reference:
 // lowrank.py:87-140 and 159-205, two kernels that both read dy).
 //
-// Tile: a wavefront owns 16 rows x 64 channels; lane l = 16q + n owns rows
-// 4q..4q+3 and the channel quartet 4n..4n+3 (64-bit loads, 128 contiguous
-// bytes per row across the 16 lanes of a row group).  With
+// Tile: a wavefront owns 16 rows x CPW channels (CPW = 64, or 32 for two rank
+// chunks); lane l = 16q + n owns rows 4q..4q+3 and the NJ = CPW/16 channels
+// NJ*n .. NJ*n+NJ-1 (one 8- or 4-byte load per row, 128 or 64 contiguous bytes
+// per row across the 16 lanes of a row group).  With
 // G_k[t, d] = bf16(dy[t, d] * x[t-k, d]) (the reference also rounds this
 // product to bf16 before its dot products, lowrank.py:128):
 //   * dU[r, kD+d] += sum_t z_eff[t, r] G_k[t, d]: MFMA with K = the 16 rows.
-//     For each j the lane's four G values of column 4n+j are exactly the
+//     For each j the lane's four G values of column NJ*n+j are exactly the
 //     B operand (rows 4q..4q+3 of column n); A is z_eff transposed.
 //   * dz[t, r] += sum_d G_k[t, d] U_eff[r, kD+d]: needs K = channels.  The
 //     same packed G registers fed as the *A* operand of an MFMA against the
@@ -25,15 +26,18 @@ namespace dc {
 //     rows 4q..4q+3+W-1 come from NB = ceil((W+3)/4) MFMA row blocks (A rows
 //     shifted by 4), so every lane has the look-ahead rows it needs without
 //     cross-lane traffic; dy rows 4q..4q+W+2 are read from L1.
-// A workgroup is NRW row runs x 4 wavefronts on 4 adjacent 64-channel chunks
-// of the same rows.  dz partial sums over the 256 channels are added in LDS in
-// wave order, once per batch of tiles, and written as one fp32 partial per
-// 256-channel group; dU accumulates in registers over the wavefront's run of
+// A workgroup is NRW row runs x NCW = 256/CPW wavefronts on NCW adjacent
+// channel chunks of the same rows.  dz partial sums over the 256 channels are
+// added in LDS in wave order, once per batch of tiles, and written as one fp32
+// partial per 256-channel group; dU accumulates in registers over the wavefront's run of
 // tiles, the NRW runs of a chunk are added in LDS at the end (run order), and
 // one fp32 partial per workgroup is written.  reduce_partials sums both
 // deterministically.  NRW = 2 (8 wavefronts, 2 per SIMD at 255 VGPRs) halves
 // the dU partials that are written and read back; it needs one rank chunk and
-// W <= 4 (registers for the tap operands, LDS for the run exchange).
+// W <= 4 (registers for the tap operands, LDS for the run exchange).  Two rank
+// chunks use CPW = 32: the dU accumulators (RC x W x NJ MFMA tiles) then fit
+// two wavefronts per SIMD where 64-channel tiles allowed one, and with the
+// same wavefront count the runs are twice as long (half the dU partials).
 //
 // Groups: up to kMaxGroups independent problems of one shape share a launch
 // (block index -> group); x and dx may have row strides xld, dxld > D, so the
@@ -53,8 +57,8 @@ struct LrBwdGroup {
 
 struct LrBwdArgs {
   int Tn, D, R, RK, residual;
-  int nch;    // ceil(D / 64) channel chunks
-  int ncg;    // ceil(nch / 4) chunk groups: one workgroup column
+  int nch;    // ceil(D / CPW) channel chunks
+  int ncg;    // ceil(nch / NCW) chunk groups of 256 channels: one workgroup column
   int seg;    // tiles per run
   int nspb;   // runs per sequence
   int nseg;   // B * nspb
@@ -69,68 +73,99 @@ struct LrBwdArgs {
 };
 
 
-// U_eff operands of one wavefront's 64-channel chunk, staged once per run (the
+// NJ (4 or 2) 16-bit channels of one row held by a lane: one 8- or 4-byte unit.
+template <int NJ> struct LaneVec;
+template <> struct LaneVec<4> {
+  typedef u32x2 type;
+  __device__ static __forceinline__ type load(rsrc_t r, int off) { return bload64(r, off); }
+  __device__ static __forceinline__ void store(type v, rsrc_t r, int off) { bstore64<true>(v, r, off); }
+  __device__ static __forceinline__ uint32_t elem(const type& v, int j) { return elem16x2(v, j); }
+  template <typename T>
+  __device__ static __forceinline__ type pack(const float* f) {
+    return type{pack2<T>(f[0], f[1]), pack2<T>(f[2], f[3])};
+  }
+};
+template <> struct LaneVec<2> {
+  typedef uint32_t type;
+  __device__ static __forceinline__ type load(rsrc_t r, int off) { return bload32(r, off); }
+  __device__ static __forceinline__ void store(type v, rsrc_t r, int off) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kNt);
+  }
+  __device__ static __forceinline__ uint32_t elem(const type& v, int j) { return j ? (v >> 16) : (v & 0xFFFFu); }
+  template <typename T>
+  __device__ static __forceinline__ type pack(const float* f) {
+    return pack2<T>(f[0], f[1]);
+  }
+};
+
+// U_eff operands of one wavefront's CPW-channel chunk, staged once per run (the
 // chunk never changes across it): the dz operands always in LDS, the tap-weight
 // operands in registers when W*RC <= 8 (UWREG) and in LDS otherwise.  For tap k
 // and rank chunk c, lane (q, n) reads
-//   uw[j] (j = 0..3): ranks 16c+4q..16c+4q+3 of channel 4n+j, packed (B operand
-//                     of the 16x16x16 tap-weight MFMA);
-//   uz[s] (s = 0, 1): rank 16c+n, channels 32s+8q..32s+8q+7 as they lie in U
-//                     (B operand of the 16x16x32 dz MFMA).
-template <int W, int RC, bool UWREG>
-__device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds, u32x2 (&uw_reg)[UWREG ? W * RC * 4 : 1],
+//   uw[j] (j < NJ): ranks 16c+4q..16c+4q+3 of channel NJ*n+j, packed (B operand
+//                   of the 16x16x16 tap-weight MFMA);
+//   uz[s] (s < NS = CPW/32): rank 16c+n, channels 32s+8q..32s+8q+7 as they lie
+//                   in U (B operand of the 16x16x32 dz MFMA).
+template <int W, int RC, bool UWREG, int NJ, int NS>
+__device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds, u32x2 (&uw_reg)[UWREG ? W * RC * NJ : 1],
                                            u32x4* __restrict__ uz_lds, const uint16_t* __restrict__ U,
                                            const uint16_t* __restrict__ sw, int R, int RK, int D, int d0, int q,
                                            int n, int lane) {
+  typedef LaneVec<NJ> LV;
   const int64_t WD = (int64_t)W * D;
-  const bool chv = d0 + 4 * n < D;
+  const bool chv = d0 + NJ * n < D;
 #pragma unroll
   for (int k = 0; k < W; ++k) {
 #pragma unroll
     for (int c = 0; c < RC; ++c) {
-      u32x2 rows[4];
+      typename LV::type rows[4];
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const int r = 16 * c + 4 * q + kk;
         const uint16_t* src = nullptr;
-        if (chv && r < R) src = U + (int64_t)r * WD + (int64_t)k * D + d0 + 4 * n;
-        else if (chv && r < RK) src = sw + (int64_t)k * D + d0 + 4 * n;
-        rows[kk] = src ? *reinterpret_cast<const u32x2*>(src) : u32x2{0u, 0u};
+        if (chv && r < R) src = U + (int64_t)r * WD + (int64_t)k * D + d0 + NJ * n;
+        else if (chv && r < RK) src = sw + (int64_t)k * D + d0 + NJ * n;
+        rows[kk] = src ? *reinterpret_cast<const typename LV::type*>(src) : typename LV::type{};
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         u32x2 uw;
-        uw[0] = elem16x2(rows[0], j) | (elem16x2(rows[1], j) << 16);
-        uw[1] = elem16x2(rows[2], j) | (elem16x2(rows[3], j) << 16);
+        uw[0] = LV::elem(rows[0], j) | (LV::elem(rows[1], j) << 16);
+        uw[1] = LV::elem(rows[2], j) | (LV::elem(rows[3], j) << 16);
         if constexpr (UWREG)
-          uw_reg[(k * RC + c) * 4 + j] = uw;
+          uw_reg[(k * RC + c) * NJ + j] = uw;
         else
-          uw_lds[((k * RC + c) * 4 + j) * 64 + lane] = uw;
+          uw_lds[((k * RC + c) * NJ + j) * 64 + lane] = uw;
       }
       const int r = 16 * c + n;
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
+      for (int s2 = 0; s2 < NS; ++s2) {
         const int dd = d0 + 32 * s2 + 8 * q;  // multiple of 8; D % 16 == 0, so dd < D means dd + 8 <= D
         const uint16_t* src = nullptr;
         if (dd < D && r < R) src = U + (int64_t)r * WD + (int64_t)k * D + dd;
         else if (dd < D && r < RK) src = sw + (int64_t)k * D + dd;
-        uz_lds[((k * RC + c) * 2 + s2) * 64 + lane] = src ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
+        uz_lds[((k * RC + c) * NS + s2) * 64 + lane] = src ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
       }
     }
   }
 }
 
-template <typename T, int W, int RC, bool ZV, int NRW>
-__global__ __launch_bounds__(256 * NRW) __attribute__((amdgpu_waves_per_eu(W <= 4 && RC == 1 ? 2 : 1, 8))) void
-lr_bwd_mfma(LrBwdArgs a) {
-  constexpr int NW = 4 * NRW;      // wavefronts per workgroup
-  static_assert(NRW == 1 || (RC == 1 && W <= 4), "two runs per workgroup: one rank chunk, W <= 4");
+template <typename T, int W, int RC, bool ZV, int NRW, int CPW>
+__global__ __launch_bounds__(64 * (256 / CPW) * NRW)
+__attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))) void lr_bwd_mfma(LrBwdArgs a) {
+  constexpr int NJ = CPW / 16;     // channels per lane
+  constexpr int NS = CPW / 32;     // 32-channel K blocks of the dz MFMA
+  constexpr int NCW = 256 / CPW;   // channel-chunk wavefronts per run: 256 channels per workgroup
+  constexpr int NW = NCW * NRW;    // wavefronts per workgroup
+  static_assert(CPW == 64 || CPW == 32, "64- or 32-channel tiles");
+  static_assert(NRW == 1 || (RC == 1 && W <= 4 && CPW == 64), "two runs per workgroup: one rank chunk, W <= 4");
+  typedef LaneVec<NJ> LV;
   constexpr int NB = (W + 6) / 4;  // MFMA row blocks for the dx look-ahead
   constexpr int NR = W + 3;        // x rows 4q-W+1 .. 4q+3 and dy rows 4q .. 4q+W+2 per lane
   constexpr bool UWREG = W * RC <= 8;   // tap-weight operands in registers
-  constexpr int NUW = W * RC * 4;  // packed tap-weight operands per lane
-  constexpr int NUZ = W * RC * 2;  // dz operands per lane
-  constexpr int GROW = 72;         // G tile row pitch (64 channels + 8 pad: conflict-free reads)
+  constexpr int NUW = W * RC * NJ;  // packed tap-weight operands per lane
+  constexpr int NUZ = W * RC * NS;  // dz operands per lane
+  constexpr int GROW = CPW + 8;     // G tile row pitch (CPW channels + 8 pad: conflict-free reads)
   __shared__ u32x2 uw_lds[NW][UWREG ? 1 : NUW * 64];
   __shared__ u32x4 uz_lds[NW][NUZ * 64];
   __shared__ __attribute__((aligned(16))) uint16_t gtile[NW][16 * GROW];
@@ -138,11 +173,11 @@ lr_bwd_mfma(LrBwdArgs a) {
   // reduced once per batch (double-buffered: one barrier per batch).  Two
   // rank chunks batch too once registers already hold occupancy at one
   // wavefront per SIMD (W >= 2); at W = 1 the smaller LDS keeps two.
-  constexpr int DZB = (UWREG && (RC == 1 || (RC == 2 && W >= 2))) ? 4 : 1;
-  __shared__ float dzred[2][NRW][4][DZB][RC * 256];
+  constexpr int DZB = !UWREG ? 1 : RC == 1 ? 4 : (RC == 2 && W >= 2) ? (CPW == 32 ? 2 : 4) : 1;
+  __shared__ float dzred[2][NRW][NCW][DZB][RC * 256];
 
   const int lane = threadIdx.x & 63, wave = wave_id();
-  const int cw = wave & 3, rw = wave >> 2;  // chunk and run of this wavefront in the workgroup
+  const int cw = wave % NCW, rw = wave / NCW;  // chunk and run of this wavefront in the workgroup
   const int q = lane >> 4, n = lane & 15;
   const int lb0 = xcd_remap(blockIdx.x, a.nblk);
   const int g = __builtin_amdgcn_readfirstlane(lb0 / a.nblk1);
@@ -156,11 +191,11 @@ lr_bwd_mfma(LrBwdArgs a) {
   float* __restrict__ part_dz = pick(a.grp, g, &LrBwdGroup::part_dz);
   float* __restrict__ part_du = pick(a.grp, g, &LrBwdGroup::part_du);
   const int cg = lb % a.ncg, sp = lb / a.ncg;
-  const int chunk = cg * 4 + cw;
+  const int chunk = cg * NCW + cw;
   const int D = a.D, Tn = a.Tn;
-  const int d0 = chunk * 64;
-  const bool chv = d0 + 4 * n < D;  // lane quartet inside D (D % 16 == 0)
-  const int col = d0 + 4 * n;
+  const int d0 = chunk * CPW;
+  const int col = d0 + NJ * n;
+  const bool chv = col < D;  // the lane's channels inside D (D % 16 == 0)
   const int64_t WD = (int64_t)W * D;
   const int ntile = (Tn + 15) >> 4;
   // Run s of the grid: tiles [tile0, tile1) of sequence b.  A workgroup's last
@@ -199,13 +234,13 @@ lr_bwd_mfma(LrBwdArgs a) {
   const rsrc_t rdy = make_rsrc(dy + row0 * D, (int64_t)Tn * rowb);
   const rsrc_t rdx = make_rsrc(dx + row0 * a.dxld, (int64_t)Tn * dxrowb);
   const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 2);
-  // byte offsets of the lane's row 4q quartet in dy, x and dx
+  // byte offsets of the lane's row-4q channels in dy, x and dx
   const int lane_off = chv ? (4 * q * D + col) * 2 : kOobLane;
   const int xlane_off = chv ? (4 * q * a.xld + col) * 2 : kOobLane;
   const int dxlane_off = chv ? (4 * q * a.dxld + col) * 2 : kOobLane;
 
   u32x2 uw_reg[UWREG ? NUW : 1];
-  stage_uops<W, RC, UWREG>(my_uw, uw_reg, my_uz, U, sw, R, RK, D, d0, q, n, lane);
+  stage_uops<W, RC, UWREG, NJ, NS>(my_uw, uw_reg, my_uz, U, sw, R, RK, D, d0, q, n, lane);
 
   // Identity as the B operand: lane (q, n) gives rows 4q..4q+3 of column n.
   u32x2 ident;
@@ -218,13 +253,13 @@ lr_bwd_mfma(LrBwdArgs a) {
     ident[1] = e[2] | (e[3] << 16);
   }
 
-  f32x4 du[W][RC][4];
+  f32x4 du[W][RC][NJ];
 #pragma unroll
   for (int k = 0; k < W; ++k)
 #pragma unroll
     for (int c = 0; c < RC; ++c)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) du[k][c][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < NJ; ++j) du[k][c][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Tile inputs (buffer loads: out-of-range rows / channels read as 0).  Two
   // buffers, A and B, alternate: while one tile is computed the next one's
@@ -232,7 +267,7 @@ lr_bwd_mfma(LrBwdArgs a) {
   // reads the out-of-range offset kOobTile: 0, no memory traffic) and no
   // register is copied, so the compiler's waits stay partial (vmcnt(N)).
   struct TileIn {
-    u32x2 xr[NR], dyr[NR];
+    typename LV::type xr[NR], dyr[NR];
     ZR zr[NB];  // z_eff rows t0+4bb+n, ranks 16c+4q..+3: A operand of the tap-weight MFMA
   };
   auto load_tile = [&](int tile, TileIn& in) {
@@ -241,8 +276,8 @@ lr_bwd_mfma(LrBwdArgs a) {
     const int toff = live ? tile * 16 * rowb : kOobTile;
 #pragma unroll
     for (int m = 0; m < NR; ++m) {
-      in.xr[m] = bload64(rx, xlane_off + xtoff + (m - (W - 1)) * xrowb);
-      in.dyr[m] = bload64(rdy, lane_off + toff + m * rowb);
+      in.xr[m] = LV::load(rx, xlane_off + xtoff + (m - (W - 1)) * xrowb);
+      in.dyr[m] = LV::load(rdy, lane_off + toff + m * rowb);
     }
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb) in.zr[bb].load(rz, live ? (tile * 16 + 4 * bb + n) * R * 2 : kOobTile, R, q);
@@ -252,8 +287,8 @@ lr_bwd_mfma(LrBwdArgs a) {
     const bool live = tile < tile1;
     const int t0 = tile * 16;
     const int dxtoff = live ? t0 * dxrowb : kOobTile;  // tiles past the run store nothing
-    const u32x2(&xr)[NR] = in.xr;
-    const u32x2(&dyr)[NR] = in.dyr;
+    const typename LV::type(&xr)[NR] = in.xr;
+    const typename LV::type(&dyr)[NR] = in.dyr;
     u32x2 zA[NB][RC];
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb) in.zr[bb].finish(zA[bb], t0 + 4 * bb + n, R, RK, Tn, q);
@@ -267,40 +302,36 @@ lr_bwd_mfma(LrBwdArgs a) {
       zT[c][1] = pack2<T>(tz[2], tz[3]);
     }
 
-    float dyf[NR][4];
+    float dyf[NR][NJ];
 #pragma unroll
     for (int m = 0; m < NR; ++m)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) dyf[m][j] = q4f<T>(dyr[m], j);
+      for (int j = 0; j < NJ; ++j) dyf[m][j] = Mma16<T>::to_f(LV::elem(dyr[m], j));
 
-    float dxa[4][4];
+    float dxa[4][NJ];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) dxa[i][j] = 0.f;
+      for (int j = 0; j < NJ; ++j) dxa[i][j] = 0.f;
     f32x4 dz[RC];
 #pragma unroll
     for (int c = 0; c < RC; ++c) dz[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
     for (int k = 0; k < W; ++k) {
-      // G_k = bf16(dy * x_shift) for rows 4q..4q+3, channels 4n..4n+3 (fp32 products).
-      float gf[4][4];
+      // G_k = bf16(dy * x_shift) for rows 4q..4q+3, the lane's NJ channels (fp32 products).
+      float gf[4][NJ];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) gf[i][j] = dyf[i][j] * q4f<T>(xr[i - k + W - 1], j);
+        for (int j = 0; j < NJ; ++j) gf[i][j] = dyf[i][j] * Mma16<T>::to_f(LV::elem(xr[i - k + W - 1], j));
       // Row-major copy of the G tile in this wavefront's LDS, read back below as
       // the transposed (channel-contiguous) A operand of the dz MFMA.
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        u32x2 w;
-        w[0] = pack2<T>(gf[i][0], gf[i][1]);
-        w[1] = pack2<T>(gf[i][2], gf[i][3]);
-        *reinterpret_cast<u32x2*>(my_g + (4 * q + i) * GROW + 4 * n) = w;
-      }
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<typename LV::type*>(my_g + (4 * q + i) * GROW + NJ * n) = LV::template pack<T>(gf[i]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         // dx += dy[4q+i+k] * Kw[4q+i+k, k]: tap weights of the row blocks that hold rows k..k+3.
 #pragma unroll
         for (int bb = 0; bb < NB; ++bb) {
@@ -308,8 +339,8 @@ lr_bwd_mfma(LrBwdArgs a) {
           f32x4 wk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int c = 0; c < RC; ++c)
-            wk = Mma16<T>::run(zA[bb][c], UWREG ? uw_reg[UWREG ? (k * RC + c) * 4 + j : 0]
-                                                : my_uw[((k * RC + c) * 4 + j) * 64 + lane], wk);
+            wk = Mma16<T>::run(zA[bb][c], UWREG ? uw_reg[UWREG ? (k * RC + c) * NJ + j : 0]
+                                                : my_uw[((k * RC + c) * NJ + j) * 64 + lane], wk);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int tr = i + k;  // row offset of dy / Kw in the lane window
@@ -325,26 +356,23 @@ lr_bwd_mfma(LrBwdArgs a) {
       }
       // dz (K = 32 channels): A = G row n (this lane: row = lane % 16), channels 32s+8q..+7.
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
+      for (int s2 = 0; s2 < NS; ++s2) {
         const u32x4 ga = *reinterpret_cast<const u32x4*>(my_g + n * GROW + 32 * s2 + 8 * q);
 #pragma unroll
-        for (int c = 0; c < RC; ++c) dz[c] = Mma32<T>::run(ga, my_uz[((k * RC + c) * 2 + s2) * 64 + lane], dz[c]);
+        for (int c = 0; c < RC; ++c) dz[c] = Mma32<T>::run(ga, my_uz[((k * RC + c) * NS + s2) * 64 + lane], dz[c]);
       }
     }
 
     // ---- dx rows 4q..4q+3 (+ residual dy); out-of-range stores are dropped
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float v[4];
+      float v[NJ];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = a.residual ? dxa[i][j] + dyf[i][j] : dxa[i][j];
-      u32x2 o;
-      o[0] = pack2<T>(v[0], v[1]);
-      o[1] = pack2<T>(v[2], v[3]);
-      bstore64<true>(o, rdx, dxlane_off + dxtoff + i * dxrowb);
+      for (int j = 0; j < NJ; ++j) v[j] = a.residual ? dxa[i][j] + dyf[i][j] : dxa[i][j];
+      LV::store(LV::template pack<T>(v), rdx, dxlane_off + dxtoff + i * dxrowb);
     }
     // ---- dz: gather this wavefront's tile sums; every DZB iterations (and at the
-    // last one) add each run's 4 chunk wavefronts in wave order, one partial per group.
+    // last one) add each run's NCW chunk wavefronts in wave order, one partial per group.
     const int slot = it % DZB;
     const int buf = (it / DZB) & 1;
 #pragma unroll
@@ -355,7 +383,7 @@ lr_bwd_mfma(LrBwdArgs a) {
       __syncthreads();
       constexpr int PER_RUN = RC * 256;
       const int per_batch = (slot + 1) * PER_RUN;
-      for (int e = threadIdx.x; e < NRW * per_batch; e += 256 * NRW) {
+      for (int e = threadIdx.x; e < NRW * per_batch; e += 64 * NW) {
         const int ri = e / per_batch, e2 = e - ri * per_batch;
         const int sl = e2 / PER_RUN, rem = e2 - sl * PER_RUN;
         const int c = rem >> 8, rr = (rem >> 4) & 15, nn = rem & 15;
@@ -363,8 +391,9 @@ lr_bwd_mfma(LrBwdArgs a) {
         const Run& ru = ri == 0 ? runs[0] : runs[NRW - 1];
         const int ti = ru.tile0 + it - slot + sl;  // the slot's tile of run ri
         const int t = ti * 16 + rr;
-        const float v = ((dzred[buf][ri][0][sl][rem] + dzred[buf][ri][1][sl][rem]) + dzred[buf][ri][2][sl][rem]) +
-                        dzred[buf][ri][3][sl][rem];
+        float v = dzred[buf][ri][0][sl][rem];
+#pragma unroll
+        for (int w2 = 1; w2 < NCW; ++w2) v += dzred[buf][ri][w2][sl][rem];
         if (ti < ru.tile1 && r < R && t < Tn) part_dz[((int64_t)cg * a.BT + ru.row0 + t) * R + r] = v;
       }
     }
@@ -387,7 +416,7 @@ lr_bwd_mfma(LrBwdArgs a) {
     // The second run's wavefronts hand their dU sums to the first run's
     // wavefronts of the same chunk through LDS (the dz buffers, now free).
     float* xch = &dzred[0][0][0][0][0];
-    constexpr int NDU = W * RC * 4 * 4;  // dU floats per lane
+    constexpr int NDU = W * RC * NJ * 4;  // dU floats per lane
     static_assert(4 * NDU * 64 <= 2 * NRW * 4 * DZB * RC * 256, "dU exchange fits the dz buffers");
     __syncthreads();
     if (rw == 1) {
@@ -414,7 +443,7 @@ lr_bwd_mfma(LrBwdArgs a) {
 #pragma unroll
     for (int c = 0; c < RC; ++c)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = 16 * c + 4 * q + i;
@@ -425,26 +454,36 @@ lr_bwd_mfma(LrBwdArgs a) {
 // ------------------------------------------------------------------- host
 namespace {
 
+// Tile width and row runs per workgroup of a backward launch (see the kernel):
+// 32-channel tiles for two rank chunks at W <= 4, two row runs per workgroup
+// for one rank chunk at W <= 4, else 64-channel tiles and one run.
+struct BwdShape {
+  int cpw, nrw;
+};
+constexpr BwdShape bwd_shape(int W, int RC) {
+  return BwdShape{(RC == 2 && W <= 4) ? 32 : 64, (RC == 1 && W <= 4) ? 2 : 1};
+}
+
 LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   LrBwdArgs a;
+  const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
+  const BwdShape sh = bwd_shape((int)p.W, rc);
+  const int ncw = 256 / sh.cpw;
   a.Tn = (int)p.T;
   a.D = (int)p.D;
   a.R = (int)p.R;
   a.RK = (int)p.R + (p.static_w ? 1 : 0);
   a.residual = p.residual;
-  a.nch = (int)((p.D + 63) / 64);
-  a.ncg = (a.nch + 3) / 4;
+  a.nch = (int)((p.D + sh.cpw - 1) / sh.cpw);
+  a.ncg = (a.nch + ncw - 1) / ncw;
   const int64_t ntile = (p.T + 15) / 16;
-  int64_t seg = (p.B * ntile * a.ncg * 4 + target_waves - 1) / target_waves;
+  int64_t seg = (p.B * ntile * a.ncg * ncw + target_waves - 1) / target_waves;
   if (seg < 1) seg = 1;
   if (seg > ntile) seg = ntile;
   a.seg = (int)seg;
   a.nspb = (int)((ntile + seg - 1) / seg);
   a.nseg = (int)(p.B * a.nspb);
-  // row runs per workgroup: two when one rank chunk and W <= 4 (see the kernel)
-  const int64_t rc = (p.R + (p.static_w ? 1 : 0) + 15) / 16;
-  const int nrw = (rc == 1 && p.W <= 4) ? 2 : 1;
-  a.npair = (a.nseg + nrw - 1) / nrw;
+  a.npair = (a.nseg + sh.nrw - 1) / sh.nrw;
   a.nblk = a.npair * a.ncg;
   a.BT = p.B * p.T;
   a.zvec = p.R % 4 == 0 && aligned_to(p.z, 8);
@@ -468,7 +507,8 @@ BwdWs bwd_ws(const LrProblem& p, const LrBwdArgs& a) {
 
 template <typename T, int W, int RC>
 hipError_t launch_bwd(const LrProblem* p, int G) {
-  constexpr int NRW = (RC == 1 && W <= 4) ? 2 : 1;  // matches make_bwd_args
+  constexpr BwdShape SH = bwd_shape(W, RC);  // as make_bwd_args
+  constexpr int NRW = SH.nrw, CPW = SH.cpw, NT = 64 * (256 / CPW) * NRW;
   LrBwdArgs a = make_bwd_args(p[0], kBwdTargetWaves);
   const BwdWs w = bwd_ws(p[0], a);
   a.nblk1 = a.nblk;
@@ -482,9 +522,9 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
     a.zvec = a.zvec && aligned_to(p[g].z, 8);
   }
   if (a.zvec)
-    lr_bwd_mfma<T, W, RC, true, NRW><<<a.nblk, 256 * NRW, 0, p[0].stream>>>(a);
+    lr_bwd_mfma<T, W, RC, true, NRW, CPW><<<a.nblk, NT, 0, p[0].stream>>>(a);
   else
-    lr_bwd_mfma<T, W, RC, false, NRW><<<a.nblk, 256 * NRW, 0, p[0].stream>>>(a);
+    lr_bwd_mfma<T, W, RC, false, NRW, CPW><<<a.nblk, NT, 0, p[0].stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t WD = p[0].W * p[0].D, RKWD = (int64_t)a.RK * WD, R = p[0].R;
