@@ -142,6 +142,11 @@ LR_EDGE = [
     (2, 21, 40, 4, 3, True, True, torch.float32),       # D % 8 != 0
     (1, 50, 64, 3, 4, False, True, torch.bfloat16),     # rank 3: C-ABI general case
     (1, 50, 64, 5, 2, True, True, torch.float32),       # kernel rank 6: C-ABI general case
+    # backward plans with an odd run count (the last 8-wavefront workgroup's
+    # second run is empty) and a short last run: 201 tiles in runs of 2
+    (3, 3216, 256, 16, 4, False, True, torch.bfloat16),
+    (3, 3216, 256, 31, 4, True, True, torch.bfloat16),  # two rank chunks: 32-channel tiles
+    (2, 1000, 272, 15, 3, True, False, torch.float16),  # D not a multiple of 256: partial channel groups
 ]
 
 
