@@ -203,6 +203,7 @@ bool lr_mfma_ok(const LrProblem& p, bool bwd) {
 
 int64_t lr_bwd_ws_bytes(const LrProblem& p) {
   if (lr_mfma_ok(p, true)) return lr_mfma_ws_bytes(p);
+  if (lr_f32_ok(p)) return lr_f32_ws_bytes(p);
   const int64_t RK = p.R + (p.static_w ? 1 : 0);
   return (int64_t)generic_partials(p.B * p.T) * RK * p.W * p.D * (int64_t)sizeof(float);
 }
@@ -216,12 +217,16 @@ bool all_mfma_ok(const LrProblem* p, int G, bool bwd) {
 }  // namespace
 
 // G problems of one shape (see dc_launch.h): one MFMA launch for all of them,
-// or one generic launch sequence per group.
+// or per group the fp32 VALU kernels or the generic launch sequence.
 hipError_t lr_fwd(const LrProblem* p, int G) {
   if (G < 1 || G > kMaxGroups) return hipErrorInvalidValue;
   if (all_mfma_ok(p, G, false)) return lr_mfma_fwd(p, G);
   for (int g = 0; g < G; ++g) {
     hipError_t e;
+    if (lr_f32_ok(p[g])) {
+      if ((e = lr_f32(p[g], false)) != hipSuccess) return e;
+      continue;
+    }
     switch (p[g].dtype) {
       case kBF16: e = fwd_generic<bf16>(p[g]); break;
       case kFP16: e = fwd_generic<fp16>(p[g]); break;
@@ -237,6 +242,10 @@ hipError_t lr_bwd(const LrProblem* p, int G) {
   if (all_mfma_ok(p, G, true)) return lr_mfma_bwd(p, G);
   for (int g = 0; g < G; ++g) {
     hipError_t e;
+    if (lr_f32_ok(p[g])) {
+      if ((e = lr_f32(p[g], true)) != hipSuccess) return e;
+      continue;
+    }
     switch (p[g].dtype) {
       case kBF16: e = bwd_generic<bf16>(p[g]); break;
       case kFP16: e = bwd_generic<fp16>(p[g]); break;

@@ -147,6 +147,12 @@ LR_EDGE = [
     (3, 3216, 256, 16, 4, False, True, torch.bfloat16),
     (3, 3216, 256, 31, 4, True, True, torch.bfloat16),  # two rank chunks: 32-channel tiles
     (2, 1000, 272, 15, 3, True, False, torch.float16),  # D not a multiple of 256: partial channel groups
+    # fp32 kernels: ranks padded to 8 / 16 / 32, partial channel groups, runs of 16+ rows
+    (2, 1000, 272, 15, 3, True, False, torch.float32),
+    (1, 70, 128, 31, 4, True, True, torch.float32),     # kernel rank 32
+    (2, 300, 64, 1, 1, False, True, torch.float32),     # rank 1, W 1
+    (1, 9, 100, 7, 4, False, True, torch.float32),      # T below one run, D % 64 != 0
+    (1, 40, 64, 40, 4, False, False, torch.float32),    # kernel rank 40: generic kernels
 ]
 
 
