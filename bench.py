@@ -60,7 +60,8 @@ CONFIGS = {
 }
 EXTRA = {
     "lr_qkv": dict(kind="lr", B=2, T=8192, D=4096, R=31, W=4, static=True, residual=True, calls=3),
-    "lr_qkv_grouped": dict(kind="lrg", B=2, T=8192, D=4096, R=31, W=4, static=True, residual=True, G=3),
+    "lr_qkv_grouped": dict(kind="lrg", B=2, T=8192, D=4096, R=31, W=4, static=True, residual=True, G=3,
+                           head_dim=128),
 }
 STEP = ["hw_hs1", "hw_hs32", "lr_r16"]
 
@@ -221,12 +222,12 @@ def abi_launchers(c, sets, torch):
         def fwd(i):
             d = sets[i]
             _capi.check(lib.dc_lowrank_fwd_grouped(G, p(d["x"]), G * D, pa(d["zs"]), pa(d["Us"]), pa(d["sws"]),
-                                                   pa(d["ys"]), B, T, D, R, W, 0, res, st), "grouped fwd")
+                                                   pa(d["ys"]), 0, B, T, D, R, W, 0, res, st), "grouped fwd")
 
         def bwd(i):
             d = sets[i]
             _capi.check(lib.dc_lowrank_bwd_grouped(G, p(d["x"]), G * D, pa(d["zs"]), pa(d["Us"]), pa(d["sws"]),
-                                                   pa(d["dys"]), p(d["dx"]), G * D, pa(d["dzs"]), pa(d["dUs"]),
+                                                   pa(d["dys"]), 0, p(d["dx"]), G * D, pa(d["dzs"]), pa(d["dUs"]),
                                                    pa(d["dsws"]), p(d["ws"]), d["nws"], B, T, D, R, W, 0, res, st),
                         "grouped bwd")
         return fwd, bwd
@@ -305,8 +306,23 @@ def qkv_end_to_end(torch, dev, reps=10):
     def grouped():
         torch.autograd.backward(lrg(qkv, zs, Us, sws, residual=True), dys)
 
+    # README.md:106-110 then reshapes q, k, v into heads for attention; contiguous
+    # head-major copies against the grouped operator writing that layout itself.
+    hd = c["head_dim"]
+    H = D // hd
+    dys_h = [d.view(B, T, H, hd).transpose(1, 2).contiguous() for d in dys]
+
+    def readme_heads():
+        outs = [lr(part.contiguous(), zs[g], Us[g], sws[g], residual=True).view(B, T, H, hd).transpose(1, 2)
+                .contiguous() for g, part in enumerate(qkv.split(D, dim=-1))]
+        torch.autograd.backward(outs, dys_h)
+
+    def grouped_heads():
+        torch.autograd.backward(lrg(qkv, zs, Us, sws, residual=True, head_dim=hd), dys_h)
+
     out = {}
-    for name, fn in (("readme_split_contiguous_3_calls", readme), ("grouped", grouped)):
+    for name, fn in (("readme_split_contiguous_3_calls", readme), ("grouped", grouped),
+                     ("readme_heads_contiguous", readme_heads), ("grouped_head_major", grouped_heads)):
         for t in [qkv] + zs + Us + sws:
             t.grad = None
         fn()
@@ -323,8 +339,12 @@ def qkv_end_to_end(torch, dev, reps=10):
     fb, bb = alg_bytes(c)
     out["alg_MB"] = round((fb + bb) / 1e6, 1)
     out["speedup"] = round(out["readme_split_contiguous_3_calls_us"] / out["grouped_us"], 3)
+    out["head_dim"] = hd
+    out["speedup_heads"] = round(out["readme_heads_contiguous_us"] / out["grouped_head_major_us"], 3)
     print(f"[bench] qkv end to end (fwd+bwd, autograd): README pattern {out['readme_split_contiguous_3_calls_us']} us, "
-          f"grouped {out['grouped_us']} us ({out['speedup']}x)", file=sys.stderr, flush=True)
+          f"grouped {out['grouped_us']} us ({out['speedup']}x); with [B,H,T,{hd}] outputs: README + contiguous "
+          f"{out['readme_heads_contiguous_us']} us, grouped head-major {out['grouped_head_major_us']} us "
+          f"({out['speedup_heads']}x)", file=sys.stderr, flush=True)
     return out
 
 

@@ -197,15 +197,18 @@ int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* stat
 // ------------------------------------------------------------------ grouped
 // G problems of one shape in one launch; group g reads x + g*D with rows
 // x_ld elements apart (the q / k / v slices of a fused projection) and, in the
-// backward, writes dx + g*D with rows dx_ld elements apart.
+// backward, writes dx + g*D with rows dx_ld elements apart.  y (dy) is
+// [B, T, D] when y_hd (dy_hd) is 0, else head-major [B, D/hd, T, hd].
+
+static bool head_dim_ok(int64_t hd, int64_t D) { return hd == 0 || (hd > 0 && hd <= D && D % hd == 0); }
 
 int dc_lowrank_fwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z, const void* const* U,
-                           const void* const* static_w, void* const* y, int64_t B, int64_t T, int64_t D,
-                           int64_t R, int64_t W, int dtype, int residual, void* stream) {
+                           const void* const* static_w, void* const* y, int64_t y_hd, int64_t B, int64_t T,
+                           int64_t D, int64_t R, int64_t W, int dtype, int residual, void* stream) {
   if (G < 1 || G > DC_MAX_GROUPS) return DC_ERR_UNSUPPORTED;
   int s = check_lowrank(B, T, D, R, W, dtype, static_w != nullptr);
   if (s != DC_OK) return s;
-  if (x_ld < G * D || x_ld > kI32Max) return DC_ERR_SHAPE;
+  if (x_ld < G * D || x_ld > kI32Max || !head_dim_ok(y_hd, D)) return DC_ERR_SHAPE;
   if (!x || !z || !U || !y) return DC_ERR_NULL;
   const int es = dc::dtype_size(dtype);
   if (!aligned_to(x, es)) return DC_ERR_ALIGN;
@@ -217,7 +220,7 @@ int dc_lowrank_fwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* c
       return DC_ERR_ALIGN;
     dc::LrProblem& q = p[g];
     q.x = (const char*)x + g * D * es; q.z = z[g]; q.U = U[g]; q.static_w = sw; q.y = y[g];
-    q.B = B; q.T = T; q.D = D; q.R = R; q.W = W; q.x_ld = x_ld;
+    q.B = B; q.T = T; q.D = D; q.R = R; q.W = W; q.x_ld = x_ld; q.y_hd = y_hd;
     q.dtype = dtype; q.residual = residual ? 1 : 0; q.stream = (hipStream_t)stream;
   }
   if ((s = device_status()) != DC_OK) return s;
@@ -238,14 +241,15 @@ int64_t dc_lowrank_bwd_grouped_ws_bytes(int64_t G, int64_t B, int64_t T, int64_t
 }
 
 int dc_lowrank_bwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z, const void* const* U,
-                           const void* const* static_w, const void* const* dy, void* dx, int64_t dx_ld,
-                           void* const* dz, void* const* dU, void* const* dstatic_w, void* workspace,
-                           int64_t ws_bytes, int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype,
-                           int residual, void* stream) {
+                           const void* const* static_w, const void* const* dy, int64_t dy_hd, void* dx,
+                           int64_t dx_ld, void* const* dz, void* const* dU, void* const* dstatic_w,
+                           void* workspace, int64_t ws_bytes, int64_t B, int64_t T, int64_t D, int64_t R,
+                           int64_t W, int dtype, int residual, void* stream) {
   if (G < 1 || G > DC_MAX_GROUPS) return DC_ERR_UNSUPPORTED;
   int s = check_lowrank(B, T, D, R, W, dtype, static_w != nullptr);
   if (s != DC_OK) return s;
-  if (x_ld < G * D || x_ld > kI32Max || dx_ld < G * D || dx_ld > kI32Max) return DC_ERR_SHAPE;
+  if (x_ld < G * D || x_ld > kI32Max || dx_ld < G * D || dx_ld > kI32Max || !head_dim_ok(dy_hd, D))
+    return DC_ERR_SHAPE;
   if (!x || !z || !U || !dy || !dx || !dz || !dU) return DC_ERR_NULL;
   if ((static_w == nullptr) != (dstatic_w == nullptr)) return DC_ERR_NULL;
   const int es = dc::dtype_size(dtype);
@@ -266,7 +270,7 @@ int dc_lowrank_bwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* c
     q.x = (const char*)x + g * D * es; q.z = z[g]; q.U = U[g]; q.static_w = sw; q.dy = dy[g];
     q.dx = (char*)dx + g * D * es; q.dz = dz[g]; q.dU = dU[g]; q.dstatic_w = dsw;
     q.ws = share > 0 ? (float*)((char*)workspace + g * share) : nullptr;
-    q.B = B; q.T = T; q.D = D; q.R = R; q.W = W; q.x_ld = x_ld; q.dx_ld = dx_ld;
+    q.B = B; q.T = T; q.D = D; q.R = R; q.W = W; q.x_ld = x_ld; q.dx_ld = dx_ld; q.y_hd = dy_hd;
     q.dtype = dtype; q.residual = residual ? 1 : 0; q.stream = (hipStream_t)stream;
   }
   if ((s = device_status()) != DC_OK) return s;

@@ -51,11 +51,16 @@ struct LrProblem {
   int64_t B, T, D, R, W;  // R = dynamic rank (z.shape[-1])
   int64_t x_ld;           // row stride of x in elements (0: D, contiguous)
   int64_t dx_ld;          // row stride of dx in elements (0: D, contiguous)
+  // Layout of y (forward) and dy (backward): 0 or D for [B, T, D]; otherwise
+  // the head dim hd of the head-major layout [B, D/hd, T, hd] (D % hd == 0),
+  // in which element (b, t, d) sits at b*T*D + (d/hd)*T*hd + t*hd + d%hd.
+  int64_t y_hd;
   int dtype;
   int residual;
   hipStream_t stream;
   int64_t xld() const { return x_ld > 0 ? x_ld : D; }
   int64_t dxld() const { return dx_ld > 0 ? dx_ld : D; }
+  int64_t yhd() const { return y_hd > 0 ? y_hd : D; }
 };
 
 // Independent problems launched together (the q / k / v convolutions of one

@@ -16,6 +16,16 @@
 
 namespace dc {
 
+// Element offset of (row = b*T + t, channel d) in y / dy: row*D + d for
+// [B, T, D] (hd == D), else b*T*D + (d/hd)*T*hd + t*hd + d%hd for the
+// head-major [B, D/hd, T, hd].
+__device__ __forceinline__ int64_t yoff(int64_t row, int d, int Tn, int D, int hd) {
+  if (hd == D) return row * D + d;
+  const int64_t b = row / Tn;
+  const int t = (int)(row - b * Tn), h = d / hd;
+  return (b * D + (int64_t)h * hd) * Tn + (int64_t)t * hd + (d - h * hd);
+}
+
 template <typename T>
 __device__ __forceinline__ float zrank(const T* __restrict__ z, int64_t row, int R, int r) {
   return r < R ? (float)z[row * R + r] : 1.0f;
@@ -42,7 +52,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void lr_fwd_generic(const T* __restrict__ x, const T* __restrict__ z,
                                                       const T* __restrict__ U, const T* __restrict__ sw,
                                                       T* __restrict__ y, int64_t BT, int Tn, int D, int64_t xld,
-                                                      int R, int W, int residual) {
+                                                      int hd, int R, int W, int residual) {
   const int64_t n = BT * D;
   const int64_t WD = (int64_t)W * D;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
@@ -53,7 +63,7 @@ __global__ __launch_bounds__(256) void lr_fwd_generic(const T* __restrict__ x, c
     for (int k = 0; k < W && k <= t; ++k)
       acc = fmaf(lr_tap(z, U, sw, row, R, WD, (int64_t)k * D + d), (float)x[(row - k) * xld + d], acc);
     if (residual) acc += (float)x[row * xld + d];
-    y[i] = (T)acc;
+    y[yoff(row, d, Tn, D, hd)] = (T)acc;
   }
 }
 
@@ -61,7 +71,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void lr_bwd_dx_generic(const T* __restrict__ z, const T* __restrict__ U,
                                                          const T* __restrict__ sw, const T* __restrict__ dy,
                                                          T* __restrict__ dx, int64_t BT, int Tn, int D,
-                                                         int64_t dxld, int R, int W, int residual) {
+                                                         int64_t dxld, int hd, int R, int W, int residual) {
   const int64_t n = BT * D;
   const int64_t WD = (int64_t)W * D;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
@@ -70,8 +80,8 @@ __global__ __launch_bounds__(256) void lr_bwd_dx_generic(const T* __restrict__ z
     const int t = (int)(row % Tn);
     float acc = 0.f;
     for (int k = 0; k < W && t + k < Tn; ++k)
-      acc = fmaf((float)dy[(row + k) * D + d], lr_tap(z, U, sw, row + k, R, WD, (int64_t)k * D + d), acc);
-    if (residual) acc += (float)dy[i];
+      acc = fmaf((float)dy[yoff(row + k, d, Tn, D, hd)], lr_tap(z, U, sw, row + k, R, WD, (int64_t)k * D + d), acc);
+    if (residual) acc += (float)dy[yoff(row, d, Tn, D, hd)];
     dx[row * dxld + d] = (T)acc;
   }
 }
@@ -81,7 +91,7 @@ __global__ __launch_bounds__(256) void lr_bwd_dx_generic(const T* __restrict__ z
 template <typename T>
 __global__ __launch_bounds__(256) void lr_bwd_dz_generic(const T* __restrict__ x, const T* __restrict__ U,
                                                          const T* __restrict__ dy, T* __restrict__ dz, int Tn,
-                                                         int D, int64_t xld, int R, int W) {
+                                                         int D, int64_t xld, int hd, int R, int W) {
   __shared__ float red[256];
   const int64_t row = blockIdx.x;
   const int t = (int)(row % Tn);
@@ -92,7 +102,7 @@ __global__ __launch_bounds__(256) void lr_bwd_dz_generic(const T* __restrict__ x
       const T* xr = x + (row - k) * xld;
       const T* ur = U + (int64_t)r * WD + (int64_t)k * D;
       for (int d = threadIdx.x; d < D; d += 256)
-        acc = fmaf((float)dy[row * D + d] * (float)xr[d], (float)ur[d], acc);
+        acc = fmaf((float)dy[yoff(row, d, Tn, D, hd)] * (float)xr[d], (float)ur[d], acc);
     }
     red[threadIdx.x] = acc;
     __syncthreads();
@@ -109,8 +119,8 @@ __global__ __launch_bounds__(256) void lr_bwd_dz_generic(const T* __restrict__ x
 template <typename T>
 __global__ __launch_bounds__(256) void lr_bwd_du_generic(const T* __restrict__ x, const T* __restrict__ z,
                                                          const T* __restrict__ dy, float* __restrict__ part,
-                                                         int64_t BT, int Tn, int D, int64_t xld, int R, int RK,
-                                                         int W, int64_t rows_per) {
+                                                         int64_t BT, int Tn, int D, int64_t xld, int hd, int R,
+                                                         int RK, int W, int64_t rows_per) {
   const int64_t WD = (int64_t)W * D;
   const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (c >= (int64_t)RK * WD) return;
@@ -123,7 +133,8 @@ __global__ __launch_bounds__(256) void lr_bwd_du_generic(const T* __restrict__ x
   float acc = 0.f;
   for (int64_t row = r0; row < r1; ++row) {
     const int t = (int)(row % Tn);
-    if (t >= k) acc = fmaf(zrank(z, row, R, r), (float)dy[row * D + d] * (float)x[(row - k) * xld + d], acc);
+    if (t >= k)
+      acc = fmaf(zrank(z, row, R, r), (float)dy[yoff(row, d, Tn, D, hd)] * (float)x[(row - k) * xld + d], acc);
   }
   part[(int64_t)blockIdx.y * RK * WD + c] = acc;
 }
@@ -150,7 +161,7 @@ hipError_t fwd_generic(const LrProblem& p) {
   const int64_t BT = p.B * p.T;
   lr_fwd_generic<T><<<generic_grid(BT * p.D), 256, 0, p.stream>>>(
       (const T*)p.x, (const T*)p.z, (const T*)p.U, (const T*)p.static_w, (T*)p.y, BT, (int)p.T, (int)p.D, p.xld(),
-      (int)p.R, (int)p.W, p.residual);
+      (int)p.yhd(), (int)p.R, (int)p.W, p.residual);
   return hipGetLastError();
 }
 
@@ -161,15 +172,16 @@ hipError_t bwd_generic(const LrProblem& p) {
   const int64_t WD = p.W * p.D;
   lr_bwd_dx_generic<T><<<generic_grid(BT * p.D), 256, 0, p.stream>>>(
       (const T*)p.z, (const T*)p.U, (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, BT, (int)p.T, (int)p.D,
-      p.dxld(), (int)p.R, (int)p.W, p.residual);
+      p.dxld(), (int)p.yhd(), (int)p.R, (int)p.W, p.residual);
   lr_bwd_dz_generic<T><<<(unsigned)BT, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.U, (const T*)p.dy,
-                                                           (T*)p.dz, (int)p.T, (int)p.D, p.xld(), (int)p.R,
-                                                           (int)p.W);
+                                                           (T*)p.dz, (int)p.T, (int)p.D, p.xld(), (int)p.yhd(),
+                                                           (int)p.R, (int)p.W);
   const int P = generic_partials(BT);
   const int64_t rows_per = (BT + P - 1) / P;
   dim3 grid((unsigned)((RK * WD + 255) / 256), (unsigned)P);
   lr_bwd_du_generic<T><<<grid, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.dy, p.ws, BT,
-                                                   (int)p.T, (int)p.D, p.xld(), (int)p.R, RK, (int)p.W, rows_per);
+                                                   (int)p.T, (int)p.D, p.xld(), (int)p.yhd(), (int)p.R, RK,
+                                                   (int)p.W, rows_per);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const PartialReduce jobs[2] = {
@@ -195,9 +207,11 @@ bool lr_mfma_ok(const LrProblem& p, bool bwd) {
   if (!bwd) {
     // 16-byte row pieces of x at every row: xld a multiple of 8 elements
     if (p.D % 8 != 0 || p.xld() % 8 != 0) return false;
+    if (p.yhd() % 8 != 0) return false;  // a lane's y octet inside one head
     return aligned_to16(p.x) && aligned_to16(p.U) && aligned_to16(p.static_w) && aligned_to16(p.y);
   }
   if (p.D % 16 != 0 || p.xld() % 4 != 0 || p.dxld() % 4 != 0) return false;
+  if (p.yhd() != p.D && p.yhd() % 64 != 0) return false;  // a wavefront's dy channels inside one head
   return aligned_to8(p.x) && aligned_to8(p.dy) && aligned_to8(p.dx) && aligned_to16(p.U) && aligned_to16(p.static_w);
 }
 

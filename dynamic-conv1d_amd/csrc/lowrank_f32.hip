@@ -28,6 +28,7 @@ namespace dc {
 struct LrF32Args {
   int Tn, D, R, RK, residual;
   int xld, dxld;  // row strides of x and dx (elements)
+  int yhd;        // y / dy layout: D ([B, T, D]) or the head dim of [B, D/yhd, T, yhd] (yhd % 64 == 0)
   int nch;        // ceil(D / 64) chunks
   int ncg;        // ceil(nch / 4): workgroup columns (256 channels)
   int seg;        // rows per run
@@ -117,10 +118,14 @@ __global__ __launch_bounds__(256) void lr_fwd_f32(const float* __restrict__ x, c
   const int t0 = (s - b * a.nspb) * a.seg;
   const int t1 = min(t0 + a.seg, Tn);
   const int64_t row0 = (int64_t)b * Tn;
-  const int xrowb = a.xld * 4, yrowb = D * 4;
+  // y: the wavefront's 64 channels lie in one head (yhd % 64 == 0), whose
+  // [T, yhd] block the resource covers (the whole [T, D] row block when yhd == D).
+  const int yhd = a.yhd, head = ((cg * 4 + wave) * 64) / yhd;
+  const int xrowb = a.xld * 4, yrowb = yhd * 4;
   const rsrc_t rx = make_rsrc(x + row0 * a.xld, (int64_t)Tn * xrowb);
-  const rsrc_t ry = make_rsrc(y + row0 * D, (int64_t)Tn * yrowb);
+  const rsrc_t ry = make_rsrc(y + row0 * D + (int64_t)head * Tn * yhd, (int64_t)Tn * yrowb);
   const int lo = dv ? d * 4 : kOobLane;
+  const int ylo = dv ? (d - head * yhd) * 4 : kOobLane;
   const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 4);
   typedef ZChunk<UC, RKP> ZC;
   float zfill[ZC::N];
@@ -163,7 +168,7 @@ __global__ __launch_bounds__(256) void lr_fwd_f32(const float* __restrict__ x, c
         acc = fmaf(kw, xf[f32ring<W>(uu, k)], acc);
       }
       if (a.residual) acc += xf[p];
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc), ry, lo + (t < t1 ? t * yrowb : kOobTile), 0, kNt);
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc), ry, ylo + (t < t1 ? t * yrowb : kOobTile), 0, kNt);
     }
   };
   Chunk ca, cb;
@@ -254,11 +259,14 @@ __global__ __launch_bounds__(256) void lr_bwd_f32(const float* __restrict__ x, c
   const int t1 = min(t0 + a.seg, Tn);
   const int tend = t1 + W - 1;  // steps t0 .. tend-1: dx of row t needs dy, z of rows t .. t+W-1
   const int64_t row0 = (int64_t)b * Tn;
-  const int xrowb = a.xld * 4, rowb = D * 4, dxrowb = a.dxld * 4;
+  // dy: [B, T, D] or head-major, as y in the forward
+  const int yhd = a.yhd, head = ((cg * 4 + wave) * 64) / yhd;
+  const int xrowb = a.xld * 4, rowb = yhd * 4, dxrowb = a.dxld * 4;
   const rsrc_t rx = make_rsrc(x + row0 * a.xld, (int64_t)Tn * xrowb);
-  const rsrc_t rdy = make_rsrc(dy + row0 * D, (int64_t)Tn * rowb);
+  const rsrc_t rdy = make_rsrc(dy + row0 * D + (int64_t)head * Tn * yhd, (int64_t)Tn * rowb);
   const rsrc_t rdx = make_rsrc(dx + row0 * a.dxld, (int64_t)Tn * dxrowb);
   const int lo = dv ? d * 4 : kOobLane;
+  const int ylo = dv ? (d - head * yhd) * 4 : kOobLane;
   const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 4);
   typedef ZChunk<UC, RKP> ZC;
   float zfill[ZC::N];
@@ -286,7 +294,7 @@ __global__ __launch_bounds__(256) void lr_bwd_f32(const float* __restrict__ x, c
 #pragma unroll
     for (int uu = 0; uu < UC; ++uu) {
       const int t = tc + uu;
-      c.dy[uu] = __uint_as_float(bload32(rdy, lo + (t < tend ? t * rowb : kOobTile)));  // rows past T read 0
+      c.dy[uu] = __uint_as_float(bload32(rdy, ylo + (t < tend ? t * rowb : kOobTile)));  // rows past T read 0
       c.x[uu] = __uint_as_float(bload32(rx, lo + (t < t1 ? t * xrowb : kOobTile)));
     }
     c.z.load(rz, tc, R, lane);
@@ -385,6 +393,7 @@ LrF32Args make_f32_args(const LrProblem& p, int target_waves) {
   a.residual = p.residual;
   a.xld = (int)p.xld();
   a.dxld = (int)p.dxld();
+  a.yhd = (int)p.yhd();
   a.nch = (int)((p.D + 63) / 64);
   a.ncg = (a.nch + 3) / 4;
   int64_t seg = (p.B * p.T * a.ncg * 4 + target_waves - 1) / target_waves;
@@ -446,6 +455,7 @@ bool lr_f32_ok(const LrProblem& p) {
   if (p.R + (p.static_w ? 1 : 0) > 32) return false;
   if (p.R * p.W * p.D * 4 >= kOobLane) return false;  // U column offsets
   if (!aligned_to(p.x, 4) || !aligned_to(p.dy, 4) || !aligned_to(p.dx, 4)) return false;  // 4-byte buffer accesses
+  if (p.yhd() != p.D && p.yhd() % 64 != 0) return false;  // a wavefront's 64 channels in one head
   const int64_t ld = p.xld() > p.dxld() ? p.xld() : p.dxld();
   if ((p.T + kSeqSlackRows) * ld * 4 > kMaxSeqBytes) return false;
   if ((p.T + kSeqSlackRows) * p.R * 4 > kMaxSeqBytes) return false;  // z rows

@@ -68,6 +68,7 @@ struct LrBwdArgs {
   int xld;    // row stride of x (elements)
   int dxld;   // row stride of dx (elements)
   int zvec;   // R % 4 == 0 and z 8-byte aligned: 8-byte z loads
+  int yhd;    // dy layout: D ([B, T, D]) or the head dim of [B, D/yhd, T, yhd]
   int64_t BT;
   LrBwdGroup grp[kMaxGroups];
 };
@@ -229,13 +230,18 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   u32x2* __restrict__ my_uw = uw_lds[wave];
   u32x4* __restrict__ my_uz = uz_lds[wave];
   uint16_t* __restrict__ my_g = gtile[wave];
-  const int rowb = D * 2, xrowb = a.xld * 2, dxrowb = a.dxld * 2;
+  // dy is [B, T, D] (yhd == D) or head-major [B, D/yhd, T, yhd]; the host takes
+  // this path only when yhd % CPW == 0, so a wavefront's channels lie in one
+  // head and its dy resource covers that head's [T, yhd] block (rows past T
+  // stay out of range either way).
+  const int yhd = a.yhd, head = d0 / yhd;
+  const int rowb = yhd * 2, xrowb = a.xld * 2, dxrowb = a.dxld * 2;
   const rsrc_t rx = make_rsrc(x + row0 * a.xld, (int64_t)Tn * xrowb);
-  const rsrc_t rdy = make_rsrc(dy + row0 * D, (int64_t)Tn * rowb);
+  const rsrc_t rdy = make_rsrc(dy + row0 * D + (int64_t)head * Tn * yhd, (int64_t)Tn * rowb);
   const rsrc_t rdx = make_rsrc(dx + row0 * a.dxld, (int64_t)Tn * dxrowb);
   const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 2);
   // byte offsets of the lane's row-4q channels in dy, x and dx
-  const int lane_off = chv ? (4 * q * D + col) * 2 : kOobLane;
+  const int lane_off = chv ? (4 * q * yhd + col - head * yhd) * 2 : kOobLane;
   const int xlane_off = chv ? (4 * q * a.xld + col) * 2 : kOobLane;
   const int dxlane_off = chv ? (4 * q * a.dxld + col) * 2 : kOobLane;
 
@@ -515,6 +521,7 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
   a.nblk = G * a.nblk1;
   a.xld = (int)p[0].xld();
   a.dxld = (int)p[0].dxld();
+  a.yhd = (int)p[0].yhd();
   for (int g = 0; g < G; ++g) {
     float* pdz = (float*)((char*)p[g].ws + w.dz_off);
     float* pdu = (float*)((char*)p[g].ws + w.du_off);

@@ -43,6 +43,7 @@ struct LrArgs {
   int nblk1;       // blocks per group
   int xld;         // row stride of x (elements)
   int zvec;        // R % 4 == 0 and z 8-byte aligned: 8-byte z loads (host dispatch)
+  int yhd;         // y layout: D ([B, T, D]) or the head dim of [B, D/yhd, T, yhd] (yhd % 8 == 0)
   LrFwdGroup grp[kMaxGroups];
 };
 
@@ -104,11 +105,15 @@ __global__ __launch_bounds__(256) void lr_fwd_mfma(LrArgs a) {
   const int tile0 = (sg - b * a.nspb) * a.seg;
   const int tile1 = min(tile0 + a.seg, ntile);
   const int64_t row0 = (int64_t)b * Tn;
-  const int rowb = D * 2, xrowb = a.xld * 2;
+  // y is [B, T, D] (yhd == D) or head-major [B, D/yhd, T, yhd]: the lane's
+  // octet lies in head yh, whose rows are yhd elements apart.  Rows past T
+  // would land in the next head's block there, so stores check the row.
+  const int yhd = a.yhd, yh = dl / yhd;
+  const int rowb = yhd * 2, xrowb = a.xld * 2;
   const rsrc_t rx = make_rsrc(x + row0 * a.xld, (int64_t)Tn * xrowb);
-  const rsrc_t ry = make_rsrc(y + row0 * D, (int64_t)Tn * rowb);
+  const rsrc_t ry = make_rsrc(y + row0 * D, (int64_t)Tn * D * 2);
   const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 2);
-  const int lane_off = chv ? (4 * q * D + dl) * 2 : kOobLane;         // y byte offset of the lane's row 4q octet
+  const int lane_off = chv ? ((yh * Tn + 4 * q) * yhd + dl - yh * yhd) * 2 : kOobLane;  // y: the lane's row 4q octet
   const int xlane_off = chv ? (4 * q * a.xld + dl) * 2 : kOobLane;   // the same in x
 
   // Tile inputs (rows out of the sequence read as 0).  Two buffers, A and B,
@@ -158,7 +163,7 @@ __global__ __launch_bounds__(256) void lr_fwd_mfma(LrArgs a) {
       u32x4 o;
 #pragma unroll
       for (int h = 0; h < 4; ++h) o[h] = pack2<T>(acc[i][2 * h], acc[i][2 * h + 1]);
-      bstore128<true>(o, ry, lane_off + toff + i * rowb);
+      bstore128<true>(o, ry, tile * 16 + 4 * q + i < Tn ? lane_off + toff + i * rowb : kOobTile);
     }
   };
 
@@ -206,6 +211,7 @@ hipError_t launch_fwd(const LrProblem* p, int G) {
   a.nblk1 = a.nblk;
   a.nblk = G * a.nblk1;
   a.xld = (int)p[0].xld();
+  a.yhd = (int)p[0].yhd();
   for (int g = 0; g < G; ++g) {
     a.grp[g] = LrFwdGroup{p[g].x, p[g].z, p[g].U, p[g].static_w, p[g].y};
     a.zvec = a.zvec && aligned_to(p[g].z, 8);

@@ -112,22 +112,24 @@ class _GroupedLowrankDynamicConvolutionFn(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, x, residual, G, has_static, *params):
+    def forward(ctx, x, residual, G, has_static, hd, *params):
         zs, Us = params[:G], params[G:2 * G]
         sws = params[2 * G:3 * G] if has_static else None
         B, T, C = x.shape
         D = C // G
         R = zs[0].shape[-1]
         W = Us[0].shape[-1] // D
-        ys = [torch.empty(B, T, D, dtype=x.dtype, device=x.device) for _ in range(G)]
+        shape = (B, T, D) if hd == 0 else (B, D // hd, T, hd)
+        ys = [torch.empty(shape, dtype=x.dtype, device=x.device) for _ in range(G)]
         lib = _capi.load()
         status = lib.dc_lowrank_fwd_grouped(
             G, _capi.ptr(x), x.stride(1), _capi.ptr_array(zs), _capi.ptr_array(Us), _capi.ptr_array(sws),
-            _capi.ptr_array(ys), B, T, D, R, W, _capi.dtype_code(x.dtype), int(bool(residual)), _capi.stream_of(x),
+            _capi.ptr_array(ys), hd, B, T, D, R, W, _capi.dtype_code(x.dtype), int(bool(residual)),
+            _capi.stream_of(x),
         )
         _capi.check(status, "grouped lowrank forward")
         ctx.save_for_backward(x, *params)
-        ctx.G, ctx.has_static, ctx.residual = G, has_static, bool(residual)
+        ctx.G, ctx.has_static, ctx.residual, ctx.hd = G, has_static, bool(residual), hd
         return tuple(ys)
 
     @staticmethod
@@ -141,8 +143,10 @@ class _GroupedLowrankDynamicConvolutionFn(torch.autograd.Function):
         R = zs[0].shape[-1]
         W = Us[0].shape[-1] // D
         dtype = _capi.dtype_code(x.dtype)
+        hd = ctx.hd
         # an output that did not reach the loss has no gradient: it contributes zeros
-        dys = [torch.zeros(B, T, D, dtype=x.dtype, device=x.device) if d is None else d.to(x.dtype).contiguous()
+        shape = (B, T, D) if hd == 0 else (B, D // hd, T, hd)
+        dys = [torch.zeros(shape, dtype=x.dtype, device=x.device) if d is None else d.to(x.dtype).contiguous()
                for d in dys]
         dx = torch.empty(B, T, C, dtype=x.dtype, device=x.device)
         dzs = [torch.empty_like(z) for z in zs]
@@ -154,12 +158,12 @@ class _GroupedLowrankDynamicConvolutionFn(torch.autograd.Function):
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes > 0 else None
         status = lib.dc_lowrank_bwd_grouped(
             G, _capi.ptr(x), x.stride(1), _capi.ptr_array(zs), _capi.ptr_array(Us), _capi.ptr_array(sws),
-            _capi.ptr_array(dys), _capi.ptr(dx), C, _capi.ptr_array(dzs), _capi.ptr_array(dUs),
+            _capi.ptr_array(dys), hd, _capi.ptr(dx), C, _capi.ptr_array(dzs), _capi.ptr_array(dUs),
             _capi.ptr_array(dsws), _capi.ptr(ws), ws_bytes, B, T, D, R, W, dtype, int(ctx.residual),
             _capi.stream_of(x),
         )
         _capi.check(status, "grouped lowrank backward")
-        return (dx, None, None, None, *dzs, *dUs, *(dsws or []))
+        return (dx, None, None, None, None, *dzs, *dUs, *(dsws or []))
 
 
 def lowrank_dynamic_convolution_grouped(
@@ -168,13 +172,17 @@ def lowrank_dynamic_convolution_grouped(
     U,
     static_w=None,
     residual: bool = False,
+    head_dim=None,
 ):
     """G lowrank dynamic short convolutions of one shape, e.g. on the q, k and v of an attention layer.
 
     Equivalent to
         [lowrank_dynamic_convolution(x[..., g*D:(g+1)*D].contiguous(), z[g], U[g], static_w[g], residual)
          for g in range(G)]
-    (README.md:57-110), computed by one launch per direction with x read in place.
+    (README.md:57-110), computed by one launch per direction with x read in place.  With head_dim
+    set, each output is written head-major, as
+        y.view(B, T, D // head_dim, head_dim).transpose(1, 2).contiguous()
+    (README.md:106-110): the layout attention reads, produced by the kernel's own stores.
 
     Args:
         x:          [B, T, G*D] activations, e.g. the fused q|k|v projection.  Channels must be
@@ -183,9 +191,13 @@ def lowrank_dynamic_convolution_grouped(
         U:          G tensors [R, W*D], contiguous.
         static_w:   None, or G tensors [W, D] fused as one extra rank each.
         residual:   add each group's input to its output.
+        head_dim:   None for [B, T, D] outputs, or a head dim hd (D % hd == 0) for contiguous
+                    [B, D // hd, T, hd] outputs.  hd a multiple of 64 keeps the fast kernels of
+                    every dtype (bitwise the values of the [B, T, D] layout); other head dims
+                    take slower kernels in some cases.
 
     Returns:
-        a tuple of G tensors [B, T, D].
+        a tuple of G tensors [B, T, D] (or [B, D // head_dim, T, head_dim]).
 
     Per group, the preconditions of lowrank_dynamic_convolution (lowrank.py:328-337); G <= 4.
     """
@@ -217,5 +229,7 @@ def lowrank_dynamic_convolution_grouped(
             assert s.is_cuda and s.is_contiguous()
             assert s.dtype == z[g].dtype == U[g].dtype
             assert s.shape == (U[g].shape[-1] // D, D)
+    hd = 0 if head_dim is None else int(head_dim)
+    assert hd == 0 or (0 < hd <= D and D % hd == 0), "head_dim must divide D"
     params = z + U + (static_w if has_static else [])
-    return _GroupedLowrankDynamicConvolutionFn.apply(x, residual, G, has_static, *params)
+    return _GroupedLowrankDynamicConvolutionFn.apply(x, residual, G, has_static, hd, *params)

@@ -54,15 +54,19 @@ class GroupedLowRankDynamicShortConvolution(nn.Module):
     q|k|v projection of README.md:99-104) and returns G tensors [B, T, d_model],
     group g being what a LowRankDynamicShortConvolution with parameters
     (proj_in.weight[g*R:(g+1)*R], proj_out[g], proj_out_bias[g]) returns for
-    x[..., g*d_model:(g+1)*d_model].
+    x[..., g*d_model:(g+1)*d_model].  With head_dim set the outputs come as
+    [B, d_model // head_dim, T, head_dim] (README.md:106-110's
+    .view(B, T, H, head_dim).transpose(1, 2), written directly).
     """
 
-    def __init__(self, d_model: int, R: int, W: int, groups: int = 3):
+    def __init__(self, d_model: int, R: int, W: int, groups: int = 3, head_dim=None):
         super().__init__()
         _check_rank(R)
         if not 1 <= groups <= 4:
             raise ValueError("groups must be between 1 and 4")
-        self.d_model, self.R, self.W, self.groups = d_model, R, W, groups
+        if head_dim is not None and (head_dim <= 0 or d_model % head_dim != 0):
+            raise ValueError("head_dim must divide d_model")
+        self.d_model, self.R, self.W, self.groups, self.head_dim = d_model, R, W, groups, head_dim
         self.proj_in = nn.Linear(d_model, groups * R, bias=False)
         self.proj_out = nn.Parameter(torch.zeros(groups, R, W * d_model))
         self.proj_out_bias = nn.Parameter(torch.empty(groups, W, d_model))
@@ -74,4 +78,4 @@ class GroupedLowRankDynamicShortConvolution(nn.Module):
         zs = [z[..., g * R:(g + 1) * R].contiguous() for g in range(G)]
         Us = [self.proj_out[g] for g in range(G)]
         sws = [self.proj_out_bias[g] for g in range(G)]
-        return lowrank_dynamic_convolution_grouped(x, zs, Us, static_w=sws, residual=True)
+        return lowrank_dynamic_convolution_grouped(x, zs, Us, static_w=sws, residual=True, head_dim=self.head_dim)

@@ -18,7 +18,9 @@
  *   dc_lowrank_fwd_grouped, dc_lowrank_bwd_grouped
  *                     <- README.md:57-110 (the QKV usage: three lowrank_dynamic_convolution
  *                                              calls, lowrank.py:302-338, on .contiguous()
- *                                              slices of one fused projection)
+ *                                              slices of one fused projection, and the
+ *                                              .view(B, T, H, hd).transpose(1, 2) of
+ *                                              their outputs, README.md:106-110)
  *
  * Conventions
  *   - Every tensor pointer is a DEVICE pointer to a contiguous row-major array:
@@ -49,7 +51,7 @@
 extern "C" {
 #endif
 
-#define DC_ABI_VERSION 2
+#define DC_ABI_VERSION 3
 
 /* Largest convolution width and (kernel) rank accepted. */
 #define DC_MAX_W 8
@@ -125,11 +127,16 @@ int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* stat
  * projection, read in place); z, U, y are arrays of G device pointers, each a
  * contiguous tensor as in dc_lowrank_fwd; static_w is NULL (no static filter in
  * any group) or an array of G non-NULL pointers.  Each group's y equals what
- * dc_lowrank_fwd computes for it.  Replaces the three calls of README.md:57-110
- * (lowrank.py:302-338 each) and the .contiguous() copies of their inputs. */
+ * dc_lowrank_fwd computes for it.  y_hd = 0 writes each y as [B, T, D]; a head
+ * dim y_hd > 0 (D % y_hd == 0) writes it head-major, [B, D/y_hd, T, y_hd]
+ * contiguous: the layout attention reads.  The values are bitwise those of the
+ * [B, T, D] layout when y_hd is a multiple of 64 (fp32) or 8 (bf16 / fp16);
+ * other head dims take the generic kernels (same tolerance).  Replaces the
+ * three calls of README.md:57-110 (lowrank.py:302-338 each), the .contiguous()
+ * copies of their inputs and the head transposes of their outputs. */
 int dc_lowrank_fwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z,
                            const void* const* U, const void* const* static_w, void* const* y,
-                           int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
+                           int64_t y_hd, int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
                            int dtype, int residual, void* stream);
 
 /* Workspace bytes needed by dc_lowrank_bwd_grouped, or a negative dc_status. */
@@ -139,13 +146,16 @@ int64_t dc_lowrank_bwd_grouped_ws_bytes(int64_t G, int64_t B, int64_t T, int64_t
 /* The G backwards of dc_lowrank_fwd_grouped in one pass: group g writes its dx
  * into dx + g*D (rows dx_ld >= G*D elements apart: the gradient of the fused
  * projection, written in place), and dz[g], dU[g] (and dstatic_w[g]) as
- * dc_lowrank_bwd does; dy is an array of G contiguous [B, T, D] gradients.
- * dstatic_w is NULL exactly when static_w is.  Per group, results are bitwise
- * those of dc_lowrank_bwd.  Replaces README.md:57-110's three backwards
- * (lowrank.py:251-299 each) and the concatenation of dq, dk, dv. */
+ * dc_lowrank_bwd does; dy is an array of G contiguous gradients, [B, T, D]
+ * when dy_hd = 0 and head-major [B, D/dy_hd, T, dy_hd] otherwise (the layout
+ * of dc_lowrank_fwd_grouped's y_hd).  dstatic_w is NULL exactly when static_w
+ * is.  Per group, results are bitwise those of dc_lowrank_bwd (with a head
+ * dim: when it is a multiple of 64, else the generic kernels).  Replaces
+ * README.md:57-110's three backwards (lowrank.py:251-299 each) and the
+ * concatenation of dq, dk, dv. */
 int dc_lowrank_bwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z,
                            const void* const* U, const void* const* static_w,
-                           const void* const* dy, void* dx, int64_t dx_ld,
+                           const void* const* dy, int64_t dy_hd, void* dx, int64_t dx_ld,
                            void* const* dz, void* const* dU, void* const* dstatic_w,
                            void* workspace, int64_t ws_bytes,
                            int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,

@@ -43,7 +43,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_strings(lib):
-    assert lib.dc_abi_version() == 2
+    assert lib.dc_abi_version() == 3
     for s in (OK, E_NULL, E_SHAPE, E_DTYPE, E_UNSUP, E_WS, E_ALIGN, E_DEV, E_LAUNCH):
         assert len(lib.dc_status_string(s)) > 0
     assert b"unknown" in lib.dc_status_string(-99)
@@ -123,11 +123,11 @@ def arr(*ptrs):
     return (ctypes.c_void_p * len(ptrs))(*ptrs)
 
 
-def lr_fwd_g(lib, G=3, x=P, x_ld=48, z="ok", U="ok", sw=None, y="ok", B=2, T=8, D=16, R=4, W=4, dt=0):
+def lr_fwd_g(lib, G=3, x=P, x_ld=48, z="ok", U="ok", sw=None, y="ok", y_hd=0, B=2, T=8, D=16, R=4, W=4, dt=0):
     z = arr(*[P] * G) if z == "ok" else z
     U = arr(*[P] * G) if U == "ok" else U
     y = arr(*[P] * G) if y == "ok" else y
-    return lib.dc_lowrank_fwd_grouped(G, x, x_ld, z, U, sw, y, B, T, D, R, W, dt, 0, None)
+    return lib.dc_lowrank_fwd_grouped(G, x, x_ld, z, U, sw, y, y_hd, B, T, D, R, W, dt, 0, None)
 
 
 def test_lowrank_grouped_fwd_validation(lib):
@@ -144,8 +144,13 @@ def test_lowrank_grouped_fwd_validation(lib):
     assert lr_fwd_g(lib, sw=arr(P, P, None)) == E_NULL      # static_w for every group or none
     assert lr_fwd_g(lib, U=arr(P, P + 1, P)) == E_ALIGN
     assert lr_fwd_g(lib, x=P + 1) == E_ALIGN
+    assert lr_fwd_g(lib, y_hd=-1) == E_SHAPE               # head dims: D % y_hd == 0, y_hd <= D
+    assert lr_fwd_g(lib, y_hd=5) == E_SHAPE
+    assert lr_fwd_g(lib, y_hd=32) == E_SHAPE
     if no_dev:
         assert lr_fwd_g(lib) == E_DEV
+        assert lr_fwd_g(lib, y_hd=4) == E_DEV               # head-major y [B, 4, T, 4]
+        assert lr_fwd_g(lib, y_hd=16) == E_DEV
         assert lr_fwd_g(lib, G=1, x_ld=16, sw=arr(P)) == E_DEV
         assert lr_fwd_g(lib, G=4, x_ld=100, sw=arr(P, P, P, P)) == E_DEV
 
@@ -159,8 +164,8 @@ def test_lowrank_grouped_bwd_validation(lib):
     assert lib.dc_lowrank_bwd_grouped_ws_bytes(3, 2, 8, 16, 0, 4, 0, 1) == E_SHAPE
     g3 = arr(P, P, P)
 
-    def call(G=3, x_ld=48, dx_ld=48, sw=None, dsw=None, ws=P, nws=need, dz=g3, dy=g3):
-        return lib.dc_lowrank_bwd_grouped(G, P, x_ld, g3, g3, sw, dy, P, dx_ld, dz, g3, dsw, ws, nws,
+    def call(G=3, x_ld=48, dx_ld=48, sw=None, dsw=None, ws=P, nws=need, dz=g3, dy=g3, dy_hd=0):
+        return lib.dc_lowrank_bwd_grouped(G, P, x_ld, g3, g3, sw, dy, dy_hd, P, dx_ld, dz, g3, dsw, ws, nws,
                                           2, 8, 16, 4, 4, 0, 0, None)
 
     assert call(G=5) == E_UNSUP
@@ -173,5 +178,8 @@ def test_lowrank_grouped_bwd_validation(lib):
     assert call(sw=g3, dsw=g3, ws=None) == E_WS
     assert call(sw=g3, dsw=g3, nws=need - 256) == E_WS
     assert call(sw=g3, dsw=g3, ws=P + 16) == E_WS           # workspace shares start 256-byte aligned
+    assert call(dy_hd=3) == E_SHAPE                         # D % dy_hd != 0
+    assert call(dy_hd=-2) == E_SHAPE
     if no_dev:
         assert call(sw=g3, dsw=g3) == E_DEV
+        assert call(sw=g3, dsw=g3, dy_hd=8) == E_DEV

@@ -206,3 +206,83 @@ def test_readme_module_against_oracle():
     assert_ns(x.grad, xr.grad, dtype, "dx")
     assert_ns(m.proj_out.grad, Ur.grad, dtype, "dU", elementwise=False)
     assert_ns(m.proj_out_bias.grad, sr.grad, dtype, "dstatic_w", elementwise=False)
+
+
+# ------------------------------------------------------ head-major outputs
+HEAD_CASES = [
+    # G, B, T, D, R, W, static, head_dim, dtype, bitwise (fast kernels in both layouts)
+    (3, 2, 70, 256, 15, 4, True, 64, torch.bfloat16, True),    # T % 16 != 0: the last tile's rows past T
+    (3, 1, 96, 256, 16, 4, False, 128, torch.bfloat16, True),
+    (2, 2, 50, 128, 31, 3, True, 64, torch.float16, True),     # two rank chunks
+    (3, 2, 45, 128, 15, 4, True, 64, torch.float32, True),     # fp32 VALU kernels
+    (3, 2, 40, 128, 15, 4, True, 32, torch.bfloat16, False),   # head dim 32: generic backward
+    (2, 1, 33, 64, 7, 2, True, 16, torch.float32, False),      # fp32 head dim 16: generic kernels
+]
+
+
+@pytest.mark.parametrize("G,Bn,Tn,Dn,R,W,static,hd,dtype,bitwise", HEAD_CASES)
+def test_grouped_head_major(G, Bn, Tn, Dn, R, W, static, hd, dtype, bitwise):
+    """head_dim writes y as y.view(B, T, H, hd).transpose(1, 2) and takes dy in that layout."""
+    H = Dn // hd
+    xw, zs, Us, sws, dys = _inputs(G, Bn, Tn, Dn, R, W, static, 0, seed=Tn * 7 + hd + Dn)
+    dyk = [d.to(dtype).to(DEV) for d in dys]
+
+    def run(head_dim):
+        x = _leaf(xw, dtype)
+        zk = [_leaf(t, dtype) for t in zs]
+        Uk = [_leaf(t, dtype) for t in Us]
+        sk = [_leaf(t, dtype) for t in sws] if static else None
+        ys = lr_grouped(x, zk, Uk, sk, residual=True, head_dim=head_dim)
+        if head_dim is None:
+            grads = dyk
+        else:
+            grads = [d.view(Bn, Tn, H, hd).transpose(1, 2).contiguous() for d in dyk]
+        torch.autograd.backward(ys, grads)
+        torch.cuda.synchronize()
+        return ys, x.grad, [t.grad for t in zk], [t.grad for t in Uk], [t.grad for t in sk] if static else []
+
+    ys_h, dx_h, dz_h, dU_h, ds_h = run(hd)
+    for y in ys_h:
+        assert y.shape == (Bn, H, Tn, hd) and y.is_contiguous()
+    if bitwise:
+        ys_t, dx_t, dz_t, dU_t, ds_t = run(None)
+        for g in range(G):
+            assert torch.equal(ys_h[g], ys_t[g].view(Bn, Tn, H, hd).transpose(1, 2)), f"group {g}: y"
+            assert torch.equal(dz_h[g], dz_t[g]), f"group {g}: dz"
+            assert torch.equal(dU_h[g], dU_t[g]), f"group {g}: dU"
+            if static:
+                assert torch.equal(ds_h[g], ds_t[g]), f"group {g}: dstatic_w"
+        assert torch.equal(dx_h, dx_t), "dx"
+        return
+    for g in range(G):
+        xs = xw[..., g * Dn:(g + 1) * Dn].to(dtype).float().requires_grad_()
+        zr = zs[g].to(dtype).float().requires_grad_()
+        Ur = Us[g].to(dtype).float().requires_grad_()
+        sr = sws[g].to(dtype).float().requires_grad_() if static else None
+        yr = lr_ref(xs, zr, Ur, sr, residual=True)
+        yr.backward(dys[g].to(dtype).float())
+        assert_ns(ys_h[g].transpose(1, 2).reshape(Bn, Tn, Dn), yr, dtype, f"g{g} y")
+        assert_ns(dx_h[..., g * Dn:(g + 1) * Dn], xs.grad, dtype, f"g{g} dx")
+        assert_ns(dz_h[g], zr.grad, dtype, f"g{g} dz", elementwise=False)
+        assert_ns(dU_h[g], Ur.grad, dtype, f"g{g} dU", elementwise=False)
+        if static:
+            assert_ns(ds_h[g], sr.grad, dtype, f"g{g} dstatic_w", elementwise=False)
+
+
+def test_module_head_major():
+    """GroupedLowRankDynamicShortConvolution(head_dim=...) returns the README's q.view(...).transpose(1, 2)."""
+    from dynconv import GroupedLowRankDynamicShortConvolution
+
+    torch.manual_seed(2)
+    Dm, R, W, G, Bn, Tn, hd = 256, 15, 4, 3, 2, 64, 64
+    dtype = torch.bfloat16
+    a = GroupedLowRankDynamicShortConvolution(Dm, R, W, groups=G).to(DEV, dtype)
+    b = GroupedLowRankDynamicShortConvolution(Dm, R, W, groups=G, head_dim=hd).to(DEV, dtype)
+    with torch.no_grad():
+        a.proj_out.normal_(0, 1 / math.sqrt((R + 1) * W))
+        b.load_state_dict(a.state_dict())
+    pre_z = torch.randn(Bn, Tn, Dm, device=DEV, dtype=dtype)
+    qkv = torch.randn(Bn, Tn, G * Dm, device=DEV, dtype=dtype)
+    outs_a, outs_b = a(qkv, pre_z), b(qkv, pre_z)
+    for g in range(G):
+        assert torch.equal(outs_b[g], outs_a[g].view(Bn, Tn, Dm // hd, hd).transpose(1, 2))
