@@ -9,6 +9,9 @@ the three B4 T4096 D2048 W4 bf16 configurations of BASELINE.json:
     hw_hs1   headwise, head_size 1 (H 2048), static_w, residual   (configs[1])
     hw_hs32  headwise, head_size 32 (H 64), static_w, residual    (configs[2])
     lr_r16   lowrank, R 16, no static_w, residual                  (configs[3])
+The three forwards run first, then the backwards as a training step's
+loss.backward() would: hw_hs32 and lr_r16 in one autograd call, hw_hs1 (the
+roofline launch) in a second one between events.
 `value` = algorithmic bytes of one step (each input read once, each output
 written once, at bf16) x steps / timed seconds, in GB/s.  Inputs are
 synthetic (BASELINE.json distributions, CPU generator seed 0) and resident in
@@ -388,35 +391,39 @@ def main():
     ROOF = "hw_hs1"  # the dominant launch: its backward is bracketed by events in the timed loop
     roof_ev = []
 
-    def fwdbwd(name, timed=False):
-        c = CONFIGS[name]
-        a, dy = data[name]
-        for t in a:
-            if t is not None:
-                t.grad = None
-        fn = hw if c["kind"] == "hw" else lr
-        y = fn(*a, residual=c["residual"])
-        if timed and name == ROOF:
+    def step(timed=False):
+        """Forward of every config, then the backwards, as a training step's loss.backward() would run
+        them: one autograd call for the others, and one for the roofline config between events."""
+        ys, dys = {}, {}
+        for name in STEP:
+            c = CONFIGS[name]
+            a, dys[name] = data[name]
+            for t in a:
+                if t is not None:
+                    t.grad = None
+            fn = hw if c["kind"] == "hw" else lr
+            ys[name] = fn(*a, residual=c["residual"])
+        rest = [n for n in STEP if n != ROOF]
+        torch.autograd.backward([ys[n] for n in rest], [dys[n] for n in rest])
+        if timed:
             # events on the stream the backward kernels are launched on (torch's current stream)
             b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             b0.record()
-            y.backward(dy)
+            ys[ROOF].backward(dys[ROOF])
             b1.record()
             roof_ev.append((b0, b1))
         else:
-            y.backward(dy)
+            ys[ROOF].backward(dys[ROOF])
 
     step_bytes = sum(sum(alg_bytes(CONFIGS[n])) for n in STEP)
     for _ in range(args.warmup):
-        for n in STEP:
-            fwdbwd(n)
+        step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s_ev.record()
     for _ in range(args.steps):
-        for n in STEP:
-            fwdbwd(n, timed=True)
+        step(timed=True)
     e_ev.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0

@@ -116,11 +116,9 @@ __global__ __launch_bounds__(256) void lr_fwd_mfma(LrArgs a) {
   const int lane_off = chv ? ((yh * Tn + 4 * q) * yhd + dl - yh * yhd) * 2 : kOobLane;  // y: the lane's row 4q octet
   const int xlane_off = chv ? (4 * q * a.xld + dl) * 2 : kOobLane;   // the same in x
 
-  // Tile inputs (rows out of the sequence read as 0).  Two buffers, A and B,
-  // alternate: while one tile is computed the next one's loads are in flight.
-  // The loads are unconditional (a tile past the run reads the out-of-range
-  // offset kOobTile, which returns 0 and touches no memory) and no register
-  // is copied, so the compiler's waits stay partial (vmcnt(N), not vmcnt(0)).
+  // Tile inputs (rows out of the sequence read as 0).  The loads are
+  // unconditional (a tile past the run reads the out-of-range offset
+  // kOobTile, which returns 0 and touches no memory).
   auto load_tile = [&](int tile, u32x4(&xr)[NR], ZR& zr) {
     const bool live = tile < tile1;
     const int toff = live ? tile * 16 * xrowb : kOobTile;
@@ -167,21 +165,28 @@ __global__ __launch_bounds__(256) void lr_fwd_mfma(LrArgs a) {
     }
   };
 
-  u32x4 xa[NR], xb[NR];
-  ZR za, zb;
-  load_tile(tile0, xa, za);
-  for (int tile = tile0; tile < tile1; tile += 2) {
-    load_tile(tile + 1, xb, zb);
-    __builtin_amdgcn_sched_barrier(0);  // issue the next tile's loads before this tile's waits
-    compute_tile(tile, xa, za);
-    load_tile(tile + 2, xa, za);
-    __builtin_amdgcn_sched_barrier(0);
-    if (tile + 1 < tile1) compute_tile(tile + 1, xb, zb);
+  // One tile in flight per wavefront: at 114-125 VGPRs the kernel runs 4
+  // wavefronts per SIMD, which hide the loads better than a second tile
+  // buffer at 3 wavefronts (B4 T4096 D2048 R16: 32.3 -> 31.4 us).
+  for (int tile = tile0; tile < tile1; ++tile) {
+    u32x4 xr[NR];
+    ZR zr;
+    load_tile(tile, xr, zr);
+    compute_tile(tile, xr, zr);
   }
 }
 
 // ------------------------------------------------------------------- host
 namespace {
+
+// Wavefronts per problem: runs of about 8 tiles, at most 4096 wavefronts
+// (4 per SIMD).  B4 T4096 D2048: 2048 wavefronts (31.4 us, 31.9 at 4096);
+// B2 T8192 D4096: 4096 (61.8 us, 64.0 at 2048).
+int fwd_target_waves(const LrProblem& p) {
+  const int64_t tiles = p.B * ((p.T + 15) / 16) * ((p.D + 127) / 128);
+  const int64_t w = tiles / 8;
+  return (int)(w < 1 ? 1 : w > 4096 ? 4096 : w);
+}
 
 LrArgs make_args(const LrProblem& p, int target_waves) {
   LrArgs a;
@@ -207,7 +212,7 @@ LrArgs make_args(const LrProblem& p, int target_waves) {
 
 template <typename T, int W, int RC>
 hipError_t launch_fwd(const LrProblem* p, int G) {
-  LrArgs a = make_args(p[0], 2048);
+  LrArgs a = make_args(p[0], fwd_target_waves(p[0]));
   a.nblk1 = a.nblk;
   a.nblk = G * a.nblk1;
   a.xld = (int)p[0].xld();
