@@ -96,7 +96,7 @@ __device__ __forceinline__ float q4f(const u32x2& v, int j) {
 // values), rows past T and channels past D (lane offset kOobLane) read 0 and
 // drop stores, without branches or clamped addresses.  The host takes these
 // paths only when (T + kSeqSlackRows) rows of a sequence span at most
-// kMaxSeqBytes: every offset a kernel forms (rows -7 .. T + 25, plus kOobLane)
+// kMaxSeqBytes: every offset a kernel forms (rows -7 .. T + 30, plus kOobLane)
 // then stays below 2^31, and every wrapped negative offset stays above
 // kMaxSeqBytes.
 constexpr int kOobLane = 0x40000000;

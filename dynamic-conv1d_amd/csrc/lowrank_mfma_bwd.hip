@@ -17,15 +17,18 @@ namespace dc {
 //   * dU[r, kD+d] += sum_t z_eff[t, r] G_k[t, d]: MFMA with K = the 16 rows.
 //     For each j the lane's four G values of column NJ*n+j are exactly the
 //     B operand (rows 4q..4q+3 of column n); A is z_eff transposed.
-//   * dz[t, r] += sum_d G_k[t, d] U_eff[r, kD+d]: needs K = channels.  The
-//     same packed G registers fed as the *A* operand of an MFMA against the
-//     16x16 identity return G transposed (lane now holds one row and four
-//     channels 4(4q+i)+j), which is the A operand of the dz MFMA.  All
-//     values are bf16-exact, so the transpose is exact.
-//   * dx[t, d] = sum_k dy[t+k, d] Kw[t+k, k, d] (+ dy): the tap weights of
-//     rows 4q..4q+3+W-1 come from NB = ceil((W+3)/4) MFMA row blocks (A rows
-//     shifted by 4), so every lane has the look-ahead rows it needs without
-//     cross-lane traffic; dy rows 4q..4q+W+2 are read from L1.
+//   * dz[t, r] += sum_d G_k[t, d] U_eff[r, kD+d]: needs K = channels.  Each
+//     wavefront writes its G tile row-major into its own LDS slot and reads
+//     it back channel-contiguous (one row, 8 channels per lane), the A operand
+//     of a 16x16x32 MFMA.  All values are bf16-exact, so this is exact.
+//   * dx[t, d] = sum_k dy[t+k, d] Kw[t+k, k, d] (+ dy).  For 2 <= W <= 4 in
+//     scatter form: a lane takes the tap weights of its own rows 4q..4q+3
+//     (one MFMA row block) and adds dy[s] Kw[s, k] to dx row s-k; the sums
+//     for rows of the group above (s-k < 4q) go to that group with one
+//     ds_bpermute each, and group 3's rows wait one tile for group 0's sums
+//     of the next tile.  Otherwise in gather form: the tap weights of rows
+//     4q..4q+3+W-1 come from NB = ceil((W+3)/4) row blocks (A rows shifted by
+//     4) and dy rows 4q..4q+W+2 are read from L1.
 // A workgroup is NRW row runs x NCW = 256/CPW wavefronts on NCW adjacent
 // channel chunks of the same rows.  dz partial sums over the 256 channels are
 // added in LDS in wave order, once per batch of tiles, and written as one fp32
@@ -161,8 +164,14 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   static_assert(CPW == 64 || CPW == 32, "64- or 32-channel tiles");
   static_assert(NRW == 1 || (RC == 1 && W <= 4 && CPW == 64), "two runs per workgroup: one rank chunk, W <= 4");
   typedef LaneVec<NJ> LV;
-  constexpr int NB = (W + 6) / 4;  // MFMA row blocks for the dx look-ahead
-  constexpr int NR = W + 3;        // x rows 4q-W+1 .. 4q+3 and dy rows 4q .. 4q+W+2 per lane
+  // dx in scatter form for 2 <= W <= 4 (SC): tap weights of the lane's own rows
+  // only, partial sums for the rows of the group above passed across lanes.
+  // Otherwise (gather form) NB row blocks of tap weights cover the look-ahead.
+  constexpr bool SC = W >= 2 && W <= 4;
+  constexpr int NB = SC ? 1 : (W + 6) / 4;  // MFMA row blocks of tap weights
+  constexpr int NR = W + 3;                 // x rows 4q-W+1 .. 4q+3 per lane
+  constexpr int NDY = SC ? 4 : W + 3;       // dy rows 4q .. 4q+NDY-1 per lane
+  constexpr int NSC = SC ? W - 1 : 1;       // scatter partial sums per channel
   constexpr bool UWREG = W * RC <= 8;   // tap-weight operands in registers
   constexpr int NUW = W * RC * NJ;  // packed tap-weight operands per lane
   constexpr int NUZ = W * RC * NS;  // dz operands per lane
@@ -273,20 +282,85 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   // reads the out-of-range offset kOobTile: 0, no memory traffic) and no
   // register is copied, so the compiler's waits stay partial (vmcnt(N)).
   struct TileIn {
-    typename LV::type xr[NR], dyr[NR];
+    typename LV::type xr[NR], dyr[NDY];
     ZR zr[NB];  // z_eff rows t0+4bb+n, ranks 16c+4q..+3: A operand of the tap-weight MFMA
   };
   auto load_tile = [&](int tile, TileIn& in) {
     const bool live = tile < tile1;
+    // The scatter form also reads dy and z of the tile after the run: its
+    // first rows close the run's last dx rows.
+    const bool ylive = SC ? tile <= tile1 : live;
     const int xtoff = live ? tile * 16 * xrowb : kOobTile;
-    const int toff = live ? tile * 16 * rowb : kOobTile;
+    const int toff = ylive ? tile * 16 * rowb : kOobTile;
 #pragma unroll
-    for (int m = 0; m < NR; ++m) {
-      in.xr[m] = LV::load(rx, xlane_off + xtoff + (m - (W - 1)) * xrowb);
-      in.dyr[m] = LV::load(rdy, lane_off + toff + m * rowb);
+    for (int m = 0; m < NR; ++m) in.xr[m] = LV::load(rx, xlane_off + xtoff + (m - (W - 1)) * xrowb);
+#pragma unroll
+    for (int m = 0; m < NDY; ++m) in.dyr[m] = LV::load(rdy, lane_off + toff + m * rowb);
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) in.zr[bb].load(rz, ylive ? (tile * 16 + 4 * bb + n) * R * 2 : kOobTile, R, q);
+  };
+
+  // Scatter form: S[m] holds the lane's contributions to row 4q-1-m (the group
+  // above).  Each group passes S to the group above (lane - 16) and takes the
+  // group below's for its rows 4q+3-m; group 3 takes group 0's, which belong
+  // to rows 15-m of the tile before.  Groups 0-2 then store this tile's rows
+  // 4q..4q+3.  Group 3 stores this tile's rows 12 .. 15-NSC (complete) and the
+  // tile before's rows 16-NSC .. 15, held in `carry`, and carries this tile's.
+  // Rows outside [tile0, tile1) are not stored.
+  constexpr int NOPEN = NSC;  // rows of group 3 that wait for the next tile
+  float carry[NOPEN][NJ];
+#pragma unroll
+  for (int i = 0; i < NOPEN; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) carry[i][j] = 0.f;
+  auto close_rows = [&](const float(&own)[4][NJ], const float(&S)[NSC][NJ], int tile) {
+    const int src = ((lane + 16) & 63) << 2;  // ds_bpermute byte index of the group below
+    float recv[NSC][NJ];
+#pragma unroll
+    for (int m = 0; m < NSC; ++m)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        recv[m][j] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(S[m][j])));
+    const bool top = q == 3;
+    const bool cur_live = tile < tile1;
+    const bool prev_live = tile > tile0 && tile <= tile1;
+    const int cur_off = cur_live ? dxlane_off + tile * 16 * dxrowb : kOobTile;
+    const int prev_off = prev_live ? dxlane_off + (tile - 1) * 16 * dxrowb : kOobTile;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      constexpr int kFirstOpen = 4 - NOPEN;
+      const bool open = i >= kFirstOpen;  // rows that take the group below's sums
+      float v[NJ];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        float b = own[i][j];
+        if (open) b = (top ? carry[i - kFirstOpen][j] : b) + recv[3 - i][j];
+        v[j] = b;
+      }
+      LV::store(LV::template pack<T>(v), rdx, (top && open ? prev_off : cur_off) + i * dxrowb);
     }
 #pragma unroll
-    for (int bb = 0; bb < NB; ++bb) in.zr[bb].load(rz, live ? (tile * 16 + 4 * bb + n) * R * 2 : kOobTile, R, q);
+    for (int i = 0; i < NOPEN; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) carry[i][j] = own[4 - NOPEN + i][j];
+  };
+  // Tap weights of the lane's rows 4q..4q+3 (row block 0) times dy: into
+  // `own` for rows of the lane, into S for rows of the group above.
+  auto scatter_taps = [&](const u32x2(&zA0)[RC], const float(&dyf)[NDY][NJ], int k, int j, float(&own)[4][NJ],
+                          float(&S)[NSC][NJ]) {
+    f32x4 wk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < RC; ++c)
+      wk = Mma16<T>::run(zA0[c], UWREG ? uw_reg[UWREG ? (k * RC + c) * NJ + j : 0]
+                                       : my_uw[((k * RC + c) * NJ + j) * 64 + lane], wk);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = i - k;  // dx row of this contribution, relative to 4q
+      if (r >= 0)
+        own[r][j] = fmaf(dyf[i][j], wk[i], own[r][j]);
+      else
+        S[-r - 1][j] = fmaf(dyf[i][j], wk[i], S[-r - 1][j]);
+    }
   };
   auto compute_tile = [&](int it, const TileIn& in) {
     const int tile = tile0 + it;
@@ -294,7 +368,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     const int t0 = tile * 16;
     const int dxtoff = live ? t0 * dxrowb : kOobTile;  // tiles past the run store nothing
     const typename LV::type(&xr)[NR] = in.xr;
-    const typename LV::type(&dyr)[NR] = in.dyr;
+    const typename LV::type(&dyr)[NDY] = in.dyr;
     u32x2 zA[NB][RC];
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb) in.zr[bb].finish(zA[bb], t0 + 4 * bb + n, R, RK, Tn, q);
@@ -308,17 +382,21 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
       zT[c][1] = pack2<T>(tz[2], tz[3]);
     }
 
-    float dyf[NR][NJ];
+    float dyf[NDY][NJ];
 #pragma unroll
-    for (int m = 0; m < NR; ++m)
+    for (int m = 0; m < NDY; ++m)
 #pragma unroll
       for (int j = 0; j < NJ; ++j) dyf[m][j] = Mma16<T>::to_f(LV::elem(dyr[m], j));
 
-    float dxa[4][NJ];
+    float dxa[4][NJ], S[NSC][NJ];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < NJ; ++j) dxa[i][j] = 0.f;
+#pragma unroll
+    for (int m = 0; m < NSC; ++m)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) S[m][j] = 0.f;
     f32x4 dz[RC];
 #pragma unroll
     for (int c = 0; c < RC; ++c) dz[c] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -338,9 +416,10 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
         *reinterpret_cast<typename LV::type*>(my_g + (4 * q + i) * GROW + NJ * n) = LV::template pack<T>(gf[i]);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        // dx += dy[4q+i+k] * Kw[4q+i+k, k]: tap weights of the row blocks that hold rows k..k+3.
+        if constexpr (SC) scatter_taps(zA[0], dyf, k, j, dxa, S);
+        // Gather form: dx += dy[4q+i+k] * Kw[4q+i+k, k] from the row blocks that hold rows k..k+3.
 #pragma unroll
-        for (int bb = 0; bb < NB; ++bb) {
+        for (int bb = 0; bb < (SC ? 0 : NB); ++bb) {
           if (4 * bb > 3 + k || 4 * bb + 3 < k) continue;
           f32x4 wk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -369,13 +448,18 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
       }
     }
 
-    // ---- dx rows 4q..4q+3 (+ residual dy); out-of-range stores are dropped
+    // ---- dx rows (+ residual dy); out-of-range stores are dropped
+    if (a.residual) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float v[NJ];
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) v[j] = a.residual ? dxa[i][j] + dyf[i][j] : dxa[i][j];
-      LV::store(LV::template pack<T>(v), rdx, dxlane_off + dxtoff + i * dxrowb);
+        for (int j = 0; j < NJ; ++j) dxa[i][j] += dyf[i][j];
+    }
+    if constexpr (SC) {
+      close_rows(dxa, S, tile);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) LV::store(LV::template pack<T>(dxa[i]), rdx, dxlane_off + dxtoff + i * dxrowb);
     }
     // ---- dz: gather this wavefront's tile sums; every DZB iterations (and at the
     // last one) add each run's NCW chunk wavefronts in wave order, one partial per group.
@@ -416,6 +500,38 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     load_tile(tile0 + it + 2, ta);
     __builtin_amdgcn_sched_barrier(0);
     if (it + 1 < nit) compute_tile(it + 1, tb);
+  }
+  if constexpr (SC) {
+    // The tile after the longest run (loaded into the buffer that is next in
+    // turn) closes that run's last rows; in shorter runs it lies past tile1
+    // and stores nothing.
+    auto flush = [&](const TileIn& in) {
+      const int tile = tile0 + nit;
+      u32x2 zA0[RC];
+      in.zr[0].finish(zA0, tile * 16 + n, R, RK, Tn, q);
+      float dyf[NDY][NJ], own[4][NJ], S[NSC][NJ];
+#pragma unroll
+      for (int m = 0; m < NDY; ++m)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) dyf[m][j] = Mma16<T>::to_f(LV::elem(in.dyr[m], j));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) own[i][j] = 0.f;
+#pragma unroll
+      for (int m = 0; m < NSC; ++m)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) S[m][j] = 0.f;
+#pragma unroll
+      for (int k = 1; k < W; ++k)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) scatter_taps(zA0, dyf, k, j, own, S);
+      close_rows(own, S, tile);
+    };
+    if (nit & 1)
+      flush(tb);
+    else
+      flush(ta);
   }
 
   if constexpr (NRW == 2) {
