@@ -473,18 +473,22 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
       __syncthreads();
       constexpr int PER_RUN = RC * 256;
       const int per_batch = (slot + 1) * PER_RUN;
-      for (int e = threadIdx.x; e < NRW * per_batch; e += 64 * NW) {
-        const int ri = e / per_batch, e2 = e - ri * per_batch;
-        const int sl = e2 / PER_RUN, rem = e2 - sl * PER_RUN;
-        const int c = rem >> 8, rr = (rem >> 4) & 15, nn = rem & 15;
-        const int r = 16 * c + nn;
-        const Run& ru = ri == 0 ? runs[0] : runs[NRW - 1];
-        const int ti = ru.tile0 + it - slot + sl;  // the slot's tile of run ri
-        const int t = ti * 16 + rr;
-        float v = dzred[buf][ri][0][sl][rem];
 #pragma unroll
-        for (int w2 = 1; w2 < NCW; ++w2) v += dzred[buf][ri][w2][sl][rem];
-        if (ti < ru.tile1 && r < R && t < Tn) part_dz[((int64_t)cg * a.BT + ru.row0 + t) * R + r] = v;
+      for (int ri = 0; ri < NRW; ++ri) {
+        const Run& ru = ri == 0 ? runs[0] : runs[NRW - 1];
+        float* __restrict__ out = part_dz + ((int64_t)cg * a.BT + ru.row0) * R;  // row 0 of run ri's sequence
+        const int tb = ru.tile0 + it - slot;  // run ri's tile of slot 0
+        for (int e2 = threadIdx.x; e2 < per_batch; e2 += 64 * NW) {
+          const int sl = e2 / PER_RUN, rem = e2 - sl * PER_RUN;
+          const int c = rem >> 8, rr = (rem >> 4) & 15, nn = rem & 15;
+          const int r = 16 * c + nn;
+          const int ti = tb + sl;  // the slot's tile of run ri
+          const int t = ti * 16 + rr;
+          float v = dzred[buf][ri][0][sl][rem];
+#pragma unroll
+          for (int w2 = 1; w2 < NCW; ++w2) v += dzred[buf][ri][w2][sl][rem];
+          if (ti < ru.tile1 && r < R && t < Tn) out[t * R + r] = v;
+        }
       }
     }
   };
