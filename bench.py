@@ -55,6 +55,16 @@ for _p in (ROOT, os.path.join(ROOT, "dynamic-conv1d_amd")):
 METRIC = "fwd+bwd ms & HBM GB/s (% peak), B4 T4096 D2048 W4 bf16, headwise+lowrank"
 PEAK_GBS = 8000.0  # MI355X HBM3E
 BF16 = 2
+# element size and C-ABI dtype code of a config's "dtype" (bf16 unless stated)
+DTYPES = {"bf16": (2, 0), "fp16": (2, 1), "fp32": (4, 2)}
+
+
+def esize(c):
+    return DTYPES[c.get("dtype", "bf16")][0]
+
+
+def dcode(c):
+    return DTYPES[c.get("dtype", "bf16")][1]
 
 CONFIGS = {
     "hw_hs1": dict(kind="hw", B=4, T=4096, D=2048, H=2048, W=4, static=True, residual=True),
@@ -65,6 +75,9 @@ EXTRA = {
     "lr_qkv": dict(kind="lr", B=2, T=8192, D=4096, R=31, W=4, static=True, residual=True, calls=3),
     "lr_qkv_grouped": dict(kind="lrg", B=2, T=8192, D=4096, R=31, W=4, static=True, residual=True, G=3,
                            head_dim=128),
+    # the fp32 tier (reference test.py's 1e-5 cases) at the B4 shapes
+    "hw_hs32_fp32": dict(kind="hw", B=4, T=4096, D=2048, H=64, W=4, static=True, residual=True, dtype="fp32"),
+    "lr_r16_fp32": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=4, static=False, residual=True, dtype="fp32"),
 }
 STEP = ["hw_hs1", "hw_hs32", "lr_r16"]
 
@@ -74,13 +87,14 @@ def alg_bytes(c):
     if c["kind"] == "lrg":
         f, b = alg_bytes(dict(c, kind="lr"))
         return c["G"] * f, c["G"] * b
-    x = c["B"] * c["T"] * c["D"] * BF16
-    sw = c["W"] * c["D"] * BF16 if c["static"] else 0
+    e = esize(c)
+    x = c["B"] * c["T"] * c["D"] * e
+    sw = c["W"] * c["D"] * e if c["static"] else 0
     if c["kind"] == "hw":
-        w = c["B"] * c["T"] * c["H"] * c["W"] * BF16
+        w = c["B"] * c["T"] * c["H"] * c["W"] * e
         return 2 * x + w + sw, 3 * x + 2 * w + 2 * sw
-    z = c["B"] * c["T"] * c["R"] * BF16
-    U = c["R"] * c["W"] * c["D"] * BF16
+    z = c["B"] * c["T"] * c["R"] * e
+    U = c["R"] * c["W"] * c["D"] * e
     return 2 * x + z + U + sw, 3 * x + 2 * z + 2 * U + 2 * sw
 
 
@@ -162,12 +176,13 @@ def n_sets(c):
 
 
 def abi_sets(c, torch, dev):
-    """`n_sets(c)` sets of bf16 inputs (device-generated, BASELINE scales) with preallocated outputs."""
+    """`n_sets(c)` sets of inputs (device-generated, BASELINE scales, the config's dtype) with outputs."""
     from dynconv import _capi
 
     lib = _capi.load()
     B, T, D, W = c["B"], c["T"], c["D"], c["W"]
-    bf = torch.bfloat16
+    bf = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[c.get("dtype", "bf16")]
+    dt = dcode(c)
     sets = []
     if c["kind"] == "lrg":
         G, R = c["G"], c["R"]
@@ -184,7 +199,7 @@ def abi_sets(c, torch, dev):
             d["dzs"] = [torch.empty_like(z) for z in d["zs"]]
             d["dUs"] = [torch.empty_like(u) for u in d["Us"]]
             d["dsws"] = [torch.empty_like(s) for s in d["sws"]] if c["static"] else None
-            d["nws"] = lib.dc_lowrank_bwd_grouped_ws_bytes(G, B, T, D, R, W, 0, int(c["static"]))
+            d["nws"] = lib.dc_lowrank_bwd_grouped_ws_bytes(G, B, T, D, R, W, dt, int(c["static"]))
             d["ws"] = torch.empty(max(d["nws"], 1), dtype=torch.uint8, device=dev)
             sets.append(d)
         return sets
@@ -194,13 +209,13 @@ def abi_sets(c, torch, dev):
         if c["kind"] == "hw":
             d["w"] = (torch.randn(B, T, c["H"], W, device=dev) / math.sqrt(W)).to(bf)
             d["dw"] = torch.empty_like(d["w"])
-            nws = lib.dc_headwise_bwd_ws_bytes(B, T, D, c["H"], W, 0, int(c["static"]))
+            nws = lib.dc_headwise_bwd_ws_bytes(B, T, D, c["H"], W, dt, int(c["static"]))
         else:
             rk = c["R"] + (1 if c["static"] else 0)
             d["z"] = torch.randn(B, T, c["R"], device=dev).to(bf)
             d["U"] = (torch.randn(c["R"], W * D, device=dev) / math.sqrt(rk * W)).to(bf)
             d["dz"], d["dU"] = torch.empty_like(d["z"]), torch.empty_like(d["U"])
-            nws = lib.dc_lowrank_bwd_ws_bytes(B, T, D, c["R"], W, 0, int(c["static"]))
+            nws = lib.dc_lowrank_bwd_ws_bytes(B, T, D, c["R"], W, dt, int(c["static"]))
         d["y"], d["dx"] = torch.empty_like(d["x"]), torch.empty_like(d["x"])
         d["dsw"] = torch.empty_like(d["sw"]) if c["static"] else None
         d["nws"] = nws
@@ -218,6 +233,7 @@ def abi_launchers(c, sets, torch):
     B, T, D, W = c["B"], c["T"], c["D"], c["W"]
     p = _capi.ptr
     res = int(c["residual"])
+    dt = dcode(c)
     if c["kind"] == "lrg":
         G, R = c["G"], c["R"]
         pa = _capi.ptr_array
@@ -225,13 +241,13 @@ def abi_launchers(c, sets, torch):
         def fwd(i):
             d = sets[i]
             _capi.check(lib.dc_lowrank_fwd_grouped(G, p(d["x"]), G * D, pa(d["zs"]), pa(d["Us"]), pa(d["sws"]),
-                                                   pa(d["ys"]), 0, B, T, D, R, W, 0, res, st), "grouped fwd")
+                                                   pa(d["ys"]), 0, B, T, D, R, W, dt, res, st), "grouped fwd")
 
         def bwd(i):
             d = sets[i]
             _capi.check(lib.dc_lowrank_bwd_grouped(G, p(d["x"]), G * D, pa(d["zs"]), pa(d["Us"]), pa(d["sws"]),
                                                    pa(d["dys"]), 0, p(d["dx"]), G * D, pa(d["dzs"]), pa(d["dUs"]),
-                                                   pa(d["dsws"]), p(d["ws"]), d["nws"], B, T, D, R, W, 0, res, st),
+                                                   pa(d["dsws"]), p(d["ws"]), d["nws"], B, T, D, R, W, dt, res, st),
                         "grouped bwd")
         return fwd, bwd
     if c["kind"] == "hw":
@@ -239,26 +255,26 @@ def abi_launchers(c, sets, torch):
 
         def fwd(i):
             d = sets[i]
-            _capi.check(lib.dc_headwise_fwd(p(d["x"]), p(d["w"]), p(d["sw"]), p(d["y"]), B, T, D, H, W, 0, res, st),
+            _capi.check(lib.dc_headwise_fwd(p(d["x"]), p(d["w"]), p(d["sw"]), p(d["y"]), B, T, D, H, W, dt, res, st),
                         "fwd")
 
         def bwd(i):
             d = sets[i]
             _capi.check(lib.dc_headwise_bwd(p(d["x"]), p(d["w"]), p(d["sw"]), p(d["dy"]), p(d["dx"]), p(d["dw"]),
-                                            p(d["dsw"]), p(d["ws"]), d["nws"], B, T, D, H, W, 0, res, st), "bwd")
+                                            p(d["dsw"]), p(d["ws"]), d["nws"], B, T, D, H, W, dt, res, st), "bwd")
     else:
         R = c["R"]
 
         def fwd(i):
             d = sets[i]
             _capi.check(lib.dc_lowrank_fwd(p(d["x"]), p(d["z"]), p(d["U"]), p(d["sw"]), p(d["y"]),
-                                           B, T, D, R, W, 0, res, st), "fwd")
+                                           B, T, D, R, W, dt, res, st), "fwd")
 
         def bwd(i):
             d = sets[i]
             _capi.check(lib.dc_lowrank_bwd(p(d["x"]), p(d["z"]), p(d["U"]), p(d["sw"]), p(d["dy"]), p(d["dx"]),
                                            p(d["dz"]), p(d["dU"]), p(d["dsw"]), p(d["ws"]), d["nws"],
-                                           B, T, D, R, W, 0, res, st), "bwd")
+                                           B, T, D, R, W, dt, res, st), "bwd")
     return fwd, bwd
 
 
