@@ -36,7 +36,8 @@ COMMON = [
 # Per-file flags.  The lowrank forward lets its MFMA results land in VGPRs
 # directly (no v_accvgpr_read per result); the backward keeps the default,
 # where accumulation registers are what keeps its larger tiles in 512 registers.
-PER_FILE = {"lowrank_mfma_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+PER_FILE = {"lowrank_mfma_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+            "lowrank_f32_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def hipcc() -> str:

@@ -231,12 +231,17 @@ bool all_mfma_ok(const LrProblem* p, int G, bool bwd) {
 }  // namespace
 
 // G problems of one shape (see dc_launch.h): one MFMA launch for all of them,
-// or per group the fp32 VALU kernels or the generic launch sequence.
+// or per group the fp32 kernels (forward on matrix cores, backward on the
+// VALU) or the generic launch sequence.
 hipError_t lr_fwd(const LrProblem* p, int G) {
   if (G < 1 || G > kMaxGroups) return hipErrorInvalidValue;
   if (all_mfma_ok(p, G, false)) return lr_mfma_fwd(p, G);
   for (int g = 0; g < G; ++g) {
     hipError_t e;
+    if (lr_f32m_fwd_ok(p[g])) {
+      if ((e = lr_f32m_fwd(p[g])) != hipSuccess) return e;
+      continue;
+    }
     if (lr_f32_ok(p[g])) {
       if ((e = lr_f32(p[g], false)) != hipSuccess) return e;
       continue;
