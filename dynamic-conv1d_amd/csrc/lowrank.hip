@@ -217,7 +217,12 @@ bool lr_mfma_ok(const LrProblem& p, bool bwd) {
 
 int64_t lr_bwd_ws_bytes(const LrProblem& p) {
   if (lr_mfma_ok(p, true)) return lr_mfma_ws_bytes(p);
-  if (lr_f32_ok(p)) return lr_f32_ws_bytes(p);
+  if (lr_f32m_bwd_ok(p) || lr_f32_ok(p)) {
+    // fp32: the larger of the two fast paths' needs (alignment picks between them at the call)
+    const int64_t m = lr_f32m_bwd_ok(p) ? lr_f32m_ws_bytes(p) : 0;
+    const int64_t v = lr_f32_ok(p) ? lr_f32_ws_bytes(p) : 0;
+    return m > v ? m : v;
+  }
   const int64_t RK = p.R + (p.static_w ? 1 : 0);
   return (int64_t)generic_partials(p.B * p.T) * RK * p.W * p.D * (int64_t)sizeof(float);
 }
@@ -231,8 +236,8 @@ bool all_mfma_ok(const LrProblem* p, int G, bool bwd) {
 }  // namespace
 
 // G problems of one shape (see dc_launch.h): one MFMA launch for all of them,
-// or per group the fp32 kernels (forward on matrix cores, backward on the
-// VALU) or the generic launch sequence.
+// or per group the fp32 kernels (matrix cores, else the VALU) or the generic
+// launch sequence.
 hipError_t lr_fwd(const LrProblem* p, int G) {
   if (G < 1 || G > kMaxGroups) return hipErrorInvalidValue;
   if (all_mfma_ok(p, G, false)) return lr_mfma_fwd(p, G);
@@ -261,6 +266,10 @@ hipError_t lr_bwd(const LrProblem* p, int G) {
   if (all_mfma_ok(p, G, true)) return lr_mfma_bwd(p, G);
   for (int g = 0; g < G; ++g) {
     hipError_t e;
+    if (lr_f32m_bwd_ok(p[g])) {
+      if ((e = lr_f32m_bwd(p[g])) != hipSuccess) return e;
+      continue;
+    }
     if (lr_f32_ok(p[g])) {
       if ((e = lr_f32(p[g], true)) != hipSuccess) return e;
       continue;

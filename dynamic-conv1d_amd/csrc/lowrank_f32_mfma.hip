@@ -152,6 +152,341 @@ __global__ __launch_bounds__(256) void lr_fwd_f32m(const float* __restrict__ x, 
   }
 }
 
+// ----------------------------------------------------------------- backward
+//
+// One pass over x and dy gives dx, dz, dU and dstatic_w in fp32 (reference:
+// lowrank.py:87-140 and 159-205, fp32 branch 130-132, 196-198).
+//
+// Tile: 16 rows x 32 channels per wavefront; lane (q, n) owns rows 4q..4q+3
+// and channels 2n, 2n+1 (8 bytes per row, 128 contiguous bytes across the 16
+// lanes of a row group).  A workgroup is 8 wavefronts on 8 adjacent channel
+// chunks (256 channels) of one run of rows.  With G_k[t, d] = dy[t, d] x[t-k, d]:
+//   * dx, in scatter form as in the bf16 kernel: tap weights of the lane's own
+//     rows (A = z_eff rows, B = U_eff), dy[s] K_w[s, k] added to dx row s-k;
+//     the sums for rows of the group above go there by ds_bpermute, and group
+//     3's last W-1 rows wait one tile (carry).
+//   * dU[r, kD+d] += sum_t z_eff[t, r] G_k[t, d]: K = rows, 4 per MFMA.  In
+//     step i lane group q supplies row 4q+i: A = z_eff[t0+4q+i, n] (rank n),
+//     B = G_k[4q+i, 2n+jj], the lane's own value.
+//   * dz[t, r] += sum_{k,d} G_k[t, d] U_eff[r, kD+d]: K = (tap, channel), 4 per
+//     MFMA.  A needs G by row (lane (q,n): row n, channels 8q..8q+7), so each
+//     tap's G tile goes through the wavefront's LDS slot (row-major, read back
+//     by row); B = U_eff[n, kD + d0+8q .. +7], staged once per run in LDS.
+// dz is summed over the 8 chunk wavefronts in LDS, in wave order, every DZB
+// tiles (one barrier) and written as one fp32 partial per 256 channels; dU
+// accumulates in registers over the run and is written as one partial per
+// run.  reduce_partials adds both in a fixed order (deterministic).
+struct LrF32mBwdArgs {
+  int Tn, D, R, RK, residual;
+  int nch;   // ceil(D / 32) chunks
+  int ncg;   // ceil(nch / 8): workgroup columns (256 channels)
+  int seg;   // 16-row tiles per run
+  int nspb;  // runs per sequence
+  int nseg;  // B * nspb
+  int nblk;  // ncg * nseg
+  int xld, dxld;  // row strides of x and dx (elements)
+  int yhd;        // dy layout: D ([B, T, D]) or the head dim of [B, D/yhd, T, yhd] (yhd % 32 == 0)
+  int64_t BT;
+};
+
+template <int W, int NKB>
+__global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, const float* __restrict__ z,
+                                                   const float* __restrict__ U, const float* __restrict__ sw,
+                                                   const float* __restrict__ dy, float* __restrict__ dx,
+                                                   float* __restrict__ part_dz, float* __restrict__ part_du,
+                                                   LrF32mBwdArgs a) {
+  static_assert(W >= 2 && W <= 4, "scatter form: 2 <= W <= 4");
+  static_assert(NKB >= 1 && NKB <= 4, "kernel rank <= 16");
+  constexpr int NR = W + 3;   // x rows 4q-W+1 .. 4q+3 per lane
+  constexpr int NCW = 8;      // chunk wavefronts per workgroup
+  constexpr int NSC = W - 1;  // scatter partial sums per channel
+  constexpr int DZB = 2;      // tiles per dz batch
+  constexpr int GP = 36;      // G tile row pitch (floats): 32 channels + 4 pad
+  __shared__ f32x4 uz_lds[NCW][W * 2 * 64];  // dz B operands of each wavefront
+  __shared__ __attribute__((aligned(16))) float gt[NCW][16 * GP];
+  __shared__ float dzred[2][NCW][DZB][256];
+
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int q = lane >> 4, n = lane & 15;
+  const int lb = xcd_remap(blockIdx.x, a.nblk);
+  const int cg = lb % a.ncg, s = lb / a.ncg;
+  const int chunk = cg * NCW + wave;
+  const int D = a.D, Tn = a.Tn, R = a.R, RK = a.RK;
+  const int d0 = chunk * 32;
+  const int col = d0 + 2 * n;
+  const bool chv = col < D;  // D % 4 == 0: a lane's 2 channels are both inside or both outside
+  const int b = s / a.nspb;
+  const int ntile = (Tn + 15) >> 4;
+  const int tile0 = (s - b * a.nspb) * a.seg;
+  const int tile1 = min(tile0 + a.seg, ntile);
+  const int nit = tile1 - tile0;  // the same for every wavefront of the workgroup
+  const int64_t row0 = (int64_t)b * Tn;
+  const int yhd = a.yhd, head = d0 / yhd;  // yhd % 32 == 0: the chunk lies in one head
+  const int xrowb = a.xld * 4, yrowb = yhd * 4, dxrowb = a.dxld * 4;
+  const rsrc_t rx = make_rsrc(x + row0 * a.xld, (int64_t)Tn * xrowb);
+  const rsrc_t rdy = make_rsrc(dy + row0 * D + (int64_t)head * Tn * yhd, (int64_t)Tn * yrowb);
+  const rsrc_t rdx = make_rsrc(dx + row0 * a.dxld, (int64_t)Tn * dxrowb);
+  const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 4);
+  const int xlo = chv ? (4 * q * a.xld + col) * 4 : kOobLane;
+  const int ylo = chv ? (4 * q * yhd + col - head * yhd) * 4 : kOobLane;
+  const int dxlo = chv ? (4 * q * a.dxld + col) * 4 : kOobLane;
+
+  // ---- U_eff operands of the chunk (rank rows r < RK, zero beyond)
+  const rsrc_t ru = make_rsrc(U, (int64_t)R * W * D * 4);
+  const rsrc_t rs = make_rsrc(sw, sw ? (int64_t)W * D * 4 : 0);
+  float uw[W][NKB][2];  // tap-weight B: U_eff[4kb+q, k*D + col + jj]
+#pragma unroll
+  for (int k = 0; k < W; ++k)
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int r = 4 * kb + q;
+      const int c4 = (k * D + col) * 4;
+      const u32x2 vu = bload64(ru, chv && r < R ? r * W * D * 4 + c4 : kOobLane);
+      const u32x2 vs = bload64(rs, chv && r == R && r < RK ? c4 : kOobLane);
+      uw[k][kb][0] = __uint_as_float(vu[0]) + __uint_as_float(vs[0]);
+      uw[k][kb][1] = __uint_as_float(vu[1]) + __uint_as_float(vs[1]);
+    }
+  f32x4* __restrict__ my_uz = uz_lds[wave];
+#pragma unroll
+  for (int k = 0; k < W; ++k)
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      // dz B: U_eff[n, k*D + d0 + 8q + 4p .. +3]
+      const int dd = d0 + 8 * q + 4 * p;
+      const int c4 = (k * D + dd) * 4;
+      const bool in = dd < D;
+      const u32x4 vu = bload128(ru, in && n < R ? n * W * D * 4 + c4 : kOobLane);
+      const u32x4 vs = bload128(rs, in && n == R && n < RK ? c4 : kOobLane);
+      f32x4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(vu[i]) + __uint_as_float(vs[i]);
+      my_uz[(k * 2 + p) * 64 + lane] = v;  // read back by this lane only
+    }
+  float* __restrict__ my_g = gt[wave];
+
+  f32x4 du[W][2];
+#pragma unroll
+  for (int k = 0; k < W; ++k)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) du[k][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float carry[NSC][2];
+#pragma unroll
+  for (int i = 0; i < NSC; ++i) carry[i][0] = carry[i][1] = 0.f;
+
+  struct TileIn {
+    u32x2 xr[NR], dyr[4];
+    float za[NKB];  // z_eff[t0+n, 4kb+q]: tap-weight A
+    float zt[4];    // z_eff[t0+4q+i, n]: dU A
+  };
+  auto load_tile = [&](int tile, TileIn& in) {
+    const bool live = tile < tile1;
+    const bool ylive = tile <= tile1;  // the tile after the run closes its last dx rows
+    const int t0 = tile * 16;
+    const int xt = live ? t0 * xrowb : kOobTile;
+    const int yt = ylive ? t0 * yrowb : kOobTile;
+#pragma unroll
+    for (int m = 0; m < NR; ++m) in.xr[m] = bload64(rx, xlo + xt + (m - (W - 1)) * xrowb);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) in.dyr[m] = bload64(rdy, ylo + yt + m * yrowb);
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int r = 4 * kb + q;
+      in.za[kb] = __uint_as_float(bload32(rz, ylive && r < R ? ((t0 + n) * R + r) * 4 : kOobTile));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      in.zt[i] = __uint_as_float(bload32(rz, ylive && n < R ? ((t0 + 4 * q + i) * R + n) * 4 : kOobTile));
+  };
+
+  // Scatter form (as lowrank_mfma_bwd.hip): S[m] holds the lane's sums for row
+  // 4q-1-m; groups take the group below's for rows 4q+3-m; group 3 stores this
+  // tile's rows 12 .. 15-NSC and the tile before's last NSC rows (carry).
+  auto close_rows = [&](const float(&own)[4][2], const float(&S)[NSC][2], int tile) {
+    const int src = ((lane + 16) & 63) << 2;
+    float recv[NSC][2];
+#pragma unroll
+    for (int m = 0; m < NSC; ++m)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+        recv[m][jj] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(S[m][jj])));
+    const bool top = q == 3;
+    const int cur_off = tile < tile1 ? dxlo + tile * 16 * dxrowb : kOobTile;
+    const int prev_off = tile > tile0 && tile <= tile1 ? dxlo + (tile - 1) * 16 * dxrowb : kOobTile;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      constexpr int kFirstOpen = 4 - NSC;
+      const bool open = i >= kFirstOpen;
+      u32x2 v;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        float bv = own[i][jj];
+        if (open) bv = (top ? carry[i - kFirstOpen][jj] : bv) + recv[3 - i][jj];
+        v[jj] = __float_as_uint(bv);
+      }
+      bstore64<true>(v, rdx, (top && open ? prev_off : cur_off) + i * dxrowb);
+    }
+#pragma unroll
+    for (int i = 0; i < NSC; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) carry[i][jj] = own[4 - NSC + i][jj];
+  };
+  // Tap weights of the lane's rows (K = ranks) times dy, into own / S.
+  auto scatter_taps = [&](const float(&za)[NKB], const float(&dyf)[4][2], int k, float(&own)[4][2],
+                          float(&S)[NSC][2]) {
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      f32x4 kw = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) kw = __builtin_amdgcn_mfma_f32_16x16x4f32(za[kb], uw[k][kb][jj], kw, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = i - k;
+        if (r >= 0)
+          own[r][jj] = fmaf(dyf[i][jj], kw[i], own[r][jj]);
+        else
+          S[-r - 1][jj] = fmaf(dyf[i][jj], kw[i], S[-r - 1][jj]);
+      }
+    }
+  };
+  // z_eff: the static rank R is 1 inside the sequence (the loads read 0 there)
+  auto finish_z = [&](float(&za)[NKB], float(&zt)[4], int t0) {
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+      if (4 * kb + q == R && R < RK) za[kb] = t0 + n < Tn ? 1.f : 0.f;
+    if (n == R && R < RK) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) zt[i] = t0 + 4 * q + i < Tn ? 1.f : 0.f;
+    }
+  };
+
+  auto compute_tile = [&](int it, const TileIn& in) {
+    const int tile = tile0 + it;
+    const int t0 = tile * 16;
+    float za[NKB], zt[4];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) za[kb] = in.za[kb];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) zt[i] = in.zt[i];
+    finish_z(za, zt, t0);
+    float dyf[4][2], xf[NR][2];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      dyf[m][0] = __uint_as_float(in.dyr[m][0]);
+      dyf[m][1] = __uint_as_float(in.dyr[m][1]);
+    }
+#pragma unroll
+    for (int m = 0; m < NR; ++m) {
+      xf[m][0] = __uint_as_float(in.xr[m][0]);
+      xf[m][1] = __uint_as_float(in.xr[m][1]);
+    }
+    float own[4][2], S[NSC][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) own[i][0] = own[i][1] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NSC; ++i) S[i][0] = S[i][1] = 0.f;
+    f32x4 dz = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      scatter_taps(za, dyf, k, own, S);
+      float g[4][2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) g[i][jj] = dyf[i][jj] * xf[i - k + W - 1][jj];
+      // dU (K = rows): step i takes row 4q+i of every lane group
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) du[k][jj] = __builtin_amdgcn_mfma_f32_16x16x4f32(zt[i], g[i][jj], du[k][jj], 0, 0, 0);
+      // dz (K = channels): the G tile by row through this wavefront's LDS slot
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f32x2 gw = {g[i][0], g[i][1]};
+        *reinterpret_cast<f32x2*>(my_g + (4 * q + i) * GP + 2 * n) = gw;
+      }
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const f32x4 ga = *reinterpret_cast<const f32x4*>(my_g + n * GP + 8 * q + 4 * p);
+        const f32x4 ub = my_uz[(k * 2 + p) * 64 + lane];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dz = __builtin_amdgcn_mfma_f32_16x16x4f32(ga[e], ub[e], dz, 0, 0, 0);
+      }
+    }
+    if (a.residual) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) own[i][jj] += dyf[i][jj];
+    }
+    close_rows(own, S, tile);
+    // dz rows 4q..4q+3, rank n: batch over DZB tiles, then the 8 wavefronts' sums in wave order
+    const int slot = it % DZB, buf = (it / DZB) & 1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dzred[buf][wave][slot][(4 * q + i) * 16 + n] = dz[i];
+    if (slot == DZB - 1 || it == nit - 1) {
+      __syncthreads();
+      float* __restrict__ out = part_dz + ((int64_t)cg * a.BT + row0) * R;
+      const int tb = tile - slot;
+      for (int e = threadIdx.x; e < (slot + 1) * 256; e += 64 * NCW) {
+        const int sl = e >> 8, rem = e & 255, rr = rem >> 4, nn = rem & 15;
+        float v = dzred[buf][0][sl][rem];
+#pragma unroll
+        for (int w2 = 1; w2 < NCW; ++w2) v += dzred[buf][w2][sl][rem];
+        const int t = (tb + sl) * 16 + rr;
+        if (nn < R && t < Tn) out[t * R + nn] = v;
+      }
+    }
+  };
+
+  TileIn ta, tb;
+  load_tile(tile0, ta);
+  for (int it = 0; it < nit; it += 2) {
+    load_tile(tile0 + it + 1, tb);
+    __builtin_amdgcn_sched_barrier(0);
+    compute_tile(it, ta);
+    load_tile(tile0 + it + 2, ta);
+    __builtin_amdgcn_sched_barrier(0);
+    if (it + 1 < nit) compute_tile(it + 1, tb);
+  }
+  // the tile after the run closes its last rows
+  auto flush = [&](const TileIn& in) {
+    const int tile = tile0 + nit;
+    float za[NKB], zt[4];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) za[kb] = in.za[kb];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) zt[i] = 0.f;
+    finish_z(za, zt, tile * 16);
+    float dyf[4][2], own[4][2], S[NSC][2];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      dyf[m][0] = __uint_as_float(in.dyr[m][0]);
+      dyf[m][1] = __uint_as_float(in.dyr[m][1]);
+      own[m][0] = own[m][1] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < NSC; ++i) S[i][0] = S[i][1] = 0.f;
+#pragma unroll
+    for (int k = 1; k < W; ++k) scatter_taps(za, dyf, k, own, S);
+    close_rows(own, S, tile);
+  };
+  if (nit & 1)
+    flush(tb);
+  else
+    flush(ta);
+
+  // ---- dU (and dstatic_w as rank R) partial of this run: ranks 4q+r, channels col, col+1
+#pragma unroll
+  for (int k = 0; k < W; ++k)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rk = 4 * q + r;
+        if (rk < RK && chv) part_du[((int64_t)s * RK + rk) * W * D + (int64_t)k * D + col + jj] = du[k][jj][r];
+      }
+}
+
 // ------------------------------------------------------------------- host
 namespace {
 
@@ -219,6 +554,100 @@ hipError_t lr_f32m_fwd(const LrProblem& p) {
   DC_F32M_CASE(3, 2) DC_F32M_CASE(3, 4) DC_F32M_CASE(3, 8)
   DC_F32M_CASE(4, 2) DC_F32M_CASE(4, 4) DC_F32M_CASE(4, 8)
 #undef DC_F32M_CASE
+  return hipErrorInvalidValue;
+}
+
+namespace {
+
+LrF32mBwdArgs make_f32m_bwd_args(const LrProblem& p) {
+  LrF32mBwdArgs a;
+  a.Tn = (int)p.T;
+  a.D = (int)p.D;
+  a.R = (int)p.R;
+  a.RK = (int)p.R + (p.static_w ? 1 : 0);
+  a.residual = p.residual;
+  a.nch = (int)((p.D + 31) / 32);
+  a.ncg = (a.nch + 7) / 8;
+  // 2048 wavefronts (2 per SIMD): runs of ceil(tiles * 8 chunks / 2048) tiles
+  const int64_t ntile = (p.T + 15) / 16;
+  int64_t seg = (p.B * ntile * a.ncg * 8 + 2047) / 2048;
+  if (seg < 2) seg = 2;
+  if (seg > ntile) seg = ntile;
+  a.seg = (int)seg;
+  a.nspb = (int)((ntile + seg - 1) / seg);
+  a.nseg = (int)(p.B * a.nspb);
+  a.nblk = a.nseg * a.ncg;
+  a.xld = (int)p.xld();
+  a.dxld = (int)p.dxld();
+  a.yhd = (int)p.yhd();
+  a.BT = p.B * p.T;
+  return a;
+}
+
+struct F32mWs {
+  int64_t dz_off, du_off, total;
+};
+F32mWs f32m_ws(const LrProblem& p, const LrF32mBwdArgs& a) {
+  F32mWs w;
+  w.dz_off = 0;
+  w.du_off = ((int64_t)a.ncg * a.BT * a.R * 4 + 255) / 256 * 256;
+  w.total = w.du_off + (int64_t)a.nseg * a.RK * p.W * p.D * 4;
+  return w;
+}
+
+template <int W, int NKB>
+hipError_t launch_f32m_bwd(const LrProblem& p) {
+  const LrF32mBwdArgs a = make_f32m_bwd_args(p);
+  const F32mWs w = f32m_ws(p, a);
+  float* pdz = (float*)((char*)p.ws + w.dz_off);
+  float* pdu = (float*)((char*)p.ws + w.du_off);
+  lr_bwd_f32m<W, NKB><<<a.nblk, 512, 0, p.stream>>>((const float*)p.x, (const float*)p.z, (const float*)p.U,
+                                                      (const float*)p.static_w, (const float*)p.dy, (float*)p.dx,
+                                                      pdz, pdu, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t WD = p.W * p.D, RKWD = (int64_t)a.RK * WD;
+  const PartialReduce jobs[3] = {
+      {pdu, RKWD, a.nseg, p.R * WD, p.dU},
+      {pdu + p.R * WD, RKWD, a.nseg, p.static_w ? WD : 0, p.dstatic_w},
+      {pdz, a.BT * a.R, a.ncg, a.BT * a.R, p.dz},
+  };
+  return reduce_partials_multi(jobs, 3, p.dtype, p.stream);
+}
+
+}  // namespace
+
+// fp32, 2 <= W <= 4, kernel rank <= 16; D, x / dx row strides multiples of 4
+// (8-byte lane pieces, 16-byte operand pieces); dy's head dim a multiple of 32
+// (a chunk inside one head); 16-byte aligned x, dy, dx, U, static_w; every
+// sequence within the buffer range.
+bool lr_f32m_bwd_ok(const LrProblem& p) {
+  if (p.dtype != kFP32) return false;
+  if (p.W < 2 || p.W > 4) return false;
+  if (p.R + (p.static_w ? 1 : 0) > 16) return false;
+  if (p.D % 4 != 0 || p.xld() % 4 != 0 || p.dxld() % 4 != 0) return false;
+  if (p.yhd() != p.D && p.yhd() % 32 != 0) return false;
+  if (!aligned_to(p.x, 16) || !aligned_to(p.dy, 16) || !aligned_to(p.dx, 16) || !aligned_to(p.U, 16) ||
+      !aligned_to(p.static_w, 16))
+    return false;
+  if (p.R * p.W * p.D * 4 >= kOobLane) return false;
+  const int64_t ld = p.xld() > p.dxld() ? p.xld() : p.dxld();
+  if ((p.T + kSeqSlackRows) * ld * 4 > kMaxSeqBytes) return false;
+  if ((p.T + kSeqSlackRows) * p.D * 4 > kMaxSeqBytes) return false;
+  return (p.T + kSeqSlackRows) * p.R * 4 <= kMaxSeqBytes;
+}
+
+int64_t lr_f32m_ws_bytes(const LrProblem& p) { return f32m_ws(p, make_f32m_bwd_args(p)).total; }
+
+hipError_t lr_f32m_bwd(const LrProblem& p) {
+  const int nkb = (int)((p.R + (p.static_w ? 1 : 0) + 3) / 4);
+  const int kb = nkb <= 2 ? 2 : 4;
+#define DC_F32MB_CASE(WW, KB) \
+  if (p.W == WW && kb == KB) return launch_f32m_bwd<WW, KB>(p);
+  DC_F32MB_CASE(2, 2) DC_F32MB_CASE(2, 4)
+  DC_F32MB_CASE(3, 2) DC_F32MB_CASE(3, 4)
+  DC_F32MB_CASE(4, 2) DC_F32MB_CASE(4, 4)
+#undef DC_F32MB_CASE
   return hipErrorInvalidValue;
 }
 

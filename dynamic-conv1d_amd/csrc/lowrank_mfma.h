@@ -173,9 +173,12 @@ __device__ __forceinline__ F pick(const S (&a)[kMaxGroups], int g, F S::*f) {
 hipError_t lr_mfma_fwd(const LrProblem* p, int G);
 int64_t lr_mfma_ws_bytes(const LrProblem& p);
 hipError_t lr_mfma_bwd(const LrProblem* p, int G);
-// fp32 forward on matrix cores (lowrank_f32_mfma.hip), one problem per launch.
+// fp32 on matrix cores (lowrank_f32_mfma.hip), one problem per launch sequence.
 bool lr_f32m_fwd_ok(const LrProblem& p);
 hipError_t lr_f32m_fwd(const LrProblem& p);
+bool lr_f32m_bwd_ok(const LrProblem& p);
+int64_t lr_f32m_ws_bytes(const LrProblem& p);
+hipError_t lr_f32m_bwd(const LrProblem& p);
 // fp32 VALU kernels (lowrank_f32.hip), one problem per launch sequence.
 bool lr_f32_ok(const LrProblem& p);
 int64_t lr_f32_ws_bytes(const LrProblem& p);
