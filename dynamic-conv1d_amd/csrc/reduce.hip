@@ -21,6 +21,7 @@ struct ReduceJob {
   void* out;          // C outputs of the launch dtype
   int P;              // partials
   int vec;            // 4: columns, pstride and pointers allow float4 access
+  int plog;           // log2 of the partial lanes per column (PL = 1 .. 16)
   int block0;         // first block of this job
 };
 
@@ -29,39 +30,44 @@ struct ReduceJobs {
   int n;
 };
 
-// 256 threads = 64 column lanes x 4 partial lanes; a column lane owns 4
-// consecutive columns when `vec` (float4 loads), else 1.  Partial lane pl sums
-// partials pl, pl+4, ...; the 4 lane sums are added in index order in LDS.
+// 256 threads = 256/PL column lanes x PL partial lanes (PL a power of two, so
+// each thread adds about 4-16 partials and the loads of a thread are
+// independent); a column lane owns 4 consecutive columns when `vec` (float4
+// loads), else 1.  Partial lane pl sums partials pl, pl+PL, ... in order; the
+// PL lane sums are then added in lane order from LDS.  The order is fixed by
+// (P, PL), so results are the same run to run.
 template <typename T>
 __global__ __launch_bounds__(256) void reduce_partials_kernel(ReduceJobs jobs) {
-  __shared__ float4 red[4][64];
+  __shared__ float4 red[256];
   int ji = 0;
 #pragma unroll
   for (int i = 1; i < kMaxJobs; ++i)
     if (i < jobs.n && (int)blockIdx.x >= jobs.j[i].block0) ji = i;
   const ReduceJob& J = jobs.j[ji];
-  const int cl = threadIdx.x & 63, pl = threadIdx.x >> 6;
+  const int PL = 1 << J.plog, CL = 256 >> J.plog;
+  const int cl = threadIdx.x & (CL - 1), pl = threadIdx.x >> (8 - J.plog);
   const int per = J.vec;  // columns per lane
-  const int64_t c0 = ((int64_t)(blockIdx.x - J.block0) * 64 + cl) * per;
+  const int64_t c0 = ((int64_t)(blockIdx.x - J.block0) * CL + cl) * per;
   float4 s = {0.f, 0.f, 0.f, 0.f};
   if (c0 < J.C) {
     const float* q = J.part + c0;
     if (per == 4) {
-      for (int p = pl; p < J.P; p += 4) {
+#pragma unroll 4
+      for (int p = pl; p < J.P; p += PL) {
         const float4 v = *reinterpret_cast<const float4*>(q + (int64_t)p * J.pstride);
         s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
       }
     } else {
-      for (int p = pl; p < J.P; p += 4) s.x += q[(int64_t)p * J.pstride];
+#pragma unroll 4
+      for (int p = pl; p < J.P; p += PL) s.x += q[(int64_t)p * J.pstride];
     }
   }
-  red[pl][cl] = s;
+  red[threadIdx.x] = s;
   __syncthreads();
   if (pl == 0 && c0 < J.C) {
-    float4 t = red[0][cl];
-#pragma unroll
-    for (int i = 1; i < 4; ++i) {
-      const float4 u = red[i][cl];
+    float4 t = red[cl];
+    for (int i = 1; i < PL; ++i) {
+      const float4 u = red[i * CL + cl];
       t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
     }
     T* o = reinterpret_cast<T*>(J.out) + c0;
@@ -91,8 +97,13 @@ hipError_t reduce_partials_multi(const PartialReduce* r, int n, int dtype, hipSt
                     (reinterpret_cast<uintptr_t>(r[i].part) % 16 == 0) &&
                     (reinterpret_cast<uintptr_t>(r[i].out) % (4 * es) == 0);
     J.vec = v4 ? 4 : 1;
+    // partial lanes: the largest power of two <= P/4, between 1 and 16
+    int plog = 0;
+    while (plog < 4 && (4 << (plog + 1)) <= J.P) ++plog;
+    J.plog = plog;
+    const int64_t cols = (int64_t)(256 >> plog) * J.vec;  // columns per block
     J.block0 = blocks;
-    blocks += (int)((J.C + 64 * J.vec - 1) / (64 * J.vec));
+    blocks += (int)((J.C + cols - 1) / cols);
   }
   if (jobs.n == 0) return hipSuccess;
   switch (dtype) {
