@@ -28,7 +28,6 @@ namespace dc {
 
 struct LrF32mArgs {
   int Tn, D, R, RK, residual;
-  int nkb;   // rank steps of 4: ceil(RK / 4)
   int nch;   // ceil(D / 64) channel chunks
   int seg;   // 16-row tiles per run
   int nspb;  // runs per sequence
@@ -497,7 +496,6 @@ LrF32mArgs make_f32m_args(const LrProblem& p) {
   a.R = (int)p.R;
   a.RK = (int)p.R + (p.static_w ? 1 : 0);
   a.residual = p.residual;
-  a.nkb = (a.RK + 3) / 4;
   a.nch = (int)((p.D + 63) / 64);
   // runs of about 8 tiles, at most 4096 wavefronts
   const int64_t ntile = (p.T + 15) / 16;
