@@ -483,22 +483,32 @@ void launch_bwd_kernel(const HwProblem& p, const HwPlan& pl) {
 
 template <typename T, int W, int HSV>
 hipError_t launch_bwd_fast(const HwProblem& p, const HwPlan& pl) {
+  bool launched = false;
   if constexpr (TdwOf<T, W, HSV>::value) {
-    if (pl.tdw)
-      launch_bwd_kernel<T, W, HSV, true, 1>(p, pl);
-    else
-      launch_bwd_kernel<T, W, HSV, false, 1>(p, pl);
-  } else if constexpr (HSV == VecOf<T>::value) {
-    // head_size >= VEC: lanes per head from the plan
-    switch (pl.a.lph) {
-      case 1: launch_bwd_kernel<T, W, HSV, false, 1>(p, pl); break;
-      case 2: launch_bwd_kernel<T, W, HSV, false, 2>(p, pl); break;
-      case 4: launch_bwd_kernel<T, W, HSV, false, 4>(p, pl); break;
-      case 8: launch_bwd_kernel<T, W, HSV, false, 8>(p, pl); break;
-      default: launch_bwd_kernel<T, W, HSV, false, 0>(p, pl); break;
+    // The transposed dweight store needs lanes that own whole heads (one lane
+    // per head or several heads per lane); heads over several lanes sum across
+    // them first (below).
+    if (pl.a.lph == 1) {
+      if (pl.tdw)
+        launch_bwd_kernel<T, W, HSV, true, 1>(p, pl);
+      else
+        launch_bwd_kernel<T, W, HSV, false, 1>(p, pl);
+      launched = true;
     }
-  } else {
-    launch_bwd_kernel<T, W, HSV, false, 1>(p, pl);
+  }
+  if (!launched) {
+    if constexpr (HSV == VecOf<T>::value) {
+      // head_size >= VEC: lanes per head from the plan
+      switch (pl.a.lph) {
+        case 1: launch_bwd_kernel<T, W, HSV, false, 1>(p, pl); break;
+        case 2: launch_bwd_kernel<T, W, HSV, false, 2>(p, pl); break;
+        case 4: launch_bwd_kernel<T, W, HSV, false, 4>(p, pl); break;
+        case 8: launch_bwd_kernel<T, W, HSV, false, 8>(p, pl); break;
+        default: launch_bwd_kernel<T, W, HSV, false, 0>(p, pl); break;
+      }
+    } else {
+      launch_bwd_kernel<T, W, HSV, false, 1>(p, pl);
+    }
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !p.static_w) return e;

@@ -107,6 +107,11 @@ HW_EDGE = [
     (2, 50, 96, 96, 4, True, True, torch.float16),      # fp16, D not a multiple of 64*VEC
     (1, 20, 12, 4, 2, True, True, torch.bfloat16),      # D % 8 != 0 and hs 3: generic path
     (2, 33, 64, 16, 1, True, True, torch.float32),      # W 1
+    # fp32 W 8: a lane's dweight piece is 32 bytes; heads over 2 and 8 lanes
+    # must sum across lanes before the store (found by the random sweep)
+    (1, 40, 128, 16, 8, True, False, torch.float32),
+    (2, 33, 256, 8, 8, False, True, torch.float32),
+    (1, 37, 128, 32, 8, True, True, torch.float32),     # hs 4: one lane per head, transposed store
     (1, 5, 64, 64, 8, True, True, torch.bfloat16),      # W > T
     (1, 1, 64, 8, 4, True, True, torch.bfloat16),       # T 1
     (3, 129, 200, 50, 7, True, True, torch.float32),    # hs 4 fp32, W 7, D % 64*4 != 0
