@@ -24,6 +24,7 @@ from oracle.reference_cpu import (
 )
 import headwise as hw_mod
 import lowrank as lr_mod
+from dynconv import lowrank as dlr
 
 pytestmark = pytest.mark.gpu
 
@@ -111,3 +112,60 @@ def test_random_headwise(Bn, Tn, Dn, H, W, static, residual, dtype):
     for a, b, n in zip(g_k, g_q, ["dx", "dweight", "dstatic_w"]):
         if b is not None:
             assert_ns(a, b, dtype, n, elementwise=n != "dstatic_w")
+
+
+def _grouped_case(i):
+    rnd = random.Random(15485863 * i + 11)
+    dtype = rnd.choice(DTYPES)
+    G = rnd.randint(1, 4)
+    Bn = rnd.randint(1, 2)
+    Tn = rnd.choice([1, 5, 16, 17, 40, 100])
+    Dn = rnd.choice([8, 16, 40, 64, 128, 192])
+    extra = rnd.choice([0, 0, 8, 24])  # x is a column slice of a wider tensor
+    W = rnd.randint(1, 8)
+    static = rnd.random() < 0.5
+    R = rnd.randint(1, 31)
+    hd = rnd.choice([None, None] + [d for d in (4, 8, 16, 32, 64) if Dn % d == 0])
+    return G, Bn, Tn, Dn, extra, R, W, static, hd, dtype
+
+
+GR_CASES = [_grouped_case(i) for i in range(32)]
+
+
+@pytest.mark.parametrize("G,Bn,Tn,Dn,extra,R,W,static,hd,dtype", GR_CASES,
+                         ids=[f"g{i}-G{c[0]}B{c[1]}T{c[2]}D{c[3]}x{c[4]}-R{c[5]}W{c[6]}-st{int(c[7])}-hd{c[8]}-"
+                              f"{str(c[9])[6:]}" for i, c in enumerate(GR_CASES)])
+def test_random_grouped(G, Bn, Tn, Dn, extra, R, W, static, hd, dtype):
+    """The grouped operator (x read in place, optional head-major outputs) on random shapes."""
+    g = gen(G * 101 + Bn * 7 + Tn * 131 + Dn * 17 + R * 3 + W + extra)
+    xw = randn(g, Bn, Tn, G * Dn + extra)
+    zs = [randn(g, Bn, Tn, R) for _ in range(G)]
+    Us = [randn(g, R, W * Dn, scale=1 / math.sqrt((R + 1) * W)) for _ in range(G)]
+    sws = [uniform(g, W, Dn, lo=-1 / math.sqrt(W), hi=1 / math.sqrt(W)) for _ in range(G)] if static else None
+    dys = [randn(g, Bn, Tn, Dn) for _ in range(G)]
+    x_k = xw.to(dtype).to(DEV)[..., :G * Dn].detach().requires_grad_()
+    zk = [t.to(dtype).to(DEV).requires_grad_() for t in zs]
+    Uk = [t.to(dtype).to(DEV).requires_grad_() for t in Us]
+    sk = [t.to(dtype).to(DEV).requires_grad_() for t in sws] if static else None
+    # the Python API keeps the reference's power-of-two rank rule; other ranks via the Function
+    ys = dlr._GroupedLowrankDynamicConvolutionFn.apply(x_k, True, G, static, hd or 0,
+                                                       *(zk + Uk + (sk if static else [])))
+    H = Dn // hd if hd else None
+    grads = [d.to(dtype).to(DEV) if hd is None else d.to(dtype).to(DEV).view(Bn, Tn, H, hd).transpose(1, 2)
+             .contiguous() for d in dys]
+    torch.autograd.backward(ys, grads)
+    torch.cuda.synchronize()
+    for gi in range(G):
+        xs = xw[..., gi * Dn:(gi + 1) * Dn].to(dtype).float().requires_grad_()
+        zr = zs[gi].to(dtype).float().requires_grad_()
+        Ur = Us[gi].to(dtype).float().requires_grad_()
+        sr = sws[gi].to(dtype).float().requires_grad_() if static else None
+        yr = lr_ref(xs, zr, Ur, sr, residual=True)
+        yr.backward(dys[gi].to(dtype).float())
+        y = ys[gi] if hd is None else ys[gi].transpose(1, 2).reshape(Bn, Tn, Dn)
+        assert_ns(y, yr, dtype, f"g{gi} y")
+        assert_ns(x_k.grad[..., gi * Dn:(gi + 1) * Dn], xs.grad, dtype, f"g{gi} dx")
+        assert_ns(zk[gi].grad, zr.grad, dtype, f"g{gi} dz", elementwise=False)
+        assert_ns(Uk[gi].grad, Ur.grad, dtype, f"g{gi} dU", elementwise=False)
+        if static:
+            assert_ns(sk[gi].grad, sr.grad, dtype, f"g{gi} dstatic_w", elementwise=False)
