@@ -124,6 +124,17 @@ __device__ __forceinline__ void bstore128(u32x4 v, rsrc_t r, int off) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, NT ? kNt : 0);
 }
 
+// ds_read_b64_tr_b16 (gfx950): each lane addresses 8 bytes (four 16-bit
+// elements) of LDS; within every group of 16 lanes, lane 4a+e receives as its
+// element i the element e read by lane a+4i (a 4x4 transpose of 4-element
+// chunks).  p must point into a __shared__ array, 8-byte aligned.
+__device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
 // Load / store of one unit of A bytes (A = 2, 4, 8, 16) through a buffer resource.
 template <int A> struct BufUnit;
 template <> struct BufUnit<16> {

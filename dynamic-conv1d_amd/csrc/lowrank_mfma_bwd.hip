@@ -18,9 +18,11 @@ namespace dc {
 //     For each j the lane's four G values of column NJ*n+j are exactly the
 //     B operand (rows 4q..4q+3 of column n); A is z_eff transposed.
 //   * dz[t, r] += sum_d G_k[t, d] U_eff[r, kD+d]: needs K = channels.  Each
-//     wavefront writes its G tile row-major into its own LDS slot and reads
-//     it back channel-contiguous (one row, 8 channels per lane), the A operand
+//     wavefront writes the packed dU operands (G transposed: channel-major,
+//     4 rows per 8 bytes) into its own LDS slot, and two transposing reads
+//     (ds_read_b64_tr_b16) return one row, 8 channels per lane: the A operand
 //     of a 16x16x32 MFMA.  All values are bf16-exact, so this is exact.
+//   * The residual's dy term rides on tap 0: its MFMA accumulator starts at 1.
 //   * dx[t, d] = sum_k dy[t+k, d] Kw[t+k, k, d] (+ dy).  For 2 <= W <= 4 in
 //     scatter form: a lane takes the tap weights of its own rows 4q..4q+3
 //     (one MFMA row block) and adds dy[s] Kw[s, k] to dx row s-k; the sums
@@ -175,10 +177,14 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   constexpr bool UWREG = W * RC <= 8;   // tap-weight operands in registers
   constexpr int NUW = W * RC * NJ;  // packed tap-weight operands per lane
   constexpr int NUZ = W * RC * NS;  // dz operands per lane
-  constexpr int GROW = CPW + 8;     // G tile row pitch (CPW channels + 8 pad: conflict-free reads)
+  // G tile in LDS, transposed: channel c's rows 4p..4p+3 (8 bytes) at byte
+  // p*GPL + 8c + 8(c/16).  Written from the dU operands as they are packed;
+  // read back with ds_read_b64_tr_b16 as the dz operand.  The pad of 8 bytes
+  // per 16 channels keeps both access patterns within two-way bank conflicts.
+  constexpr int GPL = 8 * CPW + CPW / 2;  // bytes per 4-row plane
   __shared__ u32x2 uw_lds[NW][UWREG ? 1 : NUW * 64];
   __shared__ u32x4 uz_lds[NW][NUZ * 64];
-  __shared__ __attribute__((aligned(16))) uint16_t gtile[NW][16 * GROW];
+  __shared__ __attribute__((aligned(16))) uint8_t gtile[NW][4 * GPL];
   // dz partial sums of the workgroup's 4 chunks, gathered for DZB tiles and
   // reduced once per batch (double-buffered: one barrier per batch).  Two
   // rank chunks batch too once registers already hold occupancy at one
@@ -238,7 +244,15 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   typedef ZRaw<T, RC, ZV> ZR;
   u32x2* __restrict__ my_uw = uw_lds[wave];
   u32x4* __restrict__ my_uz = uz_lds[wave];
-  uint16_t* __restrict__ my_g = gtile[wave];
+  // G^T write position of the lane's channel NJ*n (plus 8j for channel NJ*n+j,
+  // j < NJ), and the transposed-read position that returns row n, channels
+  // 8q..8q+3 (plus 32 for 8q+4..8q+7, plus 8*32+16 per 32-channel block): the
+  // instruction hands lane 4a+e of a 16-lane group element e of the 8 bytes
+  // addressed by lane a+4i, as its element i.
+  uint8_t* const my_g = gtile[wave];
+  const int gw_lane = q * GPL + NJ * 8 * n + (n / (16 / NJ)) * 8;
+  const int gr_lane = (n & 3) * GPL + (8 * q + (n >> 2)) * 8 + (q >> 1) * 8;
+  const float res = a.residual ? 1.f : 0.f;  // tap 0's weight + 1: the residual term dy
   // dy is [B, T, D] (yhd == D) or head-major [B, D/yhd, T, yhd]; the host takes
   // this path only when yhd % CPW == 0, so a wavefront's channels lie in one
   // head and its dy resource covers that head's [T, yhd] block (rows past T
@@ -348,7 +362,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   // `own` for rows of the lane, into S for rows of the group above.
   auto scatter_taps = [&](const u32x2(&zA0)[RC], const float(&dyf)[NDY][NJ], int k, int j, float(&own)[4][NJ],
                           float(&S)[NSC][NJ]) {
-    f32x4 wk = {0.f, 0.f, 0.f, 0.f};
+    const float w0 = k == 0 ? res : 0.f;
+    f32x4 wk = {w0, w0, w0, w0};
 #pragma unroll
     for (int c = 0; c < RC; ++c)
       wk = Mma16<T>::run(zA0[c], UWREG ? uw_reg[UWREG ? (k * RC + c) * NJ + j : 0]
@@ -409,11 +424,6 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j) gf[i][j] = dyf[i][j] * Mma16<T>::to_f(LV::elem(xr[i - k + W - 1], j));
-      // Row-major copy of the G tile in this wavefront's LDS, read back below as
-      // the transposed (channel-contiguous) A operand of the dz MFMA.
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<typename LV::type*>(my_g + (4 * q + i) * GROW + NJ * n) = LV::template pack<T>(gf[i]);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         if constexpr (SC) scatter_taps(zA[0], dyf, k, j, dxa, S);
@@ -421,7 +431,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
 #pragma unroll
         for (int bb = 0; bb < (SC ? 0 : NB); ++bb) {
           if (4 * bb > 3 + k || 4 * bb + 3 < k) continue;
-          f32x4 wk = {0.f, 0.f, 0.f, 0.f};
+          const float w0 = k == 0 ? res : 0.f;  // k = 0 uses block 0 only
+          f32x4 wk = {w0, w0, w0, w0};
 #pragma unroll
           for (int c = 0; c < RC; ++c)
             wk = Mma16<T>::run(zA[bb][c], UWREG ? uw_reg[UWREG ? (k * RC + c) * NJ + j : 0]
@@ -432,29 +443,27 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
             if (tr >= 4 * bb && tr < 4 * bb + 4) dxa[i][j] = fmaf(dyf[tr][j], wk[tr - 4 * bb], dxa[i][j]);
           }
         }
-        // dU (K = rows): column j of G, rows 4q..4q+3, is the B operand as it lies.
+        // dU (K = rows): column j of G, rows 4q..4q+3, is the B operand as it
+        // lies; the same 8 bytes go to the transposed G tile.
         u32x2 g;
         g[0] = pack2<T>(gf[0][j], gf[1][j]);
         g[1] = pack2<T>(gf[2][j], gf[3][j]);
+        *reinterpret_cast<u32x2*>(my_g + gw_lane + 8 * j) = g;
 #pragma unroll
         for (int c = 0; c < RC; ++c) du[k][c][j] = Mma16<T>::run(zT[c], g, du[k][c][j]);
       }
       // dz (K = 32 channels): A = G row n (this lane: row = lane % 16), channels 32s+8q..+7.
 #pragma unroll
       for (int s2 = 0; s2 < NS; ++s2) {
-        const u32x4 ga = *reinterpret_cast<const u32x4*>(my_g + n * GROW + 32 * s2 + 8 * q);
+        const u32x2 lo = lds_read_tr16(my_g + gr_lane + s2 * (8 * 32 + 16));
+        const u32x2 hi = lds_read_tr16(my_g + gr_lane + s2 * (8 * 32 + 16) + 32);
+        const u32x4 ga = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
         for (int c = 0; c < RC; ++c) dz[c] = Mma32<T>::run(ga, my_uz[((k * RC + c) * NS + s2) * 64 + lane], dz[c]);
       }
     }
 
-    // ---- dx rows (+ residual dy); out-of-range stores are dropped
-    if (a.residual) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) dxa[i][j] += dyf[i][j];
-    }
+    // ---- dx rows (the residual dy rides on tap 0's weight); out-of-range stores are dropped
     if constexpr (SC) {
       close_rows(dxa, S, tile);
     } else {
@@ -472,13 +481,17 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     if (slot == DZB - 1 || it == nit - 1) {
       __syncthreads();
       constexpr int PER_RUN = RC * 256;
-      const int per_batch = (slot + 1) * PER_RUN;
+      constexpr int NTH = 64 * NW;
+      static_assert(DZB * PER_RUN % NTH == 0, "whole passes over a full batch");
 #pragma unroll
       for (int ri = 0; ri < NRW; ++ri) {
         const Run& ru = ri == 0 ? runs[0] : runs[NRW - 1];
-        float* __restrict__ out = part_dz + ((int64_t)cg * a.BT + ru.row0) * R;  // row 0 of run ri's sequence
+        // rows of run ri's sequence; t >= T falls outside the resource
+        const rsrc_t rout = make_rsrc(part_dz + ((int64_t)cg * a.BT + ru.row0) * R, (int64_t)Tn * R * 4);
         const int tb = ru.tile0 + it - slot;  // run ri's tile of slot 0
-        for (int e2 = threadIdx.x; e2 < per_batch; e2 += 64 * NW) {
+#pragma unroll
+        for (int m = 0; m < DZB * PER_RUN / NTH; ++m) {
+          const int e2 = (int)threadIdx.x + m * NTH;
           const int sl = e2 / PER_RUN, rem = e2 - sl * PER_RUN;
           const int c = rem >> 8, rr = (rem >> 4) & 15, nn = rem & 15;
           const int r = 16 * c + nn;
@@ -487,7 +500,9 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
           float v = dzred[buf][ri][0][sl][rem];
 #pragma unroll
           for (int w2 = 1; w2 < NCW; ++w2) v += dzred[buf][ri][w2][sl][rem];
-          if (ti < ru.tile1 && r < R && t < Tn) out[t * R + r] = v;
+          // slots past this batch (a short last batch), tiles past the run and ranks >= R store nothing
+          const bool ok = sl <= slot && ti < ru.tile1 && r < R;
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rout, ok ? (t * R + r) * 4 : kOobLane, 0, 0);
         }
       }
     }
@@ -563,18 +578,23 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
         for (int i = 0; i < 4; ++i) du[k][0][j][i] += xch[((cw * W + k) * 16 + j * 4 + i) * 64 + lane];
   }
 
-  // ---- dU partial of this workgroup row: rows r < RK of U_eff, the wavefront's 64 columns per tap
+  // ---- dU partial of this workgroup row: rows r < RK of U_eff, the wavefront's
+  // CPW columns per tap.  The resource spans this row's RK x W*D partial, so
+  // rows r >= RK fall outside it (the host keeps (RK + 16) * W * D * 4 bytes
+  // below kOobLane, so no offset wraps).
+  const rsrc_t rdu = make_rsrc(part_du + (int64_t)sp * RK * WD, (int64_t)RK * WD * 4);
+  const int du_lane = chv ? (4 * q * (int)WD + col) * 4 : kOobLane;
 #pragma unroll
   for (int k = 0; k < W; ++k)
 #pragma unroll
     for (int c = 0; c < RC; ++c)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j)
+      for (int i = 0; i < 4; ++i) {
+        const int off = du_lane + ((16 * c + i) * (int)WD + k * D) * 4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 16 * c + 4 * q + i;
-          if (r < RK && chv) part_du[((int64_t)sp * RK + r) * WD + (int64_t)k * D + col + j] = du[k][c][j][i];
-        }
+        for (int j = 0; j < NJ; ++j)
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(du[k][c][j][i]), rdu, off + 4 * j, 0, 0);
+      }
 }
 
 // ------------------------------------------------------------------- host
