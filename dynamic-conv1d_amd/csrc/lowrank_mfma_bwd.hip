@@ -118,42 +118,52 @@ __device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds, u32x2 (&u
                                            const uint16_t* __restrict__ sw, int R, int RK, int D, int d0, int q,
                                            int n, int lane) {
   typedef LaneVec<NJ> LV;
-  const int64_t WD = (int64_t)W * D;
-  const bool chv = d0 + NJ * n < D;
+  const int WD = W * D;  // R * W * D * 2 bytes lie below kOobLane (host check)
+  // Buffer loads, all issued before the first use: rows r >= R of U and lanes
+  // outside D read 0; the static row (r == R < RK) is read from sw and OR-ed in.
+  const rsrc_t ru = make_rsrc(U, (int64_t)R * WD * 2);
+  const rsrc_t rs = make_rsrc(sw, RK > R ? (int64_t)WD * 2 : 0);
+  const int cw = d0 + NJ * n < D ? (d0 + NJ * n) * 2 : kOobLane;  // the lane's tap-weight channels
+  typename LV::type rows[W][RC][4];
+  u32x4 zr[W][RC][NS];
 #pragma unroll
-  for (int k = 0; k < W; ++k) {
+  for (int k = 0; k < W; ++k)
 #pragma unroll
     for (int c = 0; c < RC; ++c) {
-      typename LV::type rows[4];
+      const bool has_static = RK > R && R >= 16 * c && R < 16 * c + 16;  // chunk c holds the static row
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const int r = 16 * c + 4 * q + kk;
-        const uint16_t* src = nullptr;
-        if (chv && r < R) src = U + (int64_t)r * WD + (int64_t)k * D + d0 + NJ * n;
-        else if (chv && r < RK) src = sw + (int64_t)k * D + d0 + NJ * n;
-        rows[kk] = src ? *reinterpret_cast<const typename LV::type*>(src) : typename LV::type{};
-      }
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        u32x2 uw;
-        uw[0] = LV::elem(rows[0], j) | (LV::elem(rows[1], j) << 16);
-        uw[1] = LV::elem(rows[2], j) | (LV::elem(rows[3], j) << 16);
-        if constexpr (UWREG)
-          uw_reg[(k * RC + c) * NJ + j] = uw;
-        else
-          uw_lds[((k * RC + c) * NJ + j) * 64 + lane] = uw;
+        rows[k][c][kk] = LV::load(ru, r < R ? cw + (r * WD + k * D) * 2 : kOobLane) |
+                         LV::load(rs, has_static && r == R ? cw + k * D * 2 : kOobLane);
       }
       const int r = 16 * c + n;
 #pragma unroll
       for (int s2 = 0; s2 < NS; ++s2) {
         const int dd = d0 + 32 * s2 + 8 * q;  // multiple of 8; D % 16 == 0, so dd < D means dd + 8 <= D
-        const uint16_t* src = nullptr;
-        if (dd < D && r < R) src = U + (int64_t)r * WD + (int64_t)k * D + dd;
-        else if (dd < D && r < RK) src = sw + (int64_t)k * D + dd;
-        uz_lds[((k * RC + c) * NS + s2) * 64 + lane] = src ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
+        const int cz = dd < D ? dd * 2 : kOobLane;
+        zr[k][c][s2] = bload128(ru, r < R ? cz + (r * WD + k * D) * 2 : kOobLane) |
+                       bload128(rs, has_static && r == R ? cz + k * D * 2 : kOobLane);
       }
     }
-  }
+#pragma unroll
+  for (int k = 0; k < W; ++k)
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const typename LV::type(&rw)[4] = rows[k][c];
+        u32x2 uw;
+        uw[0] = LV::elem(rw[0], j) | (LV::elem(rw[1], j) << 16);
+        uw[1] = LV::elem(rw[2], j) | (LV::elem(rw[3], j) << 16);
+        if constexpr (UWREG)
+          uw_reg[(k * RC + c) * NJ + j] = uw;
+        else
+          uw_lds[((k * RC + c) * NJ + j) * 64 + lane] = uw;
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < NS; ++s2) uz_lds[((k * RC + c) * NS + s2) * 64 + lane] = zr[k][c][s2];
+    }
 }
 
 template <typename T, int W, int RC, bool ZV, int NRW, int CPW>
@@ -268,8 +278,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   const int xlane_off = chv ? (4 * q * a.xld + col) * 2 : kOobLane;
   const int dxlane_off = chv ? (4 * q * a.dxld + col) * 2 : kOobLane;
 
-  u32x2 uw_reg[UWREG ? NUW : 1];
-  stage_uops<W, RC, UWREG, NJ, NS>(my_uw, uw_reg, my_uz, U, sw, R, RK, D, d0, q, n, lane);
+  u32x2 uw_reg[UWREG ? NUW : 1];  // staged below, after the first tile's loads are issued
 
   // Identity as the B operand: lane (q, n) gives rows 4q..4q+3 of column n.
   u32x2 ident;
@@ -512,6 +521,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   // dz batches are shared); tiles past its own run load and store nothing.
   TileIn ta, tb;
   load_tile(tile0, ta);
+  __builtin_amdgcn_sched_barrier(0);  // the first tile's loads go out before the U staging waits
+  stage_uops<W, RC, UWREG, NJ, NS>(my_uw, uw_reg, my_uz, U, sw, R, RK, D, d0, q, n, lane);
   for (int it = 0; it < nit; it += 2) {
     load_tile(tile0 + it + 1, tb);
     __builtin_amdgcn_sched_barrier(0);  // issue the next tile's loads before this tile's waits
