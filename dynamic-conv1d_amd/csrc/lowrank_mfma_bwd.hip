@@ -72,7 +72,11 @@ struct LrBwdArgs {
   int nblk1;  // ncg * npair: blocks per group
   int xld;    // row stride of x (elements)
   int dxld;   // row stride of dx (elements)
-  int zvec;   // R % 4 == 0 and z 8-byte aligned: 8-byte z loads
+  // z rows: zld elements apart, ranks < zr loaded, ranks zr .. zrk-1 of z_eff
+  // added as the static rank (ZRaw).  z itself (zld = zr = R, zrk = RK) when
+  // R % 4 == 0 and z is 8-byte aligned, else the padded z_eff copy in the
+  // workspace (zld = zr = zrk = RP, the static column included).
+  int zld, zr, zrk;
   int yhd;    // dy layout: D ([B, T, D]) or the head dim of [B, D/yhd, T, yhd]
   int64_t BT;
   LrBwdGroup grp[kMaxGroups];
@@ -166,7 +170,7 @@ __device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds, u32x2 (&u
     }
 }
 
-template <typename T, int W, int RC, bool ZV, int NRW, int CPW>
+template <typename T, int W, int RC, int NRW, int CPW>
 __global__ __launch_bounds__(64 * (256 / CPW) * NRW)
 __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))) void lr_bwd_mfma(LrBwdArgs a) {
   constexpr int NJ = CPW / 16;     // channels per lane
@@ -251,7 +255,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   const int tile0 = me.tile0, tile1 = me.tile1;
   const int64_t row0 = me.row0;
   const int R = a.R, RK = a.RK;
-  typedef ZRaw<T, RC, ZV> ZR;
+  typedef ZRaw<T, RC, true> ZR;  // 8-byte z loads: rows of zld % 4 == 0 elements
   u32x2* __restrict__ my_uw = uw_lds[wave];
   u32x4* __restrict__ my_uz = uz_lds[wave];
   // G^T write position of the lane's channel NJ*n (plus 8j for channel NJ*n+j,
@@ -272,7 +276,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   const rsrc_t rx = make_rsrc(x + row0 * a.xld, (int64_t)Tn * xrowb);
   const rsrc_t rdy = make_rsrc(dy + row0 * D + (int64_t)head * Tn * yhd, (int64_t)Tn * rowb);
   const rsrc_t rdx = make_rsrc(dx + row0 * a.dxld, (int64_t)Tn * dxrowb);
-  const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 2);
+  const int zld = a.zld, zr = a.zr, zrk = a.zrk;
+  const rsrc_t rz = make_rsrc(z + row0 * zld, (int64_t)Tn * zld * 2);
   // byte offsets of the lane's row-4q channels in dy, x and dx
   const int lane_off = chv ? (4 * q * yhd + col - head * yhd) * 2 : kOobLane;
   const int xlane_off = chv ? (4 * q * a.xld + col) * 2 : kOobLane;
@@ -320,7 +325,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
 #pragma unroll
     for (int m = 0; m < NDY; ++m) in.dyr[m] = LV::load(rdy, lane_off + toff + m * rowb);
 #pragma unroll
-    for (int bb = 0; bb < NB; ++bb) in.zr[bb].load(rz, ylive ? (tile * 16 + 4 * bb + n) * R * 2 : kOobTile, R, q);
+    for (int bb = 0; bb < NB; ++bb) in.zr[bb].load(rz, ylive ? (tile * 16 + 4 * bb + n) * zld * 2 : kOobTile, zr, q);
   };
 
   // Scatter form: S[m] holds the lane's contributions to row 4q-1-m (the group
@@ -395,7 +400,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     const typename LV::type(&dyr)[NDY] = in.dyr;
     u32x2 zA[NB][RC];
 #pragma unroll
-    for (int bb = 0; bb < NB; ++bb) in.zr[bb].finish(zA[bb], t0 + 4 * bb + n, R, RK, Tn, q);
+    for (int bb = 0; bb < NB; ++bb) in.zr[bb].finish(zA[bb], t0 + 4 * bb + n, zr, zrk, Tn, q);
     // z_eff transposed (rank n, rows 4q..4q+3), the A operand of the dU MFMA,
     // from row block 0 through the exact identity transpose.
     u32x2 zT[RC];
@@ -538,7 +543,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     auto flush = [&](const TileIn& in) {
       const int tile = tile0 + nit;
       u32x2 zA0[RC];
-      in.zr[0].finish(zA0, tile * 16 + n, R, RK, Tn, q);
+      in.zr[0].finish(zA0, tile * 16 + n, zr, zrk, Tn, q);
       float dyf[NDY][NJ], own[4][NJ], S[NSC][NJ];
 #pragma unroll
       for (int m = 0; m < NDY; ++m)
@@ -643,22 +648,48 @@ LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   a.npair = (a.nseg + sh.nrw - 1) / sh.nrw;
   a.nblk = a.npair * a.ncg;
   a.BT = p.B * p.T;
-  a.zvec = p.R % 4 == 0 && aligned_to(p.z, 8);
+  a.zld = a.zr = (int)p.R;
+  a.zrk = a.RK;
   return a;
+}
+
+// Ranks of the padded z_eff copy: RK rounded up to a multiple of 4.
+inline int64_t zpad_ranks(const LrProblem& p) { return (p.R + (p.static_w ? 1 : 0) + 3) / 4 * 4; }
+
+// z_eff[t, r] = z[t, r] (r < R), 1 (r == R, static_w given), 0 up to RP: the
+// backward's z operand when z cannot be read 8 bytes at a time.
+struct ZpadArgs {
+  const uint16_t* z[kMaxGroups];
+  uint16_t* zp[kMaxGroups];
+  int64_t n;  // BT * RP elements per group
+  int R, RP, stat, one;
+};
+__global__ __launch_bounds__(256) void lr_zpad(ZpadArgs a) {
+  const int g = blockIdx.y;
+  const uint16_t* __restrict__ z = g == 0 ? a.z[0] : g == 1 ? a.z[1] : g == 2 ? a.z[2] : a.z[3];
+  uint16_t* __restrict__ zp = g == 0 ? a.zp[0] : g == 1 ? a.zp[1] : g == 2 ? a.zp[2] : a.zp[3];
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.n) return;
+  const int64_t t = i / a.RP;
+  const int r = (int)(i - t * a.RP);
+  zp[i] = r < a.R ? z[t * a.R + r] : (uint16_t)(r == a.R && a.stat ? a.one : 0);
 }
 
 constexpr int kBwdTargetWaves = 2048;
 
-// Workspace: [dz partials: ncg x BT x R fp32][dU partials: npair x RK x W*D fp32], 256-byte aligned.
+// Workspace: [dz partials: ncg x BT x R fp32][dU partials: npair x RK x W*D fp32]
+// [padded z_eff: BT x RP of z's type], each 256-byte aligned.  The z_eff part
+// is reserved whatever the pointers' alignment (the size query has none).
 struct BwdWs {
-  int64_t dz_off, du_off, total;
+  int64_t dz_off, du_off, zp_off, total;
 };
 BwdWs bwd_ws(const LrProblem& p, const LrBwdArgs& a) {
   BwdWs w;
   const int64_t dz = (int64_t)a.ncg * a.BT * a.R * 4;
   w.dz_off = 0;
   w.du_off = (dz + 255) / 256 * 256;
-  w.total = w.du_off + (int64_t)a.npair * a.RK * p.W * p.D * 4;
+  w.zp_off = (w.du_off + (int64_t)a.npair * a.RK * p.W * p.D * 4 + 255) / 256 * 256;
+  w.total = w.zp_off + a.BT * zpad_ranks(p) * 2;
   return w;
 }
 
@@ -673,17 +704,33 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
   a.xld = (int)p[0].xld();
   a.dxld = (int)p[0].dxld();
   a.yhd = (int)p[0].yhd();
+  bool zvec = p[0].R % 4 == 0;
   for (int g = 0; g < G; ++g) {
     float* pdz = (float*)((char*)p[g].ws + w.dz_off);
     float* pdu = (float*)((char*)p[g].ws + w.du_off);
     a.grp[g] = LrBwdGroup{p[g].x, p[g].z, p[g].U, p[g].static_w, p[g].dy, p[g].dx, pdz, pdu};
-    a.zvec = a.zvec && aligned_to(p[g].z, 8);
+    zvec = zvec && aligned_to(p[g].z, 8);
   }
-  if (a.zvec)
-    lr_bwd_mfma<T, W, RC, true, NRW, CPW><<<a.nblk, NT, 0, p[0].stream>>>(a);
-  else
-    lr_bwd_mfma<T, W, RC, false, NRW, CPW><<<a.nblk, NT, 0, p[0].stream>>>(a);
-  hipError_t e = hipGetLastError();
+  hipError_t e;
+  if (!zvec) {
+    ZpadArgs za;
+    const int64_t RP = zpad_ranks(p[0]);
+    za.n = a.BT * RP;
+    za.R = (int)p[0].R;
+    za.RP = (int)RP;
+    za.stat = p[0].static_w != nullptr;
+    za.one = Mma16<T>::kOne;
+    for (int g = 0; g < kMaxGroups; ++g) {
+      za.z[g] = (const uint16_t*)p[g < G ? g : 0].z;
+      za.zp[g] = (uint16_t*)((char*)p[g < G ? g : 0].ws + w.zp_off);
+    }
+    for (int g = 0; g < G; ++g) a.grp[g].z = za.zp[g];
+    a.zld = a.zr = a.zrk = (int)RP;
+    lr_zpad<<<dim3((unsigned)((za.n + 255) / 256), G), 256, 0, p[0].stream>>>(za);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  lr_bwd_mfma<T, W, RC, NRW, CPW><<<a.nblk, NT, 0, p[0].stream>>>(a);
+  e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t WD = p[0].W * p[0].D, RKWD = (int64_t)a.RK * WD, R = p[0].R;
   PartialReduce jobs[kMaxReduceJobs];
