@@ -199,10 +199,12 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   __shared__ u32x2 uw_lds[NW][UWREG ? 1 : NUW * 64];
   __shared__ u32x4 uz_lds[NW][NUZ * 64];
   __shared__ __attribute__((aligned(16))) uint8_t gtile[NW][4 * GPL];
-  // dz partial sums of the workgroup's 4 chunks, gathered for DZB tiles and
+  // dz partial sums of the workgroup's chunks, gathered for DZB tiles and
   // reduced once per batch (double-buffered: one barrier per batch).  Two
   // rank chunks batch too once registers already hold occupancy at one
-  // wavefront per SIMD (W >= 2); at W = 1 the smaller LDS keeps two.
+  // wavefront per SIMD (W >= 2); at W = 1 the smaller LDS keeps two.  Row r,
+  // rank n of a tile sits at (16r + n) ^ ((r / 4) << 4): the XOR puts the
+  // four row groups a lane quarter writes at once in different banks.
   constexpr int DZB = !UWREG ? 1 : RC == 1 ? 4 : (RC == 2 && W >= 2) ? (CPW == 32 ? 2 : 4) : 1;
   __shared__ float dzred[2][NRW][NCW][DZB][RC * 256];
 
@@ -491,7 +493,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
 #pragma unroll
     for (int c = 0; c < RC; ++c)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dzred[buf][rw][cw][slot][c * 256 + (4 * q + i) * 16 + n] = dz[c][i];
+      for (int i = 0; i < 4; ++i) dzred[buf][rw][cw][slot][c * 256 + (((4 * q + i) * 16 + n) ^ (q << 4))] = dz[c][i];
     if (slot == DZB - 1 || it == nit - 1) {
       __syncthreads();
       constexpr int PER_RUN = RC * 256;
@@ -511,9 +513,10 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
           const int r = 16 * c + nn;
           const int ti = tb + sl;  // the slot's tile of run ri
           const int t = ti * 16 + rr;
-          float v = dzred[buf][ri][0][sl][rem];
+          const int pos = rem ^ (((rem >> 6) & 3) << 4);  // as written: row group (rr / 4) XOR-ed into bits 4-5
+          float v = dzred[buf][ri][0][sl][pos];
 #pragma unroll
-          for (int w2 = 1; w2 < NCW; ++w2) v += dzred[buf][ri][w2][sl][rem];
+          for (int w2 = 1; w2 < NCW; ++w2) v += dzred[buf][ri][w2][sl][pos];
           // slots past this batch (a short last batch), tiles past the run and ranks >= R store nothing
           const bool ok = sl <= slot && ti < ru.tile1 && r < R;
           __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rout, ok ? (t * R + r) * 4 : kOobLane, 0, 0);
