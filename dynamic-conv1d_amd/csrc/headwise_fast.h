@@ -109,6 +109,22 @@ struct HwRun {
   __device__ __forceinline__ int wrow(int t, bool live = true) const { return live ? (t - base) * wrowb : kHwRowOob; }
 };
 
+// acc + a.lo * b.lo + a.hi * b.hi for packed 16-bit pairs (v_dot2c_f32_bf16 /
+// v_dot2c_f32_f16): the products of two 16-bit values are exact in fp32.
+template <typename T> struct Dot2;
+template <> struct Dot2<bf16> {
+  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+  __device__ static __forceinline__ float run(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), acc, false);
+  }
+};
+template <> struct Dot2<fp16> {
+  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+  __device__ static __forceinline__ float run(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), acc, false);
+  }
+};
+
 // Sum over aligned groups of N lanes (N a power of two, 1..64), leaving the
 // group sum in every lane of the group: DPP butterflies (quad_perm xor 1,
 // xor 2, row_half_mirror, row_mirror: each pairs a lane with one of the other
@@ -265,6 +281,11 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
   constexpr int NWE = NHL * W;
   constexpr int U = Unroll<W>::value;
   constexpr int ES = (int)sizeof(T);
+  // 16-bit types with heads of 2+ channels in a lane: dweight's head sums by
+  // dot2 on packed pairs; the fp32 x ring then only serves dstatic_w.
+  constexpr bool DOT = ES == 2 && HSV >= 2;
+  constexpr bool XF = !DOT || HAS_STATIC;
+  constexpr int NPW = VEC * ES / 4;  // 32-bit words of a lane's row piece
   typedef Raw<T, VEC> XR;
   typedef Raw<T, NWE> WR;
   const int lb = xcd_remap(blockIdx.x, a.nblk);
@@ -311,17 +332,21 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
       else
         swr[k].zero();
     }
-    // x ring (fp32, each row converted once): row t in slot (t - t0) mod W.
-    float xf[W][VEC];
+    // x rings, row t in slot (t - t0) mod W: fp32 (each row converted once)
+    // for the per-channel products, packed 16-bit pairs for the head sums.
+    float xf[XF ? W : 1][VEC];
+    uint32_t xw[DOT ? W : 1][NPW];
     float dxa[W][VEC];
 #pragma unroll
     for (int k = 0; k < W; ++k) zero_vals<VEC>(dxa[k]);
-    zero_vals<VEC>(xf[0]);
+    if constexpr (XF) zero_vals<VEC>(xf[0]);
+    if constexpr (DOT) __builtin_memset(xw[0], 0, sizeof(xw[0]));
 #pragma unroll
     for (int i = 1; i < W; ++i) {
       XR h;
       bload_raw(h, rx, xlo + run.xrow(t0 - i));
-      h.to_float(xf[W - i]);
+      if constexpr (XF) h.to_float(xf[W - i]);
+      if constexpr (DOT) __builtin_memcpy(xw[W - i], h.u, sizeof(xw[0]));
     }
 
     struct Chunk {
@@ -359,24 +384,47 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
             dxa[q][j] = fmaf(dyv[j], c.w[u].get((j / HSV) * W + k) + swr[k].get(j), dxa[q][j]);
         }
         if (t < t1) {  // wave-uniform; no loads below
-          c.x[u].to_float(xf[p]);
+          if constexpr (XF) c.x[u].to_float(xf[p]);
           float dwv[NWE];
+          if constexpr (DOT) {
+            // dstatic_w per channel (fused products); dweight's head sums from
+            // the packed pairs of dy and x, HSV / 2 dot2 steps per head and tap.
+            __builtin_memcpy(xw[p], c.x[u].u, sizeof(xw[0]));
+            uint32_t dyw[NPW];
+            __builtin_memcpy(dyw, c.dy[u].u, sizeof(dyw));
 #pragma unroll
-          for (int k = 0; k < W; ++k) {
-            const int q = ring<W>(u, k);
-            float pr[VEC];
+            for (int k = 0; k < W; ++k) {
+              const int q = ring<W>(u, k);
+              if (HAS_STATIC) {
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) pr[j] = dyv[j] * xf[q][j];
-            if (HAS_STATIC) {
+                for (int j = 0; j < VEC; ++j) dsw[k][j] = fmaf(dyv[j], xf[q][j], dsw[k][j]);
+              }
 #pragma unroll
-              for (int j = 0; j < VEC; ++j) dsw[k][j] += pr[j];
+              for (int hh = 0; hh < NHL; ++hh) {
+                float sacc = 0.f;
+#pragma unroll
+                for (int j = 0; j < HSV / 2; ++j) sacc = Dot2<T>::run(dyw[hh * HSV / 2 + j], xw[q][hh * HSV / 2 + j], sacc);
+                dwv[hh * W + k] = sacc;
+              }
             }
+          } else {
 #pragma unroll
-            for (int hh = 0; hh < NHL; ++hh) {
-              float sacc = 0.f;
+            for (int k = 0; k < W; ++k) {
+              const int q = ring<W>(u, k);
+              float pr[VEC];
 #pragma unroll
-              for (int j = 0; j < HSV; ++j) sacc += pr[hh * HSV + j];
-              dwv[hh * W + k] = sacc;
+              for (int j = 0; j < VEC; ++j) pr[j] = dyv[j] * xf[q][j];
+              if (HAS_STATIC) {
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) dsw[k][j] += pr[j];
+              }
+#pragma unroll
+              for (int hh = 0; hh < NHL; ++hh) {
+                float sacc = 0.f;
+#pragma unroll
+                for (int j = 0; j < HSV; ++j) sacc += pr[hh * HSV + j];
+                dwv[hh * W + k] = sacc;
+              }
             }
           }
           if constexpr (LPH == 0) {
