@@ -115,7 +115,7 @@ constexpr int kOobTile = (int)kMaxSeqBytes;
 // wait for every load issued before it), ZRaw::finish forms the operands once
 // they are needed.  ZV (R % 4 == 0, z 8-byte aligned): one 8-byte load per rank
 // chunk, whose four ranks are all dynamic or all not; otherwise 2-byte element
-// loads.  Ranks >= R load nothing (out-of-range offset); finish sets the static
+// loads (the forward only: the backward reads a padded z_eff copy instead).  Ranks >= R load nothing (out-of-range offset); finish sets the static
 // rank R (inside the sequence) to 1 and ranks beyond to 0.  `base` is the z
 // byte offset of row t, or kOobTile for a tile that does not exist.
 template <typename T, int RC, bool ZV>

@@ -664,18 +664,27 @@ inline int64_t zpad_ranks(const LrProblem& p) { return (p.R + (p.static_w ? 1 : 
 struct ZpadArgs {
   const uint16_t* z[kMaxGroups];
   uint16_t* zp[kMaxGroups];
-  int64_t n;  // BT * RP elements per group
+  int64_t n;  // BT * RP / 4: 4-rank pieces per group
   int R, RP, stat, one;
 };
+// One thread per 4 ranks of a padded row (RP % 4 == 0): four 2-byte reads of
+// z (its rows need not be 4-byte aligned), one 8-byte store.
 __global__ __launch_bounds__(256) void lr_zpad(ZpadArgs a) {
   const int g = blockIdx.y;
   const uint16_t* __restrict__ z = g == 0 ? a.z[0] : g == 1 ? a.z[1] : g == 2 ? a.z[2] : a.z[3];
   uint16_t* __restrict__ zp = g == 0 ? a.zp[0] : g == 1 ? a.zp[1] : g == 2 ? a.zp[2] : a.zp[3];
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= a.n) return;
-  const int64_t t = i / a.RP;
-  const int r = (int)(i - t * a.RP);
-  zp[i] = r < a.R ? z[t * a.R + r] : (uint16_t)(r == a.R && a.stat ? a.one : 0);
+  const int64_t e = 4 * i;  // first element of the piece
+  const int64_t t = e / a.RP;
+  const int r0 = (int)(e - t * a.RP);
+  uint32_t v[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    const int r = r0 + kk;
+    v[kk] = r < a.R ? z[t * a.R + r] : (r == a.R && a.stat ? (uint32_t)a.one : 0u);
+  }
+  *reinterpret_cast<u32x2*>(zp + e) = u32x2{v[0] | (v[1] << 16), v[2] | (v[3] << 16)};
 }
 
 constexpr int kBwdTargetWaves = 2048;
@@ -718,7 +727,7 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
   if (!zvec) {
     ZpadArgs za;
     const int64_t RP = zpad_ranks(p[0]);
-    za.n = a.BT * RP;
+    za.n = a.BT * RP / 4;
     za.R = (int)p[0].R;
     za.RP = (int)RP;
     za.stat = p[0].static_w != nullptr;
