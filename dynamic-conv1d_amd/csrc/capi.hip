@@ -126,7 +126,7 @@ int dc_headwise_bwd(const void* x, const void* weight, const void* static_w, con
     return DC_ERR_ALIGN;
   const int64_t need = dc_headwise_bwd_ws_bytes(B, T, D, H, W, dtype, static_w != nullptr);
   if (need < 0) return (int)need;
-  if (need > 0 && (workspace == nullptr || ws_bytes < need || !aligned_to(workspace, 4))) return DC_ERR_WORKSPACE;
+  if (need > 0 && (workspace == nullptr || ws_bytes < need || !aligned_to(workspace, 16))) return DC_ERR_WORKSPACE;
   if ((s = device_status()) != DC_OK) return s;
   dc::HwProblem p{};
   p.x = x; p.weight = weight; p.static_w = static_w; p.dy = dy;
@@ -184,7 +184,7 @@ int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* stat
     return DC_ERR_ALIGN;
   const int64_t need = dc_lowrank_bwd_ws_bytes(B, T, D, R, W, dtype, static_w != nullptr);
   if (need < 0) return (int)need;
-  if (need > 0 && (workspace == nullptr || ws_bytes < need || !aligned_to(workspace, 4))) return DC_ERR_WORKSPACE;
+  if (need > 0 && (workspace == nullptr || ws_bytes < need || !aligned_to(workspace, 16))) return DC_ERR_WORKSPACE;
   if ((s = device_status()) != DC_OK) return s;
   dc::LrProblem p{};
   p.x = x; p.z = z; p.U = U; p.static_w = static_w; p.dy = dy;

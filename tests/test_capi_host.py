@@ -87,6 +87,7 @@ def test_headwise_bwd_validation(lib):
     assert hw_bwd(lib, sw=None, dsw=P) == E_NULL
     assert hw_bwd(lib, sw=P, dsw=P, ws=None, nws=need) == E_WS
     assert hw_bwd(lib, sw=P, dsw=P, ws=P, nws=need - 4) == E_WS
+    assert hw_bwd(lib, sw=P, dsw=P, ws=P + 4, nws=need) == E_WS   # workspace below 16-byte alignment
     if no_dev:
         assert hw_bwd(lib) == E_DEV
         assert hw_bwd(lib, sw=P, dsw=P, ws=P, nws=need) == E_DEV
@@ -110,6 +111,8 @@ def test_lowrank_validation(lib):
     assert lib.dc_lowrank_bwd_ws_bytes(2, 8, 16, 4, 9, 0, 1) == E_UNSUP
     st = lib.dc_lowrank_bwd(P, P, P, P, P, P, P, P, P, None, 0, 2, 8, 16, 4, 4, 0, 0, None)
     assert st == E_WS
+    st = lib.dc_lowrank_bwd(P, P, P, P, P, P, P, P, P, P + 8, need, 2, 8, 16, 4, 4, 0, 0, None)
+    assert st == E_WS  # workspace below 16-byte alignment
     st = lib.dc_lowrank_bwd(P, P, P, None, P, P, P, P, P, P, need, 2, 8, 16, 4, 4, 0, 0, None)
     assert st == E_NULL
     if no_dev:
