@@ -204,7 +204,7 @@ bool lr_mfma_ok(const LrProblem& p, bool bwd) {
   const int64_t ld = p.xld() > p.dxld() ? p.xld() : p.dxld();
   if ((p.T + kSeqSlackRows) * ld * 2 > kMaxSeqBytes) return false;
   // z rows: R ranks, or the backward's padded z_eff rows of RK rounded up to 4 (>= R)
-  const int64_t zrow = bwd ? (p.R + (p.static_w ? 1 : 0) + 3) / 4 * 4 : p.R;
+  const int64_t zrow = bwd ? lr_bwd_zrow(p.R, p.static_w != nullptr) : p.R;
   if ((p.T + kSeqSlackRows) * zrow * 2 > kMaxSeqBytes) return false;
   if (!bwd) {
     // 16-byte row pieces of x at every row: xld a multiple of 8 elements

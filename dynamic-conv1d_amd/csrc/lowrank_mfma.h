@@ -161,6 +161,13 @@ struct ZRaw {
 
 inline bool aligned_to(const void* p, int a) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// Ranks per row of the backward's padded z_eff copy: the kernel rank RK rounded
+// up to 4, or 32 for two rank chunks (17 <= RK <= 32).
+inline int64_t lr_bwd_zrow(int64_t R, bool has_static) {
+  const int64_t rk = R + (has_static ? 1 : 0);
+  return rk > 16 && rk <= 32 ? 32 : (rk + 3) / 4 * 4;
+}
+
 // Field f of group g's entry in a kernel-argument table, by selects on the
 // wave-uniform g (no dynamic indexing of the argument block).
 template <class S, class F>

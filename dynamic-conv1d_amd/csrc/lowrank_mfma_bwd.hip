@@ -116,8 +116,9 @@ template <> struct LaneVec<2> {
 //                   of the 16x16x16 tap-weight MFMA);
 //   uz[s] (s < NS = CPW/32): rank 16c+n, channels 32s+8q..32s+8q+7 as they lie
 //                   in U (B operand of the 16x16x32 dz MFMA).
-template <int W, int RC, bool UWREG, int NJ, int NS>
-__device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds, u32x2 (&uw_reg)[UWREG ? W * RC * NJ : 1],
+template <int W, int RC, bool UWREG, int NJ, int NS, bool STAGE_UW = true>
+__device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds,
+                                           u32x2 (&uw_reg)[UWREG && STAGE_UW ? W * RC * NJ : 1],
                                            u32x4* __restrict__ uz_lds, const uint16_t* __restrict__ U,
                                            const uint16_t* __restrict__ sw, int R, int RK, int D, int d0, int q,
                                            int n, int lane) {
@@ -138,8 +139,9 @@ __device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds, u32x2 (&u
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const int r = 16 * c + 4 * q + kk;
-        rows[k][c][kk] = LV::load(ru, r < R ? cw + (r * WD + k * D) * 2 : kOobLane) |
-                         LV::load(rs, has_static && r == R ? cw + k * D * 2 : kOobLane);
+        if constexpr (STAGE_UW)
+          rows[k][c][kk] = LV::load(ru, r < R ? cw + (r * WD + k * D) * 2 : kOobLane) |
+                           LV::load(rs, has_static && r == R ? cw + k * D * 2 : kOobLane);
       }
       const int r = 16 * c + n;
 #pragma unroll
@@ -155,7 +157,7 @@ __device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds, u32x2 (&u
 #pragma unroll
     for (int c = 0; c < RC; ++c) {
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
+      for (int j = 0; j < (STAGE_UW ? NJ : 0); ++j) {
         const typename LV::type(&rw)[4] = rows[k][c];
         u32x2 uw;
         uw[0] = LV::elem(rw[0], j) | (LV::elem(rw[1], j) << 16);
@@ -169,6 +171,43 @@ __device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds, u32x2 (&u
       for (int s2 = 0; s2 < NS; ++s2) uz_lds[((k * RC + c) * NS + s2) * 64 + lane] = zr[k][c][s2];
     }
 }
+
+// Tap-weight operands for K = 32 ranks (two rank chunks): lane (q, n) gives
+// ranks 8q..8q+7 of channel NJ*n+j, packed (B operand of the 16x16x32 MFMA
+// whose A is z_eff row n, ranks 8q..8q+7).  Row R (< RK) is static_w.
+template <int W, int NJ>
+__device__ __forceinline__ void stage_uw32(u32x4 (&uw)[W * NJ], const uint16_t* __restrict__ U,
+                                           const uint16_t* __restrict__ sw, int R, int RK, int D, int d0, int q,
+                                           int n) {
+  typedef LaneVec<NJ> LV;
+  const int WD = W * D;
+  const rsrc_t ru = make_rsrc(U, (int64_t)R * WD * 2);
+  const rsrc_t rs = make_rsrc(sw, RK > R ? (int64_t)WD * 2 : 0);
+  const int cw = d0 + NJ * n < D ? (d0 + NJ * n) * 2 : kOobLane;
+  typename LV::type rows[W][8];
+#pragma unroll
+  for (int k = 0; k < W; ++k)
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const int r = 8 * q + kk;
+      rows[k][kk] = LV::load(ru, r < R ? cw + (r * WD + k * D) * 2 : kOobLane) |
+                    LV::load(rs, RK > R && r == R ? cw + k * D * 2 : kOobLane);
+    }
+#pragma unroll
+  for (int k = 0; k < W; ++k)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      u32x4 v;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) v[h] = LV::elem(rows[k][2 * h], j) | (LV::elem(rows[k][2 * h + 1], j) << 16);
+      uw[k * NJ + j] = v;
+    }
+}
+
+// A operands of the tap-weight MFMA for one row block: four ranks per rank
+// chunk (16x16x16, K = 16) or, with two rank chunks, eight ranks (16x16x32).
+template <int RC, bool K32> struct ZOp { u32x2 c[RC]; };
+template <int RC> struct ZOp<RC, true> { u32x4 v; };
 
 template <typename T, int W, int RC, int NRW, int CPW>
 __global__ __launch_bounds__(64 * (256 / CPW) * NRW)
@@ -189,6 +228,11 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   constexpr int NDY = SC ? 4 : W + 3;       // dy rows 4q .. 4q+NDY-1 per lane
   constexpr int NSC = SC ? W - 1 : 1;       // scatter partial sums per channel
   constexpr bool UWREG = W * RC <= 8;   // tap-weight operands in registers
+  // Two rank chunks: the tap weights take K = 32 ranks in one 16x16x32 MFMA
+  // (z rows of exactly 32 ranks: z itself or the padded z_eff copy).
+  constexpr bool K32 = RC == 2;
+  static_assert(!K32 || UWREG, "two rank chunks keep their tap-weight operands in registers");
+  typedef ZOp<RC, K32> ZO;
   constexpr int NUW = W * RC * NJ;  // packed tap-weight operands per lane
   constexpr int NUZ = W * RC * NS;  // dz operands per lane
   // G tile in LDS, transposed: channel c's rows 4p..4p+3 (8 bytes) at byte
@@ -285,7 +329,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   const int xlane_off = chv ? (4 * q * a.xld + col) * 2 : kOobLane;
   const int dxlane_off = chv ? (4 * q * a.dxld + col) * 2 : kOobLane;
 
-  u32x2 uw_reg[UWREG ? NUW : 1];  // staged below, after the first tile's loads are issued
+  u32x2 uw_reg[UWREG && !K32 ? NUW : 1];  // staged below, after the first tile's loads are issued
+  u32x4 uw32[K32 ? W * NJ : 1];
 
   // Identity as the B operand: lane (q, n) gives rows 4q..4q+3 of column n.
   u32x2 ident;
@@ -296,6 +341,20 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     for (int kk = 0; kk < 4; ++kk) e[kk] = (4 * q + kk == n) ? one : 0u;
     ident[0] = e[0] | (e[1] << 16);
     ident[1] = e[2] | (e[3] << 16);
+  }
+  // K32: selection matrices as the B operand (ranks 8q..8q+7 of column n):
+  // sel[c] picks rank 16c+n, so z_eff x sel[c] is z_eff's rank chunk c.
+  u32x4 sel[K32 ? 2 : 1];
+  if constexpr (K32) {
+    const uint32_t one = Mma16<T>::kOne;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const uint32_t lo = (8 * q + 2 * h == 16 * c + n) ? one : 0u;
+        const uint32_t hi = (8 * q + 2 * h + 1 == 16 * c + n) ? one : 0u;
+        sel[c][h] = lo | (hi << 16);
+      }
   }
 
   f32x4 du[W][RC][NJ];
@@ -313,7 +372,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   // register is copied, so the compiler's waits stay partial (vmcnt(N)).
   struct TileIn {
     typename LV::type xr[NR], dyr[NDY];
-    ZR zr[NB];  // z_eff rows t0+4bb+n, ranks 16c+4q..+3: A operand of the tap-weight MFMA
+    ZR zr[K32 ? 1 : NB];   // z_eff rows t0+4bb+n, ranks 16c+4q..+3: A operand of the tap-weight MFMA
+    u32x4 z32[K32 ? NB : 1];  // K32: z_eff rows t0+4bb+n, ranks 8q..8q+7
   };
   auto load_tile = [&](int tile, TileIn& in) {
     const bool live = tile < tile1;
@@ -327,7 +387,12 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
 #pragma unroll
     for (int m = 0; m < NDY; ++m) in.dyr[m] = LV::load(rdy, lane_off + toff + m * rowb);
 #pragma unroll
-    for (int bb = 0; bb < NB; ++bb) in.zr[bb].load(rz, ylive ? (tile * 16 + 4 * bb + n) * zld * 2 : kOobTile, zr, q);
+    for (int bb = 0; bb < NB; ++bb) {
+      if constexpr (K32)
+        in.z32[bb] = bload128(rz, ylive ? ((tile * 16 + 4 * bb + n) * zld + 8 * q) * 2 : kOobTile);
+      else
+        in.zr[bb].load(rz, ylive ? (tile * 16 + 4 * bb + n) * zld * 2 : kOobTile, zr, q);
+    }
   };
 
   // Scatter form: S[m] holds the lane's contributions to row 4q-1-m (the group
@@ -376,14 +441,22 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   };
   // Tap weights of the lane's rows 4q..4q+3 (row block 0) times dy: into
   // `own` for rows of the lane, into S for rows of the group above.
-  auto scatter_taps = [&](const u32x2(&zA0)[RC], const float(&dyf)[NDY][NJ], int k, int j, float(&own)[4][NJ],
-                          float(&S)[NSC][NJ]) {
-    const float w0 = k == 0 ? res : 0.f;
+  // Tap k's weights of the operand's rows for channel NJ*n+j, accumulator started at w0.
+  auto tap_w = [&](const ZO& za, int k, int j, float w0) {
     f32x4 wk = {w0, w0, w0, w0};
+    if constexpr (K32) {
+      wk = Mma32<T>::run(za.v, uw32[k * NJ + j], wk);
+    } else {
 #pragma unroll
-    for (int c = 0; c < RC; ++c)
-      wk = Mma16<T>::run(zA0[c], UWREG ? uw_reg[UWREG ? (k * RC + c) * NJ + j : 0]
-                                       : my_uw[((k * RC + c) * NJ + j) * 64 + lane], wk);
+      for (int c = 0; c < RC; ++c)
+        wk = Mma16<T>::run(za.c[c], UWREG ? uw_reg[UWREG ? (k * RC + c) * NJ + j : 0]
+                                          : my_uw[((k * RC + c) * NJ + j) * 64 + lane], wk);
+    }
+    return wk;
+  };
+  auto scatter_taps = [&](const ZO& zA0, const float(&dyf)[NDY][NJ], int k, int j, float(&own)[4][NJ],
+                          float(&S)[NSC][NJ]) {
+    const f32x4 wk = tap_w(zA0, k, j, k == 0 ? res : 0.f);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = i - k;  // dx row of this contribution, relative to 4q
@@ -400,15 +473,24 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     const int dxtoff = live ? t0 * dxrowb : kOobTile;  // tiles past the run store nothing
     const typename LV::type(&xr)[NR] = in.xr;
     const typename LV::type(&dyr)[NDY] = in.dyr;
-    u32x2 zA[NB][RC];
+    ZO zA[NB];
 #pragma unroll
-    for (int bb = 0; bb < NB; ++bb) in.zr[bb].finish(zA[bb], t0 + 4 * bb + n, zr, zrk, Tn, q);
+    for (int bb = 0; bb < NB; ++bb) {
+      if constexpr (K32)
+        zA[bb].v = in.z32[bb];
+      else
+        in.zr[bb].finish(zA[bb].c, t0 + 4 * bb + n, zr, zrk, Tn, q);
+    }
     // z_eff transposed (rank n, rows 4q..4q+3), the A operand of the dU MFMA,
-    // from row block 0 through the exact identity transpose.
+    // from row block 0 through an exact identity (K32: selection) product.
     u32x2 zT[RC];
 #pragma unroll
     for (int c = 0; c < RC; ++c) {
-      const f32x4 tz = Mma16<T>::run(zA[0][c], ident, f32x4{0.f, 0.f, 0.f, 0.f});
+      f32x4 tz;
+      if constexpr (K32)
+        tz = Mma32<T>::run(zA[0].v, sel[c], f32x4{0.f, 0.f, 0.f, 0.f});
+      else
+        tz = Mma16<T>::run(zA[0].c[c], ident, f32x4{0.f, 0.f, 0.f, 0.f});
       zT[c][0] = pack2<T>(tz[0], tz[1]);
       zT[c][1] = pack2<T>(tz[2], tz[3]);
     }
@@ -447,12 +529,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
 #pragma unroll
         for (int bb = 0; bb < (SC ? 0 : NB); ++bb) {
           if (4 * bb > 3 + k || 4 * bb + 3 < k) continue;
-          const float w0 = k == 0 ? res : 0.f;  // k = 0 uses block 0 only
-          f32x4 wk = {w0, w0, w0, w0};
-#pragma unroll
-          for (int c = 0; c < RC; ++c)
-            wk = Mma16<T>::run(zA[bb][c], UWREG ? uw_reg[UWREG ? (k * RC + c) * NJ + j : 0]
-                                                : my_uw[((k * RC + c) * NJ + j) * 64 + lane], wk);
+          const f32x4 wk = tap_w(zA[bb], k, j, k == 0 ? res : 0.f);  // k = 0 uses block 0 only
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int tr = i + k;  // row offset of dy / Kw in the lane window
@@ -530,7 +607,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   TileIn ta, tb;
   load_tile(tile0, ta);
   __builtin_amdgcn_sched_barrier(0);  // the first tile's loads go out before the U staging waits
-  stage_uops<W, RC, UWREG, NJ, NS>(my_uw, uw_reg, my_uz, U, sw, R, RK, D, d0, q, n, lane);
+  stage_uops<W, RC, UWREG, NJ, NS, !K32>(my_uw, uw_reg, my_uz, U, sw, R, RK, D, d0, q, n, lane);
+  if constexpr (K32) stage_uw32<W, NJ>(uw32, U, sw, R, RK, D, d0, q, n);
   for (int it = 0; it < nit; it += 2) {
     load_tile(tile0 + it + 1, tb);
     __builtin_amdgcn_sched_barrier(0);  // issue the next tile's loads before this tile's waits
@@ -545,8 +623,11 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     // and stores nothing.
     auto flush = [&](const TileIn& in) {
       const int tile = tile0 + nit;
-      u32x2 zA0[RC];
-      in.zr[0].finish(zA0, tile * 16 + n, zr, zrk, Tn, q);
+      ZO zA0;
+      if constexpr (K32)
+        zA0.v = in.z32[0];
+      else
+        in.zr[0].finish(zA0.c, tile * 16 + n, zr, zrk, Tn, q);
       float dyf[NDY][NJ], own[4][NJ], S[NSC][NJ];
 #pragma unroll
       for (int m = 0; m < NDY; ++m)
@@ -656,8 +737,9 @@ LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   return a;
 }
 
-// Ranks of the padded z_eff copy: RK rounded up to a multiple of 4.
-inline int64_t zpad_ranks(const LrProblem& p) { return (p.R + (p.static_w ? 1 : 0) + 3) / 4 * 4; }
+// Ranks of the padded z_eff copy: RK rounded up to a multiple of 4, or 32 for
+// two rank chunks (their 16x16x32 operands read ranks 8q..8q+7 of every row).
+inline int64_t zpad_ranks(const LrProblem& p) { return lr_bwd_zrow(p.R, p.static_w != nullptr); }
 
 // z_eff[t, r] = z[t, r] (r < R), 1 (r == R, static_w given), 0 up to RP: the
 // backward's z operand when z cannot be read 8 bytes at a time.
@@ -716,12 +798,15 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
   a.xld = (int)p[0].xld();
   a.dxld = (int)p[0].dxld();
   a.yhd = (int)p[0].yhd();
-  bool zvec = p[0].R % 4 == 0;
+  // z itself when its rows are what the kernel reads: R % 4 == 0 and 8-byte
+  // aligned, or (two rank chunks) exactly 32 dynamic ranks, 16-byte aligned.
+  constexpr bool K32 = RC == 2;
+  bool zvec = K32 ? (p[0].R == 32 && p[0].static_w == nullptr) : p[0].R % 4 == 0;
   for (int g = 0; g < G; ++g) {
     float* pdz = (float*)((char*)p[g].ws + w.dz_off);
     float* pdu = (float*)((char*)p[g].ws + w.du_off);
     a.grp[g] = LrBwdGroup{p[g].x, p[g].z, p[g].U, p[g].static_w, p[g].dy, p[g].dx, pdz, pdu};
-    zvec = zvec && aligned_to(p[g].z, 8);
+    zvec = zvec && aligned_to(p[g].z, K32 ? 16 : 8);
   }
   hipError_t e;
   if (!zvec) {
