@@ -184,25 +184,27 @@ def test_edge_shapes_lowrank(Bn, Tn, Dn, R, W, static, residual, dtype):
             assert_ns(a, b, dtype, n, elementwise=n == "dx")
 
 
-@pytest.mark.parametrize("R,static,dtype", [(16, False, torch.bfloat16), (12, True, torch.bfloat16),
-                                            (32, False, torch.float16), (15, True, torch.bfloat16)])
-def test_lowrank_misaligned_z(R, static, dtype):
-    """z at a 2-byte offset: the backward pads z (with the static column) into its workspace, whatever R is."""
-    g = gen(31 * R + static)
+@pytest.mark.parametrize("R,static,dtype,off", [(16, False, torch.bfloat16, 1), (12, True, torch.bfloat16, 1),
+                                                (32, False, torch.float16, 1), (15, True, torch.bfloat16, 1),
+                                                (32, False, torch.bfloat16, 4), (16, False, torch.bfloat16, 4)])
+def test_lowrank_misaligned_z(R, static, dtype, off):
+    """z `off` elements into a buffer: the backward pads z (with the static column) into its workspace
+    when its rows cannot be read whole (8-byte rows; 16-byte for two rank chunks), whatever R is."""
+    g = gen(31 * R + static + 7 * off)
     Bn, Tn, Dn, W = 2, 72, 128, 4
     x, dy, z = randn(g, Bn, Tn, Dn), randn(g, Bn, Tn, Dn), randn(g, Bn, Tn, R)
     U = randn(g, R, W * Dn, scale=1 / math.sqrt((R + 1) * W))
     sw = uniform(g, W, Dn, lo=-1 / math.sqrt(W), hi=1 / math.sqrt(W)) if static else None
-    buf = torch.empty(Bn * Tn * R + 1, dtype=dtype, device=DEV)
-    z_off = buf[1:].view(Bn, Tn, R)
+    buf = torch.empty(Bn * Tn * R + off, dtype=dtype, device=DEV)
+    z_off = buf[off:].view(Bn, Tn, R)
     z_off.copy_(z.to(dtype))
-    assert z_off.data_ptr() % 8 != 0 and z_off.is_contiguous()
+    assert z_off.data_ptr() % 16 != 0 and z_off.is_contiguous()
     kernel = lambda a, b, c, d, residual: lr_mod._LowrankDynamicConvolutionFn.apply(a, b, c, d, residual)  # noqa: E731
     src_q = [None if t is None else t.to(dtype).float() for t in (x, z, U, sw)]
     y_q, g_q = run_fwd_bwd(lr_ref, src_q, dy.to(dtype).float(), True)
     leaves = [_to(x, dtype), z_off.detach(), _to(U, dtype), _to(sw, dtype)]  # no clone: z keeps its offset
     leaves = [None if t is None else t.requires_grad_() for t in leaves]
-    assert leaves[1].data_ptr() % 8 != 0
+    assert leaves[1].data_ptr() % 16 != 0
     y_k = kernel(*leaves, residual=True)
     y_k.backward(_to(dy, dtype))
     g_k = [None if t is None else t.grad for t in leaves]
