@@ -23,6 +23,11 @@ namespace dc {
 //     (ds_read_b64_tr_b16) return one row, 8 channels per lane: the A operand
 //     of a 16x16x32 MFMA.  All values are bf16-exact, so this is exact.
 //   * The residual's dy term rides on tap 0: its MFMA accumulator starts at 1.
+//   * Tap weights Kw[t, k, :] = z_eff[t, :] U_eff[:, k]: one 16x16x16 MFMA per
+//     rank chunk, or with two rank chunks one 16x16x32 over K = 32 ranks (z
+//     rows of 32 ranks, 16-byte aligned).  z is read 8 or 16 bytes per lane
+//     and row: z itself when its rows allow that, else a padded z_eff copy
+//     (static column included) that lr_zpad writes into the workspace first.
 //   * dx[t, d] = sum_k dy[t+k, d] Kw[t+k, k, d] (+ dy).  For 2 <= W <= 4 in
 //     scatter form: a lane takes the tap weights of its own rows 4q..4q+3
 //     (one MFMA row block) and adds dy[s] Kw[s, k] to dx row s-k; the sums
