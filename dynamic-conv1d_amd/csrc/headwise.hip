@@ -70,13 +70,22 @@ __global__ __launch_bounds__(256) void hw_bwd_dw_generic(const T* __restrict__ x
     const int h = (int)(i - row * H);
     const int t = (int)(row % Tn);
     for (int k = 0; k < W; ++k) {
-      float acc = 0.f;
+      // Compensated (Neumaier) sum over the head: a plain running fp32 sum of
+      // hundreds of products drifts well past the reference's blocked sum.
+      float s = 0.f, comp = 0.f;
       if (k <= t) {
         const T* dyr = dy + row * D + (int64_t)h * hs;
         const T* xr = x + (row - k) * D + (int64_t)h * hs;
-        for (int c = 0; c < hs; ++c) acc = fmaf((float)dyr[c], (float)xr[c], acc);
+        for (int c = 0; c < hs; ++c) {
+          // __fmul_rn / __fadd_rn: no contraction into an FMA, which would
+          // make u differ from s + p and void the compensation
+          const float p = __fmul_rn((float)dyr[c], (float)xr[c]);
+          const float u = __fadd_rn(s, p);
+          comp += fabsf(s) >= fabsf(p) ? __fadd_rn(__fsub_rn(s, u), p) : __fadd_rn(__fsub_rn(p, u), s);
+          s = u;
+        }
       }
-      dwt[i * W + k] = (T)acc;
+      dwt[i * W + k] = (T)(s + comp);
     }
   }
 }

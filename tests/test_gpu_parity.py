@@ -115,6 +115,9 @@ HW_EDGE = [
     (1, 5, 64, 64, 8, True, True, torch.bfloat16),      # W > T
     (1, 1, 64, 8, 4, True, True, torch.bfloat16),       # T 1
     (3, 129, 200, 50, 7, True, True, torch.float32),    # hs 4 fp32, W 7, D % 64*4 != 0
+    # one 320-channel head (generic kernels), fp32: dweight's head sum must stay
+    # within the elementwise 1e-5 bar (found by the random sweep)
+    (3, 200, 320, 1, 8, False, True, torch.float32),
 ]
 
 
