@@ -103,15 +103,24 @@ struct Raw {
 // at once, would make the compiler wait for every load issued before it
 // (vmcnt counts in order).
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
-// Cache-policy operand of a buffer store: nontemporal (gfx940 family `nt` bit).
+// Cache-policy operand of a buffer access: nontemporal (gfx940 family `nt` bit).
+// Stores of outputs take it.  Loads take it only where one instruction reads
+// whole cache lines that nothing reads again soon (full 1 KiB rows of a
+// wavefront): measured on a 64 MiB copy, nontemporal loads move 6.0 TB/s
+// against 5.5 TB/s for default loads.  Loads whose lines are completed by the
+// following instructions (strided per-lane pieces) or re-read as a halo keep
+// the default policy: with `nt` those lines are fetched again.
 constexpr int kNt = 2;
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
-__device__ __forceinline__ u32x4 bload128(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
-__device__ __forceinline__ u32x2 bload64(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0); }
-__device__ __forceinline__ uint32_t bload32(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
+template <int POL = 0>
+__device__ __forceinline__ u32x4 bload128(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL); }
+template <int POL = 0>
+__device__ __forceinline__ u32x2 bload64(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, POL); }
+template <int POL = 0>
+__device__ __forceinline__ uint32_t bload32(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, POL); }
 __device__ __forceinline__ uint32_t bload16(rsrc_t r, int off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
 }
@@ -138,22 +147,26 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
 // Load / store of one unit of A bytes (A = 2, 4, 8, 16) through a buffer resource.
 template <int A> struct BufUnit;
 template <> struct BufUnit<16> {
-  __device__ static __forceinline__ u32x4 load(rsrc_t r, int off) { return bload128(r, off); }
+  template <int POL = 0>
+  __device__ static __forceinline__ u32x4 load(rsrc_t r, int off) { return bload128<POL>(r, off); }
   template <bool NT> __device__ static __forceinline__ void store(u32x4 v, rsrc_t r, int off) { bstore128<NT>(v, r, off); }
 };
 template <> struct BufUnit<8> {
-  __device__ static __forceinline__ u32x2 load(rsrc_t r, int off) { return bload64(r, off); }
+  template <int POL = 0>
+  __device__ static __forceinline__ u32x2 load(rsrc_t r, int off) { return bload64<POL>(r, off); }
   template <bool NT> __device__ static __forceinline__ void store(u32x2 v, rsrc_t r, int off) { bstore64<NT>(v, r, off); }
 };
 template <> struct BufUnit<4> {
-  __device__ static __forceinline__ uint32_t load(rsrc_t r, int off) { return bload32(r, off); }
+  template <int POL = 0>
+  __device__ static __forceinline__ uint32_t load(rsrc_t r, int off) { return bload32<POL>(r, off); }
   template <bool NT> __device__ static __forceinline__ void store(uint32_t v, rsrc_t r, int off) {
     __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, NT ? kNt : 0);
   }
 };
 template <> struct BufUnit<2> {
+  template <int POL = 0>
   __device__ static __forceinline__ uint16_t load(rsrc_t r, int off) {
-    return (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    return (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, POL);
   }
   template <bool NT> __device__ static __forceinline__ void store(uint16_t v, rsrc_t r, int off) {
     __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, NT ? kNt : 0);
@@ -161,12 +174,13 @@ template <> struct BufUnit<2> {
 };
 
 // Raw<T, N> through a buffer resource: unconditional loads (an out-of-range
-// offset reads 0) and stores (an out-of-range offset writes nothing).
-template <typename T, int N>
+// offset reads 0; POL is the cache-policy operand) and stores (an
+// out-of-range offset writes nothing).
+template <int POL = 0, typename T, int N>
 __device__ __forceinline__ void bload_raw(Raw<T, N>& v, rsrc_t r, int off) {
   typedef Raw<T, N> R;
 #pragma unroll
-  for (int i = 0; i < R::NU; ++i) v.u[i] = BufUnit<R::A>::load(r, off + i * R::A);
+  for (int i = 0; i < R::NU; ++i) v.u[i] = BufUnit<R::A>::template load<POL>(r, off + i * R::A);
 }
 template <typename T, int N, bool NT = false>
 __device__ __forceinline__ void bstore_vals(rsrc_t r, int off, const float* in) {

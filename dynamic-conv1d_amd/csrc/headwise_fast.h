@@ -26,7 +26,13 @@
 // alternate: the next chunk's loads are issued before the current chunk is
 // computed and no register is copied between them, so the compiler's waits
 // stay partial (vmcnt counts in order: a load under a branch or a copy of a
-// just-loaded register would make it wait for every load in flight).
+// just-loaded register would make it wait for every load in flight).  x and
+// dy rows are whole 1 KiB wavefront rows read once: nontemporal loads (B4
+// T4096 D2048 W4 bf16: head size 32 forward 29.5 -> 27.6 us, backward
+// 50.6 -> 47.2 us; head size 1 75.6 -> 72.7 and 150.9 -> 146.4 us).  The
+// weights keep the default policy: at head size 1 a lane's 64-byte piece
+// takes 4 instructions, and nontemporal lines are fetched again between them
+// (forward 75 -> 98 us).
 //
 // Backward.  dx uses the scatter form: the row-t terms dy[t]*(w[t,k]+sw[k])
 // are added into the open accumulator of row t-k; row t-W+1 is complete
@@ -202,7 +208,7 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
 #pragma unroll
   for (int i = 1; i < W; ++i) {
     XR h;
-    bload_raw(h, rx, xlo + run.xrow(t0 - i));
+    bload_raw<kNt>(h, rx, xlo + run.xrow(t0 - i));
     h.to_float(xf[W - i]);
   }
 
@@ -210,7 +216,7 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int t = tc + u;
-      bload_raw(xc[u], rx, xlo + run.xrow(t, t < t1));
+      bload_raw<kNt>(xc[u], rx, xlo + run.xrow(t, t < t1));
       bload_raw(wc[u], rw, wlo + run.wrow(t, t < t1));
     }
   };
@@ -344,7 +350,7 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
 #pragma unroll
     for (int i = 1; i < W; ++i) {
       XR h;
-      bload_raw(h, rx, xlo + run.xrow(t0 - i));
+      bload_raw<kNt>(h, rx, xlo + run.xrow(t0 - i));
       if constexpr (XF) h.to_float(xf[W - i]);
       if constexpr (DOT) __builtin_memcpy(xw[W - i], h.u, sizeof(xw[0]));
     }
@@ -357,9 +363,9 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int t = tc + u;
-        bload_raw(c.dy[u], rdy, xlo + run.xrow(t, t < tend));  // rows past T read 0
+        bload_raw<kNt>(c.dy[u], rdy, xlo + run.xrow(t, t < tend));  // rows past T read 0
         bload_raw(c.w[u], rw, wlo + run.wrow(t, t < tend));
-        bload_raw(c.x[u], rx, xlo + run.xrow(t, t < t1));
+        bload_raw<kNt>(c.x[u], rx, xlo + run.xrow(t, t < t1));
       }
     };
     auto compute_chunk = [&](int tc, const Chunk& c) {
