@@ -29,10 +29,12 @@
 // just-loaded register would make it wait for every load in flight).  x and
 // dy rows are whole 1 KiB wavefront rows read once: nontemporal loads (B4
 // T4096 D2048 W4 bf16: head size 32 forward 29.5 -> 27.6 us, backward
-// 50.6 -> 47.2 us; head size 1 75.6 -> 72.7 and 150.9 -> 146.4 us).  The
-// weights keep the default policy: at head size 1 a lane's 64-byte piece
+// 50.6 -> 47.2 us; head size 1 75.6 -> 72.7 and 150.9 -> 146.4 us).  Per-lane
+// weight loads keep the default policy: at head size 1 a lane's 64-byte piece
 // takes 4 instructions, and nontemporal lines are fetched again between them
-// (forward 75 -> 98 us).
+// (forward 75 -> 98 us).  In whole wavefronts such pieces are loaded as
+// contiguous 1 KiB instructions and handed to their lanes through LDS
+// instead (TdwOf below), and those loads are nontemporal.
 //
 // Backward.  dx uses the scatter form: the row-t terms dy[t]*(w[t,k]+sw[k])
 // are added into the open accumulator of row t-k; row t-W+1 is complete
@@ -166,8 +168,41 @@ __device__ __forceinline__ float group_sum_sel(float v, int n) {
   return v;
 }
 
+// A lane that owns whole heads (head_size <= VEC, one lane per head group)
+// holds a weight / dweight row piece of NP 16-byte units.  With NP > 1,
+// instruction i of a per-lane access would touch every lane's i-th unit, 64
+// partial cache lines.  In whole wavefronts (nvc % 64 == 0) these pieces move
+// through LDS instead: the wavefront loads / stores its NP KiB of the row
+// as NP contiguous 1 KiB instructions (slot i*64 + l), and lane l's piece j is
+// slot l*NP + j.  Weight loads then take the nontemporal policy (head size 1,
+// B4 T4096 D2048 W4 bf16: forward 72.6 -> 72.0 us, backward 146.8 -> 143.7 us);
+// dweight stores would otherwise write each line in several partial pieces.
+template <typename T, int W, int HSV> struct TdwOf {
+  static constexpr int BYTES = (VecOf<T>::value / HSV) * W * (int)sizeof(T);
+  static constexpr bool value = BYTES % 16 == 0 && BYTES > 16;
+  static constexpr int NP = BYTES / 16;  // pieces per lane
+};
+
+// Exchanges between the lanes of one wavefront through its own LDS slots.  The
+// hardware runs a wavefront's LDS instructions in order, so no s_barrier is
+// needed, but the compiler sees only this lane's addresses: it may move a
+// later write above an earlier read that this lane provably does not alias
+// (another lane's does).  __builtin_amdgcn_wave_barrier() keeps the phases in
+// program order.
+//
+// Slots of the wavefront's contiguous 1 KiB loads -> the lane's own NP units.
+template <int NP>
+__device__ __forceinline__ void own_pieces(u32x4* my, const u32x4 (&in)[NP], u32x4 (&out)[NP], int lane) {
+  __builtin_amdgcn_wave_barrier();  // the previous exchange's reads are done
+#pragma unroll
+  for (int i = 0; i < NP; ++i) my[i * 64 + lane] = in[i];
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int j = 0; j < NP; ++j) out[j] = my[lane * NP + j];
+}
+
 // ------------------------------------------------------------------ forward
-template <typename T, int W, int HSV>
+template <typename T, int W, int HSV, bool TWL>
 __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, const T* __restrict__ wt,
                                                    const T* __restrict__ sw, T* __restrict__ y, HwArgs a) {
   constexpr int VEC = VecOf<T>::value;
@@ -192,6 +227,10 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
   const rsrc_t ry = make_rsrc(y + run.xrow0, run.xrec);
   const rsrc_t rw = make_rsrc(wt + run.wrow0, run.wrec);
   const int64_t D = a.D;
+  // TWL: transposed weight loads (TdwOf; the host guarantees whole wavefronts)
+  constexpr int NPW = TWL ? TdwOf<T, W, HSV>::NP : 1;
+  __shared__ u32x4 wlt[4][TWL ? NPW * 64 : 1];
+  const int wlo0 = (((vc - lane) * VEC) >> a.hs_shift) * W * ES;  // weight byte offset of the wavefront's lane 0
 
   XR swr[W];
 #pragma unroll
@@ -217,7 +256,12 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
     for (int u = 0; u < U; ++u) {
       const int t = tc + u;
       bload_raw<kNt>(xc[u], rx, xlo + run.xrow(t, t < t1));
-      bload_raw(wc[u], rw, wlo + run.wrow(t, t < t1));
+      if constexpr (TWL) {
+#pragma unroll
+        for (int i = 0; i < NPW; ++i) wc[u].u[i] = bload128<kNt>(rw, wlo0 + run.wrow(t, t < t1) + (i * 64 + lane) * 16);
+      } else {
+        bload_raw(wc[u], rw, wlo + run.wrow(t, t < t1));
+      }
     }
   };
   auto compute_chunk = [&](int tc, const XR(&xc)[U], const WR(&wc)[U]) {
@@ -226,13 +270,18 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
       const int t = tc + u;
       const int p = u % W;
       xc[u].to_float(xf[p]);
+      WR wr;
+      if constexpr (TWL)
+        own_pieces<NPW>(wlt[wave], wc[u].u, wr.u, lane);
+      else
+        wr = wc[u];
       float acc[VEC];
       zero_vals<VEC>(acc);
 #pragma unroll
       for (int k = 0; k < W; ++k) {
         const int q = ring<W>(u, k);
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) acc[j] = fmaf(wc[u].get((j / HSV) * W + k) + swr[k].get(j), xf[q][j], acc[j]);
+        for (int j = 0; j < VEC; ++j) acc[j] = fmaf(wr.get((j / HSV) * W + k) + swr[k].get(j), xf[q][j], acc[j]);
       }
       if (a.residual) {
 #pragma unroll
@@ -268,12 +317,6 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
 }
 
 // ----------------------------------------------------------------- backward
-// Transposed dweight store possible: 16-byte pieces, more than one per lane.
-template <typename T, int W, int HSV> struct TdwOf {
-  static constexpr int BYTES = (VecOf<T>::value / HSV) * W * (int)sizeof(T);
-  static constexpr bool value = BYTES % 16 == 0 && BYTES > 16;
-  static constexpr int NP = BYTES / 16;  // pieces per lane
-};
 
 // LPH: lanes per head when known at compile time (1, 2, 4, 8), or 0 for the
 // run-time group size a.lph (head sizes of 16 lanes and more).
@@ -301,7 +344,8 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
   const int s = sgp * 4 + wave;
   // TDW: the host guarantees nvc % 64 == 0, so every lane is inside D.
   constexpr int NP = TDW ? TdwOf<T, W, HSV>::NP : 1;
-  __shared__ u32x4 dwt[4][TDW ? NP * 64 : 1];
+  __shared__ u32x4 dwt[4][TDW ? NP * 64 : 1];  // dweight stores
+  __shared__ u32x4 wlt[4][TDW ? NP * 64 : 1];  // weight loads
 
   float dsw[W][VEC];
 #pragma unroll
@@ -320,7 +364,7 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
     const int lph = LPH > 0 ? LPH : a.lph;
     const bool leader = (vc & (lph - 1)) == 0;
     const int dwlo = leader ? wlo : kHwLaneOob;  // one lane of a head stores its dweight
-    // dweight byte offset of the wavefront's lane 0 (TDW: lanes own consecutive heads)
+    // weight / dweight byte offset of the wavefront's lane 0 (TDW: lanes own consecutive heads)
     const int wlo0 = (((vc - lane) * VEC) >> a.hs_shift) * W * ES;
     const rsrc_t rx = make_rsrc(x + run.xrow0, run.xrec);
     const rsrc_t rdy = make_rsrc(dy + run.xrow0, run.xrec);
@@ -364,7 +408,12 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
       for (int u = 0; u < U; ++u) {
         const int t = tc + u;
         bload_raw<kNt>(c.dy[u], rdy, xlo + run.xrow(t, t < tend));  // rows past T read 0
-        bload_raw(c.w[u], rw, wlo + run.wrow(t, t < tend));
+        if constexpr (TDW) {
+#pragma unroll
+          for (int i = 0; i < NP; ++i) c.w[u].u[i] = bload128<kNt>(rw, wlo0 + run.wrow(t, t < tend) + (i * 64 + lane) * 16);
+        } else {
+          bload_raw(c.w[u], rw, wlo + run.wrow(t, t < tend));
+        }
         bload_raw<kNt>(c.x[u], rx, xlo + run.xrow(t, t < t1));
       }
     };
@@ -375,11 +424,16 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
         const int p = u % W;
         float dyv[VEC];
         c.dy[u].to_float(dyv);
+        WR wr;
+        if constexpr (TDW)
+          own_pieces<NP>(wlt[wave], c.w[u].u, wr.u, lane);
+        else
+          wr = c.w[u];
         // dx[t-k] += dy[t] * (w[t, h, k] + sw[k]); row t opens with its k = 0 term.
         // Steps past tend read dy = w = 0 and add nothing.
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
-          const float v = dyv[j] * (c.w[u].get((j / HSV) * W) + swr[0].get(j));
+          const float v = dyv[j] * (wr.get((j / HSV) * W) + swr[0].get(j));
           dxa[p][j] = residual ? v + dyv[j] : v;
         }
 #pragma unroll
@@ -387,7 +441,7 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
           const int q = ring<W>(u, k);
 #pragma unroll
           for (int j = 0; j < VEC; ++j)
-            dxa[q][j] = fmaf(dyv[j], c.w[u].get((j / HSV) * W + k) + swr[k].get(j), dxa[q][j]);
+            dxa[q][j] = fmaf(dyv[j], wr.get((j / HSV) * W + k) + swr[k].get(j), dxa[q][j]);
         }
         if (t < t1) {  // wave-uniform; no loads below
           if constexpr (XF) c.x[u].to_float(xf[p]);
@@ -442,16 +496,18 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
           }
           if constexpr (TDW) {
             // Lane l's piece j goes to slot l*NP + j; slot i*64 + l is then
-            // the wavefront's i-th contiguous 1 KiB.  One wavefront writes
-            // and reads its own slots, in order: no barrier.
+            // the wavefront's i-th contiguous 1 KiB (an exchange within the
+            // wavefront, as own_pieces).
             T e[NWE];
 #pragma unroll
             for (int i = 0; i < NWE; ++i) e[i] = (T)dwv[i];
             u32x4 pc[NP];
             __builtin_memcpy(pc, e, sizeof(pc));
             u32x4* my = dwt[wave];
+            __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int j = 0; j < NP; ++j) my[lane * NP + j] = pc[j];
+            __builtin_amdgcn_wave_barrier();
             const int o = wlo0 + run.wrow(t);
 #pragma unroll
             for (int i = 0; i < NP; ++i) bstore128<true>(my[i * 64 + lane], rdw, o + (i * 64 + lane) * 16);
@@ -518,8 +574,16 @@ struct HwPlan {
 
 template <typename T, int W, int HSV>
 hipError_t launch_fwd_fast(const HwProblem& p, const HwPlan& pl) {
-  hw_fwd_fast<T, W, HSV><<<pl.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.weight, (const T*)p.static_w,
-                                                         (T*)p.y, pl.a);
+  if constexpr (TdwOf<T, W, HSV>::value) {
+    // lanes that own whole heads (one or more), in whole wavefronts
+    if (pl.tdw && pl.a.lph == 1) {
+      hw_fwd_fast<T, W, HSV, true><<<pl.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.weight,
+                                                                  (const T*)p.static_w, (T*)p.y, pl.a);
+      return hipGetLastError();
+    }
+  }
+  hw_fwd_fast<T, W, HSV, false><<<pl.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.weight,
+                                                               (const T*)p.static_w, (T*)p.y, pl.a);
   return hipGetLastError();
 }
 

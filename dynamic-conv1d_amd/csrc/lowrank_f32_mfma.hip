@@ -397,12 +397,16 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
       for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
         for (int i = 0; i < 4; ++i) du[k][jj] = __builtin_amdgcn_mfma_f32_16x16x4f32(zt[i], g[i][jj], du[k][jj], 0, 0, 0);
-      // dz (K = channels): the G tile by row through this wavefront's LDS slot
+      // dz (K = channels): the G tile by row through this wavefront's LDS slot.
+      // The wave barriers keep the compiler from moving a write above a read
+      // of another lane's slot (the hardware keeps a wavefront's LDS order).
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         f32x2 gw = {g[i][0], g[i][1]};
         *reinterpret_cast<f32x2*>(my_g + (4 * q + i) * GP + 2 * n) = gw;
       }
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         const f32x4 ga = *reinterpret_cast<const f32x4*>(my_g + n * GP + 8 * q + 4 * p);

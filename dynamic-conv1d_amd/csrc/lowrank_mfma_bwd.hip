@@ -522,6 +522,10 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
 #pragma unroll
     for (int k = 0; k < W; ++k) {
       // G_k = bf16(dy * x_shift) for rows 4q..4q+3, the lane's NJ channels (fp32 products).
+      // The G tile passes between lanes through the wavefront's LDS slot: the
+      // wave barriers keep the compiler from moving a write above a read of
+      // another lane's bytes (the hardware keeps a wavefront's LDS order).
+      __builtin_amdgcn_wave_barrier();
       float gf[4][NJ];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -551,6 +555,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
         for (int c = 0; c < RC; ++c) du[k][c][j] = Mma16<T>::run(zT[c], g, du[k][c][j]);
       }
       // dz (K = 32 channels): A = G row n (this lane: row = lane % 16), channels 32s+8q..+7.
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
       for (int s2 = 0; s2 < NS; ++s2) {
         const u32x2 lo = lds_read_tr16(my_g + gr_lane + s2 * (8 * 32 + 16));
