@@ -12,6 +12,13 @@
 // run as 128-bit row pieces and repacked; the A operand is the lane's row
 // of z_eff.  Reference: lowrank.py:24-67 (Triton forward kernel).
 //
+// x rows: a lane needs rows 4q-W+1 .. 4q+3.  For 2 <= W <= 4 it loads only
+// its own 4 rows; the W-1 rows above them are own rows of the lane group
+// above (lane - 16), and group 0's are those of group 3 in the tile before,
+// so they come over ds_bpermute (12 per tile at W = 4) instead of 3 more
+// 128-bit loads per lane whose lines the L1 / L2 had to serve again
+// (B4 T4096 D2048 R16: 31.3 -> 29.3 us).
+//
 // Groups: up to kMaxGroups independent problems of one shape share a launch
 // (block index -> group); x may have a row stride xld > D, so the q / k / v
 // inputs are read straight out of a fused [B, T, 3D] projection.
@@ -115,6 +122,12 @@ __global__ __launch_bounds__(256) void lr_fwd_mfma(LrArgs a) {
   const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 2);
   const int lane_off = chv ? ((yh * Tn + 4 * q) * yhd + dl - yh * yhd) * 2 : kOobLane;  // y: the lane's row 4q octet
   const int xlane_off = chv ? (4 * q * a.xld + dl) * 2 : kOobLane;   // the same in x
+  // HX (2 <= W <= 4): a lane loads only its own rows 4q..4q+3; the W-1 rows
+  // above them are the own rows of the lane group above (lane - 16), or for
+  // group 0 those of group 3 in the tile before, passed with ds_bpermute.
+  constexpr bool HX = W >= 2 && W <= 4;
+  const int above = ((lane + 48) & 63) << 2;  // ds_bpermute byte address of lane - 16
+  u32x4 prev[HX ? W - 1 : 1];                 // rows 16-W+1 .. 15 of the tile before (group 3 sends them)
 
   // Tile inputs (rows out of the sequence read as 0).  The loads are
   // unconditional (a tile past the run reads the out-of-range offset
@@ -123,12 +136,24 @@ __global__ __launch_bounds__(256) void lr_fwd_mfma(LrArgs a) {
     const bool live = tile < tile1;
     const int toff = live ? tile * 16 * xrowb : kOobTile;
 #pragma unroll
-    for (int m = 0; m < NR; ++m) xr[m] = bload128(rx, xlane_off + toff + (m - (W - 1)) * xrowb);
+    for (int m = HX ? W - 1 : 0; m < NR; ++m) xr[m] = bload128(rx, xlane_off + toff + (m - (W - 1)) * xrowb);
     zr.load(rz, live ? (tile * 16 + n) * R * 2 : kOobTile, R, q);
   };
-  auto compute_tile = [&](int tile, const u32x4(&xc)[NR], const ZR& zr) {
+  auto compute_tile = [&](int tile, u32x4(&xc)[NR], const ZR& zr) {
     u32x2 zc[RC];
     zr.finish(zc, tile * 16 + n, R, RK, Tn, q);
+    if constexpr (HX) {
+      // row 4q-W+1+m is own row 5-W+m (slot m+4) of the group above
+#pragma unroll
+      for (int m = 0; m < W - 1; ++m) {
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const uint32_t s = q == 3 ? prev[m][h] : xc[m + 4][h];
+          xc[m][h] = (uint32_t)__builtin_amdgcn_ds_bpermute(above, (int)s);
+        }
+        prev[m] = xc[m + 4];
+      }
+    }
     float acc[4][8];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -168,6 +193,12 @@ __global__ __launch_bounds__(256) void lr_fwd_mfma(LrArgs a) {
   // One tile in flight per wavefront: at 114-125 VGPRs the kernel runs 4
   // wavefronts per SIMD, which hide the loads better than a second tile
   // buffer at 3 wavefronts (B4 T4096 D2048 R16: 32.3 -> 31.4 us).
+  if constexpr (HX) {
+    // the run's first tile: rows 16*tile0-W+1 .. 16*tile0-1 (before the sequence: 0), as group 3 would send them
+    const int xcol = chv ? dl * 2 : kOobLane;
+#pragma unroll
+    for (int m = 0; m < W - 1; ++m) prev[m] = bload128(rx, xcol + (tile0 * 16 + m + 1 - W) * xrowb);
+  }
   for (int tile = tile0; tile < tile1; ++tile) {
     u32x4 xr[NR];
     ZR zr;
