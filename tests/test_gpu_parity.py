@@ -118,6 +118,13 @@ HW_EDGE = [
     # one 320-channel head (generic kernels), fp32: dweight's head sum must stay
     # within the elementwise 1e-5 bar (found by the random sweep)
     (3, 200, 320, 1, 8, False, True, torch.float32),
+    # whole wavefronts with lanes that own whole heads: weight rows loaded as
+    # contiguous 1 KiB instructions and handed to the lanes through LDS
+    # (pieces of NP = 2, 3, 4 units), runs of several chunks
+    (2, 300, 512, 512, 3, True, True, torch.float16),   # hs 1, W 3: NP 3
+    (1, 260, 256, 256, 2, False, True, torch.float32),  # hs 1 fp32, W 2: NP 2
+    (2, 181, 512, 256, 4, True, False, torch.bfloat16), # hs 2, W 4: NP 2
+    (1, 333, 1024, 1024, 4, True, True, torch.bfloat16),  # hs 1, W 4: NP 4, two wavefront columns
 ]
 
 
