@@ -211,6 +211,12 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
   constexpr int ES = (int)sizeof(T);
   typedef Raw<T, VEC> XR;
   typedef Raw<T, NWE> WR;
+  // per-lane weight loads: nontemporal when a lane's piece is one unit of whole
+  // heads, so an instruction reads the lanes' pieces as one contiguous run
+  // (head size 4: forward 39.1 -> 37.5 us); several units per lane take the
+  // transposed loads below in whole wavefronts, and heads over several lanes
+  // (a shared piece per head) measured faster with the default policy
+  constexpr int WPOL = (HSV < VEC && WR::NU == 1) ? kNt : 0;
   const int lb = xcd_remap(blockIdx.x, a.nblk);
   const int vg = lb % a.nvg, sgp = lb / a.nvg;
   const int wave = wave_id(), lane = threadIdx.x & 63;
@@ -260,7 +266,7 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
 #pragma unroll
         for (int i = 0; i < NPW; ++i) wc[u].u[i] = bload128<kNt>(rw, wlo0 + run.wrow(t, t < t1) + (i * 64 + lane) * 16);
       } else {
-        bload_raw(wc[u], rw, wlo + run.wrow(t, t < t1));
+        bload_raw<WPOL>(wc[u], rw, wlo + run.wrow(t, t < t1));
       }
     }
   };
@@ -337,6 +343,12 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
   constexpr int NPW = VEC * ES / 4;  // 32-bit words of a lane's row piece
   typedef Raw<T, VEC> XR;
   typedef Raw<T, NWE> WR;
+  // per-lane weight loads: nontemporal when a lane's piece is one unit of whole
+  // heads, so an instruction reads the lanes' pieces as one contiguous run
+  // (head size 4: forward 39.1 -> 37.5 us); several units per lane take the
+  // transposed loads below in whole wavefronts, and heads over several lanes
+  // (a shared piece per head) measured faster with the default policy
+  constexpr int WPOL = (HSV < VEC && WR::NU == 1) ? kNt : 0;
   const int lb = xcd_remap(blockIdx.x, a.nblk);
   const int vg = lb % a.nvg, sgp = lb / a.nvg;
   const int wave = wave_id(), lane = threadIdx.x & 63;
@@ -412,7 +424,7 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
 #pragma unroll
           for (int i = 0; i < NP; ++i) c.w[u].u[i] = bload128<kNt>(rw, wlo0 + run.wrow(t, t < tend) + (i * 64 + lane) * 16);
         } else {
-          bload_raw(c.w[u], rw, wlo + run.wrow(t, t < tend));
+          bload_raw<WPOL>(c.w[u], rw, wlo + run.wrow(t, t < tend));
         }
         bload_raw<kNt>(c.x[u], rx, xlo + run.xrow(t, t < t1));
       }
