@@ -303,6 +303,40 @@ def test_baseline_configs(cfg):
             assert_ns(g_k[3], dsw, dtype, "dstatic_w", elementwise=False)
 
 
+# ---------------------------------------------------------- long sequence
+# One sequence of x spans more than 512 MiB (131172 rows of 2048 bf16): the
+# headwise kernels cap each run's buffer range at 512 MiB, and the lowrank
+# MFMA kernels (whose offsets cover one sequence) give way to the generic ones.
+# Local outputs are checked on row windows, including the rows around 512 MiB.
+@pytest.mark.parametrize("kind", ["hw32", "lr16"])
+def test_long_sequence(kind):
+    dtype = torch.bfloat16
+    Bn, Tn, Dn, W = 1, 131172, 2048, 4
+    g = gen(11)
+    x = randn(g, Bn, Tn, Dn)
+    dy = randn(g, Bn, Tn, Dn)
+    sw = uniform(g, W, Dn, lo=-1 / math.sqrt(W), hi=1 / math.sqrt(W))
+    if kind == "hw32":
+        src, fn, ref = [x, randn(g, Bn, Tn, Dn // 32, W, scale=1 / math.sqrt(W)), sw], hw, hw_ref
+    else:
+        R = 15
+        src, fn, ref = [x, randn(g, Bn, Tn, R), randn(g, R, W * Dn, scale=1 / math.sqrt(16 * W)), sw], lr, lr_ref
+    y_k, g_k = run_fwd_bwd(fn, [_to(t, dtype) for t in src], _to(dy, dtype), True)
+    q = [t.to(dtype).float() for t in src]
+    dyq = dy.to(dtype).float()
+    edge = (1 << 29) // (Dn * 2)  # first row past 512 MiB of x
+    for t0, t1 in _windows(Tn) + [(edge - 40, edge + 24)]:
+        a, e = max(0, t0 - W + 1), min(Tn, t1 + W - 1)
+        win = [t[:, a:e] if t.dim() >= 3 else t for t in q]
+        if kind == "lr16":
+            win[2] = q[2]
+        y_w, g_w = run_fwd_bwd(ref, win, dyq[:, a:e], True)
+        sl = slice(t0 - a, t1 - a)
+        assert_ns(y_k[:, t0:t1], y_w[:, sl], dtype, f"y[{t0}:{t1}]")
+        assert_ns(g_k[0][:, t0:t1], g_w[0][:, sl], dtype, f"dx[{t0}:{t1}]")
+        assert_ns(g_k[1][:, t0:t1], g_w[1][:, sl], dtype, f"d1[{t0}:{t1}]", elementwise=kind == "hw32")
+
+
 # ------------------------------------------------------------ determinism
 @pytest.mark.parametrize("kind", ["hw1", "hw32", "lr16s"])
 def test_deterministic(kind):
