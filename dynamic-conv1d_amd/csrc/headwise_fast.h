@@ -233,7 +233,8 @@ __global__ __launch_bounds__(256) void hw_fwd_fast(const T* __restrict__ x, cons
   const rsrc_t ry = make_rsrc(y + run.xrow0, run.xrec);
   const rsrc_t rw = make_rsrc(wt + run.wrow0, run.wrec);
   const int64_t D = a.D;
-  // TWL: transposed weight loads (TdwOf; the host guarantees whole wavefronts)
+  // TWL: transposed weight loads (TdwOf; the host takes them only in whole
+  // wavefronts whose lanes own whole heads)
   constexpr int NPW = TWL ? TdwOf<T, W, HSV>::NP : 1;
   __shared__ u32x4 wlt[4][TWL ? NPW * 64 : 1];
   const int wlo0 = (((vc - lane) * VEC) >> a.hs_shift) * W * ES;  // weight byte offset of the wavefront's lane 0
