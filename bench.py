@@ -208,6 +208,9 @@ def abi_sets(c, torch, dev):
             d["dUs"] = [torch.empty_like(u) for u in d["Us"]]
             d["dsws"] = [torch.empty_like(s) for s in d["sws"]] if c["static"] else None
             d["nws"] = lib.dc_lowrank_bwd_grouped_ws_bytes(G, B, T, D, R, W, dt, int(c["static"]))
+            # the forward's padded z copy for the backward, as the autograd Function keeps it
+            nz = lib.dc_lowrank_zeff_bytes(B, T, D, R, W, dt, int(c["static"]))
+            d["zeffs"] = [torch.empty(nz, dtype=torch.uint8, device=dev) for _ in range(G)] if nz > 0 else None
             d["ws"] = torch.empty(max(d["nws"], 1), dtype=torch.uint8, device=dev)
             sets.append(d)
         return sets
@@ -224,6 +227,8 @@ def abi_sets(c, torch, dev):
             d["U"] = (torch.randn(c["R"], W * D, device=dev) / math.sqrt(rk * W)).to(bf)
             d["dz"], d["dU"] = torch.empty_like(d["z"]), torch.empty_like(d["U"])
             nws = lib.dc_lowrank_bwd_ws_bytes(B, T, D, c["R"], W, dt, int(c["static"]))
+            nz = lib.dc_lowrank_zeff_bytes(B, T, D, c["R"], W, dt, int(c["static"]))
+            d["zeff"] = torch.empty(nz, dtype=torch.uint8, device=dev) if nz > 0 else None
         d["y"], d["dx"] = torch.empty_like(d["x"]), torch.empty_like(d["x"])
         d["dsw"] = torch.empty_like(d["sw"]) if c["static"] else None
         d["nws"] = nws
@@ -249,12 +254,14 @@ def abi_launchers(c, sets, torch):
         def fwd(i):
             d = sets[i]
             _capi.check(lib.dc_lowrank_fwd_grouped(G, p(d["x"]), G * D, pa(d["zs"]), pa(d["Us"]), pa(d["sws"]),
-                                                   pa(d["ys"]), 0, B, T, D, R, W, dt, res, st), "grouped fwd")
+                                                   pa(d["ys"]), pa(d["zeffs"]), 0, B, T, D, R, W, dt, res, st),
+                        "grouped fwd")
 
         def bwd(i):
             d = sets[i]
             _capi.check(lib.dc_lowrank_bwd_grouped(G, p(d["x"]), G * D, pa(d["zs"]), pa(d["Us"]), pa(d["sws"]),
-                                                   pa(d["dys"]), 0, p(d["dx"]), G * D, pa(d["dzs"]), pa(d["dUs"]),
+                                                   pa(d["zeffs"]), pa(d["dys"]), 0, p(d["dx"]), G * D, pa(d["dzs"]),
+                                                   pa(d["dUs"]),
                                                    pa(d["dsws"]), p(d["ws"]), d["nws"], B, T, D, R, W, dt, res, st),
                         "grouped bwd")
         return fwd, bwd
@@ -275,12 +282,13 @@ def abi_launchers(c, sets, torch):
 
         def fwd(i):
             d = sets[i]
-            _capi.check(lib.dc_lowrank_fwd(p(d["x"]), p(d["z"]), p(d["U"]), p(d["sw"]), p(d["y"]),
+            _capi.check(lib.dc_lowrank_fwd(p(d["x"]), p(d["z"]), p(d["U"]), p(d["sw"]), p(d["y"]), p(d["zeff"]),
                                            B, T, D, R, W, dt, res, st), "fwd")
 
         def bwd(i):
             d = sets[i]
-            _capi.check(lib.dc_lowrank_bwd(p(d["x"]), p(d["z"]), p(d["U"]), p(d["sw"]), p(d["dy"]), p(d["dx"]),
+            _capi.check(lib.dc_lowrank_bwd(p(d["x"]), p(d["z"]), p(d["U"]), p(d["sw"]), p(d["zeff"]), p(d["dy"]),
+                                           p(d["dx"]),
                                            p(d["dz"]), p(d["dU"]), p(d["dsw"]), p(d["ws"]), d["nws"],
                                            B, T, D, R, W, dt, res, st), "bwd")
     return fwd, bwd

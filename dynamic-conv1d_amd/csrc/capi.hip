@@ -136,18 +136,38 @@ int dc_headwise_bwd(const void* x, const void* weight, const void* static_w, con
   return launch_status(dc::hw_bwd(p));
 }
 
-int dc_lowrank_fwd(const void* x, const void* z, const void* U, const void* static_w, void* y, int64_t B,
-                   int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int residual, void* stream) {
+int64_t dc_lowrank_zeff_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int has_static) {
+  int s = check_lowrank(B, T, D, R, W, dtype, has_static != 0);
+  if (s != DC_OK) return s;
+  static const char kAligned[16] __attribute__((aligned(256))) = {0};
+  dc::LrProblem p{};
+  p.x = p.z = p.U = p.dy = kAligned;
+  p.y = p.dx = p.dz = p.dU = (void*)kAligned;
+  p.static_w = has_static ? kAligned : nullptr;
+  p.dstatic_w = has_static ? (void*)kAligned : nullptr;
+  p.B = B; p.T = T; p.D = D; p.R = R; p.W = W; p.dtype = dtype;
+  return dc::lr_zeff_bytes(p);
+}
+
+// The z_eff buffer a call uses: the caller's when the shape has one, else none.
+static void* zeff_of(const void* z_eff, int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype,
+                     bool has_static) {
+  return z_eff && dc_lowrank_zeff_bytes(B, T, D, R, W, dtype, has_static) > 0 ? const_cast<void*>(z_eff) : nullptr;
+}
+
+int dc_lowrank_fwd(const void* x, const void* z, const void* U, const void* static_w, void* y, void* z_eff,
+                   int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int residual, void* stream) {
   int s = check_lowrank(B, T, D, R, W, dtype, static_w != nullptr);
   if (s != DC_OK) return s;
   if (!x || !z || !U || !y) return DC_ERR_NULL;
   const int es = dc::dtype_size(dtype);
   if (!aligned_to(x, es) || !aligned_to(z, es) || !aligned_to(U, es) || !aligned_to(static_w, es) ||
-      !aligned_to(y, es))
+      !aligned_to(y, es) || !aligned_to(z_eff, 16))
     return DC_ERR_ALIGN;
   if ((s = device_status()) != DC_OK) return s;
   dc::LrProblem p{};
   p.x = x; p.z = z; p.U = U; p.static_w = static_w; p.y = y;
+  p.zeff = zeff_of(z_eff, B, T, D, R, W, dtype, static_w != nullptr);
   p.B = B; p.T = T; p.D = D; p.R = R; p.W = W;
   p.dtype = dtype; p.residual = residual ? 1 : 0; p.stream = (hipStream_t)stream;
   return launch_status(dc::lr_fwd(&p, 1));
@@ -170,9 +190,9 @@ int64_t dc_lowrank_bwd_ws_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int6
   return fast > gen ? fast : gen;
 }
 
-int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* static_w, const void* dy, void* dx,
-                   void* dz, void* dU, void* dstatic_w, void* workspace, int64_t ws_bytes, int64_t B, int64_t T,
-                   int64_t D, int64_t R, int64_t W, int dtype, int residual, void* stream) {
+int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* static_w, const void* z_eff,
+                   const void* dy, void* dx, void* dz, void* dU, void* dstatic_w, void* workspace, int64_t ws_bytes,
+                   int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int residual, void* stream) {
   int s = check_lowrank(B, T, D, R, W, dtype, static_w != nullptr);
   if (s != DC_OK) return s;
   if (!x || !z || !U || !dy || !dx || !dz || !dU) return DC_ERR_NULL;
@@ -180,7 +200,7 @@ int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* stat
   const int es = dc::dtype_size(dtype);
   if (!aligned_to(x, es) || !aligned_to(z, es) || !aligned_to(U, es) || !aligned_to(static_w, es) ||
       !aligned_to(dy, es) || !aligned_to(dx, es) || !aligned_to(dz, es) || !aligned_to(dU, es) ||
-      !aligned_to(dstatic_w, es))
+      !aligned_to(dstatic_w, es) || !aligned_to(z_eff, 16))
     return DC_ERR_ALIGN;
   const int64_t need = dc_lowrank_bwd_ws_bytes(B, T, D, R, W, dtype, static_w != nullptr);
   if (need < 0) return (int)need;
@@ -189,6 +209,7 @@ int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* stat
   dc::LrProblem p{};
   p.x = x; p.z = z; p.U = U; p.static_w = static_w; p.dy = dy;
   p.dx = dx; p.dz = dz; p.dU = dU; p.dstatic_w = dstatic_w; p.ws = (float*)workspace;
+  p.zeff = zeff_of(z_eff, B, T, D, R, W, dtype, static_w != nullptr);
   p.B = B; p.T = T; p.D = D; p.R = R; p.W = W;
   p.dtype = dtype; p.residual = residual ? 1 : 0; p.stream = (hipStream_t)stream;
   return launch_status(dc::lr_bwd(&p, 1));
@@ -203,8 +224,9 @@ int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* stat
 static bool head_dim_ok(int64_t hd, int64_t D) { return hd == 0 || (hd > 0 && hd <= D && D % hd == 0); }
 
 int dc_lowrank_fwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z, const void* const* U,
-                           const void* const* static_w, void* const* y, int64_t y_hd, int64_t B, int64_t T,
-                           int64_t D, int64_t R, int64_t W, int dtype, int residual, void* stream) {
+                           const void* const* static_w, void* const* y, void* const* z_eff, int64_t y_hd,
+                           int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int residual,
+                           void* stream) {
   if (G < 1 || G > DC_MAX_GROUPS) return DC_ERR_UNSUPPORTED;
   int s = check_lowrank(B, T, D, R, W, dtype, static_w != nullptr);
   if (s != DC_OK) return s;
@@ -215,11 +237,13 @@ int dc_lowrank_fwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* c
   dc::LrProblem p[DC_MAX_GROUPS] = {};
   for (int64_t g = 0; g < G; ++g) {
     const void* sw = static_w ? static_w[g] : nullptr;
-    if (!z[g] || !U[g] || !y[g] || (static_w && !sw)) return DC_ERR_NULL;
-    if (!aligned_to(z[g], es) || !aligned_to(U[g], es) || !aligned_to(sw, es) || !aligned_to(y[g], es))
+    if (!z[g] || !U[g] || !y[g] || (static_w && !sw) || (z_eff && !z_eff[g])) return DC_ERR_NULL;
+    if (!aligned_to(z[g], es) || !aligned_to(U[g], es) || !aligned_to(sw, es) || !aligned_to(y[g], es) ||
+        (z_eff && !aligned_to(z_eff[g], 16)))
       return DC_ERR_ALIGN;
     dc::LrProblem& q = p[g];
     q.x = (const char*)x + g * D * es; q.z = z[g]; q.U = U[g]; q.static_w = sw; q.y = y[g];
+    q.zeff = z_eff ? zeff_of(z_eff[g], B, T, D, R, W, dtype, static_w != nullptr) : nullptr;
     q.B = B; q.T = T; q.D = D; q.R = R; q.W = W; q.x_ld = x_ld; q.y_hd = y_hd;
     q.dtype = dtype; q.residual = residual ? 1 : 0; q.stream = (hipStream_t)stream;
   }
@@ -241,7 +265,8 @@ int64_t dc_lowrank_bwd_grouped_ws_bytes(int64_t G, int64_t B, int64_t T, int64_t
 }
 
 int dc_lowrank_bwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z, const void* const* U,
-                           const void* const* static_w, const void* const* dy, int64_t dy_hd, void* dx,
+                           const void* const* static_w, const void* const* z_eff, const void* const* dy,
+                           int64_t dy_hd, void* dx,
                            int64_t dx_ld, void* const* dz, void* const* dU, void* const* dstatic_w,
                            void* workspace, int64_t ws_bytes, int64_t B, int64_t T, int64_t D, int64_t R,
                            int64_t W, int dtype, int residual, void* stream) {
@@ -262,13 +287,16 @@ int dc_lowrank_bwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* c
   for (int64_t g = 0; g < G; ++g) {
     const void* sw = static_w ? static_w[g] : nullptr;
     void* dsw = dstatic_w ? dstatic_w[g] : nullptr;
-    if (!z[g] || !U[g] || !dy[g] || !dz[g] || !dU[g] || (static_w && (!sw || !dsw))) return DC_ERR_NULL;
+    if (!z[g] || !U[g] || !dy[g] || !dz[g] || !dU[g] || (static_w && (!sw || !dsw)) || (z_eff && !z_eff[g]))
+      return DC_ERR_NULL;
     if (!aligned_to(z[g], es) || !aligned_to(U[g], es) || !aligned_to(sw, es) || !aligned_to(dy[g], es) ||
-        !aligned_to(dz[g], es) || !aligned_to(dU[g], es) || !aligned_to(dsw, es))
+        !aligned_to(dz[g], es) || !aligned_to(dU[g], es) || !aligned_to(dsw, es) ||
+        (z_eff && !aligned_to(z_eff[g], 16)))
       return DC_ERR_ALIGN;
     dc::LrProblem& q = p[g];
     q.x = (const char*)x + g * D * es; q.z = z[g]; q.U = U[g]; q.static_w = sw; q.dy = dy[g];
     q.dx = (char*)dx + g * D * es; q.dz = dz[g]; q.dU = dU[g]; q.dstatic_w = dsw;
+    q.zeff = z_eff ? zeff_of(z_eff[g], B, T, D, R, W, dtype, static_w != nullptr) : nullptr;
     q.ws = share > 0 ? (float*)((char*)workspace + g * share) : nullptr;
     q.B = B; q.T = T; q.D = D; q.R = R; q.W = W; q.x_ld = x_ld; q.dx_ld = dx_ld; q.y_hd = dy_hd;
     q.dtype = dtype; q.residual = residual ? 1 : 0; q.stream = (hipStream_t)stream;

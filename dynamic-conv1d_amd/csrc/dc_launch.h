@@ -48,6 +48,9 @@ struct LrProblem {
   void* dU;
   void* dstatic_w;
   float* ws;
+  // Padded z_eff [B*T, RP] of z's type (RP = lr_bwd_zrow), or null: the forward
+  // writes it, the backward reads it instead of building it (lowrank only).
+  void* zeff;
   int64_t B, T, D, R, W;  // R = dynamic rank (z.shape[-1])
   int64_t x_ld;           // row stride of x in elements (0: D, contiguous)
   int64_t dx_ld;          // row stride of dx in elements (0: D, contiguous)
@@ -71,6 +74,8 @@ constexpr int kMaxGroups = 4;
 
 bool lr_mfma_ok(const LrProblem& p, bool bwd);
 int64_t lr_bwd_ws_bytes(const LrProblem& p);
+// Bytes of the padded z_eff the MFMA backward builds for p (0: it reads z itself).
+int64_t lr_zeff_bytes(const LrProblem& p);
 hipError_t lr_fwd(const LrProblem* p, int G);
 hipError_t lr_bwd(const LrProblem* p, int G);
 

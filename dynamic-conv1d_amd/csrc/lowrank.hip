@@ -219,6 +219,16 @@ bool lr_mfma_ok(const LrProblem& p, bool bwd) {
   return aligned_to8(p.x) && aligned_to8(p.dy) && aligned_to8(p.dx) && aligned_to16(p.U) && aligned_to16(p.static_w);
 }
 
+int64_t lr_zeff_bytes(const LrProblem& p) {
+  if (!lr_mfma_ok(p, true)) return 0;
+  const bool has_static = p.static_w != nullptr;
+  const int64_t rc = (p.R + (has_static ? 1 : 0) + 15) / 16;
+  // the backward reads z itself when its rows are what the kernel loads: R % 4
+  // == 0 (8-byte loads) or, for two rank chunks, exactly 32 dynamic ranks
+  const bool pad = rc == 2 ? !(p.R == 32 && !has_static) : p.R % 4 != 0;
+  return pad ? p.B * p.T * lr_bwd_zrow(p.R, has_static) * 2 : 0;
+}
+
 int64_t lr_bwd_ws_bytes(const LrProblem& p) {
   if (lr_mfma_ok(p, true)) return lr_mfma_ws_bytes(p);
   if (lr_f32m_bwd_ok(p) || lr_f32_ok(p)) {
@@ -244,7 +254,11 @@ bool all_mfma_ok(const LrProblem* p, int G, bool bwd) {
 // launch sequence.
 hipError_t lr_fwd(const LrProblem* p, int G) {
   if (G < 1 || G > kMaxGroups) return hipErrorInvalidValue;
-  if (all_mfma_ok(p, G, false)) return lr_mfma_fwd(p, G);
+  if (all_mfma_ok(p, G, false)) return lr_mfma_fwd(p, G);  // writes z_eff when asked
+  if (p[0].zeff) {
+    hipError_t e = lr_zeff_fill(p, G);
+    if (e != hipSuccess) return e;
+  }
   for (int g = 0; g < G; ++g) {
     hipError_t e;
     if (lr_f32m_fwd_ok(p[g])) {

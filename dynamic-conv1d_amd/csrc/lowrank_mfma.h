@@ -178,6 +178,9 @@ __device__ __forceinline__ F pick(const S (&a)[kMaxGroups], int g, F S::*f) {
 
 // Host entry points of the two MFMA translation units.
 hipError_t lr_mfma_fwd(const LrProblem* p, int G);
+// Writes each group's z_eff (p[g].zeff, RP = lr_bwd_zrow ranks per row) from z:
+// the forward's copy for the backward when the MFMA forward does not write it.
+hipError_t lr_zeff_fill(const LrProblem* p, int G);
 int64_t lr_mfma_ws_bytes(const LrProblem& p);
 hipError_t lr_mfma_bwd(const LrProblem* p, int G);
 // fp32 on matrix cores (lowrank_f32_mfma.hip), one problem per launch sequence.

@@ -779,6 +779,24 @@ __global__ __launch_bounds__(256) void lr_zpad(ZpadArgs a) {
   *reinterpret_cast<u32x2*>(zp + e) = u32x2{v[0] | (v[1] << 16), v[2] | (v[3] << 16)};
 }
 
+// lr_zpad over G problems: z_eff of group g into dst[g].
+template <typename T>
+hipError_t launch_zpad(const LrProblem* p, int G, void* const* dst) {
+  ZpadArgs za;
+  const int64_t RP = zpad_ranks(p[0]);
+  za.n = p[0].B * p[0].T * RP / 4;
+  za.R = (int)p[0].R;
+  za.RP = (int)RP;
+  za.stat = p[0].static_w != nullptr;
+  za.one = Mma16<T>::kOne;
+  for (int g = 0; g < kMaxGroups; ++g) {
+    za.z[g] = (const uint16_t*)p[g < G ? g : 0].z;
+    za.zp[g] = (uint16_t*)dst[g < G ? g : 0];
+  }
+  lr_zpad<<<dim3((unsigned)((za.n + 255) / 256), G), 256, 0, p[0].stream>>>(za);
+  return hipGetLastError();
+}
+
 constexpr int kBwdTargetWaves = 2048;
 
 // Workspace: [dz partials: ncg x BT x R fp32][dU partials: npair x RK x W*D fp32]
@@ -820,21 +838,15 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
   }
   hipError_t e;
   if (!zvec) {
-    ZpadArgs za;
-    const int64_t RP = zpad_ranks(p[0]);
-    za.n = a.BT * RP / 4;
-    za.R = (int)p[0].R;
-    za.RP = (int)RP;
-    za.stat = p[0].static_w != nullptr;
-    za.one = Mma16<T>::kOne;
-    for (int g = 0; g < kMaxGroups; ++g) {
-      za.z[g] = (const uint16_t*)p[g < G ? g : 0].z;
-      za.zp[g] = (uint16_t*)((char*)p[g < G ? g : 0].ws + w.zp_off);
-    }
-    for (int g = 0; g < G; ++g) a.grp[g].z = za.zp[g];
-    a.zld = a.zr = a.zrk = (int)RP;
-    lr_zpad<<<dim3((unsigned)((za.n + 255) / 256), G), 256, 0, p[0].stream>>>(za);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    // padded z_eff rows: the forward's copy when the caller kept it, else
+    // written into the workspace first
+    bool saved = true;
+    for (int g = 0; g < G; ++g) saved = saved && p[g].zeff != nullptr;
+    void* zp[kMaxGroups];
+    for (int g = 0; g < G; ++g) zp[g] = saved ? p[g].zeff : (char*)p[g].ws + w.zp_off;
+    if (!saved && (e = launch_zpad<T>(p, G, zp)) != hipSuccess) return e;
+    for (int g = 0; g < G; ++g) a.grp[g].z = zp[g];
+    a.zld = a.zr = a.zrk = (int)zpad_ranks(p[0]);
   }
   lr_bwd_mfma<T, W, RC, NRW, CPW><<<a.nblk, NT, 0, p[0].stream>>>(a);
   e = hipGetLastError();
@@ -871,6 +883,12 @@ hipError_t dispatch_bwd(const LrProblem* pp, int G) {
 }  // namespace
 
 int64_t lr_mfma_ws_bytes(const LrProblem& p) { return bwd_ws(p, make_bwd_args(p, kBwdTargetWaves)).total; }
+
+hipError_t lr_zeff_fill(const LrProblem* p, int G) {
+  void* dst[kMaxGroups];
+  for (int g = 0; g < G; ++g) dst[g] = p[g].zeff;
+  return p[0].dtype == kBF16 ? launch_zpad<bf16>(p, G, dst) : launch_zpad<fp16>(p, G, dst);
+}
 
 hipError_t lr_mfma_bwd(const LrProblem* p, int G) {
   return p[0].dtype == kBF16 ? dispatch_bwd<bf16>(p, G) : dispatch_bwd<fp16>(p, G);

@@ -32,6 +32,7 @@ struct LrFwdGroup {
   const void* U;
   const void* sw;
   void* y;
+  void* zeff;     // padded z_eff for the backward (rows of zrp ranks), when zrp > 0
 };
 
 struct LrArgs {
@@ -51,6 +52,7 @@ struct LrArgs {
   int xld;         // row stride of x (elements)
   int zvec;        // R % 4 == 0 and z 8-byte aligned: 8-byte z loads (host dispatch)
   int yhd;         // y layout: D ([B, T, D]) or the head dim of [B, D/yhd, T, yhd] (yhd % 8 == 0)
+  int zrp;         // > 0: the 128-channel chunk 0 wavefronts write z_eff rows of zrp ranks
   LrFwdGroup grp[kMaxGroups];
 };
 
@@ -82,8 +84,14 @@ __device__ __forceinline__ void stage_u(u32x2* __restrict__ lds, const uint16_t*
   }
 }
 
-template <typename T, int W, int RC, bool ZV>
-__global__ __launch_bounds__(256) void lr_fwd_mfma(LrArgs a) {
+// ZE: also write the padded z_eff for the backward (a separate instantiation,
+// so calls without it run the kernel unchanged).  With it the compiler is held
+// to 4 wavefronts per SIMD (<= 128 VGPRs) where the operands allow it: left
+// alone it took 138 VGPRs at W 4 with two rank chunks, and the launches of 4096
+// wavefronts (B2 T8192 D4096) need all four resident (forward 61.5 -> 68.9 us).
+template <typename T, int W, int RC, bool ZV, bool ZE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZE && W <= 4 && RC <= 2 ? 4 : 1, 8)))
+void lr_fwd_mfma(LrArgs a) {
   constexpr int NR = W + 3;  // x rows 4q-W+1 .. 4q+3 of a lane
   typedef ZRaw<T, RC, ZV> ZR;
   __shared__ u32x2 ub[W * RC * 8 * 64];
@@ -120,6 +128,10 @@ __global__ __launch_bounds__(256) void lr_fwd_mfma(LrArgs a) {
   const rsrc_t rx = make_rsrc(x + row0 * a.xld, (int64_t)Tn * xrowb);
   const rsrc_t ry = make_rsrc(y + row0 * D, (int64_t)Tn * D * 2);
   const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 2);
+  const int zrp = ZE ? a.zrp : 0;
+  const bool zrow_mine = ZE && n % a.nch == chunk;  // this wavefront writes row n of each tile's z_eff
+  const rsrc_t rze = make_rsrc(ZE ? (const uint16_t*)pick(a.grp, g, &LrFwdGroup::zeff) + row0 * zrp : z,
+                               ZE ? (int64_t)Tn * zrp * 2 : 0);
   const int lane_off = chv ? ((yh * Tn + 4 * q) * yhd + dl - yh * yhd) * 2 : kOobLane;  // y: the lane's row 4q octet
   const int xlane_off = chv ? (4 * q * a.xld + dl) * 2 : kOobLane;   // the same in x
   // HX (2 <= W <= 4): a lane loads only its own rows 4q..4q+3; the W-1 rows
@@ -142,6 +154,18 @@ __global__ __launch_bounds__(256) void lr_fwd_mfma(LrArgs a) {
   auto compute_tile = [&](int tile, u32x4(&xc)[NR], const ZR& zr) {
     u32x2 zc[RC];
     zr.finish(zc, tile * 16 + n, R, RK, Tn, q);
+    if constexpr (ZE) {
+      // z_eff for the backward: lane (q, n) holds ranks 16c+4q .. +3 of row n,
+      // static rank included (finish), as the backward's padded rows need them.
+      // Row n of a tile is written by the chunk n % nch, so every wavefront
+      // takes an equal share (one writer per row).
+#pragma unroll
+      for (int c = 0; c < RC; ++c) {
+        const int r0 = 16 * c + 4 * q;
+        bstore64<false>(zc[c], rze,
+                        zrow_mine && tile * 16 + n < Tn && r0 < zrp ? ((tile * 16 + n) * zrp + r0) * 2 : kOobTile);
+      }
+    }
     if constexpr (HX) {
       // row 4q-W+1+m is own row 5-W+m (slot m+4) of the group above
 #pragma unroll
@@ -248,14 +272,22 @@ hipError_t launch_fwd(const LrProblem* p, int G) {
   a.nblk = G * a.nblk1;
   a.xld = (int)p[0].xld();
   a.yhd = (int)p[0].yhd();
+  a.zrp = p[0].zeff ? (int)lr_bwd_zrow(p[0].R, p[0].static_w != nullptr) : 0;
   for (int g = 0; g < G; ++g) {
-    a.grp[g] = LrFwdGroup{p[g].x, p[g].z, p[g].U, p[g].static_w, p[g].y};
+    a.grp[g] = LrFwdGroup{p[g].x, p[g].z, p[g].U, p[g].static_w, p[g].y, p[g].zeff};
     a.zvec = a.zvec && aligned_to(p[g].z, 8);
   }
-  if (a.zvec)
-    lr_fwd_mfma<T, W, RC, true><<<a.nblk, 256, 0, p[0].stream>>>(a);
-  else
-    lr_fwd_mfma<T, W, RC, false><<<a.nblk, 256, 0, p[0].stream>>>(a);
+  if (a.zrp > 0) {
+    if (a.zvec)
+      lr_fwd_mfma<T, W, RC, true, true><<<a.nblk, 256, 0, p[0].stream>>>(a);
+    else
+      lr_fwd_mfma<T, W, RC, false, true><<<a.nblk, 256, 0, p[0].stream>>>(a);
+  } else {
+    if (a.zvec)
+      lr_fwd_mfma<T, W, RC, true, false><<<a.nblk, 256, 0, p[0].stream>>>(a);
+    else
+      lr_fwd_mfma<T, W, RC, false, false><<<a.nblk, 256, 0, p[0].stream>>>(a);
+  }
   return hipGetLastError();
 }
 

@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdynconv.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
@@ -29,12 +29,13 @@ SIGNATURES = {
     "dc_headwise_fwd": (_c_int, [_c_vp] * 4 + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
     "dc_headwise_bwd_ws_bytes": (_c_i64, [_c_i64] * 5 + [_c_int, _c_int]),
     "dc_headwise_bwd": (_c_int, [_c_vp] * 8 + [_c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
-    "dc_lowrank_fwd": (_c_int, [_c_vp] * 5 + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
+    "dc_lowrank_zeff_bytes": (_c_i64, [_c_i64] * 5 + [_c_int, _c_int]),
+    "dc_lowrank_fwd": (_c_int, [_c_vp] * 6 + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
     "dc_lowrank_bwd_ws_bytes": (_c_i64, [_c_i64] * 5 + [_c_int, _c_int]),
-    "dc_lowrank_bwd": (_c_int, [_c_vp] * 10 + [_c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
-    "dc_lowrank_fwd_grouped": (_c_int, [_c_i64, _c_vp, _c_i64] + [_c_pp] * 4 + [_c_i64] * 6 + [_c_int, _c_int, _c_vp]),
+    "dc_lowrank_bwd": (_c_int, [_c_vp] * 11 + [_c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
+    "dc_lowrank_fwd_grouped": (_c_int, [_c_i64, _c_vp, _c_i64] + [_c_pp] * 5 + [_c_i64] * 6 + [_c_int, _c_int, _c_vp]),
     "dc_lowrank_bwd_grouped_ws_bytes": (_c_i64, [_c_i64] * 6 + [_c_int, _c_int]),
-    "dc_lowrank_bwd_grouped": (_c_int, [_c_i64, _c_vp, _c_i64] + [_c_pp] * 4 + [_c_i64, _c_vp, _c_i64] + [_c_pp] * 3
+    "dc_lowrank_bwd_grouped": (_c_int, [_c_i64, _c_vp, _c_i64] + [_c_pp] * 5 + [_c_i64, _c_vp, _c_i64] + [_c_pp] * 3
                                + [_c_vp, _c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
 }
 

@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define DC_ABI_VERSION 3
+#define DC_ABI_VERSION 4
 
 /* Largest convolution width and (kernel) rank accepted. */
 #define DC_MAX_W 8
@@ -102,11 +102,23 @@ int dc_headwise_bwd(const void* x, const void* weight, const void* static_w, con
                     int64_t B, int64_t T, int64_t D, int64_t H, int64_t W,
                     int dtype, int residual, void* stream);
 
+/* Bytes of the padded z_eff (z with the static column and zero ranks, rows of
+ * 4*k or 32 ranks) that dc_lowrank_bwd builds before its main kernel for this
+ * shape, or 0 when it reads z itself, or a negative dc_status.  A caller that
+ * keeps such a buffer from the forward to the backward saves that pass: the
+ * forward writes it as a by-product (z_eff of dc_lowrank_fwd) and the backward
+ * reads it (z_eff of dc_lowrank_bwd).  No counterpart in the reference, whose
+ * forward saves the padded z and concatenated U (lowrank.py:223-225, 244). */
+int64_t dc_lowrank_zeff_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
+                              int dtype, int has_static);
+
 /* y = lowrank dynamic convolution; the per-token weights z @ U (+ static_w as an
  * implicit extra rank with z == 1) are formed on chip and never written out.
- * Replaces lowrank.py:214-249.  R is the dynamic rank (z.shape[-1]). */
+ * Replaces lowrank.py:214-249.  R is the dynamic rank (z.shape[-1]).  z_eff is
+ * NULL or a 16-byte aligned buffer of dc_lowrank_zeff_bytes bytes, which the
+ * forward then fills for the backward (nothing happens when that size is 0). */
 int dc_lowrank_fwd(const void* x, const void* z, const void* U, const void* static_w, void* y,
-                   int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
+                   void* z_eff, int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
                    int dtype, int residual, void* stream);
 
 /* Workspace bytes needed by dc_lowrank_bwd, or a negative dc_status. */
@@ -114,9 +126,10 @@ int64_t dc_lowrank_bwd_ws_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int6
                                 int dtype, int has_static);
 
 /* dx, dz, dU and (when static_w != NULL) dstatic_w from dy, in one pass over
- * x and dy.  Replaces lowrank.py:251-299. */
+ * x and dy.  Replaces lowrank.py:251-299.  z_eff is NULL or the buffer that
+ * dc_lowrank_fwd filled for the same z and static_w presence. */
 int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* static_w,
-                   const void* dy, void* dx, void* dz, void* dU, void* dstatic_w,
+                   const void* z_eff, const void* dy, void* dx, void* dz, void* dU, void* dstatic_w,
                    void* workspace, int64_t ws_bytes,
                    int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
                    int dtype, int residual, void* stream);
@@ -133,11 +146,12 @@ int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* stat
  * [B, T, D] layout when y_hd is a multiple of 64 (fp32) or 8 (bf16 / fp16);
  * other head dims take the generic kernels (same tolerance).  Replaces the
  * three calls of README.md:57-110 (lowrank.py:302-338 each), the .contiguous()
- * copies of their inputs and the head transposes of their outputs. */
+ * copies of their inputs and the head transposes of their outputs.  z_eff is
+ * NULL or an array of G buffers, each as z_eff of dc_lowrank_fwd. */
 int dc_lowrank_fwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z,
                            const void* const* U, const void* const* static_w, void* const* y,
-                           int64_t y_hd, int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
-                           int dtype, int residual, void* stream);
+                           void* const* z_eff, int64_t y_hd, int64_t B, int64_t T, int64_t D,
+                           int64_t R, int64_t W, int dtype, int residual, void* stream);
 
 /* Workspace bytes needed by dc_lowrank_bwd_grouped, or a negative dc_status. */
 int64_t dc_lowrank_bwd_grouped_ws_bytes(int64_t G, int64_t B, int64_t T, int64_t D, int64_t R,
@@ -152,10 +166,12 @@ int64_t dc_lowrank_bwd_grouped_ws_bytes(int64_t G, int64_t B, int64_t T, int64_t
  * is.  Per group, results are bitwise those of dc_lowrank_bwd (with a head
  * dim: when it is a multiple of 64, else the generic kernels).  Replaces
  * README.md:57-110's three backwards (lowrank.py:251-299 each) and the
- * concatenation of dq, dk, dv. */
+ * concatenation of dq, dk, dv.  z_eff is NULL or the array of G buffers that
+ * dc_lowrank_fwd_grouped filled. */
 int dc_lowrank_bwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z,
                            const void* const* U, const void* const* static_w,
-                           const void* const* dy, int64_t dy_hd, void* dx, int64_t dx_ld,
+                           const void* const* z_eff, const void* const* dy, int64_t dy_hd,
+                           void* dx, int64_t dx_ld,
                            void* const* dz, void* const* dU, void* const* dstatic_w,
                            void* workspace, int64_t ws_bytes,
                            int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,

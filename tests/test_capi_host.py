@@ -35,7 +35,7 @@ def header_functions():
 
 def test_exports_every_declared_symbol(lib):
     names = header_functions()
-    assert len(names) == 11, names
+    assert len(names) == 12, names
     raw = ctypes.CDLL(_capi.LIB_PATH)
     for n in names:
         assert hasattr(raw, n), f"{n} declared in dynconv.h but not exported"
@@ -43,7 +43,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_strings(lib):
-    assert lib.dc_abi_version() == 3
+    assert lib.dc_abi_version() == 4
     for s in (OK, E_NULL, E_SHAPE, E_DTYPE, E_UNSUP, E_WS, E_ALIGN, E_DEV, E_LAUNCH):
         assert len(lib.dc_status_string(s)) > 0
     assert b"unknown" in lib.dc_status_string(-99)
@@ -93,8 +93,8 @@ def test_headwise_bwd_validation(lib):
         assert hw_bwd(lib, sw=P, dsw=P, ws=P, nws=need) == E_DEV
 
 
-def lr_fwd(lib, x=P, z=P, U=P, sw=None, B=2, T=8, D=16, R=4, W=4, dt=0):
-    return lib.dc_lowrank_fwd(x, z, U, sw, P, B, T, D, R, W, dt, 0, None)
+def lr_fwd(lib, x=P, z=P, U=P, sw=None, zeff=None, B=2, T=8, D=16, R=4, W=4, dt=0):
+    return lib.dc_lowrank_fwd(x, z, U, sw, P, zeff, B, T, D, R, W, dt, 0, None)
 
 
 def test_lowrank_validation(lib):
@@ -106,18 +106,36 @@ def test_lowrank_validation(lib):
     assert lr_fwd(lib, W=0) == E_SHAPE
     assert lr_fwd(lib, z=None) == E_NULL
     assert lr_fwd(lib, U=P + 1) == E_ALIGN
+    assert lr_fwd(lib, zeff=P + 8) == E_ALIGN      # the padded z copy: 16-byte aligned
+    # the padded z copy the backward would build: none when z's own rows serve (R % 4 == 0,
+    # or 32 dynamic ranks for two rank chunks), else B*T rows of 4*k (one chunk) or 32 ranks
+    zb = lib.dc_lowrank_zeff_bytes
+    assert zb(2, 8, 16, 4, 4, 0, 1) == 0
+    assert zb(2, 8, 16, 3, 4, 0, 1) == 2 * 8 * 4 * 2
+    assert zb(2, 8, 16, 15, 4, 1, 1) == 2 * 8 * 16 * 2
+    assert zb(2, 8, 16, 31, 4, 0, 1) == 2 * 8 * 32 * 2
+    assert zb(2, 8, 16, 32, 4, 0, 0) == 0
+    assert zb(2, 8, 16, 28, 4, 0, 0) == 2 * 8 * 32 * 2
+    assert zb(2, 8, 16, 3, 4, 2, 1) == 0              # fp32: the backward reads z itself
+    assert zb(2, 8, 20, 3, 4, 0, 1) == 0              # D % 16 != 0: no matrix-core backward
+    assert zb(2, 8, 16, 0, 4, 0, 1) == E_SHAPE
     need = lib.dc_lowrank_bwd_ws_bytes(2, 8, 16, 4, 4, 0, 1)
     assert need > 0
     assert lib.dc_lowrank_bwd_ws_bytes(2, 8, 16, 4, 9, 0, 1) == E_UNSUP
-    st = lib.dc_lowrank_bwd(P, P, P, P, P, P, P, P, P, None, 0, 2, 8, 16, 4, 4, 0, 0, None)
+    st = lib.dc_lowrank_bwd(P, P, P, P, None, P, P, P, P, P, None, 0, 2, 8, 16, 4, 4, 0, 0, None)
     assert st == E_WS
-    st = lib.dc_lowrank_bwd(P, P, P, P, P, P, P, P, P, P + 8, need, 2, 8, 16, 4, 4, 0, 0, None)
+    st = lib.dc_lowrank_bwd(P, P, P, P, None, P, P, P, P, P, P + 8, need, 2, 8, 16, 4, 4, 0, 0, None)
     assert st == E_WS  # workspace below 16-byte alignment
-    st = lib.dc_lowrank_bwd(P, P, P, None, P, P, P, P, P, P, need, 2, 8, 16, 4, 4, 0, 0, None)
+    st = lib.dc_lowrank_bwd(P, P, P, None, None, P, P, P, P, P, P, need, 2, 8, 16, 4, 4, 0, 0, None)
     assert st == E_NULL
+    st = lib.dc_lowrank_bwd(P, P, P, P, P + 8, P, P, P, P, P, P, need, 2, 8, 16, 4, 4, 0, 0, None)
+    assert st == E_ALIGN  # the padded z copy below 16-byte alignment
     if no_dev:
         assert lr_fwd(lib) == E_DEV
-        st = lib.dc_lowrank_bwd(P, P, P, P, P, P, P, P, P, P, need, 2, 8, 16, 4, 4, 0, 0, None)
+        assert lr_fwd(lib, R=3, sw=P, zeff=P) == E_DEV
+        st = lib.dc_lowrank_bwd(P, P, P, P, None, P, P, P, P, P, P, need, 2, 8, 16, 4, 4, 0, 0, None)
+        assert st == E_DEV
+        st = lib.dc_lowrank_bwd(P, P, P, P, P, P, P, P, P, P, P, need, 2, 8, 16, 3, 4, 0, 0, None)
         assert st == E_DEV
 
 
@@ -126,11 +144,12 @@ def arr(*ptrs):
     return (ctypes.c_void_p * len(ptrs))(*ptrs)
 
 
-def lr_fwd_g(lib, G=3, x=P, x_ld=48, z="ok", U="ok", sw=None, y="ok", y_hd=0, B=2, T=8, D=16, R=4, W=4, dt=0):
+def lr_fwd_g(lib, G=3, x=P, x_ld=48, z="ok", U="ok", sw=None, y="ok", zeff=None, y_hd=0, B=2, T=8, D=16, R=4, W=4,
+             dt=0):
     z = arr(*[P] * G) if z == "ok" else z
     U = arr(*[P] * G) if U == "ok" else U
     y = arr(*[P] * G) if y == "ok" else y
-    return lib.dc_lowrank_fwd_grouped(G, x, x_ld, z, U, sw, y, y_hd, B, T, D, R, W, dt, 0, None)
+    return lib.dc_lowrank_fwd_grouped(G, x, x_ld, z, U, sw, y, zeff, y_hd, B, T, D, R, W, dt, 0, None)
 
 
 def test_lowrank_grouped_fwd_validation(lib):
@@ -146,6 +165,8 @@ def test_lowrank_grouped_fwd_validation(lib):
     assert lr_fwd_g(lib, y=arr(P, None, P)) == E_NULL      # a NULL entry
     assert lr_fwd_g(lib, sw=arr(P, P, None)) == E_NULL      # static_w for every group or none
     assert lr_fwd_g(lib, U=arr(P, P + 1, P)) == E_ALIGN
+    assert lr_fwd_g(lib, zeff=arr(P, None, P)) == E_NULL    # padded z copies for every group or none
+    assert lr_fwd_g(lib, zeff=arr(P, P + 8, P)) == E_ALIGN
     assert lr_fwd_g(lib, x=P + 1) == E_ALIGN
     assert lr_fwd_g(lib, y_hd=-1) == E_SHAPE               # head dims: D % y_hd == 0, y_hd <= D
     assert lr_fwd_g(lib, y_hd=5) == E_SHAPE
@@ -167,8 +188,8 @@ def test_lowrank_grouped_bwd_validation(lib):
     assert lib.dc_lowrank_bwd_grouped_ws_bytes(3, 2, 8, 16, 0, 4, 0, 1) == E_SHAPE
     g3 = arr(P, P, P)
 
-    def call(G=3, x_ld=48, dx_ld=48, sw=None, dsw=None, ws=P, nws=need, dz=g3, dy=g3, dy_hd=0):
-        return lib.dc_lowrank_bwd_grouped(G, P, x_ld, g3, g3, sw, dy, dy_hd, P, dx_ld, dz, g3, dsw, ws, nws,
+    def call(G=3, x_ld=48, dx_ld=48, sw=None, dsw=None, ws=P, nws=need, dz=g3, dy=g3, dy_hd=0, zeff=None):
+        return lib.dc_lowrank_bwd_grouped(G, P, x_ld, g3, g3, sw, zeff, dy, dy_hd, P, dx_ld, dz, g3, dsw, ws, nws,
                                           2, 8, 16, 4, 4, 0, 0, None)
 
     assert call(G=5) == E_UNSUP
@@ -178,6 +199,8 @@ def test_lowrank_grouped_bwd_validation(lib):
     assert call(sw=None, dsw=g3) == E_NULL
     assert call(dz=arr(P, None, P)) == E_NULL
     assert call(dy=None) == E_NULL
+    assert call(zeff=arr(P, P, None)) == E_NULL
+    assert call(zeff=arr(P + 8, P, P)) == E_ALIGN
     assert call(sw=g3, dsw=g3, ws=None) == E_WS
     assert call(sw=g3, dsw=g3, nws=need - 256) == E_WS
     assert call(sw=g3, dsw=g3, ws=P + 16) == E_WS           # workspace shares start 256-byte aligned

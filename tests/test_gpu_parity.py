@@ -381,3 +381,52 @@ def test_generic_matches_vector_path():
     assert max_rel(y_v, y_g) < 1e-2
     for a, b in zip(g_v, g_g):
         assert max_rel(a, b) < 1e-2
+
+
+# ------------------------------------------------- padded z copy from the forward
+@pytest.mark.parametrize("R,static,xoff", [(15, True, 0), (31, True, 0), (3, False, 0), (28, False, 0),
+                                           (15, True, 4)])
+def test_lowrank_zeff_saved(R, static, xoff):
+    """The forward's padded z copy (z, the static column as 1, zero ranks up to RP) feeds the
+    backward exactly as the copy the backward builds itself: bitwise equal gradients.  xoff = 4
+    puts x 8 bytes off 16-byte alignment: the forward takes its element-aligned kernels and
+    fills the copy in a launch of its own, the backward stays on matrix cores."""
+    from dynconv import _capi
+
+    lib = _capi.load()
+    Bn, Tn, Dn, W = 2, 300, 256, 4
+    g = gen(17 + R)
+    bf = torch.bfloat16
+    xb = randn(g, Bn * Tn * Dn + xoff).to(bf).to(DEV)
+    x = xb[xoff:].view(Bn, Tn, Dn)
+    z = randn(g, Bn, Tn, R).to(bf).to(DEV)
+    U = randn(g, R, W * Dn, scale=1 / math.sqrt((R + 1) * W)).to(bf).to(DEV)
+    sw = uniform(g, W, Dn, lo=-0.5, hi=0.5).to(bf).to(DEV) if static else None
+    dy = randn(g, Bn, Tn, Dn).to(bf).to(DEV)
+    rk = R + (1 if static else 0)
+    rp = 32 if 16 < rk <= 32 else (rk + 3) // 4 * 4
+    nz = lib.dc_lowrank_zeff_bytes(Bn, Tn, Dn, R, W, 0, int(static))
+    assert nz == Bn * Tn * rp * 2
+    zeff = torch.full((nz,), 0xAB, dtype=torch.uint8, device=DEV)  # the forward overwrites all of it
+    y = torch.empty_like(x)
+    p = _capi.ptr
+    st = torch.cuda.current_stream().cuda_stream
+    _capi.check(lib.dc_lowrank_fwd(p(x), p(z), p(U), p(sw), p(y), p(zeff), Bn, Tn, Dn, R, W, 0, 1, st), "fwd")
+    want = torch.zeros(Bn * Tn, rp, dtype=bf, device=DEV)
+    want[:, :R] = z.reshape(-1, R)
+    if static:
+        want[:, R] = 1.0
+    torch.cuda.synchronize()
+    assert torch.equal(zeff.view(bf).view(Bn * Tn, rp), want)
+    nws = lib.dc_lowrank_bwd_ws_bytes(Bn, Tn, Dn, R, W, 0, int(static))
+    outs = []
+    for zp in (None, zeff):
+        ws = torch.empty(nws, dtype=torch.uint8, device=DEV)
+        dx, dz, dU = torch.empty_like(x), torch.empty_like(z), torch.empty_like(U)
+        dsw = torch.empty_like(sw) if static else None
+        _capi.check(lib.dc_lowrank_bwd(p(x), p(z), p(U), p(sw), p(zp), p(dy), p(dx), p(dz), p(dU), p(dsw), p(ws),
+                                       nws, Bn, Tn, Dn, R, W, 0, 1, st), "bwd")
+        outs.append([dx, dz, dU] + ([dsw] if static else []))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
