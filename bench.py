@@ -75,6 +75,8 @@ CONFIGS = {
     "lr_r16": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=4, static=False, residual=True),
 }
 EXTRA = {
+    # BASELINE configs[0], the CPU baseline's own workload, on the GPU (fp32, loss y.sum() in the baseline)
+    "cfg0_hw_fp32": dict(kind="hw", B=2, T=1024, D=512, H=512, W=4, static=False, residual=False, dtype="fp32"),
     "lr_qkv": dict(kind="lr", B=2, T=8192, D=4096, R=31, W=4, static=True, residual=True, calls=3),
     "lr_qkv_grouped": dict(kind="lrg", B=2, T=8192, D=4096, R=31, W=4, static=True, residual=True, G=3,
                            head_dim=128),
@@ -211,6 +213,7 @@ def abi_sets(c, torch, dev):
             # the forward's padded z copy for the backward, as the autograd Function keeps it
             nz = lib.dc_lowrank_zeff_bytes(B, T, D, R, W, dt, int(c["static"]))
             d["zeffs"] = [torch.empty(nz, dtype=torch.uint8, device=dev) for _ in range(G)] if nz > 0 else None
+            d["nzeff"] = max(nz, 0)
             d["ws"] = torch.empty(max(d["nws"], 1), dtype=torch.uint8, device=dev)
             sets.append(d)
         return sets
@@ -229,6 +232,7 @@ def abi_sets(c, torch, dev):
             nws = lib.dc_lowrank_bwd_ws_bytes(B, T, D, c["R"], W, dt, int(c["static"]))
             nz = lib.dc_lowrank_zeff_bytes(B, T, D, c["R"], W, dt, int(c["static"]))
             d["zeff"] = torch.empty(nz, dtype=torch.uint8, device=dev) if nz > 0 else None
+            d["nzeff"] = max(nz, 0)
         d["y"], d["dx"] = torch.empty_like(d["x"]), torch.empty_like(d["x"])
         d["dsw"] = torch.empty_like(d["sw"]) if c["static"] else None
         d["nws"] = nws
@@ -254,13 +258,15 @@ def abi_launchers(c, sets, torch):
         def fwd(i):
             d = sets[i]
             _capi.check(lib.dc_lowrank_fwd_grouped(G, p(d["x"]), G * D, pa(d["zs"]), pa(d["Us"]), pa(d["sws"]),
-                                                   pa(d["ys"]), pa(d["zeffs"]), 0, B, T, D, R, W, dt, res, st),
+                                                   pa(d["ys"]), pa(d["zeffs"]), d["nzeff"], 0, B, T, D, R, W, dt,
+                                                   res, st),
                         "grouped fwd")
 
         def bwd(i):
             d = sets[i]
             _capi.check(lib.dc_lowrank_bwd_grouped(G, p(d["x"]), G * D, pa(d["zs"]), pa(d["Us"]), pa(d["sws"]),
-                                                   pa(d["zeffs"]), pa(d["dys"]), 0, p(d["dx"]), G * D, pa(d["dzs"]),
+                                                   pa(d["zeffs"]), d["nzeff"], pa(d["dys"]), 0, p(d["dx"]), G * D,
+                                                   pa(d["dzs"]),
                                                    pa(d["dUs"]),
                                                    pa(d["dsws"]), p(d["ws"]), d["nws"], B, T, D, R, W, dt, res, st),
                         "grouped bwd")
@@ -283,12 +289,12 @@ def abi_launchers(c, sets, torch):
         def fwd(i):
             d = sets[i]
             _capi.check(lib.dc_lowrank_fwd(p(d["x"]), p(d["z"]), p(d["U"]), p(d["sw"]), p(d["y"]), p(d["zeff"]),
-                                           B, T, D, R, W, dt, res, st), "fwd")
+                                           d["nzeff"], B, T, D, R, W, dt, res, st), "fwd")
 
         def bwd(i):
             d = sets[i]
-            _capi.check(lib.dc_lowrank_bwd(p(d["x"]), p(d["z"]), p(d["U"]), p(d["sw"]), p(d["zeff"]), p(d["dy"]),
-                                           p(d["dx"]),
+            _capi.check(lib.dc_lowrank_bwd(p(d["x"]), p(d["z"]), p(d["U"]), p(d["sw"]), p(d["zeff"]), d["nzeff"],
+                                           p(d["dy"]), p(d["dx"]),
                                            p(d["dz"]), p(d["dU"]), p(d["dsw"]), p(d["ws"]), d["nws"],
                                            B, T, D, R, W, dt, res, st), "bwd")
     return fwd, bwd
@@ -380,6 +386,42 @@ def qkv_end_to_end(torch, dev, reps=10):
           f"grouped {out['grouped_us']} us ({out['speedup']}x); with [B,H,T,{hd}] outputs: README + contiguous "
           f"{out['readme_heads_contiguous_us']} us, grouped head-major {out['grouped_head_major_us']} us "
           f"({out['speedup_heads']}x)", file=sys.stderr, flush=True)
+    return out
+
+
+def proj_in_gemm(torch, dev, reps=20):
+    """The upstream proj_in GEMM of the grouped QKV module at configs[4] (README.md:67, 75): z = pre_z @ W_in^T
+    for all three groups at once ([B*T, D] x [D, 3R]), and its backward (dW_in = dz^T pre_z, d pre_z = dz W_in),
+    as torch (hipBLASLt) runs them: time per launch rotating over input sets that do not fit the MALL, and the
+    bandwidth each reaches on its algorithmic bytes (the GEMMs are far below the bf16 ridge: 2*3R flop/byte)."""
+    c = EXTRA["lr_qkv_grouped"]
+    B, T, D, R, G = c["B"], c["T"], c["D"], c["R"], c["G"]
+    bf = torch.bfloat16
+    n = max(2, math.ceil(4 * MALL_BYTES / (B * T * D * 2)))
+    pre = [torch.randn(B, T, D, device=dev).to(bf).requires_grad_() for _ in range(n)]
+    win = (torch.randn(G * R, D, device=dev) / math.sqrt(D)).to(bf).requires_grad_()
+    dz = [torch.randn(B, T, G * R, device=dev).to(bf) for _ in range(n)]
+    F = torch.nn.functional
+    zs = [F.linear(p, win) for p in pre]
+
+    def fwd(i):
+        F.linear(pre[i], win)
+
+    def bwd(i):
+        pre[i].grad = win.grad = None  # fresh gradients: no accumulation kernels in the timing
+        torch.autograd.backward(zs[i], dz[i], retain_graph=True)
+
+    f_us = time_launches(torch, fwd, n, reps)
+    b_us = time_launches(torch, bwd, n, reps)
+    e = 2
+    f_bytes = (B * T * D + G * R * D + B * T * G * R) * e
+    b_bytes = (B * T * G * R + B * T * D + G * R * D) * e + (G * R * D + B * T * D) * e  # reads dz, pre_z, W_in
+    out = {"shape": f"[{B * T}, {D}] x [{D}, {G * R}] bf16",
+           "fwd_us": round(f_us, 2), "fwd_GBs": round(f_bytes / (f_us * 1e-6) / 1e9, 1),
+           "bwd_us": round(b_us, 2), "bwd_GBs": round(b_bytes / (b_us * 1e-6) / 1e9, 1),
+           "alg_MB": round((f_bytes + b_bytes) / 1e6, 1)}
+    print(f"[bench] proj_in GEMM (configs[4], 3 groups): fwd {f_us:.1f} us ({out['fwd_GBs']} GB/s), bwd {b_us:.1f} us "
+          f"({out['bwd_GBs']} GB/s)", file=sys.stderr, flush=True)
     return out
 
 
@@ -514,6 +556,14 @@ def main():
 
     qkv = None if args.no_extra else qkv_end_to_end(torch, dev)
     torch.cuda.empty_cache()
+    if qkv is not None:
+        qkv["proj_in_gemm"] = proj_in_gemm(torch, dev)
+        torch.cuda.empty_cache()
+    cpu = None if args.no_cpu_baseline else cpu_baseline(torch)
+    if cpu is not None and "cfg0_hw_fp32" in breakdown:
+        g0 = breakdown["cfg0_hw_fp32"]
+        cpu["gpu_same_config"] = {"fwdbwd_us": g0["fwdbwd_us"], "GBs": g0["fwdbwd_GBs"],
+                                  "gpu_over_cpu": round(g0["fwdbwd_GBs"] / cpu["value"], 1)}
 
     out = {
         "metric": METRIC,
@@ -535,7 +585,7 @@ def main():
             "frac_of_peak": round(value / PEAK_GBS, 4),
         },
         "roofline": roofline,
-        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(torch),
+        "cpu_baseline": cpu,
         "breakdown": breakdown,
         "qkv": qkv,
     }

@@ -70,7 +70,7 @@ const char* dc_status_string(int status) {
     case DC_ERR_SHAPE: return "invalid shape (non-positive size, D % H != 0, or size too large)";
     case DC_ERR_DTYPE: return "unsupported dtype";
     case DC_ERR_UNSUPPORTED: return "unsupported configuration (W or rank above the library maximum)";
-    case DC_ERR_WORKSPACE: return "workspace missing or smaller than the size query";
+    case DC_ERR_WORKSPACE: return "workspace (or z_eff buffer) missing or smaller than its size query";
     case DC_ERR_ALIGN: return "pointer not aligned to its element size";
     case DC_ERR_DEVICE: return "no HIP device available";
     case DC_ERR_LAUNCH: return "kernel launch failed";
@@ -92,6 +92,23 @@ int dc_headwise_fwd(const void* x, const void* weight, const void* static_w, voi
   p.B = B; p.T = T; p.D = D; p.H = H; p.W = W;
   p.dtype = dtype; p.residual = residual ? 1 : 0; p.stream = (hipStream_t)stream;
   return launch_status(dc::hw_fwd(p));
+}
+
+static_assert(DC_PATH_GENERIC == 0 && DC_PATH_VECTOR == 1 && DC_PATH_MFMA == 2 && DC_PATH_F32_MFMA == 3 &&
+                  DC_PATH_F32_VALU == 4,
+              "dc_path codes returned by hw_path / lr_path");
+
+int dc_headwise_path(int64_t B, int64_t T, int64_t D, int64_t H, int64_t W, int dtype, int has_static, int bwd) {
+  int s = check_headwise(B, T, D, H, W, dtype);
+  if (s != DC_OK) return s;
+  static const char kAligned[16] __attribute__((aligned(256))) = {0};
+  dc::HwProblem p{};
+  p.x = p.weight = p.dy = kAligned;
+  p.dx = p.dweight = p.y = (void*)kAligned;
+  p.static_w = has_static ? kAligned : nullptr;
+  p.dstatic_w = has_static ? (void*)kAligned : nullptr;
+  p.B = B; p.T = T; p.D = D; p.H = H; p.W = W; p.dtype = dtype;
+  return dc::hw_path(p, bwd != 0);
 }
 
 int64_t dc_headwise_bwd_ws_bytes(int64_t B, int64_t T, int64_t D, int64_t H, int64_t W, int dtype,
@@ -149,14 +166,24 @@ int64_t dc_lowrank_zeff_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_
   return dc::lr_zeff_bytes(p);
 }
 
-// The z_eff buffer a call uses: the caller's when the shape has one, else none.
-static void* zeff_of(const void* z_eff, int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype,
-                     bool has_static) {
-  return z_eff && dc_lowrank_zeff_bytes(B, T, D, R, W, dtype, has_static) > 0 ? const_cast<void*>(z_eff) : nullptr;
+// z_eff bytes a call needs (dc_lowrank_zeff_bytes; the shape is already valid).
+static int64_t zeff_need(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, bool has_static) {
+  const int64_t n = dc_lowrank_zeff_bytes(B, T, D, R, W, dtype, has_static);
+  return n > 0 ? n : 0;
 }
 
+// A caller's z_eff buffer: DC_ERR_WORKSPACE when the shape uses one and the
+// buffer is shorter than the size query.
+static int zeff_status(const void* z_eff, int64_t z_eff_bytes, int64_t need) {
+  return z_eff && need > 0 && z_eff_bytes < need ? DC_ERR_WORKSPACE : DC_OK;
+}
+
+// The z_eff buffer a call uses: the caller's when the shape has one, else none.
+static void* zeff_of(const void* z_eff, int64_t need) { return z_eff && need > 0 ? const_cast<void*>(z_eff) : nullptr; }
+
 int dc_lowrank_fwd(const void* x, const void* z, const void* U, const void* static_w, void* y, void* z_eff,
-                   int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int residual, void* stream) {
+                   int64_t z_eff_bytes, int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype,
+                   int residual, void* stream) {
   int s = check_lowrank(B, T, D, R, W, dtype, static_w != nullptr);
   if (s != DC_OK) return s;
   if (!x || !z || !U || !y) return DC_ERR_NULL;
@@ -164,13 +191,28 @@ int dc_lowrank_fwd(const void* x, const void* z, const void* U, const void* stat
   if (!aligned_to(x, es) || !aligned_to(z, es) || !aligned_to(U, es) || !aligned_to(static_w, es) ||
       !aligned_to(y, es) || !aligned_to(z_eff, 16))
     return DC_ERR_ALIGN;
+  const int64_t zneed = zeff_need(B, T, D, R, W, dtype, static_w != nullptr);
+  if ((s = zeff_status(z_eff, z_eff_bytes, zneed)) != DC_OK) return s;
   if ((s = device_status()) != DC_OK) return s;
   dc::LrProblem p{};
   p.x = x; p.z = z; p.U = U; p.static_w = static_w; p.y = y;
-  p.zeff = zeff_of(z_eff, B, T, D, R, W, dtype, static_w != nullptr);
+  p.zeff = zeff_of(z_eff, zneed);
   p.B = B; p.T = T; p.D = D; p.R = R; p.W = W;
   p.dtype = dtype; p.residual = residual ? 1 : 0; p.stream = (hipStream_t)stream;
   return launch_status(dc::lr_fwd(&p, 1));
+}
+
+int dc_lowrank_path(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int has_static, int bwd) {
+  int s = check_lowrank(B, T, D, R, W, dtype, has_static != 0);
+  if (s != DC_OK) return s;
+  static const char kAligned[16] __attribute__((aligned(256))) = {0};
+  dc::LrProblem p{};
+  p.x = p.z = p.U = p.dy = kAligned;
+  p.y = p.dx = p.dz = p.dU = (void*)kAligned;
+  p.static_w = has_static ? kAligned : nullptr;
+  p.dstatic_w = has_static ? (void*)kAligned : nullptr;
+  p.B = B; p.T = T; p.D = D; p.R = R; p.W = W; p.dtype = dtype;
+  return dc::lr_path(p, bwd != 0);
 }
 
 int64_t dc_lowrank_bwd_ws_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype,
@@ -191,8 +233,9 @@ int64_t dc_lowrank_bwd_ws_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int6
 }
 
 int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* static_w, const void* z_eff,
-                   const void* dy, void* dx, void* dz, void* dU, void* dstatic_w, void* workspace, int64_t ws_bytes,
-                   int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int residual, void* stream) {
+                   int64_t z_eff_bytes, const void* dy, void* dx, void* dz, void* dU, void* dstatic_w,
+                   void* workspace, int64_t ws_bytes, int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
+                   int dtype, int residual, void* stream) {
   int s = check_lowrank(B, T, D, R, W, dtype, static_w != nullptr);
   if (s != DC_OK) return s;
   if (!x || !z || !U || !dy || !dx || !dz || !dU) return DC_ERR_NULL;
@@ -205,11 +248,13 @@ int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* stat
   const int64_t need = dc_lowrank_bwd_ws_bytes(B, T, D, R, W, dtype, static_w != nullptr);
   if (need < 0) return (int)need;
   if (need > 0 && (workspace == nullptr || ws_bytes < need || !aligned_to(workspace, 16))) return DC_ERR_WORKSPACE;
+  const int64_t zneed = zeff_need(B, T, D, R, W, dtype, static_w != nullptr);
+  if ((s = zeff_status(z_eff, z_eff_bytes, zneed)) != DC_OK) return s;
   if ((s = device_status()) != DC_OK) return s;
   dc::LrProblem p{};
   p.x = x; p.z = z; p.U = U; p.static_w = static_w; p.dy = dy;
   p.dx = dx; p.dz = dz; p.dU = dU; p.dstatic_w = dstatic_w; p.ws = (float*)workspace;
-  p.zeff = zeff_of(z_eff, B, T, D, R, W, dtype, static_w != nullptr);
+  p.zeff = zeff_of(z_eff, zneed);
   p.B = B; p.T = T; p.D = D; p.R = R; p.W = W;
   p.dtype = dtype; p.residual = residual ? 1 : 0; p.stream = (hipStream_t)stream;
   return launch_status(dc::lr_bwd(&p, 1));
@@ -224,9 +269,9 @@ int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* stat
 static bool head_dim_ok(int64_t hd, int64_t D) { return hd == 0 || (hd > 0 && hd <= D && D % hd == 0); }
 
 int dc_lowrank_fwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z, const void* const* U,
-                           const void* const* static_w, void* const* y, void* const* z_eff, int64_t y_hd,
-                           int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int residual,
-                           void* stream) {
+                           const void* const* static_w, void* const* y, void* const* z_eff, int64_t z_eff_bytes,
+                           int64_t y_hd, int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype,
+                           int residual, void* stream) {
   if (G < 1 || G > DC_MAX_GROUPS) return DC_ERR_UNSUPPORTED;
   int s = check_lowrank(B, T, D, R, W, dtype, static_w != nullptr);
   if (s != DC_OK) return s;
@@ -234,6 +279,7 @@ int dc_lowrank_fwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* c
   if (!x || !z || !U || !y) return DC_ERR_NULL;
   const int es = dc::dtype_size(dtype);
   if (!aligned_to(x, es)) return DC_ERR_ALIGN;
+  const int64_t zneed = zeff_need(B, T, D, R, W, dtype, static_w != nullptr);
   dc::LrProblem p[DC_MAX_GROUPS] = {};
   for (int64_t g = 0; g < G; ++g) {
     const void* sw = static_w ? static_w[g] : nullptr;
@@ -243,10 +289,11 @@ int dc_lowrank_fwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* c
       return DC_ERR_ALIGN;
     dc::LrProblem& q = p[g];
     q.x = (const char*)x + g * D * es; q.z = z[g]; q.U = U[g]; q.static_w = sw; q.y = y[g];
-    q.zeff = z_eff ? zeff_of(z_eff[g], B, T, D, R, W, dtype, static_w != nullptr) : nullptr;
+    q.zeff = z_eff ? zeff_of(z_eff[g], zneed) : nullptr;
     q.B = B; q.T = T; q.D = D; q.R = R; q.W = W; q.x_ld = x_ld; q.y_hd = y_hd;
     q.dtype = dtype; q.residual = residual ? 1 : 0; q.stream = (hipStream_t)stream;
   }
+  if (z_eff && (s = zeff_status(z_eff[0], z_eff_bytes, zneed)) != DC_OK) return s;
   if ((s = device_status()) != DC_OK) return s;
   return launch_status(dc::lr_fwd(p, (int)G));
 }
@@ -265,8 +312,8 @@ int64_t dc_lowrank_bwd_grouped_ws_bytes(int64_t G, int64_t B, int64_t T, int64_t
 }
 
 int dc_lowrank_bwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z, const void* const* U,
-                           const void* const* static_w, const void* const* z_eff, const void* const* dy,
-                           int64_t dy_hd, void* dx,
+                           const void* const* static_w, const void* const* z_eff, int64_t z_eff_bytes,
+                           const void* const* dy, int64_t dy_hd, void* dx,
                            int64_t dx_ld, void* const* dz, void* const* dU, void* const* dstatic_w,
                            void* workspace, int64_t ws_bytes, int64_t B, int64_t T, int64_t D, int64_t R,
                            int64_t W, int dtype, int residual, void* stream) {
@@ -283,6 +330,7 @@ int dc_lowrank_bwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* c
   if (share < 0) return (int)share;
   if (share > 0 && (workspace == nullptr || ws_bytes < G * share || !aligned_to(workspace, 256)))
     return DC_ERR_WORKSPACE;
+  const int64_t zneed = zeff_need(B, T, D, R, W, dtype, static_w != nullptr);
   dc::LrProblem p[DC_MAX_GROUPS] = {};
   for (int64_t g = 0; g < G; ++g) {
     const void* sw = static_w ? static_w[g] : nullptr;
@@ -296,11 +344,12 @@ int dc_lowrank_bwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* c
     dc::LrProblem& q = p[g];
     q.x = (const char*)x + g * D * es; q.z = z[g]; q.U = U[g]; q.static_w = sw; q.dy = dy[g];
     q.dx = (char*)dx + g * D * es; q.dz = dz[g]; q.dU = dU[g]; q.dstatic_w = dsw;
-    q.zeff = z_eff ? zeff_of(z_eff[g], B, T, D, R, W, dtype, static_w != nullptr) : nullptr;
+    q.zeff = z_eff ? zeff_of(z_eff[g], zneed) : nullptr;
     q.ws = share > 0 ? (float*)((char*)workspace + g * share) : nullptr;
     q.B = B; q.T = T; q.D = D; q.R = R; q.W = W; q.x_ld = x_ld; q.dx_ld = dx_ld; q.y_hd = dy_hd;
     q.dtype = dtype; q.residual = residual ? 1 : 0; q.stream = (hipStream_t)stream;
   }
+  if (z_eff && (s = zeff_status(z_eff[0], z_eff_bytes, zneed)) != DC_OK) return s;
   if ((s = device_status()) != DC_OK) return s;
   return launch_status(dc::lr_bwd(p, (int)G));
 }

@@ -32,6 +32,8 @@ struct HwProblem {
 bool hw_fast_ok(const HwProblem& p, bool bwd);
 // Bytes of fp32 partials the backward needs (0 without a static filter).
 int64_t hw_bwd_ws_bytes(const HwProblem& p);
+// dc_path code of the kernels hw_fwd / hw_bwd run for p.
+int hw_path(const HwProblem& p, bool bwd);
 hipError_t hw_fwd(const HwProblem& p);
 hipError_t hw_bwd(const HwProblem& p);
 
@@ -73,6 +75,8 @@ struct LrProblem {
 constexpr int kMaxGroups = 4;
 
 bool lr_mfma_ok(const LrProblem& p, bool bwd);
+// dc_path code of the kernels lr_fwd / lr_bwd run for one problem p.
+int lr_path(const LrProblem& p, bool bwd);
 int64_t lr_bwd_ws_bytes(const LrProblem& p);
 // Bytes of the padded z_eff the MFMA backward builds for p (0: it reads z itself).
 int64_t lr_zeff_bytes(const LrProblem& p);

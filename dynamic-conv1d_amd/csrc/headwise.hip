@@ -246,6 +246,8 @@ int64_t hw_bwd_ws_bytes(const HwProblem& p) {
   return (int64_t)P * p.W * p.D * (int64_t)sizeof(float);
 }
 
+int hw_path(const HwProblem& p, bool bwd) { return hw_fast_ok(p, bwd) ? 1 : 0; }
+
 hipError_t hw_fwd(const HwProblem& p) {
   if (hw_fast_ok(p, false)) {
     const HwPlan pl = make_plan(p, false);

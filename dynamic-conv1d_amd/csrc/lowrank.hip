@@ -87,31 +87,33 @@ __global__ __launch_bounds__(256) void lr_bwd_dx_generic(const T* __restrict__ z
 }
 
 // dz[row, r] = sum_{k, d} dy[row, d] * x[row-k, d] * U[r, k*D+d]; one
-// workgroup per row, tree reduction in LDS.
+// workgroup per row (a grid-stride loop over rows: the grid is capped like the
+// other generic launches), tree reduction in LDS.
 template <typename T>
 __global__ __launch_bounds__(256) void lr_bwd_dz_generic(const T* __restrict__ x, const T* __restrict__ U,
-                                                         const T* __restrict__ dy, T* __restrict__ dz, int Tn,
-                                                         int D, int64_t xld, int hd, int R, int W) {
+                                                         const T* __restrict__ dy, T* __restrict__ dz, int64_t BT,
+                                                         int Tn, int D, int64_t xld, int hd, int R, int W) {
   __shared__ float red[256];
-  const int64_t row = blockIdx.x;
-  const int t = (int)(row % Tn);
   const int64_t WD = (int64_t)W * D;
-  for (int r = 0; r < R; ++r) {
-    float acc = 0.f;
-    for (int k = 0; k < W && k <= t; ++k) {
-      const T* xr = x + (row - k) * xld;
-      const T* ur = U + (int64_t)r * WD + (int64_t)k * D;
-      for (int d = threadIdx.x; d < D; d += 256)
-        acc = fmaf((float)dy[yoff(row, d, Tn, D, hd)] * (float)xr[d], (float)ur[d], acc);
-    }
-    red[threadIdx.x] = acc;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-      if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+  for (int64_t row = blockIdx.x; row < BT; row += gridDim.x) {
+    const int t = (int)(row % Tn);
+    for (int r = 0; r < R; ++r) {
+      float acc = 0.f;
+      for (int k = 0; k < W && k <= t; ++k) {
+        const T* xr = x + (row - k) * xld;
+        const T* ur = U + (int64_t)r * WD + (int64_t)k * D;
+        for (int d = threadIdx.x; d < D; d += 256)
+          acc = fmaf((float)dy[yoff(row, d, Tn, D, hd)] * (float)xr[d], (float)ur[d], acc);
+      }
+      red[threadIdx.x] = acc;
+      __syncthreads();
+      for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+        __syncthreads();
+      }
+      if (threadIdx.x == 0) dz[row * R + r] = (T)red[0];
       __syncthreads();
     }
-    if (threadIdx.x == 0) dz[row * R + r] = (T)red[0];
-    __syncthreads();
   }
 }
 
@@ -151,6 +153,11 @@ unsigned generic_grid(int64_t n) {
   return (unsigned)(g < 1 ? 1 : g);
 }
 
+// Workgroups of the generic dz launch: one per row, at most 65536 (a
+// grid-stride loop takes the rest).  HIP rejects grids above 2^32 work-items,
+// which one workgroup of 256 per row would reach at B*T >= 2^24.
+unsigned dz_grid(int64_t BT) { return (unsigned)(BT < 65536 ? BT : 65536); }
+
 int generic_partials(int64_t BT) {
   int64_t P = (BT + 255) / 256;
   return (int)(P > 64 ? 64 : (P < 1 ? 1 : P));
@@ -173,9 +180,9 @@ hipError_t bwd_generic(const LrProblem& p) {
   lr_bwd_dx_generic<T><<<generic_grid(BT * p.D), 256, 0, p.stream>>>(
       (const T*)p.z, (const T*)p.U, (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, BT, (int)p.T, (int)p.D,
       p.dxld(), (int)p.yhd(), (int)p.R, (int)p.W, p.residual);
-  lr_bwd_dz_generic<T><<<(unsigned)BT, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.U, (const T*)p.dy,
-                                                           (T*)p.dz, (int)p.T, (int)p.D, p.xld(), (int)p.yhd(),
-                                                           (int)p.R, (int)p.W);
+  lr_bwd_dz_generic<T><<<dz_grid(BT), 256, 0, p.stream>>>((const T*)p.x, (const T*)p.U, (const T*)p.dy,
+                                                          (T*)p.dz, BT, (int)p.T, (int)p.D, p.xld(), (int)p.yhd(),
+                                                          (int)p.R, (int)p.W);
   const int P = generic_partials(BT);
   const int64_t rows_per = (BT + P - 1) / P;
   dim3 grid((unsigned)((RK * WD + 255) / 256), (unsigned)P);
@@ -239,6 +246,14 @@ int64_t lr_bwd_ws_bytes(const LrProblem& p) {
   }
   const int64_t RK = p.R + (p.static_w ? 1 : 0);
   return (int64_t)generic_partials(p.B * p.T) * RK * p.W * p.D * (int64_t)sizeof(float);
+}
+
+// The dispatch order of lr_fwd / lr_bwd below, as dc_path codes.
+int lr_path(const LrProblem& p, bool bwd) {
+  if (lr_mfma_ok(p, bwd)) return 2;
+  if (bwd ? lr_f32m_bwd_ok(p) : lr_f32m_fwd_ok(p)) return 3;
+  if (lr_f32_ok(p)) return 4;
+  return 0;
 }
 
 namespace {

@@ -760,23 +760,24 @@ struct ZpadArgs {
   int R, RP, stat, one;
 };
 // One thread per 4 ranks of a padded row (RP % 4 == 0): four 2-byte reads of
-// z (its rows need not be 4-byte aligned), one 8-byte store.
+// z (its rows need not be 4-byte aligned), one 8-byte store.  A grid-stride
+// loop: the grid is capped (launch_zpad).
 __global__ __launch_bounds__(256) void lr_zpad(ZpadArgs a) {
   const int g = blockIdx.y;
   const uint16_t* __restrict__ z = g == 0 ? a.z[0] : g == 1 ? a.z[1] : g == 2 ? a.z[2] : a.z[3];
   uint16_t* __restrict__ zp = g == 0 ? a.zp[0] : g == 1 ? a.zp[1] : g == 2 ? a.zp[2] : a.zp[3];
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= a.n) return;
-  const int64_t e = 4 * i;  // first element of the piece
-  const int64_t t = e / a.RP;
-  const int r0 = (int)(e - t * a.RP);
-  uint32_t v[4];
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n; i += (int64_t)gridDim.x * 256) {
+    const int64_t e = 4 * i;  // first element of the piece
+    const int64_t t = e / a.RP;
+    const int r0 = (int)(e - t * a.RP);
+    uint32_t v[4];
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    const int r = r0 + kk;
-    v[kk] = r < a.R ? z[t * a.R + r] : (r == a.R && a.stat ? (uint32_t)a.one : 0u);
+    for (int kk = 0; kk < 4; ++kk) {
+      const int r = r0 + kk;
+      v[kk] = r < a.R ? z[t * a.R + r] : (r == a.R && a.stat ? (uint32_t)a.one : 0u);
+    }
+    *reinterpret_cast<u32x2*>(zp + e) = u32x2{v[0] | (v[1] << 16), v[2] | (v[3] << 16)};
   }
-  *reinterpret_cast<u32x2*>(zp + e) = u32x2{v[0] | (v[1] << 16), v[2] | (v[3] << 16)};
 }
 
 // lr_zpad over G problems: z_eff of group g into dst[g].
@@ -793,7 +794,8 @@ hipError_t launch_zpad(const LrProblem* p, int G, void* const* dst) {
     za.z[g] = (const uint16_t*)p[g < G ? g : 0].z;
     za.zp[g] = (uint16_t*)dst[g < G ? g : 0];
   }
-  lr_zpad<<<dim3((unsigned)((za.n + 255) / 256), G), 256, 0, p[0].stream>>>(za);
+  const int64_t blocks = (za.n + 255) / 256;
+  lr_zpad<<<dim3((unsigned)(blocks < 65536 ? blocks : 65536), G), 256, 0, p[0].stream>>>(za);
   return hipGetLastError();
 }
 

@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdynconv.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
@@ -27,15 +27,19 @@ SIGNATURES = {
     "dc_abi_version": (_c_int, []),
     "dc_status_string": (ctypes.c_char_p, [_c_int]),
     "dc_headwise_fwd": (_c_int, [_c_vp] * 4 + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
+    "dc_headwise_path": (_c_int, [_c_i64] * 5 + [_c_int] * 3),
+    "dc_lowrank_path": (_c_int, [_c_i64] * 5 + [_c_int] * 3),
     "dc_headwise_bwd_ws_bytes": (_c_i64, [_c_i64] * 5 + [_c_int, _c_int]),
     "dc_headwise_bwd": (_c_int, [_c_vp] * 8 + [_c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
     "dc_lowrank_zeff_bytes": (_c_i64, [_c_i64] * 5 + [_c_int, _c_int]),
-    "dc_lowrank_fwd": (_c_int, [_c_vp] * 6 + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
+    "dc_lowrank_fwd": (_c_int, [_c_vp] * 6 + [_c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
     "dc_lowrank_bwd_ws_bytes": (_c_i64, [_c_i64] * 5 + [_c_int, _c_int]),
-    "dc_lowrank_bwd": (_c_int, [_c_vp] * 11 + [_c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
-    "dc_lowrank_fwd_grouped": (_c_int, [_c_i64, _c_vp, _c_i64] + [_c_pp] * 5 + [_c_i64] * 6 + [_c_int, _c_int, _c_vp]),
+    "dc_lowrank_bwd": (_c_int, [_c_vp] * 5 + [_c_i64] + [_c_vp] * 6 + [_c_i64] + [_c_i64] * 5
+                       + [_c_int, _c_int, _c_vp]),
+    "dc_lowrank_fwd_grouped": (_c_int, [_c_i64, _c_vp, _c_i64] + [_c_pp] * 5 + [_c_i64] * 7 + [_c_int, _c_int, _c_vp]),
     "dc_lowrank_bwd_grouped_ws_bytes": (_c_i64, [_c_i64] * 6 + [_c_int, _c_int]),
-    "dc_lowrank_bwd_grouped": (_c_int, [_c_i64, _c_vp, _c_i64] + [_c_pp] * 5 + [_c_i64, _c_vp, _c_i64] + [_c_pp] * 3
+    "dc_lowrank_bwd_grouped": (_c_int, [_c_i64, _c_vp, _c_i64] + [_c_pp] * 4 + [_c_i64] + [_c_pp]
+                               + [_c_i64, _c_vp, _c_i64] + [_c_pp] * 3
                                + [_c_vp, _c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
 }
 
@@ -66,6 +70,10 @@ def load(path: str = LIB_PATH):
             raise RuntimeError(f"libdynconv.so ABI version {ver}, expected {ABI_VERSION}")
         _lib = lib
     return _lib
+
+
+# dc_path codes (include/dynconv.h): which kernel family a shape runs on
+PATHS = {0: "generic", 1: "vector", 2: "mfma", 3: "f32_mfma", 4: "f32_valu"}
 
 
 def status_string(status: int) -> str:

@@ -16,12 +16,12 @@ from . import _capi
 
 
 def _zeff_buffers(lib, n, B, T, D, R, W, dtype, has_static, device):
-    """n buffers for the forward's padded z copy, or None when the backward reads z itself."""
+    """(n buffers for the forward's padded z copy, their size), or (None, 0) when the backward reads z itself."""
     nb = lib.dc_lowrank_zeff_bytes(B, T, D, R, W, dtype, int(has_static))
     _capi.check(int(nb) if nb < 0 else 0, "lowrank z_eff size query")
     if nb <= 0:
-        return None
-    return [torch.empty(nb, dtype=torch.uint8, device=device) for _ in range(n)]
+        return None, 0
+    return [torch.empty(nb, dtype=torch.uint8, device=device) for _ in range(n)], nb
 
 
 class _LowrankDynamicConvolutionFn(torch.autograd.Function):
@@ -35,15 +35,16 @@ class _LowrankDynamicConvolutionFn(torch.autograd.Function):
         y = torch.empty_like(x)
         lib = _capi.load()
         dtype = _capi.dtype_code(x.dtype)
-        zeff = _zeff_buffers(lib, 1, B, T, D, R, W, dtype, static_w is not None, x.device)
-        zeff = zeff[0] if zeff else None
+        zeffs, nzeff = _zeff_buffers(lib, 1, B, T, D, R, W, dtype, static_w is not None, x.device)
+        zeff = zeffs[0] if zeffs else None
         status = lib.dc_lowrank_fwd(
-            _capi.ptr(x), _capi.ptr(z), _capi.ptr(U), _capi.ptr(static_w), _capi.ptr(y), _capi.ptr(zeff),
+            _capi.ptr(x), _capi.ptr(z), _capi.ptr(U), _capi.ptr(static_w), _capi.ptr(y), _capi.ptr(zeff), nzeff,
             B, T, D, R, W, dtype, int(bool(residual)), _capi.stream_of(x),
         )
         _capi.check(status, "lowrank forward")
         ctx.save_for_backward(x, z, U, static_w)
         ctx.zeff = zeff  # internal buffer, a function of z: kept on ctx like the reference's padded z
+        ctx.nzeff = nzeff
         ctx.residual = bool(residual)
         return y
 
@@ -67,7 +68,8 @@ class _LowrankDynamicConvolutionFn(torch.autograd.Function):
         _capi.check(int(ws_bytes) if ws_bytes < 0 else 0, "lowrank backward workspace query")
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes > 0 else None
         status = lib.dc_lowrank_bwd(
-            _capi.ptr(x), _capi.ptr(z), _capi.ptr(U), _capi.ptr(static_w), _capi.ptr(ctx.zeff), _capi.ptr(dy),
+            _capi.ptr(x), _capi.ptr(z), _capi.ptr(U), _capi.ptr(static_w), _capi.ptr(ctx.zeff), ctx.nzeff,
+            _capi.ptr(dy),
             _capi.ptr(dx), _capi.ptr(dz), _capi.ptr(dU), _capi.ptr(dstatic_w), _capi.ptr(ws), ws_bytes,
             B, T, D, R, W, dtype, int(ctx.residual), _capi.stream_of(x),
         )
@@ -140,15 +142,15 @@ class _GroupedLowrankDynamicConvolutionFn(torch.autograd.Function):
         ys = [torch.empty(shape, dtype=x.dtype, device=x.device) for _ in range(G)]
         lib = _capi.load()
         dtype = _capi.dtype_code(x.dtype)
-        zeffs = _zeff_buffers(lib, G, B, T, D, R, W, dtype, has_static, x.device)
+        zeffs, nzeff = _zeff_buffers(lib, G, B, T, D, R, W, dtype, has_static, x.device)
         status = lib.dc_lowrank_fwd_grouped(
             G, _capi.ptr(x), x.stride(1), _capi.ptr_array(zs), _capi.ptr_array(Us), _capi.ptr_array(sws),
-            _capi.ptr_array(ys), _capi.ptr_array(zeffs), hd, B, T, D, R, W, dtype, int(bool(residual)),
+            _capi.ptr_array(ys), _capi.ptr_array(zeffs), nzeff, hd, B, T, D, R, W, dtype, int(bool(residual)),
             _capi.stream_of(x),
         )
         _capi.check(status, "grouped lowrank forward")
         ctx.save_for_backward(x, *params)
-        ctx.zeffs = zeffs
+        ctx.zeffs, ctx.nzeff = zeffs, nzeff
         ctx.G, ctx.has_static, ctx.residual, ctx.hd = G, has_static, bool(residual), hd
         return tuple(ys)
 
@@ -178,7 +180,7 @@ class _GroupedLowrankDynamicConvolutionFn(torch.autograd.Function):
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes > 0 else None
         status = lib.dc_lowrank_bwd_grouped(
             G, _capi.ptr(x), x.stride(1), _capi.ptr_array(zs), _capi.ptr_array(Us), _capi.ptr_array(sws),
-            _capi.ptr_array(ctx.zeffs), _capi.ptr_array(dys), hd, _capi.ptr(dx), C, _capi.ptr_array(dzs),
+            _capi.ptr_array(ctx.zeffs), ctx.nzeff, _capi.ptr_array(dys), hd, _capi.ptr(dx), C, _capi.ptr_array(dzs),
             _capi.ptr_array(dUs),
             _capi.ptr_array(dsws), _capi.ptr(ws), ws_bytes, B, T, D, R, W, dtype, int(ctx.residual),
             _capi.stream_of(x),

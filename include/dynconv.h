@@ -51,13 +51,15 @@
 extern "C" {
 #endif
 
-#define DC_ABI_VERSION 4
+#define DC_ABI_VERSION 5
 
-/* Largest convolution width and (kernel) rank accepted. */
-#define DC_MAX_W 8
+/* Largest convolution width and (kernel) rank accepted.  Widths up to 8 and
+ * kernel ranks up to 64 run on the vectorised / matrix-core kernels (subject
+ * to shape and alignment); the rest take the generic kernels. */
+#define DC_MAX_W 32
+#define DC_MAX_R 256
 /* Largest number of problems in one grouped lowrank call. */
 #define DC_MAX_GROUPS 4
-#define DC_MAX_R 64
 
 typedef enum dc_dtype {
   DC_DTYPE_BF16 = 0,
@@ -71,11 +73,20 @@ typedef enum dc_status {
   DC_ERR_SHAPE = -2,       /* a size <= 0, D % H != 0, or a size too large         */
   DC_ERR_DTYPE = -3,       /* dtype is not a dc_dtype                              */
   DC_ERR_UNSUPPORTED = -4, /* W > DC_MAX_W, R(+1) > DC_MAX_R, head_size too large  */
-  DC_ERR_WORKSPACE = -5,   /* workspace NULL or smaller than the size query        */
+  DC_ERR_WORKSPACE = -5,   /* workspace (or z_eff) NULL or below its size query    */
   DC_ERR_ALIGN = -6,       /* a pointer is not aligned to its element size          */
   DC_ERR_DEVICE = -7,      /* no HIP device available                               */
   DC_ERR_LAUNCH = -8       /* the HIP runtime rejected a kernel launch              */
 } dc_status;
+
+/* Kernel family a call of a given shape runs (dc_headwise_path, dc_lowrank_path). */
+typedef enum dc_path {
+  DC_PATH_GENERIC = 0,   /* one thread per output element (any shape; slow)        */
+  DC_PATH_VECTOR = 1,    /* headwise: 128-bit register-ring kernels                 */
+  DC_PATH_MFMA = 2,      /* lowrank bf16 / fp16: matrix-core kernels                */
+  DC_PATH_F32_MFMA = 3,  /* lowrank fp32: fp32 matrix-core kernels                  */
+  DC_PATH_F32_VALU = 4   /* lowrank fp32: vector-ALU kernels                        */
+} dc_path;
 
 /* DC_ABI_VERSION of the loaded library. */
 int dc_abi_version(void);
@@ -88,6 +99,13 @@ const char* dc_status_string(int status);
 int dc_headwise_fwd(const void* x, const void* weight, const void* static_w, void* y,
                     int64_t B, int64_t T, int64_t D, int64_t H, int64_t W,
                     int dtype, int residual, void* stream);
+
+/* The dc_path that dc_headwise_fwd (bwd = 0) or dc_headwise_bwd (bwd = 1)
+ * takes for these sizes with 256-byte aligned tensors, or a negative
+ * dc_status for invalid sizes.  No counterpart in the reference, whose
+ * autotuner picks among tile sizes of one kernel (headwise.py:8-23). */
+int dc_headwise_path(int64_t B, int64_t T, int64_t D, int64_t H, int64_t W, int dtype, int has_static,
+                     int bwd);
 
 /* Workspace bytes needed by dc_headwise_bwd for these sizes (>= 0), or a
  * negative dc_status for invalid sizes. */
@@ -115,21 +133,30 @@ int64_t dc_lowrank_zeff_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_
 /* y = lowrank dynamic convolution; the per-token weights z @ U (+ static_w as an
  * implicit extra rank with z == 1) are formed on chip and never written out.
  * Replaces lowrank.py:214-249.  R is the dynamic rank (z.shape[-1]).  z_eff is
- * NULL or a 16-byte aligned buffer of dc_lowrank_zeff_bytes bytes, which the
- * forward then fills for the backward (nothing happens when that size is 0). */
+ * NULL or a 16-byte aligned buffer of z_eff_bytes >= dc_lowrank_zeff_bytes(...)
+ * bytes (DC_ERR_WORKSPACE otherwise), which the forward then fills for the
+ * backward; when that size query is 0 the buffer is not used. */
 int dc_lowrank_fwd(const void* x, const void* z, const void* U, const void* static_w, void* y,
-                   void* z_eff, int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
-                   int dtype, int residual, void* stream);
+                   void* z_eff, int64_t z_eff_bytes, int64_t B, int64_t T, int64_t D, int64_t R,
+                   int64_t W, int dtype, int residual, void* stream);
+
+/* The dc_path that dc_lowrank_fwd (bwd = 0) or dc_lowrank_bwd (bwd = 1) takes
+ * for these sizes with contiguous, 256-byte aligned tensors, or a negative
+ * dc_status.  No counterpart in the reference (lowrank.py:14-23, 75-85 and
+ * 148-157 autotune tile sizes of one kernel each). */
+int dc_lowrank_path(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int has_static, int bwd);
 
 /* Workspace bytes needed by dc_lowrank_bwd, or a negative dc_status. */
 int64_t dc_lowrank_bwd_ws_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
                                 int dtype, int has_static);
 
 /* dx, dz, dU and (when static_w != NULL) dstatic_w from dy, in one pass over
- * x and dy.  Replaces lowrank.py:251-299.  z_eff is NULL or the buffer that
- * dc_lowrank_fwd filled for the same z and static_w presence. */
+ * x and dy.  Replaces lowrank.py:251-299.  z_eff is NULL or the buffer (of
+ * z_eff_bytes, checked as in dc_lowrank_fwd) that dc_lowrank_fwd filled for
+ * the same z and static_w presence; its contents are trusted, not checked. */
 int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* static_w,
-                   const void* z_eff, const void* dy, void* dx, void* dz, void* dU, void* dstatic_w,
+                   const void* z_eff, int64_t z_eff_bytes, const void* dy, void* dx, void* dz,
+                   void* dU, void* dstatic_w,
                    void* workspace, int64_t ws_bytes,
                    int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
                    int dtype, int residual, void* stream);
@@ -147,11 +174,12 @@ int dc_lowrank_bwd(const void* x, const void* z, const void* U, const void* stat
  * other head dims take the generic kernels (same tolerance).  Replaces the
  * three calls of README.md:57-110 (lowrank.py:302-338 each), the .contiguous()
  * copies of their inputs and the head transposes of their outputs.  z_eff is
- * NULL or an array of G buffers, each as z_eff of dc_lowrank_fwd. */
+ * NULL or an array of G buffers of z_eff_bytes each, as z_eff of dc_lowrank_fwd. */
 int dc_lowrank_fwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z,
                            const void* const* U, const void* const* static_w, void* const* y,
-                           void* const* z_eff, int64_t y_hd, int64_t B, int64_t T, int64_t D,
-                           int64_t R, int64_t W, int dtype, int residual, void* stream);
+                           void* const* z_eff, int64_t z_eff_bytes, int64_t y_hd, int64_t B,
+                           int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int residual,
+                           void* stream);
 
 /* Workspace bytes needed by dc_lowrank_bwd_grouped, or a negative dc_status. */
 int64_t dc_lowrank_bwd_grouped_ws_bytes(int64_t G, int64_t B, int64_t T, int64_t D, int64_t R,
@@ -166,11 +194,12 @@ int64_t dc_lowrank_bwd_grouped_ws_bytes(int64_t G, int64_t B, int64_t T, int64_t
  * is.  Per group, results are bitwise those of dc_lowrank_bwd (with a head
  * dim: when it is a multiple of 64, else the generic kernels).  Replaces
  * README.md:57-110's three backwards (lowrank.py:251-299 each) and the
- * concatenation of dq, dk, dv.  z_eff is NULL or the array of G buffers that
- * dc_lowrank_fwd_grouped filled. */
+ * concatenation of dq, dk, dv.  z_eff is NULL or the array of G buffers (of
+ * z_eff_bytes each) that dc_lowrank_fwd_grouped filled. */
 int dc_lowrank_bwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* const* z,
                            const void* const* U, const void* const* static_w,
-                           const void* const* z_eff, const void* const* dy, int64_t dy_hd,
+                           const void* const* z_eff, int64_t z_eff_bytes,
+                           const void* const* dy, int64_t dy_hd,
                            void* dx, int64_t dx_ld,
                            void* const* dz, void* const* dU, void* const* dstatic_w,
                            void* workspace, int64_t ws_bytes,

@@ -57,6 +57,117 @@ def assert_ns(a, b, dtype, name="", elementwise=True):
                                    atol=tol["atol"], rtol=tol["rtol"], msg=lambda m: f"{name}: {m}")
 
 
+# Per-entry bound for the long reductions (lowrank dU, dz, dstatic_w; headwise
+# dstatic_w) against b, the float64 sum of the terms formed from the same
+# dtype-rounded inputs:
+#     |a - b| <= k_in * L2 + k_acc * L1 + k_out * |b|
+# with L1 = sum |term| and L2 = sqrt(sum term^2), both in float64.
+#   k_in:  the per-term rounding before the sum.  The 16-bit lowrank backward
+#          rounds dy*x to the I/O type before its products (lowrank.py:128):
+#          relative errors of at most u = 2^-8 (bf16) / 2^-11 (fp16) whose
+#          standard deviation is below u/2, independent across terms, so their
+#          sum is bounded statistically by L2: k_in = 4u is over 7 standard
+#          deviations.  Headwise dstatic_w and fp32 have no such rounding.
+#   k_acc: fp32 accumulation, 2^-20 of L1 (sequential fp32 sums of 512 to
+#          131072 products stay within 1e-7 of L1, 10x below it).
+#   k_out: the final rounding to the output dtype, 2u.
+# A plausible kernel mistake fails it: a dropped 16-row tile of a 16384-row
+# bf16 reduction moves an entry by about 4 rms(term); the bound there is about
+# 2 rms(term) + |b| / 128.
+SUM_TOL = {
+    torch.bfloat16: dict(k_in=2.0**-6, k_acc=2.0**-20, k_out=2.0**-7),
+    torch.float16: dict(k_in=2.0**-9, k_acc=2.0**-20, k_out=2.0**-10),
+    torch.float32: dict(k_in=0.0, k_acc=2.0**-20, k_out=2.0**-23),
+}
+
+
+def assert_sum(a, ref, dtype, name, rounded_terms=True):
+    """Per-entry check of a long reduction `a` against ref = (b, L1, L2) (float64, CPU; see SUM_TOL)."""
+    b, l1, l2 = ref
+    t = SUM_TOL[dtype]
+    a = a.detach().double().cpu().reshape(b.shape)
+    k_in = t["k_in"] if rounded_terms else 0.0
+    bound = k_in * l2 + t["k_acc"] * l1 + t["k_out"] * b.abs()
+    err = (a - b).abs()
+    ratio = err / bound.clamp_min(1e-300)
+    worst = ratio.max().item()
+    if not worst <= 1.0:
+        i = int(ratio.argmax())
+        idx = [int(v) for v in torch.unravel_index(torch.tensor(i), b.shape)]
+        raise AssertionError(
+            f"{name}: |a-b| above the per-entry bound at {idx}: a={a.flatten()[i].item():.6g} "
+            f"b={b.flatten()[i].item():.6g} bound={bound.flatten()[i].item():.3g} (err/bound {worst:.3g}; "
+            f"{int((ratio > 1).sum())} of {ratio.numel()} entries)")
+
+
+def _shift(x, k):
+    if k == 0:
+        return x
+    out = torch.zeros_like(x)
+    out[:, k:] = x[:, :-k]
+    return out
+
+
+def _sum3(parts):
+    """(sum, L1, L2) of a list of (sum, L1, sum of squares) triples."""
+    s = sum(p[0] for p in parts)
+    return s, sum(p[1] for p in parts), torch.sqrt(sum(p[2] for p in parts))
+
+
+def dstatic_sums(x, dy, W):
+    """(b, L1, L2) of dstatic_w[k, d] = sum_{b,t} dy[b,t,d] x[b,t-k,d], float64 (inputs: rounded, CPU)."""
+    x64, dy64 = x.detach().double().cpu(), dy.detach().double().cpu()
+    rows = []
+    for k in range(W):
+        g = dy64 * _shift(x64, k)
+        rows.append((g.sum((0, 1)), g.abs().sum((0, 1)), (g * g).sum((0, 1))))
+    return (torch.stack([r[0] for r in rows]), torch.stack([r[1] for r in rows]),
+            torch.sqrt(torch.stack([r[2] for r in rows])))
+
+
+def lowrank_sums(x, z, U, dy):
+    """(b, L1, L2) of the lowrank backward's reductions, float64 on the CPU from the rounded inputs:
+    dU[r, kD+d] = sum_{b,t} z[b,t,r] G_k[b,t,d] and dz[b,t,r] = sum_{k,d} G_k[b,t,d] U[r, kD+d], where
+    G_k = dy * x shifted by k rows (reference.py:23-39 differentiated)."""
+    x64, dy64 = x.detach().double().cpu(), dy.detach().double().cpu()
+    z64, U64 = z.detach().double().cpu(), U.detach().double().cpu()
+    Bn, Tn, Dn = x64.shape
+    R = z64.shape[-1]
+    W = U64.shape[1] // Dn
+    zf = z64.reshape(-1, R)
+    dU, dz = [], []
+    for k in range(W):
+        G = (dy64 * _shift(x64, k)).reshape(-1, Dn)
+        Ga, G2 = G.abs(), G * G
+        dU.append((zf.t() @ G, zf.abs().t() @ Ga, (zf * zf).t() @ G2))
+        Uk = U64[:, k * Dn:(k + 1) * Dn]
+        dz.append((G @ Uk.t(), Ga @ Uk.abs().t(), G2 @ (Uk * Uk).t()))
+        del G, Ga, G2
+    dU = tuple(torch.cat([p[i] for p in dU], dim=1) for i in range(3))
+    dU = (dU[0], dU[1], torch.sqrt(dU[2]))
+    dz = _sum3(dz)
+    return {"dU": dU, "dz": tuple(t.reshape(Bn, Tn, R) for t in dz)}
+
+
+def check_reductions(kind, src_q, dyq, grads, dtype, tag=""):
+    """Per-entry bounds (assert_sum) on the long reductions of one case: headwise ("hw") dstatic_w,
+    lowrank ("lr") dz, dU and dstatic_w.  src_q: the dtype-rounded inputs (fp32, CPU) in the
+    operator's argument order; grads: the kernel's gradients in the same order."""
+    x = src_q[0]
+    if kind == "hw":
+        W = src_q[1].shape[-1]
+        if src_q[2] is not None:
+            assert_sum(grads[2], dstatic_sums(x, dyq, W), dtype, tag + "dstatic_w", rounded_terms=False)
+        return
+    z, U, sw = src_q[1], src_q[2], src_q[3]
+    ref = lowrank_sums(x, z, U, dyq)
+    assert_sum(grads[1], ref["dz"], dtype, tag + "dz")
+    assert_sum(grads[2], ref["dU"], dtype, tag + "dU")
+    if sw is not None:
+        W = U.shape[1] // x.shape[-1]
+        assert_sum(grads[3], dstatic_sums(x, dyq, W), dtype, tag + "dstatic_w")
+
+
 def run_fwd_bwd(fn, inputs, dy, residual):
     """Run fn(*inputs) forward+backward; return (y, [grads]) (grads None for None inputs)."""
     leaves = [t.detach().clone().requires_grad_() if t is not None else None for t in inputs]

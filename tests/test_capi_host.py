@@ -35,7 +35,7 @@ def header_functions():
 
 def test_exports_every_declared_symbol(lib):
     names = header_functions()
-    assert len(names) == 12, names
+    assert len(names) == 14, names
     raw = ctypes.CDLL(_capi.LIB_PATH)
     for n in names:
         assert hasattr(raw, n), f"{n} declared in dynconv.h but not exported"
@@ -43,7 +43,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_strings(lib):
-    assert lib.dc_abi_version() == 4
+    assert lib.dc_abi_version() == 5
     for s in (OK, E_NULL, E_SHAPE, E_DTYPE, E_UNSUP, E_WS, E_ALIGN, E_DEV, E_LAUNCH):
         assert len(lib.dc_status_string(s)) > 0
     assert b"unknown" in lib.dc_status_string(-99)
@@ -60,7 +60,7 @@ def test_headwise_fwd_validation(lib):
     assert hw_fwd(lib, T=-1) == E_SHAPE
     assert hw_fwd(lib, H=3) == E_SHAPE           # 16 % 3 != 0
     assert hw_fwd(lib, H=0) == E_SHAPE
-    assert hw_fwd(lib, W=9) == E_UNSUP           # > DC_MAX_W
+    assert hw_fwd(lib, W=33) == E_UNSUP          # > DC_MAX_W
     assert hw_fwd(lib, T=1 << 31) == E_SHAPE     # int32 row indexing bound
     assert hw_fwd(lib, x=None) == E_NULL
     assert hw_fwd(lib, y=None) == E_NULL
@@ -69,6 +69,7 @@ def test_headwise_fwd_validation(lib):
     if no_dev:
         assert hw_fwd(lib) == E_DEV
         assert hw_fwd(lib, sw=P, res=1, W=1) == E_DEV
+        assert hw_fwd(lib, W=32) == E_DEV         # widths above 8 take the generic kernels
 
 
 def hw_bwd(lib, sw=None, dsw=None, ws=None, nws=0, B=2, T=8, D=16, H=4, W=4, dt=0, dy=P):
@@ -93,20 +94,23 @@ def test_headwise_bwd_validation(lib):
         assert hw_bwd(lib, sw=P, dsw=P, ws=P, nws=need) == E_DEV
 
 
-def lr_fwd(lib, x=P, z=P, U=P, sw=None, zeff=None, B=2, T=8, D=16, R=4, W=4, dt=0):
-    return lib.dc_lowrank_fwd(x, z, U, sw, P, zeff, B, T, D, R, W, dt, 0, None)
+def lr_fwd(lib, x=P, z=P, U=P, sw=None, zeff=None, nzeff=1 << 20, B=2, T=8, D=16, R=4, W=4, dt=0):
+    return lib.dc_lowrank_fwd(x, z, U, sw, P, zeff, nzeff, B, T, D, R, W, dt, 0, None)
 
 
 def test_lowrank_validation(lib):
     no_dev = not torch.cuda.is_available()
     assert lr_fwd(lib, dt=-1) == E_DTYPE
     assert lr_fwd(lib, R=0) == E_SHAPE
-    assert lr_fwd(lib, R=64, sw=P) == E_UNSUP    # kernel rank 65 > DC_MAX_R
-    assert lr_fwd(lib, R=65) == E_UNSUP
+    assert lr_fwd(lib, R=256, sw=P) == E_UNSUP   # kernel rank 257 > DC_MAX_R
+    assert lr_fwd(lib, R=257) == E_UNSUP
+    assert lr_fwd(lib, W=33) == E_UNSUP
     assert lr_fwd(lib, W=0) == E_SHAPE
     assert lr_fwd(lib, z=None) == E_NULL
     assert lr_fwd(lib, U=P + 1) == E_ALIGN
     assert lr_fwd(lib, zeff=P + 8) == E_ALIGN      # the padded z copy: 16-byte aligned
+    # a padded z copy shorter than its size query (R 3 + static: 2*8 rows of 4 ranks)
+    assert lr_fwd(lib, R=3, sw=P, zeff=P, nzeff=2 * 8 * 4 * 2 - 2) == E_WS
     # the padded z copy the backward would build: none when z's own rows serve (R % 4 == 0,
     # or 32 dynamic ranks for two rank chunks), else B*T rows of 4*k (one chunk) or 32 ranks
     zb = lib.dc_lowrank_zeff_bytes
@@ -121,22 +125,27 @@ def test_lowrank_validation(lib):
     assert zb(2, 8, 16, 0, 4, 0, 1) == E_SHAPE
     need = lib.dc_lowrank_bwd_ws_bytes(2, 8, 16, 4, 4, 0, 1)
     assert need > 0
-    assert lib.dc_lowrank_bwd_ws_bytes(2, 8, 16, 4, 9, 0, 1) == E_UNSUP
-    st = lib.dc_lowrank_bwd(P, P, P, P, None, P, P, P, P, P, None, 0, 2, 8, 16, 4, 4, 0, 0, None)
-    assert st == E_WS
-    st = lib.dc_lowrank_bwd(P, P, P, P, None, P, P, P, P, P, P + 8, need, 2, 8, 16, 4, 4, 0, 0, None)
-    assert st == E_WS  # workspace below 16-byte alignment
-    st = lib.dc_lowrank_bwd(P, P, P, None, None, P, P, P, P, P, P, need, 2, 8, 16, 4, 4, 0, 0, None)
-    assert st == E_NULL
-    st = lib.dc_lowrank_bwd(P, P, P, P, P + 8, P, P, P, P, P, P, need, 2, 8, 16, 4, 4, 0, 0, None)
-    assert st == E_ALIGN  # the padded z copy below 16-byte alignment
+    assert lib.dc_lowrank_bwd_ws_bytes(2, 8, 16, 4, 33, 0, 1) == E_UNSUP
+    assert lib.dc_lowrank_bwd_ws_bytes(2, 8, 16, 127, 12, 0, 1) > 0   # generic kernels: W 12, kernel rank 128
+
+    def bwd(zeff=None, nzeff=0, ws=P, nws=need, sw=P, R=4):
+        return lib.dc_lowrank_bwd(P, P, P, sw, zeff, nzeff, P, P, P, P, sw, ws, nws, 2, 8, 16, R, 4, 0, 0, None)
+
+    assert bwd(ws=None, nws=0) == E_WS
+    assert bwd(ws=P + 8) == E_WS  # workspace below 16-byte alignment
+    assert lib.dc_lowrank_bwd(P, P, P, None, None, 0, P, P, P, P, P, P, need, 2, 8, 16, 4, 4, 0, 0, None) == E_NULL
+    assert bwd(zeff=P + 8, nzeff=1 << 20) == E_ALIGN  # the padded z copy below 16-byte alignment
+    need3 = lib.dc_lowrank_bwd_ws_bytes(2, 8, 16, 3, 4, 0, 1)
+    nz3 = zb(2, 8, 16, 3, 4, 0, 1)
+    assert bwd(zeff=P, nzeff=nz3 - 1, R=3, nws=need3) == E_WS  # padded z copy below its size query
     if no_dev:
         assert lr_fwd(lib) == E_DEV
         assert lr_fwd(lib, R=3, sw=P, zeff=P) == E_DEV
-        st = lib.dc_lowrank_bwd(P, P, P, P, None, P, P, P, P, P, P, need, 2, 8, 16, 4, 4, 0, 0, None)
-        assert st == E_DEV
-        st = lib.dc_lowrank_bwd(P, P, P, P, P, P, P, P, P, P, P, need, 2, 8, 16, 3, 4, 0, 0, None)
-        assert st == E_DEV
+        assert lr_fwd(lib, R=3, sw=P, zeff=P, nzeff=nz3) == E_DEV
+        assert lr_fwd(lib, R=4, zeff=P, nzeff=0) == E_DEV   # no copy for this shape: the buffer is not used
+        assert lr_fwd(lib, R=127, sw=P, W=12) == E_DEV      # generic kernels
+        assert bwd() == E_DEV
+        assert bwd(zeff=P, nzeff=nz3, R=3, nws=need3) == E_DEV
 
 
 def arr(*ptrs):
@@ -144,12 +153,12 @@ def arr(*ptrs):
     return (ctypes.c_void_p * len(ptrs))(*ptrs)
 
 
-def lr_fwd_g(lib, G=3, x=P, x_ld=48, z="ok", U="ok", sw=None, y="ok", zeff=None, y_hd=0, B=2, T=8, D=16, R=4, W=4,
-             dt=0):
+def lr_fwd_g(lib, G=3, x=P, x_ld=48, z="ok", U="ok", sw=None, y="ok", zeff=None, nzeff=1 << 20, y_hd=0, B=2, T=8,
+             D=16, R=4, W=4, dt=0):
     z = arr(*[P] * G) if z == "ok" else z
     U = arr(*[P] * G) if U == "ok" else U
     y = arr(*[P] * G) if y == "ok" else y
-    return lib.dc_lowrank_fwd_grouped(G, x, x_ld, z, U, sw, y, zeff, y_hd, B, T, D, R, W, dt, 0, None)
+    return lib.dc_lowrank_fwd_grouped(G, x, x_ld, z, U, sw, y, zeff, nzeff, y_hd, B, T, D, R, W, dt, 0, None)
 
 
 def test_lowrank_grouped_fwd_validation(lib):
@@ -159,7 +168,7 @@ def test_lowrank_grouped_fwd_validation(lib):
     assert lr_fwd_g(lib, x_ld=47) == E_SHAPE               # rows narrower than G*D
     assert lr_fwd_g(lib, x_ld=1 << 31) == E_SHAPE
     assert lr_fwd_g(lib, dt=9) == E_DTYPE
-    assert lr_fwd_g(lib, W=9) == E_UNSUP
+    assert lr_fwd_g(lib, W=33) == E_UNSUP
     assert lr_fwd_g(lib, x=None) == E_NULL
     assert lr_fwd_g(lib, z=None) == E_NULL
     assert lr_fwd_g(lib, y=arr(P, None, P)) == E_NULL      # a NULL entry
@@ -167,6 +176,7 @@ def test_lowrank_grouped_fwd_validation(lib):
     assert lr_fwd_g(lib, U=arr(P, P + 1, P)) == E_ALIGN
     assert lr_fwd_g(lib, zeff=arr(P, None, P)) == E_NULL    # padded z copies for every group or none
     assert lr_fwd_g(lib, zeff=arr(P, P + 8, P)) == E_ALIGN
+    assert lr_fwd_g(lib, R=3, sw=arr(P, P, P), zeff=arr(P, P, P), nzeff=2 * 8 * 4 * 2 - 1) == E_WS
     assert lr_fwd_g(lib, x=P + 1) == E_ALIGN
     assert lr_fwd_g(lib, y_hd=-1) == E_SHAPE               # head dims: D % y_hd == 0, y_hd <= D
     assert lr_fwd_g(lib, y_hd=5) == E_SHAPE
@@ -188,9 +198,10 @@ def test_lowrank_grouped_bwd_validation(lib):
     assert lib.dc_lowrank_bwd_grouped_ws_bytes(3, 2, 8, 16, 0, 4, 0, 1) == E_SHAPE
     g3 = arr(P, P, P)
 
-    def call(G=3, x_ld=48, dx_ld=48, sw=None, dsw=None, ws=P, nws=need, dz=g3, dy=g3, dy_hd=0, zeff=None):
-        return lib.dc_lowrank_bwd_grouped(G, P, x_ld, g3, g3, sw, zeff, dy, dy_hd, P, dx_ld, dz, g3, dsw, ws, nws,
-                                          2, 8, 16, 4, 4, 0, 0, None)
+    def call(G=3, x_ld=48, dx_ld=48, sw=None, dsw=None, ws=P, nws=need, dz=g3, dy=g3, dy_hd=0, zeff=None,
+             nzeff=1 << 20, R=4):
+        return lib.dc_lowrank_bwd_grouped(G, P, x_ld, g3, g3, sw, zeff, nzeff, dy, dy_hd, P, dx_ld, dz, g3, dsw, ws,
+                                          nws, 2, 8, 16, R, 4, 0, 0, None)
 
     assert call(G=5) == E_UNSUP
     assert call(dx_ld=40) == E_SHAPE
@@ -201,6 +212,8 @@ def test_lowrank_grouped_bwd_validation(lib):
     assert call(dy=None) == E_NULL
     assert call(zeff=arr(P, P, None)) == E_NULL
     assert call(zeff=arr(P + 8, P, P)) == E_ALIGN
+    need3 = lib.dc_lowrank_bwd_grouped_ws_bytes(3, 2, 8, 16, 3, 4, 0, 1)
+    assert call(R=3, sw=g3, dsw=g3, nws=need3, zeff=g3, nzeff=2 * 8 * 4 * 2 - 1) == E_WS
     assert call(sw=g3, dsw=g3, ws=None) == E_WS
     assert call(sw=g3, dsw=g3, nws=need - 256) == E_WS
     assert call(sw=g3, dsw=g3, ws=P + 16) == E_WS           # workspace shares start 256-byte aligned
@@ -209,3 +222,29 @@ def test_lowrank_grouped_bwd_validation(lib):
     if no_dev:
         assert call(sw=g3, dsw=g3) == E_DEV
         assert call(sw=g3, dsw=g3, dy_hd=8) == E_DEV
+
+
+def test_kernel_paths(lib):
+    """dc_headwise_path / dc_lowrank_path: the kernel family each BASELINE shape and a few edge shapes
+    take (0 generic, 1 vector, 2 matrix cores, 3 fp32 matrix cores, 4 fp32 VALU); host logic only."""
+    bf, f16, f32 = 0, 1, 2
+    hp, lp = lib.dc_headwise_path, lib.dc_lowrank_path
+    for bwd in (0, 1):
+        assert hp(2, 1024, 512, 512, 4, f32, 0, bwd) == 1      # configs[0]
+        assert hp(4, 4096, 2048, 2048, 4, bf, 1, bwd) == 1     # configs[1]
+        assert hp(4, 4096, 2048, 64, 4, bf, 1, bwd) == 1       # configs[2]
+        assert lp(4, 4096, 2048, 16, 4, bf, 0, bwd) == 2       # configs[3]
+        assert lp(2, 8192, 4096, 31, 4, bf, 1, bwd) == 2       # configs[4]
+        assert lp(4, 4096, 2048, 16, 4, f32, 0, bwd) == 3      # the fp32 tier on matrix cores
+        assert hp(1, 40, 2048, 2, 4, bf, 1, bwd) == 0          # head size 1024: generic
+        assert hp(1, 50, 64, 16, 12, bf, 1, bwd) == 0          # W 12: generic
+        assert lp(1, 45, 64, 127, 12, bf, 1, bwd) == 0         # W 12, kernel rank 128: generic
+        assert lp(1, 70, 128, 64, 1, bf, 0, bwd) == 2          # kernel rank 64, W 1
+        assert lp(1, 40, 128, 40, 2, f16, 0, bwd) == 2         # kernel rank 40, W 2
+    assert lp(1, 300, 64, 1, 1, f32, 0, 0) == 3                # fp32 W 1: forward on fp32 matrix cores,
+    assert lp(1, 300, 64, 1, 1, f32, 0, 1) == 4                # backward on the VALU kernels
+    assert lp(2, 50, 256, 63, 2, bf, 1, 0) == 2                # kernel rank 64, W 2: forward on matrix cores,
+    assert lp(2, 50, 256, 63, 2, bf, 1, 1) == 0                # the backward's LDS would exceed 160 KiB
+    assert hp(2, 8, 16, 3, 4, bf, 0, 0) == E_SHAPE
+    assert lp(2, 8, 16, 0, 4, bf, 0, 0) == E_SHAPE
+    assert lp(2, 8, 16, 4, 33, bf, 0, 1) == E_UNSUP

@@ -22,7 +22,7 @@ import math
 import pytest
 import torch
 
-from helpers import assert_ns, gen, randn, uniform
+from helpers import assert_ns, check_reductions, gen, randn, uniform
 from oracle.reference_cpu import lowrank_dynamic_convolution_ref as lr_ref
 import lowrank as lr_mod
 
@@ -86,6 +86,9 @@ def test_grouped_against_oracle(G, Bn, Tn, Dn, R, W, static, extra, dtype):
         assert_ns(Uk[g].grad, Ur.grad, dtype, f"g{g} dU", elementwise=False)
         if static:
             assert_ns(sk[g].grad, sr.grad, dtype, f"g{g} dstatic_w", elementwise=False)
+        check_reductions("lr", [xs.detach(), zr.detach(), Ur.detach(), None if sr is None else sr.detach()],
+                         dys[g].to(dtype).float(), [None, zk[g].grad, Uk[g].grad, sk[g].grad if static else None],
+                         dtype, tag=f"g{g} ")
 
 
 @pytest.mark.parametrize("static", [False, True])
@@ -190,10 +193,19 @@ def test_readme_module_against_oracle():
     with torch.no_grad():
         m.proj_out.normal_(0, 1 / math.sqrt((R + 1) * W))
     x = torch.randn(Bn, Tn, Dm, device=DEV, dtype=dtype, requires_grad=True)
-    pre_z = torch.randn(Bn, Tn, Dm, device=DEV, dtype=dtype)
+    pre_z = torch.randn(Bn, Tn, Dm, device=DEV, dtype=dtype, requires_grad=True)
     dy = torch.randn(Bn, Tn, Dm, device=DEV, dtype=dtype)
     y = m(x, pre_z)
     y.backward(dy)
+    # the whole module in fp32 on the CPU: z = pre_z @ W_in^T unrounded (proj_in and pre_z gradients)
+    pz = pre_z.detach().float().cpu().requires_grad_()
+    wi = m.proj_in.weight.detach().float().cpu().requires_grad_()
+    y_full = lr_ref(x.detach().float().cpu(), pz @ wi.t(), m.proj_out.detach().float().cpu(),
+                    m.proj_out_bias.detach().float().cpu(), residual=True)
+    y_full.backward(dy.float().cpu())
+    assert_ns(y, y_full, dtype, "y (fp32 z)")
+    assert_ns(m.proj_in.weight.grad, wi.grad, dtype, "proj_in", elementwise=False)
+    assert_ns(pre_z.grad, pz.grad, dtype, "d pre_z", elementwise=False)
     # oracle: the same bf16 z (torch's GEMM), then the fp32 restatement of reference.py
     z = m.proj_in(pre_z).detach()
     xr = x.detach().float().cpu().requires_grad_()
@@ -206,6 +218,52 @@ def test_readme_module_against_oracle():
     assert_ns(x.grad, xr.grad, dtype, "dx")
     assert_ns(m.proj_out.grad, Ur.grad, dtype, "dU", elementwise=False)
     assert_ns(m.proj_out_bias.grad, sr.grad, dtype, "dstatic_w", elementwise=False)
+
+
+@pytest.mark.parametrize("head_dim", [None, 64])
+def test_grouped_module_against_oracle(head_dim):
+    """GroupedLowRankDynamicShortConvolution end to end against an fp32 CPU oracle of the whole module:
+    z = pre_z @ proj_in.weight^T in fp32, then reference.py's lowrank operator per group on its slice of
+    the fused q|k|v projection (README.md:57-83, 99-110).  Every gradient: the fused projection x, pre_z,
+    proj_in.weight, proj_out and proj_out_bias.  The kernel path rounds z to bf16 after torch's GEMM;
+    the oracle keeps it in fp32, so the checks are the north-star ones (2e-2)."""
+    from dynconv import GroupedLowRankDynamicShortConvolution
+
+    torch.manual_seed(3)
+    Dm, R, W, G, Bn, Tn = 256, 15, 4, 3, 2, 96
+    dtype = torch.bfloat16
+    m = GroupedLowRankDynamicShortConvolution(Dm, R, W, groups=G, head_dim=head_dim).to(DEV, dtype)
+    with torch.no_grad():
+        m.proj_out.normal_(0, 1 / math.sqrt((R + 1) * W))  # the README initialises U to zero
+    qkv = torch.randn(Bn, Tn, G * Dm, device=DEV, dtype=dtype, requires_grad=True)
+    pre_z = torch.randn(Bn, Tn, Dm, device=DEV, dtype=dtype, requires_grad=True)
+    dys = [torch.randn(Bn, Tn, Dm, device=DEV, dtype=dtype) for _ in range(G)]
+    outs = m(qkv, pre_z)
+    if head_dim is None:
+        torch.autograd.backward(outs, dys)
+    else:
+        H = Dm // head_dim
+        torch.autograd.backward(outs, [d.view(Bn, Tn, H, head_dim).transpose(1, 2).contiguous() for d in dys])
+        outs = [o.transpose(1, 2).reshape(Bn, Tn, Dm) for o in outs]
+    torch.cuda.synchronize()
+
+    def cpu_leaf(t):
+        return t.detach().float().cpu().requires_grad_()
+
+    xr, pzr = cpu_leaf(qkv), cpu_leaf(pre_z)
+    win, uo, sb = cpu_leaf(m.proj_in.weight), cpu_leaf(m.proj_out), cpu_leaf(m.proj_out_bias)
+    z = pzr @ win.t()  # [B, T, G*R] in fp32
+    outs_r = [lr_ref(xr[..., g * Dm:(g + 1) * Dm], z[..., g * R:(g + 1) * R], uo[g], sb[g], residual=True)
+              for g in range(G)]
+    torch.autograd.backward(outs_r, [d.float().cpu() for d in dys])
+    for g in range(G):
+        assert_ns(outs[g], outs_r[g], dtype, f"g{g} y")
+        assert_ns(m.proj_out.grad[g], uo.grad[g], dtype, f"g{g} proj_out", elementwise=False)
+        assert_ns(m.proj_out_bias.grad[g], sb.grad[g], dtype, f"g{g} proj_out_bias", elementwise=False)
+        assert_ns(m.proj_in.weight.grad[g * R:(g + 1) * R], win.grad[g * R:(g + 1) * R], dtype, f"g{g} proj_in",
+                  elementwise=False)
+    assert_ns(qkv.grad, xr.grad, dtype, "d qkv")
+    assert_ns(pre_z.grad, pzr.grad, dtype, "d pre_z", elementwise=False)
 
 
 # ------------------------------------------------------ head-major outputs
@@ -267,6 +325,9 @@ def test_grouped_head_major(G, Bn, Tn, Dn, R, W, static, hd, dtype, bitwise):
         assert_ns(dU_h[g], Ur.grad, dtype, f"g{g} dU", elementwise=False)
         if static:
             assert_ns(ds_h[g], sr.grad, dtype, f"g{g} dstatic_w", elementwise=False)
+        check_reductions("lr", [xs.detach(), zr.detach(), Ur.detach(), None if sr is None else sr.detach()],
+                         dys[g].to(dtype).float(), [None, dz_h[g], dU_h[g], ds_h[g] if static else None], dtype,
+                         tag=f"g{g} ")
 
 
 def test_module_head_major():

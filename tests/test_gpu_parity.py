@@ -26,7 +26,8 @@ import zlib
 import pytest
 import torch
 
-from helpers import REF_TOL, assert_ns, gen, max_rel, randn, run_fwd_bwd, uniform
+from helpers import (REF_TOL, assert_ns, assert_sum, check_reductions, dstatic_sums, gen, lowrank_sums, max_rel,
+                     randn, run_fwd_bwd, uniform)
 from oracle.reference_cpu import (
     headwise_dynamic_convolution_ref as hw_ref,
     lowrank_dynamic_convolution_ref as lr_ref,
@@ -50,7 +51,7 @@ def _f32cpu(t):
     return None if t is None else t.detach().float().cpu()
 
 
-def _check_case(kernel, ref, src, dy, dtype, residual, names, local):
+def _check_case(kernel, ref, src, dy, dtype, residual, names, local, kind):
     """Run both criteria for one case.  src: fp32 CPU tensors (None allowed)."""
     # 1. test.py criterion
     atol, rtol = REF_TOL[dtype]
@@ -66,6 +67,8 @@ def _check_case(kernel, ref, src, dy, dtype, residual, names, local):
     for a, b, n in zip(g_k, g_q, names):
         if b is not None:
             assert_ns(a, b, dtype, n, elementwise=n in local)
+    # 3. per-entry bounds on the long reductions (float64 sums of the same rounded terms)
+    check_reductions(kind, src_q, dy.to(dtype).float(), [None] + g_k[1:], dtype)
 
 
 # ----------------------------------------------------------- test.py sweep
@@ -84,14 +87,15 @@ def test_reference_sweep(dtype, residual, W, kind, static):
     if kind.startswith("hw"):
         hs = int(kind[2:])
         w = randn(g, B, T, D // hs, W, scale=0.1)
-        _check_case(hw, hw_ref, [x, w, sw], dy, dtype, residual, ["dx", "dweight", "dstatic_w"], {"dx", "dweight"})
+        _check_case(hw, hw_ref, [x, w, sw], dy, dtype, residual, ["dx", "dweight", "dstatic_w"], {"dx", "dweight"},
+                    "hw")
     else:
         R = 16
         z = randn(g, B, T, R, scale=0.1 / R**0.5)
         U = randn(g, R, W * D)
         if static:
             z, U = z[..., :-1].contiguous(), U[:-1].contiguous()
-        _check_case(lr, lr_ref, [x, z, U, sw], dy, dtype, residual, ["dx", "dz", "dU", "dstatic_w"], {"dx"})
+        _check_case(lr, lr_ref, [x, z, U, sw], dy, dtype, residual, ["dx", "dz", "dU", "dstatic_w"], {"dx"}, "lr")
 
 
 # -------------------------------------------------------------- edge shapes
@@ -125,12 +129,19 @@ HW_EDGE = [
     (1, 260, 256, 256, 2, False, True, torch.float32),  # hs 1 fp32, W 2: NP 2
     (2, 181, 512, 256, 4, True, False, torch.bfloat16), # hs 2, W 4: NP 2
     (1, 333, 1024, 1024, 4, True, True, torch.bfloat16),  # hs 1, W 4: NP 4, two wavefront columns
+    # widths above 8 (the generic kernels; the reference accepts any W, headwise.py:226)
+    (1, 50, 64, 16, 12, True, True, torch.bfloat16),   # W 12
+    (2, 40, 128, 128, 16, True, False, torch.float32),  # W 16, head size 1
+    (1, 10, 64, 32, 32, True, True, torch.bfloat16),   # W 32 (the maximum) > T
 ]
 
 
 @pytest.mark.parametrize("Bn,Tn,Dn,H,W,static,residual,dtype", HW_EDGE)
 def test_edge_shapes_headwise(Bn, Tn, Dn, H, W, static, residual, dtype):
     g = gen(Bn * 1000003 + Tn * 1009 + Dn * 7 + H + W)
+    want = "vector" if W <= 8 and _hw_vector_shape(Dn, H, dtype) else "generic"
+    for bwd in (0, 1):
+        assert _path("hw", Bn, Tn, Dn, H, W, dtype, static, bwd) == want
     x = randn(g, Bn, Tn, Dn)
     dy = randn(g, Bn, Tn, Dn)
     w = randn(g, Bn, Tn, H, W, scale=1 / math.sqrt(W))
@@ -143,10 +154,30 @@ def test_edge_shapes_headwise(Bn, Tn, Dn, H, W, static, residual, dtype):
     for a, b, n in zip(g_k, g_q, ["dx", "dweight", "dstatic_w"]):
         if b is not None:
             assert_ns(a, b, dtype, n, elementwise=n != "dstatic_w")
+    check_reductions("hw", src_q, dy.to(dtype).float(), g_k, dtype)
+
+
+def _hw_vector_shape(Dn, H, dtype):
+    """Shapes the headwise vector kernels take (contiguous, aligned tensors): D a multiple of the
+    16-byte lane width, a power-of-two head size of at most 64 lanes."""
+    vec = 16 // torch.tensor([], dtype=dtype).element_size()
+    hs = Dn // H
+    return Dn % vec == 0 and hs & (hs - 1) == 0 and hs <= 64 * vec
+
+
+def _path(kind, Bn, Tn, Dn, HR, W, dtype, static, bwd):
+    """Kernel family (dc_headwise_path / dc_lowrank_path) a call of this shape runs on."""
+    from dynconv import _capi
+
+    lib = _capi.load()
+    fn = lib.dc_headwise_path if kind == "hw" else lib.dc_lowrank_path
+    code = fn(Bn, Tn, Dn, HR, W, _capi.dtype_code(dtype), int(static), bwd)
+    assert code >= 0, _capi.status_string(code)
+    return _capi.PATHS[code]
 
 
 LR_EDGE = [
-    # B, T, D, R, W, static, residual, dtype
+    # B, T, D, R, W, static, residual, dtype, (forward, backward) kernel family
     (1, 37, 256, 16, 3, False, True, torch.bfloat16),
     (2, 70, 128, 31, 4, True, True, torch.bfloat16),    # kernel rank 32
     (1, 64, 256, 32, 2, False, False, torch.bfloat16),
@@ -168,11 +199,25 @@ LR_EDGE = [
     (2, 300, 64, 1, 1, False, True, torch.float32),     # rank 1, W 1
     (1, 9, 100, 7, 4, False, True, torch.float32),      # T below one run, D % 64 != 0
     (1, 40, 64, 40, 4, False, False, torch.float32),    # kernel rank 40: generic kernels
+    # matrix-core plans with three and four rank chunks (kernel ranks 33-64 at W 1-2)
+    (1, 70, 128, 64, 1, False, True, torch.bfloat16, ("mfma", "mfma")),      # <W1, 4 chunks>
+    (2, 50, 256, 63, 2, True, True, torch.bfloat16, ("mfma", "generic")),    # <W2, 4 chunks> forward only
+    (1, 40, 128, 40, 2, False, False, torch.float16, ("mfma", "mfma")),      # <W2, 3 chunks>
+    (2, 60, 128, 40, 1, True, True, torch.bfloat16, ("mfma", "mfma")),       # <W1, 3 chunks>, kernel rank 41
+    # widths above 8 and kernel ranks above 64 (the generic kernels; the reference accepts any
+    # W and power-of-two ranks, lowrank.py:220, 331-333)
+    (1, 45, 64, 127, 12, True, True, torch.bfloat16, ("generic", "generic")),  # W 12, kernel rank 128
+    (1, 30, 32, 255, 3, True, False, torch.float32, ("generic", "generic")),   # kernel rank 256 (the maximum)
+    (1, 9, 64, 8, 16, False, True, torch.bfloat16, ("generic", "generic")),    # W 16 > T
 ]
 
 
-@pytest.mark.parametrize("Bn,Tn,Dn,R,W,static,residual,dtype", LR_EDGE)
-def test_edge_shapes_lowrank(Bn, Tn, Dn, R, W, static, residual, dtype):
+@pytest.mark.parametrize("case", LR_EDGE, ids=[f"lr{i}" for i in range(len(LR_EDGE))])
+def test_edge_shapes_lowrank(case):
+    Bn, Tn, Dn, R, W, static, residual, dtype = case[:8]
+    if len(case) > 8:  # the kernel family the dispatch must pick for this shape
+        for bwd, want in enumerate(case[8]):
+            assert _path("lr", Bn, Tn, Dn, R, W, dtype, static, bwd) == want, ("bwd" if bwd else "fwd", want)
     g = gen(Bn * 1000003 + Tn * 1009 + Dn * 7 + R + W)
     x = randn(g, Bn, Tn, Dn)
     dy = randn(g, Bn, Tn, Dn)
@@ -192,6 +237,7 @@ def test_edge_shapes_lowrank(Bn, Tn, Dn, R, W, static, residual, dtype):
     for a, b, n in zip(g_k, g_q, ["dx", "dz", "dU", "dstatic_w"]):
         if b is not None:
             assert_ns(a, b, dtype, n, elementwise=n == "dx")
+    check_reductions("lr", src_q, dy.to(dtype).float(), g_k, dtype)
 
 
 @pytest.mark.parametrize("R,static,dtype,off", [(16, False, torch.bfloat16, 1), (12, True, torch.bfloat16, 1),
@@ -222,9 +268,26 @@ def test_lowrank_misaligned_z(R, static, dtype, off):
     for a, b, n in zip(g_k, g_q, ["dx", "dz", "dU", "dstatic_w"]):
         if b is not None:
             assert_ns(a, b, dtype, n, elementwise=n == "dx")
+    check_reductions("lr", src_q, dy.to(dtype).float(), g_k, dtype)
 
 
 # --------------------------------------------------------- BASELINE configs
+@pytest.mark.parametrize("loss", ["sum", "randn"])
+def test_config0(loss):
+    """BASELINE.json configs[0] on the GPU: headwise fp32, B2 T1024 D512 H512 (head size 1) W4, no static_w,
+    no residual, x ~ N(0, 1), weights ~ N(0, 1/W); loss y.sum() (dy = 1) as the CPU baseline runs it, and a
+    random dy.  test.py's criterion (test.py:17, 59-69) and the north-star one (1e-5 elementwise)."""
+    Bn, Tn, Dn, H, W = 2, 1024, 512, 512, 4
+    assert _path("hw", Bn, Tn, Dn, H, W, torch.float32, False, 0) == "vector"
+    assert _path("hw", Bn, Tn, Dn, H, W, torch.float32, False, 1) == "vector"
+    g = gen(0)
+    x = randn(g, Bn, Tn, Dn)
+    w = randn(g, Bn, Tn, H, W, scale=1 / math.sqrt(W))
+    dy = torch.ones(Bn, Tn, Dn) if loss == "sum" else randn(g, Bn, Tn, Dn)
+    _check_case(hw, hw_ref, [x, w, None], dy, torch.float32, False, ["dx", "dweight", "dstatic_w"],
+                {"dx", "dweight"}, "hw")
+
+
 def _windows(Tn, n=64):
     return [(0, n), (Tn // 2 - n // 2, Tn // 2 + n // 2), (Tn - n, Tn)]
 
@@ -287,20 +350,9 @@ def test_baseline_configs(cfg):
             assert_ns(y_k[b : b + 1, t0:t1], y_w[:, sl], dtype, f"y[{b},{t0}:{t1}]")
             assert_ns(g_k[0][b : b + 1, t0:t1], g_w[0][:, sl], dtype, f"dx[{b},{t0}:{t1}]")
             assert_ns(g_k[1][b : b + 1, t0:t1], g_w[1][:, sl], dtype, f"d1[{b},{t0}:{t1}]", elementwise=kind == "hw")
-    # global reductions in float64 on the CPU
-    x64, dy64 = q[0].double(), dyq.double()
-    Dn = x64.shape[-1]
-    G = [dy64 * _shift(x64, k) for k in range(W)]
-    if kind == "hw":
-        dsw = torch.stack([gk.sum((0, 1)) for gk in G])
-        assert_ns(g_k[2], dsw, dtype, "dstatic_w", elementwise=False)
-    else:
-        z64 = q[1].double().reshape(-1, q[1].shape[-1])
-        dU = torch.cat([z64.t() @ gk.reshape(-1, Dn) for gk in G], dim=1)
-        assert_ns(g_k[2], dU, dtype, "dU", elementwise=False)
-        if q[3] is not None:
-            dsw = torch.stack([gk.sum((0, 1)) for gk in G])
-            assert_ns(g_k[3], dsw, dtype, "dstatic_w", elementwise=False)
+    # the long reductions over the whole tensors: per-entry bounds against float64 sums
+    # (dz of every row, every dU / dstatic_w entry)
+    check_reductions(kind, q, dyq, g_k, dtype)
 
 
 # ---------------------------------------------------------- long sequence
@@ -335,6 +387,9 @@ def test_long_sequence(kind):
         assert_ns(y_k[:, t0:t1], y_w[:, sl], dtype, f"y[{t0}:{t1}]")
         assert_ns(g_k[0][:, t0:t1], g_w[0][:, sl], dtype, f"dx[{t0}:{t1}]")
         assert_ns(g_k[1][:, t0:t1], g_w[1][:, sl], dtype, f"d1[{t0}:{t1}]", elementwise=kind == "hw32")
+    # the global reductions over the whole sequence (headwise dstatic_w; lowrank dz, dU,
+    # dstatic_w): per-entry bounds against float64 sums
+    check_reductions("hw" if kind == "hw32" else "lr", q, dyq, g_k, dtype)
 
 
 # ------------------------------------------------------------ determinism
@@ -411,7 +466,7 @@ def test_lowrank_zeff_saved(R, static, xoff):
     y = torch.empty_like(x)
     p = _capi.ptr
     st = torch.cuda.current_stream().cuda_stream
-    _capi.check(lib.dc_lowrank_fwd(p(x), p(z), p(U), p(sw), p(y), p(zeff), Bn, Tn, Dn, R, W, 0, 1, st), "fwd")
+    _capi.check(lib.dc_lowrank_fwd(p(x), p(z), p(U), p(sw), p(y), p(zeff), nz, Bn, Tn, Dn, R, W, 0, 1, st), "fwd")
     want = torch.zeros(Bn * Tn, rp, dtype=bf, device=DEV)
     want[:, :R] = z.reshape(-1, R)
     if static:
@@ -424,8 +479,8 @@ def test_lowrank_zeff_saved(R, static, xoff):
         ws = torch.empty(nws, dtype=torch.uint8, device=DEV)
         dx, dz, dU = torch.empty_like(x), torch.empty_like(z), torch.empty_like(U)
         dsw = torch.empty_like(sw) if static else None
-        _capi.check(lib.dc_lowrank_bwd(p(x), p(z), p(U), p(sw), p(zp), p(dy), p(dx), p(dz), p(dU), p(dsw), p(ws),
-                                       nws, Bn, Tn, Dn, R, W, 0, 1, st), "bwd")
+        _capi.check(lib.dc_lowrank_bwd(p(x), p(z), p(U), p(sw), p(zp), nz if zp is not None else 0, p(dy), p(dx),
+                                       p(dz), p(dU), p(dsw), p(ws), nws, Bn, Tn, Dn, R, W, 0, 1, st), "bwd")
         outs.append([dx, dz, dU] + ([dsw] if static else []))
     torch.cuda.synchronize()
     for a, b in zip(*outs):

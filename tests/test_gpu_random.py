@@ -17,7 +17,7 @@ import random
 import pytest
 import torch
 
-from helpers import assert_ns, gen, randn, run_fwd_bwd, uniform
+from helpers import assert_ns, check_reductions, gen, randn, run_fwd_bwd, uniform
 from oracle.reference_cpu import (
     headwise_dynamic_convolution_ref as hw_ref,
     lowrank_dynamic_convolution_ref as lr_ref,
@@ -93,6 +93,7 @@ def test_random_lowrank(Bn, Tn, Dn, R, W, static, residual, dtype):
     for a, b, n in zip(g_k, g_q, ["dx", "dz", "dU", "dstatic_w"]):
         if b is not None:
             assert_ns(a, b, dtype, n, elementwise=n == "dx")
+    check_reductions("lr", src_q, dy.to(dtype).float(), g_k, dtype)
 
 
 @pytest.mark.parametrize("Bn,Tn,Dn,H,W,static,residual,dtype", HW_CASES, ids=_ids(HW_CASES, "hw"))
@@ -112,6 +113,7 @@ def test_random_headwise(Bn, Tn, Dn, H, W, static, residual, dtype):
     for a, b, n in zip(g_k, g_q, ["dx", "dweight", "dstatic_w"]):
         if b is not None:
             assert_ns(a, b, dtype, n, elementwise=n != "dstatic_w")
+    check_reductions("hw", src_q, dy.to(dtype).float(), g_k, dtype)
 
 
 def _grouped_case(i):
@@ -169,3 +171,6 @@ def test_random_grouped(G, Bn, Tn, Dn, extra, R, W, static, hd, dtype):
         assert_ns(Uk[gi].grad, Ur.grad, dtype, f"g{gi} dU", elementwise=False)
         if static:
             assert_ns(sk[gi].grad, sr.grad, dtype, f"g{gi} dstatic_w", elementwise=False)
+        check_reductions("lr", [xs.detach(), zr.detach(), Ur.detach(), None if sr is None else sr.detach()],
+                         dys[gi].to(dtype).float(), [None, zk[gi].grad, Uk[gi].grad, sk[gi].grad if static else None],
+                         dtype, tag=f"g{gi} ")
