@@ -3,7 +3,8 @@
 // Every entry point validates its arguments on the host before touching the
 // HIP runtime and returns a dc_status; nothing here allocates, synchronises
 // or throws.  The only process-wide state is the once-initialised device
-// probe below.
+// probe and the per-device address of the allocation-free scratch array below.
+#include <atomic>
 #include <mutex>
 
 #include "dynconv.h"
@@ -57,6 +58,35 @@ int check_lowrank(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dty
 
 int launch_status(hipError_t e) { return e == hipSuccess ? DC_OK : DC_ERR_LAUNCH; }
 
+// Scratch of dc_headwise_bwd_noalloc: the fp32 dstatic_w partial sums that
+// dc_headwise_bwd keeps in its caller's workspace.  Each GPU holds its own copy
+// of this array (at its own address) for the life of the process.  In host
+// code `scratch` names a host-side stand-in, not a device address: only the
+// address hipGetSymbolAddress returns for the current device is passed on.
+static __device__ __align__(256) char scratch[DC_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch array, looked up once per
+// device with that device current.  DC_ERR_DEVICE when there is none.
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return DC_ERR_DEVICE;
+  void* ptr = g_scratch[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return DC_ERR_DEVICE;
+      g_scratch[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return DC_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -74,6 +104,7 @@ const char* dc_status_string(int status) {
     case DC_ERR_ALIGN: return "pointer not aligned to its element size";
     case DC_ERR_DEVICE: return "no HIP device available";
     case DC_ERR_LAUNCH: return "kernel launch failed";
+    case DC_ERR_SCRATCH: return "problem needs more scratch than the allocation-free entry point holds";
     default: return "unknown dynconv status";
   }
 }
@@ -148,6 +179,31 @@ int dc_headwise_bwd(const void* x, const void* weight, const void* static_w, con
   dc::HwProblem p{};
   p.x = x; p.weight = weight; p.static_w = static_w; p.dy = dy;
   p.dx = dx; p.dweight = dweight; p.dstatic_w = dstatic_w; p.ws = (float*)workspace;
+  p.B = B; p.T = T; p.D = D; p.H = H; p.W = W;
+  p.dtype = dtype; p.residual = residual ? 1 : 0; p.stream = (hipStream_t)stream;
+  return launch_status(dc::hw_bwd(p));
+}
+
+int dc_headwise_bwd_noalloc(const void* x, const void* weight, const void* static_w, const void* dy, void* dx,
+                            void* dweight, void* dstatic_w, int64_t B, int64_t T, int64_t D, int64_t H, int64_t W,
+                            int dtype, int residual, void* stream) {
+  int s = check_headwise(B, T, D, H, W, dtype);
+  if (s != DC_OK) return s;
+  if (!x || !weight || !dy || !dx || !dweight) return DC_ERR_NULL;
+  if ((static_w == nullptr) != (dstatic_w == nullptr)) return DC_ERR_NULL;
+  const int es = dc::dtype_size(dtype);
+  if (!aligned_to(x, es) || !aligned_to(weight, es) || !aligned_to(static_w, es) || !aligned_to(dy, es) ||
+      !aligned_to(dx, es) || !aligned_to(dweight, es) || !aligned_to(dstatic_w, es))
+    return DC_ERR_ALIGN;
+  const int64_t need = dc_headwise_bwd_ws_bytes(B, T, D, H, W, dtype, static_w != nullptr);
+  if (need < 0) return (int)need;
+  if (need > DC_NOALLOC_SCRATCH_BYTES) return DC_ERR_SCRATCH;
+  if ((s = device_status()) != DC_OK) return s;
+  void* ws = nullptr;
+  if (need > 0 && (s = scratch_of_current_device(&ws)) != DC_OK) return s;
+  dc::HwProblem p{};
+  p.x = x; p.weight = weight; p.static_w = static_w; p.dy = dy;
+  p.dx = dx; p.dweight = dweight; p.dstatic_w = dstatic_w; p.ws = (float*)ws;
   p.B = B; p.T = T; p.D = D; p.H = H; p.W = W;
   p.dtype = dtype; p.residual = residual ? 1 : 0; p.stream = (hipStream_t)stream;
   return launch_status(dc::hw_bwd(p));

@@ -31,6 +31,7 @@ SIGNATURES = {
     "dc_lowrank_path": (_c_int, [_c_i64] * 5 + [_c_int] * 3),
     "dc_headwise_bwd_ws_bytes": (_c_i64, [_c_i64] * 5 + [_c_int, _c_int]),
     "dc_headwise_bwd": (_c_int, [_c_vp] * 8 + [_c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
+    "dc_headwise_bwd_noalloc": (_c_int, [_c_vp] * 7 + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
     "dc_lowrank_zeff_bytes": (_c_i64, [_c_i64] * 5 + [_c_int, _c_int]),
     "dc_lowrank_fwd": (_c_int, [_c_vp] * 6 + [_c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
     "dc_lowrank_bwd_ws_bytes": (_c_i64, [_c_i64] * 5 + [_c_int, _c_int]),

@@ -76,7 +76,8 @@ typedef enum dc_status {
   DC_ERR_WORKSPACE = -5,   /* workspace (or z_eff) NULL or below its size query    */
   DC_ERR_ALIGN = -6,       /* a pointer is not aligned to its element size          */
   DC_ERR_DEVICE = -7,      /* no HIP device available                               */
-  DC_ERR_LAUNCH = -8       /* the HIP runtime rejected a kernel launch              */
+  DC_ERR_LAUNCH = -8,      /* the HIP runtime rejected a kernel launch              */
+  DC_ERR_SCRATCH = -9      /* the problem needs more than DC_NOALLOC_SCRATCH_BYTES  */
 } dc_status;
 
 /* Kernel family a call of a given shape runs (dc_headwise_path, dc_lowrank_path). */
@@ -119,6 +120,23 @@ int dc_headwise_bwd(const void* x, const void* weight, const void* static_w, con
                     void* workspace, int64_t ws_bytes,
                     int64_t B, int64_t T, int64_t D, int64_t H, int64_t W,
                     int dtype, int residual, void* stream);
+
+/* dc_headwise_bwd for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * the same kernels and results, bitwise, with the workspace replaced by a
+ * fixed scratch array of DC_NOALLOC_SCRATCH_BYTES that the library holds on
+ * every GPU it runs on until the process ends.  No counterpart in the
+ * reference.  Returns DC_ERR_SCRATCH when dc_headwise_bwd_ws_bytes(...)
+ * exceeds DC_NOALLOC_SCRATCH_BYTES.  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (on different streams, or from several
+ * host threads) race; calls ordered on one stream do not.  The array needs no
+ * initial contents (each call overwrites what it reads).  Nothing here calls
+ * hipMalloc, hipFree or an allocating library routine. */
+#define DC_NOALLOC_SCRATCH_BYTES (8 << 20)
+int dc_headwise_bwd_noalloc(const void* x, const void* weight, const void* static_w, const void* dy,
+                            void* dx, void* dweight, void* dstatic_w,
+                            int64_t B, int64_t T, int64_t D, int64_t H, int64_t W,
+                            int dtype, int residual, void* stream);
 
 /* Bytes of the padded z_eff (z with the static column and zero ranks, rows of
  * 4*k or 32 ranks) that dc_lowrank_bwd builds before its main kernel for this

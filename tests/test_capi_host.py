@@ -19,7 +19,7 @@ from dynconv import _capi
 
 HEADER = os.path.join(ROOT, "include", "dynconv.h")
 
-OK, E_NULL, E_SHAPE, E_DTYPE, E_UNSUP, E_WS, E_ALIGN, E_DEV, E_LAUNCH = 0, -1, -2, -3, -4, -5, -6, -7, -8
+OK, E_NULL, E_SHAPE, E_DTYPE, E_UNSUP, E_WS, E_ALIGN, E_DEV, E_LAUNCH, E_SCRATCH = 0, -1, -2, -3, -4, -5, -6, -7, -8, -9
 P = 0x10000  # a fake, 256-byte aligned "device pointer"; never dereferenced on these paths
 
 
@@ -35,7 +35,7 @@ def header_functions():
 
 def test_exports_every_declared_symbol(lib):
     names = header_functions()
-    assert len(names) == 14, names
+    assert len(names) == 15, names
     raw = ctypes.CDLL(_capi.LIB_PATH)
     for n in names:
         assert hasattr(raw, n), f"{n} declared in dynconv.h but not exported"
@@ -44,7 +44,7 @@ def test_exports_every_declared_symbol(lib):
 
 def test_abi_version_and_strings(lib):
     assert lib.dc_abi_version() == 5
-    for s in (OK, E_NULL, E_SHAPE, E_DTYPE, E_UNSUP, E_WS, E_ALIGN, E_DEV, E_LAUNCH):
+    for s in (OK, E_NULL, E_SHAPE, E_DTYPE, E_UNSUP, E_WS, E_ALIGN, E_DEV, E_LAUNCH, E_SCRATCH):
         assert len(lib.dc_status_string(s)) > 0
     assert b"unknown" in lib.dc_status_string(-99)
 
@@ -222,6 +222,32 @@ def test_lowrank_grouped_bwd_validation(lib):
     if no_dev:
         assert call(sw=g3, dsw=g3) == E_DEV
         assert call(sw=g3, dsw=g3, dy_hd=8) == E_DEV
+
+
+def test_headwise_bwd_noalloc_validation(lib):
+    """The allocation-free backward: the checks of dc_headwise_bwd, and DC_ERR_SCRATCH for problems whose
+    dstatic_w partials exceed the fixed scratch array (the workspace size query's bytes)."""
+    no_dev = not torch.cuda.is_available()
+    limit = 8 << 20  # DC_NOALLOC_SCRATCH_BYTES
+
+    def call(sw=None, dsw=None, B=2, T=8, D=16, H=4, W=4, dt=0, dy=P):
+        return lib.dc_headwise_bwd_noalloc(P, P, sw, dy, P, P, dsw, B, T, D, H, W, dt, 0, None)
+
+    assert call(dt=5) == E_DTYPE
+    assert call(H=3) == E_SHAPE
+    assert call(W=33) == E_UNSUP
+    assert call(dy=None) == E_NULL
+    assert call(sw=P, dsw=None) == E_NULL
+    assert call(sw=P + 1, dsw=P) == E_ALIGN
+    # the largest shapes: the partials of a wide, long problem exceed the scratch array
+    big = dict(B=64, T=1 << 16, D=1 << 15, H=1 << 15, W=16)
+    assert lib.dc_headwise_bwd_ws_bytes(big["B"], big["T"], big["D"], big["H"], big["W"], 0, 1) > limit
+    assert call(sw=P, dsw=P, **big) == E_SCRATCH
+    assert lib.dc_headwise_bwd_ws_bytes(2, 8, 16, 4, 4, 0, 1) <= limit
+    if no_dev:
+        assert call() == E_DEV
+        assert call(sw=P, dsw=P) == E_DEV
+        assert call(**big) == E_DEV  # no static filter: no scratch needed, any size
 
 
 def test_kernel_paths(lib):
