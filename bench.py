@@ -80,6 +80,9 @@ EXTRA = {
     "lr_qkv": dict(kind="lr", B=2, T=8192, D=4096, R=31, W=4, static=True, residual=True, calls=3),
     "lr_qkv_grouped": dict(kind="lrg", B=2, T=8192, D=4096, R=31, W=4, static=True, residual=True, G=3,
                            head_dim=128),
+    # the same grouped q|k|v op on one sequence of 32768 tokens (x spans 768 MiB): per-run buffer
+    # resources keep it on the matrix-core kernels; per-token time against lr_qkv_grouped's 16384 tokens
+    "lr_qkv_grouped_T32k": dict(kind="lrg", B=1, T=32768, D=4096, R=31, W=4, static=True, residual=True, G=3),
     # the fp32 tier (reference test.py's 1e-5 cases) at the B4 shapes
     "hw_hs32_fp32": dict(kind="hw", B=4, T=4096, D=2048, H=64, W=4, static=True, residual=True, dtype="fp32"),
     "lr_r16_fp32": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=4, static=False, residual=True, dtype="fp32"),
@@ -535,6 +538,7 @@ def main():
             "fwd_GBs": round(fb / (f_us * 1e-6) / 1e9, 1), "bwd_GBs": round(bb / (b_us * 1e-6) / 1e9, 1),
             "fwdbwd_GBs": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
             "alg_MB": round((fb + bb) * calls / 1e6, 2),
+            "ns_per_token": round(fb_us * calls * 1e3 / (c["B"] * c["T"]), 3),
         }
         print(f"[bench] {name}: fwd {f_us:.1f} us ({breakdown[name]['fwd_GBs']} GB/s)  bwd {b_us:.1f} us "
               f"({breakdown[name]['bwd_GBs']} GB/s)  fwd+bwd {fb_us:.1f} us = {gbs:.0f} GB/s ({gbs / PEAK_GBS:.1%})",

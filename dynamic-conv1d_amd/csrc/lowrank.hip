@@ -207,12 +207,9 @@ bool lr_mfma_ok(const LrProblem& p, bool bwd) {
   const int64_t rc = (p.R + (p.static_w ? 1 : 0) + 15) / 16;
   if (rc > 4 || p.W * rc > 8) return false;  // staged operands / accumulators bound W*RC
   if (bwd && rc == 4 && p.W > 1) return false;  // backward LDS (operands + dz sums) above 160 KiB
-  // buffer-offset range of one sequence (x, y, dy, dx rows and z rows)
-  const int64_t ld = p.xld() > p.dxld() ? p.xld() : p.dxld();
-  if ((p.T + kSeqSlackRows) * ld * 2 > kMaxSeqBytes) return false;
-  // z rows: R ranks, or the backward's padded z_eff rows of RK rounded up to 4 (>= R)
-  const int64_t zrow = bwd ? lr_bwd_zrow(p.R, p.static_w != nullptr) : p.R;
-  if ((p.T + kSeqSlackRows) * zrow * 2 > kMaxSeqBytes) return false;
+  // buffer-offset range of a run (resources start at each run's base row, so
+  // the sequence length is free): at least one tile must fit
+  if ((bwd ? lr_bwd_max_run_tiles(p) : lr_fwd_max_run_tiles(p)) < 1) return false;
   if (!bwd) {
     // 16-byte row pieces of x at every row: xld a multiple of 8 elements
     if (p.D % 8 != 0 || p.xld() % 8 != 0) return false;

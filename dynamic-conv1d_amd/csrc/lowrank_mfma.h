@@ -91,22 +91,33 @@ __device__ __forceinline__ float q4f(const u32x2& v, int j) {
   return Mma16<T>::to_f(elem16x2(v, j));
 }
 
-// Buffer resources (dc_common.h) of the lowrank kernels cover one sequence
-// ([T, C] elements): rows before 0 (negative offsets wrap to large unsigned
-// values), rows past T and channels past D (lane offset kOobLane) read 0 and
-// drop stores, without branches or clamped addresses.  The host takes these
-// paths only when (T + kSeqSlackRows) rows of a sequence span at most
-// kMaxSeqBytes: every offset a kernel forms (rows -7 .. T + 30, plus kOobLane)
-// then stays below 2^31, and every wrapped negative offset stays above
-// kMaxSeqBytes.
+// Buffer resources (dc_common.h) of the matrix-core lowrank kernels cover one
+// run of tiles: they start at the run's base row rb = max(16 * tile0 - 8, 0)
+// (the first tile's rows less an 8-row halo, W - 1 <= 7) and end at T, capped
+// at kMaxSeqBytes - kSeqSlackRows rows (run_rsrc).  Rows before 0 (negative
+// offsets wrap to large unsigned values), rows past T and channels past D
+// (lane offset kOobLane) read 0 and drop stores, without branches or clamped
+// addresses.  The host caps a run at lr_max_run_tiles, so every row a run
+// touches (its tiles, the halo, the tile after it) lies below that cap: offsets
+// stay within int32, and kOobTile, kOobTile less the halo and kOobLane are out
+// of range.  A sequence of any length therefore takes these kernels.
 constexpr int kOobLane = 0x40000000;
 constexpr int64_t kMaxSeqBytes = int64_t(1) << 29;
 constexpr int kSeqSlackRows = 32;
 
-// A byte offset that every buffer access of a sequence treats as out of range
-// (returns 0, touches no memory): the host guarantees a sequence's x / z
-// offsets stay below kMaxSeqBytes - kSeqSlackRows rows.
+// A byte offset that every buffer access of a run treats as out of range
+// (returns 0, touches no memory), also less 7 rows of halo.
 constexpr int kOobTile = (int)kMaxSeqBytes;
+
+// First row covered by the buffer resources of a run whose first tile is tile0.
+__device__ __forceinline__ int run_base_row(int tile0) { return max(tile0 * 16 - 8, 0); }
+
+// Resource over rows [rb, rb + nrows) of `rowb` bytes each, starting at p (row
+// rb), capped so that kOobTile less 7 rows stays out of range.
+__device__ __forceinline__ rsrc_t run_rsrc(const void* p, int64_t nrows, int64_t rowb) {
+  const int64_t bytes = nrows * rowb, cap = kMaxSeqBytes - kSeqSlackRows * rowb;
+  return make_rsrc(p, bytes < cap ? bytes : cap);
+}
 
 // A operands of a 16-row tile: z_eff[t, 16c+4q .. 16c+4q+3] for c < RC, where
 // t is the lane's row (column n of the MFMA's A).  Split in two so the loads can
@@ -161,6 +172,14 @@ struct ZRaw {
 
 inline bool aligned_to(const void* p, int a) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// Longest run (in 16-row tiles) whose rows fit the resource cap when rows are
+// `rowb` bytes: the run's tiles, the 8-row halo, the tile after it and the
+// slack rows.  0 when not even one tile fits.
+inline int64_t run_tiles_cap(int64_t rowb) {
+  const int64_t rows = kMaxSeqBytes / (rowb > 0 ? rowb : 1) - kSeqSlackRows - 8 - 32;
+  return rows > 0 ? rows / 16 : 0;
+}
+
 // Ranks per row of the backward's padded z_eff copy: the kernel rank RK rounded
 // up to 4, or 32 for two rank chunks (17 <= RK <= 32).
 inline int64_t lr_bwd_zrow(int64_t R, bool has_static) {
@@ -175,6 +194,11 @@ __device__ __forceinline__ F pick(const S (&a)[kMaxGroups], int g, F S::*f) {
   static_assert(kMaxGroups == 4, "pick() selects among four groups");
   return g == 0 ? a[0].*f : g == 1 ? a[1].*f : g == 2 ? a[2].*f : a[3].*f;
 }
+
+// Longest run (16-row tiles) of the MFMA forward / backward for p whose rows
+// fit the buffer resources (0: not even one tile; the generic kernels take p).
+int64_t lr_fwd_max_run_tiles(const LrProblem& p);
+int64_t lr_bwd_max_run_tiles(const LrProblem& p);
 
 // Host entry points of the two MFMA translation units.
 hipError_t lr_mfma_fwd(const LrProblem* p, int G);

@@ -279,18 +279,20 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   const bool chv = col < D;  // the lane's channels inside D (D % 16 == 0)
   const int64_t WD = (int64_t)W * D;
   const int ntile = (Tn + 15) >> 4;
-  // Run s of the grid: tiles [tile0, tile1) of sequence b.  A workgroup's last
-  // run can lie past nseg (odd nseg): it has no tiles.
+  // Run s of the grid: tiles [tile0, tile1) of sequence b, whose buffer
+  // resources start at row rb (run_base_row).  A workgroup's last run can lie
+  // past nseg (odd nseg): it has no tiles.
   struct Run {
-    int tile0, tile1;
+    int tile0, tile1, rb;
     int64_t row0;
   };
   auto run_of = [&](int s) {
-    Run r{0, 0, 0};
+    Run r{0, 0, 0, 0};
     if (s < a.nseg) {
       const int b = s / a.nspb;
       r.tile0 = (s - b * a.nspb) * a.seg;
       r.tile1 = min(r.tile0 + a.seg, ntile);
+      r.rb = run_base_row(r.tile0);
       r.row0 = (int64_t)b * Tn;
     }
     return r;
@@ -303,8 +305,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     nit = max(nit, runs[i].tile1 - runs[i].tile0);
   }
   const Run me = rw == 0 ? runs[0] : runs[NRW - 1];
-  const int tile0 = me.tile0, tile1 = me.tile1;
-  const int64_t row0 = me.row0;
+  const int tile0 = me.tile0, tile1 = me.tile1, rb = me.rb;
+  const int64_t row0 = me.row0, rrow = row0 + rb;
   const int R = a.R, RK = a.RK;
   typedef ZRaw<T, RC, true> ZR;  // 8-byte z loads: rows of zld % 4 == 0 elements
   u32x2* __restrict__ my_uw = uw_lds[wave];
@@ -324,11 +326,12 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   // stay out of range either way).
   const int yhd = a.yhd, head = d0 / yhd;
   const int rowb = yhd * 2, xrowb = a.xld * 2, dxrowb = a.dxld * 2;
-  const rsrc_t rx = make_rsrc(x + row0 * a.xld, (int64_t)Tn * xrowb);
-  const rsrc_t rdy = make_rsrc(dy + row0 * D + (int64_t)head * Tn * yhd, (int64_t)Tn * rowb);
-  const rsrc_t rdx = make_rsrc(dx + row0 * a.dxld, (int64_t)Tn * dxrowb);
+  // resources of the run's rows from rb (offsets below are relative to row rb)
+  const rsrc_t rx = run_rsrc(x + rrow * a.xld, Tn - rb, xrowb);
+  const rsrc_t rdy = run_rsrc(dy + row0 * D + ((int64_t)head * Tn + rb) * yhd, Tn - rb, rowb);
+  const rsrc_t rdx = run_rsrc(dx + rrow * a.dxld, Tn - rb, dxrowb);
   const int zld = a.zld, zr = a.zr, zrk = a.zrk;
-  const rsrc_t rz = make_rsrc(z + row0 * zld, (int64_t)Tn * zld * 2);
+  const rsrc_t rz = run_rsrc(z + rrow * zld, Tn - rb, zld * 2);
   // byte offsets of the lane's row-4q channels in dy, x and dx
   const int lane_off = chv ? (4 * q * yhd + col - head * yhd) * 2 : kOobLane;
   const int xlane_off = chv ? (4 * q * a.xld + col) * 2 : kOobLane;
@@ -385,8 +388,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     // The scatter form also reads dy and z of the tile after the run: its
     // first rows close the run's last dx rows.
     const bool ylive = SC ? tile <= tile1 : live;
-    const int xtoff = live ? tile * 16 * xrowb : kOobTile;
-    const int toff = ylive ? tile * 16 * rowb : kOobTile;
+    const int xtoff = live ? (tile * 16 - rb) * xrowb : kOobTile;
+    const int toff = ylive ? (tile * 16 - rb) * rowb : kOobTile;
 #pragma unroll
     for (int m = 0; m < NR; ++m) in.xr[m] = LV::load(rx, xlane_off + xtoff + (m - (W - 1)) * xrowb);
 #pragma unroll
@@ -394,9 +397,9 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb) {
       if constexpr (K32)
-        in.z32[bb] = bload128(rz, ylive ? ((tile * 16 + 4 * bb + n) * zld + 8 * q) * 2 : kOobTile);
+        in.z32[bb] = bload128(rz, ylive ? ((tile * 16 + 4 * bb + n - rb) * zld + 8 * q) * 2 : kOobTile);
       else
-        in.zr[bb].load(rz, ylive ? (tile * 16 + 4 * bb + n) * zld * 2 : kOobTile, zr, q);
+        in.zr[bb].load(rz, ylive ? (tile * 16 + 4 * bb + n - rb) * zld * 2 : kOobTile, zr, q);
     }
   };
 
@@ -424,8 +427,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     const bool top = q == 3;
     const bool cur_live = tile < tile1;
     const bool prev_live = tile > tile0 && tile <= tile1;
-    const int cur_off = cur_live ? dxlane_off + tile * 16 * dxrowb : kOobTile;
-    const int prev_off = prev_live ? dxlane_off + (tile - 1) * 16 * dxrowb : kOobTile;
+    const int cur_off = cur_live ? dxlane_off + (tile * 16 - rb) * dxrowb : kOobTile;
+    const int prev_off = prev_live ? dxlane_off + ((tile - 1) * 16 - rb) * dxrowb : kOobTile;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       constexpr int kFirstOpen = 4 - NOPEN;
@@ -475,7 +478,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     const int tile = tile0 + it;
     const bool live = tile < tile1;
     const int t0 = tile * 16;
-    const int dxtoff = live ? t0 * dxrowb : kOobTile;  // tiles past the run store nothing
+    const int dxtoff = live ? (t0 - rb) * dxrowb : kOobTile;  // tiles past the run store nothing
     const typename LV::type(&xr)[NR] = in.xr;
     const typename LV::type(&dyr)[NDY] = in.dyr;
     ZO zA[NB];
@@ -589,8 +592,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
 #pragma unroll
       for (int ri = 0; ri < NRW; ++ri) {
         const Run& ru = ri == 0 ? runs[0] : runs[NRW - 1];
-        // rows of run ri's sequence; t >= T falls outside the resource
-        const rsrc_t rout = make_rsrc(part_dz + ((int64_t)cg * a.BT + ru.row0) * R, (int64_t)Tn * R * 4);
+        // rows of run ri from its base row; t >= T falls outside the resource
+        const rsrc_t rout = run_rsrc(part_dz + ((int64_t)cg * a.BT + ru.row0 + ru.rb) * R, Tn - ru.rb, R * 4);
         const int tb = ru.tile0 + it - slot;  // run ri's tile of slot 0
 #pragma unroll
         for (int m = 0; m < DZB * PER_RUN / NTH; ++m) {
@@ -606,7 +609,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
           for (int w2 = 1; w2 < NCW; ++w2) v += dzred[buf][ri][w2][sl][pos];
           // slots past this batch (a short last batch), tiles past the run and ranks >= R store nothing
           const bool ok = sl <= slot && ti < ru.tile1 && r < R;
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rout, ok ? (t * R + r) * 4 : kOobLane, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rout, ok ? ((t - ru.rb) * R + r) * 4 : kOobLane, 0,
+                                                0);
         }
       }
     }
@@ -720,6 +724,20 @@ constexpr BwdShape bwd_shape(int W, int RC) {
   return BwdShape{(RC == 2 && W <= 4) ? 32 : 64, (RC == 1 && W <= 4) ? 2 : 1};
 }
 
+}  // namespace
+
+// Longest backward run (tiles) whose resources fit (see run_rsrc): rows of x,
+// dx, dy (one head's block of head-major dy), the z rows the kernel reads (z
+// itself or the padded copy) and the fp32 dz partials.
+int64_t lr_bwd_max_run_tiles(const LrProblem& p) {
+  int64_t rowb = p.xld() * 2;
+  const int64_t others[4] = {p.dxld() * 2, p.yhd() * 2, lr_bwd_zrow(p.R, p.static_w != nullptr) * 2, p.R * 4};
+  for (int64_t v : others) rowb = rowb > v ? rowb : v;
+  return run_tiles_cap(rowb);
+}
+
+namespace {
+
 LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   LrBwdArgs a;
   const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
@@ -736,6 +754,8 @@ LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   int64_t seg = (p.B * ntile * a.ncg * ncw + target_waves - 1) / target_waves;
   if (seg < 1) seg = 1;
   if (seg > ntile) seg = ntile;
+  const int64_t cap = lr_bwd_max_run_tiles(p);  // >= 1 (lr_mfma_ok)
+  if (seg > cap) seg = cap;
   a.seg = (int)seg;
   a.nspb = (int)((ntile + seg - 1) / seg);
   a.nseg = (int)(p.B * a.nspb);

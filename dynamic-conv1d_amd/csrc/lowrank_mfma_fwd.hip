@@ -120,19 +120,26 @@ void lr_fwd_mfma(LrArgs a) {
   const int tile0 = (sg - b * a.nspb) * a.seg;
   const int tile1 = min(tile0 + a.seg, ntile);
   const int64_t row0 = (int64_t)b * Tn;
+  // The run's resources start at row rb (run_base_row): offsets are relative to it.
+  const int rb = run_base_row(tile0);
+  const int64_t rrow = row0 + rb;
   // y is [B, T, D] (yhd == D) or head-major [B, D/yhd, T, yhd]: the lane's
-  // octet lies in head yh, whose rows are yhd elements apart.  Rows past T
-  // would land in the next head's block there, so stores check the row.
+  // octet lies in head yh, whose rows are yhd elements apart.  The y resource
+  // starts at row rb of head yh0, the head of the wavefront's first channel,
+  // and spans its heads up to yhl.  Rows past T would land in the next head's
+  // block there, so stores check the row.
   const int yhd = a.yhd, yh = dl / yhd;
+  const int yh0 = chunk * 128 / yhd, yhl = min(chunk * 128 + 127, D - 1) / yhd;
   const int rowb = yhd * 2, xrowb = a.xld * 2;
-  const rsrc_t rx = make_rsrc(x + row0 * a.xld, (int64_t)Tn * xrowb);
-  const rsrc_t ry = make_rsrc(y + row0 * D, (int64_t)Tn * D * 2);
-  const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 2);
+  const rsrc_t rx = run_rsrc(x + rrow * a.xld, Tn - rb, xrowb);
+  const rsrc_t ry = run_rsrc(y + row0 * D + ((int64_t)yh0 * Tn + rb) * yhd, (int64_t)(yhl - yh0) * Tn + Tn - rb, rowb);
+  const rsrc_t rz = run_rsrc(z + rrow * R, Tn - rb, R * 2);
   const int zrp = ZE ? a.zrp : 0;
   const bool zrow_mine = ZE && n % a.nch == chunk;  // this wavefront writes row n of each tile's z_eff
-  const rsrc_t rze = make_rsrc(ZE ? (const uint16_t*)pick(a.grp, g, &LrFwdGroup::zeff) + row0 * zrp : z,
-                               ZE ? (int64_t)Tn * zrp * 2 : 0);
-  const int lane_off = chv ? ((yh * Tn + 4 * q) * yhd + dl - yh * yhd) * 2 : kOobLane;  // y: the lane's row 4q octet
+  const rsrc_t rze = ZE ? run_rsrc((const uint16_t*)pick(a.grp, g, &LrFwdGroup::zeff) + rrow * zrp, Tn - rb, zrp * 2)
+                        : make_rsrc(z, 0);
+  // y: the lane's row-4q octet (head yh, relative to head yh0's row rb)
+  const int lane_off = chv ? (((yh - yh0) * Tn + 4 * q) * yhd + dl - yh * yhd) * 2 : kOobLane;
   const int xlane_off = chv ? (4 * q * a.xld + dl) * 2 : kOobLane;   // the same in x
   // HX (2 <= W <= 4): a lane loads only its own rows 4q..4q+3; the W-1 rows
   // above them are the own rows of the lane group above (lane - 16), or for
@@ -146,10 +153,10 @@ void lr_fwd_mfma(LrArgs a) {
   // kOobTile, which returns 0 and touches no memory).
   auto load_tile = [&](int tile, u32x4(&xr)[NR], ZR& zr) {
     const bool live = tile < tile1;
-    const int toff = live ? tile * 16 * xrowb : kOobTile;
+    const int toff = live ? (tile * 16 - rb) * xrowb : kOobTile;
 #pragma unroll
     for (int m = HX ? W - 1 : 0; m < NR; ++m) xr[m] = bload128(rx, xlane_off + toff + (m - (W - 1)) * xrowb);
-    zr.load(rz, live ? (tile * 16 + n) * R * 2 : kOobTile, R, q);
+    zr.load(rz, live ? (tile * 16 + n - rb) * R * 2 : kOobTile, R, q);
   };
   auto compute_tile = [&](int tile, u32x4(&xc)[NR], const ZR& zr) {
     u32x2 zc[RC];
@@ -163,7 +170,7 @@ void lr_fwd_mfma(LrArgs a) {
       for (int c = 0; c < RC; ++c) {
         const int r0 = 16 * c + 4 * q;
         bstore64<false>(zc[c], rze,
-                        zrow_mine && tile * 16 + n < Tn && r0 < zrp ? ((tile * 16 + n) * zrp + r0) * 2 : kOobTile);
+                        zrow_mine && tile * 16 + n < Tn && r0 < zrp ? ((tile * 16 + n - rb) * zrp + r0) * 2 : kOobTile);
       }
     }
     if constexpr (HX) {
@@ -204,7 +211,7 @@ void lr_fwd_mfma(LrArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] += Mma16<T>::to_f(elem16(xc[i + W - 1], j));
     }
-    const int toff = tile * 16 * rowb;
+    const int toff = (tile * 16 - rb) * rowb;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       u32x4 o;
@@ -221,7 +228,7 @@ void lr_fwd_mfma(LrArgs a) {
     // the run's first tile: rows 16*tile0-W+1 .. 16*tile0-1 (before the sequence: 0), as group 3 would send them
     const int xcol = chv ? dl * 2 : kOobLane;
 #pragma unroll
-    for (int m = 0; m < W - 1; ++m) prev[m] = bload128(rx, xcol + (tile0 * 16 + m + 1 - W) * xrowb);
+    for (int m = 0; m < W - 1; ++m) prev[m] = bload128(rx, xcol + (tile0 * 16 + m + 1 - W - rb) * xrowb);
   }
   for (int tile = tile0; tile < tile1; ++tile) {
     u32x4 xr[NR];
@@ -243,6 +250,31 @@ int fwd_target_waves(const LrProblem& p) {
   return (int)(w < 1 ? 1 : w > 4096 ? 4096 : w);
 }
 
+}  // namespace
+
+// Longest forward run (tiles) whose resources fit (see run_rsrc): rows of x, y,
+// z and z_eff; with head-major y a wavefront's resource also spans the blocks
+// of the heads its 128 channels touch (up to 127 / hd + 1 more, T rows each).
+int64_t lr_fwd_max_run_tiles(const LrProblem& p) {
+  const int64_t hd = p.yhd();
+  int64_t rowb = p.xld() * 2;
+  rowb = rowb > hd * 2 ? rowb : hd * 2;
+  rowb = rowb > p.R * 2 ? rowb : p.R * 2;
+  const int64_t zrp = p.zeff ? lr_bwd_zrow(p.R, p.static_w != nullptr) : 0;
+  rowb = rowb > zrp * 2 ? rowb : zrp * 2;
+  int64_t tiles = run_tiles_cap(rowb);
+  if (hd != p.D) {
+    // head-major y: rows of the other heads' blocks come first in its offsets
+    const int64_t extra = (127 / hd + 1) * p.T * hd * 2;
+    const int64_t rows = (kMaxSeqBytes - extra) / (hd * 2) - kSeqSlackRows - 8 - 32;
+    const int64_t yt = rows > 0 ? rows / 16 : 0;
+    tiles = tiles < yt ? tiles : yt;
+  }
+  return tiles;
+}
+
+namespace {
+
 LrArgs make_args(const LrProblem& p, int target_waves) {
   LrArgs a;
   a.Tn = (int)p.T;
@@ -258,6 +290,8 @@ LrArgs make_args(const LrProblem& p, int target_waves) {
   int64_t seg = (p.B * ntile * a.nch + target_waves - 1) / target_waves;
   if (seg < 1) seg = 1;
   if (seg > ntile) seg = ntile;
+  const int64_t cap = lr_fwd_max_run_tiles(p);  // >= 1 (lr_mfma_ok)
+  if (seg > cap) seg = cap;
   a.seg = (int)seg;
   a.nspb = (int)((ntile + seg - 1) / seg);
   a.nseg = (int)(p.B * a.nspb);

@@ -22,7 +22,7 @@ import math
 import pytest
 import torch
 
-from helpers import assert_ns, check_reductions, gen, randn, uniform
+from helpers import assert_ns, check_reductions, gen, randn, run_fwd_bwd, uniform
 from oracle.reference_cpu import lowrank_dynamic_convolution_ref as lr_ref
 import lowrank as lr_mod
 
@@ -89,6 +89,45 @@ def test_grouped_against_oracle(G, Bn, Tn, Dn, R, W, static, extra, dtype):
         check_reductions("lr", [xs.detach(), zr.detach(), Ur.detach(), None if sr is None else sr.detach()],
                          dys[g].to(dtype).float(), [None, zk[g].grad, Uk[g].grad, sk[g].grad if static else None],
                          dtype, tag=f"g{g} ")
+
+
+def test_grouped_long_sequence():
+    """The grouped op on one long sequence, B1 T32768 D4096 x3 (the q|k|v of configs[4] at four times the
+    length), R15 + static_w: x rows are 3 * 4096 elements apart, so the sequence's x spans 768 MiB.  The
+    matrix-core kernels give each run of tiles its own buffer resources (before, sequences past 512 MiB,
+    here T > 21813, took the generic kernels).  Local outputs on row windows at both ends, in the middle
+    and around row 21813; every dz row and dU / dstatic_w entry of each group against float64 sums."""
+    G, Bn, Tn, Dn, R, W = 3, 1, 32768, 4096, 15, 4
+    dtype = torch.bfloat16
+    print(f"[long grouped] G{G} B{Bn} T{Tn} D{Dn} R{R}+static W{W}", flush=True)
+    g = gen(23)
+    xw = randn(g, Bn, Tn, G * Dn).to(dtype)
+    zs = [randn(g, Bn, Tn, R).to(dtype) for _ in range(G)]
+    Us = [randn(g, R, W * Dn, scale=1 / math.sqrt((R + 1) * W)).to(dtype) for _ in range(G)]
+    sws = [uniform(g, W, Dn, lo=-1 / math.sqrt(W), hi=1 / math.sqrt(W)).to(dtype) for _ in range(G)]
+    dys = [randn(g, Bn, Tn, Dn).to(dtype) for _ in range(G)]
+    x_k = xw.to(DEV).requires_grad_()
+    zk = [t.to(DEV).requires_grad_() for t in zs]
+    Uk = [t.to(DEV).requires_grad_() for t in Us]
+    sk = [t.to(DEV).requires_grad_() for t in sws]
+    ys = lr_grouped(x_k, zk, Uk, sk, residual=True)
+    torch.autograd.backward(ys, [d.to(DEV) for d in dys])
+    torch.cuda.synchronize()
+    old_limit = (1 << 29) // (G * Dn * 2) - 32  # first row past the former per-sequence limit
+    windows = [(0, 64), (Tn // 2 - 32, Tn // 2 + 32), (Tn - 64, Tn), (old_limit - 40, old_limit + 24)]
+    dx_all = x_k.grad.cpu()
+    for gi in range(G):
+        xs = xw[..., gi * Dn:(gi + 1) * Dn].float()
+        y_k, dz_k = ys[gi].cpu(), zk[gi].grad.cpu()
+        for t0, t1 in windows:
+            a, e = max(0, t0 - W + 1), min(Tn, t1 + W - 1)
+            win = [xs[:, a:e].clone(), zs[gi][:, a:e].float(), Us[gi].float(), sws[gi].float()]
+            y_w, g_w = run_fwd_bwd(lr_ref, win, dys[gi][:, a:e].float(), True)
+            sl = slice(t0 - a, t1 - a)
+            assert_ns(y_k[:, t0:t1], y_w[:, sl], dtype, f"g{gi} y[{t0}:{t1}]")
+            assert_ns(dx_all[:, t0:t1, gi * Dn:(gi + 1) * Dn], g_w[0][:, sl], dtype, f"g{gi} dx[{t0}:{t1}]")
+        check_reductions("lr", [xs, zs[gi].float(), Us[gi].float(), sws[gi].float()], dys[gi].float(),
+                         [None, dz_k, Uk[gi].grad, sk[gi].grad], dtype, tag=f"g{gi} ")
 
 
 @pytest.mark.parametrize("static", [False, True])

@@ -357,13 +357,19 @@ def test_baseline_configs(cfg):
 
 # ---------------------------------------------------------- long sequence
 # One sequence of x spans more than 512 MiB (131172 rows of 2048 bf16): the
-# headwise kernels cap each run's buffer range at 512 MiB, and the lowrank
-# MFMA kernels (whose offsets cover one sequence) give way to the generic ones.
-# Local outputs are checked on row windows, including the rows around 512 MiB.
+# headwise and lowrank kernels give each run of tiles buffer resources that
+# start at the run's own first rows, so they stay on the vector / matrix-core
+# kernels.  Local outputs are checked on row windows, including the rows
+# around 512 MiB; the reductions over the whole sequence entry by entry.
 @pytest.mark.parametrize("kind", ["hw32", "lr16"])
 def test_long_sequence(kind):
     dtype = torch.bfloat16
     Bn, Tn, Dn, W = 1, 131172, 2048, 4
+    for bwd in (0, 1):
+        if kind == "hw32":
+            assert _path("hw", Bn, Tn, Dn, Dn // 32, W, dtype, True, bwd) == "vector"
+        else:
+            assert _path("lr", Bn, Tn, Dn, 15, W, dtype, True, bwd) == "mfma"
     g = gen(11)
     x = randn(g, Bn, Tn, Dn)
     dy = randn(g, Bn, Tn, Dn)
