@@ -394,9 +394,12 @@ def qkv_end_to_end(torch, dev, reps=10):
 
 def proj_in_gemm(torch, dev, reps=20):
     """The upstream proj_in GEMM of the grouped QKV module at configs[4] (README.md:67, 75): z = pre_z @ W_in^T
-    for all three groups at once ([B*T, D] x [D, 3R]), and its backward (dW_in = dz^T pre_z, d pre_z = dz W_in),
-    as torch (hipBLASLt) runs them: time per launch rotating over input sets that do not fit the MALL, and the
-    bandwidth each reaches on its algorithmic bytes (the GEMMs are far below the bf16 ridge: 2*3R flop/byte)."""
+    for all three groups at once ([B*T, D] x [D, 3R]), and its backward (dW_in = dz^T pre_z, d pre_z = dz W_in):
+    torch's GEMM (hipBLASLt, F.linear) against libdynconv.so's kernels (dc_proj_in_fwd / dc_proj_in_bwd), time per
+    launch rotating over input sets that do not fit the MALL, and the bandwidth each reaches on its algorithmic
+    bytes (the GEMMs are far below the bf16 ridge: 2*3R flop/byte)."""
+    from dynconv.modules import _ProjInFn
+
     c = EXTRA["lr_qkv_grouped"]
     B, T, D, R, G = c["B"], c["T"], c["D"], c["R"], c["G"]
     bf = torch.bfloat16
@@ -404,27 +407,37 @@ def proj_in_gemm(torch, dev, reps=20):
     pre = [torch.randn(B, T, D, device=dev).to(bf).requires_grad_() for _ in range(n)]
     win = (torch.randn(G * R, D, device=dev) / math.sqrt(D)).to(bf).requires_grad_()
     dz = [torch.randn(B, T, G * R, device=dev).to(bf) for _ in range(n)]
+    dzs = [[d[..., g * R:(g + 1) * R].contiguous() for g in range(G)] for d in dz]
     F = torch.nn.functional
-    zs = [F.linear(p, win) for p in pre]
-
-    def fwd(i):
-        F.linear(pre[i], win)
-
-    def bwd(i):
-        pre[i].grad = win.grad = None  # fresh gradients: no accumulation kernels in the timing
-        torch.autograd.backward(zs[i], dz[i], retain_graph=True)
-
-    f_us = time_launches(torch, fwd, n, reps)
-    b_us = time_launches(torch, bwd, n, reps)
     e = 2
     f_bytes = (B * T * D + G * R * D + B * T * G * R) * e
     b_bytes = (B * T * G * R + B * T * D + G * R * D) * e + (G * R * D + B * T * D) * e  # reads dz, pre_z, W_in
-    out = {"shape": f"[{B * T}, {D}] x [{D}, {G * R}] bf16",
-           "fwd_us": round(f_us, 2), "fwd_GBs": round(f_bytes / (f_us * 1e-6) / 1e9, 1),
-           "bwd_us": round(b_us, 2), "bwd_GBs": round(b_bytes / (b_us * 1e-6) / 1e9, 1),
-           "alg_MB": round((f_bytes + b_bytes) / 1e6, 1)}
-    print(f"[bench] proj_in GEMM (configs[4], 3 groups): fwd {f_us:.1f} us ({out['fwd_GBs']} GB/s), bwd {b_us:.1f} us "
-          f"({out['bwd_GBs']} GB/s)", file=sys.stderr, flush=True)
+    out = {"shape": f"[{B * T}, {D}] x [{D}, {G * R}] bf16", "alg_MB": round((f_bytes + b_bytes) / 1e6, 1)}
+    for name in ("torch_F.linear", "dynconv"):
+        if name == "dynconv":
+            zs = [_ProjInFn.apply(p, win, G, R) for p in pre]
+            grads = dzs
+
+            def fwd(i):
+                _ProjInFn.apply(pre[i], win, G, R)
+        else:
+            zs = [F.linear(p, win) for p in pre]
+            grads = dz
+
+            def fwd(i):
+                F.linear(pre[i], win)
+
+        def bwd(i):
+            pre[i].grad = win.grad = None  # fresh gradients: no accumulation kernels in the timing
+            torch.autograd.backward(zs[i], grads[i], retain_graph=True)
+
+        f_us = time_launches(torch, fwd, n, reps)
+        b_us = time_launches(torch, bwd, n, reps)
+        out[name] = {"fwd_us": round(f_us, 2), "fwd_GBs": round(f_bytes / (f_us * 1e-6) / 1e9, 1),
+                     "bwd_us": round(b_us, 2), "bwd_GBs": round(b_bytes / (b_us * 1e-6) / 1e9, 1)}
+        print(f"[bench] proj_in GEMM (configs[4], 3 groups) {name}: fwd {f_us:.1f} us ({out[name]['fwd_GBs']} GB/s), "
+              f"bwd {b_us:.1f} us ({out[name]['bwd_GBs']} GB/s)", file=sys.stderr, flush=True)
+        del zs
     return out
 
 

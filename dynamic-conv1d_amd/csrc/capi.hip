@@ -410,4 +410,62 @@ int dc_lowrank_bwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* c
   return launch_status(dc::lr_bwd(p, (int)G));
 }
 
+// ------------------------------------------------------------------ proj_in
+
+static int check_proj(int64_t G, int64_t M, int64_t K, int64_t R, int dtype, dc::ProjProblem* p) {
+  if (!dtype_ok(dtype)) return DC_ERR_DTYPE;
+  if (G < 1 || M <= 0 || K <= 0 || R <= 0) return DC_ERR_SHAPE;
+  if (G > DC_MAX_GROUPS) return DC_ERR_UNSUPPORTED;
+  if (M > kI32Max || K > kI32Max || G * R > kI32Max) return DC_ERR_SHAPE;
+  *p = dc::ProjProblem{};
+  p->G = G; p->M = M; p->K = K; p->R = R; p->dtype = dtype;
+  return dc::proj_shape_ok(*p) ? DC_OK : DC_ERR_UNSUPPORTED;
+}
+
+int dc_proj_in_fwd(const void* pre_z, const void* w_in, void* const* z, int64_t G, int64_t M, int64_t K, int64_t R,
+                   int dtype, void* stream) {
+  dc::ProjProblem p;
+  int s = check_proj(G, M, K, R, dtype, &p);
+  if (s != DC_OK) return s;
+  if (!pre_z || !w_in || !z) return DC_ERR_NULL;
+  if (!aligned_to(pre_z, 16) || !aligned_to(w_in, 16)) return DC_ERR_ALIGN;
+  for (int64_t g = 0; g < G; ++g) {
+    if (!z[g]) return DC_ERR_NULL;
+    if (!aligned_to(z[g], 2)) return DC_ERR_ALIGN;
+    p.z[g] = z[g];
+  }
+  if ((s = device_status()) != DC_OK) return s;
+  p.pre_z = pre_z; p.w_in = w_in; p.stream = (hipStream_t)stream;
+  return launch_status(dc::proj_fwd_launch(p));
+}
+
+int64_t dc_proj_in_bwd_ws_bytes(int64_t G, int64_t M, int64_t K, int64_t R, int dtype) {
+  dc::ProjProblem p;
+  int s = check_proj(G, M, K, R, dtype, &p);
+  if (s != DC_OK) return s;
+  return dc::proj_bwd_ws_bytes(p);
+}
+
+int dc_proj_in_bwd(const void* pre_z, const void* w_in, const void* const* dz, void* dpre_z, void* dw_in,
+                   void* workspace, int64_t ws_bytes, int64_t G, int64_t M, int64_t K, int64_t R, int dtype,
+                   void* stream) {
+  dc::ProjProblem p;
+  int s = check_proj(G, M, K, R, dtype, &p);
+  if (s != DC_OK) return s;
+  if (!pre_z || !w_in || !dz || !dpre_z || !dw_in) return DC_ERR_NULL;
+  if (!aligned_to(pre_z, 16) || !aligned_to(w_in, 16) || !aligned_to(dpre_z, 16) || !aligned_to(dw_in, 2))
+    return DC_ERR_ALIGN;
+  for (int64_t g = 0; g < G; ++g) {
+    if (!dz[g]) return DC_ERR_NULL;
+    if (!aligned_to(dz[g], 2)) return DC_ERR_ALIGN;
+    p.dz[g] = dz[g];
+  }
+  const int64_t need = dc::proj_bwd_ws_bytes(p);
+  if (workspace == nullptr || ws_bytes < need || !aligned_to(workspace, 16)) return DC_ERR_WORKSPACE;
+  if ((s = device_status()) != DC_OK) return s;
+  p.pre_z = pre_z; p.w_in = w_in; p.dpre_z = dpre_z; p.dw_in = dw_in; p.ws = (float*)workspace;
+  p.stream = (hipStream_t)stream;
+  return launch_status(dc::proj_bwd_launch(p));
+}
+
 }  // extern "C"

@@ -83,6 +83,26 @@ int64_t lr_zeff_bytes(const LrProblem& p);
 hipError_t lr_fwd(const LrProblem* p, int G);
 hipError_t lr_bwd(const LrProblem* p, int G);
 
+// ---------------------------------------------------------------- proj_in
+// z = pre_z W_in^T and its backward (proj_in.hip): pre_z [M, K], W_in [G*R, K],
+// z / dz as G tensors [M, R] (group g holds ranks g*R .. g*R+R-1).
+struct ProjProblem {
+  const void* pre_z;
+  const void* w_in;
+  void* z[kMaxGroups];         // forward outputs
+  const void* dz[kMaxGroups];  // backward inputs
+  void* dpre_z;
+  void* dw_in;
+  float* ws;                   // backward: dW_in partials
+  int64_t G, M, K, R;
+  int dtype;
+  hipStream_t stream;
+};
+bool proj_shape_ok(const ProjProblem& p);
+int64_t proj_bwd_ws_bytes(const ProjProblem& p);
+hipError_t proj_fwd_launch(const ProjProblem& p);
+hipError_t proj_bwd_launch(const ProjProblem& p);
+
 // ------------------------------------------------------------------ shared
 // out[c] = (T) sum_{p < P} part[p * pstride + c] for c < C, summed in a fixed
 // order (deterministic).

@@ -39,6 +39,9 @@ SIGNATURES = {
                        + [_c_int, _c_int, _c_vp]),
     "dc_lowrank_fwd_grouped": (_c_int, [_c_i64, _c_vp, _c_i64] + [_c_pp] * 5 + [_c_i64] * 7 + [_c_int, _c_int, _c_vp]),
     "dc_lowrank_bwd_grouped_ws_bytes": (_c_i64, [_c_i64] * 6 + [_c_int, _c_int]),
+    "dc_proj_in_fwd": (_c_int, [_c_vp, _c_vp, _c_pp] + [_c_i64] * 4 + [_c_int, _c_vp]),
+    "dc_proj_in_bwd_ws_bytes": (_c_i64, [_c_i64] * 4 + [_c_int]),
+    "dc_proj_in_bwd": (_c_int, [_c_vp, _c_vp, _c_pp, _c_vp, _c_vp, _c_vp, _c_i64] + [_c_i64] * 4 + [_c_int, _c_vp]),
     "dc_lowrank_bwd_grouped": (_c_int, [_c_i64, _c_vp, _c_i64] + [_c_pp] * 4 + [_c_i64] + [_c_pp]
                                + [_c_i64, _c_vp, _c_i64] + [_c_pp] * 3
                                + [_c_vp, _c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),

@@ -8,14 +8,76 @@ GroupedLowRankDynamicShortConvolution holds G such modules (the q, k and v
 convolutions of README.md:86-110) and runs them as one grouped operator: one
 proj_in GEMM for all groups, and one launch per direction that reads the fused
 [B, T, G*D] projection in place instead of three .contiguous() slices.
+
+The proj_in GEMM (README.md:67, 75) runs on libdynconv.so's own matrix-core
+kernels (dc_proj_in_fwd / dc_proj_in_bwd): skinny products bound by streaming
+pre_z, which the library GEMM runs at about a quarter of HBM bandwidth in the
+backward.  Shapes those kernels do not take (fp32, G*R > 128, d_model % 8 != 0,
+non-contiguous pre_z) use torch's GEMM (F.linear).
 """
 
 import math
 
 import torch
+import torch.nn.functional as F
 from torch import nn
 
+from . import _capi
 from .lowrank import lowrank_dynamic_convolution, lowrank_dynamic_convolution_grouped
+
+
+class _ProjInFn(torch.autograd.Function):
+    """z_g = (pre_z @ W_in^T)[..., g*R:(g+1)*R] for g < G, as G contiguous tensors, and its backward."""
+
+    @staticmethod
+    def forward(ctx, pre_z, w_in, G, R):
+        B, T, K = pre_z.shape
+        M = B * T
+        zs = [torch.empty(B, T, R, dtype=pre_z.dtype, device=pre_z.device) for _ in range(G)]
+        lib = _capi.load()
+        status = lib.dc_proj_in_fwd(_capi.ptr(pre_z), _capi.ptr(w_in), _capi.ptr_array(zs), G, M, K, R,
+                                    _capi.dtype_code(pre_z.dtype), _capi.stream_of(pre_z))
+        _capi.check(status, "proj_in forward")
+        ctx.save_for_backward(pre_z, w_in)
+        ctx.G, ctx.R = G, R
+        return tuple(zs)
+
+    @staticmethod
+    def backward(ctx, *dzs):
+        pre_z, w_in = ctx.saved_tensors
+        G, R = ctx.G, ctx.R
+        B, T, K = pre_z.shape
+        M = B * T
+        dzs = [torch.zeros(B, T, R, dtype=pre_z.dtype, device=pre_z.device) if d is None
+               else d.to(pre_z.dtype).contiguous() for d in dzs]
+        dpre = torch.empty_like(pre_z)
+        dw = torch.empty_like(w_in)
+        lib = _capi.load()
+        dtype = _capi.dtype_code(pre_z.dtype)
+        nws = lib.dc_proj_in_bwd_ws_bytes(G, M, K, R, dtype)
+        _capi.check(int(nws) if nws < 0 else 0, "proj_in backward workspace query")
+        ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=pre_z.device)
+        status = lib.dc_proj_in_bwd(_capi.ptr(pre_z), _capi.ptr(w_in), _capi.ptr_array(dzs), _capi.ptr(dpre),
+                                    _capi.ptr(dw), _capi.ptr(ws), nws, G, M, K, R, dtype, _capi.stream_of(pre_z))
+        _capi.check(status, "proj_in backward")
+        return dpre, dw, None, None
+
+
+def _proj_in_native(pre_z, w_in, G, R) -> bool:
+    """Whether the library's proj_in kernels take this call (else torch's GEMM)."""
+    return (pre_z.is_cuda and pre_z.dim() == 3 and pre_z.dtype in (torch.bfloat16, torch.float16)
+            and w_in.dtype == pre_z.dtype and pre_z.is_contiguous() and w_in.is_contiguous()
+            and G * R <= 128 and pre_z.shape[-1] % 8 == 0
+            and pre_z.data_ptr() % 16 == 0 and w_in.data_ptr() % 16 == 0)
+
+
+def proj_in(pre_z: torch.Tensor, w_in: torch.Tensor, G: int, R: int):
+    """The modules' proj_in GEMM for G groups: a tuple of G contiguous [B, T, R] tensors,
+    group g being pre_z @ w_in[g*R:(g+1)*R].T (README.md:67, 75)."""
+    if _proj_in_native(pre_z, w_in, G, R):
+        return _ProjInFn.apply(pre_z, w_in, G, R)
+    z = F.linear(pre_z, w_in)
+    return tuple(z[..., g * R:(g + 1) * R].contiguous() for g in range(G))
 
 
 def _check_rank(R: int) -> None:
@@ -37,7 +99,7 @@ class LowRankDynamicShortConvolution(nn.Module):
         nn.init.uniform_(self.proj_out_bias, -1.0 / math.sqrt(W), +1.0 / math.sqrt(W))
 
     def forward(self, x: torch.Tensor, pre_z: torch.Tensor) -> torch.Tensor:
-        z = self.proj_in(pre_z)
+        (z,) = proj_in(pre_z, self.proj_in.weight, 1, self.R)
         return lowrank_dynamic_convolution(
             x=x.contiguous(),
             z=z.contiguous(),
@@ -74,8 +136,7 @@ class GroupedLowRankDynamicShortConvolution(nn.Module):
 
     def forward(self, x: torch.Tensor, pre_z: torch.Tensor):
         G, R = self.groups, self.R
-        z = self.proj_in(pre_z)  # [B, T, G*R]: one GEMM for every group
-        zs = [z[..., g * R:(g + 1) * R].contiguous() for g in range(G)]
+        zs = list(proj_in(pre_z, self.proj_in.weight, G, R))  # one GEMM for every group
         Us = [self.proj_out[g] for g in range(G)]
         sws = [self.proj_out_bias[g] for g in range(G)]
         return lowrank_dynamic_convolution_grouped(x, zs, Us, static_w=sws, residual=True, head_dim=self.head_dim)

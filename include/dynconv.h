@@ -224,6 +224,31 @@ int dc_lowrank_bwd_grouped(int64_t G, const void* x, int64_t x_ld, const void* c
                            int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,
                            int dtype, int residual, void* stream);
 
+/* ------------------------------------------------------------- proj_in
+ * The lowrank module's upstream projection z = pre_z @ W_in^T (README.md:67,
+ * 75: nn.Linear(d_model, R, bias=False) applied to pre_z) and its backward,
+ * for G modules at once (the grouped q / k / v module: W_in rows g*R ..
+ * g*R+R-1 belong to group g).  pre_z [M, K] (M = B*T, K = d_model), W_in
+ * [G*R, K], z and dz: arrays of G tensors [M, R], dpre_z [M, K], dW_in
+ * [G*R, K]; bf16 or fp16, fp32 accumulation.  Needs G*R <= 128 and K % 8 == 0
+ * (DC_ERR_UNSUPPORTED otherwise, also for fp32: callers use a library GEMM
+ * then) and 16-byte aligned pre_z, W_in and dpre_z. */
+
+/* z[g] = (pre_z @ W_in^T)[:, g*R : g*R+R] for g < G. */
+int dc_proj_in_fwd(const void* pre_z, const void* w_in, void* const* z, int64_t G, int64_t M, int64_t K,
+                   int64_t R, int dtype, void* stream);
+
+/* Workspace bytes needed by dc_proj_in_bwd (fp32 partial sums of dW_in), or a
+ * negative dc_status. */
+int64_t dc_proj_in_bwd_ws_bytes(int64_t G, int64_t M, int64_t K, int64_t R, int dtype);
+
+/* dpre_z = dz_cat @ W_in and dW_in = dz_cat^T @ pre_z, where dz_cat is the G
+ * tensors dz[g] side by side ([M, G*R]), in one pass over pre_z; dW_in is
+ * summed in a fixed order (deterministic). */
+int dc_proj_in_bwd(const void* pre_z, const void* w_in, const void* const* dz, void* dpre_z, void* dw_in,
+                   void* workspace, int64_t ws_bytes, int64_t G, int64_t M, int64_t K, int64_t R, int dtype,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,7 +35,7 @@ def header_functions():
 
 def test_exports_every_declared_symbol(lib):
     names = header_functions()
-    assert len(names) == 15, names
+    assert len(names) == 18, names
     raw = ctypes.CDLL(_capi.LIB_PATH)
     for n in names:
         assert hasattr(raw, n), f"{n} declared in dynconv.h but not exported"
@@ -274,3 +274,31 @@ def test_kernel_paths(lib):
     assert hp(2, 8, 16, 3, 4, bf, 0, 0) == E_SHAPE
     assert lp(2, 8, 16, 0, 4, bf, 0, 0) == E_SHAPE
     assert lp(2, 8, 16, 4, 33, bf, 0, 1) == E_UNSUP
+
+
+def test_proj_in_validation(lib):
+    """dc_proj_in_*: shape limits of the matrix-core kernels (G*R <= 128, K % 8 == 0, 16-bit types),
+    pointers and workspace, before any device call."""
+    no_dev = not torch.cuda.is_available()
+    g3 = arr(P, P, P)
+    fwd = lambda G=3, M=64, K=256, R=31, dt=0, pre=P, w=P, z=g3: lib.dc_proj_in_fwd(pre, w, z, G, M, K, R, dt, None)  # noqa: E731
+    assert fwd(dt=7) == E_DTYPE
+    assert fwd(dt=2) == E_UNSUP          # fp32: a library GEMM takes it
+    assert fwd(R=43) == E_UNSUP          # G*R = 129 > 128
+    assert fwd(K=100) == E_UNSUP         # K % 8 != 0
+    assert fwd(G=5, z=arr(P, P, P, P, P)) == E_UNSUP
+    assert fwd(M=0) == E_SHAPE
+    assert fwd(pre=None) == E_NULL
+    assert fwd(z=arr(P, None, P)) == E_NULL
+    assert fwd(pre=P + 8) == E_ALIGN
+    need = lib.dc_proj_in_bwd_ws_bytes(3, 64, 256, 31, 0)
+    assert need > 0 and need % (3 * 31 * 256 * 4) == 0   # one fp32 dW_in partial per row run
+    bwd = lambda ws=P, nws=need, dz=g3, dpre=P: lib.dc_proj_in_bwd(P, P, dz, dpre, P, ws, nws, 3, 64, 256, 31, 0, None)  # noqa: E731
+    assert bwd(ws=None) == E_WS
+    assert bwd(nws=need - 4) == E_WS
+    assert bwd(dz=arr(P, P, None)) == E_NULL
+    assert bwd(dpre=P + 2) == E_ALIGN
+    if no_dev:
+        assert fwd() == E_DEV
+        assert fwd(G=1, z=arr(P), R=128) == E_DEV
+        assert bwd() == E_DEV
