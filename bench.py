@@ -83,6 +83,8 @@ EXTRA = {
     # the same grouped q|k|v op on one sequence of 32768 tokens (x spans 768 MiB): per-run buffer
     # resources keep it on the matrix-core kernels; per-token time against lr_qkv_grouped's 16384 tokens
     "lr_qkv_grouped_T32k": dict(kind="lrg", B=1, T=32768, D=4096, R=31, W=4, static=True, residual=True, G=3),
+    # configs[4]'s shape at W 8 (two rank chunks): the backward runs as two passes of 4 taps
+    "lr_qkv_W8": dict(kind="lr", B=2, T=8192, D=4096, R=31, W=8, static=True, residual=True),
     # the fp32 tier (reference test.py's 1e-5 cases) at the B4 shapes
     "hw_hs32_fp32": dict(kind="hw", B=4, T=4096, D=2048, H=64, W=4, static=True, residual=True, dtype="fp32"),
     "lr_r16_fp32": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=4, static=False, residual=True, dtype="fp32"),

@@ -204,9 +204,10 @@ hipError_t bwd_generic(const LrProblem& p) {
 bool lr_mfma_ok(const LrProblem& p, bool bwd) {
   if (p.dtype != kBF16 && p.dtype != kFP16) return false;
   if (p.W < 1 || p.W > 8) return false;
+  // every W <= 8 at every kernel rank <= 64: the forward stages W x RC operand
+  // chunks (up to 128 KiB of LDS); the backward runs wide W x RC as passes of taps
   const int64_t rc = (p.R + (p.static_w ? 1 : 0) + 15) / 16;
-  if (rc > 4 || p.W * rc > 8) return false;  // staged operands / accumulators bound W*RC
-  if (bwd && rc == 4 && p.W > 1) return false;  // backward LDS (operands + dz sums) above 160 KiB
+  if (rc > 4) return false;
   // buffer-offset range of a run (resources start at each run's base row, so
   // the sequence length is free): at least one tile must fit
   if ((bwd ? lr_bwd_max_run_tiles(p) : lr_fwd_max_run_tiles(p)) < 1) return false;

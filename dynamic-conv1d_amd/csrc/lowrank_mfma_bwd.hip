@@ -83,6 +83,9 @@ struct LrBwdArgs {
   // workspace (zld = zr = zrk = RP, the static column included).
   int zld, zr, zrk;
   int yhd;    // dy layout: D ([B, T, D]) or the head dim of [B, D/yhd, T, yhd]
+  int uld;    // row stride of U and of the dU partials: the problem's W * D (all taps)
+  int kofs;   // first tap of this pass (0 without a tap split)
+  int accdx;  // add dx to what an earlier pass stored
   int64_t BT;
   LrBwdGroup grp[kMaxGroups];
 };
@@ -127,14 +130,17 @@ template <int W, int RC, bool UWREG, int NJ, int NS, bool STAGE_UW = true>
 __device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds,
                                            u32x2 (&uw_reg)[UWREG && STAGE_UW ? W * RC * NJ : 1],
                                            u32x4* __restrict__ uz_lds, const uint16_t* __restrict__ U,
-                                           const uint16_t* __restrict__ sw, int R, int RK, int D, int d0, int q,
-                                           int n, int lane) {
+                                           const uint16_t* __restrict__ sw, int R, int RK, int D, int uld, int d0,
+                                           int q, int n, int lane) {
   typedef LaneVec<NJ> LV;
-  const int WD = W * D;  // R * W * D * 2 bytes lie below kOobLane (host check)
+  // U rows are uld elements apart (the whole problem's W*D: a pass of taps
+  // starts U at its first tap's columns); R * uld * 2 bytes lie below kOobLane
+  // (host check).  sw starts at the pass's first tap too.
+  const int WD = uld;
   // Buffer loads, all issued before the first use: rows r >= R of U and lanes
   // outside D read 0; the static row (r == R < RK) is read from sw and OR-ed in.
   const rsrc_t ru = make_rsrc(U, (int64_t)R * WD * 2);
-  const rsrc_t rs = make_rsrc(sw, RK > R ? (int64_t)WD * 2 : 0);
+  const rsrc_t rs = make_rsrc(sw, RK > R ? (int64_t)W * D * 2 : 0);
   const int cw = d0 + NJ * n < D ? (d0 + NJ * n) * 2 : kOobLane;  // the lane's tap-weight channels
   typename LV::type rows[W][RC][4];
   u32x4 zr[W][RC][NS];
@@ -184,12 +190,12 @@ __device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds,
 // whose A is z_eff row n, ranks 8q..8q+7).  Row R (< RK) is static_w.
 template <int W, int NJ>
 __device__ __forceinline__ void stage_uw32(u32x4 (&uw)[W * NJ], const uint16_t* __restrict__ U,
-                                           const uint16_t* __restrict__ sw, int R, int RK, int D, int d0, int q,
-                                           int n) {
+                                           const uint16_t* __restrict__ sw, int R, int RK, int D, int uld, int d0,
+                                           int q, int n) {
   typedef LaneVec<NJ> LV;
-  const int WD = W * D;
+  const int WD = uld;  // U row stride (see stage_uops)
   const rsrc_t ru = make_rsrc(U, (int64_t)R * WD * 2);
-  const rsrc_t rs = make_rsrc(sw, RK > R ? (int64_t)WD * 2 : 0);
+  const rsrc_t rs = make_rsrc(sw, RK > R ? (int64_t)W * D * 2 : 0);
   const int cw = d0 + NJ * n < D ? (d0 + NJ * n) * 2 : kOobLane;
   typename LV::type rows[W][8];
 #pragma unroll
@@ -279,7 +285,6 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   const int d0 = chunk * CPW;
   const int col = d0 + NJ * n;
   const bool chv = col < D;  // the lane's channels inside D (D % 16 == 0)
-  const int64_t WD = (int64_t)W * D;
   const int ntile = (Tn + 15) >> 4;
   // Run s of the grid: tiles [tile0, tile1) of sequence b, whose buffer
   // resources start at row rb (run_base_row).  A workgroup's last run can lie
@@ -321,7 +326,14 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   uint8_t* const my_g = gtile[wave];
   const int gw_lane = q * GPL + NJ * 8 * n + (n / (16 / NJ)) * 8;
   const int gr_lane = (n & 3) * GPL + (8 * q + (n >> 2)) * 8 + (q >> 1) * 8;
-  const float res = a.residual ? 1.f : 0.f;  // tap 0's weight + 1: the residual term dy
+  const float res = a.residual && a.kofs == 0 ? 1.f : 0.f;  // tap 0's weight + 1: the residual term dy
+  // A pass of taps kofs .. kofs+W-1 (the host splits W when the tap-weight
+  // operands of all taps do not fit): it is the W-tap problem on x shifted
+  // down by kofs rows, so x rows are read kofs rows earlier and its dx rows
+  // land kofs rows earlier (rows before 0 are the causal padding: dropped),
+  // added to what the previous passes stored (accdx).
+  const int kofs = a.kofs;
+  const bool accdx = a.accdx != 0;
   // dy is [B, T, D] (yhd == D) or head-major [B, D/yhd, T, yhd]; the host takes
   // this path only when yhd % CPW == 0, so a wavefront's channels lie in one
   // head and its dy resource covers that head's [T, yhd] block (rows past T
@@ -390,7 +402,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     // The scatter form also reads dy and z of the tile after the run: its
     // first rows close the run's last dx rows.
     const bool ylive = SC ? tile <= tile1 : live;
-    const int xtoff = live ? (tile * 16 - rb) * xrowb : kOobTile;
+    const int xtoff = live ? (tile * 16 - rb - kofs) * xrowb : kOobTile;
     const int toff = ylive ? (tile * 16 - rb) * rowb : kOobTile;
 #pragma unroll
     for (int m = 0; m < NR; ++m) in.xr[m] = LV::load(rx, xlane_off + xtoff + (m - (W - 1)) * xrowb);
@@ -433,8 +445,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     const bool top = q == 3;
     const bool cur_live = tile < tile1;
     const bool prev_live = tile > tile0 && tile <= tile1;
-    const int cur_off = cur_live ? dxlane_off + (tile * 16 - rb) * dxrowb : kOobTile;
-    const int prev_off = prev_live ? dxlane_off + ((tile - 1) * 16 - rb) * dxrowb : kOobTile;
+    const int cur_off = cur_live ? dxlane_off + (tile * 16 - rb - kofs) * dxrowb : kOobTile;
+    const int prev_off = prev_live ? dxlane_off + ((tile - 1) * 16 - rb - kofs) * dxrowb : kOobTile;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       constexpr int kFirstOpen = 4 - NOPEN;
@@ -446,7 +458,13 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
         if (open) b = (top ? carry[i - kFirstOpen][j] : b) + recv[3 - i][j];
         v[j] = b;
       }
-      LV::store(LV::template pack<T>(v), rdx, (top && open ? prev_off : cur_off) + i * dxrowb);
+      const int off = (top && open ? prev_off : cur_off) + i * dxrowb;
+      if (accdx) {  // wave-uniform: a later pass of taps adds to the stored rows
+        const typename LV::type o = LV::load(rdx, off);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) v[j] += Mma16<T>::to_f(LV::elem(o, j));
+      }
+      LV::store(LV::template pack<T>(v), rdx, off);
     }
 #pragma unroll
     for (int i = 0; i < NOPEN; ++i)
@@ -484,7 +502,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     const int tile = tile0 + it;
     const bool live = tile < tile1;
     const int t0 = tile * 16;
-    const int dxtoff = live ? (t0 - rb) * dxrowb : kOobTile;  // tiles past the run store nothing
+    const int dxtoff = live ? (t0 - rb - kofs) * dxrowb : kOobTile;  // tiles past the run store nothing
     const typename LV::type(&xr)[NR] = in.xr;
     const typename LV::type(&dyr)[NDY] = in.dyr;
     ZO zA[NB];
@@ -580,7 +598,15 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
       close_rows(dxa, S, tile);
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) LV::store(LV::template pack<T>(dxa[i]), rdx, dxlane_off + dxtoff + i * dxrowb);
+      for (int i = 0; i < 4; ++i) {
+        const int off = dxlane_off + dxtoff + i * dxrowb;
+        if (accdx) {  // wave-uniform: a later pass of taps adds to the stored rows
+          const typename LV::type o = LV::load(rdx, off);
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) dxa[i][j] += Mma16<T>::to_f(LV::elem(o, j));
+        }
+        LV::store(LV::template pack<T>(dxa[i]), rdx, off);
+      }
     }
     // ---- dz: gather this wavefront's tile sums; every DZB iterations (and at the
     // last one) add each run's NCW chunk wavefronts in wave order, one partial per group.
@@ -627,8 +653,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   TileIn ta, tb;
   load_tile(tile0, ta);
   __builtin_amdgcn_sched_barrier(0);  // the first tile's loads go out before the U staging waits
-  stage_uops<W, RC, UWREG, NJ, NS, !K32>(my_uw, uw_reg, my_uz, U, sw, R, RK, D, d0, q, n, lane);
-  if constexpr (K32) stage_uw32<W, NJ>(uw32, U, sw, R, RK, D, d0, q, n);
+  stage_uops<W, RC, UWREG, NJ, NS, !K32>(my_uw, uw_reg, my_uz, U, sw, R, RK, D, a.uld, d0, q, n, lane);
+  if constexpr (K32) stage_uw32<W, NJ>(uw32, U, sw, R, RK, D, a.uld, d0, q, n);
   for (int it = 0; it < nit; it += 2) {
     load_tile(tile0 + it + 1, tb);
     __builtin_amdgcn_sched_barrier(0);  // issue the next tile's loads before this tile's waits
@@ -702,15 +728,18 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   // CPW columns per tap.  The resource spans this row's RK x W*D partial, so
   // rows r >= RK fall outside it (the host keeps (RK + 16) * W * D * 4 bytes
   // below kOobLane, so no offset wraps).
-  const rsrc_t rdu = make_rsrc(part_du + (int64_t)sp * RK * WD, (int64_t)RK * WD * 4);
-  const int du_lane = chv ? (4 * q * (int)WD + col) * 4 : kOobLane;
+  // The partial's rows are uld (all taps' W*D) floats apart; a pass of taps
+  // writes its own taps' columns (part_du starts at its first tap's).
+  const int UL = a.uld;
+  const rsrc_t rdu = make_rsrc(part_du + (int64_t)sp * RK * UL, (int64_t)RK * UL * 4);
+  const int du_lane = chv ? (4 * q * UL + col) * 4 : kOobLane;
 #pragma unroll
   for (int k = 0; k < W; ++k)
 #pragma unroll
     for (int c = 0; c < RC; ++c)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int off = du_lane + ((16 * c + i) * (int)WD + k * D) * 4;
+        const int off = du_lane + ((16 * c + i) * UL + k * D) * 4;
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
           __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(du[k][c][j][i]), rdu, off + 4 * j, 0, 0);
@@ -730,6 +759,15 @@ constexpr BwdShape bwd_shape(int W, int RC) {
   return BwdShape{(RC == 2 && W <= 4) ? 32 : 64, (RC == 1 && W <= 4) ? 2 : 1};
 }
 
+// Taps per backward pass: what one pass's tap-weight and dz operands (registers
+// and LDS) and dU accumulators hold for RC rank chunks.  Wider problems run as
+// consecutive passes of taps kofs .. kofs+taps-1 (see the kernel's kofs): every
+// W <= 8 at every rank <= 64 stays on matrix cores, reading x and dy once per pass.
+constexpr int pass_taps(int W, int RC) {
+  return RC == 1 ? W : RC == 2 ? (W < 4 ? W : 4) : RC == 3 ? (W < 2 ? W : 2) : 1;
+}
+constexpr int npasses(int W, int RC) { return (W + pass_taps(W, RC) - 1) / pass_taps(W, RC); }
+
 }  // namespace
 
 // Longest backward run (tiles) whose resources fit (see run_rsrc): rows of x,
@@ -747,7 +785,7 @@ namespace {
 LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   LrBwdArgs a;
   const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
-  const BwdShape sh = bwd_shape((int)p.W, rc);
+  const BwdShape sh = bwd_shape(pass_taps((int)p.W, rc), rc);  // every pass has the same shape
   const int ncw = 256 / sh.cpw;
   a.Tn = (int)p.T;
   a.D = (int)p.D;
@@ -770,6 +808,9 @@ LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   a.BT = p.B * p.T;
   a.zld = a.zr = (int)p.R;
   a.zrk = a.RK;
+  a.uld = (int)(p.W * p.D);
+  a.kofs = 0;
+  a.accdx = 0;
   return a;
 }
 
@@ -827,15 +868,16 @@ hipError_t launch_zpad(const LrProblem* p, int G, void* const* dst) {
 
 constexpr int kBwdTargetWaves = 2048;
 
-// Workspace: [dz partials: ncg x BT x R fp32][dU partials: npair x RK x W*D fp32]
-// [padded z_eff: BT x RP of z's type], each 256-byte aligned.  The z_eff part
-// is reserved whatever the pointers' alignment (the size query has none).
+// Workspace: [dz partials: passes x ncg x BT x R fp32][dU partials: npair x RK
+// x W*D fp32][padded z_eff: BT x RP of z's type], each 256-byte aligned.  The
+// z_eff part is reserved whatever the pointers' alignment (the size query has none).
 struct BwdWs {
   int64_t dz_off, du_off, zp_off, total;
 };
 BwdWs bwd_ws(const LrProblem& p, const LrBwdArgs& a) {
   BwdWs w;
-  const int64_t dz = (int64_t)a.ncg * a.BT * a.R * 4;
+  const int rc = (a.RK + 15) / 16;
+  const int64_t dz = (int64_t)npasses((int)p.W, rc) * a.ncg * a.BT * a.R * 4;
   w.dz_off = 0;
   w.du_off = (dz + 255) / 256 * 256;
   w.zp_off = (w.du_off + (int64_t)a.npair * a.RK * p.W * p.D * 4 + 255) / 256 * 256;
@@ -844,9 +886,32 @@ BwdWs bwd_ws(const LrProblem& p, const LrBwdArgs& a) {
 }
 
 template <typename T, int W, int RC>
-hipError_t launch_bwd(const LrProblem* p, int G) {
+hipError_t launch_bwd_kernel(const LrBwdArgs& a, hipStream_t stream) {
   constexpr BwdShape SH = bwd_shape(W, RC);  // as make_bwd_args
   constexpr int NRW = SH.nrw, CPW = SH.cpw, NT = 64 * (256 / CPW) * NRW;
+  lr_bwd_mfma<T, W, RC, NRW, CPW><<<a.nblk, NT, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+// One pass's kernel for wq taps and rc rank chunks (the instantiated pairs:
+// pass_taps(W, RC) and the last pass's remainder).
+template <typename T>
+hipError_t dispatch_bwd_kernel(const LrBwdArgs& a, int wq, int rc, hipStream_t stream) {
+#define DC_LR_CASE(WW, CC) \
+  if (wq == WW && rc == CC) return launch_bwd_kernel<T, WW, CC>(a, stream);
+  DC_LR_CASE(1, 1) DC_LR_CASE(2, 1) DC_LR_CASE(3, 1) DC_LR_CASE(4, 1)
+  DC_LR_CASE(5, 1) DC_LR_CASE(6, 1) DC_LR_CASE(7, 1) DC_LR_CASE(8, 1)
+  DC_LR_CASE(1, 2) DC_LR_CASE(2, 2) DC_LR_CASE(3, 2) DC_LR_CASE(4, 2)
+  DC_LR_CASE(1, 3) DC_LR_CASE(2, 3)
+  DC_LR_CASE(1, 4)
+#undef DC_LR_CASE
+  return hipErrorInvalidValue;
+}
+
+template <typename T>
+hipError_t launch_bwd(const LrProblem* p, int G) {
+  const int rc = (int)((p[0].R + (p[0].static_w ? 1 : 0) + 15) / 16);
+  const int W = (int)p[0].W, wp = pass_taps(W, rc), np = npasses(W, rc);
   LrBwdArgs a = make_bwd_args(p[0], kBwdTargetWaves);
   const BwdWs w = bwd_ws(p[0], a);
   a.nblk1 = a.nblk;
@@ -856,7 +921,7 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
   a.yhd = (int)p[0].yhd();
   // z itself when its rows are what the kernel reads: R % 4 == 0 and 8-byte
   // aligned, or (two rank chunks) exactly 32 dynamic ranks, 16-byte aligned.
-  constexpr bool K32 = RC == 2;
+  const bool K32 = rc == 2;
   bool zvec = K32 ? (p[0].R == 32 && p[0].static_w == nullptr) : p[0].R % 4 == 0;
   for (int g = 0; g < G; ++g) {
     float* pdz = (float*)((char*)p[g].ws + w.dz_off);
@@ -876,10 +941,23 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
     for (int g = 0; g < G; ++g) a.grp[g].z = zp[g];
     a.zld = a.zr = a.zrk = (int)zpad_ranks(p[0]);
   }
-  lr_bwd_mfma<T, W, RC, NRW, CPW><<<a.nblk, NT, 0, p[0].stream>>>(a);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  const int64_t WD = p[0].W * p[0].D, RKWD = (int64_t)a.RK * WD, R = p[0].R;
+  const int64_t D = p[0].D, WD = p[0].W * D, RKWD = (int64_t)a.RK * WD, R = p[0].R;
+  const int64_t dz_slot = (int64_t)a.ncg * a.BT * R;  // one pass's dz partials
+  for (int ps = 0; ps < np; ++ps) {
+    // pass ps: taps kofs .. kofs+wq-1 (U, static_w and the dU partials start at
+    // the pass's first tap; its dz partials take their own slots)
+    const int kofs = ps * wp, wq = W - kofs < wp ? W - kofs : wp;
+    LrBwdArgs b = a;
+    b.kofs = kofs;
+    b.accdx = ps > 0;
+    for (int g = 0; g < G; ++g) {
+      b.grp[g].U = (const uint16_t*)p[g].U + kofs * D;
+      b.grp[g].sw = p[g].static_w ? (const void*)((const uint16_t*)p[g].static_w + kofs * D) : nullptr;
+      b.grp[g].part_dz = a.grp[g].part_dz + ps * dz_slot;
+      b.grp[g].part_du = a.grp[g].part_du + kofs * D;
+    }
+    if ((e = dispatch_bwd_kernel<T>(b, wq, rc, p[0].stream)) != hipSuccess) return e;
+  }
   PartialReduce jobs[kMaxReduceJobs];
   int nj = 0;
   for (int g = 0; g < G; ++g) {
@@ -887,26 +965,10 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
     const float* pdu = a.grp[g].part_du;
     jobs[nj++] = {pdu, RKWD, a.npair, R * WD, p[g].dU};
     jobs[nj++] = {pdu + R * WD, RKWD, a.npair, p[g].static_w ? WD : 0, p[g].dstatic_w};
-    jobs[nj++] = {pdz, a.BT * R, a.ncg, a.BT * R, p[g].dz};
+    jobs[nj++] = {pdz, a.BT * R, np * a.ncg, a.BT * R, p[g].dz};
   }
   return reduce_partials_multi(jobs, nj, p[0].dtype, p[0].stream);
 }
-
-template <typename T>
-hipError_t dispatch_bwd(const LrProblem* pp, int G) {
-  const LrProblem& p = pp[0];
-  const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
-#define DC_LR_CASE(WW, CC) \
-  if (p.W == WW && rc == CC) return launch_bwd<T, WW, CC>(pp, G);
-  DC_LR_CASE(1, 1) DC_LR_CASE(1, 2) DC_LR_CASE(1, 3) DC_LR_CASE(1, 4)
-  DC_LR_CASE(2, 1) DC_LR_CASE(2, 2) DC_LR_CASE(2, 3)
-  DC_LR_CASE(3, 1) DC_LR_CASE(3, 2)
-  DC_LR_CASE(4, 1) DC_LR_CASE(4, 2)
-  DC_LR_CASE(5, 1) DC_LR_CASE(6, 1) DC_LR_CASE(7, 1) DC_LR_CASE(8, 1)
-#undef DC_LR_CASE
-  return hipErrorInvalidValue;
-}
-
 
 }  // namespace
 
@@ -919,7 +981,7 @@ hipError_t lr_zeff_fill(const LrProblem* p, int G) {
 }
 
 hipError_t lr_mfma_bwd(const LrProblem* p, int G) {
-  return p[0].dtype == kBF16 ? dispatch_bwd<bf16>(p, G) : dispatch_bwd<fp16>(p, G);
+  return p[0].dtype == kBF16 ? launch_bwd<bf16>(p, G) : launch_bwd<fp16>(p, G);
 }
 
 }  // namespace dc

@@ -269,8 +269,12 @@ def test_kernel_paths(lib):
         assert lp(1, 40, 128, 40, 2, f16, 0, bwd) == 2         # kernel rank 40, W 2
     assert lp(1, 300, 64, 1, 1, f32, 0, 0) == 3                # fp32 W 1: forward on fp32 matrix cores,
     assert lp(1, 300, 64, 1, 1, f32, 0, 1) == 4                # backward on the VALU kernels
-    assert lp(2, 50, 256, 63, 2, bf, 1, 0) == 2                # kernel rank 64, W 2: forward on matrix cores,
-    assert lp(2, 50, 256, 63, 2, bf, 1, 1) == 0                # the backward's LDS would exceed 160 KiB
+    for bwd in (0, 1):                                         # every W <= 8 at every kernel rank <= 64:
+        assert lp(2, 50, 256, 63, 2, bf, 1, bwd) == 2          # the backward as passes of taps
+        assert lp(2, 8192, 4096, 31, 8, bf, 1, bwd) == 2       # W 8, two rank chunks
+        assert lp(1, 64, 256, 40, 5, f16, 0, bwd) == 2         # W 5, three rank chunks
+        assert lp(1, 64, 256, 63, 8, bf, 1, bwd) == 2          # W 8, four rank chunks
+        assert lp(1, 64, 256, 64, 8, bf, 1, bwd) == 0          # kernel rank 65: generic
     assert hp(2, 8, 16, 3, 4, bf, 0, 0) == E_SHAPE
     assert lp(2, 8, 16, 0, 4, bf, 0, 0) == E_SHAPE
     assert lp(2, 8, 16, 4, 33, bf, 0, 1) == E_UNSUP

@@ -201,9 +201,17 @@ LR_EDGE = [
     (1, 40, 64, 40, 4, False, False, torch.float32),    # kernel rank 40: generic kernels
     # matrix-core plans with three and four rank chunks (kernel ranks 33-64 at W 1-2)
     (1, 70, 128, 64, 1, False, True, torch.bfloat16, ("mfma", "mfma")),      # <W1, 4 chunks>
-    (2, 50, 256, 63, 2, True, True, torch.bfloat16, ("mfma", "generic")),    # <W2, 4 chunks> forward only
+    (2, 50, 256, 63, 2, True, True, torch.bfloat16, ("mfma", "mfma")),       # <W2, 4 chunks>: backward in 2 passes
     (1, 40, 128, 40, 2, False, False, torch.float16, ("mfma", "mfma")),      # <W2, 3 chunks>
     (2, 60, 128, 40, 1, True, True, torch.bfloat16, ("mfma", "mfma")),       # <W1, 3 chunks>, kernel rank 41
+    # wide W x rank: the backward runs passes of taps (x shifted by each pass's first tap,
+    # dx accumulated, dz partials per pass), the forward stages every tap's operands
+    (2, 70, 128, 31, 8, True, True, torch.bfloat16, ("mfma", "mfma")),       # W 8, 2 chunks: 2 passes
+    (1, 100, 256, 20, 6, False, False, torch.bfloat16, ("mfma", "mfma")),    # W 6, 2 chunks: passes of 4 + 2
+    (2, 45, 128, 40, 5, False, True, torch.float16, ("mfma", "mfma")),       # W 5, 3 chunks: passes 2 + 2 + 1
+    (1, 60, 256, 63, 8, True, True, torch.bfloat16, ("mfma", "mfma")),       # W 8, 4 chunks: 8 passes of 1
+    (1, 3216, 256, 31, 7, True, True, torch.bfloat16, ("mfma", "mfma")),     # W 7: passes of 4 + 3, long runs
+    (2, 37, 64, 47, 3, True, False, torch.bfloat16, ("mfma", "mfma")),       # W 3, 3 chunks: passes 2 + 1
     # widths above 8 and kernel ranks above 64 (the generic kernels; the reference accepts any
     # W and power-of-two ranks, lowrank.py:220, 331-333)
     (1, 45, 64, 127, 12, True, True, torch.bfloat16, ("generic", "generic")),  # W 12, kernel rank 128
