@@ -222,7 +222,10 @@ __device__ __forceinline__ void stage_uw32(u32x4 (&uw)[W * NJ], const uint16_t* 
 template <int RC, bool K32> struct ZOp { u32x2 c[RC]; };
 template <int RC> struct ZOp<RC, true> { u32x4 v; };
 
-template <typename T, int W, int RC, int NRW, int CPW>
+// ACC: a later pass of taps (the host splits wide W), which adds its dx to
+// what the earlier passes stored; a separate instantiation, so single-pass
+// launches carry none of it.
+template <typename T, int W, int RC, int NRW, int CPW, bool ACC>
 __global__ __launch_bounds__(64 * (256 / CPW) * NRW)
 __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))) void lr_bwd_mfma(LrBwdArgs a) {
   constexpr int NJ = CPW / 16;     // channels per lane
@@ -332,8 +335,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   // down by kofs rows, so x rows are read kofs rows earlier and its dx rows
   // land kofs rows earlier (rows before 0 are the causal padding: dropped),
   // added to what the previous passes stored (accdx).
-  const int kofs = a.kofs;
-  const bool accdx = a.accdx != 0;
+  const int kofs = ACC ? a.kofs : 0;  // the first pass (or the only one) starts at tap 0: a constant
+                                       // keeps the single-pass kernels' offsets as lean as before
   // dy is [B, T, D] (yhd == D) or head-major [B, D/yhd, T, yhd]; the host takes
   // this path only when yhd % CPW == 0, so a wavefront's channels lie in one
   // head and its dy resource covers that head's [T, yhd] block (rows past T
@@ -396,6 +399,9 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     typename LV::type xr[NR], dyr[NDY];
     ZR zr[K32 ? 1 : NB];   // z_eff rows t0+4bb+n, ranks 16c+4q..+3: A operand of the tap-weight MFMA
     u32x4 z32[K32 ? NB : 1];  // K32: z_eff rows t0+4bb+n, ranks 8q..8q+7
+    // ACC: the earlier passes' dx of the tile's rows 4q..4q+3 (shifted by kofs),
+    // loaded with the tile's inputs so that the adds before the stores do not wait
+    typename LV::type dxo[ACC ? 4 : 1];
   };
   auto load_tile = [&](int tile, TileIn& in) {
     const bool live = tile < tile1;
@@ -419,6 +425,11 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
       else
         in.zr[bb].load(rz, ylive ? (tile * 16 + 4 * bb + n - rb) * zld * 2 : kOobTile, zr, q);
     }
+    if constexpr (ACC) {
+      const int dxo_off = live ? dxlane_off + (tile * 16 - rb - kofs) * dxrowb : kOobTile;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) in.dxo[i] = LV::load(rdx, dxo_off + i * dxrowb);
+    }
   };
 
   // Scatter form: S[m] holds the lane's contributions to row 4q-1-m (the group
@@ -434,7 +445,11 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   for (int i = 0; i < NOPEN; ++i)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) carry[i][j] = 0.f;
-  auto close_rows = [&](const float(&own)[4][NJ], const float(&S)[NSC][NJ], int tile) {
+  // ACC: group 3's open rows are stored one tile late; their earlier-pass dx
+  // (loaded with the tile before) waits here
+  typename LV::type dxo_carry[ACC ? NOPEN : 1] = {};  // the first tile's open rows store nothing
+  auto close_rows = [&](const float(&own)[4][NJ], const float(&S)[NSC][NJ], int tile,
+                        const typename LV::type(&dxo)[ACC ? 4 : 1]) {
     const int src = ((lane + 16) & 63) << 2;  // ds_bpermute byte index of the group below
     float recv[NSC][NJ];
 #pragma unroll
@@ -459,8 +474,9 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
         v[j] = b;
       }
       const int off = (top && open ? prev_off : cur_off) + i * dxrowb;
-      if (accdx) {  // wave-uniform: a later pass of taps adds to the stored rows
-        const typename LV::type o = LV::load(rdx, off);
+      if constexpr (ACC) {  // a later pass of taps adds to the stored rows
+        typename LV::type o = dxo[ACC ? i : 0];
+        if (open) o = top ? dxo_carry[ACC ? i - kFirstOpen : 0] : o;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) v[j] += Mma16<T>::to_f(LV::elem(o, j));
       }
@@ -470,6 +486,10 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     for (int i = 0; i < NOPEN; ++i)
 #pragma unroll
       for (int j = 0; j < NJ; ++j) carry[i][j] = own[4 - NOPEN + i][j];
+    if constexpr (ACC) {
+#pragma unroll
+      for (int i = 0; i < NOPEN; ++i) dxo_carry[i] = dxo[4 - NOPEN + i];
+    }
   };
   // Tap weights of the lane's rows 4q..4q+3 (row block 0) times dy: into
   // `own` for rows of the lane, into S for rows of the group above.
@@ -595,15 +615,14 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
 
     // ---- dx rows (the residual dy rides on tap 0's weight); out-of-range stores are dropped
     if constexpr (SC) {
-      close_rows(dxa, S, tile);
+      close_rows(dxa, S, tile, in.dxo);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int off = dxlane_off + dxtoff + i * dxrowb;
-        if (accdx) {  // wave-uniform: a later pass of taps adds to the stored rows
-          const typename LV::type o = LV::load(rdx, off);
+        if constexpr (ACC) {  // a later pass of taps adds to the stored rows (loaded with the tile)
 #pragma unroll
-          for (int j = 0; j < NJ; ++j) dxa[i][j] += Mma16<T>::to_f(LV::elem(o, j));
+          for (int j = 0; j < NJ; ++j) dxa[i][j] += Mma16<T>::to_f(LV::elem(in.dxo[ACC ? i : 0], j));
         }
         LV::store(LV::template pack<T>(dxa[i]), rdx, off);
       }
@@ -691,7 +710,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
       for (int k = 1; k < W; ++k)
 #pragma unroll
         for (int j = 0; j < NJ; ++j) scatter_taps(zA0, dyf, k, j, own, S);
-      close_rows(own, S, tile);
+      close_rows(own, S, tile, in.dxo);
     };
     if (nit & 1)
       flush(tb);
@@ -889,7 +908,13 @@ template <typename T, int W, int RC>
 hipError_t launch_bwd_kernel(const LrBwdArgs& a, hipStream_t stream) {
   constexpr BwdShape SH = bwd_shape(W, RC);  // as make_bwd_args
   constexpr int NRW = SH.nrw, CPW = SH.cpw, NT = 64 * (256 / CPW) * NRW;
-  lr_bwd_mfma<T, W, RC, NRW, CPW><<<a.nblk, NT, 0, stream>>>(a);
+  if constexpr (RC >= 2) {  // only problems of 2+ rank chunks run several passes
+    if (a.accdx) {
+      lr_bwd_mfma<T, W, RC, NRW, CPW, true><<<a.nblk, NT, 0, stream>>>(a);
+      return hipGetLastError();
+    }
+  }
+  lr_bwd_mfma<T, W, RC, NRW, CPW, false><<<a.nblk, NT, 0, stream>>>(a);
   return hipGetLastError();
 }
 
