@@ -406,6 +406,35 @@ def test_long_sequence(kind):
     check_reductions("hw" if kind == "hw32" else "lr", q, dyq, g_k, dtype)
 
 
+def test_generic_lowrank_rows_past_2_24():
+    """The generic lowrank backward (D = 8 is off its matrix-core path; the forward takes the
+    matrix cores) over more than 2^24 rows: the per-row dz launch loops over rows with a capped
+    grid (one workgroup per row would ask for more than 2^32 work-items).  Row windows at both
+    ends against the oracle; dz, dU and dstatic_w entry by entry against float64 sums over the
+    whole sequence."""
+    dtype = torch.bfloat16
+    Bn, Tn, Dn, R, W = 1, (1 << 24) + 40, 8, 3, 4  # R + static = 4 (the API's power of two)
+    assert _path("lr", Bn, Tn, Dn, R, W, dtype, True, 0) == "mfma"
+    assert _path("lr", Bn, Tn, Dn, R, W, dtype, True, 1) == "generic"
+    g = gen(13)
+    x = randn(g, Bn, Tn, Dn)
+    dy = randn(g, Bn, Tn, Dn)
+    sw = uniform(g, W, Dn, lo=-1 / math.sqrt(W), hi=1 / math.sqrt(W))
+    src = [x, randn(g, Bn, Tn, R), randn(g, R, W * Dn, scale=1 / math.sqrt(R * W)), sw]
+    y_k, g_k = run_fwd_bwd(lr, [_to(t, dtype) for t in src], _to(dy, dtype), True)
+    y_k, g_k = y_k.cpu(), [t.cpu() for t in g_k]
+    q = [t.to(dtype).float() for t in src]
+    dyq = dy.to(dtype).float()
+    for t0, t1 in [(0, 64), (Tn - 64, Tn)]:
+        a, e = max(0, t0 - W + 1), min(Tn, t1 + W - 1)
+        win = [q[0][:, a:e], q[1][:, a:e], q[2], q[3]]
+        y_w, g_w = run_fwd_bwd(lr_ref, win, dyq[:, a:e], True)
+        sl = slice(t0 - a, t1 - a)
+        assert_ns(y_k[:, t0:t1], y_w[:, sl], dtype, f"y[{t0}:{t1}]")
+        assert_ns(g_k[0][:, t0:t1], g_w[0][:, sl], dtype, f"dx[{t0}:{t1}]")
+    check_reductions("lr", q, dyq, g_k, dtype)
+
+
 # ------------------------------------------------------------ determinism
 @pytest.mark.parametrize("kind", ["hw1", "hw32", "lr16s"])
 def test_deterministic(kind):
