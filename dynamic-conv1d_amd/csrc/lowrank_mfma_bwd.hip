@@ -758,10 +758,16 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     for (int c = 0; c < RC; ++c)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
+        // the lane's NJ consecutive columns in one store (16- or 8-byte aligned: col % NJ == 0,
+        // UL % 16 == 0, the partial 256-byte aligned plus a pass's kofs * D floats)
         const int off = du_lane + ((16 * c + i) * UL + k * D) * 4;
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(du[k][c][j][i]), rdu, off + 4 * j, 0, 0);
+        if constexpr (NJ == 4)
+          bstore128<false>(u32x4{__float_as_uint(du[k][c][0][i]), __float_as_uint(du[k][c][1][i]),
+                                 __float_as_uint(du[k][c][2][i]), __float_as_uint(du[k][c][3][i])},
+                           rdu, off);
+        else
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(du[k][c][0][i]), __float_as_uint(du[k][c][1][i])},
+                                                rdu, off, 0, 0);
       }
 }
 
