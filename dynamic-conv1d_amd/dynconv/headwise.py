@@ -77,14 +77,31 @@ def headwise_dynamic_convolution(
         (+ x[b, t, d] if residual).
 
     Preconditions as headwise.py:332-336, plus (checked here, assumed by the
-    reference) a 4-D weight of x's dtype; a non-contiguous weight is copied.
+    reference) a 4-D weight; a non-contiguous weight is copied.
+
+    weight and static_w may have dtypes other than x's (float32, bfloat16 or
+    float16), as in the reference, whose kernels load both in fp32
+    (headwise.py:63, 78, 180, 187) and return dweight in weight's dtype and
+    dstatic_w in static_w's (headwise.py:268, 305).  Such calls run the
+    kernels in float32 on float32 copies (every 16-bit value is exact in
+    float32) and round y and each gradient once to its tensor's dtype, as the
+    reference stores its fp32 results; one dtype throughout takes no copies.
     """
     assert x.is_cuda and x.is_contiguous()
     if static_w is not None:
         assert static_w.is_cuda and static_w.is_contiguous()
-        assert static_w.dtype == x.dtype
         assert static_w.shape == (weight.shape[-1], x.shape[-1])
+        assert static_w.dtype in _FLOATS, "static_w must be float32, bfloat16 or float16"
     assert weight.dim() == 4 and weight.shape[:2] == x.shape[:2], "weight must be [B, T, H, W]"
-    assert weight.dtype == x.dtype, "weight must have x's dtype"
+    assert weight.dtype in _FLOATS, "weight must be float32, bfloat16 or float16"
     assert weight.is_cuda
-    return _HeadwiseDynamicConvolutionFn.apply(x, weight.contiguous(), static_w, residual)
+    if weight.dtype == x.dtype and (static_w is None or static_w.dtype == x.dtype):
+        return _HeadwiseDynamicConvolutionFn.apply(x, weight.contiguous(), static_w, residual)
+    # mixed dtypes: float32 operands; autograd rounds each gradient back to its input's dtype
+    f32 = torch.float32
+    sw = None if static_w is None else static_w.to(f32)
+    y = _HeadwiseDynamicConvolutionFn.apply(x.to(f32), weight.to(f32).contiguous(), sw, residual)
+    return y.to(x.dtype)
+
+
+_FLOATS = (torch.float32, torch.bfloat16, torch.float16)

@@ -16,6 +16,10 @@
 * test_baseline_configs runs BASELINE.json configs 2-5 at full size and
   checks local outputs (y, dx, dweight, dz) on row windows against the
   oracle and the global reductions (dstatic_w, dU) against float64 sums.
+* test_headwise_mixed_dtypes: weight / static_w in other dtypes than x, each
+  gradient in its own tensor's dtype, against the oracle.
+* test_generic_lowrank_rows_past_2_24: the generic lowrank backward over more
+  than 2^24 rows (its capped dz grid).
 * test_deterministic: two backward passes are bitwise identical.
 """
 
@@ -155,6 +159,39 @@ def test_edge_shapes_headwise(Bn, Tn, Dn, H, W, static, residual, dtype):
         if b is not None:
             assert_ns(a, b, dtype, n, elementwise=n != "dstatic_w")
     check_reductions("hw", src_q, dy.to(dtype).float(), g_k, dtype)
+
+
+HW_MIXED = [
+    # B, T, D, H, W, static, residual, x dtype, weight dtype, static_w dtype
+    (2, 70, 256, 256, 4, True, True, torch.bfloat16, torch.float32, torch.bfloat16),   # hs 1
+    (1, 64, 512, 32, 3, True, False, torch.bfloat16, torch.float32, torch.float32),    # hs 16
+    (2, 33, 128, 32, 4, False, True, torch.float32, torch.bfloat16, None),             # hs 4, fp32 x
+    (1, 50, 256, 32, 4, True, True, torch.float16, torch.bfloat16, torch.float32),     # two 16-bit types
+]
+
+
+@pytest.mark.parametrize("Bn,Tn,Dn,H,W,static,residual,xd,wd,sd", HW_MIXED)
+def test_headwise_mixed_dtypes(Bn, Tn, Dn, H, W, static, residual, xd, wd, sd):
+    """weight / static_w in other dtypes than x, as the reference accepts (it loads them in fp32,
+    headwise.py:63, 78, 180, 187, and returns dweight and dstatic_w in their own dtypes,
+    headwise.py:268, 305): the oracle in fp32 on the same rounded inputs; every output carries
+    its own tensor's dtype and is checked to that dtype's bar."""
+    g = gen(Bn * 7919 + Tn * 31 + Dn + H + W)
+    x = randn(g, Bn, Tn, Dn)
+    dy = randn(g, Bn, Tn, Dn)
+    w = randn(g, Bn, Tn, H, W, scale=1 / math.sqrt(W))
+    sw = uniform(g, W, Dn, lo=-1 / math.sqrt(W), hi=1 / math.sqrt(W)) if static else None
+    dts = [xd, wd, sd]
+    src_q = [None if t is None else t.to(d).float() for t, d in zip([x, w, sw], dts)]
+    y_q, g_q = run_fwd_bwd(hw_ref, src_q, dy.to(xd).float(), residual)
+    y_k, g_k = run_fwd_bwd(hw, [None if t is None else t.to(d).to(DEV) for t, d in zip([x, w, sw], dts)],
+                           _to(dy, xd), residual)
+    assert y_k.dtype == xd
+    assert_ns(y_k, y_q, xd, "y")
+    for a, b, n, d in zip(g_k, g_q, ["dx", "dweight", "dstatic_w"], dts):
+        if b is not None:
+            assert a.dtype == d, f"{n}: {a.dtype} != {d}"
+            assert_ns(a, b, d, n, elementwise=n != "dstatic_w")
 
 
 def _hw_vector_shape(Dn, H, dtype):
