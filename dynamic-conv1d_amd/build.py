@@ -36,7 +36,10 @@ COMMON = [
 # Per-file flags.  The lowrank forward lets its MFMA results land in VGPRs
 # directly (no v_accvgpr_read per result); the backward keeps the default,
 # where accumulation registers are what keeps its larger tiles in 512 registers.
+# lowrank_mfma_fwd_ilp.hip is the forward's one-rank-chunk kernel scheduled
+# for instruction-level parallelism (see that file).
 PER_FILE = {"lowrank_mfma_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+            "lowrank_mfma_fwd_ilp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-sched-strategy=max-ilp"],
             "lowrank_f32_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
