@@ -7,7 +7,7 @@
 // z == 1 and U row = static_w (the reference's fusion, lowrank.py:223-225),
 // and by zero ranks up to a multiple of 16; neither is materialised.
 //
-// Shared device helpers of the MFMA kernels (lowrank_mfma_fwd.hip,
+// Shared device helpers of the MFMA kernels (lowrank_mfma_fwd_kernel.h,
 // lowrank_mfma_bwd.hip): operand types, buffer resources, the z_eff loader.
 #pragma once
 
