@@ -3,7 +3,7 @@
 Each case draws B, T, D, the head size (headwise) or rank (lowrank), W,
 static_w, residual and dtype from a fixed seed, so every dispatch path meets
 shapes nobody picked by hand: the vector / MFMA kernels with partial channel
-chunks and tiles, the fp32 matrix-core and VALU kernels, and the generic
+chunks and tiles, the lowrank backward's passes of taps (kernel ranks 33-64), the fp32 matrix-core and VALU kernels, and the generic
 kernels (D not a multiple of the vector width, head sizes that are not a power
 of two, ranks and W outside the fast plans).  Criterion: the north-star
 tolerance (tests/helpers.py) against the fp32 oracle on the same
@@ -63,7 +63,22 @@ def _headwise_case(i):
     return Bn, Tn, Dn, Dn // hs, W, static, residual, dtype
 
 
-LR_CASES = [_lowrank_case(i) for i in range(64)]
+def _lowrank_wide_case(i):
+    """Kernel ranks 33-64 (3-4 rank chunks) at W 1-8 in 16-bit types: the matrix-core backward's
+    passes of taps (each pass's dx added to the earlier passes', its dz in slots of its own)."""
+    rnd = random.Random(6113 * i + 29)
+    dtype = rnd.choice([torch.bfloat16, torch.float16])
+    Bn = rnd.randint(1, 2)
+    Tn = rnd.choice([1, 15, 16, 17, 33, 64, 100, 129])
+    Dn = rnd.choice([16, 64, 128, 144, 256])
+    W = rnd.randint(1, 8)
+    static = rnd.random() < 0.5
+    R = rnd.randint(32, 63) if static else rnd.randint(33, 64)
+    residual = rnd.random() < 0.5
+    return Bn, Tn, Dn, R, W, static, residual, dtype
+
+
+LR_CASES = [_lowrank_case(i) for i in range(64)] + [_lowrank_wide_case(i) for i in range(24)]
 HW_CASES = [_headwise_case(i) for i in range(64)]
 
 
