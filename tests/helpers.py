@@ -1,5 +1,6 @@
 """Shared test helpers: seeded inputs, tolerance checks, library loading."""
 
+import math
 import os
 import sys
 
@@ -63,7 +64,9 @@ def assert_ns(a, b, dtype, name="", elementwise=True):
 #     |a - b| <= k_in * L2 + k_acc * L1 + k_out * |b|
 # with L1 = sum |term| and L2 = sqrt(sum term^2), both in float64.
 #   k_in:  the per-term rounding before the sum.  The 16-bit lowrank backward
-#          rounds dy*x to the I/O type before its products (lowrank.py:128):
+#          rounds dy*x to the I/O type before its products, as the reference
+#          does for bf16 (lowrank.py:127-130; for fp16 the reference keeps fp32
+#          products, lowrank.py:131-134, so there the rounding is this build's):
 #          relative errors of at most u = 2^-8 (bf16) / 2^-11 (fp16) whose
 #          standard deviation is below u/2, independent across terms, so their
 #          sum is bounded statistically by L2: k_in = 4u is over 7 standard
@@ -71,6 +74,12 @@ def assert_ns(a, b, dtype, name="", elementwise=True):
 #   k_acc: fp32 accumulation, 2^-20 of L1 (sequential fp32 sums of 512 to
 #          131072 products stay within 1e-7 of L1, 10x below it).
 #   k_out: the final rounding to the output dtype, 2u.
+#   fp16's subnormal range (below 2^-14) rounds to absolute steps of 2^-24,
+#   not relative ones: a rounded product dy*x there is off by at most 2^-25
+#   times the other factor of its term (z for dU, U for dz), and an output by
+#   at most 2^-25.  The fp16 bound adds 4 sqrt(n) 2^-25 max|other factor| over
+#   the entry's n terms (the `floor` of lowrank_sums) and 2^-25.  bf16's
+#   subnormals start at 2^-126 and do not matter at these magnitudes.
 # A plausible kernel mistake fails it: a dropped 16-row tile of a 16384-row
 # bf16 reduction moves an entry by about 4 rms(term); the bound there is about
 # 2 rms(term) + |b| / 128.
@@ -81,13 +90,18 @@ SUM_TOL = {
 }
 
 
-def assert_sum(a, ref, dtype, name, rounded_terms=True):
-    """Per-entry check of a long reduction `a` against ref = (b, L1, L2) (float64, CPU; see SUM_TOL)."""
+def assert_sum(a, ref, dtype, name, rounded_terms=True, floor=None):
+    """Per-entry check of a long reduction `a` against ref = (b, L1, L2) (float64, CPU; see SUM_TOL).
+    floor: fp16 only, the subnormal rounding of the terms (broadcast against b)."""
     b, l1, l2 = ref
     t = SUM_TOL[dtype]
     a = a.detach().double().cpu().reshape(b.shape)
     k_in = t["k_in"] if rounded_terms else 0.0
     bound = k_in * l2 + t["k_acc"] * l1 + t["k_out"] * b.abs()
+    if dtype == torch.float16:
+        bound = bound + 2.0**-25
+        if rounded_terms and floor is not None:
+            bound = bound + floor
     err = (a - b).abs()
     ratio = err / bound.clamp_min(1e-300)
     worst = ratio.max().item()
@@ -146,7 +160,12 @@ def lowrank_sums(x, z, U, dy):
     dU = tuple(torch.cat([p[i] for p in dU], dim=1) for i in range(3))
     dU = (dU[0], dU[1], torch.sqrt(dU[2]))
     dz = _sum3(dz)
-    return {"dU": dU, "dz": tuple(t.reshape(Bn, Tn, R) for t in dz)}
+    # fp16 subnormal floor of the rounded products (see SUM_TOL): dU[r, :] has B*T terms whose other
+    # factor is z[:, r]; dz[b, t, r] has W*D terms whose other factor is U[r, :]
+    sub = 4 * 2.0**-25
+    floor_du = (sub * math.sqrt(Bn * Tn) * zf.abs().amax(0)).reshape(R, 1)
+    floor_dz = (sub * math.sqrt(W * Dn) * U64.abs().amax(1)).reshape(1, 1, R)
+    return {"dU": dU, "dz": tuple(t.reshape(Bn, Tn, R) for t in dz), "floor_dU": floor_du, "floor_dz": floor_dz}
 
 
 def check_reductions(kind, src_q, dyq, grads, dtype, tag=""):
@@ -161,11 +180,13 @@ def check_reductions(kind, src_q, dyq, grads, dtype, tag=""):
         return
     z, U, sw = src_q[1], src_q[2], src_q[3]
     ref = lowrank_sums(x, z, U, dyq)
-    assert_sum(grads[1], ref["dz"], dtype, tag + "dz")
-    assert_sum(grads[2], ref["dU"], dtype, tag + "dU")
+    assert_sum(grads[1], ref["dz"], dtype, tag + "dz", floor=ref["floor_dz"])
+    assert_sum(grads[2], ref["dU"], dtype, tag + "dU", floor=ref["floor_dU"])
     if sw is not None:
         W = U.shape[1] // x.shape[-1]
-        assert_sum(grads[3], dstatic_sums(x, dyq, W), dtype, tag + "dstatic_w")
+        # the static rank's other factor is 1: B*T terms
+        assert_sum(grads[3], dstatic_sums(x, dyq, W), dtype, tag + "dstatic_w",
+                   floor=4 * 2.0**-25 * math.sqrt(x.shape[0] * x.shape[1]))
 
 
 def run_fwd_bwd(fn, inputs, dy, residual):
