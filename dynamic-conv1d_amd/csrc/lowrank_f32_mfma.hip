@@ -175,6 +175,12 @@ __global__ __launch_bounds__(256) void lr_fwd_f32m(const float* __restrict__ x, 
 // tiles (one barrier) and written as one fp32 partial per 256 channels; dU
 // accumulates in registers over the run and is written as one partial per
 // run.  reduce_partials adds both in a fixed order (deterministic).
+//
+// Rank passes: a launch covers the 16 kernel ranks rofs .. rofs+15 (kernel
+// ranks 17-32 run as two launches).  Its tap weights, dU rows and dz columns
+// are those ranks' (disjoint outputs); its dx adds to what the earlier pass
+// stored (ACC, a separate instantiation); only the first pass adds the
+// residual.
 struct LrF32mBwdArgs {
   int Tn, D, R, RK, residual;
   int nch;   // ceil(D / 32) chunks
@@ -185,10 +191,11 @@ struct LrF32mBwdArgs {
   int nblk;  // ncg * nseg
   int xld, dxld;  // row strides of x and dx (elements)
   int yhd;        // dy layout: D ([B, T, D]) or the head dim of [B, D/yhd, T, yhd] (yhd % 32 == 0)
+  int rofs;       // first kernel rank of this pass (0, or 16 for the second of two)
   int64_t BT;
 };
 
-template <int W, int NKB>
+template <int W, int NKB, bool ACC>
 __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, const float* __restrict__ z,
                                                    const float* __restrict__ U, const float* __restrict__ sw,
                                                    const float* __restrict__ dy, float* __restrict__ dx,
@@ -210,7 +217,7 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
   const int lb = xcd_remap(blockIdx.x, a.nblk);
   const int cg = lb % a.ncg, s = lb / a.ncg;
   const int chunk = cg * NCW + wave;
-  const int D = a.D, Tn = a.Tn, R = a.R, RK = a.RK;
+  const int D = a.D, Tn = a.Tn, R = a.R, RK = a.RK, rofs = ACC ? a.rofs : 0;
   const int d0 = chunk * 32;
   const int col = d0 + 2 * n;
   const bool chv = col < D;  // D % 4 == 0: a lane's 2 channels are both inside or both outside
@@ -238,7 +245,7 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
   for (int k = 0; k < W; ++k)
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      const int r = 4 * kb + q;
+      const int r = rofs + 4 * kb + q;  // kernel rank
       const int c4 = (k * D + col) * 4;
       const u32x2 vu = bload64(ru, chv && r < R ? r * W * D * 4 + c4 : kOobLane);
       const u32x2 vs = bload64(rs, chv && r == R && r < RK ? c4 : kOobLane);
@@ -254,8 +261,9 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
       const int dd = d0 + 8 * q + 4 * p;
       const int c4 = (k * D + dd) * 4;
       const bool in = dd < D;
-      const u32x4 vu = bload128(ru, in && n < R ? n * W * D * 4 + c4 : kOobLane);
-      const u32x4 vs = bload128(rs, in && n == R && n < RK ? c4 : kOobLane);
+      const int rn = rofs + n;  // kernel rank of the lane's dz column
+      const u32x4 vu = bload128(ru, in && rn < R ? rn * W * D * 4 + c4 : kOobLane);
+      const u32x4 vs = bload128(rs, in && rn == R && rn < RK ? c4 : kOobLane);
       f32x4 v;
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(vu[i]) + __uint_as_float(vs[i]);
@@ -289,12 +297,12 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
     for (int m = 0; m < 4; ++m) in.dyr[m] = bload64(rdy, ylo + yt + m * yrowb);
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      const int r = 4 * kb + q;
+      const int r = rofs + 4 * kb + q;
       in.za[kb] = __uint_as_float(bload32(rz, ylive && r < R ? ((t0 + n) * R + r) * 4 : kOobTile));
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      in.zt[i] = __uint_as_float(bload32(rz, ylive && n < R ? ((t0 + 4 * q + i) * R + n) * 4 : kOobTile));
+      in.zt[i] = __uint_as_float(bload32(rz, ylive && rofs + n < R ? ((t0 + 4 * q + i) * R + rofs + n) * 4 : kOobTile));
   };
 
   // Scatter form (as lowrank_mfma_bwd.hip): S[m] holds the lane's sums for row
@@ -322,7 +330,13 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
         if (open) bv = (top ? carry[i - kFirstOpen][jj] : bv) + recv[3 - i][jj];
         v[jj] = __float_as_uint(bv);
       }
-      bstore64<true>(v, rdx, (top && open ? prev_off : cur_off) + i * dxrowb);
+      const int off = (top && open ? prev_off : cur_off) + i * dxrowb;
+      if constexpr (ACC) {  // the earlier rank pass's dx of this row (0 out of range: nothing stored there)
+        const u32x2 o = bload64(rdx, off);
+        v[0] = __float_as_uint(__uint_as_float(v[0]) + __uint_as_float(o[0]));
+        v[1] = __float_as_uint(__uint_as_float(v[1]) + __uint_as_float(o[1]));
+      }
+      bstore64<true>(v, rdx, off);
     }
 #pragma unroll
     for (int i = 0; i < NSC; ++i)
@@ -351,8 +365,8 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
   auto finish_z = [&](float(&za)[NKB], float(&zt)[4], int t0) {
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
-      if (4 * kb + q == R && R < RK) za[kb] = t0 + n < Tn ? 1.f : 0.f;
-    if (n == R && R < RK) {
+      if (rofs + 4 * kb + q == R && R < RK) za[kb] = t0 + n < Tn ? 1.f : 0.f;
+    if (rofs + n == R && R < RK) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) zt[i] = t0 + 4 * q + i < Tn ? 1.f : 0.f;
     }
@@ -415,7 +429,7 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
         for (int e = 0; e < 4; ++e) dz = __builtin_amdgcn_mfma_f32_16x16x4f32(ga[e], ub[e], dz, 0, 0, 0);
       }
     }
-    if (a.residual) {
+    if (a.residual && !ACC) {  // the first rank pass adds the residual
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -436,7 +450,7 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
 #pragma unroll
         for (int w2 = 1; w2 < NCW; ++w2) v += dzred[buf][w2][sl][rem];
         const int t = (tb + sl) * 16 + rr;
-        if (nn < R && t < Tn) out[t * R + nn] = v;
+        if (rofs + nn < R && nn < 16 && t < Tn) out[t * R + rofs + nn] = v;
       }
     }
   };
@@ -485,7 +499,7 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
     for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int rk = 4 * q + r;
+        const int rk = rofs + 4 * q + r;  // kernel rank (this pass's 16)
         if (rk < RK && chv) part_du[((int64_t)s * RK + rk) * W * D + (int64_t)k * D + col + jj] = du[k][jj][r];
       }
 }
@@ -582,6 +596,7 @@ LrF32mBwdArgs make_f32m_bwd_args(const LrProblem& p) {
   a.xld = (int)p.xld();
   a.dxld = (int)p.dxld();
   a.yhd = (int)p.yhd();
+  a.rofs = 0;
   a.BT = p.B * p.T;
   return a;
 }
@@ -597,17 +612,35 @@ F32mWs f32m_ws(const LrProblem& p, const LrF32mBwdArgs& a) {
   return w;
 }
 
+// One rank pass: NKB rank steps of 4 (ranks rofs .. rofs+4*NKB-1).
 template <int W, int NKB>
+hipError_t launch_f32m_pass(const LrProblem& p, LrF32mBwdArgs a, int rofs, float* pdz, float* pdu) {
+  a.rofs = rofs;
+  if (rofs > 0)
+    lr_bwd_f32m<W, NKB, true><<<a.nblk, 512, 0, p.stream>>>((const float*)p.x, (const float*)p.z, (const float*)p.U,
+                                                             (const float*)p.static_w, (const float*)p.dy,
+                                                             (float*)p.dx, pdz, pdu, a);
+  else
+    lr_bwd_f32m<W, NKB, false><<<a.nblk, 512, 0, p.stream>>>((const float*)p.x, (const float*)p.z, (const float*)p.U,
+                                                              (const float*)p.static_w, (const float*)p.dy,
+                                                              (float*)p.dx, pdz, pdu, a);
+  return hipGetLastError();
+}
+
+template <int W>
 hipError_t launch_f32m_bwd(const LrProblem& p) {
   const LrF32mBwdArgs a = make_f32m_bwd_args(p);
   const F32mWs w = f32m_ws(p, a);
   float* pdz = (float*)((char*)p.ws + w.dz_off);
   float* pdu = (float*)((char*)p.ws + w.du_off);
-  lr_bwd_f32m<W, NKB><<<a.nblk, 512, 0, p.stream>>>((const float*)p.x, (const float*)p.z, (const float*)p.U,
-                                                      (const float*)p.static_w, (const float*)p.dy, (float*)p.dx,
-                                                      pdz, pdu, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  // kernel ranks 1-16: one pass; 17-32: ranks 0-15, then the rest (dx added to the first pass's)
+  hipError_t e;
+  for (int rofs = 0; rofs < a.RK; rofs += 16) {
+    const int nr = a.RK - rofs < 16 ? a.RK - rofs : 16;  // ranks of this pass
+    const int nkb = (nr + 3) / 4;
+    e = nkb <= 2 ? launch_f32m_pass<W, 2>(p, a, rofs, pdz, pdu) : launch_f32m_pass<W, 4>(p, a, rofs, pdz, pdu);
+    if (e != hipSuccess) return e;
+  }
   const int64_t WD = p.W * p.D, RKWD = (int64_t)a.RK * WD;
   const PartialReduce jobs[3] = {
       {pdu, RKWD, a.nseg, p.R * WD, p.dU},
@@ -619,14 +652,14 @@ hipError_t launch_f32m_bwd(const LrProblem& p) {
 
 }  // namespace
 
-// fp32, 2 <= W <= 4, kernel rank <= 16; D, x / dx row strides multiples of 4
+// fp32, 2 <= W <= 4, kernel rank <= 32 (above 16 as two rank passes); D, x / dx row strides multiples of 4
 // (8-byte lane pieces, 16-byte operand pieces); dy's head dim a multiple of 32
 // (a chunk inside one head); 16-byte aligned x, dy, dx, U, static_w; every
 // sequence within the buffer range.
 bool lr_f32m_bwd_ok(const LrProblem& p) {
   if (p.dtype != kFP32) return false;
   if (p.W < 2 || p.W > 4) return false;
-  if (p.R + (p.static_w ? 1 : 0) > 16) return false;
+  if (p.R + (p.static_w ? 1 : 0) > 32) return false;
   if (p.D % 4 != 0 || p.xld() % 4 != 0 || p.dxld() % 4 != 0) return false;
   if (p.yhd() != p.D && p.yhd() % 32 != 0) return false;
   if (!aligned_to(p.x, 16) || !aligned_to(p.dy, 16) || !aligned_to(p.dx, 16) || !aligned_to(p.U, 16) ||
@@ -642,15 +675,12 @@ bool lr_f32m_bwd_ok(const LrProblem& p) {
 int64_t lr_f32m_ws_bytes(const LrProblem& p) { return f32m_ws(p, make_f32m_bwd_args(p)).total; }
 
 hipError_t lr_f32m_bwd(const LrProblem& p) {
-  const int nkb = (int)((p.R + (p.static_w ? 1 : 0) + 3) / 4);
-  const int kb = nkb <= 2 ? 2 : 4;
-#define DC_F32MB_CASE(WW, KB) \
-  if (p.W == WW && kb == KB) return launch_f32m_bwd<WW, KB>(p);
-  DC_F32MB_CASE(2, 2) DC_F32MB_CASE(2, 4)
-  DC_F32MB_CASE(3, 2) DC_F32MB_CASE(3, 4)
-  DC_F32MB_CASE(4, 2) DC_F32MB_CASE(4, 4)
-#undef DC_F32MB_CASE
-  return hipErrorInvalidValue;
+  switch (p.W) {
+    case 2: return launch_f32m_bwd<2>(p);
+    case 3: return launch_f32m_bwd<3>(p);
+    case 4: return launch_f32m_bwd<4>(p);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace dc

@@ -269,6 +269,10 @@ def test_kernel_paths(lib):
         assert lp(1, 40, 128, 40, 2, f16, 0, bwd) == 2         # kernel rank 40, W 2
     assert lp(1, 300, 64, 1, 1, f32, 0, 0) == 3                # fp32 W 1: forward on fp32 matrix cores,
     assert lp(1, 300, 64, 1, 1, f32, 0, 1) == 4                # backward on the VALU kernels
+    for bwd in (0, 1):                                         # fp32 kernel ranks 17-32: the backward
+        assert lp(2, 8192, 4096, 31, 4, f32, 1, bwd) == 3      # as two rank passes on matrix cores
+        assert lp(1, 100, 256, 32, 2, f32, 0, bwd) == 3
+    assert lp(1, 100, 256, 33, 4, f32, 0, 1) == 0              # kernel rank 33: the generic kernels
     for bwd in (0, 1):                                         # every W <= 8 at every kernel rank <= 64:
         assert lp(2, 50, 256, 63, 2, bf, 1, bwd) == 2          # the backward as passes of taps
         assert lp(2, 8192, 4096, 31, 8, bf, 1, bwd) == 2       # W 8, two rank chunks

@@ -236,6 +236,12 @@ LR_EDGE = [
     (2, 300, 64, 1, 1, False, True, torch.float32),     # rank 1, W 1
     (1, 9, 100, 7, 4, False, True, torch.float32),      # T below one run, D % 64 != 0
     (1, 40, 64, 40, 4, False, False, torch.float32),    # kernel rank 40: generic kernels
+    # fp32 kernel ranks 17-32: the matrix-core backward as two rank passes (ranks 0-15, then the
+    # rest; the second pass adds its dx to the first's and its dz columns / dU rows are its own)
+    (2, 300, 256, 31, 4, True, True, torch.float32, ("f32_mfma", "f32_mfma")),   # static rank in pass 2
+    (1, 100, 128, 20, 3, False, True, torch.float32, ("f32_mfma", "f32_mfma")),  # pass 2 of 4 ranks
+    (2, 1000, 272, 16, 2, True, False, torch.float32, ("f32_mfma", "f32_mfma")),  # pass 2: the static rank alone
+    (1, 64, 64, 32, 4, False, True, torch.float32, ("f32_mfma", "f32_mfma")),    # kernel rank 32, no static
     # matrix-core plans with three and four rank chunks (kernel ranks 33-64 at W 1-2)
     (1, 70, 128, 64, 1, False, True, torch.bfloat16, ("mfma", "mfma")),      # <W1, 4 chunks>
     (2, 50, 256, 63, 2, True, True, torch.bfloat16, ("mfma", "mfma")),       # <W2, 4 chunks>: backward in 2 passes
