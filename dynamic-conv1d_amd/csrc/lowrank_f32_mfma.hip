@@ -176,11 +176,16 @@ __global__ __launch_bounds__(256) void lr_fwd_f32m(const float* __restrict__ x, 
 // accumulates in registers over the run and is written as one partial per
 // run.  reduce_partials adds both in a fixed order (deterministic).
 //
-// Rank passes: a launch covers the 16 kernel ranks rofs .. rofs+15 (kernel
-// ranks 17-32 run as two launches).  Its tap weights, dU rows and dz columns
-// are those ranks' (disjoint outputs); its dx adds to what the earlier pass
-// stored (ACC, a separate instantiation); only the first pass adds the
-// residual.
+// Passes: a launch covers the 16 kernel ranks rofs .. rofs+15 (kernel ranks
+// 17-32 run as two rank passes) and the W taps kofs .. kofs+W-1 of the
+// problem's (W 5-8 run as two tap passes of 2-4 taps each, as the scatter
+// form needs).  A rank pass's tap weights, dU rows and dz columns are its
+// ranks' (disjoint outputs).  A tap pass is the W-tap problem on x shifted
+// down by kofs rows: x rows t-kofs-k, dx rows s-kofs (rows before 0, the
+// causal padding, are out of range), U / static_w / dU columns from tap kofs
+// (rows uld elements apart), and dz partials in slots of its own.  Every pass
+// after the first adds its dx to what the earlier ones stored (ACC, a separate
+// instantiation); only the first adds the residual.
 struct LrF32mBwdArgs {
   int Tn, D, R, RK, residual;
   int nch;   // ceil(D / 32) chunks
@@ -192,6 +197,8 @@ struct LrF32mBwdArgs {
   int xld, dxld;  // row strides of x and dx (elements)
   int yhd;        // dy layout: D ([B, T, D]) or the head dim of [B, D/yhd, T, yhd] (yhd % 32 == 0)
   int rofs;       // first kernel rank of this pass (0, or 16 for the second of two)
+  int kofs;       // first tap of this pass
+  int uld;        // row stride of U and of the dU partials: the problem's W * D (all taps)
   int64_t BT;
 };
 
@@ -217,7 +224,8 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
   const int lb = xcd_remap(blockIdx.x, a.nblk);
   const int cg = lb % a.ncg, s = lb / a.ncg;
   const int chunk = cg * NCW + wave;
-  const int D = a.D, Tn = a.Tn, R = a.R, RK = a.RK, rofs = ACC ? a.rofs : 0;
+  const int D = a.D, Tn = a.Tn, R = a.R, RK = a.RK, rofs = ACC ? a.rofs : 0, kofs = ACC ? a.kofs : 0;
+  const int uld = a.uld;
   const int d0 = chunk * 32;
   const int col = d0 + 2 * n;
   const bool chv = col < D;  // D % 4 == 0: a lane's 2 channels are both inside or both outside
@@ -238,7 +246,7 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
   const int dxlo = chv ? (4 * q * a.dxld + col) * 4 : kOobLane;
 
   // ---- U_eff operands of the chunk (rank rows r < RK, zero beyond)
-  const rsrc_t ru = make_rsrc(U, (int64_t)R * W * D * 4);
+  const rsrc_t ru = make_rsrc(U, (int64_t)R * uld * 4);
   const rsrc_t rs = make_rsrc(sw, sw ? (int64_t)W * D * 4 : 0);
   float uw[W][NKB][2];  // tap-weight B: U_eff[4kb+q, k*D + col + jj]
 #pragma unroll
@@ -247,7 +255,7 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
     for (int kb = 0; kb < NKB; ++kb) {
       const int r = rofs + 4 * kb + q;  // kernel rank
       const int c4 = (k * D + col) * 4;
-      const u32x2 vu = bload64(ru, chv && r < R ? r * W * D * 4 + c4 : kOobLane);
+      const u32x2 vu = bload64(ru, chv && r < R ? r * uld * 4 + c4 : kOobLane);
       const u32x2 vs = bload64(rs, chv && r == R && r < RK ? c4 : kOobLane);
       uw[k][kb][0] = __uint_as_float(vu[0]) + __uint_as_float(vs[0]);
       uw[k][kb][1] = __uint_as_float(vu[1]) + __uint_as_float(vs[1]);
@@ -262,7 +270,7 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
       const int c4 = (k * D + dd) * 4;
       const bool in = dd < D;
       const int rn = rofs + n;  // kernel rank of the lane's dz column
-      const u32x4 vu = bload128(ru, in && rn < R ? rn * W * D * 4 + c4 : kOobLane);
+      const u32x4 vu = bload128(ru, in && rn < R ? rn * uld * 4 + c4 : kOobLane);
       const u32x4 vs = bload128(rs, in && rn == R && rn < RK ? c4 : kOobLane);
       f32x4 v;
 #pragma unroll
@@ -289,7 +297,7 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
     const bool live = tile < tile1;
     const bool ylive = tile <= tile1;  // the tile after the run closes its last dx rows
     const int t0 = tile * 16;
-    const int xt = live ? t0 * xrowb : kOobTile;
+    const int xt = live ? (t0 - kofs) * xrowb : kOobTile;  // rows before 0 fall out of range
     const int yt = ylive ? t0 * yrowb : kOobTile;
 #pragma unroll
     for (int m = 0; m < NR; ++m) in.xr[m] = bload64(rx, xlo + xt + (m - (W - 1)) * xrowb);
@@ -317,8 +325,8 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
       for (int jj = 0; jj < 2; ++jj)
         recv[m][jj] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(S[m][jj])));
     const bool top = q == 3;
-    const int cur_off = tile < tile1 ? dxlo + tile * 16 * dxrowb : kOobTile;
-    const int prev_off = tile > tile0 && tile <= tile1 ? dxlo + (tile - 1) * 16 * dxrowb : kOobTile;
+    const int cur_off = tile < tile1 ? dxlo + (tile * 16 - kofs) * dxrowb : kOobTile;
+    const int prev_off = tile > tile0 && tile <= tile1 ? dxlo + ((tile - 1) * 16 - kofs) * dxrowb : kOobTile;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       constexpr int kFirstOpen = 4 - NSC;
@@ -500,7 +508,7 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int rk = rofs + 4 * q + r;  // kernel rank (this pass's 16)
-        if (rk < RK && chv) part_du[((int64_t)s * RK + rk) * W * D + (int64_t)k * D + col + jj] = du[k][jj][r];
+        if (rk < RK && chv) part_du[((int64_t)s * RK + rk) * uld + (int64_t)k * D + col + jj] = du[k][jj][r];
       }
 }
 
@@ -543,12 +551,12 @@ hipError_t launch_f32m(const LrProblem& p) {
 
 }  // namespace
 
-// fp32, W <= 4, kernel rank <= 32, 16-byte pieces of x / y / U / static_w at
+// fp32, W <= 8, kernel rank <= 32, 16-byte pieces of x / y / U / static_w at
 // every row (D, x row stride and head dim multiples of 4, pointers 16-byte
 // aligned), sequences within the buffer range.
 bool lr_f32m_fwd_ok(const LrProblem& p) {
   if (p.dtype != kFP32) return false;
-  if (p.W < 1 || p.W > 4) return false;
+  if (p.W < 1 || p.W > 8) return false;
   const int64_t rk = p.R + (p.static_w ? 1 : 0);
   if (rk > 4 * kF32mMaxKb) return false;
   if (p.D % 4 != 0 || p.xld() % 4 != 0 || p.yhd() % 4 != 0) return false;
@@ -569,6 +577,10 @@ hipError_t lr_f32m_fwd(const LrProblem& p) {
   DC_F32M_CASE(2, 2) DC_F32M_CASE(2, 4) DC_F32M_CASE(2, 8)
   DC_F32M_CASE(3, 2) DC_F32M_CASE(3, 4) DC_F32M_CASE(3, 8)
   DC_F32M_CASE(4, 2) DC_F32M_CASE(4, 4) DC_F32M_CASE(4, 8)
+  DC_F32M_CASE(5, 2) DC_F32M_CASE(5, 4) DC_F32M_CASE(5, 8)
+  DC_F32M_CASE(6, 2) DC_F32M_CASE(6, 4) DC_F32M_CASE(6, 8)
+  DC_F32M_CASE(7, 2) DC_F32M_CASE(7, 4) DC_F32M_CASE(7, 8)
+  DC_F32M_CASE(8, 2) DC_F32M_CASE(8, 4) DC_F32M_CASE(8, 8)
 #undef DC_F32M_CASE
   return hipErrorInvalidValue;
 }
@@ -597,6 +609,8 @@ LrF32mBwdArgs make_f32m_bwd_args(const LrProblem& p) {
   a.dxld = (int)p.dxld();
   a.yhd = (int)p.yhd();
   a.rofs = 0;
+  a.kofs = 0;
+  a.uld = (int)(p.W * p.D);
   a.BT = p.B * p.T;
   return a;
 }
@@ -604,61 +618,93 @@ LrF32mBwdArgs make_f32m_bwd_args(const LrProblem& p) {
 struct F32mWs {
   int64_t dz_off, du_off, total;
 };
+// Tap passes of a W-tap problem: one for W <= 4, else two of 2-4 taps (the
+// scatter form needs at least 2): W 5 = 3 + 2, 6 = 3 + 3, 7 = 4 + 3, 8 = 4 + 4.
+inline int f32m_tap_passes(int W) { return W <= 4 ? 1 : 2; }
+inline int f32m_pass_taps(int W, int tp) { return W <= 4 ? W : tp == 0 ? (W + 1) / 2 : W / 2; }
+
 F32mWs f32m_ws(const LrProblem& p, const LrF32mBwdArgs& a) {
   F32mWs w;
   w.dz_off = 0;
-  w.du_off = ((int64_t)a.ncg * a.BT * a.R * 4 + 255) / 256 * 256;
+  w.du_off = ((int64_t)f32m_tap_passes((int)p.W) * a.ncg * a.BT * a.R * 4 + 255) / 256 * 256;
   w.total = w.du_off + (int64_t)a.nseg * a.RK * p.W * p.D * 4;
   return w;
 }
 
-// One rank pass: NKB rank steps of 4 (ranks rofs .. rofs+4*NKB-1).
+// One pass: W taps from kofs, NKB rank steps of 4 (ranks rofs .. rofs+4*NKB-1);
+// U, static_w, the dz and dU partials already start at the pass's tap / slot.
 template <int W, int NKB>
-hipError_t launch_f32m_pass(const LrProblem& p, LrF32mBwdArgs a, int rofs, float* pdz, float* pdu) {
-  a.rofs = rofs;
-  if (rofs > 0)
-    lr_bwd_f32m<W, NKB, true><<<a.nblk, 512, 0, p.stream>>>((const float*)p.x, (const float*)p.z, (const float*)p.U,
-                                                             (const float*)p.static_w, (const float*)p.dy,
-                                                             (float*)p.dx, pdz, pdu, a);
+hipError_t launch_f32m_pass(const LrProblem& p, LrF32mBwdArgs a, const float* U, const float* sw, float* pdz,
+                            float* pdu) {
+  const bool first = a.rofs == 0 && a.kofs == 0;
+  if (!first)
+    lr_bwd_f32m<W, NKB, true><<<a.nblk, 512, 0, p.stream>>>((const float*)p.x, (const float*)p.z, U, sw,
+                                                             (const float*)p.dy, (float*)p.dx, pdz, pdu, a);
   else
-    lr_bwd_f32m<W, NKB, false><<<a.nblk, 512, 0, p.stream>>>((const float*)p.x, (const float*)p.z, (const float*)p.U,
-                                                              (const float*)p.static_w, (const float*)p.dy,
-                                                              (float*)p.dx, pdz, pdu, a);
+    lr_bwd_f32m<W, NKB, false><<<a.nblk, 512, 0, p.stream>>>((const float*)p.x, (const float*)p.z, U, sw,
+                                                              (const float*)p.dy, (float*)p.dx, pdz, pdu, a);
   return hipGetLastError();
 }
 
 template <int W>
+hipError_t launch_f32m_taps(const LrProblem& p, const LrF32mBwdArgs& a, const float* U, const float* sw, float* pdz,
+                            float* pdu) {
+  // kernel ranks 1-16: one pass; 17-32: ranks 0-15, then the rest
+  for (int rofs = 0; rofs < a.RK; rofs += 16) {
+    const int nr = a.RK - rofs < 16 ? a.RK - rofs : 16;  // ranks of this pass
+    const int nkb = (nr + 3) / 4;
+    LrF32mBwdArgs b = a;
+    b.rofs = rofs;
+    const hipError_t e = nkb <= 2 ? launch_f32m_pass<W, 2>(p, b, U, sw, pdz, pdu)
+                                  : launch_f32m_pass<W, 4>(p, b, U, sw, pdz, pdu);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 hipError_t launch_f32m_bwd(const LrProblem& p) {
   const LrF32mBwdArgs a = make_f32m_bwd_args(p);
   const F32mWs w = f32m_ws(p, a);
   float* pdz = (float*)((char*)p.ws + w.dz_off);
   float* pdu = (float*)((char*)p.ws + w.du_off);
-  // kernel ranks 1-16: one pass; 17-32: ranks 0-15, then the rest (dx added to the first pass's)
+  const int ntp = f32m_tap_passes((int)p.W);
+  const int64_t dz_slot = (int64_t)a.ncg * a.BT * a.R;  // one tap pass's dz partials
   hipError_t e;
-  for (int rofs = 0; rofs < a.RK; rofs += 16) {
-    const int nr = a.RK - rofs < 16 ? a.RK - rofs : 16;  // ranks of this pass
-    const int nkb = (nr + 3) / 4;
-    e = nkb <= 2 ? launch_f32m_pass<W, 2>(p, a, rofs, pdz, pdu) : launch_f32m_pass<W, 4>(p, a, rofs, pdz, pdu);
+  for (int tp = 0, kofs = 0; tp < ntp; kofs += f32m_pass_taps((int)p.W, tp), ++tp) {
+    const int wq = f32m_pass_taps((int)p.W, tp);
+    LrF32mBwdArgs b = a;
+    b.kofs = kofs;
+    const float* U = (const float*)p.U + (int64_t)kofs * p.D;
+    const float* sw = p.static_w ? (const float*)p.static_w + (int64_t)kofs * p.D : nullptr;
+    float* dz_t = pdz + tp * dz_slot;
+    float* du_t = pdu + (int64_t)kofs * p.D;
+    switch (wq) {
+      case 2: e = launch_f32m_taps<2>(p, b, U, sw, dz_t, du_t); break;
+      case 3: e = launch_f32m_taps<3>(p, b, U, sw, dz_t, du_t); break;
+      case 4: e = launch_f32m_taps<4>(p, b, U, sw, dz_t, du_t); break;
+      default: e = hipErrorInvalidValue; break;
+    }
     if (e != hipSuccess) return e;
   }
   const int64_t WD = p.W * p.D, RKWD = (int64_t)a.RK * WD;
   const PartialReduce jobs[3] = {
       {pdu, RKWD, a.nseg, p.R * WD, p.dU},
       {pdu + p.R * WD, RKWD, a.nseg, p.static_w ? WD : 0, p.dstatic_w},
-      {pdz, a.BT * a.R, a.ncg, a.BT * a.R, p.dz},
+      {pdz, a.BT * a.R, ntp * a.ncg, a.BT * a.R, p.dz},
   };
   return reduce_partials_multi(jobs, 3, p.dtype, p.stream);
 }
 
 }  // namespace
 
-// fp32, 2 <= W <= 4, kernel rank <= 32 (above 16 as two rank passes); D, x / dx row strides multiples of 4
+// fp32, 2 <= W <= 8 (above 4 as two tap passes), kernel rank <= 32 (above 16 as
+// two rank passes); D, x / dx row strides multiples of 4
 // (8-byte lane pieces, 16-byte operand pieces); dy's head dim a multiple of 32
 // (a chunk inside one head); 16-byte aligned x, dy, dx, U, static_w; every
 // sequence within the buffer range.
 bool lr_f32m_bwd_ok(const LrProblem& p) {
   if (p.dtype != kFP32) return false;
-  if (p.W < 2 || p.W > 4) return false;
+  if (p.W < 2 || p.W > 8) return false;
   if (p.R + (p.static_w ? 1 : 0) > 32) return false;
   if (p.D % 4 != 0 || p.xld() % 4 != 0 || p.dxld() % 4 != 0) return false;
   if (p.yhd() != p.D && p.yhd() % 32 != 0) return false;
@@ -674,13 +720,6 @@ bool lr_f32m_bwd_ok(const LrProblem& p) {
 
 int64_t lr_f32m_ws_bytes(const LrProblem& p) { return f32m_ws(p, make_f32m_bwd_args(p)).total; }
 
-hipError_t lr_f32m_bwd(const LrProblem& p) {
-  switch (p.W) {
-    case 2: return launch_f32m_bwd<2>(p);
-    case 3: return launch_f32m_bwd<3>(p);
-    case 4: return launch_f32m_bwd<4>(p);
-    default: return hipErrorInvalidValue;
-  }
-}
+hipError_t lr_f32m_bwd(const LrProblem& p) { return launch_f32m_bwd(p); }
 
 }  // namespace dc

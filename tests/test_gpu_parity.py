@@ -242,6 +242,12 @@ LR_EDGE = [
     (1, 100, 128, 20, 3, False, True, torch.float32, ("f32_mfma", "f32_mfma")),  # pass 2 of 4 ranks
     (2, 1000, 272, 16, 2, True, False, torch.float32, ("f32_mfma", "f32_mfma")),  # pass 2: the static rank alone
     (1, 64, 64, 32, 4, False, True, torch.float32, ("f32_mfma", "f32_mfma")),    # kernel rank 32, no static
+    # fp32 W 5-8: the matrix-core forward at any W <= 8; the backward as two tap passes (x shifted by
+    # the second pass's first tap, dx added, dz partials per pass), with rank passes above 16
+    (2, 300, 256, 16, 8, False, True, torch.float32, ("f32_mfma", "f32_mfma")),   # W 8: 4 + 4
+    (1, 100, 128, 31, 5, True, True, torch.float32, ("f32_mfma", "f32_mfma")),    # W 5: 3 + 2, x 2 rank passes
+    (2, 1000, 272, 7, 6, True, False, torch.float32, ("f32_mfma", "f32_mfma")),   # W 6: 3 + 3, long runs
+    (1, 40, 64, 20, 7, False, True, torch.float32, ("f32_mfma", "f32_mfma")),     # W 7: 4 + 3, rank passes
     # matrix-core plans with three and four rank chunks (kernel ranks 33-64 at W 1-2)
     (1, 70, 128, 64, 1, False, True, torch.bfloat16, ("mfma", "mfma")),      # <W1, 4 chunks>
     (2, 50, 256, 63, 2, True, True, torch.bfloat16, ("mfma", "mfma")),       # <W2, 4 chunks>: backward in 2 passes
