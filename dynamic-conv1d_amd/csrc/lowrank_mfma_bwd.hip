@@ -49,6 +49,13 @@ namespace dc {
 // two wavefronts per SIMD where 64-channel tiles allowed one, and with the
 // same wavefront count the runs are twice as long (half the dU partials).
 //
+// Passes of taps: a launch holds the tap-weight and dz operands and the dU
+// accumulators of at most pass_taps(W, RC) taps (host code below), so wider
+// problems run as consecutive launches over taps kofs .. kofs+W'-1: the W'-tap
+// problem on x shifted down by kofs rows, whose dx rows land kofs rows earlier
+// and are added to what the earlier passes stored (ACC), with U, static_w and
+// the dU partial columns from tap kofs and dz partials in slots of their own.
+//
 // Groups: up to kMaxGroups independent problems of one shape share a launch
 // (block index -> group); x and dx may have row strides xld, dxld > D, so the
 // q / k / v convolutions read x out of a fused [B, T, 3D] projection and write
