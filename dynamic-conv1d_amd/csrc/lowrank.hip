@@ -217,7 +217,8 @@ bool lr_mfma_ok(const LrProblem& p, bool bwd) {
     if (p.yhd() % 8 != 0) return false;  // a lane's y octet inside one head
     return aligned_to16(p.x) && aligned_to16(p.U) && aligned_to16(p.static_w) && aligned_to16(p.y);
   }
-  if (p.D % 16 != 0 || p.xld() % 4 != 0 || p.dxld() % 4 != 0) return false;
+  // whole 8-channel dz operand pieces (D % 8 == 0) and 4-byte-aligned row pieces of x / dx
+  if (p.D % 8 != 0 || p.xld() % 4 != 0 || p.dxld() % 4 != 0) return false;
   // dU partial stores: byte offsets up to (RK + 16) rows of W*D fp32 stay below kOobLane
   if ((p.R + 1 + 16) * p.W * p.D * 4 > kOobLane) return false;
   if (p.yhd() != p.D && p.yhd() % 64 != 0) return false;  // a wavefront's dy channels inside one head

@@ -166,7 +166,7 @@ __device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds,
       const int r = 16 * c + n;
 #pragma unroll
       for (int s2 = 0; s2 < NS; ++s2) {
-        const int dd = d0 + 32 * s2 + 8 * q;  // multiple of 8; D % 16 == 0, so dd < D means dd + 8 <= D
+        const int dd = d0 + 32 * s2 + 8 * q;  // multiple of 8; D % 8 == 0, so dd < D means dd + 8 <= D
         const int cz = dd < D ? dd * 2 : kOobLane;
         zr[k][c][s2] = bload128(ru, r < R ? cz + (r * WD + k * D) * 2 : kOobLane) |
                        bload128(rs, has_static && r == R ? cz + k * D * 2 : kOobLane);
@@ -294,7 +294,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   const int D = a.D, Tn = a.Tn;
   const int d0 = chunk * CPW;
   const int col = d0 + NJ * n;
-  const bool chv = col < D;  // the lane's channels inside D (D % 16 == 0)
+  const bool chv = col < D;  // the lane's NJ channels inside D (D % 8 == 0: all or none)
   const int ntile = (Tn + 15) >> 4;
   // Run s of the grid: tiles [tile0, tile1) of sequence b, whose buffer
   // resources start at row rb (run_base_row).  A workgroup's last run can lie

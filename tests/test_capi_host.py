@@ -121,7 +121,8 @@ def test_lowrank_validation(lib):
     assert zb(2, 8, 16, 32, 4, 0, 0) == 0
     assert zb(2, 8, 16, 28, 4, 0, 0) == 2 * 8 * 32 * 2
     assert zb(2, 8, 16, 3, 4, 2, 1) == 0              # fp32: the backward reads z itself
-    assert zb(2, 8, 20, 3, 4, 0, 1) == 0              # D % 16 != 0: no matrix-core backward
+    assert zb(2, 8, 20, 3, 4, 0, 1) == 0              # D % 8 != 0: no matrix-core backward
+    assert zb(2, 8, 24, 3, 4, 0, 1) == 2 * 8 * 4 * 2  # D % 8 == 0 suffices
     assert zb(2, 8, 16, 0, 4, 0, 1) == E_SHAPE
     need = lib.dc_lowrank_bwd_ws_bytes(2, 8, 16, 4, 4, 0, 1)
     assert need > 0
@@ -282,6 +283,10 @@ def test_kernel_paths(lib):
         assert lp(1, 64, 256, 40, 5, f16, 0, bwd) == 2         # W 5, three rank chunks
         assert lp(1, 64, 256, 63, 8, bf, 1, bwd) == 2          # W 8, four rank chunks
         assert lp(1, 64, 256, 64, 8, bf, 1, bwd) == 0          # kernel rank 65: generic
+    for bwd in (0, 1):                                         # D a multiple of 8, not of 16
+        assert lp(2, 100, 200, 16, 4, bf, 0, bwd) == 2
+        assert lp(1, 50, 1000, 15, 3, f16, 1, bwd) == 2
+        assert lp(2, 100, 20, 16, 4, bf, 0, bwd) == 0          # D % 8 != 0: generic
     assert hp(2, 8, 16, 3, 4, bf, 0, 0) == E_SHAPE
     assert lp(2, 8, 16, 0, 4, bf, 0, 0) == E_SHAPE
     assert lp(2, 8, 16, 4, 33, bf, 0, 1) == E_UNSUP

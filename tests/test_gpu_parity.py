@@ -261,6 +261,13 @@ LR_EDGE = [
     (1, 60, 256, 63, 8, True, True, torch.bfloat16, ("mfma", "mfma")),       # W 8, 4 chunks: 8 passes of 1
     (1, 3216, 256, 31, 7, True, True, torch.bfloat16, ("mfma", "mfma")),     # W 7: passes of 4 + 3, long runs
     (2, 37, 64, 47, 3, True, False, torch.bfloat16, ("mfma", "mfma")),       # W 3, 3 chunks: passes 2 + 1
+    # D a multiple of 8 but not of 16 on the matrix-core backward: the last 16-channel group and
+    # 32-channel dz block half inside D (their other channels read 0 and store nothing)
+    (2, 100, 200, 16, 4, False, True, torch.bfloat16, ("mfma", "mfma")),      # 64-channel tiles
+    (1, 70, 40, 31, 4, True, True, torch.bfloat16, ("mfma", "mfma")),         # two rank chunks: 32-channel tiles
+    (1, 50, 1000, 15, 3, True, False, torch.float16, ("mfma", "mfma")),       # partial channel group
+    (2, 33, 24, 7, 8, True, True, torch.bfloat16, ("mfma", "mfma")),          # W 8 gather form
+    (1, 64, 72, 63, 2, False, True, torch.bfloat16, ("mfma", "mfma")),        # four rank chunks, tap passes
     # widths above 8 and kernel ranks above 64 (the generic kernels; the reference accepts any
     # W and power-of-two ranks, lowrank.py:220, 331-333)
     (1, 45, 64, 127, 12, True, True, torch.bfloat16, ("generic", "generic")),  # W 12, kernel rank 128
@@ -456,14 +463,14 @@ def test_long_sequence(kind):
 
 
 def test_generic_lowrank_rows_past_2_24():
-    """The generic lowrank backward (D = 8 is off its matrix-core path; the forward takes the
-    matrix cores) over more than 2^24 rows: the per-row dz launch loops over rows with a capped
+    """The generic lowrank kernels (D = 4 is off the matrix-core paths, which take whole
+    8-channel pieces) over more than 2^24 rows: the per-row dz launch loops over rows with a capped
     grid (one workgroup per row would ask for more than 2^32 work-items).  Row windows at both
     ends against the oracle; dz, dU and dstatic_w entry by entry against float64 sums over the
     whole sequence."""
     dtype = torch.bfloat16
-    Bn, Tn, Dn, R, W = 1, (1 << 24) + 40, 8, 3, 4  # R + static = 4 (the API's power of two)
-    assert _path("lr", Bn, Tn, Dn, R, W, dtype, True, 0) == "mfma"
+    Bn, Tn, Dn, R, W = 1, (1 << 24) + 40, 4, 3, 4  # R + static = 4 (the API's power of two)
+    assert _path("lr", Bn, Tn, Dn, R, W, dtype, True, 0) == "generic"
     assert _path("lr", Bn, Tn, Dn, R, W, dtype, True, 1) == "generic"
     g = gen(13)
     x = randn(g, Bn, Tn, Dn)
