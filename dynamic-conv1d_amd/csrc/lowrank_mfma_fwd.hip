@@ -16,6 +16,14 @@ int fwd_target_waves(const LrProblem& p) {
   return (int)(w < 1 ? 1 : w > 4096 ? 4096 : w);
 }
 
+// One rank chunk without the z_eff writer: at most two wavefronts per SIMD, on
+// the ILP build (longer runs where the problem is larger).  B2 T8192 D4096 R16:
+// 54.5 us at 4096 wavefronts of the default build, 59.6 us at 3072 of the ILP
+// build, 50.7 us at 2048; B4 T16384 D4096 R16: 240.4 -> 200.2 us (5.37 TB/s).
+// Kernels with two or more rank chunks or the z_eff writer keep the wider
+// launches (B2 T8192 D4096 R31 + static: 61.5 us at 4096, 72 us at 2048).
+constexpr int kFwdIlpWaves = 2 * 4 * 256;
+
 }  // namespace
 
 // Longest forward run (tiles) whose resources fit (see run_rsrc): rows of x, y,
@@ -67,7 +75,9 @@ LrArgs make_args(const LrProblem& p, int target_waves) {
 
 template <typename T, int W, int RC>
 hipError_t launch_fwd(const LrProblem* p, int G) {
-  LrArgs a = make_args(p[0], fwd_target_waves(p[0]));
+  int waves = fwd_target_waves(p[0]);
+  if (RC == 1 && !p[0].zeff && waves > kFwdIlpWaves) waves = kFwdIlpWaves;
+  LrArgs a = make_args(p[0], waves);
   a.nblk1 = a.nblk;
   a.nblk = G * a.nblk1;
   a.xld = (int)p[0].xld();
@@ -78,7 +88,8 @@ hipError_t launch_fwd(const LrProblem* p, int G) {
     a.zvec = a.zvec && aligned_to(p[g].z, 8);
   }
   if constexpr (RC == 1) {
-    // all wavefronts resident at the ILP build's three per SIMD (see lowrank_mfma_fwd_ilp.hip)
+    // all wavefronts resident at the ILP build's three per SIMD (see lowrank_mfma_fwd_ilp.hip);
+    // more only where the run length cap forces them
     if (a.zrp == 0 && a.nblk * 4 <= kFwdIlpMaxWaves) return lr_fwd_ilp_launch<T, W>(a, p[0].stream);
   }
   if (a.zrp > 0) {

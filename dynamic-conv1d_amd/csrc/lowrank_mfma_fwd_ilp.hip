@@ -6,8 +6,9 @@
 // and pads with s_nop.  B4 T4096 D2048 R16 W4 forward 29.0 -> 27.8 us, W8
 // 38.6 -> 36.0 us; W1-3 and W5 unchanged.  It takes up to 149 VGPRs (three
 // wavefronts per SIMD), so launches above kFwdIlpMaxWaves wavefronts keep the
-// default build (B2 T8192 D4096 R16, 4096 wavefronts: 54.3 us against 59.7 us
-// for this build at 3072).
+// default build; the launch plan gives this build at most two wavefronts per
+// SIMD (B2 T8192 D4096 R16: 50.7 us at 2048 wavefronts, 59.7 us at 3072, 54.3 us
+// for the default build at 4096).
 #include "lowrank_mfma_fwd_kernel.h"
 
 namespace dc {

@@ -425,7 +425,9 @@ def test_baseline_configs(cfg):
 # start at the run's own first rows, so they stay on the vector / matrix-core
 # kernels.  Local outputs are checked on row windows, including the rows
 # around 512 MiB; the reductions over the whole sequence entry by entry.
-@pytest.mark.parametrize("kind", ["hw32", "lr16"])
+# lr16n (rank 16, no static_w: the forward without the z_eff writer) runs
+# 2048 forward wavefronts with runs of 65 tiles.
+@pytest.mark.parametrize("kind", ["hw32", "lr16", "lr16n"])
 def test_long_sequence(kind):
     dtype = torch.bfloat16
     Bn, Tn, Dn, W = 1, 131172, 2048, 4
@@ -433,7 +435,7 @@ def test_long_sequence(kind):
         if kind == "hw32":
             assert _path("hw", Bn, Tn, Dn, Dn // 32, W, dtype, True, bwd) == "vector"
         else:
-            assert _path("lr", Bn, Tn, Dn, 15, W, dtype, True, bwd) == "mfma"
+            assert _path("lr", Bn, Tn, Dn, 16 if kind == "lr16n" else 15, W, dtype, kind == "lr16", bwd) == "mfma"
     g = gen(11)
     x = randn(g, Bn, Tn, Dn)
     dy = randn(g, Bn, Tn, Dn)
@@ -441,17 +443,16 @@ def test_long_sequence(kind):
     if kind == "hw32":
         src, fn, ref = [x, randn(g, Bn, Tn, Dn // 32, W, scale=1 / math.sqrt(W)), sw], hw, hw_ref
     else:
-        R = 15
-        src, fn, ref = [x, randn(g, Bn, Tn, R), randn(g, R, W * Dn, scale=1 / math.sqrt(16 * W)), sw], lr, lr_ref
+        R = 16 if kind == "lr16n" else 15
+        src, fn, ref = [x, randn(g, Bn, Tn, R), randn(g, R, W * Dn, scale=1 / math.sqrt(16 * W)),
+                        sw if kind == "lr16" else None], lr, lr_ref
     y_k, g_k = run_fwd_bwd(fn, [_to(t, dtype) for t in src], _to(dy, dtype), True)
-    q = [t.to(dtype).float() for t in src]
+    q = [t.to(dtype).float() if t is not None else None for t in src]
     dyq = dy.to(dtype).float()
     edge = (1 << 29) // (Dn * 2)  # first row past 512 MiB of x
     for t0, t1 in _windows(Tn) + [(edge - 40, edge + 24)]:
         a, e = max(0, t0 - W + 1), min(Tn, t1 + W - 1)
-        win = [t[:, a:e] if t.dim() >= 3 else t for t in q]
-        if kind == "lr16":
-            win[2] = q[2]
+        win = [t[:, a:e] if t is not None and t.dim() >= 3 else t for t in q]
         y_w, g_w = run_fwd_bwd(ref, win, dyq[:, a:e], True)
         sl = slice(t0 - a, t1 - a)
         assert_ns(y_k[:, t0:t1], y_w[:, sl], dtype, f"y[{t0}:{t1}]")
