@@ -644,6 +644,11 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
       for (int i = 0; i < 4; ++i) dzred[buf][rw][cw][slot][c * 256 + (((4 * q + i) * 16 + n) ^ (q << 4))] = dz[c][i];
     if (slot == DZB - 1 || it == nit - 1) {
       __syncthreads();
+      // The batch's sums go out at raised wave priority: every wavefront of the
+      // workgroup waits at the next batch's barrier for the slowest one here
+      // (configs[4] backward 156 -> 149 us, grouped 397 -> 383 us, W 8 285 ->
+      // 276 us; one rank chunk unchanged).
+      __builtin_amdgcn_s_setprio(1);
       constexpr int PER_RUN = RC * 256;
       constexpr int NTH = 64 * NW;
       static_assert(DZB * PER_RUN % NTH == 0, "whole passes over a full batch");
@@ -671,6 +676,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
                                                 0);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
     }
   };
 
