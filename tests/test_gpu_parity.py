@@ -539,13 +539,16 @@ def test_generic_matches_vector_path():
 
 
 # ------------------------------------------------- padded z copy from the forward
-@pytest.mark.parametrize("R,static,xoff", [(15, True, 0), (31, True, 0), (3, False, 0), (28, False, 0),
-                                           (15, True, 4)])
-def test_lowrank_zeff_saved(R, static, xoff):
+@pytest.mark.parametrize("R,static,xoff,zoff", [(15, True, 0, 0), (31, True, 0, 0), (3, False, 0, 0), (28, False, 0, 0),
+                                                (15, True, 4, 0), (63, True, 0, 0), (37, False, 4, 0), (15, True, 0, 1),
+                                                (31, True, 4, 1)])
+def test_lowrank_zeff_saved(R, static, xoff, zoff):
     """The forward's padded z copy (z, the static column as 1, zero ranks up to RP) feeds the
     backward exactly as the copy the backward builds itself: bitwise equal gradients.  xoff = 4
     puts x 8 bytes off 16-byte alignment: the forward takes its element-aligned kernels and
-    fills the copy in a launch of its own, the backward stays on matrix cores."""
+    fills the copy in a launch of its own (the padding kernel), the backward stays on matrix
+    cores.  zoff = 1 starts z 2 bytes into its buffer (rows not 4-byte aligned); R 63 and 37
+    pad to 64 and 40 ranks."""
     from dynconv import _capi
 
     lib = _capi.load()
@@ -554,7 +557,8 @@ def test_lowrank_zeff_saved(R, static, xoff):
     bf = torch.bfloat16
     xb = randn(g, Bn * Tn * Dn + xoff).to(bf).to(DEV)
     x = xb[xoff:].view(Bn, Tn, Dn)
-    z = randn(g, Bn, Tn, R).to(bf).to(DEV)
+    zb = randn(g, Bn * Tn * R + zoff).to(bf).to(DEV)
+    z = zb[zoff:].view(Bn, Tn, R)
     U = randn(g, R, W * Dn, scale=1 / math.sqrt((R + 1) * W)).to(bf).to(DEV)
     sw = uniform(g, W, Dn, lo=-0.5, hi=0.5).to(bf).to(DEV) if static else None
     dy = randn(g, Bn, Tn, Dn).to(bf).to(DEV)
