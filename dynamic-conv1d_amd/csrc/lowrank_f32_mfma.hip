@@ -22,6 +22,11 @@
 // chunk.  Rows outside the sequence, ranks >= R and lanes past D use buffer
 // range checks, as the other fast paths do.  y may be head-major (attention
 // layout, [B, D/hd, T, hd]); stores then check the row against T.
+//
+// Both kernels give each run of tiles buffer resources that start at the run's
+// base row (run_base_row: its first tile less an 8-row halo) and the host caps
+// a run's length (lr_f32m_{fwd,bwd}_max_run_tiles), so offsets stay in int32
+// and sequences of any length take these kernels, as in the 16-bit ones.
 #include "lowrank_mfma.h"
 
 namespace dc {
@@ -80,24 +85,30 @@ __global__ __launch_bounds__(256) void lr_fwd_f32m(const float* __restrict__ x, 
   const int tile0 = (sg - b * a.nspb) * a.seg;
   const int tile1 = min(tile0 + a.seg, ntile);
   const int64_t row0 = (int64_t)b * Tn;
+  const int rb = run_base_row(tile0);  // offsets below are relative to the run's base row
+  const int64_t rrow = row0 + rb;
   const int xrowb = a.xld * 4;
   const int yhd = a.yhd, yh = dl / yhd;
   const int yrowb = yhd * 4;
-  const rsrc_t rx = make_rsrc(x + row0 * a.xld, (int64_t)Tn * xrowb);
-  const rsrc_t ry = make_rsrc(y + row0 * D, (int64_t)Tn * D * 4);
-  const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 4);
+  // y is [B, T, D] (yhd == D) or head-major: the resource starts at row rb of
+  // head yh0, the head of the chunk's first channel, and spans its heads up to
+  // yhl (rows past T would land in the next head's block: stores check the row)
+  const int yh0 = chunk * 64 / yhd, yhl = min(chunk * 64 + 63, D - 1) / yhd;
+  const rsrc_t rx = run_rsrc(x + rrow * a.xld, Tn - rb, xrowb);
+  const rsrc_t ry = run_rsrc(y + row0 * D + ((int64_t)yh0 * Tn + rb) * yhd, (int64_t)(yhl - yh0) * Tn + Tn - rb, yrowb);
+  const rsrc_t rz = run_rsrc(z + rrow * R, Tn - rb, R * 4);
   const int xlane_off = chv ? (4 * q * a.xld + dl) * 4 : kOobLane;
   // y: the lane's piece lies in head yh (yhd % 4 == 0), rows yhd elements apart
-  const int ylane_off = chv ? ((yh * Tn + 4 * q) * yhd + dl - yh * yhd) * 4 : kOobLane;
+  const int ylane_off = chv ? (((yh - yh0) * Tn + 4 * q) * yhd + dl - yh * yhd) * 4 : kOobLane;
 
   for (int tile = tile0; tile < tile1; ++tile) {
     const int t0 = tile * 16;
     u32x4 xr[NR];
 #pragma unroll
-    for (int m = 0; m < NR; ++m) xr[m] = bload128(rx, xlane_off + t0 * xrowb + (m - (W - 1)) * xrowb);
+    for (int m = 0; m < NR; ++m) xr[m] = bload128(rx, xlane_off + (t0 - rb) * xrowb + (m - (W - 1)) * xrowb);
     // A operands: z_eff[t0+n, 4kb+q]; the static rank R is 1 inside the sequence
     float za[NKB];
-    const int zrow = (t0 + n) * R * 4;
+    const int zrow = (t0 + n - rb) * R * 4;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       const int r = 4 * kb + q;
@@ -146,7 +157,7 @@ __global__ __launch_bounds__(256) void lr_fwd_f32m(const float* __restrict__ x, 
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) o[jj] = __float_as_uint(acc[i][jj]);
       const int row = t0 + 4 * q + i;
-      bstore128<true>(o, ry, row < Tn ? ylane_off + (t0 + i) * yrowb : kOobTile);
+      bstore128<true>(o, ry, row < Tn ? ylane_off + (t0 - rb + i) * yrowb : kOobTile);
     }
   }
 }
@@ -237,10 +248,13 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
   const int64_t row0 = (int64_t)b * Tn;
   const int yhd = a.yhd, head = d0 / yhd;  // yhd % 32 == 0: the chunk lies in one head
   const int xrowb = a.xld * 4, yrowb = yhd * 4, dxrowb = a.dxld * 4;
-  const rsrc_t rx = make_rsrc(x + row0 * a.xld, (int64_t)Tn * xrowb);
-  const rsrc_t rdy = make_rsrc(dy + row0 * D + (int64_t)head * Tn * yhd, (int64_t)Tn * yrowb);
-  const rsrc_t rdx = make_rsrc(dx + row0 * a.dxld, (int64_t)Tn * dxrowb);
-  const rsrc_t rz = make_rsrc(z + row0 * R, (int64_t)Tn * R * 4);
+  // resources of the run's rows from its base row rb (offsets below are relative to it)
+  const int rb = run_base_row(tile0);
+  const int64_t rrow = row0 + rb;
+  const rsrc_t rx = run_rsrc(x + rrow * a.xld, Tn - rb, xrowb);
+  const rsrc_t rdy = run_rsrc(dy + row0 * D + ((int64_t)head * Tn + rb) * yhd, Tn - rb, yrowb);
+  const rsrc_t rdx = run_rsrc(dx + rrow * a.dxld, Tn - rb, dxrowb);
+  const rsrc_t rz = run_rsrc(z + rrow * R, Tn - rb, R * 4);
   const int xlo = chv ? (4 * q * a.xld + col) * 4 : kOobLane;
   const int ylo = chv ? (4 * q * yhd + col - head * yhd) * 4 : kOobLane;
   const int dxlo = chv ? (4 * q * a.dxld + col) * 4 : kOobLane;
@@ -297,8 +311,8 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
     const bool live = tile < tile1;
     const bool ylive = tile <= tile1;  // the tile after the run closes its last dx rows
     const int t0 = tile * 16;
-    const int xt = live ? (t0 - kofs) * xrowb : kOobTile;  // rows before 0 fall out of range
-    const int yt = ylive ? t0 * yrowb : kOobTile;
+    const int xt = live ? (t0 - kofs - rb) * xrowb : kOobTile;  // rows before 0 fall out of range
+    const int yt = ylive ? (t0 - rb) * yrowb : kOobTile;
 #pragma unroll
     for (int m = 0; m < NR; ++m) in.xr[m] = bload64(rx, xlo + xt + (m - (W - 1)) * xrowb);
 #pragma unroll
@@ -306,11 +320,12 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       const int r = rofs + 4 * kb + q;
-      in.za[kb] = __uint_as_float(bload32(rz, ylive && r < R ? ((t0 + n) * R + r) * 4 : kOobTile));
+      in.za[kb] = __uint_as_float(bload32(rz, ylive && r < R ? ((t0 + n - rb) * R + r) * 4 : kOobTile));
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      in.zt[i] = __uint_as_float(bload32(rz, ylive && rofs + n < R ? ((t0 + 4 * q + i) * R + rofs + n) * 4 : kOobTile));
+      in.zt[i] =
+          __uint_as_float(bload32(rz, ylive && rofs + n < R ? ((t0 + 4 * q + i - rb) * R + rofs + n) * 4 : kOobTile));
   };
 
   // Scatter form (as lowrank_mfma_bwd.hip): S[m] holds the lane's sums for row
@@ -325,8 +340,8 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
       for (int jj = 0; jj < 2; ++jj)
         recv[m][jj] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(S[m][jj])));
     const bool top = q == 3;
-    const int cur_off = tile < tile1 ? dxlo + (tile * 16 - kofs) * dxrowb : kOobTile;
-    const int prev_off = tile > tile0 && tile <= tile1 ? dxlo + ((tile - 1) * 16 - kofs) * dxrowb : kOobTile;
+    const int cur_off = tile < tile1 ? dxlo + (tile * 16 - kofs - rb) * dxrowb : kOobTile;
+    const int prev_off = tile > tile0 && tile <= tile1 ? dxlo + ((tile - 1) * 16 - kofs - rb) * dxrowb : kOobTile;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       constexpr int kFirstOpen = 4 - NSC;
@@ -458,7 +473,7 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
 #pragma unroll
         for (int w2 = 1; w2 < NCW; ++w2) v += dzred[buf][w2][sl][rem];
         const int t = (tb + sl) * 16 + rr;
-        if (rofs + nn < R && nn < 16 && t < Tn) out[t * R + rofs + nn] = v;
+        if (rofs + nn < R && nn < 16 && t < Tn) out[(int64_t)t * R + rofs + nn] = v;
       }
     }
   };
@@ -515,6 +530,33 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
 // ------------------------------------------------------------------- host
 namespace {
 
+// Longest forward run (tiles) whose resources fit (run_rsrc): rows of x, y and
+// z; head-major y spans the head blocks of a wavefront's 64 channels, which
+// adds up to (63 / hd + 1) * T * hd * 4 bytes to its offsets.
+int64_t f32m_fwd_max_run_tiles(const LrProblem& p) {
+  const int64_t hd = p.yhd();
+  int64_t rowb = p.xld() * 4;
+  if (hd * 4 > rowb) rowb = hd * 4;
+  if (p.R * 4 > rowb) rowb = p.R * 4;
+  int64_t tiles = run_tiles_cap(rowb);
+  if (hd != p.D) {
+    const int64_t extra = (63 / hd + 1) * p.T * hd * 4;
+    const int64_t rows = (kMaxSeqBytes - extra) / (hd * 4) - kSeqSlackRows - 8 - 32;
+    const int64_t yt = rows > 0 ? rows / 16 : 0;
+    tiles = tiles < yt ? tiles : yt;
+  }
+  return tiles;
+}
+
+// Longest backward run: rows of x, dx, dy (one head's block of head-major dy)
+// and z.
+int64_t f32m_bwd_max_run_tiles(const LrProblem& p) {
+  int64_t rowb = p.xld() * 4;
+  const int64_t others[3] = {p.dxld() * 4, p.yhd() * 4, p.R * 4};
+  for (int64_t v : others) rowb = rowb > v ? rowb : v;
+  return run_tiles_cap(rowb);
+}
+
 LrF32mArgs make_f32m_args(const LrProblem& p) {
   LrF32mArgs a;
   a.Tn = (int)p.T;
@@ -532,6 +574,8 @@ LrF32mArgs make_f32m_args(const LrProblem& p) {
   int64_t seg = (tiles + waves - 1) / waves;
   if (seg < 1) seg = 1;
   if (seg > ntile) seg = ntile;
+  const int64_t cap = f32m_fwd_max_run_tiles(p);  // >= 1 (lr_f32m_fwd_ok)
+  if (seg > cap) seg = cap;
   a.seg = (int)seg;
   a.nspb = (int)((ntile + seg - 1) / seg);
   a.nseg = (int)(p.B * a.nspb);
@@ -553,7 +597,7 @@ hipError_t launch_f32m(const LrProblem& p) {
 
 // fp32, W <= 8, kernel rank <= 32, 16-byte pieces of x / y / U / static_w at
 // every row (D, x row stride and head dim multiples of 4, pointers 16-byte
-// aligned), sequences within the buffer range.
+// aligned); sequences of any length (runs capped by f32m_fwd_max_run_tiles).
 bool lr_f32m_fwd_ok(const LrProblem& p) {
   if (p.dtype != kFP32) return false;
   if (p.W < 1 || p.W > 8) return false;
@@ -562,10 +606,8 @@ bool lr_f32m_fwd_ok(const LrProblem& p) {
   if (p.D % 4 != 0 || p.xld() % 4 != 0 || p.yhd() % 4 != 0) return false;
   if (!aligned_to(p.x, 16) || !aligned_to(p.y, 16) || !aligned_to(p.U, 16) || !aligned_to(p.static_w, 16))
     return false;
-  if (p.R * p.W * p.D * 4 >= kOobLane) return false;                    // U offsets
-  if ((p.T + kSeqSlackRows) * p.xld() * 4 > kMaxSeqBytes) return false;  // x rows
-  if ((p.T + kSeqSlackRows) * p.D * 4 > kMaxSeqBytes) return false;      // y rows
-  return (p.T + kSeqSlackRows) * p.R * 4 <= kMaxSeqBytes;                // z rows
+  if (p.R * p.W * p.D * 4 >= kOobLane) return false;  // U offsets
+  return f32m_fwd_max_run_tiles(p) >= 1;              // at least one tile per run fits
 }
 
 hipError_t lr_f32m_fwd(const LrProblem& p) {
@@ -601,6 +643,8 @@ LrF32mBwdArgs make_f32m_bwd_args(const LrProblem& p) {
   int64_t seg = (p.B * ntile * a.ncg * 8 + 2047) / 2048;
   if (seg < 2) seg = 2;
   if (seg > ntile) seg = ntile;
+  const int64_t cap = f32m_bwd_max_run_tiles(p);  // >= 1 (lr_f32m_bwd_ok)
+  if (seg > cap) seg = cap;
   a.seg = (int)seg;
   a.nspb = (int)((ntile + seg - 1) / seg);
   a.nseg = (int)(p.B * a.nspb);
@@ -700,8 +744,8 @@ hipError_t launch_f32m_bwd(const LrProblem& p) {
 // fp32, 2 <= W <= 8 (above 4 as two tap passes), kernel rank <= 32 (above 16 as
 // two rank passes); D, x / dx row strides multiples of 4
 // (8-byte lane pieces, 16-byte operand pieces); dy's head dim a multiple of 32
-// (a chunk inside one head); 16-byte aligned x, dy, dx, U, static_w; every
-// sequence within the buffer range.
+// (a chunk inside one head); 16-byte aligned x, dy, dx, U, static_w; sequences
+// of any length (runs capped by f32m_bwd_max_run_tiles).
 bool lr_f32m_bwd_ok(const LrProblem& p) {
   if (p.dtype != kFP32) return false;
   if (p.W < 2 || p.W > 8) return false;
@@ -712,10 +756,7 @@ bool lr_f32m_bwd_ok(const LrProblem& p) {
       !aligned_to(p.static_w, 16))
     return false;
   if (p.R * p.W * p.D * 4 >= kOobLane) return false;
-  const int64_t ld = p.xld() > p.dxld() ? p.xld() : p.dxld();
-  if ((p.T + kSeqSlackRows) * ld * 4 > kMaxSeqBytes) return false;
-  if ((p.T + kSeqSlackRows) * p.D * 4 > kMaxSeqBytes) return false;
-  return (p.T + kSeqSlackRows) * p.R * 4 <= kMaxSeqBytes;
+  return f32m_bwd_max_run_tiles(p) >= 1;
 }
 
 int64_t lr_f32m_ws_bytes(const LrProblem& p) { return f32m_ws(p, make_f32m_bwd_args(p)).total; }

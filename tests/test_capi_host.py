@@ -274,6 +274,9 @@ def test_kernel_paths(lib):
         assert lp(2, 8192, 4096, 31, 4, f32, 1, bwd) == 3      # as two rank passes on matrix cores
         assert lp(1, 100, 256, 32, 2, f32, 0, bwd) == 3
     assert lp(1, 100, 256, 33, 4, f32, 0, 1) == 0              # kernel rank 33: the generic kernels
+    for bwd in (0, 1):                                         # fp32 sequences past 512 MiB of rows:
+        assert lp(1, 65600, 2048, 15, 4, f32, 1, bwd) == 3     # per-run buffer ranges
+        assert lp(1, 1 << 20, 4096, 31, 8, f32, 1, bwd) == 3
     for bwd in (0, 1):                                         # fp32 W 5-8: forward at any W, backward
         assert lp(4, 4096, 2048, 16, 8, f32, 0, bwd) == 3      # as two tap passes
         assert lp(1, 100, 256, 31, 5, f32, 1, bwd) == 3

@@ -426,16 +426,29 @@ def test_baseline_configs(cfg):
 # kernels.  Local outputs are checked on row windows, including the rows
 # around 512 MiB; the reductions over the whole sequence entry by entry.
 # lr16n (rank 16, no static_w: the forward without the z_eff writer) runs
-# 2048 forward wavefronts with runs of 65 tiles.
-@pytest.mark.parametrize("kind", ["hw32", "lr16", "lr16n"])
+# 2048 forward wavefronts with runs of 65 tiles.  lr16f and lr32f8 are the
+# fp32 tier's matrix-core kernels (rows of 8 and 16 KiB); lr32f8's backward
+# runs as two rank passes x two tap passes (x read from 4 rows before each
+# run's first tile in the second tap pass).
+LONG = {  # kind: dtype, T, D, W, R (lowrank), static_w
+    "hw32": (torch.bfloat16, 131172, 2048, 4, None, True),
+    "lr16": (torch.bfloat16, 131172, 2048, 4, 15, True),
+    "lr16n": (torch.bfloat16, 131172, 2048, 4, 16, False),
+    "lr16f": (torch.float32, 65600, 2048, 4, 15, True),
+    "lr32f8": (torch.float32, 32800, 4096, 8, 31, True),
+}
+
+
+@pytest.mark.parametrize("kind", list(LONG))
 def test_long_sequence(kind):
-    dtype = torch.bfloat16
-    Bn, Tn, Dn, W = 1, 131172, 2048, 4
+    dtype, Tn, Dn, W, R, static = LONG[kind]
+    Bn = 1
     for bwd in (0, 1):
         if kind == "hw32":
             assert _path("hw", Bn, Tn, Dn, Dn // 32, W, dtype, True, bwd) == "vector"
         else:
-            assert _path("lr", Bn, Tn, Dn, 16 if kind == "lr16n" else 15, W, dtype, kind == "lr16", bwd) == "mfma"
+            want = "f32_mfma" if dtype == torch.float32 else "mfma"
+            assert _path("lr", Bn, Tn, Dn, R, W, dtype, static, bwd) == want
     g = gen(11)
     x = randn(g, Bn, Tn, Dn)
     dy = randn(g, Bn, Tn, Dn)
@@ -443,13 +456,13 @@ def test_long_sequence(kind):
     if kind == "hw32":
         src, fn, ref = [x, randn(g, Bn, Tn, Dn // 32, W, scale=1 / math.sqrt(W)), sw], hw, hw_ref
     else:
-        R = 16 if kind == "lr16n" else 15
-        src, fn, ref = [x, randn(g, Bn, Tn, R), randn(g, R, W * Dn, scale=1 / math.sqrt(16 * W)),
-                        sw if kind == "lr16" else None], lr, lr_ref
+        src, fn, ref = [x, randn(g, Bn, Tn, R), randn(g, R, W * Dn, scale=1 / math.sqrt((R + 1) * W)),
+                        sw if static else None], lr, lr_ref
     y_k, g_k = run_fwd_bwd(fn, [_to(t, dtype) for t in src], _to(dy, dtype), True)
     q = [t.to(dtype).float() if t is not None else None for t in src]
     dyq = dy.to(dtype).float()
-    edge = (1 << 29) // (Dn * 2)  # first row past 512 MiB of x
+    esz = 4 if dtype == torch.float32 else 2
+    edge = (1 << 29) // (Dn * esz)  # first row past 512 MiB of x
     for t0, t1 in _windows(Tn) + [(edge - 40, edge + 24)]:
         a, e = max(0, t0 - W + 1), min(Tn, t1 + W - 1)
         win = [t[:, a:e] if t is not None and t.dim() >= 3 else t for t in q]
