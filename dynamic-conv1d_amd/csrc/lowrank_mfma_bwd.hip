@@ -772,7 +772,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         // the lane's NJ consecutive columns in one store (16- or 8-byte aligned: col % NJ == 0,
-        // UL % 16 == 0, the partial 256-byte aligned plus a pass's kofs * D floats)
+        // UL and D multiples of 8 floats, the partial 256-byte aligned plus a pass's kofs * D floats)
         const int off = du_lane + ((16 * c + i) * UL + k * D) * 4;
         if constexpr (NJ == 4)
           bstore128<false>(u32x4{__float_as_uint(du[k][c][0][i]), __float_as_uint(du[k][c][1][i]),
