@@ -23,8 +23,10 @@ Also reported:
                256 MB MALL, between one pair of HIP events; plus configs[4]
                (lowrank QKV) at its own shape, as 3 calls and as one grouped
                call reading x out of the fused [B, T, 3D] projection, the fp32
-               tier, and the reference bench.py's own shapes (ref_*: head
-               sizes 1, 4, 16 and rank 16, no static_w, no residual);
+               tier, the reference bench.py's own shapes (ref_*: head
+               sizes 1, 4, 16 and rank 16, no static_w, no residual), lowrank
+               W 16 on matrix cores, and one shape on the generic kernels
+               (lowrank W 20);
   qkv          configs[4] end to end through autograd (forward + backward):
                the README's pattern (split the fused projection, .contiguous()
                each slice, three calls; autograd concatenates dq, dk, dv)
@@ -93,6 +95,10 @@ EXTRA = {
     # the fp32 tier (reference test.py's 1e-5 cases) at the B4 shapes
     "hw_hs32_fp32": dict(kind="hw", B=4, T=4096, D=2048, H=64, W=4, static=True, residual=True, dtype="fp32"),
     "lr_r16_fp32": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=4, static=False, residual=True, dtype="fp32"),
+    # W 16 at rank 16: the forward in one pass over the taps, the backward as four passes of 4 taps
+    "lr_W16": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=16, static=False, residual=True),
+    # a width the fast kernels do not take (W <= 16): the generic kernels (one thread per output), for their cost
+    "lr_W20_generic": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=20, static=False, residual=True),
     # the reference bench.py's own shapes (bench.py:7-12): head sizes 1, 4, 16 and rank 16, no static_w, no residual
     "ref_hw_hs1": dict(kind="hw", B=4, T=4096, D=2048, H=2048, W=4, static=False, residual=False),
     "ref_hw_hs4": dict(kind="hw", B=4, T=4096, D=2048, H=512, W=4, static=False, residual=False),

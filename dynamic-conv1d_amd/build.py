@@ -39,6 +39,7 @@ COMMON = [
 # lowrank_mfma_fwd_ilp.hip is the forward's one-rank-chunk kernel scheduled
 # for instruction-level parallelism (see that file).
 PER_FILE = {"lowrank_mfma_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+            "lowrank_mfma_fwd_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
             "lowrank_mfma_fwd_ilp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-sched-strategy=max-ilp"],
             "lowrank_f32_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 

@@ -24,7 +24,7 @@
 // layout, [B, D/hd, T, hd]); stores then check the row against T.
 //
 // Both kernels give each run of tiles buffer resources that start at the run's
-// base row (run_base_row: its first tile less an 8-row halo) and the host caps
+// base row (run_base_row: its first tile less a 16-row halo) and the host caps
 // a run's length (lr_f32m_{fwd,bwd}_max_run_tiles), so offsets stay in int32
 // and sequences of any length take these kernels, as in the 16-bit ones.
 #include "lowrank_mfma.h"
@@ -541,7 +541,7 @@ int64_t f32m_fwd_max_run_tiles(const LrProblem& p) {
   int64_t tiles = run_tiles_cap(rowb);
   if (hd != p.D) {
     const int64_t extra = (63 / hd + 1) * p.T * hd * 4;
-    const int64_t rows = (kMaxSeqBytes - extra) / (hd * 4) - kSeqSlackRows - 8 - 32;
+    const int64_t rows = (kMaxSeqBytes - extra) / (hd * 4) - kSeqSlackRows - kRunHaloRows - 32;
     const int64_t yt = rows > 0 ? rows / 16 : 0;
     tiles = tiles < yt ? tiles : yt;
   }

@@ -92,8 +92,9 @@ __device__ __forceinline__ float q4f(const u32x2& v, int j) {
 }
 
 // Buffer resources (dc_common.h) of the matrix-core lowrank kernels cover one
-// run of tiles: they start at the run's base row rb = max(16 * tile0 - 8, 0)
-// (the first tile's rows less an 8-row halo, W - 1 <= 7) and end at T, capped
+// run of tiles: they start at the run's base row rb = max(16 * tile0 - 16, 0)
+// (the first tile's rows less a 16-row halo: the look-back of W - 1 <= 15 rows,
+// passes of taps included) and end at T, capped
 // at kMaxSeqBytes - kSeqSlackRows rows (run_rsrc).  Rows before 0 (negative
 // offsets wrap to large unsigned values), rows past T and channels past D
 // (lane offset kOobLane) read 0 and drop stores, without branches or clamped
@@ -106,14 +107,15 @@ constexpr int64_t kMaxSeqBytes = int64_t(1) << 29;
 constexpr int kSeqSlackRows = 32;
 
 // A byte offset that every buffer access of a run treats as out of range
-// (returns 0, touches no memory), also less 7 rows of halo.
+// (returns 0, touches no memory), also less 15 rows of halo.
 constexpr int kOobTile = (int)kMaxSeqBytes;
 
 // First row covered by the buffer resources of a run whose first tile is tile0.
-__device__ __forceinline__ int run_base_row(int tile0) { return max(tile0 * 16 - 8, 0); }
+constexpr int kRunHaloRows = 16;
+__device__ __forceinline__ int run_base_row(int tile0) { return max(tile0 * 16 - kRunHaloRows, 0); }
 
 // Resource over rows [rb, rb + nrows) of `rowb` bytes each, starting at p (row
-// rb), capped so that kOobTile less 7 rows stays out of range.
+// rb), capped so that kOobTile less 15 rows stays out of range.
 __device__ __forceinline__ rsrc_t run_rsrc(const void* p, int64_t nrows, int64_t rowb) {
   const int64_t bytes = nrows * rowb, cap = kMaxSeqBytes - kSeqSlackRows * rowb;
   return make_rsrc(p, bytes < cap ? bytes : cap);
@@ -173,10 +175,10 @@ struct ZRaw {
 inline bool aligned_to(const void* p, int a) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 // Longest run (in 16-row tiles) whose rows fit the resource cap when rows are
-// `rowb` bytes: the run's tiles, the 8-row halo, the tile after it and the
-// slack rows.  0 when not even one tile fits.
+// `rowb` bytes: the run's tiles, the halo, the tile after it and the slack
+// rows.  0 when not even one tile fits.
 inline int64_t run_tiles_cap(int64_t rowb) {
-  const int64_t rows = kMaxSeqBytes / (rowb > 0 ? rowb : 1) - kSeqSlackRows - 8 - 32;
+  const int64_t rows = kMaxSeqBytes / (rowb > 0 ? rowb : 1) - kSeqSlackRows - kRunHaloRows - 32;
   return rows > 0 ? rows / 16 : 0;
 }
 

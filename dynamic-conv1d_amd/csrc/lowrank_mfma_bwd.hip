@@ -800,9 +800,13 @@ constexpr BwdShape bwd_shape(int W, int RC) {
 // Taps per backward pass: what one pass's tap-weight and dz operands (registers
 // and LDS) and dU accumulators hold for RC rank chunks.  Wider problems run as
 // consecutive passes of taps kofs .. kofs+taps-1 (see the kernel's kofs): every
-// W <= 8 at every rank <= 64 stays on matrix cores, reading x and dy once per pass.
+// W <= 8 at every rank <= 64, and W <= 16 at one or two rank chunks, stays on
+// matrix cores, reading x and dy once per pass.  Every pass of a problem takes
+// the same launch shape (bwd_shape: the dU partial rows of all passes line up),
+// so one rank chunk above W 8 runs passes of at most 4 taps (two runs per
+// workgroup, two wavefronts per SIMD; passes of 5-8 taps would hold one).
 constexpr int pass_taps(int W, int RC) {
-  return RC == 1 ? W : RC == 2 ? (W < 4 ? W : 4) : RC == 3 ? (W < 2 ? W : 2) : 1;
+  return RC == 1 ? (W <= 8 ? W : 4) : RC == 2 ? (W < 4 ? W : 4) : RC == 3 ? (W < 2 ? W : 2) : 1;
 }
 constexpr int npasses(int W, int RC) { return (W + pass_taps(W, RC) - 1) / pass_taps(W, RC); }
 
@@ -927,7 +931,9 @@ template <typename T, int W, int RC>
 hipError_t launch_bwd_kernel(const LrBwdArgs& a, hipStream_t stream) {
   constexpr BwdShape SH = bwd_shape(W, RC);  // as make_bwd_args
   constexpr int NRW = SH.nrw, CPW = SH.cpw, NT = 64 * (256 / CPW) * NRW;
-  if constexpr (RC >= 2) {  // only problems of 2+ rank chunks run several passes
+  // later passes of taps: problems of 2+ rank chunks, and one rank chunk at W > 8
+  // (passes of at most 4 taps)
+  if constexpr (RC >= 2 || W <= 4) {
     if (a.accdx) {
       lr_bwd_mfma<T, W, RC, NRW, CPW, true><<<a.nblk, NT, 0, stream>>>(a);
       return hipGetLastError();

@@ -1,0 +1,91 @@
+// Launch plans of the lowrank forward (lowrank_mfma_fwd_kernel.h), shared by
+// the host units that instantiate it: lowrank_mfma_fwd.hip (W <= 8) and
+// lowrank_mfma_fwd_wide.hip (9 <= W <= 16).
+#pragma once
+
+#include "lowrank_mfma_fwd_kernel.h"
+
+namespace dc {
+namespace {
+
+// Wavefronts per problem: runs of about 8 tiles, at most 4096 wavefronts
+// (4 per SIMD).  B4 T4096 D2048: 2048 wavefronts (31.4 us, 31.9 at 4096);
+// B2 T8192 D4096: 4096 (61.8 us, 64.0 at 2048).
+inline int fwd_target_waves(const LrProblem& p) {
+  const int64_t tiles = p.B * ((p.T + 15) / 16) * ((p.D + 127) / 128);
+  const int64_t w = tiles / 8;
+  return (int)(w < 1 ? 1 : w > 4096 ? 4096 : w);
+}
+
+// One rank chunk without the z_eff writer: at most two wavefronts per SIMD, on
+// the ILP build (longer runs where the problem is larger).  B2 T8192 D4096 R16:
+// 54.5 us at 4096 wavefronts of the default build, 59.6 us at 3072 of the ILP
+// build, 50.7 us at 2048; B4 T16384 D4096 R16: 240.4 -> 200.2 us (5.37 TB/s).
+// Kernels with two or more rank chunks or the z_eff writer keep the wider
+// launches (B2 T8192 D4096 R31 + static: 61.5 us at 4096, 72 us at 2048).
+constexpr int kFwdIlpWaves = 2 * 4 * 256;
+
+inline LrArgs make_args(const LrProblem& p, int target_waves) {
+  LrArgs a;
+  a.Tn = (int)p.T;
+  a.D = (int)p.D;
+  a.R = (int)p.R;
+  a.RK = (int)p.R + (p.static_w ? 1 : 0);
+  a.has_static = p.static_w != nullptr;
+  a.residual = p.residual;
+  a.nch = (int)((p.D + 127) / 128);
+  a.ncg = 0;
+  a.zvec = p.R % 4 == 0 && aligned_to(p.z, 8);
+  const int64_t ntile = (p.T + 15) / 16;
+  int64_t seg = (p.B * ntile * a.nch + target_waves - 1) / target_waves;
+  if (seg < 1) seg = 1;
+  if (seg > ntile) seg = ntile;
+  const int64_t cap = lr_fwd_max_run_tiles(p);  // >= 1 (lr_mfma_ok)
+  if (seg > cap) seg = cap;
+  a.seg = (int)seg;
+  a.nspb = (int)((ntile + seg - 1) / seg);
+  a.nseg = (int)(p.B * a.nspb);
+  a.nblk = ((a.nseg + 3) / 4) * a.nch;
+  return a;
+}
+
+template <typename T, int W, int RC>
+hipError_t launch_fwd(const LrProblem* p, int G) {
+  int waves = fwd_target_waves(p[0]);
+  if (RC == 1 && W <= 8 && !p[0].zeff && waves > kFwdIlpWaves) waves = kFwdIlpWaves;
+  LrArgs a = make_args(p[0], waves);
+  a.nblk1 = a.nblk;
+  a.nblk = G * a.nblk1;
+  a.xld = (int)p[0].xld();
+  a.yhd = (int)p[0].yhd();
+  a.zrp = p[0].zeff ? (int)lr_bwd_zrow(p[0].R, p[0].static_w != nullptr) : 0;
+  for (int g = 0; g < G; ++g) {
+    a.grp[g] = LrFwdGroup{p[g].x, p[g].z, p[g].U, p[g].static_w, p[g].y, p[g].zeff};
+    a.zvec = a.zvec && aligned_to(p[g].z, 8);
+  }
+  if constexpr (RC == 1 && W <= 8) {
+    // all wavefronts resident at the ILP build's three per SIMD (see lowrank_mfma_fwd_ilp.hip);
+    // more only where the run length cap forces them
+    if (a.zrp == 0 && a.nblk * 4 <= kFwdIlpMaxWaves) return lr_fwd_ilp_launch<T, W>(a, p[0].stream);
+  }
+  if (a.zrp > 0) {
+    if (a.zvec)
+      lr_fwd_mfma<T, W, RC, true, true><<<a.nblk, 256, 0, p[0].stream>>>(a);
+    else
+      lr_fwd_mfma<T, W, RC, false, true><<<a.nblk, 256, 0, p[0].stream>>>(a);
+  } else {
+    if (a.zvec)
+      lr_fwd_mfma<T, W, RC, true, false><<<a.nblk, 256, 0, p[0].stream>>>(a);
+    else
+      lr_fwd_mfma<T, W, RC, false, false><<<a.nblk, 256, 0, p[0].stream>>>(a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// The forward at 9 <= W <= 16 with one or two rank chunks (lowrank_mfma_fwd_wide.hip).
+template <typename T>
+hipError_t lr_fwd_wide_dispatch(const LrProblem* pp, int G);
+
+}  // namespace dc

@@ -286,6 +286,10 @@ def test_kernel_paths(lib):
         assert lp(1, 64, 256, 40, 5, f16, 0, bwd) == 2         # W 5, three rank chunks
         assert lp(1, 64, 256, 63, 8, bf, 1, bwd) == 2          # W 8, four rank chunks
         assert lp(1, 64, 256, 64, 8, bf, 1, bwd) == 0          # kernel rank 65: generic
+        assert lp(2, 300, 256, 16, 12, bf, 0, bwd) == 2        # W 9-16 at kernel ranks <= 32
+        assert lp(2, 77, 200, 31, 16, bf, 1, bwd) == 2
+        assert lp(1, 64, 256, 40, 9, f16, 0, bwd) == 0         # W 9, kernel rank 40: generic
+        assert lp(1, 64, 256, 16, 17, bf, 0, bwd) == 0         # W 17: generic
     for bwd in (0, 1):                                         # D a multiple of 8, not of 16
         assert lp(2, 100, 200, 16, 4, bf, 0, bwd) == 2
         assert lp(1, 50, 1000, 15, 3, f16, 1, bwd) == 2

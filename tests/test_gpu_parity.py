@@ -268,11 +268,20 @@ LR_EDGE = [
     (1, 50, 1000, 15, 3, True, False, torch.float16, ("mfma", "mfma")),       # partial channel group
     (2, 33, 24, 7, 8, True, True, torch.bfloat16, ("mfma", "mfma")),          # W 8 gather form
     (1, 64, 72, 63, 2, False, True, torch.bfloat16, ("mfma", "mfma")),        # four rank chunks, tap passes
-    # widths above 8 and kernel ranks above 64 (the generic kernels; the reference accepts any
-    # W and power-of-two ranks, lowrank.py:220, 331-333)
+    # 9 <= W <= 16 at one or two rank chunks: the forward in one pass (x rows back to 4q-15), the
+    # backward as passes of at most 4 taps (x read 12 rows before each run in the last pass)
+    (1, 9, 64, 8, 16, False, True, torch.bfloat16, ("mfma", "mfma")),          # W 16 > T
+    (2, 300, 256, 16, 12, False, True, torch.bfloat16, ("mfma", "mfma")),      # passes 4 + 4 + 4
+    (1, 520, 128, 15, 9, True, False, torch.float16, ("mfma", "mfma")),        # passes 4 + 4 + 1
+    (2, 77, 200, 31, 16, True, True, torch.bfloat16, ("mfma", "mfma")),        # two rank chunks: 4 x 4 taps
+    (1, 3300, 256, 3, 13, False, True, torch.bfloat16, ("mfma", "mfma")),      # long runs, padded z
+    (1, 64, 512, 20, 10, True, True, torch.float16, ("mfma", "mfma")),         # kernel rank 21: passes 4 + 4 + 2
+    # widths above 16 (or above 8 at kernel ranks above 32) and kernel ranks above 64: the generic
+    # kernels (the reference accepts any W and power-of-two ranks, lowrank.py:220, 331-333)
     (1, 45, 64, 127, 12, True, True, torch.bfloat16, ("generic", "generic")),  # W 12, kernel rank 128
     (1, 30, 32, 255, 3, True, False, torch.float32, ("generic", "generic")),   # kernel rank 256 (the maximum)
-    (1, 9, 64, 8, 16, False, True, torch.bfloat16, ("generic", "generic")),    # W 16 > T
+    (1, 40, 64, 40, 9, False, True, torch.bfloat16, ("generic", "generic")),   # W 9, kernel rank 40
+    (1, 25, 64, 8, 20, False, True, torch.bfloat16, ("generic", "generic")),    # W 20 > T
 ]
 
 
