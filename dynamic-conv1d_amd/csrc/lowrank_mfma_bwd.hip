@@ -789,12 +789,16 @@ namespace {
 
 // Tile width and row runs per workgroup of a backward launch (see the kernel):
 // 32-channel tiles for two rank chunks at W <= 4, two row runs per workgroup
-// for one rank chunk at W <= 4, else 64-channel tiles and one run.
+// for one rank chunk at W <= 4, else 64-channel tiles and one run.  WIDE: the
+// passes of a one-rank-chunk problem above W 8 take 32-channel tiles and one
+// run (their later passes hold the earlier passes' dx as well, which 64-channel
+// tiles at two runs per workgroup spill: W 16 at B4 T4096 D2048 R16 backward
+// 440 us).
 struct BwdShape {
   int cpw, nrw;
 };
-constexpr BwdShape bwd_shape(int W, int RC) {
-  return BwdShape{(RC == 2 && W <= 4) ? 32 : 64, (RC == 1 && W <= 4) ? 2 : 1};
+constexpr BwdShape bwd_shape(int W, int RC, bool wide = false) {
+  return wide ? BwdShape{32, 1} : BwdShape{(RC == 2 && W <= 4) ? 32 : 64, (RC == 1 && W <= 4) ? 2 : 1};
 }
 
 // Taps per backward pass: what one pass's tap-weight and dz operands (registers
@@ -802,9 +806,9 @@ constexpr BwdShape bwd_shape(int W, int RC) {
 // consecutive passes of taps kofs .. kofs+taps-1 (see the kernel's kofs): every
 // W <= 8 at every rank <= 64, and W <= 16 at one or two rank chunks, stays on
 // matrix cores, reading x and dy once per pass.  Every pass of a problem takes
-// the same launch shape (bwd_shape: the dU partial rows of all passes line up),
-// so one rank chunk above W 8 runs passes of at most 4 taps (two runs per
-// workgroup, two wavefronts per SIMD; passes of 5-8 taps would hold one).
+// the same launch shape (bwd_shape: the dU partial rows of all passes line up);
+// one rank chunk above W 8 runs passes of at most 4 taps on 32-channel tiles
+// (bwd_shape's WIDE: two wavefronts per SIMD; passes of 5-8 taps would hold one).
 constexpr int pass_taps(int W, int RC) {
   return RC == 1 ? (W <= 8 ? W : 4) : RC == 2 ? (W < 4 ? W : 4) : RC == 3 ? (W < 2 ? W : 2) : 1;
 }
@@ -827,7 +831,7 @@ namespace {
 LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   LrBwdArgs a;
   const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
-  const BwdShape sh = bwd_shape(pass_taps((int)p.W, rc), rc);  // every pass has the same shape
+  const BwdShape sh = bwd_shape(pass_taps((int)p.W, rc), rc, rc == 1 && p.W > 8);  // every pass has the same shape
   const int ncw = 256 / sh.cpw;
   a.Tn = (int)p.T;
   a.D = (int)p.D;
@@ -927,13 +931,13 @@ BwdWs bwd_ws(const LrProblem& p, const LrBwdArgs& a) {
   return w;
 }
 
-template <typename T, int W, int RC>
+template <typename T, int W, int RC, bool WIDE = false>
 hipError_t launch_bwd_kernel(const LrBwdArgs& a, hipStream_t stream) {
-  constexpr BwdShape SH = bwd_shape(W, RC);  // as make_bwd_args
+  constexpr BwdShape SH = bwd_shape(W, RC, WIDE);  // as make_bwd_args
   constexpr int NRW = SH.nrw, CPW = SH.cpw, NT = 64 * (256 / CPW) * NRW;
   // later passes of taps: problems of 2+ rank chunks, and one rank chunk at W > 8
-  // (passes of at most 4 taps)
-  if constexpr (RC >= 2 || W <= 4) {
+  // (WIDE: passes of at most 4 taps)
+  if constexpr (RC >= 2 || WIDE) {
     if (a.accdx) {
       lr_bwd_mfma<T, W, RC, NRW, CPW, true><<<a.nblk, NT, 0, stream>>>(a);
       return hipGetLastError();
@@ -944,9 +948,19 @@ hipError_t launch_bwd_kernel(const LrBwdArgs& a, hipStream_t stream) {
 }
 
 // One pass's kernel for wq taps and rc rank chunks (the instantiated pairs:
-// pass_taps(W, RC) and the last pass's remainder).
+// pass_taps(W, RC) and the last pass's remainder); wide: a one-rank-chunk
+// problem above W 8.
 template <typename T>
-hipError_t dispatch_bwd_kernel(const LrBwdArgs& a, int wq, int rc, hipStream_t stream) {
+hipError_t dispatch_bwd_kernel(const LrBwdArgs& a, int wq, int rc, bool wide, hipStream_t stream) {
+  if (wide && rc == 1) {
+    switch (wq) {
+      case 1: return launch_bwd_kernel<T, 1, 1, true>(a, stream);
+      case 2: return launch_bwd_kernel<T, 2, 1, true>(a, stream);
+      case 3: return launch_bwd_kernel<T, 3, 1, true>(a, stream);
+      case 4: return launch_bwd_kernel<T, 4, 1, true>(a, stream);
+      default: return hipErrorInvalidValue;
+    }
+  }
 #define DC_LR_CASE(WW, CC) \
   if (wq == WW && rc == CC) return launch_bwd_kernel<T, WW, CC>(a, stream);
   DC_LR_CASE(1, 1) DC_LR_CASE(2, 1) DC_LR_CASE(3, 1) DC_LR_CASE(4, 1)
@@ -1006,7 +1020,7 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
       b.grp[g].part_dz = a.grp[g].part_dz + ps * dz_slot;
       b.grp[g].part_du = a.grp[g].part_du + kofs * D;
     }
-    if ((e = dispatch_bwd_kernel<T>(b, wq, rc, p[0].stream)) != hipSuccess) return e;
+    if ((e = dispatch_bwd_kernel<T>(b, wq, rc, W > 8, p[0].stream)) != hipSuccess) return e;
   }
   PartialReduce jobs[kMaxReduceJobs];
   int nj = 0;
