@@ -55,7 +55,9 @@ CASES = [
     (4, 1, 48, 64, 31, 3, True, 8, torch.bfloat16),     # four groups, two rank chunks
     (2, 2, 33, 128, 8, 2, False, 16, torch.float16),    # odd T
     (1, 2, 40, 48, 7, 4, True, 0, torch.bfloat16),      # one group
-    (2, 2, 24, 40, 3, 3, True, 12, torch.float32),      # fp32: generic path, D % 8 != 0
+    (2, 2, 24, 40, 3, 3, True, 12, torch.float32),      # fp32
+    (3, 2, 50, 64, 15, 12, True, 8, torch.bfloat16),    # W 12: backward as three passes of 4 taps
+    (2, 1, 70, 128, 31, 10, True, 0, torch.float16),    # W 10, two rank chunks
 ]
 
 
@@ -314,6 +316,7 @@ HEAD_CASES = [
     (3, 2, 45, 128, 15, 4, True, 64, torch.float32, True),     # fp32 VALU kernels
     (3, 2, 40, 128, 15, 4, True, 32, torch.bfloat16, False),   # head dim 32: generic backward
     (2, 1, 33, 64, 7, 2, True, 16, torch.float32, False),      # fp32 head dim 16: generic kernels
+    (3, 2, 60, 256, 15, 14, True, 64, torch.bfloat16, True),   # W 14: forward in one pass over the taps
 ]
 
 
