@@ -35,7 +35,9 @@ class _LowrankDynamicConvolutionFn(torch.autograd.Function):
         y = torch.empty_like(x)
         lib = _capi.load()
         dtype = _capi.dtype_code(x.dtype)
-        zeffs, nzeff = _zeff_buffers(lib, 1, B, T, D, R, W, dtype, static_w is not None, x.device)
+        # the padded z copy only serves a backward: none when no input needs a gradient (inference)
+        zeffs, nzeff = (_zeff_buffers(lib, 1, B, T, D, R, W, dtype, static_w is not None, x.device)
+                        if any(ctx.needs_input_grad) else (None, 0))
         zeff = zeffs[0] if zeffs else None
         status = lib.dc_lowrank_fwd(
             _capi.ptr(x), _capi.ptr(z), _capi.ptr(U), _capi.ptr(static_w), _capi.ptr(y), _capi.ptr(zeff), nzeff,
@@ -142,7 +144,8 @@ class _GroupedLowrankDynamicConvolutionFn(torch.autograd.Function):
         ys = [torch.empty(shape, dtype=x.dtype, device=x.device) for _ in range(G)]
         lib = _capi.load()
         dtype = _capi.dtype_code(x.dtype)
-        zeffs, nzeff = _zeff_buffers(lib, G, B, T, D, R, W, dtype, has_static, x.device)
+        zeffs, nzeff = (_zeff_buffers(lib, G, B, T, D, R, W, dtype, has_static, x.device)
+                        if any(ctx.needs_input_grad) else (None, 0))
         status = lib.dc_lowrank_fwd_grouped(
             G, _capi.ptr(x), x.stride(1), _capi.ptr_array(zs), _capi.ptr_array(Us), _capi.ptr_array(sws),
             _capi.ptr_array(ys), _capi.ptr_array(zeffs), nzeff, hd, B, T, D, R, W, dtype, int(bool(residual)),

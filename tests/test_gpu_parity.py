@@ -514,6 +514,33 @@ def test_generic_lowrank_rows_past_2_24():
     check_reductions("lr", q, dyq, g_k, dtype)
 
 
+# ------------------------------------------------------------ inference
+@pytest.mark.parametrize("R,static,W,dtype", [(15, True, 4, torch.bfloat16), (31, True, 4, torch.float16),
+                                              (16, False, 4, torch.bfloat16), (15, True, 12, torch.bfloat16)])
+def test_lowrank_inference_forward(R, static, W, dtype):
+    """Without gradients the forward skips the padded z copy for the backward (other kernel
+    instantiations): y is bitwise the training forward's, single and grouped."""
+    g = gen(23 + R + W)
+    Bn, Tn, Dn = 2, 300, 256
+    x = randn(g, Bn, Tn, Dn).to(dtype).to(DEV)
+    z = randn(g, Bn, Tn, R).to(dtype).to(DEV)
+    U = randn(g, R, W * Dn, scale=1 / math.sqrt((R + 1) * W)).to(dtype).to(DEV)
+    sw = uniform(g, W, Dn, lo=-0.5, hi=0.5).to(dtype).to(DEV) if static else None
+    with torch.no_grad():
+        y_inf = lr(x, z, U, sw, residual=True)
+    y_trn = lr(x.clone().requires_grad_(), z, U, sw, residual=True).detach()
+    assert torch.equal(y_inf, y_trn)
+    xs = randn(g, Bn, Tn, 3 * Dn).to(dtype).to(DEV)
+    zs = [z, z.flip(1).contiguous(), (z * 0.5).contiguous()]
+    with torch.no_grad():
+        ys_inf = lr_mod.lowrank_dynamic_convolution_grouped(xs, zs, [U] * 3, [sw] * 3 if static else None,
+                                                            residual=True)
+    ys_trn = lr_mod.lowrank_dynamic_convolution_grouped(xs.clone().requires_grad_(), zs, [U] * 3,
+                                                        [sw] * 3 if static else None, residual=True)
+    for a, b in zip(ys_inf, ys_trn):
+        assert torch.equal(a, b.detach())
+
+
 # ------------------------------------------------------------ determinism
 @pytest.mark.parametrize("kind", ["hw1", "hw32", "lr16s"])
 def test_deterministic(kind):
