@@ -7,6 +7,7 @@ RuntimeError is raised.
 """
 
 import ctypes
+import functools
 import os
 import threading
 
@@ -102,6 +103,28 @@ def ptr_array(ts):
 
 # torch's current-stream handle without building a Stream object (2 us -> 0.1 us per call)
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_get_device = getattr(torch._C, "_cuda_getDevice", None)
+
+
+def on_tensor_device(fn):
+    """Run an autograd Function's forward / backward with the device of its first tensor argument
+    current: the C ABI launches on the current device (the stream handle is that device's), so a
+    call on tensors of another GPU than the current one switches to theirs, as torch's own ops do.
+    A no-op (one device query) when that device is current already."""
+
+    @functools.wraps(fn)
+    def wrapper(ctx, *args):
+        t = next((a for a in args if isinstance(a, torch.Tensor)), None)
+        if t is None or not t.is_cuda:
+            return fn(ctx, *args)
+        dev = t.get_device()
+        cur = _get_device() if _get_device is not None else torch.cuda.current_device()
+        if dev == cur:
+            return fn(ctx, *args)
+        with torch.cuda.device(dev):
+            return fn(ctx, *args)
+
+    return wrapper
 
 
 def stream_of(t: torch.Tensor):

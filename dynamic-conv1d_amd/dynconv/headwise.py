@@ -14,6 +14,7 @@ class _HeadwiseDynamicConvolutionFn(torch.autograd.Function):
     """Autograd glue; mirrors headwise.py:218-309."""
 
     @staticmethod
+    @_capi.on_tensor_device
     def forward(ctx, x, weight, static_w, residual):
         B, T, D = x.shape
         H = weight.shape[2]
@@ -31,6 +32,7 @@ class _HeadwiseDynamicConvolutionFn(torch.autograd.Function):
         return y
 
     @staticmethod
+    @_capi.on_tensor_device
     def backward(ctx, dy):
         dy = dy.contiguous()
         x, weight, static_w = ctx.saved_tensors

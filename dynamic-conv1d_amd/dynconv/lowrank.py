@@ -28,6 +28,7 @@ class _LowrankDynamicConvolutionFn(torch.autograd.Function):
     """Autograd glue; mirrors lowrank.py:214-299."""
 
     @staticmethod
+    @_capi.on_tensor_device
     def forward(ctx, x, z, U, static_w, residual):
         B, T, D = x.shape
         R = z.shape[-1]
@@ -51,6 +52,7 @@ class _LowrankDynamicConvolutionFn(torch.autograd.Function):
         return y
 
     @staticmethod
+    @_capi.on_tensor_device
     def backward(ctx, dy):
         dy = dy.contiguous()
         x, z, U, static_w = ctx.saved_tensors
@@ -133,6 +135,7 @@ class _GroupedLowrankDynamicConvolutionFn(torch.autograd.Function):
     """
 
     @staticmethod
+    @_capi.on_tensor_device
     def forward(ctx, x, residual, G, has_static, hd, *params):
         zs, Us = params[:G], params[G:2 * G]
         sws = params[2 * G:3 * G] if has_static else None
@@ -158,6 +161,7 @@ class _GroupedLowrankDynamicConvolutionFn(torch.autograd.Function):
         return tuple(ys)
 
     @staticmethod
+    @_capi.on_tensor_device
     def backward(ctx, *dys):
         x, *params = ctx.saved_tensors
         G, has_static = ctx.G, ctx.has_static

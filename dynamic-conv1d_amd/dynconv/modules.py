@@ -30,6 +30,7 @@ class _ProjInFn(torch.autograd.Function):
     """z_g = (pre_z @ W_in^T)[..., g*R:(g+1)*R] for g < G, as G contiguous tensors, and its backward."""
 
     @staticmethod
+    @_capi.on_tensor_device
     def forward(ctx, pre_z, w_in, G, R):
         B, T, K = pre_z.shape
         M = B * T
@@ -43,6 +44,7 @@ class _ProjInFn(torch.autograd.Function):
         return tuple(zs)
 
     @staticmethod
+    @_capi.on_tensor_device
     def backward(ctx, *dzs):
         pre_z, w_in = ctx.saved_tensors
         G, R = ctx.G, ctx.R

@@ -41,3 +41,21 @@ def test_signatures():
     assert s.parameters["static_w"].default is None and s.parameters["residual"].default is False
     s = inspect.signature(lowrank.lowrank_dynamic_convolution)
     assert list(s.parameters) == ["x", "z", "U", "static_w", "residual"]
+
+
+def test_device_guard_passes_through_on_cpu():
+    """The autograd Functions' device guard (dynconv._capi.on_tensor_device): with no CUDA tensor
+    among the arguments it only forwards the call, arguments and result unchanged."""
+    from dynconv import _capi
+
+    seen = []
+
+    @_capi.on_tensor_device
+    def fn(ctx, *args):
+        seen.append((ctx, args))
+        return "result"
+
+    t = torch.zeros(3)
+    assert fn("ctx", None, t, 4) == "result"
+    assert seen == [("ctx", (None, t, 4))]
+    assert fn.__name__ == "fn"
