@@ -86,38 +86,105 @@ __global__ __launch_bounds__(256) void lr_bwd_dx_generic(const T* __restrict__ z
   }
 }
 
-// dz[row, r] = sum_{k, d} dy[row, d] * x[row-k, d] * U[r, k*D+d]; one
-// workgroup per row (a grid-stride loop over rows: the grid is capped like the
-// other generic launches), tree reduction in LDS.
+// Sums of v[0 .. N) over the wavefront's 64 lanes, reduce-scattered: each step
+// pairs lanes that differ in one bit (mask 32, 16, .., 1) and keeps the half of
+// the entries that bit selects (upper when set), adding the partner's copy.
+// Lane l ends with the totals of entries N/64 * l .. N/64 * l + N/64 - 1 in
+// v[0 .. N/64).  Fixed order: deterministic.
+template <int N>
+__device__ __forceinline__ void wave_reduce_scatter(float (&v)[N], int lane) {
+  static_assert(N % 64 == 0, "whole entries per lane");
+  int n = N;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const int half = n / 2;
+    const bool upper = (lane & m) != 0;
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      if (i < half) {
+        const float send = upper ? v[i] : v[i + half];
+        const float keep = upper ? v[i + half] : v[i];
+        v[i] = keep + __shfl_xor(send, m);
+      }
+    }
+    n = half;
+  }
+}
+
+// dz[row, r] = sum_{k, d} dy[row, d] * x[row-k, d] * U[r, k*D+d].  A job is a
+// block of kDzRows consecutive rows and kDzRanks ranks: each thread sums over
+// the channels d = tid, tid+256, .. for all rows x ranks of the job in
+// registers (every U element loaded once per job), then the 256 threads' sums
+// are added: reduce-scattered within each wavefront, then the four wavefronts
+// in wave order through LDS.  A grid-stride loop over jobs (the grid is capped).
+constexpr int kDzRows = 16, kDzRanks = 8;
 template <typename T>
 __global__ __launch_bounds__(256) void lr_bwd_dz_generic(const T* __restrict__ x, const T* __restrict__ U,
                                                          const T* __restrict__ dy, T* __restrict__ dz, int64_t BT,
                                                          int Tn, int D, int64_t xld, int hd, int R, int W) {
-  __shared__ float red[256];
+  constexpr int NV = kDzRows * kDzRanks;
+  __shared__ float red[4][NV];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t WD = (int64_t)W * D;
-  for (int64_t row = blockIdx.x; row < BT; row += gridDim.x) {
-    const int t = (int)(row % Tn);
-    for (int r = 0; r < R; ++r) {
-      float acc = 0.f;
-      for (int k = 0; k < W && k <= t; ++k) {
-        const T* xr = x + (row - k) * xld;
-        const T* ur = U + (int64_t)r * WD + (int64_t)k * D;
-        for (int d = threadIdx.x; d < D; d += 256)
-          acc = fmaf((float)dy[yoff(row, d, Tn, D, hd)] * (float)xr[d], (float)ur[d], acc);
+  const int nrc = (R + kDzRanks - 1) / kDzRanks;
+  const int64_t njobs = (BT + kDzRows - 1) / kDzRows * nrc;
+  for (int64_t job = blockIdx.x; job < njobs; job += gridDim.x) {
+    const int64_t rb = job / nrc * kDzRows;
+    const int r0 = (int)(job % nrc) * kDzRanks;
+    float acc[NV];
+#pragma unroll
+    for (int e = 0; e < NV; ++e) acc[e] = 0.f;
+    int tpos[kDzRows];  // position of each row in its sequence (-1 past BT): taps k <= t reach back
+#pragma unroll
+    for (int i = 0; i < kDzRows; ++i) tpos[i] = rb + i < BT ? (int)((rb + i) % Tn) : -1;
+    for (int d = threadIdx.x; d < D; d += 256) {
+      float dyv[kDzRows];
+#pragma unroll
+      for (int i = 0; i < kDzRows; ++i) {
+        const int64_t row = rb + i;
+        dyv[i] = row < BT ? (float)dy[yoff(row, d, Tn, D, hd)] : 0.f;
       }
-      red[threadIdx.x] = acc;
-      __syncthreads();
-      for (int s = 128; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
-        __syncthreads();
+      for (int k = 0; k < W; ++k) {
+        float u[kDzRanks];
+#pragma unroll
+        for (int j = 0; j < kDzRanks; ++j)
+          u[j] = r0 + j < R ? (float)U[(int64_t)(r0 + j) * WD + (int64_t)k * D + d] : 0.f;
+        // branch-free, so that the 16 loads go out together: rows whose tap k
+        // reaches before the sequence (or rows past BT) read their own row and add 0
+        float g[kDzRows];
+#pragma unroll
+        for (int i = 0; i < kDzRows; ++i) {
+          const bool in = tpos[i] >= k;
+          const float xv = (float)x[(in ? rb + i - k : (tpos[i] < 0 ? rb : rb + i)) * xld + d];
+          g[i] = in ? dyv[i] * xv : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < kDzRows; ++i)
+#pragma unroll
+          for (int j = 0; j < kDzRanks; ++j) acc[i * kDzRanks + j] = fmaf(g[i], u[j], acc[i * kDzRanks + j]);
       }
-      if (threadIdx.x == 0) dz[row * R + r] = (T)red[0];
-      __syncthreads();
     }
+    wave_reduce_scatter<NV>(acc, lane);
+#pragma unroll
+    for (int e = 0; e < NV / 64; ++e) red[wave][NV / 64 * lane + e] = acc[e];
+    __syncthreads();
+    if ((int)threadIdx.x < NV) {
+      const int e = threadIdx.x;
+      const float v = ((red[0][e] + red[1][e]) + red[2][e]) + red[3][e];
+      const int64_t row = rb + e / kDzRanks;
+      const int r = r0 + e % kDzRanks;
+      if (row < BT && r < R) dz[row * R + r] = (T)v;
+    }
+    __syncthreads();
   }
 }
 
-// dU (and dstatic as kernel rank R) partials: grid (ceil(RK*W*D/256), P).
+// dU (and dstatic as kernel rank R) partials: a thread owns one column (k, d)
+// of U for a slice of rows (blockIdx.y) and kDuRanks kernel ranks
+// (blockIdx.z), all in registers, so each dy / x element is read once per
+// chunk of ranks; z_eff of a row is the same for the whole workgroup.  Grid
+// (ceil(W*D / 256), P, ceil(RK / kDuRanks)).
+constexpr int kDuRanks = 16;
 template <typename T>
 __global__ __launch_bounds__(256) void lr_bwd_du_generic(const T* __restrict__ x, const T* __restrict__ z,
                                                          const T* __restrict__ dy, float* __restrict__ part,
@@ -125,20 +192,45 @@ __global__ __launch_bounds__(256) void lr_bwd_du_generic(const T* __restrict__ x
                                                          int RK, int W, int64_t rows_per) {
   const int64_t WD = (int64_t)W * D;
   const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (c >= (int64_t)RK * WD) return;
-  const int r = (int)(c / WD);
-  const int64_t col = c - (int64_t)r * WD;
-  const int k = (int)(col / D);
-  const int d = (int)(col - (int64_t)k * D);
-  const int64_t r0 = (int64_t)blockIdx.y * rows_per;
-  const int64_t r1 = min(r0 + rows_per, BT);
-  float acc = 0.f;
-  for (int64_t row = r0; row < r1; ++row) {
-    const int t = (int)(row % Tn);
-    if (t >= k)
-      acc = fmaf(zrank(z, row, R, r), (float)dy[yoff(row, d, Tn, D, hd)] * (float)x[(row - k) * xld + d], acc);
+  if (c >= WD) return;  // no barriers below
+  const int k = (int)(c / D);
+  const int d = (int)(c - (int64_t)k * D);
+  const int r0 = (int)blockIdx.z * kDuRanks;
+  const int64_t s0 = (int64_t)blockIdx.y * rows_per;
+  const int64_t s1 = min(s0 + rows_per, BT);
+  float acc[kDuRanks];
+#pragma unroll
+  for (int j = 0; j < kDuRanks; ++j) acc[j] = 0.f;
+  // rows in steps of kDuStep, branch-free so that a step's loads go out
+  // together: rows past the slice, or whose tap k reaches before the sequence,
+  // read the slice's first row and add 0
+  constexpr int kDuStep = 8;
+  int t = (int)(s0 % Tn);  // the position in its sequence of the step's first row
+  for (int64_t row = s0; row < s1; row += kDuStep) {
+    float g[kDuStep];
+    int tu = t;
+#pragma unroll
+    for (int u = 0; u < kDuStep; ++u) {
+      const bool in = row + u < s1 && tu >= k;
+      const int64_t rr = in ? row + u : s0;
+      const float gv = (float)dy[yoff(rr, d, Tn, D, hd)] * (float)x[(in ? rr - k : rr) * xld + d];
+      g[u] = in ? gv : 0.f;
+      tu = tu + 1 == Tn ? 0 : tu + 1;
+    }
+#pragma unroll
+    for (int u = 0; u < kDuStep; ++u) {
+      const int64_t rr = row + u < s1 ? row + u : s0;
+#pragma unroll
+      for (int j = 0; j < kDuRanks; ++j) {
+        const int r = r0 + j;
+        if (r < RK) acc[j] = fmaf(zrank(z, rr, R, r), g[u], acc[j]);
+      }
+    }
+    t = tu;
   }
-  part[(int64_t)blockIdx.y * RK * WD + c] = acc;
+#pragma unroll
+  for (int j = 0; j < kDuRanks; ++j)
+    if (r0 + j < RK) part[((int64_t)blockIdx.y * RK + r0 + j) * WD + c] = acc[j];
 }
 
 // ------------------------------------------------------------------- host
@@ -153,10 +245,13 @@ unsigned generic_grid(int64_t n) {
   return (unsigned)(g < 1 ? 1 : g);
 }
 
-// Workgroups of the generic dz launch: one per row, at most 65536 (a
-// grid-stride loop takes the rest).  HIP rejects grids above 2^32 work-items,
-// which one workgroup of 256 per row would reach at B*T >= 2^24.
-unsigned dz_grid(int64_t BT) { return (unsigned)(BT < 65536 ? BT : 65536); }
+// Workgroups of the generic dz launch: one per job (kDzRows rows x kDzRanks
+// ranks), at most 65536 (a grid-stride loop takes the rest: HIP rejects grids
+// above 2^32 work-items).
+unsigned dz_grid(int64_t BT, int R) {
+  const int64_t jobs = (BT + kDzRows - 1) / kDzRows * ((R + kDzRanks - 1) / kDzRanks);
+  return (unsigned)(jobs < 65536 ? jobs : 65536);
+}
 
 int generic_partials(int64_t BT) {
   int64_t P = (BT + 255) / 256;
@@ -180,12 +275,12 @@ hipError_t bwd_generic(const LrProblem& p) {
   lr_bwd_dx_generic<T><<<generic_grid(BT * p.D), 256, 0, p.stream>>>(
       (const T*)p.z, (const T*)p.U, (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, BT, (int)p.T, (int)p.D,
       p.dxld(), (int)p.yhd(), (int)p.R, (int)p.W, p.residual);
-  lr_bwd_dz_generic<T><<<dz_grid(BT), 256, 0, p.stream>>>((const T*)p.x, (const T*)p.U, (const T*)p.dy,
+  lr_bwd_dz_generic<T><<<dz_grid(BT, (int)p.R), 256, 0, p.stream>>>((const T*)p.x, (const T*)p.U, (const T*)p.dy,
                                                           (T*)p.dz, BT, (int)p.T, (int)p.D, p.xld(), (int)p.yhd(),
                                                           (int)p.R, (int)p.W);
   const int P = generic_partials(BT);
   const int64_t rows_per = (BT + P - 1) / P;
-  dim3 grid((unsigned)((RK * WD + 255) / 256), (unsigned)P);
+  dim3 grid((unsigned)((WD + 255) / 256), (unsigned)P, (unsigned)((RK + kDuRanks - 1) / kDuRanks));
   lr_bwd_du_generic<T><<<grid, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.z, (const T*)p.dy, p.ws, BT,
                                                    (int)p.T, (int)p.D, p.xld(), (int)p.yhd(), (int)p.R, RK,
                                                    (int)p.W, rows_per);
