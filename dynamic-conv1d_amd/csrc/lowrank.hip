@@ -8,9 +8,8 @@
 // with z == 1 and U row = static_w (lowrank.py:223-225); here it is an
 // implicit rank R of the kernel, so no padded z or concatenated U is built.
 //
-// This file holds the one-thread-per-output kernels used for fp32 and for
-// shapes the MFMA path (lowrank_mfma_fwd.hip, lowrank_mfma_bwd.hip) does not
-// take, plus the dispatch.  x (and dx) rows may be xld (dxld) elements apart,
+// This file holds the generic kernels, for the shapes no fast path takes
+// (lowrank_mfma_*.hip, lowrank_f32*.hip), plus the dispatch.  x (and dx) rows may be xld (dxld) elements apart,
 // for inputs read out of a fused projection.
 #include "lowrank_mfma.h"
 
@@ -48,41 +47,141 @@ __device__ __forceinline__ float lr_tap(const T* __restrict__ z, const T* __rest
   return w;
 }
 
+// Generic forward and dx: a job is a block of kGenRows consecutive rows.  The
+// z rows it needs (fp32, ranks padded with zeros to a multiple of 4) are staged
+// in LDS once per job; a thread takes channels d = tid, tid+256, .. and, per
+// tap, loads each U element once for all rows of the job.  Per output the
+// arithmetic is lr_tap's (ranks in order, then the static filter) and the taps
+// add in order, as one thread per output would.  A grid-stride loop over jobs
+// (the grid is capped).
+constexpr int kGenRows = 16;
+constexpr int kGenMaxR = 256;  // kernel ranks of the generic path (DC_MAX_R)
+
+// z rows rb .. rb+nrows-1 of the job into zs[i * rp + r] (0 past R and past BT).
+template <typename T>
+__device__ __forceinline__ void stage_zrows(float* __restrict__ zs, const T* __restrict__ z, int64_t rb, int nrows,
+                                            int R, int rp, int64_t BT) {
+  for (int e = threadIdx.x; e < nrows * rp; e += 256) {
+    const int i = e / rp, r = e - i * rp;
+    const int64_t row = rb + i;
+    zs[e] = row < BT && r < R ? (float)z[row * R + r] : 0.f;
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void lr_fwd_generic(const T* __restrict__ x, const T* __restrict__ z,
                                                       const T* __restrict__ U, const T* __restrict__ sw,
                                                       T* __restrict__ y, int64_t BT, int Tn, int D, int64_t xld,
                                                       int hd, int R, int W, int residual) {
-  const int64_t n = BT * D;
+  __shared__ __attribute__((aligned(16))) float zs[kGenRows * kGenMaxR];
   const int64_t WD = (int64_t)W * D;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const int64_t row = i / D;
-    const int d = (int)(i - row * D);
-    const int t = (int)(row % Tn);
-    float acc = 0.f;
-    for (int k = 0; k < W && k <= t; ++k)
-      acc = fmaf(lr_tap(z, U, sw, row, R, WD, (int64_t)k * D + d), (float)x[(row - k) * xld + d], acc);
-    if (residual) acc += (float)x[row * xld + d];
-    y[yoff(row, d, Tn, D, hd)] = (T)acc;
+  const int rp = (R + 3) / 4 * 4;
+  const int64_t njobs = (BT + kGenRows - 1) / kGenRows;
+  for (int64_t job = blockIdx.x; job < njobs; job += gridDim.x) {
+    const int64_t rb = job * kGenRows;
+    __syncthreads();  // the previous job's reads of zs are done
+    stage_zrows(zs, z, rb, kGenRows, R, rp, BT);
+    __syncthreads();
+    int tpos[kGenRows];  // position of each row in its sequence, -1 past BT
+#pragma unroll
+    for (int i = 0; i < kGenRows; ++i) tpos[i] = rb + i < BT ? (int)((rb + i) % Tn) : -1;
+    for (int d = threadIdx.x; d < D; d += 256) {
+      float acc[kGenRows];
+#pragma unroll
+      for (int i = 0; i < kGenRows; ++i) acc[i] = 0.f;
+      for (int k = 0; k < W; ++k) {
+        float kw[kGenRows];
+#pragma unroll
+        for (int i = 0; i < kGenRows; ++i) kw[i] = 0.f;
+        for (int r = 0; r < rp; r += 4) {
+          float u[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) u[q] = r + q < R ? (float)U[(int64_t)(r + q) * WD + (int64_t)k * D + d] : 0.f;
+#pragma unroll
+          for (int i = 0; i < kGenRows; ++i) {
+            const float4 zv = *reinterpret_cast<const float4*>(zs + i * rp + r);
+            kw[i] = fmaf(zv.x, u[0], kw[i]);
+            kw[i] = fmaf(zv.y, u[1], kw[i]);
+            kw[i] = fmaf(zv.z, u[2], kw[i]);
+            kw[i] = fmaf(zv.w, u[3], kw[i]);
+          }
+        }
+        const float st = sw ? (float)sw[(int64_t)k * D + d] : 0.f;
+#pragma unroll
+        for (int i = 0; i < kGenRows; ++i) {
+          const bool in = tpos[i] >= k;  // rows whose tap k reaches before the sequence add nothing
+          const float xv = (float)x[(in ? rb + i - k : rb) * xld + d];
+          if (in) acc[i] = fmaf(sw ? kw[i] + st : kw[i], xv, acc[i]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kGenRows; ++i) {
+        if (tpos[i] < 0) continue;
+        float v = acc[i];
+        if (residual) v += (float)x[(rb + i) * xld + d];
+        y[yoff(rb + i, d, Tn, D, hd)] = (T)v;
+      }
+    }
   }
 }
 
+// dx[row, d] = sum_k dy[row+k, d] * Kw[row+k, k, d] (+ dy): the job's rows need
+// z of rows rb .. rb+kGenRows+W-2 (W <= 32).
 template <typename T>
 __global__ __launch_bounds__(256) void lr_bwd_dx_generic(const T* __restrict__ z, const T* __restrict__ U,
                                                          const T* __restrict__ sw, const T* __restrict__ dy,
                                                          T* __restrict__ dx, int64_t BT, int Tn, int D,
                                                          int64_t dxld, int hd, int R, int W, int residual) {
-  const int64_t n = BT * D;
+  __shared__ __attribute__((aligned(16))) float zs[(kGenRows + 31) * kGenMaxR / 4 * 4];
   const int64_t WD = (int64_t)W * D;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const int64_t row = i / D;
-    const int d = (int)(i - row * D);
-    const int t = (int)(row % Tn);
-    float acc = 0.f;
-    for (int k = 0; k < W && t + k < Tn; ++k)
-      acc = fmaf((float)dy[yoff(row + k, d, Tn, D, hd)], lr_tap(z, U, sw, row + k, R, WD, (int64_t)k * D + d), acc);
-    if (residual) acc += (float)dy[yoff(row, d, Tn, D, hd)];
-    dx[row * dxld + d] = (T)acc;
+  const int rp = (R + 3) / 4 * 4;
+  const int nz = kGenRows + W - 1;
+  const int64_t njobs = (BT + kGenRows - 1) / kGenRows;
+  for (int64_t job = blockIdx.x; job < njobs; job += gridDim.x) {
+    const int64_t rb = job * kGenRows;
+    __syncthreads();
+    stage_zrows(zs, z, rb, nz, R, rp, BT);
+    __syncthreads();
+    int tpos[kGenRows];
+#pragma unroll
+    for (int i = 0; i < kGenRows; ++i) tpos[i] = rb + i < BT ? (int)((rb + i) % Tn) : -1;
+    for (int d = threadIdx.x; d < D; d += 256) {
+      float acc[kGenRows];
+#pragma unroll
+      for (int i = 0; i < kGenRows; ++i) acc[i] = 0.f;
+      for (int k = 0; k < W; ++k) {
+        float kw[kGenRows];
+#pragma unroll
+        for (int i = 0; i < kGenRows; ++i) kw[i] = 0.f;
+        for (int r = 0; r < rp; r += 4) {
+          float u[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) u[q] = r + q < R ? (float)U[(int64_t)(r + q) * WD + (int64_t)k * D + d] : 0.f;
+#pragma unroll
+          for (int i = 0; i < kGenRows; ++i) {
+            const float4 zv = *reinterpret_cast<const float4*>(zs + (i + k) * rp + r);  // row rb+i+k
+            kw[i] = fmaf(zv.x, u[0], kw[i]);
+            kw[i] = fmaf(zv.y, u[1], kw[i]);
+            kw[i] = fmaf(zv.z, u[2], kw[i]);
+            kw[i] = fmaf(zv.w, u[3], kw[i]);
+          }
+        }
+        const float st = sw ? (float)sw[(int64_t)k * D + d] : 0.f;
+#pragma unroll
+        for (int i = 0; i < kGenRows; ++i) {
+          const bool in = tpos[i] >= 0 && tpos[i] + k < Tn;  // row rb+i+k in the same sequence
+          const float dv = (float)dy[yoff(in ? rb + i + k : rb, d, Tn, D, hd)];
+          if (in) acc[i] = fmaf(dv, sw ? kw[i] + st : kw[i], acc[i]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kGenRows; ++i) {
+        if (tpos[i] < 0) continue;
+        float v = acc[i];
+        if (residual) v += (float)dy[yoff(rb + i, d, Tn, D, hd)];
+        dx[(rb + i) * dxld + d] = (T)v;
+      }
+    }
   }
 }
 
@@ -239,17 +338,18 @@ namespace {
 bool aligned_to16(const void* p) { return aligned_to(p, 16); }
 bool aligned_to8(const void* p) { return aligned_to(p, 8); }
 
-unsigned generic_grid(int64_t n) {
-  int64_t g = (n + 255) / 256;
-  if (g > 65536) g = 65536;
-  return (unsigned)(g < 1 ? 1 : g);
-}
-
 // Workgroups of the generic dz launch: one per job (kDzRows rows x kDzRanks
 // ranks), at most 65536 (a grid-stride loop takes the rest: HIP rejects grids
 // above 2^32 work-items).
 unsigned dz_grid(int64_t BT, int R) {
   const int64_t jobs = (BT + kDzRows - 1) / kDzRows * ((R + kDzRanks - 1) / kDzRanks);
+  return (unsigned)(jobs < 65536 ? jobs : 65536);
+}
+
+// Workgroups of the generic forward / dx launches: one per job of kGenRows
+// rows, at most 65536 (a grid-stride loop takes the rest).
+unsigned gen_row_grid(int64_t BT) {
+  const int64_t jobs = (BT + kGenRows - 1) / kGenRows;
   return (unsigned)(jobs < 65536 ? jobs : 65536);
 }
 
@@ -261,7 +361,7 @@ int generic_partials(int64_t BT) {
 template <typename T>
 hipError_t fwd_generic(const LrProblem& p) {
   const int64_t BT = p.B * p.T;
-  lr_fwd_generic<T><<<generic_grid(BT * p.D), 256, 0, p.stream>>>(
+  lr_fwd_generic<T><<<gen_row_grid(BT), 256, 0, p.stream>>>(
       (const T*)p.x, (const T*)p.z, (const T*)p.U, (const T*)p.static_w, (T*)p.y, BT, (int)p.T, (int)p.D, p.xld(),
       (int)p.yhd(), (int)p.R, (int)p.W, p.residual);
   return hipGetLastError();
@@ -272,7 +372,7 @@ hipError_t bwd_generic(const LrProblem& p) {
   const int64_t BT = p.B * p.T;
   const int RK = (int)p.R + (p.static_w ? 1 : 0);
   const int64_t WD = p.W * p.D;
-  lr_bwd_dx_generic<T><<<generic_grid(BT * p.D), 256, 0, p.stream>>>(
+  lr_bwd_dx_generic<T><<<gen_row_grid(BT), 256, 0, p.stream>>>(
       (const T*)p.z, (const T*)p.U, (const T*)p.static_w, (const T*)p.dy, (T*)p.dx, BT, (int)p.T, (int)p.D,
       p.dxld(), (int)p.yhd(), (int)p.R, (int)p.W, p.residual);
   lr_bwd_dz_generic<T><<<dz_grid(BT, (int)p.R), 256, 0, p.stream>>>((const T*)p.x, (const T*)p.U, (const T*)p.dy,
