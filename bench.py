@@ -97,6 +97,9 @@ EXTRA = {
     "lr_r16_fp32": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=4, static=False, residual=True, dtype="fp32"),
     # W 16 at rank 16: the forward in one pass over the taps, the backward as four passes of 4 taps
     "lr_W16": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=16, static=False, residual=True),
+    # headwise above W 8: the wide row-ring kernels (head sizes 1 and 32, static filter, residual)
+    "hw_W12_hs1": dict(kind="hw", B=4, T=4096, D=2048, H=2048, W=12, static=True, residual=True),
+    "hw_W12_hs32": dict(kind="hw", B=4, T=4096, D=2048, H=64, W=12, static=True, residual=True),
     # a width the fast kernels do not take (W <= 16): the generic kernels (one thread per output), for their cost
     "lr_W20_generic": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=20, static=False, residual=True),
     # the reference bench.py's own shapes (bench.py:7-12): head sizes 1, 4, 16 and rank 16, no static_w, no residual

@@ -1,8 +1,10 @@
 // Headwise dynamic causal short convolution: host planning, generic kernels.
 //
-// The vectorised kernels live in headwise_fast.h and are instantiated per
-// (dtype, direction) in headwise_fast_*.hip so they compile in parallel.
-#include "headwise_fast.h"
+// The vectorised kernels (W <= 8) live in headwise_fast.h and the wide ones
+// (9 <= W <= 16) in headwise_wide.h; both are instantiated per (dtype,
+// direction) in headwise_fast_*.hip / headwise_wide_*.hip so they compile in
+// parallel.
+#include "headwise_wide.h"
 
 namespace dc {
 
@@ -12,6 +14,12 @@ extern template hipError_t dispatch_fast<fp16, false>(const HwProblem&, const Hw
 extern template hipError_t dispatch_fast<fp16, true>(const HwProblem&, const HwPlan&);
 extern template hipError_t dispatch_fast<float, false>(const HwProblem&, const HwPlan&);
 extern template hipError_t dispatch_fast<float, true>(const HwProblem&, const HwPlan&);
+extern template hipError_t dispatch_wide<bf16, false>(const HwProblem&, const HwWideArgs&);
+extern template hipError_t dispatch_wide<bf16, true>(const HwProblem&, const HwWideArgs&);
+extern template hipError_t dispatch_wide<fp16, false>(const HwProblem&, const HwWideArgs&);
+extern template hipError_t dispatch_wide<fp16, true>(const HwProblem&, const HwWideArgs&);
+extern template hipError_t dispatch_wide<float, false>(const HwProblem&, const HwWideArgs&);
+extern template hipError_t dispatch_wide<float, true>(const HwProblem&, const HwWideArgs&);
 
 // ------------------------------------------------------------ generic path
 // Any D, any head size dividing D, any W <= DC_MAX_W, element alignment only.
@@ -176,6 +184,71 @@ HwPlan make_plan(const HwProblem& p, bool bwd) {
   return pl;
 }
 
+// ------------------------------------------------------------ wide path
+// 9 <= W <= 16 (headwise_wide.h): power-of-two head sizes up to 128, D a
+// multiple of 128, 16-byte weight-row segments per wavefront.
+int wide_block(int W) { return W % 2 == 0 ? W : 2 * W; }
+
+// Wavefronts per launch: two per SIMD (the kernels take up to 2 x 128 VGPRs
+// per lane), runs of at least one row block.
+constexpr int kWideTargetWaves = 2048;
+
+HwWideArgs make_wide_args(const HwProblem& p) {
+  const int64_t es = dtype_size(p.dtype);
+  const int64_t hs = p.D / p.H;
+  const int L = wide_block((int)p.W);
+  HwWideArgs a;
+  a.Tn = (int)p.T;
+  a.D = (int)p.D;
+  a.H = (int)p.H;
+  a.hs_shift = ilog2(hs);
+  a.lph = hs >= 2 ? (int)(hs / 2) : 1;
+  a.nwc = (int)(p.D / kWideCols);
+  int64_t seg = (p.B * p.T * a.nwc + kWideTargetWaves - 1) / kWideTargetWaves;
+  seg = (seg + L - 1) / L * L;
+  if (seg < L) seg = L;
+  const int64_t tcap = (p.T + L - 1) / L * L;
+  if (seg > tcap) seg = tcap;
+  const int64_t seg_cap = (kHwRunBytes / max_row_bytes(p) - kHwSlackRows) / L * L;
+  if (seg > seg_cap) seg = seg_cap;
+  a.seg = (int)seg;
+  a.nspb = (int)((p.T + seg - 1) / seg);
+  a.nseg = (int)(p.B * a.nspb);
+  a.nblk = ((a.nseg + 3) / 4) * a.nwc;
+  a.sbytes = (int)((kWideCols >> a.hs_shift) * p.W * es);
+  a.residual = p.residual;
+  return a;
+}
+
+bool hw_wide_ok(const HwProblem& p, bool bwd) {
+  const int64_t es = dtype_size(p.dtype);
+  const int64_t hs = p.D / p.H;
+  if (p.W < kHwWideMinW || p.W > kHwWideMaxW) return false;
+  if ((hs & (hs - 1)) != 0 || hs > kWideCols) return false;  // a head within one wavefront
+  if (p.D % kWideCols != 0) return false;
+  // the wavefront's weight segment and a weight row: whole 16-byte pieces
+  if (((kWideCols / hs) * p.W * es) % 16 != 0 || (p.H * p.W * es) % 16 != 0) return false;
+  // a run of one row block plus the look-ahead rows fits the resource range
+  if ((wide_block((int)p.W) + kHwSlackRows) * max_row_bytes(p) > kHwRunBytes) return false;
+  const int ea = (int)(kWideCpl * es);  // a lane's channels
+  if (!aligned(p.x, ea) || !aligned(p.static_w, ea) || !aligned(p.weight, 16)) return false;
+  if (!bwd) return aligned(p.y, ea);
+  return aligned(p.dy, ea) && aligned(p.dx, ea) && aligned(p.dweight, 16);
+}
+
+template <typename T>
+hipError_t fwd_wide(const HwProblem& p) {
+  return dispatch_wide<T, false>(p, make_wide_args(p));
+}
+
+template <typename T>
+hipError_t bwd_wide(const HwProblem& p) {
+  const HwWideArgs a = make_wide_args(p);
+  hipError_t e = dispatch_wide<T, true>(p, a);
+  if (e != hipSuccess || !p.static_w) return e;
+  return reduce_partials(p.ws, p.W * p.D, (a.nseg + 3) / 4, p.W * p.D, p.dstatic_w, p.dtype, p.stream);
+}
+
 unsigned generic_grid(int64_t n) {
   int64_t g = (n + 255) / 256;
   if (g > 65536) g = 65536;
@@ -243,12 +316,16 @@ int64_t hw_bwd_ws_bytes(const HwProblem& p) {
   int P;
   if (hw_fast_ok(p, true))
     P = make_plan(p, true).P;
+  else if (hw_wide_ok(p, true))
+    P = (make_wide_args(p).nseg + 3) / 4;
   else
     P = generic_partials(p.B * p.T);
   return (int64_t)P * p.W * p.D * (int64_t)sizeof(float);
 }
 
-int hw_path(const HwProblem& p, bool bwd) { return hw_fast_ok(p, bwd) ? 1 : 0; }
+int hw_path(const HwProblem& p, bool bwd) {
+  return hw_fast_ok(p, bwd) ? 1 : hw_wide_ok(p, bwd) ? 5 : 0;
+}
 
 hipError_t hw_fwd(const HwProblem& p) {
   if (hw_fast_ok(p, false)) {
@@ -257,6 +334,13 @@ hipError_t hw_fwd(const HwProblem& p) {
       case kBF16: return dispatch_fast<bf16, false>(p, pl);
       case kFP16: return dispatch_fast<fp16, false>(p, pl);
       default: return dispatch_fast<float, false>(p, pl);
+    }
+  }
+  if (hw_wide_ok(p, false)) {
+    switch (p.dtype) {
+      case kBF16: return fwd_wide<bf16>(p);
+      case kFP16: return fwd_wide<fp16>(p);
+      default: return fwd_wide<float>(p);
     }
   }
   switch (p.dtype) {
@@ -273,6 +357,13 @@ hipError_t hw_bwd(const HwProblem& p) {
       case kBF16: return dispatch_fast<bf16, true>(p, pl);
       case kFP16: return dispatch_fast<fp16, true>(p, pl);
       default: return dispatch_fast<float, true>(p, pl);
+    }
+  }
+  if (hw_wide_ok(p, true)) {
+    switch (p.dtype) {
+      case kBF16: return bwd_wide<bf16>(p);
+      case kFP16: return bwd_wide<fp16>(p);
+      default: return bwd_wide<float>(p);
     }
   }
   switch (p.dtype) {

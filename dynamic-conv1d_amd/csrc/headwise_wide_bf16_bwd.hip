@@ -1,0 +1,6 @@
+// Wide-W headwise kernels (headwise_wide.h), bf16 backward.
+#include "headwise_wide.h"
+
+namespace dc {
+template hipError_t dispatch_wide<bf16, true>(const HwProblem&, const HwWideArgs&);
+}  // namespace dc

@@ -253,7 +253,8 @@ def test_headwise_bwd_noalloc_validation(lib):
 
 def test_kernel_paths(lib):
     """dc_headwise_path / dc_lowrank_path: the kernel family each BASELINE shape and a few edge shapes
-    take (0 generic, 1 vector, 2 matrix cores, 3 fp32 matrix cores, 4 fp32 VALU); host logic only."""
+    take (0 generic, 1 vector, 2 matrix cores, 3 fp32 matrix cores, 4 fp32 VALU, 5 headwise wide);
+    host logic only."""
     bf, f16, f32 = 0, 1, 2
     hp, lp = lib.dc_headwise_path, lib.dc_lowrank_path
     for bwd in (0, 1):
@@ -264,7 +265,10 @@ def test_kernel_paths(lib):
         assert lp(2, 8192, 4096, 31, 4, bf, 1, bwd) == 2       # configs[4]
         assert lp(4, 4096, 2048, 16, 4, f32, 0, bwd) == 3      # the fp32 tier on matrix cores
         assert hp(1, 40, 2048, 2, 4, bf, 1, bwd) == 0          # head size 1024: generic
-        assert hp(1, 50, 64, 16, 12, bf, 1, bwd) == 0          # W 12: generic
+        assert hp(1, 50, 64, 16, 12, bf, 1, bwd) == 0          # W 12, D 64: generic
+        assert hp(4, 4096, 2048, 2048, 12, bf, 1, bwd) == 5    # W 12, head size 1: wide
+        assert hp(4, 4096, 2048, 64, 16, f32, 0, bwd) == 5     # W 16, head size 32: wide
+        assert hp(1, 50, 256, 2, 9, bf, 1, bwd) == 0           # head size 128, W 9: 18-byte segments
         assert lp(1, 45, 64, 127, 12, bf, 1, bwd) == 0         # W 12, kernel rank 128: generic
         assert lp(1, 70, 128, 64, 1, bf, 0, bwd) == 2          # kernel rank 64, W 1
         assert lp(1, 40, 128, 40, 2, f16, 0, bwd) == 2         # kernel rank 40, W 2

@@ -133,17 +133,29 @@ HW_EDGE = [
     (1, 260, 256, 256, 2, False, True, torch.float32),  # hs 1 fp32, W 2: NP 2
     (2, 181, 512, 256, 4, True, False, torch.bfloat16), # hs 2, W 4: NP 2
     (1, 333, 1024, 1024, 4, True, True, torch.bfloat16),  # hs 1, W 4: NP 4, two wavefront columns
-    # widths above 8 (the generic kernels; the reference accepts any W, headwise.py:226)
-    (1, 50, 64, 16, 12, True, True, torch.bfloat16),   # W 12
-    (2, 40, 128, 128, 16, True, False, torch.float32),  # W 16, head size 1
-    (1, 10, 64, 32, 32, True, True, torch.bfloat16),   # W 32 (the maximum) > T
+    # widths above 8 (the reference accepts any W, headwise.py:226): 9 <= W <= 16 on the wide
+    # row-ring kernels when D % 128 == 0 and a head lies in one wavefront, else the generic ones
+    (1, 50, 64, 16, 12, True, True, torch.bfloat16),   # W 12, D 64: generic
+    (2, 40, 128, 128, 16, True, False, torch.float32),  # W 16, head size 1: wide
+    (1, 10, 64, 32, 32, True, True, torch.bfloat16),   # W 32 (the maximum) > T: generic
+    (2, 77, 256, 256, 9, True, True, torch.bfloat16),   # wide: hs 1, odd W (ring of W + 1 rows)
+    (1, 100, 128, 64, 10, False, True, torch.float16),  # wide: hs 2
+    (2, 61, 384, 96, 11, True, False, torch.float32),   # wide: hs 4, three wavefront columns
+    (1, 130, 256, 8, 12, True, True, torch.bfloat16),   # wide: hs 32
+    (2, 45, 256, 2, 13, True, True, torch.float32),     # wide: hs 128 (a head is a whole wavefront)
+    (1, 90, 128, 16, 14, False, False, torch.bfloat16), # wide: hs 8
+    (1, 7, 128, 128, 15, True, True, torch.float16),    # wide: T < W
+    (2, 200, 256, 32, 16, True, True, torch.float16),   # wide: hs 8, W 16
+    (1, 1, 128, 64, 16, True, True, torch.bfloat16),    # wide: T 1
+    (1, 50, 256, 2, 9, True, True, torch.bfloat16),     # hs 128 bf16 W 9: 18-byte weight segments, generic
 ]
 
 
 @pytest.mark.parametrize("Bn,Tn,Dn,H,W,static,residual,dtype", HW_EDGE)
 def test_edge_shapes_headwise(Bn, Tn, Dn, H, W, static, residual, dtype):
     g = gen(Bn * 1000003 + Tn * 1009 + Dn * 7 + H + W)
-    want = "vector" if W <= 8 and _hw_vector_shape(Dn, H, dtype) else "generic"
+    want = ("vector" if W <= 8 and _hw_vector_shape(Dn, H, dtype)
+            else "wide" if _hw_wide_shape(Dn, H, W, dtype) else "generic")
     for bwd in (0, 1):
         assert _path("hw", Bn, Tn, Dn, H, W, dtype, static, bwd) == want
     x = randn(g, Bn, Tn, Dn)
@@ -200,6 +212,16 @@ def _hw_vector_shape(Dn, H, dtype):
     vec = 16 // torch.tensor([], dtype=dtype).element_size()
     hs = Dn // H
     return Dn % vec == 0 and hs & (hs - 1) == 0 and hs <= 64 * vec
+
+
+def _hw_wide_shape(Dn, H, W, dtype):
+    """Shapes the headwise wide kernels take (contiguous, aligned tensors): 9 <= W <= 16, D a multiple
+    of 128 (a wavefront's 2-channel lanes), a power-of-two head size of at most 128, and weight-row
+    segments (a wavefront's heads, and a whole row) of whole 16-byte pieces."""
+    es = torch.tensor([], dtype=dtype).element_size()
+    hs = Dn // H
+    return (9 <= W <= 16 and Dn % 128 == 0 and hs & (hs - 1) == 0 and hs <= 128
+            and (128 // hs) * W * es % 16 == 0 and H * W * es % 16 == 0)
 
 
 def _path(kind, Bn, Tn, Dn, HR, W, dtype, static, bwd):

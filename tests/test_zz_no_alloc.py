@@ -5,7 +5,7 @@ dstatic_w partial sums) in a fixed device array of the library instead of a
 caller's allocation.  Through the C ABI, on consecutive calls whose second
 input is smaller than the first (the array keeps the last call's contents),
 its outputs must equal dc_headwise_bwd's bitwise: with and without static_w,
-on the vector kernels and on the generic ones (head size 3).
+on the vector kernels, the wide ones (W 9-16) and the generic ones (head size 3).
 """
 
 import pytest
@@ -23,6 +23,7 @@ SEQUENCES = [
     [(4, 1024, 2048, 64, 4, True, True), (2, 300, 512, 512, 3, True, False)],   # vector kernels
     [(2, 500, 1024, 1024, 4, True, True), (1, 77, 96, 32, 5, True, True)],     # then head size 3: generic
     [(2, 256, 512, 16, 4, False, True), (1, 64, 256, 8, 2, False, False)],     # no static_w: no scratch
+    [(2, 300, 512, 512, 12, True, True), (1, 70, 256, 8, 9, True, False)],     # W 9-16: wide kernels
 ]
 
 
