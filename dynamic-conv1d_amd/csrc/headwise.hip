@@ -187,7 +187,7 @@ HwPlan make_plan(const HwProblem& p, bool bwd) {
 // ------------------------------------------------------------ wide path
 // 9 <= W <= 16 (headwise_wide.h): power-of-two head sizes up to 128, D a
 // multiple of 128, 16-byte weight-row segments per wavefront.
-int wide_block(int W) { return W % 2 == 0 ? W : 2 * W; }
+int wide_block(const HwProblem& p) { return wide_rows((int)p.W, p.D == p.H); }
 
 // Wavefronts per launch: two per SIMD (the kernels take up to 2 x 128 VGPRs
 // per lane), runs of at least one row block.
@@ -196,13 +196,12 @@ constexpr int kWideTargetWaves = 2048;
 HwWideArgs make_wide_args(const HwProblem& p) {
   const int64_t es = dtype_size(p.dtype);
   const int64_t hs = p.D / p.H;
-  const int L = wide_block((int)p.W);
+  const int L = wide_block(p);
   HwWideArgs a;
   a.Tn = (int)p.T;
   a.D = (int)p.D;
   a.H = (int)p.H;
   a.hs_shift = ilog2(hs);
-  a.lph = hs >= 2 ? (int)(hs / 2) : 1;
   a.nwc = (int)(p.D / kWideCols);
   int64_t seg = (p.B * p.T * a.nwc + kWideTargetWaves - 1) / kWideTargetWaves;
   seg = (seg + L - 1) / L * L;
@@ -229,7 +228,7 @@ bool hw_wide_ok(const HwProblem& p, bool bwd) {
   // the wavefront's weight segment and a weight row: whole 16-byte pieces
   if (((kWideCols / hs) * p.W * es) % 16 != 0 || (p.H * p.W * es) % 16 != 0) return false;
   // a run of one row block plus the look-ahead rows fits the resource range
-  if ((wide_block((int)p.W) + kHwSlackRows) * max_row_bytes(p) > kHwRunBytes) return false;
+  if ((wide_block(p) + kHwSlackRows) * max_row_bytes(p) > kHwRunBytes) return false;
   const int ea = (int)(kWideCpl * es);  // a lane's channels
   if (!aligned(p.x, ea) || !aligned(p.static_w, ea) || !aligned(p.weight, 16)) return false;
   if (!bwd) return aligned(p.y, ea);

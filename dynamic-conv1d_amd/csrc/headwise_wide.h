@@ -10,11 +10,12 @@
 // channels (D % 128 == 0), and walks a run of rows of one sequence one row at
 // a time, keeping the last W rows of x (and in the backward the W open dx
 // accumulators) in fp32 register rings whose slot for row t is (t - t0) mod W.
-// The rings have M = W (W even) or W + 1 slots and rows are processed in
-// unrolled blocks of M rows (an even count, as the two raw buffers alternate),
-// so every ring index is a compile-time constant.  The rows of the next two steps are
-// in flight while a row is computed (two raw buffers, the loads of row t+2
-// issued once row t's raw values are consumed).
+// The rows of the next NB steps are in flight while a row is computed (NB raw
+// buffers, the loads of row t+NB issued once row t's raw values are consumed):
+// NB = 2 at head size 1, whose weight rows are 2W bytes per lane, and 4 at
+// larger head sizes, whose rows are mostly x (and dy).  The rings have M slots,
+// W rounded up to a multiple of NB, and rows are processed in unrolled blocks
+// of M rows, so every ring and buffer index is a compile-time constant.
 //
 // Weight rows.  A wavefront's channels cover 128/hs heads (hs <= 128), whose
 // weights are one contiguous segment of (128/hs) * W elements of the row
@@ -23,16 +24,17 @@
 // through its own LDS slot, and each lane reads its head's W weights (head
 // size 1: the two heads of its channels).  The backward's dweight row goes the
 // same way in reverse: the lanes' two-channel sums are added over the head's
-// lanes through LDS in lane order, written to the slot, and stored as
-// contiguous 16-byte pieces.
+// lanes (DPP butterflies, ds_bpermute steps beyond 16 lanes), written to the
+// slot, and stored as contiguous 16-byte pieces.
 //
 // Backward.  dx in scatter form: row s adds dy[s] * (w[s,k] + sw[k] (+1 at
 // k = 0: the residual)) to the open accumulator of row s-k; row s-W+1 is then
 // complete and stored.  A run reads dy and w for W-1 rows past its end (their
 // dx terms), which add nothing to dweight (stores dropped) or dstatic_w (dy
-// masked).  dstatic_w partial sums stay in registers over the run, are added
-// across the workgroup's 4 wavefronts in LDS in a fixed order and written as
-// one fp32 partial per workgroup, summed by reduce_partials (deterministic).
+// masked).  dstatic_w partial sums stay in registers (in LDS above W 12) over
+// the run, are added across the workgroup's 4 wavefronts in LDS in a fixed
+// order and written as one fp32 partial per workgroup, summed by
+// reduce_partials (deterministic).
 #pragma once
 
 #include "headwise_fast.h"
@@ -43,12 +45,16 @@ constexpr int kWideCpl = 2;                 // channels per lane
 constexpr int kWideCols = 64 * kWideCpl;    // channels per wavefront
 constexpr int kHwWideMinW = 9, kHwWideMaxW = 16;
 
+// Row buffers in flight per wavefront, and ring slots (= rows per unrolled
+// block) at width W; h1: head size 1.
+constexpr int wide_nb(bool h1) { return h1 ? 2 : 4; }
+constexpr int wide_rows(int W, bool h1) { return (W + wide_nb(h1) - 1) / wide_nb(h1) * wide_nb(h1); }
+
 struct HwWideArgs {
   int Tn;        // sequence length
   int D;         // channels (a multiple of kWideCols)
   int H;         // heads
   int hs_shift;  // log2(head size), 0 .. 7
-  int lph;       // lanes per head: head size / 2, or 1 at head size 1
   int nwc;       // D / kWideCols wavefront columns
   int seg;       // rows per run (a multiple of the kernel's row block)
   int nspb;      // runs per sequence
@@ -120,7 +126,7 @@ __global__ __launch_bounds__(256) void hw_fwd_wide(const T* __restrict__ x, cons
                                                    const T* __restrict__ sw, T* __restrict__ y, HwWideArgs a) {
   constexpr int ES = (int)sizeof(T);
   constexpr int NH = H1 ? 2 : 1;  // heads per lane
-  constexpr int M = (W % 2 == 0) ? W : W + 1;  // ring slots = rows per block
+  constexpr int NB = wide_nb(H1), M = wide_rows(W, H1);
   constexpr int NP = WideSeg<T, W, H1>::NP;
   constexpr bool EVEN = H1 || W % 2 == 0;
   typedef Raw<T, kWideCpl> XR;
@@ -170,8 +176,8 @@ __global__ __launch_bounds__(256) void hw_fwd_wide(const T* __restrict__ x, cons
     h.to_float(xf[M - i]);
   }
 
-  XR xr[2];
-  u32x4 wr[2][NP];
+  XR xr[NB];
+  u32x4 wr[NB][NP];
   auto load_row = [&](int t, int buf) {
     const bool live = t < t1;
     bload_raw<kNt>(xr[buf], row_rsrc(xs, D, t, live, rowb), xlo);
@@ -179,18 +185,18 @@ __global__ __launch_bounds__(256) void hw_fwd_wide(const T* __restrict__ x, cons
 #pragma unroll
     for (int i = 0; i < NP; ++i) wr[buf][i] = bload128<kNt>(rw, wpo[i]);
   };
-  load_row(t0, 0);
-  load_row(t0 + 1, 1);
+#pragma unroll
+  for (int i = 0; i < NB; ++i) load_row(t0 + i, i);
   for (int tb = t0; tb < t1; tb += M) {
 #pragma unroll
     for (int u = 0; u < M; ++u) {
       const int t = tb + u;
-      const int p = u % M, buf = u % 2;
+      const int p = u % M, buf = u % NB;
       xr[buf].to_float(xf[p]);
       __builtin_amdgcn_wave_barrier();  // the previous row's reads of the slot are done
 #pragma unroll
       for (int i = 0; i < NP; ++i) reinterpret_cast<u32x4*>(my)[i * 64 + lane] = wr[buf][i];
-      load_row(t + 2, buf);
+      load_row(t + NB, buf);
       __builtin_amdgcn_wave_barrier();
       float wv[NH * W];
       lds_elems<T, NH * W, EVEN>(my, we0, wv);
@@ -213,20 +219,24 @@ __global__ __launch_bounds__(256) void hw_fwd_wide(const T* __restrict__ x, cons
 }
 
 // ----------------------------------------------------------------- backward
-template <typename T, int W, bool H1, bool STATIC>
+// LPH: lanes per head, 0 at head size 1 (a lane's two channels are two heads).
+template <typename T, int W, int LPH, bool STATIC>
 __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, const T* __restrict__ wt,
                                                    const T* __restrict__ sw, const T* __restrict__ dy,
                                                    T* __restrict__ dx, T* __restrict__ dwt,
                                                    float* __restrict__ part, HwWideArgs a) {
   constexpr int ES = (int)sizeof(T);
+  constexpr bool H1 = LPH == 0;
   constexpr int NH = H1 ? 2 : 1;
-  constexpr int M = (W % 2 == 0) ? W : W + 1;  // ring slots = rows per block
+  // with a static filter above W 12: two row buffers, and the dstatic_w sums
+  // in LDS instead of registers (fewer spills; up to W 12 registers are faster)
+  constexpr bool WIDE_ST = STATIC && W > 12;
+  constexpr int NB = WIDE_ST ? 2 : wide_nb(H1), M = (W + NB - 1) / NB * NB;
   constexpr int NP = WideSeg<T, W, H1>::NP;
   constexpr bool EVEN = H1 || W % 2 == 0;
   typedef Raw<T, kWideCpl> XR;
   __shared__ __attribute__((aligned(16))) uint8_t stg[4][NP * 1024];
-  __shared__ float dsr[STATIC ? 4 : 1][STATIC ? W * kWideCols : 1];
-  __shared__ float red_all[H1 ? 1 : 4][H1 ? 1 : W * 65];
+  __shared__ __attribute__((aligned(8))) float dsr[STATIC ? 4 : 1][STATIC ? W * kWideCols : 1];
   __shared__ __attribute__((aligned(8))) float swl[STATIC ? W * kWideCols : 1];
 
   const int lb = xcd_remap(blockIdx.x, a.nblk);
@@ -257,15 +267,22 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
   const int we0 = hl * W;
   uint8_t* const my = stg[wave];
   const float res = a.residual ? 1.f : 0.f;  // tap 0's weight + 1: the residual's dy term
-  // head sums over lph lanes (head size 4+): nhw = 64 / lph heads per wavefront
-  const int lph = a.lph;
-  const int nhw_shift = 6 - __builtin_ctz(lph), nhw = 1 << nhw_shift;
-  float* const red = red_all[wave];
-  float dsw[W][kWideCpl];
+  // dstatic_w sums of the lane's channels over the run: in registers, or above
+  // W 12 in the wavefront's LDS slot (tap k at dsl[k * 64]; each lane reads and
+  // writes only its own)
+  float dsw[WIDE_ST ? 1 : W][kWideCpl];
+  float2* const dsl = reinterpret_cast<float2*>(dsr[wave]) + lane;
+  if constexpr (STATIC) {
 #pragma unroll
-  for (int k = 0; k < W; ++k)
-#pragma unroll
-    for (int j = 0; j < kWideCpl; ++j) dsw[k][j] = 0.f;
+    for (int k = 0; k < W; ++k) {
+      if constexpr (WIDE_ST) {
+        dsl[k * 64] = make_float2(0.f, 0.f);
+      } else {
+        dsw[k][0] = 0.f;
+        dsw[k][1] = 0.f;
+      }
+    }
+  }
   // the static filter of the workgroup's channels in LDS, read per row (in
   // registers it would hold 2W more per lane)
   if constexpr (STATIC) {
@@ -292,8 +309,8 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
   // Rows s in [t0, tend): x of rows < t1 (dweight, dstatic_w); dy and w of
   // rows < tend (their dx terms reach rows < t1).
   const int tend = has_run ? t1 + W - 1 : t1;
-  XR xr[2], dr[2];
-  u32x4 wr[2][NP];
+  XR xr[NB], dr[NB];
+  u32x4 wr[NB][NP];
   auto load_row = [&](int t, int buf) {
     bload_raw<kNt>(xr[buf], row_rsrc(xs, D, t, t < t1, rowb), xlo);
     const bool ylive = t < tend && t < Tn;
@@ -302,13 +319,13 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
 #pragma unroll
     for (int i = 0; i < NP; ++i) wr[buf][i] = bload128<kNt>(rw, wpo[i]);
   };
-  load_row(t0, 0);
-  load_row(t0 + 1, 1);
+#pragma unroll
+  for (int i = 0; i < NB; ++i) load_row(t0 + i, i);
   for (int tb = t0; tb < tend; tb += M) {
 #pragma unroll
     for (int u = 0; u < M; ++u) {
       const int t = tb + u;
-      const int p = u % M, buf = u % 2;
+      const int p = u % M, buf = u % NB;
       if constexpr (STATIC) asm volatile("" ::: "memory");  // static filter: re-read from LDS each row
       xr[buf].to_float(xf[p]);
       float dyv[kWideCpl], dym[kWideCpl];
@@ -318,7 +335,7 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
       __builtin_amdgcn_wave_barrier();  // the previous row's reads of the slot are done
 #pragma unroll
       for (int i = 0; i < NP; ++i) reinterpret_cast<u32x4*>(my)[i * 64 + lane] = wr[buf][i];
-      load_row(t + 2, buf);
+      load_row(t + NB, buf);
       __builtin_amdgcn_wave_barrier();
       float wv[NH * W];
       lds_elems<T, NH * W, EVEN>(my, we0, wv);
@@ -364,29 +381,24 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
 #pragma unroll
           for (int j = 0; j < kWideCpl; ++j) put(we0 + j * W + k, dym[j] * xf[q][j]);
         }
-      } else if (lph == 1) {  // head size 2: the lane's head is its own
+      } else if constexpr (LPH == 1) {  // head size 2: the lane's head is its own
 #pragma unroll
         for (int k = 0; k < W; ++k) {
           const int q = ((u - k) % M + M) % M;
           put(we0 + k, fmaf(dym[1], xf[q][1], dym[0] * xf[q][0]));
         }
       } else {
-        // head sums over lph lanes: the lanes' two-channel sums go to red
-        // (tap-major, rows of 65 floats: conflict-free writes and reads), then
-        // lane l adds up entries e = l, l+64, .. (head e % nhw, tap e / nhw)
-        // in lane order and puts them in the segment
+        // head sums over LPH lanes of the lanes' two-channel sums (DPP butterflies, ds_bpermute
+        // steps beyond 16 lanes); the head's first lane puts them in the segment
+        float v[W];
 #pragma unroll
         for (int k = 0; k < W; ++k) {
           const int q = ((u - k) % M + M) % M;
-          red[k * 65 + lane] = fmaf(dym[1], xf[q][1], dym[0] * xf[q][0]);
+          v[k] = group_sum<LPH>(fmaf(dym[1], xf[q][1], dym[0] * xf[q][0]));
         }
-        __builtin_amdgcn_wave_barrier();
-        for (int e = lane; e < nhw * W; e += 64) {
-          const int h = e & (nhw - 1), k = e >> nhw_shift;
-          const float* r = red + k * 65 + h * lph;
-          float acc = r[0];
-          for (int i = 1; i < lph; ++i) acc += r[i];
-          put(h * W + k, acc);
+        if ((lane & (LPH - 1)) == 0) {
+#pragma unroll
+          for (int k = 0; k < W; ++k) put(we0 + k, v[k]);
         }
       }
       __builtin_amdgcn_wave_barrier();
@@ -398,8 +410,15 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
 #pragma unroll
         for (int k = 0; k < W; ++k) {
           const int q = ((u - k) % M + M) % M;
-#pragma unroll
-          for (int j = 0; j < kWideCpl; ++j) dsw[k][j] = fmaf(dym[j], xf[q][j], dsw[k][j]);
+          if constexpr (WIDE_ST) {
+            float2 v = dsl[k * 64];
+            v.x = fmaf(dym[0], xf[q][0], v.x);
+            v.y = fmaf(dym[1], xf[q][1], v.y);
+            dsl[k * 64] = v;
+          } else {
+            dsw[k][0] = fmaf(dym[0], xf[q][0], dsw[k][0]);
+            dsw[k][1] = fmaf(dym[1], xf[q][1], dsw[k][1]);
+          }
         }
       }
       __builtin_amdgcn_sched_barrier(0);  // rows one after another: the rings are the live state
@@ -409,10 +428,10 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
   if constexpr (STATIC) {
     // dstatic_w: the workgroup's 4 runs added in wave order, one fp32 partial
     // per workgroup row: part[sgp][k * D + channel]
+    if constexpr (!WIDE_ST) {
 #pragma unroll
-    for (int k = 0; k < W; ++k)
-#pragma unroll
-      for (int j = 0; j < kWideCpl; ++j) dsr[wave][k * kWideCols + kWideCpl * lane + j] = dsw[k][j];
+      for (int k = 0; k < W; ++k) dsl[k * 64] = make_float2(dsw[k][0], dsw[k][1]);
+    }
     __syncthreads();
     for (int e = threadIdx.x; e < W * kWideCols; e += 256) {
       const float v = ((dsr[0][e] + dsr[1][e]) + dsr[2][e]) + dsr[3][e];
@@ -423,23 +442,44 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
 }
 
 // ------------------------------------------------------------------ launch
-template <typename T, bool BWD, int W, bool H1, bool ST>
-hipError_t launch_hw_wide(const HwProblem& p, const HwWideArgs& a) {
-  if constexpr (BWD)
-    hw_bwd_wide<T, W, H1, ST><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.weight, (const T*)p.static_w,
-                                                            (const T*)p.dy, (T*)p.dx, (T*)p.dweight, p.ws, a);
-  else
-    hw_fwd_wide<T, W, H1, ST><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.weight, (const T*)p.static_w,
-                                                            (T*)p.y, a);
+template <typename T, int W, bool H1, bool ST>
+hipError_t launch_hw_fwd_wide(const HwProblem& p, const HwWideArgs& a) {
+  hw_fwd_wide<T, W, H1, ST><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.weight, (const T*)p.static_w,
+                                                          (T*)p.y, a);
   return hipGetLastError();
+}
+
+template <typename T, int W, int LPH, bool ST>
+hipError_t launch_hw_bwd_wide(const HwProblem& p, const HwWideArgs& a) {
+  hw_bwd_wide<T, W, LPH, ST><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.weight, (const T*)p.static_w,
+                                                           (const T*)p.dy, (T*)p.dx, (T*)p.dweight, p.ws, a);
+  return hipGetLastError();
+}
+
+template <typename T, int W, int LPH>
+hipError_t launch_hw_bwd_wide_s(const HwProblem& p, const HwWideArgs& a) {
+  return p.static_w ? launch_hw_bwd_wide<T, W, LPH, true>(p, a) : launch_hw_bwd_wide<T, W, LPH, false>(p, a);
 }
 
 template <typename T, bool BWD, int W>
 hipError_t launch_hw_wide_w(const HwProblem& p, const HwWideArgs& a) {
   const bool st = p.static_w != nullptr;
-  if (a.hs_shift == 0)
-    return st ? launch_hw_wide<T, BWD, W, true, true>(p, a) : launch_hw_wide<T, BWD, W, true, false>(p, a);
-  return st ? launch_hw_wide<T, BWD, W, false, true>(p, a) : launch_hw_wide<T, BWD, W, false, false>(p, a);
+  if constexpr (!BWD) {
+    if (a.hs_shift == 0)
+      return st ? launch_hw_fwd_wide<T, W, true, true>(p, a) : launch_hw_fwd_wide<T, W, true, false>(p, a);
+    return st ? launch_hw_fwd_wide<T, W, false, true>(p, a) : launch_hw_fwd_wide<T, W, false, false>(p, a);
+  } else {
+    switch (a.hs_shift) {  // lanes per head: head size / 2 (a lane holds two channels)
+      case 0: return launch_hw_bwd_wide_s<T, W, 0>(p, a);
+      case 1: return launch_hw_bwd_wide_s<T, W, 1>(p, a);
+      case 2: return launch_hw_bwd_wide_s<T, W, 2>(p, a);
+      case 3: return launch_hw_bwd_wide_s<T, W, 4>(p, a);
+      case 4: return launch_hw_bwd_wide_s<T, W, 8>(p, a);
+      case 5: return launch_hw_bwd_wide_s<T, W, 16>(p, a);
+      case 6: return launch_hw_bwd_wide_s<T, W, 32>(p, a);
+      default: return launch_hw_bwd_wide_s<T, W, 64>(p, a);
+    }
+  }
 }
 
 // The wide kernels for p (host checks: hw_wide_ok); the backward's dstatic_w
