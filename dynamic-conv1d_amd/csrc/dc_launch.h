@@ -63,7 +63,15 @@ struct LrProblem {
   int dtype;
   int residual;
   hipStream_t stream;
+  // A forward pass over taps kofs .. kofs+W-1 of a wider problem (the
+  // matrix-core forward above W 16): U's row stride in elements (0: W*D; U and
+  // static_w then point at tap kofs), and accy: add to the y an earlier pass
+  // stored.
+  int64_t u_ld;
+  int kofs;
+  int accy;
   int64_t xld() const { return x_ld > 0 ? x_ld : D; }
+  int64_t uld() const { return u_ld > 0 ? u_ld : W * D; }
   int64_t dxld() const { return dx_ld > 0 ? dx_ld : D; }
   int64_t yhd() const { return y_hd > 0 ? y_hd : D; }
 };

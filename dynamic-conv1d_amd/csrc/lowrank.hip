@@ -398,10 +398,11 @@ hipError_t bwd_generic(const LrProblem& p) {
 // Shapes, dtypes and alignments the MFMA kernels (lowrank_mfma_{fwd,bwd}.hip) take.
 bool lr_mfma_ok(const LrProblem& p, bool bwd) {
   if (p.dtype != kBF16 && p.dtype != kFP16) return false;
-  if (p.W < 1 || p.W > 16) return false;
-  // every W <= 8 at every kernel rank <= 64, and W <= 16 at kernel ranks <= 32:
-  // the forward stages W x RC operand chunks (up to 128 KiB of LDS); the
-  // backward runs wide W x RC as passes of taps
+  if (p.W < 1 || p.W > 32) return false;
+  // every W <= 8 at every kernel rank <= 64, and W <= 32 at kernel ranks <= 32:
+  // the forward stages W x RC operand chunks (up to 128 KiB of LDS) and runs
+  // above W 16 as two passes of taps; the backward runs wide W x RC as passes
+  // of taps (the runs' 32-row halo covers a pass's look-back)
   const int64_t rc = (p.R + (p.static_w ? 1 : 0) + 15) / 16;
   if (rc > 4 || (p.W > 8 && rc > 2)) return false;
   // buffer-offset range of a run (resources start at each run's base row, so

@@ -24,7 +24,7 @@
 // layout, [B, D/hd, T, hd]); stores then check the row against T.
 //
 // Both kernels give each run of tiles buffer resources that start at the run's
-// base row (run_base_row: its first tile less a 16-row halo) and the host caps
+// base row (run_base_row: its first tile less a 32-row halo) and the host caps
 // a run's length (lr_f32m_{fwd,bwd}_max_run_tiles), so offsets stay in int32
 // and sequences of any length take these kernels, as in the 16-bit ones.
 #include "lowrank_mfma.h"

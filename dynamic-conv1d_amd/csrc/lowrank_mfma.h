@@ -92,9 +92,9 @@ __device__ __forceinline__ float q4f(const u32x2& v, int j) {
 }
 
 // Buffer resources (dc_common.h) of the matrix-core lowrank kernels cover one
-// run of tiles: they start at the run's base row rb = max(16 * tile0 - 16, 0)
-// (the first tile's rows less a 16-row halo: the look-back of W - 1 <= 15 rows,
-// passes of taps included) and end at T, capped
+// run of tiles: they start at the run's base row rb = max(16 * tile0 - 32, 0)
+// (the first tile's rows less a 32-row halo: the look-back of kofs + W - 1 <= 31
+// rows of a pass of taps kofs .. kofs+W-1, W <= 32) and end at T, capped
 // at kMaxSeqBytes - kSeqSlackRows rows (run_rsrc).  Rows before 0 (negative
 // offsets wrap to large unsigned values), rows past T and channels past D
 // (lane offset kOobLane) read 0 and drop stores, without branches or clamped
@@ -111,7 +111,7 @@ constexpr int kSeqSlackRows = 32;
 constexpr int kOobTile = (int)kMaxSeqBytes;
 
 // First row covered by the buffer resources of a run whose first tile is tile0.
-constexpr int kRunHaloRows = 16;
+constexpr int kRunHaloRows = 32;
 __device__ __forceinline__ int run_base_row(int tile0) { return max(tile0 * 16 - kRunHaloRows, 0); }
 
 // Resource over rows [rb, rb + nrows) of `rowb` bytes each, starting at p (row

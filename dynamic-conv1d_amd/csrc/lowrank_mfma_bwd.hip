@@ -224,6 +224,40 @@ __device__ __forceinline__ void stage_uw32(u32x4 (&uw)[W * NJ], const uint16_t* 
     }
 }
 
+// A lane's NJ channels of one dx row as the passes of taps keep them: the
+// output type (DxVec<T, NJ, false>), or above W 16 an fp32 accumulator in the
+// workspace (DxVec<T, NJ, true>), rounded to dx once after the last pass (more
+// passes than 4 rounded in 16 bits each drift past the north-star bar).
+template <typename T, int NJ, bool F32> struct DxVec {
+  typedef LaneVec<NJ> LV;
+  typedef typename LV::type type;
+  static constexpr int ES = 2;
+  __device__ static __forceinline__ type load(rsrc_t r, int off) { return LV::load(r, off); }
+  __device__ static __forceinline__ void store(type v, rsrc_t r, int off) { LV::store(v, r, off); }
+  __device__ static __forceinline__ float get(const type& v, int j) { return Mma16<T>::to_f(LV::elem(v, j)); }
+  __device__ static __forceinline__ type make(const float* f) { return LV::template pack<T>(f); }
+};
+template <typename T> struct DxVec<T, 2, true> {
+  typedef u32x2 type;
+  static constexpr int ES = 4;
+  __device__ static __forceinline__ type load(rsrc_t r, int off) { return bload64(r, off); }
+  __device__ static __forceinline__ void store(type v, rsrc_t r, int off) { bstore64<true>(v, r, off); }
+  __device__ static __forceinline__ float get(const type& v, int j) { return __uint_as_float(v[j]); }
+  __device__ static __forceinline__ type make(const float* f) {
+    return type{__float_as_uint(f[0]), __float_as_uint(f[1])};
+  }
+};
+template <typename T> struct DxVec<T, 4, true> {
+  typedef u32x4 type;
+  static constexpr int ES = 4;
+  __device__ static __forceinline__ type load(rsrc_t r, int off) { return bload128(r, off); }
+  __device__ static __forceinline__ void store(type v, rsrc_t r, int off) { bstore128<true>(v, r, off); }
+  __device__ static __forceinline__ float get(const type& v, int j) { return __uint_as_float(v[j]); }
+  __device__ static __forceinline__ type make(const float* f) {
+    return type{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])};
+  }
+};
+
 // A operands of the tap-weight MFMA for one row block: four ranks per rank
 // chunk (16x16x16, K = 16) or, with two rank chunks, eight ranks (16x16x32).
 template <int RC, bool K32> struct ZOp { u32x2 c[RC]; };
@@ -231,8 +265,9 @@ template <int RC> struct ZOp<RC, true> { u32x4 v; };
 
 // ACC: a later pass of taps (the host splits wide W), which adds its dx to
 // what the earlier passes stored; a separate instantiation, so single-pass
-// launches carry none of it.
-template <typename T, int W, int RC, int NRW, int CPW, bool ACC>
+// launches carry none of it.  F32: dx rows are the fp32 accumulator (the
+// group's dx pointer and dxld then address it), above W 16.
+template <typename T, int W, int RC, int NRW, int CPW, bool ACC, bool F32 = false>
 __global__ __launch_bounds__(64 * (256 / CPW) * NRW)
 __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))) void lr_bwd_mfma(LrBwdArgs a) {
   constexpr int NJ = CPW / 16;     // channels per lane
@@ -242,6 +277,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   static_assert(CPW == 64 || CPW == 32, "64- or 32-channel tiles");
   static_assert(NRW == 1 || (RC == 1 && W <= 4 && CPW == 64), "two runs per workgroup: one rank chunk, W <= 4");
   typedef LaneVec<NJ> LV;
+  typedef DxVec<T, NJ, F32> DV;
   // dx in scatter form for 2 <= W <= 4 (SC): tap weights of the lane's own rows
   // only, partial sums for the rows of the group above passed across lanes.
   // Otherwise (gather form) NB row blocks of tap weights cover the look-ahead.
@@ -286,7 +322,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   const uint16_t* __restrict__ U = reinterpret_cast<const uint16_t*>(pick(a.grp, g, &LrBwdGroup::U));
   const uint16_t* __restrict__ sw = reinterpret_cast<const uint16_t*>(pick(a.grp, g, &LrBwdGroup::sw));
   const uint16_t* __restrict__ dy = reinterpret_cast<const uint16_t*>(pick(a.grp, g, &LrBwdGroup::dy));
-  uint16_t* __restrict__ dx = reinterpret_cast<uint16_t*>(pick(a.grp, g, &LrBwdGroup::dx));
+  char* __restrict__ dx = reinterpret_cast<char*>(pick(a.grp, g, &LrBwdGroup::dx));
   float* __restrict__ part_dz = pick(a.grp, g, &LrBwdGroup::part_dz);
   float* __restrict__ part_du = pick(a.grp, g, &LrBwdGroup::part_du);
   const int cg = lb % a.ncg, sp = lb / a.ncg;
@@ -349,17 +385,17 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   // head and its dy resource covers that head's [T, yhd] block (rows past T
   // stay out of range either way).
   const int yhd = a.yhd, head = d0 / yhd;
-  const int rowb = yhd * 2, xrowb = a.xld * 2, dxrowb = a.dxld * 2;
+  const int rowb = yhd * 2, xrowb = a.xld * 2, dxrowb = a.dxld * DV::ES;
   // resources of the run's rows from rb (offsets below are relative to row rb)
   const rsrc_t rx = run_rsrc(x + rrow * a.xld, Tn - rb, xrowb);
   const rsrc_t rdy = run_rsrc(dy + row0 * D + ((int64_t)head * Tn + rb) * yhd, Tn - rb, rowb);
-  const rsrc_t rdx = run_rsrc(dx + rrow * a.dxld, Tn - rb, dxrowb);
+  const rsrc_t rdx = run_rsrc(dx + rrow * a.dxld * DV::ES, Tn - rb, dxrowb);
   const int zld = a.zld, zr = a.zr, zrk = a.zrk;
   const rsrc_t rz = run_rsrc(z + rrow * zld, Tn - rb, zld * 2);
   // byte offsets of the lane's row-4q channels in dy, x and dx
   const int lane_off = chv ? (4 * q * yhd + col - head * yhd) * 2 : kOobLane;
   const int xlane_off = chv ? (4 * q * a.xld + col) * 2 : kOobLane;
-  const int dxlane_off = chv ? (4 * q * a.dxld + col) * 2 : kOobLane;
+  const int dxlane_off = chv ? (4 * q * a.dxld + col) * DV::ES : kOobLane;
 
   u32x2 uw_reg[UWREG && !K32 ? NUW : 1];  // staged below, after the first tile's loads are issued
   u32x4 uw32[K32 ? W * NJ : 1];
@@ -408,7 +444,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     u32x4 z32[K32 ? NB : 1];  // K32: z_eff rows t0+4bb+n, ranks 8q..8q+7
     // ACC: the earlier passes' dx of the tile's rows 4q..4q+3 (shifted by kofs),
     // loaded with the tile's inputs so that the adds before the stores do not wait
-    typename LV::type dxo[ACC ? 4 : 1];
+    typename DV::type dxo[ACC ? 4 : 1];
   };
   auto load_tile = [&](int tile, TileIn& in) {
     const bool live = tile < tile1;
@@ -435,7 +471,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     if constexpr (ACC) {
       const int dxo_off = live ? dxlane_off + (tile * 16 - rb - kofs) * dxrowb : kOobTile;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) in.dxo[i] = LV::load(rdx, dxo_off + i * dxrowb);
+      for (int i = 0; i < 4; ++i) in.dxo[i] = DV::load(rdx, dxo_off + i * dxrowb);
     }
   };
 
@@ -454,9 +490,9 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
     for (int j = 0; j < NJ; ++j) carry[i][j] = 0.f;
   // ACC: group 3's open rows are stored one tile late; their earlier-pass dx
   // (loaded with the tile before) waits here
-  typename LV::type dxo_carry[ACC ? NOPEN : 1] = {};  // the first tile's open rows store nothing
+  typename DV::type dxo_carry[ACC ? NOPEN : 1] = {};  // the first tile's open rows store nothing
   auto close_rows = [&](const float(&own)[4][NJ], const float(&S)[NSC][NJ], int tile,
-                        const typename LV::type(&dxo)[ACC ? 4 : 1]) {
+                        const typename DV::type(&dxo)[ACC ? 4 : 1]) {
     const int src = ((lane + 16) & 63) << 2;  // ds_bpermute byte index of the group below
     float recv[NSC][NJ];
 #pragma unroll
@@ -482,12 +518,12 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
       }
       const int off = (top && open ? prev_off : cur_off) + i * dxrowb;
       if constexpr (ACC) {  // a later pass of taps adds to the stored rows
-        typename LV::type o = dxo[ACC ? i : 0];
+        typename DV::type o = dxo[ACC ? i : 0];
         if (open) o = top ? dxo_carry[ACC ? i - kFirstOpen : 0] : o;
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) v[j] += Mma16<T>::to_f(LV::elem(o, j));
+        for (int j = 0; j < NJ; ++j) v[j] += DV::get(o, j);
       }
-      LV::store(LV::template pack<T>(v), rdx, off);
+      DV::store(DV::make(v), rdx, off);
     }
 #pragma unroll
     for (int i = 0; i < NOPEN; ++i)
@@ -629,9 +665,9 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
         const int off = dxlane_off + dxtoff + i * dxrowb;
         if constexpr (ACC) {  // a later pass of taps adds to the stored rows (loaded with the tile)
 #pragma unroll
-          for (int j = 0; j < NJ; ++j) dxa[i][j] += Mma16<T>::to_f(LV::elem(in.dxo[ACC ? i : 0], j));
+          for (int j = 0; j < NJ; ++j) dxa[i][j] += DV::get(in.dxo[ACC ? i : 0], j);
         }
-        LV::store(LV::template pack<T>(dxa[i]), rdx, off);
+        DV::store(DV::make(dxa[i]), rdx, off);
       }
     }
     // ---- dz: gather this wavefront's tile sums; every DZB iterations (and at the
@@ -814,6 +850,10 @@ constexpr int pass_taps(int W, int RC) {
 }
 constexpr int npasses(int W, int RC) { return (W + pass_taps(W, RC) - 1) / pass_taps(W, RC); }
 
+// Above this width (more than four passes of taps) the passes add dx into an
+// fp32 accumulator in the workspace, rounded to dx once by lr_dx_round.
+constexpr int kBwdF32DxMinW = 16;
+
 }  // namespace
 
 // Longest backward run (tiles) whose resources fit (see run_rsrc): rows of x,
@@ -821,7 +861,9 @@ constexpr int npasses(int W, int RC) { return (W + pass_taps(W, RC) - 1) / pass_
 // itself or the padded copy) and the fp32 dz partials.
 int64_t lr_bwd_max_run_tiles(const LrProblem& p) {
   int64_t rowb = p.xld() * 2;
-  const int64_t others[4] = {p.dxld() * 2, p.yhd() * 2, lr_bwd_zrow(p.R, p.static_w != nullptr) * 2, p.R * 4};
+  // above W 16 the passes' dx rows are the fp32 accumulator (D floats each)
+  const int64_t dxb = p.W > kBwdF32DxMinW ? p.D * 4 : p.dxld() * 2;
+  const int64_t others[4] = {dxb, p.yhd() * 2, lr_bwd_zrow(p.R, p.static_w != nullptr) * 2, p.R * 4};
   for (int64_t v : others) rowb = rowb > v ? rowb : v;
   return run_tiles_cap(rowb);
 }
@@ -914,11 +956,55 @@ hipError_t launch_zpad(const LrProblem* p, int G, void* const* dst) {
 
 constexpr int kBwdTargetWaves = 2048;
 
+// dx from the passes' fp32 accumulator (rows of D floats): each group's rows
+// rounded once to the output type, into dx rows dxld elements apart.
+struct DxRoundGroup {
+  const float* src;
+  uint16_t* dst;
+};
+struct DxRoundArgs {
+  int64_t n4;   // BT * D / 4 quads per group
+  int dq;       // D / 4 quads per row
+  int64_t dld;  // row stride of dx (elements, a multiple of 4)
+  DxRoundGroup grp[kMaxGroups];
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void lr_dx_round(DxRoundArgs a) {
+  const int g = blockIdx.y;
+  const float* __restrict__ src = pick(a.grp, g, &DxRoundGroup::src);
+  uint16_t* __restrict__ dst = pick(a.grp, g, &DxRoundGroup::dst);
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < a.n4; e += (int64_t)gridDim.x * 256) {
+    const int64_t row = e / a.dq, c = (e - row * a.dq) * 4;
+    const float4 v = *reinterpret_cast<const float4*>(src + e * 4);
+    u32x2 o;
+    o[0] = pack2<T>(v.x, v.y);
+    o[1] = pack2<T>(v.z, v.w);
+    *reinterpret_cast<u32x2*>(dst + row * a.dld + c) = o;
+  }
+}
+
+template <typename T>
+hipError_t launch_dx_round(const LrProblem* p, int G, int64_t dxf_off) {
+  DxRoundArgs a;
+  a.n4 = p[0].B * p[0].T * p[0].D / 4;
+  a.dq = (int)(p[0].D / 4);
+  a.dld = p[0].dxld();
+  for (int g = 0; g < kMaxGroups; ++g) {
+    const LrProblem& q = p[g < G ? g : 0];
+    a.grp[g] = DxRoundGroup{(const float*)((const char*)q.ws + dxf_off), (uint16_t*)q.dx};
+  }
+  const int64_t blocks = (a.n4 + 255) / 256;
+  lr_dx_round<T><<<dim3((unsigned)(blocks < 8192 ? blocks : 8192), G), 256, 0, p[0].stream>>>(a);
+  return hipGetLastError();
+}
+
 // Workspace: [dz partials: passes x ncg x BT x R fp32][dU partials: npair x RK
-// x W*D fp32][padded z_eff: BT x RP of z's type], each 256-byte aligned.  The
-// z_eff part is reserved whatever the pointers' alignment (the size query has none).
+// x W*D fp32][padded z_eff: BT x RP of z's type][above W 16: the fp32 dx
+// accumulator, BT x D], each 256-byte aligned.  The z_eff part is reserved
+// whatever the pointers' alignment (the size query has none).
 struct BwdWs {
-  int64_t dz_off, du_off, zp_off, total;
+  int64_t dz_off, du_off, zp_off, dxf_off, total;
 };
 BwdWs bwd_ws(const LrProblem& p, const LrBwdArgs& a) {
   BwdWs w;
@@ -927,14 +1013,22 @@ BwdWs bwd_ws(const LrProblem& p, const LrBwdArgs& a) {
   w.dz_off = 0;
   w.du_off = (dz + 255) / 256 * 256;
   w.zp_off = (w.du_off + (int64_t)a.npair * a.RK * p.W * p.D * 4 + 255) / 256 * 256;
-  w.total = w.zp_off + a.BT * zpad_ranks(p) * 2;
+  w.dxf_off = (w.zp_off + a.BT * zpad_ranks(p) * 2 + 255) / 256 * 256;
+  w.total = w.dxf_off + (p.W > kBwdF32DxMinW ? a.BT * p.D * 4 : 0);
   return w;
 }
 
-template <typename T, int W, int RC, bool WIDE = false>
+template <typename T, int W, int RC, bool WIDE = false, bool F32 = false>
 hipError_t launch_bwd_kernel(const LrBwdArgs& a, hipStream_t stream) {
   constexpr BwdShape SH = bwd_shape(W, RC, WIDE);  // as make_bwd_args
   constexpr int NRW = SH.nrw, CPW = SH.cpw, NT = 64 * (256 / CPW) * NRW;
+  if constexpr (F32) {  // above W 16: every pass on the fp32 dx accumulator
+    if (a.accdx)
+      lr_bwd_mfma<T, W, RC, NRW, CPW, true, true><<<a.nblk, NT, 0, stream>>>(a);
+    else
+      lr_bwd_mfma<T, W, RC, NRW, CPW, false, true><<<a.nblk, NT, 0, stream>>>(a);
+    return hipGetLastError();
+  }
   // later passes of taps: problems of 2+ rank chunks, and one rank chunk at W > 8
   // (WIDE: passes of at most 4 taps)
   if constexpr (RC >= 2 || WIDE) {
@@ -951,7 +1045,20 @@ hipError_t launch_bwd_kernel(const LrBwdArgs& a, hipStream_t stream) {
 // pass_taps(W, RC) and the last pass's remainder); wide: a one-rank-chunk
 // problem above W 8.
 template <typename T>
-hipError_t dispatch_bwd_kernel(const LrBwdArgs& a, int wq, int rc, bool wide, hipStream_t stream) {
+hipError_t dispatch_bwd_kernel(const LrBwdArgs& a, int wq, int rc, bool wide, bool f32, hipStream_t stream) {
+  if (f32) {  // above W 16 (one or two rank chunks, passes of at most 4 taps)
+    switch (wq * 4 + rc) {
+      case 5: return launch_bwd_kernel<T, 1, 1, true, true>(a, stream);
+      case 9: return launch_bwd_kernel<T, 2, 1, true, true>(a, stream);
+      case 13: return launch_bwd_kernel<T, 3, 1, true, true>(a, stream);
+      case 17: return launch_bwd_kernel<T, 4, 1, true, true>(a, stream);
+      case 6: return launch_bwd_kernel<T, 1, 2, false, true>(a, stream);
+      case 10: return launch_bwd_kernel<T, 2, 2, false, true>(a, stream);
+      case 14: return launch_bwd_kernel<T, 3, 2, false, true>(a, stream);
+      case 18: return launch_bwd_kernel<T, 4, 2, false, true>(a, stream);
+      default: return hipErrorInvalidValue;
+    }
+  }
   if (wide && rc == 1) {
     switch (wq) {
       case 1: return launch_bwd_kernel<T, 1, 1, true>(a, stream);
@@ -1007,6 +1114,12 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
   }
   const int64_t D = p[0].D, WD = p[0].W * D, RKWD = (int64_t)a.RK * WD, R = p[0].R;
   const int64_t dz_slot = (int64_t)a.ncg * a.BT * R;  // one pass's dz partials
+  // above W 16 every pass works on the fp32 accumulator (rows of D floats)
+  const bool f32 = W > kBwdF32DxMinW;
+  if (f32) {
+    a.dxld = (int)D;
+    for (int g = 0; g < G; ++g) a.grp[g].dx = (char*)p[g].ws + w.dxf_off;
+  }
   for (int ps = 0; ps < np; ++ps) {
     // pass ps: taps kofs .. kofs+wq-1 (U, static_w and the dU partials start at
     // the pass's first tap; its dz partials take their own slots)
@@ -1020,8 +1133,9 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
       b.grp[g].part_dz = a.grp[g].part_dz + ps * dz_slot;
       b.grp[g].part_du = a.grp[g].part_du + kofs * D;
     }
-    if ((e = dispatch_bwd_kernel<T>(b, wq, rc, W > 8, p[0].stream)) != hipSuccess) return e;
+    if ((e = dispatch_bwd_kernel<T>(b, wq, rc, W > 8, f32, p[0].stream)) != hipSuccess) return e;
   }
+  if (f32 && (e = launch_dx_round<T>(p, G, w.dxf_off)) != hipSuccess) return e;
   PartialReduce jobs[kMaxReduceJobs];
   int nj = 0;
   for (int g = 0; g < G; ++g) {

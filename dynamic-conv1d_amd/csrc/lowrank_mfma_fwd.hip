@@ -29,8 +29,41 @@ int64_t lr_fwd_max_run_tiles(const LrProblem& p) {
 namespace {
 
 template <typename T>
+hipError_t dispatch_fwd(const LrProblem* pp, int G);
+
+// Above W 16 (up to 32), two passes of taps: taps 0 .. W-17 as a (W-16)-tap
+// problem (residual and z_eff included), then the last 16 taps, x read W-16
+// rows earlier, added to the stored y (accy).  U keeps its row stride W * D;
+// U and static_w of the second pass start at tap W - 16.  y is rounded to the
+// output type after each pass.
+template <typename T>
+hipError_t dispatch_fwd_passes(const LrProblem* pp, int G) {
+  const int W = (int)pp[0].W, kofs = W - 16;
+  LrProblem a[kMaxGroups], b[kMaxGroups];
+  for (int g = 0; g < G; ++g) {
+    const LrProblem& p = pp[g];
+    a[g] = p;
+    a[g].W = kofs;
+    a[g].u_ld = p.uld();
+    b[g] = p;
+    b[g].W = 16;
+    b[g].u_ld = p.uld();
+    b[g].kofs = kofs;
+    b[g].accy = 1;
+    b[g].U = static_cast<const T*>(p.U) + (int64_t)kofs * p.D;
+    b[g].static_w = p.static_w ? static_cast<const T*>(p.static_w) + (int64_t)kofs * p.D : nullptr;
+    b[g].residual = 0;
+    b[g].zeff = nullptr;
+  }
+  hipError_t e = dispatch_fwd<T>(a, G);
+  if (e != hipSuccess) return e;
+  return lr_fwd_wide_dispatch<T>(b, G);
+}
+
+template <typename T>
 hipError_t dispatch_fwd(const LrProblem* pp, int G) {
   const LrProblem& p = pp[0];
+  if (p.W > 16) return dispatch_fwd_passes<T>(pp, G);
   const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
 #define DC_LR_CASE(WW, CC) \
   if (p.W == WW && rc == CC) return launch_fwd<T, WW, CC>(pp, G);

@@ -57,6 +57,8 @@ struct LrArgs {
   int zvec;        // R % 4 == 0 and z 8-byte aligned: 8-byte z loads (host dispatch)
   int yhd;         // y layout: D ([B, T, D]) or the head dim of [B, D/yhd, T, yhd] (yhd % 8 == 0)
   int zrp;         // > 0: the 128-channel chunk 0 wavefronts write z_eff rows of zrp ranks
+  int64_t uld;     // row stride of U (elements): the problem's W * D, all taps
+  int kofs;        // ACC pass: its first tap (x read kofs rows earlier)
   LrFwdGroup grp[kMaxGroups];
 };
 
@@ -64,9 +66,8 @@ struct LrArgs {
 // ub[(k*RC + c)*8 + j][lane] = U_eff[16c + 4q + kk, k*D + dl + j], kk = 0..3.
 template <int W, int RC>
 __device__ __forceinline__ void stage_u(u32x2* __restrict__ lds, const uint16_t* __restrict__ U,
-                                        const uint16_t* __restrict__ sw, int R, int RK, int D, int dl, bool chv,
-                                        int q, int lane, int wave) {
-  const int64_t WD = (int64_t)W * D;
+                                        const uint16_t* __restrict__ sw, int R, int RK, int D, int64_t WD, int dl,
+                                        bool chv, int q, int lane, int wave) {
   for (int kc = wave; kc < W * RC; kc += 4) {
     const int k = kc / RC, c = kc - k * RC;
     u32x4 rows[4];
@@ -97,7 +98,12 @@ __device__ __forceinline__ void stage_u(u32x2* __restrict__ lds, const uint16_t*
 // ILP: the same kernel from the translation unit built with the scheduler's
 // ILP strategy (lowrank_mfma_fwd_ilp.hip); a template argument of its own, so
 // the two builds are distinct kernels.
-template <typename T, int W, int RC, bool ZV, bool ZE, bool ILP = false>
+//
+// ACC: a later pass of taps kofs .. kofs+W-1 of a wider problem (above W 16:
+// the host runs taps 0 .. W-17 first, then the last 16 with ACC): x is read
+// kofs rows earlier and the tile's y rows, as the first pass stored them, are
+// added before the store (each lane loads and stores only its own rows).
+template <typename T, int W, int RC, bool ZV, bool ZE, bool ILP = false, bool ACC = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZE && W <= 4 && RC <= 2 ? 4 : 1, 8)))
 void lr_fwd_mfma(LrArgs a) {
   constexpr int NR = W + 3;  // x rows 4q-W+1 .. 4q+3 of a lane
@@ -118,7 +124,7 @@ void lr_fwd_mfma(LrArgs a) {
   const int D = a.D, Tn = a.Tn, R = a.R, RK = a.RK;
   const int dl = chunk * 128 + 8 * n;  // first channel of the lane's octet
   const bool chv = dl < D;             // D % 8 == 0: octets are whole
-  stage_u<W, RC>(ub, U, sw, R, RK, D, dl, chv, q, lane, wave);
+  stage_u<W, RC>(ub, U, sw, R, RK, D, a.uld, dl, chv, q, lane, wave);
   __syncthreads();
 
   const int sg = sgp * 4 + wave;
@@ -153,6 +159,8 @@ void lr_fwd_mfma(LrArgs a) {
   // above them are the own rows of the lane group above (lane - 16), or for
   // group 0 those of group 3 in the tile before, passed with ds_bpermute.
   constexpr bool HX = W >= 2 && W <= 4;
+  static_assert(!(ACC && (HX || ZE)), "passes of taps: one-pass x rows, z_eff from the first pass");
+  const int kofs = ACC ? a.kofs : 0;
   const int above = ((lane + 48) & 63) << 2;  // ds_bpermute byte address of lane - 16
   u32x4 prev[HX ? W - 1 : 1];                 // rows 16-W+1 .. 15 of the tile before (group 3 sends them)
 
@@ -161,7 +169,7 @@ void lr_fwd_mfma(LrArgs a) {
   // kOobTile, which returns 0 and touches no memory).
   auto load_tile = [&](int tile, u32x4(&xr)[NR], ZR& zr) {
     const bool live = tile < tile1;
-    const int toff = live ? (tile * 16 - rb) * xrowb : kOobTile;
+    const int toff = live ? (tile * 16 - rb - kofs) * xrowb : kOobTile;
 #pragma unroll
     // with the halo from the lane group above (HX) every x row is loaded once: nontemporal
     // (B4 T4096 D2048 R16 forward 30.0 -> 29.2 us; R15 + static 31.8 -> 30.4 us)
@@ -222,6 +230,14 @@ void lr_fwd_mfma(LrArgs a) {
         for (int j = 0; j < 8; ++j) acc[i][j] += Mma16<T>::to_f(elem16(xc[i + W - 1], j));
     }
     const int toff = (tile * 16 - rb) * rowb;
+    if constexpr (ACC) {  // the first pass's y of the lane's rows (rows past T read 0)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 o = bload128(ry, tile * 16 + 4 * q + i < Tn ? lane_off + toff + i * rowb : kOobTile);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] += Mma16<T>::to_f(elem16(o, j));
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       u32x4 o;

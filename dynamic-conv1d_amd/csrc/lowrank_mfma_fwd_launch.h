@@ -1,6 +1,6 @@
 // Launch plans of the lowrank forward (lowrank_mfma_fwd_kernel.h), shared by
 // the host units that instantiate it: lowrank_mfma_fwd.hip (W <= 8) and
-// lowrank_mfma_fwd_wide.hip (9 <= W <= 16).
+// lowrank_mfma_fwd_wide.hip (9 <= W <= 16, and the last 16 taps above W 16).
 #pragma once
 
 #include "lowrank_mfma_fwd_kernel.h"
@@ -46,10 +46,12 @@ inline LrArgs make_args(const LrProblem& p, int target_waves) {
   a.nspb = (int)((ntile + seg - 1) / seg);
   a.nseg = (int)(p.B * a.nspb);
   a.nblk = ((a.nseg + 3) / 4) * a.nch;
+  a.uld = p.uld();
+  a.kofs = p.kofs;
   return a;
 }
 
-template <typename T, int W, int RC>
+template <typename T, int W, int RC, bool ACC = false>
 hipError_t launch_fwd(const LrProblem* p, int G) {
   int waves = fwd_target_waves(p[0]);
   if (RC == 1 && W <= 8 && !p[0].zeff && waves > kFwdIlpWaves) waves = kFwdIlpWaves;
@@ -62,6 +64,13 @@ hipError_t launch_fwd(const LrProblem* p, int G) {
   for (int g = 0; g < G; ++g) {
     a.grp[g] = LrFwdGroup{p[g].x, p[g].z, p[g].U, p[g].static_w, p[g].y, p[g].zeff};
     a.zvec = a.zvec && aligned_to(p[g].z, 8);
+  }
+  if constexpr (ACC) {  // a later pass of taps (no z_eff writer)
+    if (a.zvec)
+      lr_fwd_mfma<T, W, RC, true, false, false, true><<<a.nblk, 256, 0, p[0].stream>>>(a);
+    else
+      lr_fwd_mfma<T, W, RC, false, false, false, true><<<a.nblk, 256, 0, p[0].stream>>>(a);
+    return hipGetLastError();
   }
   if constexpr (RC == 1 && W <= 8) {
     // all wavefronts resident at the ILP build's three per SIMD (see lowrank_mfma_fwd_ilp.hip);
@@ -84,7 +93,8 @@ hipError_t launch_fwd(const LrProblem* p, int G) {
 
 }  // namespace
 
-// The forward at 9 <= W <= 16 with one or two rank chunks (lowrank_mfma_fwd_wide.hip).
+// The forward at 9 <= W <= 16 with one or two rank chunks, and (accy) the
+// second pass of taps above W 16 (lowrank_mfma_fwd_wide.hip).
 template <typename T>
 hipError_t lr_fwd_wide_dispatch(const LrProblem* pp, int G);
 

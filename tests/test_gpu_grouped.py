@@ -58,6 +58,7 @@ CASES = [
     (2, 2, 24, 40, 3, 3, True, 12, torch.float32),      # fp32
     (3, 2, 50, 64, 15, 12, True, 8, torch.bfloat16),    # W 12: backward as three passes of 4 taps
     (2, 1, 70, 128, 31, 10, True, 0, torch.float16),    # W 10, two rank chunks
+    (3, 2, 90, 128, 15, 20, True, 8, torch.bfloat16),   # W 20: two forward passes, five backward passes
 ]
 
 

@@ -298,12 +298,21 @@ LR_EDGE = [
     (2, 77, 200, 31, 16, True, True, torch.bfloat16, ("mfma", "mfma")),        # two rank chunks: 4 x 4 taps
     (1, 3300, 256, 3, 13, False, True, torch.bfloat16, ("mfma", "mfma")),      # long runs, padded z
     (1, 64, 512, 20, 10, True, True, torch.float16, ("mfma", "mfma")),         # kernel rank 21: passes 4 + 4 + 2
-    # widths above 16 (or above 8 at kernel ranks above 32) and kernel ranks above 64: the generic
-    # kernels (the reference accepts any W and power-of-two ranks, lowrank.py:220, 331-333)
+    # 17 <= W <= 32 at one or two rank chunks: the forward as two passes (taps 0 .. W-17, then the
+    # last 16 added to the stored y, x read W-16 rows earlier), the backward as passes of 4 taps;
+    # long runs reach back up to 31 rows before their first tile (the runs' 32-row halo)
+    (1, 25, 64, 8, 20, False, True, torch.bfloat16, ("mfma", "mfma")),         # W 20 > T
+    (2, 300, 256, 16, 17, True, True, torch.bfloat16, ("mfma", "mfma")),       # forward 1 + 16 taps
+    (1, 3300, 256, 15, 32, True, True, torch.bfloat16, ("mfma", "mfma")),      # W 32: backward 8 passes
+    (2, 200, 128, 31, 24, True, False, torch.float16, ("mfma", "mfma")),       # two rank chunks, 8 + 16
+    (1, 520, 200, 20, 28, False, True, torch.bfloat16, ("mfma", "mfma")),      # D % 16 != 0, 12 + 16
+    (1, 3216, 64, 31, 25, True, True, torch.float16, ("mfma", "mfma")),        # long runs, two rank chunks
+    # widths above 8 at kernel ranks above 32 and kernel ranks above 64: the generic kernels
+    # (the reference accepts any W and power-of-two ranks, lowrank.py:220, 331-333)
     (1, 45, 64, 127, 12, True, True, torch.bfloat16, ("generic", "generic")),  # W 12, kernel rank 128
     (1, 30, 32, 255, 3, True, False, torch.float32, ("generic", "generic")),   # kernel rank 256 (the maximum)
     (1, 40, 64, 40, 9, False, True, torch.bfloat16, ("generic", "generic")),   # W 9, kernel rank 40
-    (1, 25, 64, 8, 20, False, True, torch.bfloat16, ("generic", "generic")),    # W 20 > T
+    (1, 25, 64, 40, 20, False, True, torch.bfloat16, ("generic", "generic")),  # W 20 > T, kernel rank 40
 ]
 
 

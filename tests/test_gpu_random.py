@@ -3,7 +3,8 @@
 Each case draws B, T, D, the head size (headwise) or rank (lowrank), W,
 static_w, residual and dtype from a fixed seed, so every dispatch path meets
 shapes nobody picked by hand: the vector / MFMA kernels with partial channel
-chunks and tiles, the lowrank backward's passes of taps (kernel ranks 33-64, and W 9-16), the fp32 matrix-core and VALU kernels, and the generic
+chunks and tiles, the lowrank passes of taps (kernel ranks 33-64, and W 9-32), the headwise wide
+kernels (W 9-16), the fp32 matrix-core and VALU kernels, and the generic
 kernels (D not a multiple of the vector width, head sizes that are not a power
 of two, ranks and W outside the fast plans).  Criterion: the north-star
 tolerance (tests/helpers.py) against the fp32 oracle on the same
@@ -79,14 +80,15 @@ def _lowrank_wide_case(i):
 
 
 def _lowrank_widew_case(i):
-    """W 9-16 at kernel ranks up to 32 in 16-bit types: the forward in one pass over up to 16 taps,
-    the backward as passes of at most 4 taps."""
+    """W 9-32 at kernel ranks up to 32 in 16-bit types: the forward in one pass over up to 16 taps
+    (above W 16 two passes, the second added to the first's y), the backward as passes of at most
+    4 taps."""
     rnd = random.Random(4099 * i + 7)
     dtype = rnd.choice([torch.bfloat16, torch.float16])
     Bn = rnd.randint(1, 2)
     Tn = rnd.choice([1, 7, 16, 17, 33, 64, 100, 129])
     Dn = rnd.choice([8, 24, 64, 128, 200, 256])
-    W = rnd.randint(9, 16)
+    W = rnd.randint(9, 32)
     static = rnd.random() < 0.5
     R = rnd.randint(1, 31)
     residual = rnd.random() < 0.5
