@@ -25,8 +25,9 @@ Also reported:
                call reading x out of the fused [B, T, 3D] projection, the fp32
                tier, the reference bench.py's own shapes (ref_*: head
                sizes 1, 4, 16 and rank 16, no static_w, no residual), lowrank
-               W 16 and W 20 and headwise W 12 on their wide kernels, and one
-               shape on the generic kernels (lowrank W 12 at rank 40);
+               W 16, W 20 and W 12 at rank 40 and headwise W 12 on their wide
+               kernels, and one shape on the generic kernels (lowrank kernel
+               rank 128);
   qkv          configs[4] end to end through autograd (forward + backward):
                the README's pattern (split the fused projection, .contiguous()
                each slice, three calls; autograd concatenates dq, dk, dv)
@@ -102,8 +103,10 @@ EXTRA = {
     "hw_W12_hs32": dict(kind="hw", B=4, T=4096, D=2048, H=64, W=12, static=True, residual=True),
     # W 20: the forward as two passes of taps (4 + 16), the backward as five passes of 4
     "lr_W20": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=20, static=False, residual=True),
-    # a shape the fast kernels do not take (above W 8 at kernel ranks above 32): the generic kernels, for their cost
-    "lr_W12_r40_generic": dict(kind="lr", B=4, T=4096, D=2048, R=40, W=12, static=False, residual=True),
+    # W 12 at kernel rank 40 (three rank chunks): the forward as passes of 4 + 8 taps, the backward as six of 2
+    "lr_W12_r40": dict(kind="lr", B=4, T=4096, D=2048, R=40, W=12, static=False, residual=True),
+    # a shape the fast kernels do not take (kernel rank above 64): the generic kernels, for their cost
+    "lr_r128_generic": dict(kind="lr", B=4, T=4096, D=2048, R=127, W=4, static=True, residual=True),
     # the reference bench.py's own shapes (bench.py:7-12): head sizes 1, 4, 16 and rank 16, no static_w, no residual
     "ref_hw_hs1": dict(kind="hw", B=4, T=4096, D=2048, H=2048, W=4, static=False, residual=False),
     "ref_hw_hs4": dict(kind="hw", B=4, T=4096, D=2048, H=512, W=4, static=False, residual=False),

@@ -399,12 +399,13 @@ hipError_t bwd_generic(const LrProblem& p) {
 bool lr_mfma_ok(const LrProblem& p, bool bwd) {
   if (p.dtype != kBF16 && p.dtype != kFP16) return false;
   if (p.W < 1 || p.W > 32) return false;
-  // every W <= 8 at every kernel rank <= 64, and W <= 32 at kernel ranks <= 32:
-  // the forward stages W x RC operand chunks (up to 128 KiB of LDS) and runs
-  // above W 16 as two passes of taps; the backward runs wide W x RC as passes
-  // of taps (the runs' 32-row halo covers a pass's look-back)
+  // every W <= 32 at every kernel rank <= 64: the forward stages W x RC
+  // operand chunks (up to 128 KiB of LDS) and runs wider problems (above W 16
+  // at one or two rank chunks, above W 8 at three or four) as passes of taps;
+  // the backward runs wide W x RC as passes of taps (the runs' 32-row halo
+  // covers a pass's look-back)
   const int64_t rc = (p.R + (p.static_w ? 1 : 0) + 15) / 16;
-  if (rc > 4 || (p.W > 8 && rc > 2)) return false;
+  if (rc > 4) return false;
   // buffer-offset range of a run (resources start at each run's base row, so
   // the sequence length is free): at least one tile must fit
   if ((bwd ? lr_bwd_max_run_tiles(p) : lr_fwd_max_run_tiles(p)) < 1) return false;

@@ -850,9 +850,14 @@ constexpr int pass_taps(int W, int RC) {
 }
 constexpr int npasses(int W, int RC) { return (W + pass_taps(W, RC) - 1) / pass_taps(W, RC); }
 
-// Above this width (more than four passes of taps) the passes add dx into an
-// fp32 accumulator in the workspace, rounded to dx once by lr_dx_round.
-constexpr int kBwdF32DxMinW = 16;
+// More than four passes of taps add dx into an fp32 accumulator in the
+// workspace, rounded to dx once by lr_dx_round (above W 16 at one or two rank
+// chunks, above W 8 at three, above W 4 at four).
+constexpr int kBwdMaxBf16DxPasses = 4;
+inline bool bwd_f32dx(const LrProblem& p) {
+  const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
+  return npasses((int)p.W, rc) > kBwdMaxBf16DxPasses;
+}
 
 }  // namespace
 
@@ -861,8 +866,8 @@ constexpr int kBwdF32DxMinW = 16;
 // itself or the padded copy) and the fp32 dz partials.
 int64_t lr_bwd_max_run_tiles(const LrProblem& p) {
   int64_t rowb = p.xld() * 2;
-  // above W 16 the passes' dx rows are the fp32 accumulator (D floats each)
-  const int64_t dxb = p.W > kBwdF32DxMinW ? p.D * 4 : p.dxld() * 2;
+  // past four passes of taps the passes' dx rows are the fp32 accumulator (D floats each)
+  const int64_t dxb = bwd_f32dx(p) ? p.D * 4 : p.dxld() * 2;
   const int64_t others[4] = {dxb, p.yhd() * 2, lr_bwd_zrow(p.R, p.static_w != nullptr) * 2, p.R * 4};
   for (int64_t v : others) rowb = rowb > v ? rowb : v;
   return run_tiles_cap(rowb);
@@ -1014,7 +1019,7 @@ BwdWs bwd_ws(const LrProblem& p, const LrBwdArgs& a) {
   w.du_off = (dz + 255) / 256 * 256;
   w.zp_off = (w.du_off + (int64_t)a.npair * a.RK * p.W * p.D * 4 + 255) / 256 * 256;
   w.dxf_off = (w.zp_off + a.BT * zpad_ranks(p) * 2 + 255) / 256 * 256;
-  w.total = w.dxf_off + (p.W > kBwdF32DxMinW ? a.BT * p.D * 4 : 0);
+  w.total = w.dxf_off + (bwd_f32dx(p) ? a.BT * p.D * 4 : 0);
   return w;
 }
 
@@ -1046,7 +1051,7 @@ hipError_t launch_bwd_kernel(const LrBwdArgs& a, hipStream_t stream) {
 // problem above W 8.
 template <typename T>
 hipError_t dispatch_bwd_kernel(const LrBwdArgs& a, int wq, int rc, bool wide, bool f32, hipStream_t stream) {
-  if (f32) {  // above W 16 (one or two rank chunks, passes of at most 4 taps)
+  if (f32) {  // more than four passes: one or two rank chunks above W 16, three or four above W 8 / 4
     switch (wq * 4 + rc) {
       case 5: return launch_bwd_kernel<T, 1, 1, true, true>(a, stream);
       case 9: return launch_bwd_kernel<T, 2, 1, true, true>(a, stream);
@@ -1056,6 +1061,9 @@ hipError_t dispatch_bwd_kernel(const LrBwdArgs& a, int wq, int rc, bool wide, bo
       case 10: return launch_bwd_kernel<T, 2, 2, false, true>(a, stream);
       case 14: return launch_bwd_kernel<T, 3, 2, false, true>(a, stream);
       case 18: return launch_bwd_kernel<T, 4, 2, false, true>(a, stream);
+      case 7: return launch_bwd_kernel<T, 1, 3, false, true>(a, stream);
+      case 11: return launch_bwd_kernel<T, 2, 3, false, true>(a, stream);
+      case 8: return launch_bwd_kernel<T, 1, 4, false, true>(a, stream);
       default: return hipErrorInvalidValue;
     }
   }
@@ -1114,8 +1122,8 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
   }
   const int64_t D = p[0].D, WD = p[0].W * D, RKWD = (int64_t)a.RK * WD, R = p[0].R;
   const int64_t dz_slot = (int64_t)a.ncg * a.BT * R;  // one pass's dz partials
-  // above W 16 every pass works on the fp32 accumulator (rows of D floats)
-  const bool f32 = W > kBwdF32DxMinW;
+  // past four passes every pass works on the fp32 accumulator (rows of D floats)
+  const bool f32 = bwd_f32dx(p[0]);
   if (f32) {
     a.dxld = (int)D;
     for (int g = 0; g < G; ++g) a.grp[g].dx = (char*)p[g].ws + w.dxf_off;

@@ -31,40 +31,55 @@ namespace {
 template <typename T>
 hipError_t dispatch_fwd(const LrProblem* pp, int G);
 
-// Above W 16 (up to 32), two passes of taps: taps 0 .. W-17 as a (W-16)-tap
-// problem (residual and z_eff included), then the last 16 taps, x read W-16
-// rows earlier, added to the stored y (accy).  U keeps its row stride W * D;
-// U and static_w of the second pass start at tap W - 16.  y is rounded to the
-// output type after each pass.
+// Taps per forward pass: what one launch stages (W x RC operand chunks in LDS).
+constexpr int fwd_pass_taps(int rc) { return rc <= 2 ? 16 : 8; }
+
+// Wider problems (above W 16 at one or two rank chunks, above W 8 at three or
+// four) as passes of taps: taps 0 .. W0-1 as a W0-tap problem (residual and
+// z_eff included), then passes of P = fwd_pass_taps taps, each on x read kofs
+// rows earlier and added to the stored y (accy).  U keeps its row stride W * D;
+// a later pass's U and static_w start at its tap kofs.  y is rounded to the
+// output type after each pass (two passes at W <= 32 and one or two rank
+// chunks, up to four at W 32 and three or four).
 template <typename T>
-hipError_t dispatch_fwd_passes(const LrProblem* pp, int G) {
-  const int W = (int)pp[0].W, kofs = W - 16;
-  LrProblem a[kMaxGroups], b[kMaxGroups];
+hipError_t dispatch_fwd_passes(const LrProblem* pp, int G, int P) {
+  const int W = (int)pp[0].W, np = (W + P - 1) / P, w0 = W - (np - 1) * P;
+  LrProblem a[kMaxGroups];
   for (int g = 0; g < G; ++g) {
-    const LrProblem& p = pp[g];
-    a[g] = p;
-    a[g].W = kofs;
-    a[g].u_ld = p.uld();
-    b[g] = p;
-    b[g].W = 16;
-    b[g].u_ld = p.uld();
-    b[g].kofs = kofs;
-    b[g].accy = 1;
-    b[g].U = static_cast<const T*>(p.U) + (int64_t)kofs * p.D;
-    b[g].static_w = p.static_w ? static_cast<const T*>(p.static_w) + (int64_t)kofs * p.D : nullptr;
-    b[g].residual = 0;
-    b[g].zeff = nullptr;
+    a[g] = pp[g];
+    a[g].W = w0;
+    a[g].u_ld = pp[g].uld();
   }
   hipError_t e = dispatch_fwd<T>(a, G);
-  if (e != hipSuccess) return e;
-  return lr_fwd_wide_dispatch<T>(b, G);
+  for (int ps = 1; ps < np && e == hipSuccess; ++ps) {
+    const int kofs = w0 + (ps - 1) * P;
+    for (int g = 0; g < G; ++g) {
+      const LrProblem& p = pp[g];
+      a[g] = p;
+      a[g].W = P;
+      a[g].u_ld = p.uld();
+      a[g].kofs = kofs;
+      a[g].accy = 1;
+      a[g].U = static_cast<const T*>(p.U) + (int64_t)kofs * p.D;
+      a[g].static_w = p.static_w ? static_cast<const T*>(p.static_w) + (int64_t)kofs * p.D : nullptr;
+      a[g].residual = 0;
+      a[g].zeff = nullptr;
+    }
+    e = dispatch_fwd<T>(a, G);
+  }
+  return e;
 }
 
 template <typename T>
 hipError_t dispatch_fwd(const LrProblem* pp, int G) {
   const LrProblem& p = pp[0];
-  if (p.W > 16) return dispatch_fwd_passes<T>(pp, G);
   const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
+  if (p.accy) {  // a later pass: the accumulating kernels of fwd_pass_taps(rc) taps
+    if (rc <= 2) return lr_fwd_wide_dispatch<T>(pp, G);
+    if (p.W != 8) return hipErrorInvalidValue;
+    return rc == 3 ? launch_fwd<T, 8, 3, true>(pp, G) : launch_fwd<T, 8, 4, true>(pp, G);
+  }
+  if (p.W > fwd_pass_taps(rc)) return dispatch_fwd_passes<T>(pp, G, fwd_pass_taps(rc));
 #define DC_LR_CASE(WW, CC) \
   if (p.W == WW && rc == CC) return launch_fwd<T, WW, CC>(pp, G);
   DC_LR_CASE(1, 1) DC_LR_CASE(1, 2) DC_LR_CASE(1, 3) DC_LR_CASE(1, 4)

@@ -307,12 +307,19 @@ LR_EDGE = [
     (2, 200, 128, 31, 24, True, False, torch.float16, ("mfma", "mfma")),       # two rank chunks, 8 + 16
     (1, 520, 200, 20, 28, False, True, torch.bfloat16, ("mfma", "mfma")),      # D % 16 != 0, 12 + 16
     (1, 3216, 64, 31, 25, True, True, torch.float16, ("mfma", "mfma")),        # long runs, two rank chunks
-    # widths above 8 at kernel ranks above 32 and kernel ranks above 64: the generic kernels
-    # (the reference accepts any W and power-of-two ranks, lowrank.py:220, 331-333)
+    # kernel ranks 33-64 above W 8: the forward as passes of 8 taps (the first W - 8(n-1), each later
+    # one added to the stored y), the backward as passes of 2 (three rank chunks) or 1 (four) taps
+    # into the fp32 dx accumulator
+    (1, 40, 64, 40, 9, False, True, torch.bfloat16, ("mfma", "mfma")),         # forward 1 + 8, 5 passes
+    (1, 100, 128, 40, 12, False, True, torch.bfloat16, ("mfma", "mfma")),      # forward 4 + 8, 6 passes
+    (2, 70, 256, 63, 9, True, True, torch.float16, ("mfma", "mfma")),          # four chunks: 9 passes of 1
+    (1, 300, 64, 47, 20, True, False, torch.bfloat16, ("mfma", "mfma")),       # forward 4 + 8 + 8
+    (1, 25, 64, 40, 20, False, True, torch.bfloat16, ("mfma", "mfma")),        # W 20 > T
+    (1, 50, 64, 64, 32, False, True, torch.bfloat16, ("mfma", "mfma")),        # W 32: forward 4 x 8, 32 passes
+    # kernel ranks above 64: the generic kernels (the reference accepts any W and power-of-two
+    # ranks, lowrank.py:220, 331-333)
     (1, 45, 64, 127, 12, True, True, torch.bfloat16, ("generic", "generic")),  # W 12, kernel rank 128
     (1, 30, 32, 255, 3, True, False, torch.float32, ("generic", "generic")),   # kernel rank 256 (the maximum)
-    (1, 40, 64, 40, 9, False, True, torch.bfloat16, ("generic", "generic")),   # W 9, kernel rank 40
-    (1, 25, 64, 40, 20, False, True, torch.bfloat16, ("generic", "generic")),  # W 20 > T, kernel rank 40
 ]
 
 

@@ -65,14 +65,15 @@ def _headwise_case(i):
 
 
 def _lowrank_wide_case(i):
-    """Kernel ranks 33-64 (3-4 rank chunks) at W 1-8 in 16-bit types: the matrix-core backward's
-    passes of taps (each pass's dx added to the earlier passes', its dz in slots of its own)."""
+    """Kernel ranks 33-64 (3-4 rank chunks) at W 1-12 in 16-bit types: the matrix-core backward's
+    passes of taps (each pass's dx added to the earlier passes', its dz in slots of its own; past
+    four passes in fp32), above W 8 the forward's passes of 8 taps."""
     rnd = random.Random(6113 * i + 29)
     dtype = rnd.choice([torch.bfloat16, torch.float16])
     Bn = rnd.randint(1, 2)
     Tn = rnd.choice([1, 15, 16, 17, 33, 64, 100, 129])
     Dn = rnd.choice([16, 64, 128, 144, 256])
-    W = rnd.randint(1, 8)
+    W = rnd.randint(1, 12)
     static = rnd.random() < 0.5
     R = rnd.randint(32, 63) if static else rnd.randint(33, 64)
     residual = rnd.random() < 0.5
