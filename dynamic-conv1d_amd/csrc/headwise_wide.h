@@ -31,8 +31,8 @@
 // k = 0: the residual)) to the open accumulator of row s-k; row s-W+1 is then
 // complete and stored.  A run reads dy and w for W-1 rows past its end (their
 // dx terms), which add nothing to dweight (stores dropped) or dstatic_w (dy
-// masked).  dstatic_w partial sums stay in registers (in LDS above W 12) over
-// the run, are added across the workgroup's 4 wavefronts in LDS in a fixed
+// masked).  dstatic_w partial sums stay in the wavefront's LDS slot (in
+// registers at head size 1 up to W 12) over the run, are added across the workgroup's 4 wavefronts in LDS in a fixed
 // order and written as one fp32 partial per workgroup, summed by
 // reduce_partials (deterministic).
 #pragma once
@@ -228,16 +228,17 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
   constexpr int ES = (int)sizeof(T);
   constexpr bool H1 = LPH == 0;
   constexpr int NH = H1 ? 2 : 1;
-  // with a static filter above W 12: two row buffers, and the dstatic_w sums
-  // in LDS instead of registers (fewer spills; up to W 12 registers are faster)
-  constexpr bool WIDE_ST = STATIC && W > 12;
-  constexpr int NB = WIDE_ST ? 2 : wide_nb(H1), M = (W + NB - 1) / NB * NB;
+  // With a static filter the dstatic_w sums go to LDS (registers held the
+  // static backward at one wavefront per SIMD: W 12 head size 32 214 -> 163 us,
+  // W 16 358 -> 207 us), except at head size 1 up to W 12, where registers are
+  // faster (372 against 385 us); above W 12 two row buffers.
+  constexpr bool WIDE_ST = STATIC && (W > 12 || !H1);
+  constexpr int NB = STATIC && W > 12 ? 2 : wide_nb(H1), M = (W + NB - 1) / NB * NB;
   constexpr int NP = WideSeg<T, W, H1>::NP;
   constexpr bool EVEN = H1 || W % 2 == 0;
   typedef Raw<T, kWideCpl> XR;
   __shared__ __attribute__((aligned(16))) uint8_t stg[4][NP * 1024];
   __shared__ __attribute__((aligned(8))) float dsr[STATIC ? 4 : 1][STATIC ? W * kWideCols : 1];
-  __shared__ __attribute__((aligned(8))) float swl[STATIC ? W * kWideCols : 1];
 
   const int lb = xcd_remap(blockIdx.x, a.nblk);
   const int wc = lb % a.nwc, sgp = lb / a.nwc;
@@ -267,9 +268,9 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
   const int we0 = hl * W;
   uint8_t* const my = stg[wave];
   const float res = a.residual ? 1.f : 0.f;  // tap 0's weight + 1: the residual's dy term
-  // dstatic_w sums of the lane's channels over the run: in registers, or above
-  // W 12 in the wavefront's LDS slot (tap k at dsl[k * 64]; each lane reads and
-  // writes only its own)
+  // dstatic_w sums of the lane's channels over the run: in the wavefront's LDS
+  // slot (tap k at dsl[k * 64]; each lane reads and writes only its own), or in
+  // registers (WIDE_ST false)
   float dsw[WIDE_ST ? 1 : W][kWideCpl];
   float2* const dsl = reinterpret_cast<float2*>(dsr[wave]) + lane;
   if constexpr (STATIC) {
@@ -283,14 +284,17 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
       }
     }
   }
-  // the static filter of the workgroup's channels in LDS, read per row (in
-  // registers it would hold 2W more per lane)
+  // the static filter of the lane's channels, in registers for the run (read
+  // from LDS per row it took 150 more registers in the unrolled row blocks)
+  float swf[STATIC ? W : 1][kWideCpl];
   if constexpr (STATIC) {
-    for (int e = threadIdx.x; e < W * kWideCols; e += 256) {
-      const int k = e / kWideCols, cc = e - k * kWideCols;
-      swl[e] = (float)sw[(int64_t)k * D + wc * kWideCols + cc];
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      float v[kWideCpl];
+      load_vals<T, kWideCpl>(sw + (int64_t)k * D + c0, v);
+      swf[k][0] = v[0];
+      swf[k][1] = v[1];
     }
-    __syncthreads();
   }
   float xf[M][kWideCpl], dxr[M][kWideCpl];
 #pragma unroll
@@ -326,7 +330,6 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
     for (int u = 0; u < M; ++u) {
       const int t = tb + u;
       const int p = u % M, buf = u % NB;
-      if constexpr (STATIC) asm volatile("" ::: "memory");  // static filter: re-read from LDS each row
       xr[buf].to_float(xf[p]);
       float dyv[kWideCpl], dym[kWideCpl];
       dr[buf].to_float(dyv);
@@ -347,7 +350,7 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
 #pragma unroll
         for (int j = 0; j < kWideCpl; ++j) {
           float tap = wv[(H1 ? j : 0) * W + k];
-          if constexpr (STATIC) tap += swl[k * kWideCols + kWideCpl * lane + j];
+          if constexpr (STATIC) tap += swf[k][j];
           if (k == 0) tap += res;
           dxr[q][j] = fmaf(dyv[j], tap, dxr[q][j]);
         }
