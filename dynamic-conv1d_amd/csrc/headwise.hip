@@ -189,8 +189,8 @@ HwPlan make_plan(const HwProblem& p, bool bwd) {
 // multiple of 128, 16-byte weight-row segments per wavefront.
 int wide_block(const HwProblem& p) { return wide_rows((int)p.W, p.D == p.H); }
 
-// Wavefronts per launch: two per SIMD (the kernels take up to 2 x 128 VGPRs
-// per lane), runs of at least one row block.
+// Wavefronts per launch: two per SIMD (the backward's occupancy at up to 256
+// registers per lane), runs of at least one row block.
 constexpr int kWideTargetWaves = 2048;
 
 HwWideArgs make_wide_args(const HwProblem& p) {
@@ -208,8 +208,6 @@ HwWideArgs make_wide_args(const HwProblem& p) {
   if (seg < L) seg = L;
   const int64_t tcap = (p.T + L - 1) / L * L;
   if (seg > tcap) seg = tcap;
-  const int64_t seg_cap = (kHwRunBytes / max_row_bytes(p) - kHwSlackRows) / L * L;
-  if (seg > seg_cap) seg = seg_cap;
   a.seg = (int)seg;
   a.nspb = (int)((p.T + seg - 1) / seg);
   a.nseg = (int)(p.B * a.nspb);
@@ -227,8 +225,9 @@ bool hw_wide_ok(const HwProblem& p, bool bwd) {
   if (p.D % kWideCols != 0) return false;
   // the wavefront's weight segment and a weight row: whole 16-byte pieces
   if (((kWideCols / hs) * p.W * es) % 16 != 0 || (p.H * p.W * es) % 16 != 0) return false;
-  // a run of one row block plus the look-ahead rows fits the resource range
-  if ((wide_block(p) + kHwSlackRows) * max_row_bytes(p) > kHwRunBytes) return false;
+  // each row has a resource of its own (any sequence length): a row's bytes, and
+  // with them every in-row offset, stay below the out-of-range lane offset
+  if (max_row_bytes(p) >= kHwLaneOob) return false;
   const int ea = (int)(kWideCpl * es);  // a lane's channels
   if (!aligned(p.x, ea) || !aligned(p.static_w, ea) || !aligned(p.weight, 16)) return false;
   if (!bwd) return aligned(p.y, ea);

@@ -479,6 +479,7 @@ def test_baseline_configs(cfg):
 # run's first tile in the second tap pass).
 LONG = {  # kind: dtype, T, D, W, R (lowrank), static_w
     "hw32": (torch.bfloat16, 131172, 2048, 4, None, True),
+    "hw32w12": (torch.bfloat16, 131172, 2048, 12, None, True),  # the wide kernels: a resource per row
     "lr16": (torch.bfloat16, 131172, 2048, 4, 15, True),
     "lr16n": (torch.bfloat16, 131172, 2048, 4, 16, False),
     "lr16f": (torch.float32, 65600, 2048, 4, 15, True),
@@ -491,8 +492,9 @@ def test_long_sequence(kind):
     dtype, Tn, Dn, W, R, static = LONG[kind]
     Bn = 1
     for bwd in (0, 1):
-        if kind == "hw32":
-            assert _path("hw", Bn, Tn, Dn, Dn // 32, W, dtype, True, bwd) == "vector"
+        if kind.startswith("hw"):
+            want = "vector" if W <= 8 else "wide"
+            assert _path("hw", Bn, Tn, Dn, Dn // 32, W, dtype, True, bwd) == want
         else:
             want = "f32_mfma" if dtype == torch.float32 else "mfma"
             assert _path("lr", Bn, Tn, Dn, R, W, dtype, static, bwd) == want
@@ -500,7 +502,7 @@ def test_long_sequence(kind):
     x = randn(g, Bn, Tn, Dn)
     dy = randn(g, Bn, Tn, Dn)
     sw = uniform(g, W, Dn, lo=-1 / math.sqrt(W), hi=1 / math.sqrt(W))
-    if kind == "hw32":
+    if kind.startswith("hw"):
         src, fn, ref = [x, randn(g, Bn, Tn, Dn // 32, W, scale=1 / math.sqrt(W)), sw], hw, hw_ref
     else:
         src, fn, ref = [x, randn(g, Bn, Tn, R), randn(g, R, W * Dn, scale=1 / math.sqrt((R + 1) * W)),
@@ -517,10 +519,10 @@ def test_long_sequence(kind):
         sl = slice(t0 - a, t1 - a)
         assert_ns(y_k[:, t0:t1], y_w[:, sl], dtype, f"y[{t0}:{t1}]")
         assert_ns(g_k[0][:, t0:t1], g_w[0][:, sl], dtype, f"dx[{t0}:{t1}]")
-        assert_ns(g_k[1][:, t0:t1], g_w[1][:, sl], dtype, f"d1[{t0}:{t1}]", elementwise=kind == "hw32")
+        assert_ns(g_k[1][:, t0:t1], g_w[1][:, sl], dtype, f"d1[{t0}:{t1}]", elementwise=kind.startswith("hw"))
     # the global reductions over the whole sequence (headwise dstatic_w; lowrank dz, dU,
     # dstatic_w): per-entry bounds against float64 sums
-    check_reductions("hw" if kind == "hw32" else "lr", q, dyq, g_k, dtype)
+    check_reductions("hw" if kind.startswith("hw") else "lr", q, dyq, g_k, dtype)
 
 
 def test_generic_lowrank_rows_past_2_24():
