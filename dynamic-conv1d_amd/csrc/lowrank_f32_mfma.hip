@@ -40,11 +40,18 @@ struct LrF32mArgs {
   int nblk;  // ceil(nseg / 4) * nch
   int xld;   // row stride of x (elements)
   int yhd;   // y layout: D ([B, T, D]) or the head dim of [B, D/yhd, T, yhd] (yhd % 4 == 0)
+  int uld;   // row stride of U (elements): the problem's W * D, all taps
+  int kofs;  // ACC pass: its first tap (x read kofs rows earlier)
 };
 
 constexpr int kF32mMaxKb = 8;  // kernel rank <= 32
+constexpr int kF32mFwdPassTaps = 8;  // above W 8 the forward runs as passes of taps
 
-template <int W, int NKB>
+// ACC: a later pass of taps kofs .. kofs+W-1 of a wider problem (the host runs
+// taps 0 .. W0-1 first, then passes of 8): x is read kofs rows earlier, U and
+// static_w start at tap kofs, and the tile's y rows, as the earlier passes
+// stored them, are added before the store (each lane its own rows).
+template <int W, int NKB, bool ACC = false>
 __global__ __launch_bounds__(256) void lr_fwd_f32m(const float* __restrict__ x, const float* __restrict__ z,
                                                    const float* __restrict__ U, const float* __restrict__ sw,
                                                    float* __restrict__ y, LrF32mArgs a) {
@@ -62,13 +69,14 @@ __global__ __launch_bounds__(256) void lr_fwd_f32m(const float* __restrict__ x, 
 
   // ---- stage the chunk's B operands (every rank row r < RK, zero beyond)
   {
-    const rsrc_t ru = make_rsrc(U, (int64_t)R * W * D * 4);
+    // U rows uld elements apart; U may start at a later pass's tap kofs
+    const rsrc_t ru = make_rsrc(U, ((int64_t)R * a.uld - (int64_t)(ACC ? a.kofs : 0) * D) * 4);
     const rsrc_t rs = make_rsrc(sw, sw ? (int64_t)W * D * 4 : 0);
     for (int kk = wave; kk < W * NKB; kk += 4) {
       const int k = kk / NKB, kb = kk - k * NKB;
       const int r = 4 * kb + q;
       const int col = (k * D + dl) * 4;
-      const u32x4 vu = bload128(ru, chv && r < R ? r * W * D * 4 + col : kOobLane);
+      const u32x4 vu = bload128(ru, chv && r < R ? r * a.uld * 4 + col : kOobLane);
       const u32x4 vs = bload128(rs, chv && r == R && r < RK ? col : kOobLane);
       f32x4 v;
 #pragma unroll
@@ -105,7 +113,8 @@ __global__ __launch_bounds__(256) void lr_fwd_f32m(const float* __restrict__ x, 
     const int t0 = tile * 16;
     u32x4 xr[NR];
 #pragma unroll
-    for (int m = 0; m < NR; ++m) xr[m] = bload128(rx, xlane_off + (t0 - rb) * xrowb + (m - (W - 1)) * xrowb);
+    for (int m = 0; m < NR; ++m)
+      xr[m] = bload128(rx, xlane_off + (t0 - rb - (ACC ? a.kofs : 0)) * xrowb + (m - (W - 1)) * xrowb);
     // A operands: z_eff[t0+n, 4kb+q]; the static rank R is 1 inside the sequence
     float za[NKB];
     const int zrow = (t0 + n - rb) * R * 4;
@@ -153,11 +162,17 @@ __global__ __launch_bounds__(256) void lr_fwd_f32m(const float* __restrict__ x, 
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      const int row = t0 + 4 * q + i;
+      const int yoff = row < Tn ? ylane_off + (t0 - rb + i) * yrowb : kOobTile;
+      if constexpr (ACC) {  // the earlier passes' y of the lane's row
+        const u32x4 p = bload128(ry, yoff);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) acc[i][jj] += __uint_as_float(p[jj]);
+      }
       u32x4 o;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) o[jj] = __float_as_uint(acc[i][jj]);
-      const int row = t0 + 4 * q + i;
-      bstore128<true>(o, ry, row < Tn ? ylane_off + (t0 - rb + i) * yrowb : kOobTile);
+      bstore128<true>(o, ry, yoff);
     }
   }
 }
@@ -582,25 +597,30 @@ LrF32mArgs make_f32m_args(const LrProblem& p) {
   a.nblk = ((a.nseg + 3) / 4) * a.nch;
   a.xld = (int)p.xld();
   a.yhd = (int)p.yhd();
+  a.uld = (int)p.uld();
+  a.kofs = p.kofs;
   return a;
 }
 
-template <int W, int NKB>
+template <int W, int NKB, bool ACC = false>
 hipError_t launch_f32m(const LrProblem& p) {
   const LrF32mArgs a = make_f32m_args(p);
-  lr_fwd_f32m<W, NKB><<<a.nblk, 256, 0, p.stream>>>((const float*)p.x, (const float*)p.z, (const float*)p.U,
-                                                      (const float*)p.static_w, (float*)p.y, a);
+  lr_fwd_f32m<W, NKB, ACC><<<a.nblk, 256, 0, p.stream>>>((const float*)p.x, (const float*)p.z, (const float*)p.U,
+                                                           (const float*)p.static_w, (float*)p.y, a);
   return hipGetLastError();
 }
 
+hipError_t lr_f32m_fwd_one(const LrProblem& p);
+
 }  // namespace
 
-// fp32, W <= 8, kernel rank <= 32, 16-byte pieces of x / y / U / static_w at
-// every row (D, x row stride and head dim multiples of 4, pointers 16-byte
-// aligned); sequences of any length (runs capped by f32m_fwd_max_run_tiles).
+// fp32, W <= 32 (above 8 as passes of taps), kernel rank <= 32, 16-byte pieces
+// of x / y / U / static_w at every row (D, x row stride and head dim multiples
+// of 4, pointers 16-byte aligned); sequences of any length (runs capped by
+// f32m_fwd_max_run_tiles).
 bool lr_f32m_fwd_ok(const LrProblem& p) {
   if (p.dtype != kFP32) return false;
-  if (p.W < 1 || p.W > 8) return false;
+  if (p.W < 1 || p.W > 32) return false;
   const int64_t rk = p.R + (p.static_w ? 1 : 0);
   if (rk > 4 * kF32mMaxKb) return false;
   if (p.D % 4 != 0 || p.xld() % 4 != 0 || p.yhd() % 4 != 0) return false;
@@ -610,9 +630,16 @@ bool lr_f32m_fwd_ok(const LrProblem& p) {
   return f32m_fwd_max_run_tiles(p) >= 1;              // at least one tile per run fits
 }
 
-hipError_t lr_f32m_fwd(const LrProblem& p) {
+namespace {
+
+// One launch of at most kF32mFwdPassTaps taps (accy: a later pass, W 8).
+hipError_t lr_f32m_fwd_one(const LrProblem& p) {
   const int nkb = (int)((p.R + (p.static_w ? 1 : 0) + 3) / 4);
   const int kb = nkb <= 2 ? 2 : nkb <= 4 ? 4 : 8;  // rank steps, rounded up (zero steps add nothing)
+  if (p.accy) {
+    if (p.W != kF32mFwdPassTaps) return hipErrorInvalidValue;
+    return kb == 2 ? launch_f32m<8, 2, true>(p) : kb == 4 ? launch_f32m<8, 4, true>(p) : launch_f32m<8, 8, true>(p);
+  }
 #define DC_F32M_CASE(WW, KB) \
   if (p.W == WW && kb == KB) return launch_f32m<WW, KB>(p);
   DC_F32M_CASE(1, 2) DC_F32M_CASE(1, 4) DC_F32M_CASE(1, 8)
@@ -625,6 +652,34 @@ hipError_t lr_f32m_fwd(const LrProblem& p) {
   DC_F32M_CASE(8, 2) DC_F32M_CASE(8, 4) DC_F32M_CASE(8, 8)
 #undef DC_F32M_CASE
   return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+// Above W 8: taps 0 .. W0-1 (W0 = W - 8(n-1)) as a W0-tap problem (residual
+// included), then passes of 8 taps added to the stored y; U keeps its row
+// stride W * D, a later pass's U and static_w start at its tap.
+hipError_t lr_f32m_fwd(const LrProblem& p) {
+  constexpr int P = kF32mFwdPassTaps;
+  if (p.W <= P) return lr_f32m_fwd_one(p);
+  const int W = (int)p.W, np = (W + P - 1) / P, w0 = W - (np - 1) * P;
+  LrProblem a = p;
+  a.W = w0;
+  a.u_ld = p.uld();
+  hipError_t e = lr_f32m_fwd_one(a);
+  for (int ps = 1; ps < np && e == hipSuccess; ++ps) {
+    const int kofs = w0 + (ps - 1) * P;
+    a = p;
+    a.W = P;
+    a.u_ld = p.uld();
+    a.kofs = kofs;
+    a.accy = 1;
+    a.U = (const float*)p.U + (int64_t)kofs * p.D;
+    a.static_w = p.static_w ? (const float*)p.static_w + (int64_t)kofs * p.D : nullptr;
+    a.residual = 0;
+    e = lr_f32m_fwd_one(a);
+  }
+  return e;
 }
 
 namespace {
@@ -662,10 +717,14 @@ LrF32mBwdArgs make_f32m_bwd_args(const LrProblem& p) {
 struct F32mWs {
   int64_t dz_off, du_off, total;
 };
-// Tap passes of a W-tap problem: one for W <= 4, else two of 2-4 taps (the
-// scatter form needs at least 2): W 5 = 3 + 2, 6 = 3 + 3, 7 = 4 + 3, 8 = 4 + 4.
-inline int f32m_tap_passes(int W) { return W <= 4 ? 1 : 2; }
-inline int f32m_pass_taps(int W, int tp) { return W <= 4 ? W : tp == 0 ? (W + 1) / 2 : W / 2; }
+// Tap passes of a W-tap problem: one for W <= 4, else ceil(W / 4) of 2-4 taps
+// (the scatter form needs at least 2), the larger ones first: W 5 = 3 + 2,
+// 8 = 4 + 4, 9 = 3 + 3 + 3, 17 = 4 + 4 + 3 + 3 + 3, 32 = 8 x 4.
+inline int f32m_tap_passes(int W) { return W <= 4 ? 1 : (W + 3) / 4; }
+inline int f32m_pass_taps(int W, int tp) {
+  const int n = f32m_tap_passes(W), base = W / n;
+  return tp < W % n ? base + 1 : base;
+}
 
 F32mWs f32m_ws(const LrProblem& p, const LrF32mBwdArgs& a) {
   F32mWs w;
@@ -741,14 +800,14 @@ hipError_t launch_f32m_bwd(const LrProblem& p) {
 
 }  // namespace
 
-// fp32, 2 <= W <= 8 (above 4 as two tap passes), kernel rank <= 32 (above 16 as
-// two rank passes); D, x / dx row strides multiples of 4
+// fp32, 2 <= W <= 32 (above 4 as passes of 2-4 taps), kernel rank <= 32 (above
+// 16 as two rank passes); D, x / dx row strides multiples of 4
 // (8-byte lane pieces, 16-byte operand pieces); dy's head dim a multiple of 32
 // (a chunk inside one head); 16-byte aligned x, dy, dx, U, static_w; sequences
 // of any length (runs capped by f32m_bwd_max_run_tiles).
 bool lr_f32m_bwd_ok(const LrProblem& p) {
   if (p.dtype != kFP32) return false;
-  if (p.W < 2 || p.W > 8) return false;
+  if (p.W < 2 || p.W > 32) return false;
   if (p.R + (p.static_w ? 1 : 0) > 32) return false;
   if (p.D % 4 != 0 || p.xld() % 4 != 0 || p.dxld() % 4 != 0) return false;
   if (p.yhd() != p.D && p.yhd() % 32 != 0) return false;

@@ -281,8 +281,10 @@ def test_kernel_paths(lib):
     for bwd in (0, 1):                                         # fp32 sequences past 512 MiB of rows:
         assert lp(1, 65600, 2048, 15, 4, f32, 1, bwd) == 3     # per-run buffer ranges
         assert lp(1, 1 << 20, 4096, 31, 8, f32, 1, bwd) == 3
-    for bwd in (0, 1):                                         # fp32 W 5-8: forward at any W, backward
-        assert lp(4, 4096, 2048, 16, 8, f32, 0, bwd) == 3      # as two tap passes
+    for bwd in (0, 1):                                         # fp32 W 5-32: forward passes of 8 taps
+        assert lp(1, 100, 256, 16, 20, f32, 1, bwd) == 3       # above W 8, backward passes of 2-4 taps
+        assert lp(1, 100, 256, 31, 32, f32, 0, bwd) == 3
+        assert lp(4, 4096, 2048, 16, 8, f32, 0, bwd) == 3
         assert lp(1, 100, 256, 31, 5, f32, 1, bwd) == 3
     for bwd in (0, 1):                                         # every W <= 8 at every kernel rank <= 64:
         assert lp(2, 50, 256, 63, 2, bf, 1, bwd) == 2          # the backward as passes of taps

@@ -270,6 +270,12 @@ LR_EDGE = [
     (1, 100, 128, 31, 5, True, True, torch.float32, ("f32_mfma", "f32_mfma")),    # W 5: 3 + 2, x 2 rank passes
     (2, 1000, 272, 7, 6, True, False, torch.float32, ("f32_mfma", "f32_mfma")),   # W 6: 3 + 3, long runs
     (1, 40, 64, 20, 7, False, True, torch.float32, ("f32_mfma", "f32_mfma")),     # W 7: 4 + 3, rank passes
+    # fp32 W 9-32: the forward as passes of 8 taps (the first W - 8(n-1), later ones added to the
+    # stored y), the backward as ceil(W / 4) passes of 2-4 taps (dx in fp32 throughout)
+    (2, 300, 256, 16, 12, False, True, torch.float32, ("f32_mfma", "f32_mfma")),  # forward 4 + 8, 4+4+4
+    (1, 100, 128, 31, 20, True, True, torch.float32, ("f32_mfma", "f32_mfma")),   # 5 tap x 2 rank passes
+    (1, 3300, 64, 7, 32, True, False, torch.float32, ("f32_mfma", "f32_mfma")),   # W 32, long runs
+    (1, 5, 64, 3, 9, False, True, torch.float32, ("f32_mfma", "f32_mfma")),       # W 9 > T
     # matrix-core plans with three and four rank chunks (kernel ranks 33-64 at W 1-2)
     (1, 70, 128, 64, 1, False, True, torch.bfloat16, ("mfma", "mfma")),      # <W1, 4 chunks>
     (2, 50, 256, 63, 2, True, True, torch.bfloat16, ("mfma", "mfma")),       # <W2, 4 chunks>: backward in 2 passes
