@@ -25,7 +25,7 @@ Also reported:
                call reading x out of the fused [B, T, 3D] projection, the fp32
                tier, the reference bench.py's own shapes (ref_*: head
                sizes 1, 4, 16 and rank 16, no static_w, no residual), lowrank
-               W 16, W 20 and W 12 at rank 40 and headwise W 12 on their wide
+               W 16, W 20 and W 12 at rank 40 and headwise W 12 and W 24 on their wide
                kernels, and one shape on the generic kernels (lowrank kernel
                rank 128);
   qkv          configs[4] end to end through autograd (forward + backward):
@@ -101,6 +101,8 @@ EXTRA = {
     # headwise above W 8: the wide row-ring kernels (head sizes 1 and 32, static filter, residual)
     "hw_W12_hs1": dict(kind="hw", B=4, T=4096, D=2048, H=2048, W=12, static=True, residual=True),
     "hw_W12_hs32": dict(kind="hw", B=4, T=4096, D=2048, H=64, W=12, static=True, residual=True),
+    # above W 16 the wide kernels keep one channel per lane
+    "hw_W24_hs32": dict(kind="hw", B=4, T=4096, D=2048, H=64, W=24, static=True, residual=True),
     # W 20: the forward as two passes of taps (4 + 16), the backward as five passes of 4
     "lr_W20": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=20, static=False, residual=True),
     # W 12 at kernel rank 40 (three rank chunks): the forward as passes of 4 + 8 taps, the backward as six of 2

@@ -185,9 +185,11 @@ HwPlan make_plan(const HwProblem& p, bool bwd) {
 }
 
 // ------------------------------------------------------------ wide path
-// 9 <= W <= 16 (headwise_wide.h): power-of-two head sizes up to 128, D a
-// multiple of 128, 16-byte weight-row segments per wavefront.
-int wide_block(const HwProblem& p) { return wide_rows((int)p.W, p.D == p.H); }
+// 9 <= W <= 32 (headwise_wide.h): power-of-two head sizes up to a wavefront's
+// 64 * CPL channels, D a multiple of those, 16-byte weight-row segments per
+// wavefront.  Runs are rounded to 4 rows (the kernels' row blocks are W
+// rounded up to 2 or 4).
+int wide_block(const HwProblem& p) { return ((int)p.W + 3) / 4 * 4; }
 
 // Wavefronts per launch: two per SIMD (the backward's occupancy at up to 256
 // registers per lane), runs of at least one row block.
@@ -201,8 +203,10 @@ HwWideArgs make_wide_args(const HwProblem& p) {
   a.Tn = (int)p.T;
   a.D = (int)p.D;
   a.H = (int)p.H;
+  const int cols = 64 * wide_cpl((int)p.W);
   a.hs_shift = ilog2(hs);
-  a.nwc = (int)(p.D / kWideCols);
+  a.lph = hs > cols / 64 ? (int)(hs / (cols / 64)) : 1;
+  a.nwc = (int)(p.D / cols);
   int64_t seg = (p.B * p.T * a.nwc + kWideTargetWaves - 1) / kWideTargetWaves;
   seg = (seg + L - 1) / L * L;
   if (seg < L) seg = L;
@@ -212,7 +216,7 @@ HwWideArgs make_wide_args(const HwProblem& p) {
   a.nspb = (int)((p.T + seg - 1) / seg);
   a.nseg = (int)(p.B * a.nspb);
   a.nblk = ((a.nseg + 3) / 4) * a.nwc;
-  a.sbytes = (int)((kWideCols >> a.hs_shift) * p.W * es);
+  a.sbytes = (int)((cols >> a.hs_shift) * p.W * es);
   a.residual = p.residual;
   return a;
 }
@@ -221,14 +225,15 @@ bool hw_wide_ok(const HwProblem& p, bool bwd) {
   const int64_t es = dtype_size(p.dtype);
   const int64_t hs = p.D / p.H;
   if (p.W < kHwWideMinW || p.W > kHwWideMaxW) return false;
-  if ((hs & (hs - 1)) != 0 || hs > kWideCols) return false;  // a head within one wavefront
-  if (p.D % kWideCols != 0) return false;
+  const int64_t cols = 64 * wide_cpl((int)p.W);  // channels per wavefront
+  if ((hs & (hs - 1)) != 0 || hs > cols) return false;  // a head within one wavefront
+  if (p.D % cols != 0) return false;
   // the wavefront's weight segment and a weight row: whole 16-byte pieces
-  if (((kWideCols / hs) * p.W * es) % 16 != 0 || (p.H * p.W * es) % 16 != 0) return false;
+  if (((cols / hs) * p.W * es) % 16 != 0 || (p.H * p.W * es) % 16 != 0) return false;
   // each row has a resource of its own (any sequence length): a row's bytes, and
   // with them every in-row offset, stay below the out-of-range lane offset
   if (max_row_bytes(p) >= kHwLaneOob) return false;
-  const int ea = (int)(kWideCpl * es);  // a lane's channels
+  const int ea = (int)(wide_cpl((int)p.W) * es);  // a lane's channels
   if (!aligned(p.x, ea) || !aligned(p.static_w, ea) || !aligned(p.weight, 16)) return false;
   if (!bwd) return aligned(p.y, ea);
   return aligned(p.dy, ea) && aligned(p.dx, ea) && aligned(p.dweight, 16);

@@ -1,4 +1,4 @@
-// Headwise dynamic convolution for 9 <= W <= 16 (the vectorised kernels of
+// Headwise dynamic convolution for 9 <= W <= 32 (the vectorised kernels of
 // headwise_fast.h stop at W 8: their register rings grow with W x chunk rows).
 //
 //   y[b,t,d] = sum_{k<W} (w[b,t,d/hs,k] + sw[k,d]) * x[b,t-k,d]  (+ x[b,t,d])
@@ -6,56 +6,61 @@
 // Reference kernels: headwise.py:24-91 (forward) and headwise.py:105-215
 // (backward); any W (headwise.py:226).
 //
-// Layout.  A lane owns 2 channels (kWideCpl), a wavefront 128 consecutive
-// channels (D % 128 == 0), and walks a run of rows of one sequence one row at
-// a time, keeping the last W rows of x (and in the backward the W open dx
-// accumulators) in fp32 register rings whose slot for row t is (t - t0) mod W.
-// The rows of the next NB steps are in flight while a row is computed (NB raw
-// buffers, the loads of row t+NB issued once row t's raw values are consumed):
-// NB = 2 at head size 1, whose weight rows are 2W bytes per lane, and 4 at
-// larger head sizes, whose rows are mostly x (and dy).  The rings have M slots,
+// Layout.  A lane owns CPL channels (2 up to W 16, 1 above), a wavefront
+// 64 * CPL consecutive channels (D a multiple of that), and walks a run of
+// rows of one sequence one row at a time, keeping the last W rows of x (and in
+// the backward the W open dx accumulators) in fp32 register rings whose slot
+// for row t is (t - t0) mod M.  The rows of the next NB steps are in flight
+// while a row is computed (NB raw buffers, the loads of row t+NB issued once
+// row t's raw values are consumed): NB = 2 where a lane's weight piece is large
+// (two heads per lane, or one channel per lane), 4 otherwise, whose rows are
+// mostly x (and dy).  The rings have M slots,
 // W rounded up to a multiple of NB, and rows are processed in unrolled blocks
 // of M rows, so every ring and buffer index is a compile-time constant.
 //
-// Weight rows.  A wavefront's channels cover 128/hs heads (hs <= 128), whose
-// weights are one contiguous segment of (128/hs) * W elements of the row
+// Weight rows.  A wavefront's channels cover 64 * CPL / hs heads, whose
+// weights are one contiguous segment of (64 * CPL / hs) * W elements of the row
 // (16-byte multiple, checked on the host).  The wavefront loads it with
 // 16-byte lane pieces that are contiguous across the wavefront, passes it
 // through its own LDS slot, and each lane reads its head's W weights (head
 // size 1: the two heads of its channels).  The backward's dweight row goes the
-// same way in reverse: the lanes' two-channel sums are added over the head's
-// lanes (DPP butterflies, ds_bpermute steps beyond 16 lanes), written to the
-// slot, and stored as contiguous 16-byte pieces.
+// same way in reverse: the lanes' channel sums are added over the head's lanes
+// (DPP butterflies, ds_bpermute steps beyond 16 lanes; above W 16 over a
+// run-time group size), written to the slot, and stored as contiguous 16-byte
+// pieces.
 //
 // Backward.  dx in scatter form: row s adds dy[s] * (w[s,k] + sw[k] (+1 at
 // k = 0: the residual)) to the open accumulator of row s-k; row s-W+1 is then
 // complete and stored.  A run reads dy and w for W-1 rows past its end (their
 // dx terms), which add nothing to dweight (stores dropped) or dstatic_w (dy
 // masked).  dstatic_w partial sums stay in the wavefront's LDS slot (in
-// registers at head size 1 up to W 12) over the run, are added across the workgroup's 4 wavefronts in LDS in a fixed
-// order and written as one fp32 partial per workgroup, summed by
-// reduce_partials (deterministic).
+// registers at head size 1 up to W 12) over the run, are added across the
+// workgroup's 4 wavefronts in LDS in a fixed order and written as one fp32
+// partial per workgroup, summed by reduce_partials (deterministic).
 #pragma once
 
 #include "headwise_fast.h"
 
 namespace dc {
 
-constexpr int kWideCpl = 2;                 // channels per lane
-constexpr int kWideCols = 64 * kWideCpl;    // channels per wavefront
-constexpr int kHwWideMinW = 9, kHwWideMaxW = 16;
+constexpr int kHwWideMinW = 9, kHwWideMaxW = 32;
+// Channels per lane: 2 up to W 16, 1 above (the x and dx rings hold W rows of
+// a lane's channels); a wavefront covers 64 * CPL channels.
+constexpr int kWideCplMaxW = 16;
+constexpr int wide_cpl(int W) { return W <= kWideCplMaxW ? 2 : 1; }
 
-// Row buffers in flight per wavefront, and ring slots (= rows per unrolled
-// block) at width W; h1: head size 1.
-constexpr int wide_nb(bool h1) { return h1 ? 2 : 4; }
-constexpr int wide_rows(int W, bool h1) { return (W + wide_nb(h1) - 1) / wide_nb(h1) * wide_nb(h1); }
+// Row buffers in flight per wavefront: 2 where a lane's weight piece of a row
+// is large (two heads per lane, or one channel per lane up to 64 heads of W
+// taps per wavefront), else 4.  h1: two heads per lane (CPL 2, head size 1).
+constexpr int wide_nb(bool h1, int cpl) { return h1 || cpl == 1 ? 2 : 4; }
 
 struct HwWideArgs {
   int Tn;        // sequence length
-  int D;         // channels (a multiple of kWideCols)
+  int D;         // channels (a multiple of 64 * CPL)
   int H;         // heads
   int hs_shift;  // log2(head size), 0 .. 7
-  int nwc;       // D / kWideCols wavefront columns
+  int lph;       // lanes per head (head size / CPL, at least 1): the one-channel kernels' head sums
+  int nwc;       // D / (64 * CPL) wavefront columns
   int seg;       // rows per run (a multiple of the kernel's row block)
   int nspb;      // runs per sequence
   int nseg;      // B * nspb
@@ -64,10 +69,11 @@ struct HwWideArgs {
   int residual;
 };
 
-// 16-byte pieces per lane of a wavefront's weight-row segment, at most.
+// 16-byte pieces per lane of a wavefront's weight-row segment, at most: 128
+// heads with two heads per lane, else at most 64.
 template <typename T, int W, bool H1>
 struct WideSeg {
-  static constexpr int BYTES = (H1 ? kWideCols : kWideCols / 2) * W * (int)sizeof(T);
+  static constexpr int BYTES = (H1 ? 128 : 64) * W * (int)sizeof(T);
   static constexpr int NP = (BYTES + 1023) / 1024;
 };
 
@@ -120,16 +126,27 @@ __device__ __forceinline__ void lds_elems(const uint8_t* seg, int e0, float (&ou
   }
 }
 
+// A lane's CPL products dy * x added in channel order (its share of a head sum).
+template <int CPL>
+__device__ __forceinline__ float lane_sum(const float (&dy)[CPL], const float (&x)[CPL]) {
+  float s = dy[0] * x[0];
+#pragma unroll
+  for (int j = 1; j < CPL; ++j) s = fmaf(dy[j], x[j], s);
+  return s;
+}
+
 // ------------------------------------------------------------------ forward
-template <typename T, int W, bool H1, bool STATIC>
+template <typename T, int W, int CPL, bool H1, bool STATIC>
 __global__ __launch_bounds__(256) void hw_fwd_wide(const T* __restrict__ x, const T* __restrict__ wt,
                                                    const T* __restrict__ sw, T* __restrict__ y, HwWideArgs a) {
+  static_assert(CPL == 2 || !H1, "two heads per lane: two channels per lane");
   constexpr int ES = (int)sizeof(T);
+  constexpr int COLS = 64 * CPL;  // channels per wavefront
   constexpr int NH = H1 ? 2 : 1;  // heads per lane
-  constexpr int NB = wide_nb(H1), M = wide_rows(W, H1);
+  constexpr int NB = wide_nb(H1, CPL), M = (W + NB - 1) / NB * NB;
   constexpr int NP = WideSeg<T, W, H1>::NP;
   constexpr bool EVEN = H1 || W % 2 == 0;
-  typedef Raw<T, kWideCpl> XR;
+  typedef Raw<T, CPL> XR;
   __shared__ __attribute__((aligned(16))) uint8_t stg[4][NP * 1024];
 
   const int lb = xcd_remap(blockIdx.x, a.nblk);
@@ -140,35 +157,35 @@ __global__ __launch_bounds__(256) void hw_fwd_wide(const T* __restrict__ x, cons
   const WideRun run(a, s);
   const int t0 = run.t0, t1 = run.t1;
   const int D = a.D;
-  const int c0 = wc * kWideCols + kWideCpl * lane;  // the lane's first channel
+  const int c0 = wc * COLS + CPL * lane;  // the lane's first channel
   const int rowb = D * ES, wrowb = a.H * W * ES;
   const int64_t WH = (int64_t)a.H * W;
   const T* const xs = x + (int64_t)run.b * a.Tn * D;  // the sequence's first rows
   T* const ys = y + (int64_t)run.b * a.Tn * D;
   const T* const ws = wt + (int64_t)run.b * a.Tn * WH;
   const int xlo = c0 * ES;
-  const int wseg = ((wc * kWideCols) >> a.hs_shift) * W * ES;  // the wavefront's segment in a weight row
+  const int wseg = ((wc * COLS) >> a.hs_shift) * W * ES;  // the wavefront's segment in a weight row
   int wpo[NP];  // the lane's 16-byte pieces of the segment (past it: out of range)
 #pragma unroll
   for (int i = 0; i < NP; ++i) wpo[i] = (i * 64 + lane) * 16 < a.sbytes ? wseg + (i * 64 + lane) * 16 : kHwLaneOob;
   // the lane's weights in the segment: element offset of its (first) head
-  const int we0 = H1 ? 2 * lane * W : ((kWideCpl * lane) >> a.hs_shift) * W;
+  const int we0 = H1 ? 2 * lane * W : ((CPL * lane) >> a.hs_shift) * W;
   uint8_t* const my = stg[wave];
 
-  float swf[W][kWideCpl];
+  float swf[W][CPL];
 #pragma unroll
   for (int k = 0; k < W; ++k) {
     if constexpr (STATIC) {
-      float v[kWideCpl];
-      load_vals<T, kWideCpl>(sw + (int64_t)k * D + c0, v);
+      float v[CPL];
+      load_vals<T, CPL>(sw + (int64_t)k * D + c0, v);
 #pragma unroll
-      for (int j = 0; j < kWideCpl; ++j) swf[k][j] = v[j];
+      for (int j = 0; j < CPL; ++j) swf[k][j] = v[j];
     }
   }
   // x ring: row t in slot (t - t0) mod W; rows before 0 read 0 (negative offsets are out of range)
-  float xf[M][kWideCpl];
+  float xf[M][CPL];
 #pragma unroll
-  for (int j = 0; j < kWideCpl; ++j) xf[0][j] = 0.f;
+  for (int j = 0; j < CPL; ++j) xf[0][j] = 0.f;
 #pragma unroll
   for (int i = 1; i < W; ++i) {
     XR h;
@@ -200,45 +217,49 @@ __global__ __launch_bounds__(256) void hw_fwd_wide(const T* __restrict__ x, cons
       __builtin_amdgcn_wave_barrier();
       float wv[NH * W];
       lds_elems<T, NH * W, EVEN>(my, we0, wv);
-      float acc[kWideCpl];
+      float acc[CPL];
 #pragma unroll
-      for (int j = 0; j < kWideCpl; ++j) acc[j] = a.residual ? xf[p][j] : 0.f;
+      for (int j = 0; j < CPL; ++j) acc[j] = a.residual ? xf[p][j] : 0.f;
 #pragma unroll
       for (int k = 0; k < W; ++k) {
         const int q = ((u - k) % M + M) % M;
 #pragma unroll
-        for (int j = 0; j < kWideCpl; ++j) {
+        for (int j = 0; j < CPL; ++j) {
           float tap = wv[(H1 ? j : 0) * W + k];
           if constexpr (STATIC) tap += swf[k][j];
           acc[j] = fmaf(tap, xf[q][j], acc[j]);
         }
       }
-      bstore_vals<T, kWideCpl, true>(row_rsrc(ys, D, t, t < t1, rowb), xlo, acc);
+      bstore_vals<T, CPL, true>(row_rsrc(ys, D, t, t < t1, rowb), xlo, acc);
     }
   }
 }
 
 // ----------------------------------------------------------------- backward
-// LPH: lanes per head, 0 at head size 1 (a lane's two channels are two heads).
-template <typename T, int W, int LPH, bool STATIC>
+// LPH: lanes per head: 0 at head size 1 with two channels per lane (two
+// heads per lane), 1 for a lane's own head, 2..64 a compile-time group, -1 the
+// run-time a.lph (the one-channel kernels above W 16).
+template <typename T, int W, int CPL, int LPH, bool STATIC>
 __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, const T* __restrict__ wt,
                                                    const T* __restrict__ sw, const T* __restrict__ dy,
                                                    T* __restrict__ dx, T* __restrict__ dwt,
                                                    float* __restrict__ part, HwWideArgs a) {
   constexpr int ES = (int)sizeof(T);
   constexpr bool H1 = LPH == 0;
+  static_assert(CPL == 2 || !H1, "two heads per lane: two channels per lane");
+  constexpr int COLS = 64 * CPL;  // channels per wavefront
   constexpr int NH = H1 ? 2 : 1;
   // With a static filter the dstatic_w sums go to LDS (registers held the
   // static backward at one wavefront per SIMD: W 12 head size 32 214 -> 163 us,
   // W 16 358 -> 207 us), except at head size 1 up to W 12, where registers are
   // faster (372 against 385 us); above W 12 two row buffers.
   constexpr bool WIDE_ST = STATIC && (W > 12 || !H1);
-  constexpr int NB = STATIC && W > 12 ? 2 : wide_nb(H1), M = (W + NB - 1) / NB * NB;
+  constexpr int NB = STATIC && W > 12 ? 2 : wide_nb(H1, CPL), M = (W + NB - 1) / NB * NB;
   constexpr int NP = WideSeg<T, W, H1>::NP;
   constexpr bool EVEN = H1 || W % 2 == 0;
-  typedef Raw<T, kWideCpl> XR;
+  typedef Raw<T, CPL> XR;
   __shared__ __attribute__((aligned(16))) uint8_t stg[4][NP * 1024];
-  __shared__ __attribute__((aligned(8))) float dsr[STATIC ? 4 : 1][STATIC ? W * kWideCols : 1];
+  __shared__ __attribute__((aligned(8))) float dsr[STATIC ? 4 : 1][STATIC ? W * COLS : 1];
 
   const int lb = xcd_remap(blockIdx.x, a.nblk);
   const int wc = lb % a.nwc, sgp = lb / a.nwc;
@@ -250,7 +271,7 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
   const WideRun run(a, has_run ? s : 0);
   const int t0 = run.t0, t1 = has_run ? run.t1 : run.t0;
   const int D = a.D, Tn = a.Tn;
-  const int c0 = wc * kWideCols + kWideCpl * lane;
+  const int c0 = wc * COLS + CPL * lane;
   const int rowb = D * ES, wrowb = a.H * W * ES;
   const int64_t WH = (int64_t)a.H * W;
   const int64_t so = (int64_t)run.b * Tn;  // the sequence's first row
@@ -260,49 +281,44 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
   const T* const ws = wt + so * WH;
   T* const dws = dwt + so * WH;
   const int xlo = c0 * ES;
-  const int wseg = ((wc * kWideCols) >> a.hs_shift) * W * ES;
+  const int wseg = ((wc * COLS) >> a.hs_shift) * W * ES;
   int wpo[NP];
 #pragma unroll
   for (int i = 0; i < NP; ++i) wpo[i] = (i * 64 + lane) * 16 < a.sbytes ? wseg + (i * 64 + lane) * 16 : kHwLaneOob;
-  const int hl = H1 ? 2 * lane : (kWideCpl * lane) >> a.hs_shift;  // the lane's (first) head in the segment
+  const int hl = H1 ? 2 * lane : (CPL * lane) >> a.hs_shift;  // the lane's (first) head in the segment
   const int we0 = hl * W;
   uint8_t* const my = stg[wave];
   const float res = a.residual ? 1.f : 0.f;  // tap 0's weight + 1: the residual's dy term
   // dstatic_w sums of the lane's channels over the run: in the wavefront's LDS
-  // slot (tap k at dsl[k * 64]; each lane reads and writes only its own), or in
+  // slot (tap k at dsl[k * COLS]; each lane reads and writes only its own), or in
   // registers (WIDE_ST false)
-  float dsw[WIDE_ST ? 1 : W][kWideCpl];
-  float2* const dsl = reinterpret_cast<float2*>(dsr[wave]) + lane;
+  float dsw[WIDE_ST ? 1 : W][CPL];
+  float* const dsl = dsr[wave] + CPL * lane;
   if constexpr (STATIC) {
 #pragma unroll
-    for (int k = 0; k < W; ++k) {
-      if constexpr (WIDE_ST) {
-        dsl[k * 64] = make_float2(0.f, 0.f);
-      } else {
-        dsw[k][0] = 0.f;
-        dsw[k][1] = 0.f;
+    for (int k = 0; k < W; ++k)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        if constexpr (WIDE_ST)
+          dsl[k * COLS + j] = 0.f;
+        else
+          dsw[k][j] = 0.f;
       }
-    }
   }
   // the static filter of the lane's channels, in registers for the run (read
   // from LDS per row it took 150 more registers in the unrolled row blocks)
-  float swf[STATIC ? W : 1][kWideCpl];
+  float swf[STATIC ? W : 1][CPL];
   if constexpr (STATIC) {
 #pragma unroll
-    for (int k = 0; k < W; ++k) {
-      float v[kWideCpl];
-      load_vals<T, kWideCpl>(sw + (int64_t)k * D + c0, v);
-      swf[k][0] = v[0];
-      swf[k][1] = v[1];
-    }
+    for (int k = 0; k < W; ++k) load_vals<T, CPL>(sw + (int64_t)k * D + c0, swf[k]);
   }
-  float xf[M][kWideCpl], dxr[M][kWideCpl];
+  float xf[M][CPL], dxr[M][CPL];
 #pragma unroll
   for (int i = 0; i < M; ++i)
 #pragma unroll
-    for (int j = 0; j < kWideCpl; ++j) dxr[i][j] = 0.f;
+    for (int j = 0; j < CPL; ++j) dxr[i][j] = 0.f;
 #pragma unroll
-  for (int j = 0; j < kWideCpl; ++j) xf[0][j] = 0.f;
+  for (int j = 0; j < CPL; ++j) xf[0][j] = 0.f;
 #pragma unroll
   for (int i = 1; i < W; ++i) {
     XR h;
@@ -331,10 +347,10 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
       const int t = tb + u;
       const int p = u % M, buf = u % NB;
       xr[buf].to_float(xf[p]);
-      float dyv[kWideCpl], dym[kWideCpl];
+      float dyv[CPL], dym[CPL];
       dr[buf].to_float(dyv);
 #pragma unroll
-      for (int j = 0; j < kWideCpl; ++j) dym[j] = t < t1 ? dyv[j] : 0.f;  // rows past the run: dx terms only
+      for (int j = 0; j < CPL; ++j) dym[j] = t < t1 ? dyv[j] : 0.f;  // rows past the run: dx terms only
       __builtin_amdgcn_wave_barrier();  // the previous row's reads of the slot are done
 #pragma unroll
       for (int i = 0; i < NP; ++i) reinterpret_cast<u32x4*>(my)[i * 64 + lane] = wr[buf][i];
@@ -348,7 +364,7 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
       for (int k = 0; k < W; ++k) {
         const int q = ((u - k) % M + M) % M;
 #pragma unroll
-        for (int j = 0; j < kWideCpl; ++j) {
+        for (int j = 0; j < CPL; ++j) {
           float tap = wv[(H1 ? j : 0) * W + k];
           if constexpr (STATIC) tap += swf[k][j];
           if (k == 0) tap += res;
@@ -358,9 +374,9 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
       {
         const int q = ((u - W + 1) % M + M) % M;  // slot of row t-W+1
         const int td = t - W + 1;
-        bstore_vals<T, kWideCpl, true>(row_rsrc(dxs, D, td, td >= t0 && td < t1, rowb), xlo, dxr[q]);
+        bstore_vals<T, CPL, true>(row_rsrc(dxs, D, td, td >= t0 && td < t1, rowb), xlo, dxr[q]);
 #pragma unroll
-        for (int j = 0; j < kWideCpl; ++j) dxr[q][j] = 0.f;
+        for (int j = 0; j < CPL; ++j) dxr[q][j] = 0.f;
       }
 
       // dweight row t: products dy[t] * x[t-k] summed over the head's channels
@@ -382,13 +398,26 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
         for (int k = 0; k < W; ++k) {
           const int q = ((u - k) % M + M) % M;
 #pragma unroll
-          for (int j = 0; j < kWideCpl; ++j) put(we0 + j * W + k, dym[j] * xf[q][j]);
+          for (int j = 0; j < CPL; ++j) put(we0 + j * W + k, dym[j] * xf[q][j]);
         }
-      } else if constexpr (LPH == 1) {  // head size 2: the lane's head is its own
+      } else if constexpr (LPH == 1) {  // a head per lane (head size CPL): the lane's head is its own
 #pragma unroll
         for (int k = 0; k < W; ++k) {
           const int q = ((u - k) % M + M) % M;
-          put(we0 + k, fmaf(dym[1], xf[q][1], dym[0] * xf[q][0]));
+          put(we0 + k, lane_sum(dym, xf[q]));
+        }
+      } else if constexpr (LPH < 0) {
+        // run-time group of a.lph lanes (DPP steps selected by it, no branch);
+        // the head's first lane puts the sums
+        float v[W];
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          const int q = ((u - k) % M + M) % M;
+          v[k] = group_sum_sel(lane_sum(dym, xf[q]), a.lph);
+        }
+        if ((lane & (a.lph - 1)) == 0) {
+#pragma unroll
+          for (int k = 0; k < W; ++k) put(we0 + k, v[k]);
         }
       } else {
         // head sums over LPH lanes of the lanes' two-channel sums (DPP butterflies, ds_bpermute
@@ -397,7 +426,7 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
 #pragma unroll
         for (int k = 0; k < W; ++k) {
           const int q = ((u - k) % M + M) % M;
-          v[k] = group_sum<LPH>(fmaf(dym[1], xf[q][1], dym[0] * xf[q][0]));
+          v[k] = group_sum<LPH>(lane_sum(dym, xf[q]));
         }
         if ((lane & (LPH - 1)) == 0) {
 #pragma unroll
@@ -413,14 +442,12 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
 #pragma unroll
         for (int k = 0; k < W; ++k) {
           const int q = ((u - k) % M + M) % M;
-          if constexpr (WIDE_ST) {
-            float2 v = dsl[k * 64];
-            v.x = fmaf(dym[0], xf[q][0], v.x);
-            v.y = fmaf(dym[1], xf[q][1], v.y);
-            dsl[k * 64] = v;
-          } else {
-            dsw[k][0] = fmaf(dym[0], xf[q][0], dsw[k][0]);
-            dsw[k][1] = fmaf(dym[1], xf[q][1], dsw[k][1]);
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) {
+            if constexpr (WIDE_ST)
+              dsl[k * COLS + j] = fmaf(dym[j], xf[q][j], dsl[k * COLS + j]);
+            else
+              dsw[k][j] = fmaf(dym[j], xf[q][j], dsw[k][j]);
           }
         }
       }
@@ -433,54 +460,64 @@ __global__ __launch_bounds__(256) void hw_bwd_wide(const T* __restrict__ x, cons
     // per workgroup row: part[sgp][k * D + channel]
     if constexpr (!WIDE_ST) {
 #pragma unroll
-      for (int k = 0; k < W; ++k) dsl[k * 64] = make_float2(dsw[k][0], dsw[k][1]);
+      for (int k = 0; k < W; ++k)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) dsl[k * COLS + j] = dsw[k][j];
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < W * kWideCols; e += 256) {
+    for (int e = threadIdx.x; e < W * COLS; e += 256) {
       const float v = ((dsr[0][e] + dsr[1][e]) + dsr[2][e]) + dsr[3][e];
-      const int k = e / kWideCols, cc = e - k * kWideCols;
-      part[(int64_t)sgp * W * D + (int64_t)k * D + wc * kWideCols + cc] = v;
+      const int k = e / COLS, cc = e - k * COLS;
+      part[(int64_t)sgp * W * D + (int64_t)k * D + wc * COLS + cc] = v;
     }
   }
 }
 
 // ------------------------------------------------------------------ launch
-template <typename T, int W, bool H1, bool ST>
+template <typename T, int W, int CPL, bool H1, bool ST>
 hipError_t launch_hw_fwd_wide(const HwProblem& p, const HwWideArgs& a) {
-  hw_fwd_wide<T, W, H1, ST><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.weight, (const T*)p.static_w,
-                                                          (T*)p.y, a);
+  hw_fwd_wide<T, W, CPL, H1, ST><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.weight,
+                                                               (const T*)p.static_w, (T*)p.y, a);
   return hipGetLastError();
 }
 
-template <typename T, int W, int LPH, bool ST>
+template <typename T, int W, int CPL, int LPH, bool ST>
 hipError_t launch_hw_bwd_wide(const HwProblem& p, const HwWideArgs& a) {
-  hw_bwd_wide<T, W, LPH, ST><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.weight, (const T*)p.static_w,
-                                                           (const T*)p.dy, (T*)p.dx, (T*)p.dweight, p.ws, a);
+  hw_bwd_wide<T, W, CPL, LPH, ST><<<a.nblk, 256, 0, p.stream>>>((const T*)p.x, (const T*)p.weight,
+                                                                (const T*)p.static_w, (const T*)p.dy, (T*)p.dx,
+                                                                (T*)p.dweight, p.ws, a);
   return hipGetLastError();
 }
 
-template <typename T, int W, int LPH>
+template <typename T, int W, int CPL, int LPH>
 hipError_t launch_hw_bwd_wide_s(const HwProblem& p, const HwWideArgs& a) {
-  return p.static_w ? launch_hw_bwd_wide<T, W, LPH, true>(p, a) : launch_hw_bwd_wide<T, W, LPH, false>(p, a);
+  return p.static_w ? launch_hw_bwd_wide<T, W, CPL, LPH, true>(p, a) : launch_hw_bwd_wide<T, W, CPL, LPH, false>(p, a);
 }
 
+// Up to W 16: two channels per lane, head sums over compile-time lane groups;
+// above: one channel per lane, head sums over the run-time group a.lph.
 template <typename T, bool BWD, int W>
 hipError_t launch_hw_wide_w(const HwProblem& p, const HwWideArgs& a) {
   const bool st = p.static_w != nullptr;
-  if constexpr (!BWD) {
+  if constexpr (W > kWideCplMaxW) {
+    if constexpr (!BWD)
+      return st ? launch_hw_fwd_wide<T, W, 1, false, true>(p, a) : launch_hw_fwd_wide<T, W, 1, false, false>(p, a);
+    else
+      return launch_hw_bwd_wide_s<T, W, 1, -1>(p, a);
+  } else if constexpr (!BWD) {
     if (a.hs_shift == 0)
-      return st ? launch_hw_fwd_wide<T, W, true, true>(p, a) : launch_hw_fwd_wide<T, W, true, false>(p, a);
-    return st ? launch_hw_fwd_wide<T, W, false, true>(p, a) : launch_hw_fwd_wide<T, W, false, false>(p, a);
+      return st ? launch_hw_fwd_wide<T, W, 2, true, true>(p, a) : launch_hw_fwd_wide<T, W, 2, true, false>(p, a);
+    return st ? launch_hw_fwd_wide<T, W, 2, false, true>(p, a) : launch_hw_fwd_wide<T, W, 2, false, false>(p, a);
   } else {
     switch (a.hs_shift) {  // lanes per head: head size / 2 (a lane holds two channels)
-      case 0: return launch_hw_bwd_wide_s<T, W, 0>(p, a);
-      case 1: return launch_hw_bwd_wide_s<T, W, 1>(p, a);
-      case 2: return launch_hw_bwd_wide_s<T, W, 2>(p, a);
-      case 3: return launch_hw_bwd_wide_s<T, W, 4>(p, a);
-      case 4: return launch_hw_bwd_wide_s<T, W, 8>(p, a);
-      case 5: return launch_hw_bwd_wide_s<T, W, 16>(p, a);
-      case 6: return launch_hw_bwd_wide_s<T, W, 32>(p, a);
-      default: return launch_hw_bwd_wide_s<T, W, 64>(p, a);
+      case 0: return launch_hw_bwd_wide_s<T, W, 2, 0>(p, a);
+      case 1: return launch_hw_bwd_wide_s<T, W, 2, 1>(p, a);
+      case 2: return launch_hw_bwd_wide_s<T, W, 2, 2>(p, a);
+      case 3: return launch_hw_bwd_wide_s<T, W, 2, 4>(p, a);
+      case 4: return launch_hw_bwd_wide_s<T, W, 2, 8>(p, a);
+      case 5: return launch_hw_bwd_wide_s<T, W, 2, 16>(p, a);
+      case 6: return launch_hw_bwd_wide_s<T, W, 2, 32>(p, a);
+      default: return launch_hw_bwd_wide_s<T, W, 2, 64>(p, a);
     }
   }
 }
@@ -490,14 +527,13 @@ hipError_t launch_hw_wide_w(const HwProblem& p, const HwWideArgs& a) {
 template <typename T, bool BWD>
 hipError_t dispatch_wide(const HwProblem& p, const HwWideArgs& a) {
   switch (p.W) {
-    case 9: return launch_hw_wide_w<T, BWD, 9>(p, a);
-    case 10: return launch_hw_wide_w<T, BWD, 10>(p, a);
-    case 11: return launch_hw_wide_w<T, BWD, 11>(p, a);
-    case 12: return launch_hw_wide_w<T, BWD, 12>(p, a);
-    case 13: return launch_hw_wide_w<T, BWD, 13>(p, a);
-    case 14: return launch_hw_wide_w<T, BWD, 14>(p, a);
-    case 15: return launch_hw_wide_w<T, BWD, 15>(p, a);
-    case 16: return launch_hw_wide_w<T, BWD, 16>(p, a);
+#define DC_HW_WIDE(WW) \
+  case WW: return launch_hw_wide_w<T, BWD, WW>(p, a);
+    DC_HW_WIDE(9) DC_HW_WIDE(10) DC_HW_WIDE(11) DC_HW_WIDE(12) DC_HW_WIDE(13) DC_HW_WIDE(14) DC_HW_WIDE(15)
+    DC_HW_WIDE(16) DC_HW_WIDE(17) DC_HW_WIDE(18) DC_HW_WIDE(19) DC_HW_WIDE(20) DC_HW_WIDE(21) DC_HW_WIDE(22)
+    DC_HW_WIDE(23) DC_HW_WIDE(24) DC_HW_WIDE(25) DC_HW_WIDE(26) DC_HW_WIDE(27) DC_HW_WIDE(28) DC_HW_WIDE(29)
+    DC_HW_WIDE(30) DC_HW_WIDE(31) DC_HW_WIDE(32)
+#undef DC_HW_WIDE
     default: return hipErrorInvalidValue;
   }
 }

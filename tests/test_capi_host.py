@@ -268,6 +268,8 @@ def test_kernel_paths(lib):
         assert hp(1, 50, 64, 16, 12, bf, 1, bwd) == 0          # W 12, D 64: generic
         assert hp(4, 4096, 2048, 2048, 12, bf, 1, bwd) == 5    # W 12, head size 1: wide
         assert hp(4, 4096, 2048, 64, 16, f32, 0, bwd) == 5     # W 16, head size 32: wide
+        assert hp(4, 4096, 2048, 64, 24, bf, 1, bwd) == 5      # W 24: wide, one channel per lane
+        assert hp(1, 50, 96, 96, 20, bf, 1, bwd) == 0          # W 20, D % 64 != 0: generic
         assert hp(1, 50, 256, 2, 9, bf, 1, bwd) == 0           # head size 128, W 9: 18-byte segments
         assert lp(1, 45, 64, 127, 12, bf, 1, bwd) == 0         # W 12, kernel rank 128: generic
         assert lp(1, 70, 128, 64, 1, bf, 0, bwd) == 2          # kernel rank 64, W 1

@@ -137,7 +137,15 @@ HW_EDGE = [
     # row-ring kernels when D % 128 == 0 and a head lies in one wavefront, else the generic ones
     (1, 50, 64, 16, 12, True, True, torch.bfloat16),   # W 12, D 64: generic
     (2, 40, 128, 128, 16, True, False, torch.float32),  # W 16, head size 1: wide
-    (1, 10, 64, 32, 32, True, True, torch.bfloat16),   # W 32 (the maximum) > T: generic
+    (1, 10, 64, 32, 32, True, True, torch.bfloat16),   # W 32 (the maximum) > T: wide, one channel per lane
+    # 17 <= W <= 32: one channel per lane (64-channel wavefronts), head sums over a run-time group
+    (2, 77, 128, 128, 17, True, True, torch.bfloat16),  # hs 1
+    (1, 100, 256, 64, 20, False, True, torch.float16),  # hs 4
+    (2, 61, 256, 8, 24, True, False, torch.float32),    # hs 32
+    (1, 130, 128, 2, 32, True, True, torch.bfloat16),   # hs 64: a head is a whole wavefront
+    (1, 90, 128, 64, 25, True, True, torch.bfloat16),   # hs 2, odd W
+    (1, 1, 64, 16, 28, True, True, torch.float16),      # T 1
+    (1, 50, 96, 96, 20, True, True, torch.bfloat16),    # D % 64 != 0: generic
     (2, 77, 256, 256, 9, True, True, torch.bfloat16),   # wide: hs 1, odd W (ring of W + 1 rows)
     (1, 100, 128, 64, 10, False, True, torch.float16),  # wide: hs 2
     (2, 61, 384, 96, 11, True, False, torch.float32),   # wide: hs 4, three wavefront columns
@@ -215,13 +223,14 @@ def _hw_vector_shape(Dn, H, dtype):
 
 
 def _hw_wide_shape(Dn, H, W, dtype):
-    """Shapes the headwise wide kernels take (contiguous, aligned tensors): 9 <= W <= 16, D a multiple
-    of 128 (a wavefront's 2-channel lanes), a power-of-two head size of at most 128, and weight-row
-    segments (a wavefront's heads, and a whole row) of whole 16-byte pieces."""
+    """Shapes the headwise wide kernels take (contiguous, aligned tensors): 9 <= W <= 32, D a multiple
+    of a wavefront's channels (128: two per lane up to W 16; 64 above), a power-of-two head size of at
+    most that, and weight-row segments (a wavefront's heads, and a whole row) of whole 16-byte pieces."""
     es = torch.tensor([], dtype=dtype).element_size()
     hs = Dn // H
-    return (9 <= W <= 16 and Dn % 128 == 0 and hs & (hs - 1) == 0 and hs <= 128
-            and (128 // hs) * W * es % 16 == 0 and H * W * es % 16 == 0)
+    cols = 128 if W <= 16 else 64
+    return (9 <= W <= 32 and Dn % cols == 0 and hs & (hs - 1) == 0 and hs <= cols
+            and (cols // hs) * W * es % 16 == 0 and H * W * es % 16 == 0)
 
 
 def _path(kind, Bn, Tn, Dn, HR, W, dtype, static, bwd):

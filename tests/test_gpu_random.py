@@ -97,16 +97,16 @@ def _lowrank_widew_case(i):
 
 
 def _headwise_wide_case(i):
-    """9 <= W <= 16 with D a multiple of 128 and power-of-two head sizes up to 128: the wide
-    row-ring kernels (rings of W or W + 1 rows, weight segments staged through LDS), or the
-    generic ones where a wavefront's weight segment is not whole 16-byte pieces."""
+    """9 <= W <= 32 with D a multiple of 128 and power-of-two head sizes up to 128: the wide
+    row-ring kernels (two channels per lane up to W 16, one above; weight segments staged through
+    LDS), or the generic ones where a wavefront's weight segment is not whole 16-byte pieces."""
     rnd = random.Random(3571 * i + 11)
     dtype = rnd.choice(DTYPES)
     Bn = rnd.randint(1, 3)
     Tn = rnd.choice([1, 2, 9, 16, 17, 33, 64, 100, 129, 300])
     Dn = rnd.choice([128, 256, 384, 640])
     hs = rnd.choice([h for h in (1, 2, 4, 8, 16, 32, 64, 128) if Dn % h == 0])
-    W = rnd.randint(9, 16)
+    W = rnd.randint(9, 32)
     static = rnd.random() < 0.5
     residual = rnd.random() < 0.5
     return Bn, Tn, Dn, Dn // hs, W, static, residual, dtype

@@ -23,7 +23,8 @@ SEQUENCES = [
     [(4, 1024, 2048, 64, 4, True, True), (2, 300, 512, 512, 3, True, False)],   # vector kernels
     [(2, 500, 1024, 1024, 4, True, True), (1, 77, 96, 32, 5, True, True)],     # then head size 3: generic
     [(2, 256, 512, 16, 4, False, True), (1, 64, 256, 8, 2, False, False)],     # no static_w: no scratch
-    [(2, 300, 512, 512, 12, True, True), (1, 70, 256, 8, 9, True, False)],     # W 9-16: wide kernels
+    [(2, 300, 512, 512, 12, True, True), (1, 70, 256, 8, 9, True, False),      # W 9-32: wide kernels
+     (1, 50, 128, 32, 24, True, True)],
 ]
 
 
