@@ -67,6 +67,8 @@ CASES = {
     "lr_r31s_w8": _lr_case(1, 200, 256, 31, 8, True, torch.bfloat16),       # two passes of taps
     "lr_r16_fp32": _lr_case(2, 300, 256, 16, 4, False, torch.float32),
     "lr_grouped_hd64": _grouped_case(3, 2, 200, 128, 15, 4, 64, torch.bfloat16),
+    "lr_r15s_w20": _lr_case(1, 200, 256, 15, 20, True, torch.bfloat16),     # forward passes, fp32 dx rounded once
+    "hw_hs4_w24": _hw_case(1, 200, 256, 64, 24, True, torch.bfloat16),      # wide kernels, one channel per lane
 }
 
 

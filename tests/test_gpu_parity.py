@@ -597,10 +597,15 @@ def test_lowrank_inference_forward(R, static, W, dtype):
 
 
 # ------------------------------------------------------------ determinism
-@pytest.mark.parametrize("kind", ["hw1", "hw32", "lr16s"])
+@pytest.mark.parametrize("kind", ["hw1", "hw32", "lr16s", "hw32w12", "hw4w24", "lr16sw20"])
 def test_deterministic(kind):
+    """Two runs give bitwise equal outputs and gradients: no float atomics anywhere, partial sums in a
+    fixed order (W 12 / 24: the wide headwise kernels; lowrank W 20: passes of taps into the fp32 dx
+    accumulator)."""
     g = gen(5)
-    Bn, Tn, Dn, W = 2, 1024, 512, 4
+    Bn, Tn, Dn = 2, 1024, 512
+    W = int(kind.split("w")[-1]) if "w" in kind else 4
+    kind = kind.split("w")[0]
     x = randn(g, Bn, Tn, Dn).to(torch.bfloat16).to(DEV)
     dy = randn(g, Bn, Tn, Dn).to(torch.bfloat16).to(DEV)
     sw = randn(g, W, Dn, scale=0.3).to(torch.bfloat16).to(DEV)
