@@ -752,7 +752,7 @@ hipError_t launch_f32m_pass(const LrProblem& p, LrF32mBwdArgs a, const float* U,
 template <int W>
 hipError_t launch_f32m_taps(const LrProblem& p, const LrF32mBwdArgs& a, const float* U, const float* sw, float* pdz,
                             float* pdu) {
-  // kernel ranks 1-16: one pass; 17-32: ranks 0-15, then the rest
+  // kernel ranks 1-16: one pass; above: passes of 16 ranks (0-15, 16-31, ...)
   for (int rofs = 0; rofs < a.RK; rofs += 16) {
     const int nr = a.RK - rofs < 16 ? a.RK - rofs : 16;  // ranks of this pass
     const int nkb = (nr + 3) / 4;
@@ -800,15 +800,15 @@ hipError_t launch_f32m_bwd(const LrProblem& p) {
 
 }  // namespace
 
-// fp32, 2 <= W <= 32 (above 4 as passes of 2-4 taps), kernel rank <= 32 (above
-// 16 as two rank passes); D, x / dx row strides multiples of 4
+// fp32, 2 <= W <= 32 (above 4 as passes of 2-4 taps), kernel rank <= 64 (above
+// 16 as rank passes of 16); D, x / dx row strides multiples of 4
 // (8-byte lane pieces, 16-byte operand pieces); dy's head dim a multiple of 32
 // (a chunk inside one head); 16-byte aligned x, dy, dx, U, static_w; sequences
 // of any length (runs capped by f32m_bwd_max_run_tiles).
 bool lr_f32m_bwd_ok(const LrProblem& p) {
   if (p.dtype != kFP32) return false;
   if (p.W < 2 || p.W > 32) return false;
-  if (p.R + (p.static_w ? 1 : 0) > 32) return false;
+  if (p.R + (p.static_w ? 1 : 0) > 64) return false;
   if (p.D % 4 != 0 || p.xld() % 4 != 0 || p.dxld() % 4 != 0) return false;
   if (p.yhd() != p.D && p.yhd() % 32 != 0) return false;
   if (!aligned_to(p.x, 16) || !aligned_to(p.dy, 16) || !aligned_to(p.dx, 16) || !aligned_to(p.U, 16) ||
