@@ -70,8 +70,12 @@ struct LrProblem {
   int64_t u_ld;
   int kofs;
   int accy;
+  // z's row stride in elements (0: R): a pass over kernel ranks rofs .. of a
+  // wider problem reads z from column rofs of rows z_ld apart (fp32 forward)
+  int64_t z_ld;
   int64_t xld() const { return x_ld > 0 ? x_ld : D; }
   int64_t uld() const { return u_ld > 0 ? u_ld : W * D; }
+  int64_t zld() const { return z_ld > 0 ? z_ld : R; }
   int64_t dxld() const { return dx_ld > 0 ? dx_ld : D; }
   int64_t yhd() const { return y_hd > 0 ? y_hd : D; }
 };

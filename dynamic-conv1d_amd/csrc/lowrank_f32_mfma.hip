@@ -42,6 +42,7 @@ struct LrF32mArgs {
   int yhd;   // y layout: D ([B, T, D]) or the head dim of [B, D/yhd, T, yhd] (yhd % 4 == 0)
   int uld;   // row stride of U (elements): the problem's W * D, all taps
   int kofs;  // ACC pass: its first tap (x read kofs rows earlier)
+  int zld;   // row stride of z (elements): R, or the whole problem's for a pass of ranks
 };
 
 constexpr int kF32mMaxKb = 8;  // kernel rank <= 32
@@ -69,8 +70,12 @@ __global__ __launch_bounds__(256) void lr_fwd_f32m(const float* __restrict__ x, 
 
   // ---- stage the chunk's B operands (every rank row r < RK, zero beyond)
   {
-    // U rows uld elements apart; U may start at a later pass's tap kofs
-    const rsrc_t ru = make_rsrc(U, ((int64_t)R * a.uld - (int64_t)(ACC ? a.kofs : 0) * D) * 4);
+    // U rows uld elements apart; U may start at a later pass's tap kofs.  A pass
+    // of ranks may hold no dynamic rank (R == 0: the static rank alone), whose
+    // range is empty: R * uld - kofs * D would be negative there, and a negative
+    // record count wraps to a range that takes kOobLane in
+    const int64_t ubytes = R > 0 ? ((int64_t)R * a.uld - (int64_t)(ACC ? a.kofs : 0) * D) * 4 : 0;
+    const rsrc_t ru = make_rsrc(U, ubytes);
     const rsrc_t rs = make_rsrc(sw, sw ? (int64_t)W * D * 4 : 0);
     for (int kk = wave; kk < W * NKB; kk += 4) {
       const int k = kk / NKB, kb = kk - k * NKB;
@@ -104,7 +109,7 @@ __global__ __launch_bounds__(256) void lr_fwd_f32m(const float* __restrict__ x, 
   const int yh0 = chunk * 64 / yhd, yhl = min(chunk * 64 + 63, D - 1) / yhd;
   const rsrc_t rx = run_rsrc(x + rrow * a.xld, Tn - rb, xrowb);
   const rsrc_t ry = run_rsrc(y + row0 * D + ((int64_t)yh0 * Tn + rb) * yhd, (int64_t)(yhl - yh0) * Tn + Tn - rb, yrowb);
-  const rsrc_t rz = run_rsrc(z + rrow * R, Tn - rb, R * 4);
+  const rsrc_t rz = run_rsrc(z + rrow * a.zld, Tn - rb, a.zld * 4);
   const int xlane_off = chv ? (4 * q * a.xld + dl) * 4 : kOobLane;
   // y: the lane's piece lies in head yh (yhd % 4 == 0), rows yhd elements apart
   const int ylane_off = chv ? (((yh - yh0) * Tn + 4 * q) * yhd + dl - yh * yhd) * 4 : kOobLane;
@@ -117,7 +122,7 @@ __global__ __launch_bounds__(256) void lr_fwd_f32m(const float* __restrict__ x, 
       xr[m] = bload128(rx, xlane_off + (t0 - rb - (ACC ? a.kofs : 0)) * xrowb + (m - (W - 1)) * xrowb);
     // A operands: z_eff[t0+n, 4kb+q]; the static rank R is 1 inside the sequence
     float za[NKB];
-    const int zrow = (t0 + n - rb) * R * 4;
+    const int zrow = (t0 + n - rb) * a.zld * 4;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       const int r = 4 * kb + q;
@@ -552,7 +557,7 @@ int64_t f32m_fwd_max_run_tiles(const LrProblem& p) {
   const int64_t hd = p.yhd();
   int64_t rowb = p.xld() * 4;
   if (hd * 4 > rowb) rowb = hd * 4;
-  if (p.R * 4 > rowb) rowb = p.R * 4;
+  if (p.zld() * 4 > rowb) rowb = p.zld() * 4;  // z rows (a pass of ranks: the whole problem's)
   int64_t tiles = run_tiles_cap(rowb);
   if (hd != p.D) {
     const int64_t extra = (63 / hd + 1) * p.T * hd * 4;
@@ -599,6 +604,7 @@ LrF32mArgs make_f32m_args(const LrProblem& p) {
   a.yhd = (int)p.yhd();
   a.uld = (int)p.uld();
   a.kofs = p.kofs;
+  a.zld = (int)p.zld();
   return a;
 }
 
@@ -614,7 +620,8 @@ hipError_t lr_f32m_fwd_one(const LrProblem& p);
 
 }  // namespace
 
-// fp32, W <= 32 (above 8 as passes of taps), kernel rank <= 32, 16-byte pieces
+// fp32, W <= 32 (above 8 as passes of taps), kernel rank <= 64 (above 32 as
+// passes of ranks), 16-byte pieces
 // of x / y / U / static_w at every row (D, x row stride and head dim multiples
 // of 4, pointers 16-byte aligned); sequences of any length (runs capped by
 // f32m_fwd_max_run_tiles).
@@ -622,7 +629,7 @@ bool lr_f32m_fwd_ok(const LrProblem& p) {
   if (p.dtype != kFP32) return false;
   if (p.W < 1 || p.W > 32) return false;
   const int64_t rk = p.R + (p.static_w ? 1 : 0);
-  if (rk > 4 * kF32mMaxKb) return false;
+  if (rk > 2 * 4 * kF32mMaxKb) return false;
   if (p.D % 4 != 0 || p.xld() % 4 != 0 || p.yhd() % 4 != 0) return false;
   if (!aligned_to(p.x, 16) || !aligned_to(p.y, 16) || !aligned_to(p.U, 16) || !aligned_to(p.static_w, 16))
     return false;
@@ -632,16 +639,13 @@ bool lr_f32m_fwd_ok(const LrProblem& p) {
 
 namespace {
 
-// One launch of at most kF32mFwdPassTaps taps (accy: a later pass, W 8).
+// One launch of at most kF32mFwdPassTaps taps and 32 kernel ranks (accy: a
+// later pass of taps or ranks, added to the stored y).
 hipError_t lr_f32m_fwd_one(const LrProblem& p) {
   const int nkb = (int)((p.R + (p.static_w ? 1 : 0) + 3) / 4);
   const int kb = nkb <= 2 ? 2 : nkb <= 4 ? 4 : 8;  // rank steps, rounded up (zero steps add nothing)
-  if (p.accy) {
-    if (p.W != kF32mFwdPassTaps) return hipErrorInvalidValue;
-    return kb == 2 ? launch_f32m<8, 2, true>(p) : kb == 4 ? launch_f32m<8, 4, true>(p) : launch_f32m<8, 8, true>(p);
-  }
 #define DC_F32M_CASE(WW, KB) \
-  if (p.W == WW && kb == KB) return launch_f32m<WW, KB>(p);
+  if (p.W == WW && kb == KB) return p.accy ? launch_f32m<WW, KB, true>(p) : launch_f32m<WW, KB>(p);
   DC_F32M_CASE(1, 2) DC_F32M_CASE(1, 4) DC_F32M_CASE(1, 8)
   DC_F32M_CASE(2, 2) DC_F32M_CASE(2, 4) DC_F32M_CASE(2, 8)
   DC_F32M_CASE(3, 2) DC_F32M_CASE(3, 4) DC_F32M_CASE(3, 8)
@@ -656,10 +660,13 @@ hipError_t lr_f32m_fwd_one(const LrProblem& p) {
 
 }  // namespace
 
+namespace {
+
 // Above W 8: taps 0 .. W0-1 (W0 = W - 8(n-1)) as a W0-tap problem (residual
 // included), then passes of 8 taps added to the stored y; U keeps its row
-// stride W * D, a later pass's U and static_w start at its tap.
-hipError_t lr_f32m_fwd(const LrProblem& p) {
+// stride W * D, a later pass's U and static_w start at its tap.  p.accy: the
+// first pass adds to y as well (a later pass of ranks).
+hipError_t lr_f32m_fwd_taps(const LrProblem& p) {
   constexpr int P = kF32mFwdPassTaps;
   if (p.W <= P) return lr_f32m_fwd_one(p);
   const int W = (int)p.W, np = (W + P - 1) / P, w0 = W - (np - 1) * P;
@@ -678,6 +685,33 @@ hipError_t lr_f32m_fwd(const LrProblem& p) {
     a.static_w = p.static_w ? (const float*)p.static_w + (int64_t)kofs * p.D : nullptr;
     a.residual = 0;
     e = lr_f32m_fwd_one(a);
+  }
+  return e;
+}
+
+}  // namespace
+
+// Above kernel rank 32: passes of 32 kernel ranks (z columns rofs .. of rows
+// R apart, U rows rofs .., the static rank in the pass that holds index R),
+// each later one added to the stored y; each runs its passes of taps.
+hipError_t lr_f32m_fwd(const LrProblem& p) {
+  const int64_t RK = p.R + (p.static_w ? 1 : 0);
+  if (RK <= 32) return lr_f32m_fwd_taps(p);
+  hipError_t e = hipSuccess;
+  for (int64_t rofs = 0; rofs < RK && e == hipSuccess; rofs += 32) {
+    LrProblem a = p;
+    const int64_t rd = p.R - rofs;  // dynamic ranks from rofs on
+    a.R = rd < 0 ? 0 : rd > 32 ? 32 : rd;
+    a.static_w = p.static_w && rd < 32 ? p.static_w : nullptr;  // kernel rank R falls in this pass
+    a.z = (const float*)p.z + rofs;
+    a.z_ld = p.R;
+    a.U = (const float*)p.U + rofs * p.uld();
+    a.u_ld = p.uld();
+    if (rofs > 0) {
+      a.accy = 1;
+      a.residual = 0;
+    }
+    e = lr_f32m_fwd_taps(a);
   }
   return e;
 }

@@ -280,7 +280,7 @@ def test_kernel_paths(lib):
         assert lp(2, 8192, 4096, 31, 4, f32, 1, bwd) == 3      # as two rank passes on matrix cores
         assert lp(1, 100, 256, 32, 2, f32, 0, bwd) == 3
     assert lp(1, 100, 256, 33, 4, f32, 0, 1) == 3              # kernel rank 33: three rank passes
-    assert lp(1, 100, 256, 33, 4, f32, 0, 0) == 0              # its forward: the generic kernels
+    assert lp(1, 100, 256, 33, 4, f32, 0, 0) == 3              # its forward: two rank passes
     assert lp(1, 100, 256, 65, 4, f32, 0, 1) == 0              # kernel rank 65: the generic kernels
     for bwd in (0, 1):                                         # fp32 sequences past 512 MiB of rows:
         assert lp(1, 65600, 2048, 15, 4, f32, 1, bwd) == 3     # per-run buffer ranges

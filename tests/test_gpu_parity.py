@@ -266,8 +266,11 @@ LR_EDGE = [
     (1, 70, 128, 31, 4, True, True, torch.float32),     # kernel rank 32
     (2, 300, 64, 1, 1, False, True, torch.float32),     # rank 1, W 1
     (1, 9, 100, 7, 4, False, True, torch.float32),      # T below one run, D % 64 != 0
-    (1, 40, 64, 40, 4, False, False, torch.float32, ("generic", "f32_mfma")),    # kernel rank 40: 3 rank passes
-    (2, 100, 128, 63, 6, True, True, torch.float32, ("generic", "f32_mfma")),    # kernel rank 64, 3 + 3 taps
+    (1, 40, 64, 40, 4, False, False, torch.float32, ("f32_mfma", "f32_mfma")),   # kernel rank 40: rank passes
+    (2, 100, 128, 63, 6, True, True, torch.float32, ("f32_mfma", "f32_mfma")),   # kernel rank 64, 3 + 3 taps
+    # static rank alone in the second rank pass of the forward, W 12 (its later tap pass has no U rows:
+    # their buffer range must be empty, not negative)
+    (1, 60, 64, 32, 12, True, True, torch.float32, ("f32_mfma", "f32_mfma")),
     # fp32 kernel ranks 17-32: the matrix-core backward as two rank passes (ranks 0-15, then the
     # rest; the second pass adds its dx to the first's and its dz columns / dU rows are its own)
     (2, 300, 256, 31, 4, True, True, torch.float32, ("f32_mfma", "f32_mfma")),   # static rank in pass 2
