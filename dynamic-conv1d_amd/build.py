@@ -1,6 +1,6 @@
 """Build libdynconv.so (gfx950) in-tree with hipcc.
 
-    python dynamic-conv1d_amd/build.py [--jobs N] [--debug-host-asan]
+    python dynamic-conv1d_amd/build.py [--jobs N]
 
 Each csrc/*.hip translation unit is compiled in parallel to _build/*.o and
 linked into dynconv/libdynconv.so.  Always rebuilds (the driver's "does it

@@ -112,8 +112,25 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 // the default policy: with `nt` those lines are fetched again.
 constexpr int kNt = 2;
 
+// Largest byte range a resource is given: 1 GiB.  Every kernel's lane
+// out-of-range offset (1 << 30) lies at or past it, and the per-run resources
+// stay below 512 MiB, under their row out-of-range offsets (host-capped runs).
+// make_rsrc clamps the count into [0, MAX]: a negative count (an empty pass,
+// or a slip in an offset) gives an empty range, where an unclamped one would
+// wrap to a range of almost 4 GiB that takes the out-of-range offsets in.
+// The host plans keep every count inside [0, MAX] anyway; the clamp is the
+// backstop, and dc_lowrank_plan_ranges reports the counts for a test to check.
+constexpr int64_t kRsrcMaxBytes = int64_t(1) << 30;
+
+__host__ __device__ constexpr int64_t clamp_rsrc_bytes(int64_t bytes, int64_t max_bytes = kRsrcMaxBytes) {
+  return bytes < 0 ? 0 : bytes > max_bytes ? max_bytes : bytes;
+}
+
+template <int64_t MAX = kRsrcMaxBytes>
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+  static_assert(MAX > 0 && MAX < (int64_t(1) << 31), "a range the 32-bit record count holds");
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)clamp_rsrc_bytes(bytes, MAX),
+                                           0x00020000);
 }
 template <int POL = 0>
 __device__ __forceinline__ u32x4 bload128(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL); }

@@ -80,8 +80,8 @@ __global__ __launch_bounds__(256 * KS) void proj_fwd(ProjArgs a) {
   const int m0 = (blk * 4 + rt) * 16;
   const int rows = max(min(M - m0, 16), 0);
   // rows m0 .. m0+15 of pre_z: rows past M and K past the end read 0
-  const rsrc_t rp = make_rsrc(a.pre + (int64_t)max(min(m0, M), 0) * K, (int64_t)rows * K * 2);
-  const rsrc_t rw = make_rsrc(a.w, (int64_t)N * K * 2);
+  const rsrc_t rp = make_rsrc<kProjOob>(a.pre + (int64_t)max(min(m0, M), 0) * K, (int64_t)rows * K * 2);
+  const rsrc_t rw = make_rsrc<kProjOob>(a.w, (int64_t)N * K * 2);
   const int prow = n * K * 2;  // the lane's row in rp
 
   f32x4 acc[NB];
@@ -206,15 +206,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 6 ? 2
   const int tile0 = run * a.seg, tile1 = min(tile0 + a.seg, ntile);
   const int r0 = tile0 * 16;
   const int nrow = max(min(M - r0, (tile1 - tile0) * 16), 0);
-  const rsrc_t rp = make_rsrc(a.pre + (int64_t)min(r0, M) * K, (int64_t)nrow * K * 2);
-  const rsrc_t rd = make_rsrc(a.dpre + (int64_t)min(r0, M) * K, (int64_t)nrow * K * 2);
-  const int lane_off = chv ? (4 * q * K + col) * 2 : kProjOob;
+  const rsrc_t rp = make_rsrc<kProjOob>(a.pre + (int64_t)min(r0, M) * K, (int64_t)nrow * K * 2);
+  const rsrc_t rd = make_rsrc<kProjOob>(a.dpre + (int64_t)min(r0, M) * K, (int64_t)nrow * K * 2);
+  // the lane's row-4q channels in pre_z / dpre_z; lanes past K (chv false)
+  // take kProjOob alone, never kProjOob plus a row offset (that sum would
+  // overflow int32 and wrap back into the range)
+  const int lane_off = (4 * q * K + col) * 2;
 
   // W_in operands of the dpre_z product (B of v_mfma_f32_16x16x32, K = ranks):
   // step s, channel j: ranks 32s + 8q .. +7 of channel col + j, packed.
   u32x4 wop[N32][4];
   {
-    const rsrc_t rw = make_rsrc(a.w, (int64_t)N * K * 2);
+    const rsrc_t rw = make_rsrc<kProjOob>(a.w, (int64_t)N * K * 2);
 #pragma unroll
     for (int s = 0; s < N32; ++s) {
       u32x2 rows8[8];
@@ -268,9 +271,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 6 ? 2
   };
   // pre_z rows 4q .. 4q+3 of a tile, the lane's 4 channels (rows past the run read 0)
   auto load_pre = [&](int tile, u32x2(&pr)[4]) {
-    const int toff = tile < tile1 ? (tile - tile0) * 16 * K * 2 : kProjOob;
+    const bool live = chv && tile < tile1;
+    const int toff = (tile - tile0) * 16 * K * 2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pr[i] = bload64<kNt>(rp, lane_off + toff + i * K * 2);
+    for (int i = 0; i < 4; ++i) pr[i] = bload64<kNt>(rp, live ? lane_off + toff + i * K * 2 : kProjOob);
   };
 
   u32x2 pa[4], pb[4];
@@ -290,12 +294,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 6 ? 2
       for (int j = 0; j < 4; ++j) acc[j] = Mma32<T>::run(ar, wop[s][j], acc[j]);
     }
     // lane (q, n) now holds rows 4q .. 4q+3 of channels col .. col+3
-    const int toff = tile < tile1 ? (tile - tile0) * 16 * K * 2 : kProjOob;
+    const int toff = (tile - tile0) * 16 * K * 2;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = tile * 16 + 4 * q + i;
       const u32x2 o = {pack2<T>(acc[0][i], acc[1][i]), pack2<T>(acc[2][i], acc[3][i])};
-      bstore64<true>(o, rd, m < M ? lane_off + toff + i * K * 2 : kProjOob);
+      bstore64<true>(o, rd, chv && tile < tile1 && m < M ? lane_off + toff + i * K * 2 : kProjOob);
     }
     // dW_in += dz^T pre_z: A = dz^T (ranks 16c + n, rows 4q .. 4q+3), B = pre_z rows 4q .. 4q+3 of channel col + j
     u32x2 bop[4];
@@ -331,7 +335,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 6 ? 2
   }
 
   // dW_in partial of this run: rank 16c + 4q + i, channels col .. col+3
-  const rsrc_t rpart = make_rsrc(a.part + (int64_t)run * N * K, (int64_t)N * K * 4);
+  const rsrc_t rpart = make_rsrc<kProjOob>(a.part + (int64_t)run * N * K, (int64_t)N * K * 4);
 #pragma unroll
   for (int c = 0; c < NB; ++c)
 #pragma unroll
@@ -427,6 +431,8 @@ bool proj_shape_ok(const ProjProblem& p) {
   if (p.dtype != kBF16 && p.dtype != kFP16) return false;
   const int64_t N = p.G * p.R;
   if (N < 1 || N > 128 || p.K % 8 != 0) return false;
+  // row indices (tiles of 16, blocks of 64 rows) are int: m0 + 64 stays in range
+  if (p.M > INT32_MAX - 64) return false;
   // byte offsets within int32, below the out-of-range offset
   if ((int64_t)N * p.K * 4 >= kProjOob || 16 * p.K * 2 >= kProjOob) return false;
   const ProjBwdPlan pl = bwd_plan(p);

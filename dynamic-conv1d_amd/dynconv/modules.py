@@ -13,7 +13,9 @@ The proj_in GEMM (README.md:67, 75) runs on libdynconv.so's own matrix-core
 kernels (dc_proj_in_fwd / dc_proj_in_bwd): skinny products bound by streaming
 pre_z, which the library GEMM runs at about a quarter of HBM bandwidth in the
 backward.  Shapes those kernels do not take (fp32, G*R > 128, d_model % 8 != 0,
-non-contiguous pre_z) use torch's GEMM (F.linear).
+non-contiguous pre_z) use torch's GEMM (F.linear).  A proj_in that is not a
+plain bias-free nn.Linear (a subclass or wrapper in its place), one with hooks,
+and calls under autocast run the layer itself, as the reference module does.
 """
 
 import math
@@ -73,6 +75,28 @@ def _proj_in_native(pre_z, w_in, G, R) -> bool:
             and pre_z.data_ptr() % 16 == 0 and w_in.data_ptr() % 16 == 0)
 
 
+def _plain_linear(m: nn.Module) -> bool:
+    """Whether m is exactly an nn.Linear whose call is just F.linear(input, weight): no
+    subclass or wrapper in its place (adapters, quantised layers) and no hooks on it or
+    installed globally, so that calling the library kernel instead changes nothing a
+    caller could observe."""
+    return (type(m) is nn.Linear and m.bias is None and not m._forward_hooks and not m._forward_pre_hooks
+            and not m._backward_hooks and not getattr(m, "_backward_pre_hooks", None)
+            and not nn.modules.module._global_forward_hooks
+            and not nn.modules.module._global_forward_pre_hooks
+            and not nn.modules.module._global_backward_hooks)
+
+
+def _module_proj_in(layer: nn.Module, pre_z: torch.Tensor, G: int, R: int):
+    """The modules' z: the library's proj_in kernels when calling them is indistinguishable
+    from calling `layer` (a plain bias-free nn.Linear, no hooks, autocast off), else the
+    layer itself, as the reference module does (README.md:67, 75)."""
+    if _plain_linear(layer) and not torch.is_autocast_enabled(pre_z.device.type):
+        return proj_in(pre_z, layer.weight, G, R)
+    z = layer(pre_z)
+    return tuple(z[..., g * R:(g + 1) * R].contiguous() for g in range(G))
+
+
 def proj_in(pre_z: torch.Tensor, w_in: torch.Tensor, G: int, R: int):
     """The modules' proj_in GEMM for G groups: a tuple of G contiguous [B, T, R] tensors,
     group g being pre_z @ w_in[g*R:(g+1)*R].T (README.md:67, 75)."""
@@ -101,7 +125,7 @@ class LowRankDynamicShortConvolution(nn.Module):
         nn.init.uniform_(self.proj_out_bias, -1.0 / math.sqrt(W), +1.0 / math.sqrt(W))
 
     def forward(self, x: torch.Tensor, pre_z: torch.Tensor) -> torch.Tensor:
-        (z,) = proj_in(pre_z, self.proj_in.weight, 1, self.R)
+        (z,) = _module_proj_in(self.proj_in, pre_z, 1, self.R)
         return lowrank_dynamic_convolution(
             x=x.contiguous(),
             z=z.contiguous(),
@@ -138,7 +162,7 @@ class GroupedLowRankDynamicShortConvolution(nn.Module):
 
     def forward(self, x: torch.Tensor, pre_z: torch.Tensor):
         G, R = self.groups, self.R
-        zs = list(proj_in(pre_z, self.proj_in.weight, G, R))  # one GEMM for every group
+        zs = list(_module_proj_in(self.proj_in, pre_z, G, R))  # one GEMM for every group
         Us = [self.proj_out[g] for g in range(G)]
         sws = [self.proj_out_bias[g] for g in range(G)]
         return lowrank_dynamic_convolution_grouped(x, zs, Us, static_w=sws, residual=True, head_dim=self.head_dim)

@@ -58,6 +58,56 @@ def assert_ns(a, b, dtype, name="", elementwise=True):
                                    atol=tol["atol"], rtol=tol["rtol"], msg=lambda m: f"{name}: {m}")
 
 
+def assert_ns_full(a, b, dtype, name="", elementwise=True, rows=4096):
+    """assert_ns over whole (possibly multi-GB) tensors without moving them to the CPU: the
+    norm-wise ratio and, when elementwise, |a - b| <= atol + rtol |b| for every entry, computed
+    on a's device in chunks of `rows` along dim 1 (dim 0 for 2-D tensors).  On failure, names
+    the worst entry."""
+    tol = NS_TOL[dtype]
+    a = a.detach()
+    b = b.detach().to(a.device)
+    assert a.shape == b.shape, f"{name}: shape {tuple(a.shape)} != {tuple(b.shape)}"
+    dim = 1 if a.dim() >= 3 else 0
+    n = a.shape[dim]
+    num = den = 0.0
+    worst, where = 0.0, None
+    for c0 in range(0, n, rows):
+        ac = a.narrow(dim, c0, min(rows, n - c0)).float()
+        bc = b.narrow(dim, c0, min(rows, n - c0)).float()
+        d = (ac - bc).abs()
+        num = max(num, d.max().item())
+        den = max(den, bc.abs().max().item())
+        if elementwise:
+            ratio = d / (tol["atol"] + tol["rtol"] * bc.abs())
+            r = ratio.max().item()
+            if r > worst:
+                i = int(ratio.argmax())
+                idx = [int(v) for v in torch.unravel_index(torch.tensor(i), ac.shape)]
+                idx[dim] += c0
+                worst, where = r, (idx, ac.flatten()[i].item(), bc.flatten()[i].item(), int((ratio > 1).sum()))
+    r = num / den if den > 0 else num
+    assert r <= tol["nrm"], f"{name}: max|a-b|/max|b| = {r:.3e} > {tol['nrm']:.1e}"
+    if elementwise and worst > 1.0:
+        idx, av, bv, nbad = where
+        raise AssertionError(f"{name}: |a-b| > {tol['atol']} + {tol['rtol']}|b| at {idx}: a={av:.6g} b={bv:.6g} "
+                             f"({worst:.3g}x the bound; {nbad}+ entries over it)")
+
+
+class fp32_matmul_exact:
+    """Context: torch's fp32 GEMMs at full fp32 precision (TF32 / reduced-precision paths off)."""
+
+    def __enter__(self):
+        self.prev = (torch.backends.cuda.matmul.allow_tf32, torch.get_float32_matmul_precision())
+        torch.backends.cuda.matmul.allow_tf32 = False
+        torch.set_float32_matmul_precision("highest")
+        return self
+
+    def __exit__(self, *exc):
+        torch.backends.cuda.matmul.allow_tf32 = self.prev[0]
+        torch.set_float32_matmul_precision(self.prev[1])
+        return False
+
+
 # Per-entry bound for the long reductions (lowrank dU, dz, dstatic_w; headwise
 # dstatic_w) against b, the float64 sum of the terms formed from the same
 # dtype-rounded inputs:

@@ -248,7 +248,7 @@ def test_readme_module_against_oracle():
     assert_ns(y, y_full, dtype, "y (fp32 z)")
     assert_ns(m.proj_in.weight.grad, wi.grad, dtype, "proj_in", elementwise=False)
     assert_ns(pre_z.grad, pz.grad, dtype, "d pre_z", elementwise=False)
-    # oracle: the same bf16 z (torch's GEMM), then the fp32 restatement of reference.py
+    # oracle: the same bf16 z (the layer's own GEMM), then the fp32 restatement of reference.py
     z = m.proj_in(pre_z).detach()
     xr = x.detach().float().cpu().requires_grad_()
     zr = z.float().cpu().requires_grad_()
@@ -267,8 +267,9 @@ def test_grouped_module_against_oracle(head_dim):
     """GroupedLowRankDynamicShortConvolution end to end against an fp32 CPU oracle of the whole module:
     z = pre_z @ proj_in.weight^T in fp32, then reference.py's lowrank operator per group on its slice of
     the fused q|k|v projection (README.md:57-83, 99-110).  Every gradient: the fused projection x, pre_z,
-    proj_in.weight, proj_out and proj_out_bias.  The kernel path rounds z to bf16 after torch's GEMM;
-    the oracle keeps it in fp32, so the checks are the north-star ones (2e-2)."""
+    proj_in.weight, proj_out and proj_out_bias.  The kernel path rounds z to bf16 after the library's
+    proj_in GEMM (dc_proj_in_fwd); the oracle keeps it in fp32, so the checks are the north-star ones
+    (2e-2)."""
     from dynconv import GroupedLowRankDynamicShortConvolution
 
     torch.manual_seed(3)
