@@ -107,8 +107,11 @@ EXTRA = {
     "lr_W20": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=20, static=False, residual=True),
     # W 12 at kernel rank 40 (three rank chunks): the forward as passes of 4 + 8 taps, the backward as six of 2
     "lr_W12_r40": dict(kind="lr", B=4, T=4096, D=2048, R=40, W=12, static=False, residual=True),
-    # a shape the fast kernels do not take (kernel rank above 64): the generic kernels, for their cost
-    "lr_r128_generic": dict(kind="lr", B=4, T=4096, D=2048, R=127, W=4, static=True, residual=True),
+    # kernel rank 128 (R 127 + static): the forward as two passes of 64 ranks, the backward as four
+    # passes of 32 (the generic kernels took 1.9 + 15.0 ms here), and rank 32 at the same shape for
+    # its bytes per microsecond
+    "lr_r128": dict(kind="lr", B=4, T=4096, D=2048, R=127, W=4, static=True, residual=True),
+    "lr_r32_b4": dict(kind="lr", B=4, T=4096, D=2048, R=31, W=4, static=True, residual=True),
     # the reference bench.py's own shapes (bench.py:7-12): head sizes 1, 4, 16 and rank 16, no static_w, no residual
     "ref_hw_hs1": dict(kind="hw", B=4, T=4096, D=2048, H=2048, W=4, static=False, residual=False),
     "ref_hw_hs4": dict(kind="hw", B=4, T=4096, D=2048, H=512, W=4, static=False, residual=False),

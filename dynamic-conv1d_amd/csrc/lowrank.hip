@@ -404,8 +404,13 @@ bool lr_mfma_ok(const LrProblem& p, bool bwd) {
   // at one or two rank chunks, above W 8 at three or four) as passes of taps;
   // the backward runs wide W x RC as passes of taps (the runs' 32-row halo
   // covers a pass's look-back)
-  const int64_t rc = (p.R + (p.static_w ? 1 : 0) + 15) / 16;
-  if (rc > 4) return false;
+  // above kernel rank 64 (up to 256) as passes of ranks: the forward as passes of
+  // 64 (each split into passes of at most 8 taps), at most kFwdMaxPasses of
+  // them in all, since y is rounded after each; the backward as passes of 32
+  // (any number: past four its dx goes to an fp32 accumulator)
+  const int64_t RK = p.R + (p.static_w ? 1 : 0);
+  if (RK > kLrMfmaMaxRank) return false;
+  if (!bwd && lr_fwd_npasses(p) > kFwdMaxPasses) return false;
   // buffer-offset range of a run (resources start at each run's base row, so
   // the sequence length is free): at least one tile must fit
   if ((bwd ? lr_bwd_max_run_tiles(p) : lr_fwd_max_run_tiles(p)) < 1) return false;
@@ -427,6 +432,9 @@ int64_t lr_zeff_bytes(const LrProblem& p) {
   if (!lr_mfma_ok(p, true)) return 0;
   const bool has_static = p.static_w != nullptr;
   const int64_t rc = (p.R + (has_static ? 1 : 0) + 15) / 16;
+  // above kernel rank 64 the forward runs as passes of ranks and keeps no
+  // z_eff: the backward pads z itself (one small launch next to its passes)
+  if (rc > 4) return 0;
   // the backward reads z itself when its rows are what the kernel loads: R % 4
   // == 0 (8-byte loads) or, for two rank chunks, exactly 32 dynamic ranks
   const bool pad = rc == 2 ? !(p.R == 32 && !has_static) : p.R % 4 != 0;

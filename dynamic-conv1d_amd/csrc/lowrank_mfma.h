@@ -114,11 +114,34 @@ constexpr int kOobTile = (int)kMaxSeqBytes;
 constexpr int kRunHaloRows = 32;
 __device__ __forceinline__ int run_base_row(int tile0) { return max(tile0 * 16 - kRunHaloRows, 0); }
 
+// Byte counts of the per-pass (not per-run) buffer resources of the matrix-core
+// lowrank kernels, as the kernels compute them; the host audit
+// (dc_lowrank_plan_ranges) evaluates the same functions over every pass of a
+// launch plan.  U rows from tap kofs of a pass of R dynamic ranks (rows uld
+// elements apart, the pointer at row 0, tap kofs): R rows end kofs * D
+// elements before R * uld; none when R == 0 (a pass of the static rank alone).
+__host__ __device__ inline int64_t lr_u_bytes(int R, int64_t uld, int kofs, int64_t D, int es) {
+  return R > 0 ? ((int64_t)R * uld - (int64_t)kofs * D) * es : 0;
+}
+// static_w from tap kofs: the pass's W taps of D elements (none without the static rank).
+__host__ __device__ inline int64_t lr_sw_bytes(bool has, int W, int64_t D, int es) {
+  return has ? (int64_t)W * D * es : 0;
+}
+// One dU partial of the backward from its pass's first rank row and tap kofs:
+// RK rows of uld floats, less the kofs * D columns before the pointer.
+__host__ __device__ inline int64_t lr_dupart_bytes(int RK, int64_t uld, int kofs, int64_t D) {
+  return ((int64_t)RK * uld - (int64_t)kofs * D) * 4;
+}
+// A run resource (run_rsrc): nrows rows of rowb bytes, capped.
+__host__ __device__ inline int64_t run_rsrc_bytes(int64_t nrows, int64_t rowb) {
+  const int64_t bytes = nrows * rowb, cap = kMaxSeqBytes - kSeqSlackRows * rowb;
+  return bytes < cap ? bytes : cap;
+}
+
 // Resource over rows [rb, rb + nrows) of `rowb` bytes each, starting at p (row
 // rb), capped so that kOobTile less 15 rows stays out of range.
 __device__ __forceinline__ rsrc_t run_rsrc(const void* p, int64_t nrows, int64_t rowb) {
-  const int64_t bytes = nrows * rowb, cap = kMaxSeqBytes - kSeqSlackRows * rowb;
-  return make_rsrc(p, bytes < cap ? bytes : cap);
+  return make_rsrc(p, run_rsrc_bytes(nrows, rowb));
 }
 
 // A operands of a 16-row tile: z_eff[t, 16c+4q .. 16c+4q+3] for c < RC, where
@@ -183,11 +206,17 @@ inline int64_t run_tiles_cap(int64_t rowb) {
 }
 
 // Ranks per row of the backward's padded z_eff copy: the kernel rank RK rounded
-// up to 4, or 32 for two rank chunks (17 <= RK <= 32).
+// up to 4, or 32 for two rank chunks (17 <= RK <= 32), or above 64 up to 32.
 inline int64_t lr_bwd_zrow(int64_t R, bool has_static) {
   const int64_t rk = R + (has_static ? 1 : 0);
+  // above 64: passes of 32 ranks, each reading 32 of the row's ranks (16 bytes per lane)
+  if (rk > 64) return (rk + 31) / 32 * 32;
   return rk > 16 && rk <= 32 ? 32 : (rk + 3) / 4 * 4;
 }
+
+// Largest kernel rank (R + static) of the matrix-core kernels: above 64 they
+// run as passes of ranks.
+constexpr int kLrMfmaMaxRank = 256;
 
 // Field f of group g's entry in a kernel-argument table, by selects on the
 // wave-uniform g (no dynamic indexing of the argument block).
@@ -201,6 +230,30 @@ __device__ __forceinline__ F pick(const S (&a)[kMaxGroups], int g, F S::*f) {
 // fit the buffer resources (0: not even one tile; the generic kernels take p).
 int64_t lr_fwd_max_run_tiles(const LrProblem& p);
 int64_t lr_bwd_max_run_tiles(const LrProblem& p);
+
+// Passes of the matrix-core forward (lowrank_mfma_fwd.hip, fwd_plan): kernel
+// ranks rofs .. rofs+RK-1 (R of them dynamic) and taps kofs .. kofs+W-1;
+// accy: add to the y the earlier passes stored.  Above kernel rank
+// kFwdRankPass the ranks run as passes of that many.  lr_mfma_ok admits at
+// most kFwdMaxPasses passes: y is rounded to the output type after each.
+struct FwdPass {
+  int rofs, R, RK, kofs, W;
+  bool accy;
+};
+constexpr int kFwdRankPass = 64;
+constexpr int kFwdMaxPasses = 4;
+constexpr int kFwdMaxPlan = 64;  // room for every W <= 32, kernel rank <= 256 plan (rejected past kFwdMaxPasses)
+int fwd_plan(const LrProblem& p, FwdPass* out);  // number of passes, or -1
+int lr_fwd_npasses(const LrProblem& p);
+
+// Passes of the matrix-core backward (lowrank_mfma_bwd.hip, bwd_plan): kernel
+// ranks rofs .. rofs+RK-1 (R dynamic) and taps kofs .. kofs+W-1, dz partials in
+// slot `slot`.  Above kernel rank 64 the ranks run as passes of 32.
+struct BwdPass {
+  int rofs, R, RK, kofs, W, slot;
+};
+constexpr int kBwdMaxPlan = 8 * 32;  // kernel rank 256 (8 passes of ranks) x W 32 (up to 32 passes of taps)
+int bwd_plan(const LrProblem& p, BwdPass* out);  // number of passes, or -1
 
 // Host entry points of the two MFMA translation units.
 hipError_t lr_mfma_fwd(const LrProblem* p, int G);

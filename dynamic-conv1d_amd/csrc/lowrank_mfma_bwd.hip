@@ -93,6 +93,12 @@ struct LrBwdArgs {
   int uld;    // row stride of U and of the dU partials: the problem's W * D (all taps)
   int kofs;   // first tap of this pass (0 without a tap split)
   int accdx;  // add dx to what an earlier pass stored
+  // A pass of ranks writes its dz and dU partial entries into the whole
+  // problem's layout: dz partial rows dzld (its R) floats apart (part_dz starts
+  // at the pass's first rank), dU partials of dupr (its kernel rank) rows each
+  // (part_du starts at the pass's first rank row).  Without rank passes dzld = R
+  // and dupr = RK.
+  int dzld, dupr;
   int64_t BT;
   LrBwdGroup grp[kMaxGroups];
 };
@@ -137,17 +143,17 @@ template <int W, int RC, bool UWREG, int NJ, int NS, bool STAGE_UW = true>
 __device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds,
                                            u32x2 (&uw_reg)[UWREG && STAGE_UW ? W * RC * NJ : 1],
                                            u32x4* __restrict__ uz_lds, const uint16_t* __restrict__ U,
-                                           const uint16_t* __restrict__ sw, int R, int RK, int D, int uld, int d0,
-                                           int q, int n, int lane) {
+                                           const uint16_t* __restrict__ sw, int R, int RK, int D, int uld, int kofs,
+                                           int d0, int q, int n, int lane) {
   typedef LaneVec<NJ> LV;
   // U rows are uld elements apart (the whole problem's W*D: a pass of taps
-  // starts U at its first tap's columns); R * uld * 2 bytes lie below kOobLane
-  // (host check).  sw starts at the pass's first tap too.
+  // starts U at its first tap's columns, so R rows end kofs * D elements
+  // before R * uld); below kOobLane (host check).  sw starts at the pass's first tap too.
   const int WD = uld;
   // Buffer loads, all issued before the first use: rows r >= R of U and lanes
   // outside D read 0; the static row (r == R < RK) is read from sw and OR-ed in.
-  const rsrc_t ru = make_rsrc(U, (int64_t)R * WD * 2);
-  const rsrc_t rs = make_rsrc(sw, RK > R ? (int64_t)W * D * 2 : 0);
+  const rsrc_t ru = make_rsrc(U, lr_u_bytes(R, WD, kofs, D, 2));
+  const rsrc_t rs = make_rsrc(sw, lr_sw_bytes(RK > R, W, D, 2));
   const int cw = d0 + NJ * n < D ? (d0 + NJ * n) * 2 : kOobLane;  // the lane's tap-weight channels
   typename LV::type rows[W][RC][4];
   u32x4 zr[W][RC][NS];
@@ -197,12 +203,12 @@ __device__ __forceinline__ void stage_uops(u32x2* __restrict__ uw_lds,
 // whose A is z_eff row n, ranks 8q..8q+7).  Row R (< RK) is static_w.
 template <int W, int NJ>
 __device__ __forceinline__ void stage_uw32(u32x4 (&uw)[W * NJ], const uint16_t* __restrict__ U,
-                                           const uint16_t* __restrict__ sw, int R, int RK, int D, int uld, int d0,
-                                           int q, int n) {
+                                           const uint16_t* __restrict__ sw, int R, int RK, int D, int uld, int kofs,
+                                           int d0, int q, int n) {
   typedef LaneVec<NJ> LV;
   const int WD = uld;  // U row stride (see stage_uops)
-  const rsrc_t ru = make_rsrc(U, (int64_t)R * WD * 2);
-  const rsrc_t rs = make_rsrc(sw, RK > R ? (int64_t)W * D * 2 : 0);
+  const rsrc_t ru = make_rsrc(U, lr_u_bytes(R, WD, kofs, D, 2));
+  const rsrc_t rs = make_rsrc(sw, lr_sw_bytes(RK > R, W, D, 2));
   const int cw = d0 + NJ * n < D ? (d0 + NJ * n) * 2 : kOobLane;
   typename LV::type rows[W][8];
 #pragma unroll
@@ -692,7 +698,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
       for (int ri = 0; ri < NRW; ++ri) {
         const Run& ru = ri == 0 ? runs[0] : runs[NRW - 1];
         // rows of run ri from its base row; t >= T falls outside the resource
-        const rsrc_t rout = run_rsrc(part_dz + ((int64_t)cg * a.BT + ru.row0 + ru.rb) * R, Tn - ru.rb, R * 4);
+        const rsrc_t rout = run_rsrc(part_dz + ((int64_t)cg * a.BT + ru.row0 + ru.rb) * a.dzld, Tn - ru.rb, a.dzld * 4);
         const int tb = ru.tile0 + it - slot;  // run ri's tile of slot 0
 #pragma unroll
         for (int m = 0; m < DZB * PER_RUN / NTH; ++m) {
@@ -708,8 +714,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
           for (int w2 = 1; w2 < NCW; ++w2) v += dzred[buf][ri][w2][sl][pos];
           // slots past this batch (a short last batch), tiles past the run and ranks >= R store nothing
           const bool ok = sl <= slot && ti < ru.tile1 && r < R;
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rout, ok ? ((t - ru.rb) * R + r) * 4 : kOobLane, 0,
-                                                0);
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rout, ok ? ((t - ru.rb) * a.dzld + r) * 4 : kOobLane,
+                                                0, 0);
         }
       }
       __builtin_amdgcn_s_setprio(0);
@@ -721,8 +727,8 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   TileIn ta, tb;
   load_tile(tile0, ta);
   __builtin_amdgcn_sched_barrier(0);  // the first tile's loads go out before the U staging waits
-  stage_uops<W, RC, UWREG, NJ, NS, !K32>(my_uw, uw_reg, my_uz, U, sw, R, RK, D, a.uld, d0, q, n, lane);
-  if constexpr (K32) stage_uw32<W, NJ>(uw32, U, sw, R, RK, D, a.uld, d0, q, n);
+  stage_uops<W, RC, UWREG, NJ, NS, !K32>(my_uw, uw_reg, my_uz, U, sw, R, RK, D, a.uld, a.kofs, d0, q, n, lane);
+  if constexpr (K32) stage_uw32<W, NJ>(uw32, U, sw, R, RK, D, a.uld, a.kofs, d0, q, n);
   for (int it = 0; it < nit; it += 2) {
     load_tile(tile0 + it + 1, tb);
     __builtin_amdgcn_sched_barrier(0);  // issue the next tile's loads before this tile's waits
@@ -799,7 +805,7 @@ __attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))
   // The partial's rows are uld (all taps' W*D) floats apart; a pass of taps
   // writes its own taps' columns (part_du starts at its first tap's).
   const int UL = a.uld;
-  const rsrc_t rdu = make_rsrc(part_du + (int64_t)sp * RK * UL, (int64_t)RK * UL * 4);
+  const rsrc_t rdu = make_rsrc(part_du + (int64_t)sp * a.dupr * UL, lr_dupart_bytes(RK, UL, a.kofs, D));
   const int du_lane = chv ? (4 * q * UL + col) * 4 : kOobLane;
 #pragma unroll
   for (int k = 0; k < W; ++k)
@@ -850,16 +856,55 @@ constexpr int pass_taps(int W, int RC) {
 }
 constexpr int npasses(int W, int RC) { return (W + pass_taps(W, RC) - 1) / pass_taps(W, RC); }
 
-// More than four passes of taps add dx into an fp32 accumulator in the
+// Rank chunks of a problem's launch shape: up to kernel rank 64 its own
+// (one to four), above it passes of kBwdRankPass ranks on the two-chunk kernels.
+constexpr int kBwdRankPass = 32;
+inline int bwd_rc(const LrProblem& p) {
+  const int rk = (int)(p.R + (p.static_w ? 1 : 0));
+  return rk > 64 ? 2 : (rk + 15) / 16;
+}
+inline int bwd_rank_passes(const LrProblem& p) {
+  const int rk = (int)(p.R + (p.static_w ? 1 : 0));
+  return rk > 64 ? (rk + kBwdRankPass - 1) / kBwdRankPass : 1;
+}
+
+// More than four passes (ranks x taps) add dx into an fp32 accumulator in the
 // workspace, rounded to dx once by lr_dx_round (above W 16 at one or two rank
-// chunks, above W 8 at three, above W 4 at four).
+// chunks, above W 8 at three, above W 4 at four; above kernel rank 64 past
+// four rank x tap passes).
 constexpr int kBwdMaxBf16DxPasses = 4;
 inline bool bwd_f32dx(const LrProblem& p) {
-  const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
-  return npasses((int)p.W, rc) > kBwdMaxBf16DxPasses;
+  return bwd_rank_passes(p) * npasses((int)p.W, bwd_rc(p)) > kBwdMaxBf16DxPasses;
 }
 
 }  // namespace
+
+// The passes of a backward launch sequence: kernel ranks rofs .. rofs+RK-1 (R
+// of them dynamic) and taps kofs .. kofs+W-1; slot: the pass's dz partial slot
+// (its pass of taps: the passes of ranks write disjoint columns of the same
+// slots).  Every pass takes the same launch shape (bwd_rc), so the dU partial
+// rows of all passes line up.
+int bwd_plan(const LrProblem& p, BwdPass* out) {
+  const int RK = (int)(p.R + (p.static_w ? 1 : 0)), W = (int)p.W, rc = bwd_rc(p);
+  const int nrp = bwd_rank_passes(p), step = nrp > 1 ? kBwdRankPass : RK;
+  const int wp = pass_taps(W, rc), ntp = npasses(W, rc);
+  if (nrp * ntp > kBwdMaxPlan) return -1;
+  int n = 0;
+  for (int i = 0; i < nrp; ++i) {
+    const int rofs = i * step, rk = RK - rofs < step ? RK - rofs : step;
+    const int rd = (int)p.R - rofs < 0 ? 0 : ((int)p.R - rofs < rk ? (int)p.R - rofs : rk);
+    for (int t = 0; t < ntp; ++t) {
+      BwdPass& b = out[n++];
+      b.rofs = rofs;
+      b.R = rd;
+      b.RK = rk;
+      b.kofs = t * wp;
+      b.W = W - b.kofs < wp ? W - b.kofs : wp;
+      b.slot = t;
+    }
+  }
+  return n;
+}
 
 // Longest backward run (tiles) whose resources fit (see run_rsrc): rows of x,
 // dx, dy (one head's block of head-major dy), the z rows the kernel reads (z
@@ -877,7 +922,7 @@ namespace {
 
 LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   LrBwdArgs a;
-  const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
+  const int rc = bwd_rc(p);
   const BwdShape sh = bwd_shape(pass_taps((int)p.W, rc), rc, rc == 1 && p.W > 8);  // every pass has the same shape
   const int ncw = 256 / sh.cpw;
   a.Tn = (int)p.T;
@@ -904,6 +949,8 @@ LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   a.uld = (int)(p.W * p.D);
   a.kofs = 0;
   a.accdx = 0;
+  a.dzld = a.R;
+  a.dupr = a.RK;
   return a;
 }
 
@@ -1013,8 +1060,8 @@ struct BwdWs {
 };
 BwdWs bwd_ws(const LrProblem& p, const LrBwdArgs& a) {
   BwdWs w;
-  const int rc = (a.RK + 15) / 16;
-  const int64_t dz = (int64_t)npasses((int)p.W, rc) * a.ncg * a.BT * a.R * 4;
+  // one dz partial slot per pass of taps (the passes of ranks fill disjoint columns)
+  const int64_t dz = (int64_t)npasses((int)p.W, bwd_rc(p)) * a.ncg * a.BT * a.R * 4;
   w.dz_off = 0;
   w.du_off = (dz + 255) / 256 * 256;
   w.zp_off = (w.du_off + (int64_t)a.npair * a.RK * p.W * p.D * 4 + 255) / 256 * 256;
@@ -1089,8 +1136,10 @@ hipError_t dispatch_bwd_kernel(const LrBwdArgs& a, int wq, int rc, bool wide, bo
 
 template <typename T>
 hipError_t launch_bwd(const LrProblem* p, int G) {
-  const int rc = (int)((p[0].R + (p[0].static_w ? 1 : 0) + 15) / 16);
-  const int W = (int)p[0].W, wp = pass_taps(W, rc), np = npasses(W, rc);
+  const int rc = bwd_rc(p[0]);
+  BwdPass ps[kBwdMaxPlan];
+  const int np = bwd_plan(p[0], ps);
+  if (np < 1) return hipErrorInvalidValue;
   LrBwdArgs a = make_bwd_args(p[0], kBwdTargetWaves);
   const BwdWs w = bwd_ws(p[0], a);
   a.nblk1 = a.nblk;
@@ -1099,9 +1148,10 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
   a.dxld = (int)p[0].dxld();
   a.yhd = (int)p[0].yhd();
   // z itself when its rows are what the kernel reads: R % 4 == 0 and 8-byte
-  // aligned, or (two rank chunks) exactly 32 dynamic ranks, 16-byte aligned.
+  // aligned, or (two rank chunks, and passes of 32 ranks above 64) rows of a
+  // multiple of 32 dynamic ranks without the static one, 16-byte aligned.
   const bool K32 = rc == 2;
-  bool zvec = K32 ? (p[0].R == 32 && p[0].static_w == nullptr) : p[0].R % 4 == 0;
+  bool zvec = K32 ? (p[0].R % 32 == 0 && p[0].static_w == nullptr) : p[0].R % 4 == 0;
   for (int g = 0; g < G; ++g) {
     float* pdz = (float*)((char*)p[g].ws + w.dz_off);
     float* pdu = (float*)((char*)p[g].ws + w.du_off);
@@ -1121,37 +1171,45 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
     a.zld = a.zr = a.zrk = (int)zpad_ranks(p[0]);
   }
   const int64_t D = p[0].D, WD = p[0].W * D, RKWD = (int64_t)a.RK * WD, R = p[0].R;
-  const int64_t dz_slot = (int64_t)a.ncg * a.BT * R;  // one pass's dz partials
+  const int64_t dz_slot = (int64_t)a.ncg * a.BT * R;  // one pass of taps' dz partials
   // past four passes every pass works on the fp32 accumulator (rows of D floats)
   const bool f32 = bwd_f32dx(p[0]);
   if (f32) {
     a.dxld = (int)D;
     for (int g = 0; g < G; ++g) a.grp[g].dx = (char*)p[g].ws + w.dxf_off;
   }
-  for (int ps = 0; ps < np; ++ps) {
-    // pass ps: taps kofs .. kofs+wq-1 (U, static_w and the dU partials start at
-    // the pass's first tap; its dz partials take their own slots)
-    const int kofs = ps * wp, wq = W - kofs < wp ? W - kofs : wp;
+  for (int i = 0; i < np; ++i) {
+    // pass i: ranks rofs .. (z from column rofs, U and the dU partial rows from
+    // row rofs, dz partial columns from rofs, static_w in the pass that holds
+    // rank R), taps kofs .. (U, static_w and the dU partial columns from tap
+    // kofs; dz partials in the slot of its pass of taps); the residual in the
+    // first pass only
+    const BwdPass& f = ps[i];
     LrBwdArgs b = a;
-    b.kofs = kofs;
-    b.accdx = ps > 0;
+    b.R = f.R;
+    b.RK = f.RK;
+    b.kofs = f.kofs;
+    b.accdx = i > 0;
+    b.residual = a.residual && i == 0;
     for (int g = 0; g < G; ++g) {
-      b.grp[g].U = (const uint16_t*)p[g].U + kofs * D;
-      b.grp[g].sw = p[g].static_w ? (const void*)((const uint16_t*)p[g].static_w + kofs * D) : nullptr;
-      b.grp[g].part_dz = a.grp[g].part_dz + ps * dz_slot;
-      b.grp[g].part_du = a.grp[g].part_du + kofs * D;
+      b.grp[g].z = static_cast<const T*>(a.grp[g].z) + f.rofs;
+      b.grp[g].U = (const T*)p[g].U + f.rofs * WD + f.kofs * D;
+      b.grp[g].sw = p[g].static_w && f.RK > f.R ? (const void*)((const T*)p[g].static_w + f.kofs * D) : nullptr;
+      b.grp[g].part_dz = a.grp[g].part_dz + f.slot * dz_slot + f.rofs;
+      b.grp[g].part_du = a.grp[g].part_du + f.rofs * WD + f.kofs * D;
     }
-    if ((e = dispatch_bwd_kernel<T>(b, wq, rc, W > 8, f32, p[0].stream)) != hipSuccess) return e;
+    if ((e = dispatch_bwd_kernel<T>(b, f.W, rc, rc == 1 && p[0].W > 8, f32, p[0].stream)) != hipSuccess) return e;
   }
   if (f32 && (e = launch_dx_round<T>(p, G, w.dxf_off)) != hipSuccess) return e;
   PartialReduce jobs[kMaxReduceJobs];
   int nj = 0;
+  const int nslot = npasses((int)p[0].W, rc);
   for (int g = 0; g < G; ++g) {
     const float* pdz = a.grp[g].part_dz;
     const float* pdu = a.grp[g].part_du;
     jobs[nj++] = {pdu, RKWD, a.npair, R * WD, p[g].dU};
     jobs[nj++] = {pdu + R * WD, RKWD, a.npair, p[g].static_w ? WD : 0, p[g].dstatic_w};
-    jobs[nj++] = {pdz, a.BT * R, np * a.ncg, a.BT * R, p[g].dz};
+    jobs[nj++] = {pdz, a.BT * R, nslot * a.ncg, a.BT * R, p[g].dz};
   }
   return reduce_partials_multi(jobs, nj, p[0].dtype, p[0].stream);
 }

@@ -12,7 +12,7 @@ int64_t lr_fwd_max_run_tiles(const LrProblem& p) {
   const int64_t hd = p.yhd();
   int64_t rowb = p.xld() * 2;
   rowb = rowb > hd * 2 ? rowb : hd * 2;
-  rowb = rowb > p.R * 2 ? rowb : p.R * 2;
+  rowb = rowb > p.zld() * 2 ? rowb : p.zld() * 2;  // z rows (a pass of ranks: the whole problem's)
   const int64_t zrp = p.zeff ? lr_bwd_zrow(p.R, p.static_w != nullptr) : 0;
   rowb = rowb > zrp * 2 ? rowb : zrp * 2;
   int64_t tiles = run_tiles_cap(rowb);
@@ -26,60 +26,58 @@ int64_t lr_fwd_max_run_tiles(const LrProblem& p) {
   return tiles;
 }
 
-namespace {
-
-template <typename T>
-hipError_t dispatch_fwd(const LrProblem* pp, int G);
-
 // Taps per forward pass: what one launch stages (W x RC operand chunks in LDS).
 constexpr int fwd_pass_taps(int rc) { return rc <= 2 ? 16 : 8; }
 
-// Wider problems (above W 16 at one or two rank chunks, above W 8 at three or
-// four) as passes of taps: taps 0 .. W0-1 as a W0-tap problem (residual and
-// z_eff included), then passes of P = fwd_pass_taps taps, each on x read kofs
-// rows earlier and added to the stored y (accy).  U keeps its row stride W * D;
-// a later pass's U and static_w start at its tap kofs.  y is rounded to the
-// output type after each pass (two passes at W <= 32 and one or two rank
-// chunks, up to four at W 32 and three or four).
-template <typename T>
-hipError_t dispatch_fwd_passes(const LrProblem* pp, int G, int P) {
-  const int W = (int)pp[0].W, np = (W + P - 1) / P, w0 = W - (np - 1) * P;
-  LrProblem a[kMaxGroups];
-  for (int g = 0; g < G; ++g) {
-    a[g] = pp[g];
-    a[g].W = w0;
-    a[g].u_ld = pp[g].uld();
-  }
-  hipError_t e = dispatch_fwd<T>(a, G);
-  for (int ps = 1; ps < np && e == hipSuccess; ++ps) {
-    const int kofs = w0 + (ps - 1) * P;
-    for (int g = 0; g < G; ++g) {
-      const LrProblem& p = pp[g];
-      a[g] = p;
-      a[g].W = P;
-      a[g].u_ld = p.uld();
-      a[g].kofs = kofs;
-      a[g].accy = 1;
-      a[g].U = static_cast<const T*>(p.U) + (int64_t)kofs * p.D;
-      a[g].static_w = p.static_w ? static_cast<const T*>(p.static_w) + (int64_t)kofs * p.D : nullptr;
-      a[g].residual = 0;
-      a[g].zeff = nullptr;
+// The passes of a forward launch sequence (fwd_plan).  Up to kernel rank 64
+// one pass of ranks; wider problems (above W 16 at one or two rank chunks,
+// above W 8 at three or four) run as passes of taps: taps 0 .. W0-1 as a
+// W0-tap problem (residual and z_eff included), then passes of P =
+// fwd_pass_taps taps, each on x read kofs rows earlier and added to the stored
+// y (accy).  Above kernel rank 64, passes of kFwdRankPass kernel ranks (z
+// columns rofs .. of its rows, U rows rofs .., the static rank in the pass that
+// holds index R), each split into passes of at most 8 taps, every pass after
+// the first adding to the stored y.  y is rounded to the output type after
+// each pass; lr_mfma_ok admits at most kFwdMaxPasses of them.
+int fwd_plan(const LrProblem& p, FwdPass* out) {
+  const int RK = (int)(p.R + (p.static_w ? 1 : 0)), W = (int)p.W;
+  const bool ranks = RK > kFwdRankPass;
+  int n = 0;
+  for (int rofs = 0; rofs < RK; rofs += kFwdRankPass) {
+    const int rk = RK - rofs < kFwdRankPass ? RK - rofs : kFwdRankPass;  // kernel ranks of the pass
+    const int rd = (int)p.R - rofs < 0 ? 0 : ((int)p.R - rofs < rk ? (int)p.R - rofs : rk);  // dynamic ones
+    const int P = ranks ? 8 : fwd_pass_taps((rk + 15) / 16);
+    const int nt = W <= P ? 1 : (W + P - 1) / P, w0 = W - (nt - 1) * P;
+    for (int i = 0; i < nt; ++i) {
+      if (n == kFwdMaxPlan) return -1;
+      FwdPass& f = out[n++];
+      f.rofs = rofs;
+      f.R = rd;
+      f.RK = rk;
+      f.kofs = i == 0 ? 0 : w0 + (i - 1) * P;
+      f.W = i == 0 ? w0 : P;
+      f.accy = rofs > 0 || i > 0;
     }
-    e = dispatch_fwd<T>(a, G);
   }
-  return e;
+  return n;
 }
 
+int lr_fwd_npasses(const LrProblem& p) {
+  FwdPass ps[kFwdMaxPlan];
+  return fwd_plan(p, ps);
+}
+
+namespace {
+
+// The kernel of one pass: the plain kernels up to W 8 (this unit) and at
+// 9 <= W <= 16 (lowrank_mfma_fwd_wide.hip, which also holds the 16-tap
+// accumulating pass above W 16), the accumulating ones up to W 8
+// (lowrank_mfma_fwd_acc.hip).
 template <typename T>
-hipError_t dispatch_fwd(const LrProblem* pp, int G) {
+hipError_t dispatch_pass(const LrProblem* pp, int G) {
   const LrProblem& p = pp[0];
   const int rc = (int)((p.R + (p.static_w ? 1 : 0) + 15) / 16);
-  if (p.accy) {  // a later pass: the accumulating kernels of fwd_pass_taps(rc) taps
-    if (rc <= 2) return lr_fwd_wide_dispatch<T>(pp, G);
-    if (p.W != 8) return hipErrorInvalidValue;
-    return rc == 3 ? launch_fwd<T, 8, 3, true>(pp, G) : launch_fwd<T, 8, 4, true>(pp, G);
-  }
-  if (p.W > fwd_pass_taps(rc)) return dispatch_fwd_passes<T>(pp, G, fwd_pass_taps(rc));
+  if (p.accy) return p.W <= 8 ? lr_fwd_acc_dispatch<T>(pp, G) : lr_fwd_wide_dispatch<T>(pp, G);
 #define DC_LR_CASE(WW, CC) \
   if (p.W == WW && rc == CC) return launch_fwd<T, WW, CC>(pp, G);
   DC_LR_CASE(1, 1) DC_LR_CASE(1, 2) DC_LR_CASE(1, 3) DC_LR_CASE(1, 4)
@@ -93,6 +91,41 @@ hipError_t dispatch_fwd(const LrProblem* pp, int G) {
 #undef DC_LR_CASE
   if (p.W > 8) return lr_fwd_wide_dispatch<T>(pp, G);
   return hipErrorInvalidValue;
+}
+
+// Every pass of fwd_plan in order: pass f of group g is pp[g] restricted to
+// kernel ranks f.rofs .. f.rofs+f.RK-1 (z from column rofs of its rows, U from
+// row rofs, static_w in the pass that holds rank R) and taps f.kofs ..
+// f.kofs+f.W-1 (U and static_w from tap kofs), the residual in the first pass
+// only, z_eff written by the first pass (one pass of ranks: the only kind that
+// keeps a z_eff).
+template <typename T>
+hipError_t dispatch_fwd(const LrProblem* pp, int G) {
+  FwdPass ps[kFwdMaxPlan];
+  const int np = fwd_plan(pp[0], ps);
+  if (np < 1) return hipErrorInvalidValue;
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < np && e == hipSuccess; ++i) {
+    const FwdPass& f = ps[i];
+    LrProblem a[kMaxGroups];
+    for (int g = 0; g < G; ++g) {
+      const LrProblem& p = pp[g];
+      a[g] = p;
+      a[g].R = f.R;
+      a[g].W = f.W;
+      a[g].z = static_cast<const T*>(p.z) + f.rofs;
+      a[g].z_ld = p.zld();
+      a[g].U = static_cast<const T*>(p.U) + (int64_t)f.rofs * p.uld() + (int64_t)f.kofs * p.D;
+      a[g].u_ld = p.uld();
+      a[g].static_w = p.static_w && f.RK > f.R ? static_cast<const T*>(p.static_w) + (int64_t)f.kofs * p.D : nullptr;
+      a[g].kofs = f.kofs;
+      a[g].accy = f.accy;
+      a[g].residual = i == 0 ? p.residual : 0;
+      a[g].zeff = i == 0 ? p.zeff : nullptr;  // null above kernel rank 64 (lr_zeff_bytes is 0)
+    }
+    e = dispatch_pass<T>(a, G);
+  }
+  return e;
 }
 
 }  // namespace

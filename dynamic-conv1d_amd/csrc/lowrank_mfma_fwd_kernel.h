@@ -59,6 +59,7 @@ struct LrArgs {
   int zrp;         // > 0: the 128-channel chunk 0 wavefronts write z_eff rows of zrp ranks
   int64_t uld;     // row stride of U (elements): the problem's W * D, all taps
   int kofs;        // ACC pass: its first tap (x read kofs rows earlier)
+  int zld;         // row stride of z (elements): R, or a wider problem's for a pass of ranks
   LrFwdGroup grp[kMaxGroups];
 };
 
@@ -99,10 +100,12 @@ __device__ __forceinline__ void stage_u(u32x2* __restrict__ lds, const uint16_t*
 // ILP strategy (lowrank_mfma_fwd_ilp.hip); a template argument of its own, so
 // the two builds are distinct kernels.
 //
-// ACC: a later pass of taps kofs .. kofs+W-1 of a wider problem (above W 16:
-// the host runs taps 0 .. W-17 first, then the last 16 with ACC): x is read
-// kofs rows earlier and the tile's y rows, as the first pass stored them, are
-// added before the store (each lane loads and stores only its own rows).
+// ACC: a later pass of a wider problem, whose y rows, as the earlier passes
+// stored them, are added before the store (each lane loads and stores only its
+// own rows): a pass of taps kofs .. kofs+W-1 (above W 16 the host runs taps
+// 0 .. W-17 first, then the last 16), whose x is read kofs rows earlier, or a
+// pass of kernel ranks (above 64: z columns and U rows from the pass's first
+// rank, kofs 0 unless taps are split as well).
 template <typename T, int W, int RC, bool ZV, bool ZE, bool ILP = false, bool ACC = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZE && W <= 4 && RC <= 2 ? 4 : 1, 8)))
 void lr_fwd_mfma(LrArgs a) {
@@ -147,7 +150,8 @@ void lr_fwd_mfma(LrArgs a) {
   const int rowb = yhd * 2, xrowb = a.xld * 2;
   const rsrc_t rx = run_rsrc(x + rrow * a.xld, Tn - rb, xrowb);
   const rsrc_t ry = run_rsrc(y + row0 * D + ((int64_t)yh0 * Tn + rb) * yhd, (int64_t)(yhl - yh0) * Tn + Tn - rb, rowb);
-  const rsrc_t rz = run_rsrc(z + rrow * R, Tn - rb, R * 2);
+  const int zld = a.zld;  // z rows: R, or the whole problem's ranks for a pass of ranks (z then starts at its first)
+  const rsrc_t rz = run_rsrc(z + rrow * zld, Tn - rb, zld * 2);
   const int zrp = ZE ? a.zrp : 0;
   const bool zrow_mine = ZE && n % a.nch == chunk;  // this wavefront writes row n of each tile's z_eff
   const rsrc_t rze = ZE ? run_rsrc((const uint16_t*)pick(a.grp, g, &LrFwdGroup::zeff) + rrow * zrp, Tn - rb, zrp * 2)
@@ -159,7 +163,7 @@ void lr_fwd_mfma(LrArgs a) {
   // above them are the own rows of the lane group above (lane - 16), or for
   // group 0 those of group 3 in the tile before, passed with ds_bpermute.
   constexpr bool HX = W >= 2 && W <= 4;
-  static_assert(!(ACC && (HX || ZE)), "passes of taps: one-pass x rows, z_eff from the first pass");
+  static_assert(!(ACC && ZE), "passes: z_eff from the first pass only");
   const int kofs = ACC ? a.kofs : 0;
   const int above = ((lane + 48) & 63) << 2;  // ds_bpermute byte address of lane - 16
   u32x4 prev[HX ? W - 1 : 1];                 // rows 16-W+1 .. 15 of the tile before (group 3 sends them)
@@ -174,7 +178,7 @@ void lr_fwd_mfma(LrArgs a) {
     // with the halo from the lane group above (HX) every x row is loaded once: nontemporal
     // (B4 T4096 D2048 R16 forward 30.0 -> 29.2 us; R15 + static 31.8 -> 30.4 us)
     for (int m = HX ? W - 1 : 0; m < NR; ++m) xr[m] = bload128<HX ? kNt : 0>(rx, xlane_off + toff + (m - (W - 1)) * xrowb);
-    zr.load(rz, live ? (tile * 16 + n - rb) * R * 2 : kOobTile, R, q);
+    zr.load(rz, live ? (tile * 16 + n - rb) * zld * 2 : kOobTile, R, q);
   };
   auto compute_tile = [&](int tile, u32x4(&xc)[NR], const ZR& zr) {
     u32x2 zc[RC];
@@ -252,9 +256,10 @@ void lr_fwd_mfma(LrArgs a) {
   // buffer at 3 wavefronts (B4 T4096 D2048 R16: 32.3 -> 31.4 us).
   if constexpr (HX) {
     // the run's first tile: rows 16*tile0-W+1 .. 16*tile0-1 (before the sequence: 0), as group 3 would send them
+    // (a later pass of taps reads x kofs rows earlier, its halo rows as well)
     const int xcol = chv ? dl * 2 : kOobLane;
 #pragma unroll
-    for (int m = 0; m < W - 1; ++m) prev[m] = bload128(rx, xcol + (tile0 * 16 + m + 1 - W - rb) * xrowb);
+    for (int m = 0; m < W - 1; ++m) prev[m] = bload128(rx, xcol + (tile0 * 16 - kofs + m + 1 - W - rb) * xrowb);
   }
   for (int tile = tile0; tile < tile1; ++tile) {
     u32x4 xr[NR];

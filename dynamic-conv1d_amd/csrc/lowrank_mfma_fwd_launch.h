@@ -35,7 +35,9 @@ inline LrArgs make_args(const LrProblem& p, int target_waves) {
   a.residual = p.residual;
   a.nch = (int)((p.D + 127) / 128);
   a.ncg = 0;
-  a.zvec = p.R % 4 == 0 && aligned_to(p.z, 8);
+  a.zld = (int)p.zld();
+  // 8-byte z loads: four ranks at a time from 8-byte aligned rows
+  a.zvec = p.R % 4 == 0 && p.zld() % 4 == 0 && aligned_to(p.z, 8);
   const int64_t ntile = (p.T + 15) / 16;
   int64_t seg = (p.B * ntile * a.nch + target_waves - 1) / target_waves;
   if (seg < 1) seg = 1;
@@ -97,5 +99,11 @@ hipError_t launch_fwd(const LrProblem* p, int G) {
 // second pass of taps above W 16 (lowrank_mfma_fwd_wide.hip).
 template <typename T>
 hipError_t lr_fwd_wide_dispatch(const LrProblem* pp, int G);
+
+// The accumulating passes (accy) up to W 8 at every rank chunk count
+// (lowrank_mfma_fwd_acc.hip): passes of 8 taps above W 8 at three or four rank
+// chunks, and the passes of ranks above kernel rank 64.
+template <typename T>
+hipError_t lr_fwd_acc_dispatch(const LrProblem* pp, int G);
 
 }  // namespace dc

@@ -271,7 +271,7 @@ def test_kernel_paths(lib):
         assert hp(4, 4096, 2048, 64, 24, bf, 1, bwd) == 5      # W 24: wide, one channel per lane
         assert hp(1, 50, 96, 96, 20, bf, 1, bwd) == 0          # W 20, D % 64 != 0: generic
         assert hp(1, 50, 256, 2, 9, bf, 1, bwd) == 0           # head size 128, W 9: 18-byte segments
-        assert lp(1, 45, 64, 127, 12, bf, 1, bwd) == 0         # W 12, kernel rank 128: generic
+        assert lp(1, 45, 64, 127, 12, bf, 1, bwd) == 2         # W 12, kernel rank 128: 2 x 2 forward passes
         assert lp(1, 70, 128, 64, 1, bf, 0, bwd) == 2          # kernel rank 64, W 1
         assert lp(1, 40, 128, 40, 2, f16, 0, bwd) == 2         # kernel rank 40, W 2
     assert lp(1, 300, 64, 1, 1, f32, 0, 0) == 3                # fp32 W 1: forward on fp32 matrix cores,
@@ -295,7 +295,7 @@ def test_kernel_paths(lib):
         assert lp(2, 8192, 4096, 31, 8, bf, 1, bwd) == 2       # W 8, two rank chunks
         assert lp(1, 64, 256, 40, 5, f16, 0, bwd) == 2         # W 5, three rank chunks
         assert lp(1, 64, 256, 63, 8, bf, 1, bwd) == 2          # W 8, four rank chunks
-        assert lp(1, 64, 256, 64, 8, bf, 1, bwd) == 0          # kernel rank 65: generic
+        assert lp(1, 64, 256, 64, 8, bf, 1, bwd) == 2          # kernel rank 65: passes of ranks
         assert lp(2, 300, 256, 16, 12, bf, 0, bwd) == 2        # W 9-16 at kernel ranks <= 32
         assert lp(2, 77, 200, 31, 16, bf, 1, bwd) == 2
         assert lp(1, 64, 256, 40, 9, f16, 0, bwd) == 2         # W 9, kernel rank 40: passes of taps
@@ -303,8 +303,16 @@ def test_kernel_paths(lib):
         assert lp(4, 4096, 2048, 31, 32, f16, 1, bwd) == 2     # passes, backward passes of 4 taps
         assert lp(1, 64, 256, 40, 17, bf, 0, bwd) == 2         # W 17, kernel rank 40: passes of taps
         assert lp(1, 64, 256, 64, 32, bf, 0, bwd) == 2         # W 32, kernel rank 64
-        assert lp(1, 64, 256, 65, 4, bf, 0, bwd) == 0          # kernel rank 65: generic
+        assert lp(1, 64, 256, 65, 4, bf, 0, bwd) == 2          # kernel rank 65: passes of ranks
         assert lp(1, 64, 256, 16, 33, bf, 0, bwd) < 0          # W 33: above DC_MAX_W
+    for bwd in (0, 1):                                         # kernel ranks 65-256 as passes of ranks
+        assert lp(4, 4096, 2048, 127, 4, bf, 1, bwd) == 2      # (forward 64 per pass, backward 32)
+        assert lp(1, 64, 256, 255, 8, f16, 1, bwd) == 2        # kernel rank 256, W 8: 4 forward passes
+        assert lp(1, 64, 256, 100, 16, bf, 0, bwd) == 2        # 2 x 2 forward passes
+    assert lp(1, 64, 256, 127, 20, bf, 1, 0) == 0              # 2 x 3 forward passes (y rounded 6 times):
+    assert lp(1, 64, 256, 127, 20, bf, 1, 1) == 2              # generic forward; backward on matrix cores
+    assert lp(1, 64, 256, 255, 9, bf, 1, 0) == 0               # 4 x 2 forward passes: generic
+    assert lp(1, 64, 256, 256, 4, bf, 1, 0) == E_UNSUP         # kernel rank 257: above DC_MAX_R
     for bwd in (0, 1):                                         # D a multiple of 8, not of 16
         assert lp(2, 100, 200, 16, 4, bf, 0, bwd) == 2
         assert lp(1, 50, 1000, 15, 3, f16, 1, bwd) == 2

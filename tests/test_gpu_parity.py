@@ -337,10 +337,23 @@ LR_EDGE = [
     (1, 300, 64, 47, 20, True, False, torch.bfloat16, ("mfma", "mfma")),       # forward 4 + 8 + 8
     (1, 25, 64, 40, 20, False, True, torch.bfloat16, ("mfma", "mfma")),        # W 20 > T
     (1, 50, 64, 64, 32, False, True, torch.bfloat16, ("mfma", "mfma")),        # W 32: forward 4 x 8, 32 passes
-    # kernel ranks above 64: the generic kernels (the reference accepts any W and power-of-two
-    # ranks, lowrank.py:220, 331-333)
-    (1, 45, 64, 127, 12, True, True, torch.bfloat16, ("generic", "generic")),  # W 12, kernel rank 128
-    (1, 30, 32, 255, 3, True, False, torch.float32, ("generic", "generic")),   # kernel rank 256 (the maximum)
+    # kernel ranks 65-256 (the reference takes any power-of-two rank, lowrank.py:331-333): the forward
+    # as passes of 64 ranks (z columns and U rows from the pass's first rank, the static rank in the pass
+    # that holds index R, each pass split into passes of at most 8 taps, every pass after the first added
+    # to the stored y; at most 4 passes), the backward as passes of 32 ranks on the two-chunk kernels
+    # (dz partial columns and dU partial rows of the whole problem, dx accumulated; past 4 rank x tap
+    # passes in fp32)
+    (2, 300, 256, 127, 4, True, True, torch.bfloat16, ("mfma", "mfma")),      # kernel rank 128: 2 + 4 passes
+    (1, 100, 128, 64, 3, True, False, torch.float16, ("mfma", "mfma")),       # rank 65: the static rank alone
+    (1, 3216, 256, 96, 2, False, True, torch.bfloat16, ("mfma", "mfma")),     # rank 96: z itself, long runs
+    (2, 64, 128, 255, 8, True, True, torch.float16, ("mfma", "mfma")),        # rank 256, W 8: 4 + 8 x 2 passes
+    (1, 50, 64, 200, 1, False, True, torch.bfloat16, ("mfma", "mfma")),       # rank 200, W 1: padded z
+    (1, 37, 64, 100, 16, True, True, torch.bfloat16, ("mfma", "mfma")),       # rank 101, W 16: 2 x 2, 4 x 4
+    (1, 45, 64, 127, 12, True, True, torch.bfloat16, ("mfma", "mfma")),       # W 12: forward 2 x (4 + 8)
+    (1, 520, 200, 70, 5, False, False, torch.float16, ("mfma", "mfma")),      # D % 16 != 0, rank 70, W 5
+    # the forward past 4 passes takes the generic kernels (its y would be rounded more often)
+    (1, 64, 256, 127, 20, True, True, torch.bfloat16, ("generic", "mfma")),   # 2 x 3 forward passes
+    (1, 30, 32, 255, 3, True, False, torch.float32, ("generic", "generic")),  # fp32 kernel rank 256
 ]
 
 
@@ -595,26 +608,34 @@ def test_lowrank_inference_forward(R, static, W, dtype):
 
 
 # ------------------------------------------------------------ determinism
-@pytest.mark.parametrize("kind", ["hw1", "hw32", "lr16s", "hw32w12", "hw4w24", "lr16sw20"])
-def test_deterministic(kind):
+DET_CASES = [  # op, head size (headwise) or kernel rank with the static filter (lowrank), W
+    ("hw", 1, 4), ("hw", 32, 4), ("lr", 16, 4),
+    ("hw", 32, 12), ("hw", 4, 24),  # the wide headwise kernels
+    ("lr", 16, 20),                 # passes of taps into the fp32 dx accumulator
+    ("lr", 128, 4), ("lr", 128, 8),  # passes of ranks (at W 8 into the fp32 dx accumulator)
+]
+
+
+@pytest.mark.parametrize("op,n,W", DET_CASES, ids=[f"{o}{n}w{w}" for o, n, w in DET_CASES])
+def test_deterministic(op, n, W):
     """Two runs give bitwise equal outputs and gradients: no float atomics anywhere, partial sums in a
     fixed order (W 12 / 24: the wide headwise kernels; lowrank W 20: passes of taps into the fp32 dx
-    accumulator)."""
+    accumulator; kernel rank 128: passes of ranks, at W 8 into the fp32 dx accumulator)."""
     g = gen(5)
     Bn, Tn, Dn = 2, 1024, 512
-    W = int(kind.split("w")[-1]) if "w" in kind else 4
-    kind = kind.split("w")[0]
     x = randn(g, Bn, Tn, Dn).to(torch.bfloat16).to(DEV)
     dy = randn(g, Bn, Tn, Dn).to(torch.bfloat16).to(DEV)
     sw = randn(g, W, Dn, scale=0.3).to(torch.bfloat16).to(DEV)
-    if kind.startswith("hw"):
-        hs = int(kind[2:])
-        w = randn(g, Bn, Tn, Dn // hs, W, scale=0.5).to(torch.bfloat16).to(DEV)
+    if op == "hw":
+        w = randn(g, Bn, Tn, Dn // n, W, scale=0.5).to(torch.bfloat16).to(DEV)
         src, fn = [x, w, sw], hw
+        assert _path("hw", Bn, Tn, Dn, Dn // n, W, torch.bfloat16, True, 1) == ("vector" if W <= 8 else "wide")
     else:
-        z = randn(g, Bn, Tn, 15).to(torch.bfloat16).to(DEV)
-        U = randn(g, 15, W * Dn, scale=0.1).to(torch.bfloat16).to(DEV)
+        R = n - 1  # dynamic ranks; the static filter is the last kernel rank
+        z = randn(g, Bn, Tn, R).to(torch.bfloat16).to(DEV)
+        U = randn(g, R, W * Dn, scale=0.1).to(torch.bfloat16).to(DEV)
         src, fn = [x, z, U, sw], lr
+        assert _path("lr", Bn, Tn, Dn, R, W, torch.bfloat16, True, 1) == "mfma"
     outs = [run_fwd_bwd(fn, src, dy, True) for _ in range(2)]
     assert torch.equal(outs[0][0], outs[1][0])
     for a, b in zip(outs[0][1], outs[1][1]):
