@@ -271,6 +271,29 @@ int dc_lowrank_path(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int d
   return dc::lr_path(p, bwd != 0);
 }
 
+int64_t dc_lowrank_plan_ranges(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int has_static,
+                               int bwd, int64_t* out, int64_t max_pairs) {
+  int s = check_lowrank(B, T, D, R, W, dtype, has_static != 0);
+  if (s != DC_OK) return s;
+  if (max_pairs < 0 || (max_pairs > 0 && !out)) return DC_ERR_NULL;
+  // 256-byte aligned stand-in addresses: the dispatch only offsets them (nothing
+  // is launched or read while the audit is installed)
+  static const char kAligned[16] __attribute__((aligned(256))) = {0};
+  dc::LrProblem p{};
+  p.x = p.z = p.U = p.dy = kAligned;
+  p.y = p.dx = p.dz = p.dU = (void*)kAligned;
+  p.ws = (float*)kAligned;
+  p.static_w = has_static ? kAligned : nullptr;
+  p.dstatic_w = has_static ? (void*)kAligned : nullptr;
+  p.B = B; p.T = T; p.D = D; p.R = R; p.W = W; p.dtype = dtype; p.residual = 1;
+  if (dc::lr_path(p, bwd != 0) == DC_PATH_GENERIC) return 0;  // generic kernels: plain pointers
+  dc::RangeAudit audit{out, max_pairs, 0};
+  dc::g_range_audit = &audit;
+  const hipError_t e = bwd ? dc::lr_bwd(&p, 1) : dc::lr_fwd(&p, 1);
+  dc::g_range_audit = nullptr;
+  return e == hipSuccess ? audit.n : DC_ERR_LAUNCH;
+}
+
 int64_t dc_lowrank_bwd_ws_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype,
                                 int has_static) {
   int s = check_lowrank(B, T, D, R, W, dtype, has_static != 0);

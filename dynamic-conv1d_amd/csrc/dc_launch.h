@@ -115,6 +115,29 @@ int64_t proj_bwd_ws_bytes(const ProjProblem& p);
 hipError_t proj_fwd_launch(const ProjProblem& p);
 hipError_t proj_bwd_launch(const ProjProblem& p);
 
+// ------------------------------------------------------------ range audit
+// dc_lowrank_plan_ranges: while a RangeAudit is installed on the calling
+// thread, the lowrank launch functions record, for every kernel launch of the
+// plan, the byte count each buffer resource of that kernel gets (before
+// make_rsrc's clamp, from the same functions the kernels call) with the bound
+// it must stay within, and launch nothing (no HIP call is made).  Per-run
+// resources are recorded for the longest run (from row 0).
+struct RangeAudit {
+  int64_t* out;  // pairs (bytes, bound): the count must lie in [0, bound]
+  int64_t cap;   // pairs out can hold
+  int64_t n;     // pairs recorded (counted past cap too)
+};
+extern thread_local RangeAudit* g_range_audit;
+inline bool auditing() { return g_range_audit != nullptr; }
+inline void audit_range(int64_t bytes, int64_t bound) {
+  RangeAudit* a = g_range_audit;
+  if (a->n < a->cap) {
+    a->out[2 * a->n] = bytes;
+    a->out[2 * a->n + 1] = bound;
+  }
+  ++a->n;
+}
+
 // ------------------------------------------------------------------ shared
 // out[c] = (T) sum_{p < P} part[p * pstride + c] for c < C, summed in a fixed
 // order (deterministic).

@@ -89,8 +89,8 @@ struct ZChunk {
 template <int W, int RKP>
 __device__ __forceinline__ void load_ucol(float (&u)[RKP][W], const float* __restrict__ U,
                                           const float* __restrict__ sw, int R, int RK, int D, int d, bool dv) {
-  const rsrc_t ru = make_rsrc(U, (int64_t)R * W * D * 4);
-  const rsrc_t rs = make_rsrc(sw, sw ? (int64_t)W * D * 4 : 0);
+  const rsrc_t ru = make_rsrc(U, lr_u_bytes(R, (int64_t)W * D, 0, D, 4));
+  const rsrc_t rs = make_rsrc(sw, lr_sw_bytes(sw != nullptr, W, D, 4));
 #pragma unroll
   for (int r = 0; r < RKP; ++r)
 #pragma unroll
@@ -423,6 +423,14 @@ F32Ws f32_ws(const LrProblem& p, const LrF32Args& a) {
 template <int W, int RKP>
 hipError_t launch_f32(const LrProblem& p, bool bwd) {
   const LrF32Args a = make_f32_args(p, kF32TargetWaves);
+  if (auditing()) {
+    // U and static_w; one sequence of x, y or dy (one head's block) and dx, z
+    audit_range(lr_u_bytes(a.R, (int64_t)W * a.D, 0, a.D, 4), kOobLane);
+    audit_range(lr_sw_bytes(p.static_w != nullptr, W, a.D, 4), kOobLane);
+    const int64_t rows[4] = {(int64_t)a.xld * 4, (int64_t)a.yhd * 4, (int64_t)p.dxld() * 4, (int64_t)a.R * 4};
+    for (int64_t rowb : rows) audit_range((int64_t)a.Tn * rowb, kMaxSeqBytes - kSeqSlackRows * rowb);
+    return hipSuccess;
+  }
   if (!bwd) {
     lr_fwd_f32<W, RKP><<<a.nblk, 256, 0, p.stream>>>((const float*)p.x, (const float*)p.z, (const float*)p.U,
                                                       (const float*)p.static_w, (float*)p.y, a);

@@ -74,9 +74,8 @@ __global__ __launch_bounds__(256) void lr_fwd_f32m(const float* __restrict__ x, 
     // of ranks may hold no dynamic rank (R == 0: the static rank alone), whose
     // range is empty: R * uld - kofs * D would be negative there, and a negative
     // record count wraps to a range that takes kOobLane in
-    const int64_t ubytes = R > 0 ? ((int64_t)R * a.uld - (int64_t)(ACC ? a.kofs : 0) * D) * 4 : 0;
-    const rsrc_t ru = make_rsrc(U, ubytes);
-    const rsrc_t rs = make_rsrc(sw, sw ? (int64_t)W * D * 4 : 0);
+    const rsrc_t ru = make_rsrc(U, lr_u_bytes(R, a.uld, ACC ? a.kofs : 0, D, 4));
+    const rsrc_t rs = make_rsrc(sw, lr_sw_bytes(sw != nullptr, W, D, 4));
     for (int kk = wave; kk < W * NKB; kk += 4) {
       const int k = kk / NKB, kb = kk - k * NKB;
       const int r = 4 * kb + q;
@@ -280,8 +279,8 @@ __global__ __launch_bounds__(512) void lr_bwd_f32m(const float* __restrict__ x, 
   const int dxlo = chv ? (4 * q * a.dxld + col) * 4 : kOobLane;
 
   // ---- U_eff operands of the chunk (rank rows r < RK, zero beyond)
-  const rsrc_t ru = make_rsrc(U, (int64_t)R * uld * 4);
-  const rsrc_t rs = make_rsrc(sw, sw ? (int64_t)W * D * 4 : 0);
+  const rsrc_t ru = make_rsrc(U, lr_u_bytes(R, uld, kofs, D, 4));
+  const rsrc_t rs = make_rsrc(sw, lr_sw_bytes(sw != nullptr, W, D, 4));
   float uw[W][NKB][2];  // tap-weight B: U_eff[4kb+q, k*D + col + jj]
 #pragma unroll
   for (int k = 0; k < W; ++k)
@@ -611,6 +610,21 @@ LrF32mArgs make_f32m_args(const LrProblem& p) {
 template <int W, int NKB, bool ACC = false>
 hipError_t launch_f32m(const LrProblem& p) {
   const LrF32mArgs a = make_f32m_args(p);
+  if (auditing()) {
+    // U and static_w of the pass; x, z and y (the head blocks of the widest
+    // 64-channel chunk) for the longest run
+    audit_range(lr_u_bytes(a.R, a.uld, ACC ? a.kofs : 0, a.D, 4), kOobLane);
+    audit_range(lr_sw_bytes(p.static_w != nullptr, W, a.D, 4), kOobLane);
+    const int64_t rows[2] = {(int64_t)a.xld * 4, (int64_t)a.zld * 4};
+    for (int64_t rowb : rows) audit_range(run_rsrc_bytes(a.Tn, rowb), kOobTile - 15 * rowb);
+    int heads = 0;
+    for (int c = 0; c < a.nch; ++c) {
+      const int yh0 = c * 64 / a.yhd, yhl = (c * 64 + 63 < a.D - 1 ? c * 64 + 63 : a.D - 1) / a.yhd;
+      heads = yhl - yh0 > heads ? yhl - yh0 : heads;
+    }
+    audit_range(run_rsrc_bytes((int64_t)heads * a.Tn + a.Tn, (int64_t)a.yhd * 4), kOobTile - 15 * (int64_t)a.yhd * 4);
+    return hipSuccess;
+  }
   lr_fwd_f32m<W, NKB, ACC><<<a.nblk, 256, 0, p.stream>>>((const float*)p.x, (const float*)p.z, (const float*)p.U,
                                                            (const float*)p.static_w, (float*)p.y, a);
   return hipGetLastError();
@@ -774,6 +788,15 @@ template <int W, int NKB>
 hipError_t launch_f32m_pass(const LrProblem& p, LrF32mBwdArgs a, const float* U, const float* sw, float* pdz,
                             float* pdu) {
   const bool first = a.rofs == 0 && a.kofs == 0;
+  if (auditing()) {
+    // U and static_w of the pass (kofs is the kernel's for every pass but the
+    // first, which starts at tap 0); x, dy, dx and z for the longest run
+    audit_range(lr_u_bytes(a.R, a.uld, first ? 0 : a.kofs, a.D, 4), kOobLane);
+    audit_range(lr_sw_bytes(sw != nullptr, W, a.D, 4), kOobLane);
+    const int64_t rows[4] = {(int64_t)a.xld * 4, (int64_t)a.yhd * 4, (int64_t)a.dxld * 4, (int64_t)a.R * 4};
+    for (int64_t rowb : rows) audit_range(run_rsrc_bytes(a.Tn, rowb), kOobTile - 15 * rowb);
+    return hipSuccess;
+  }
   if (!first)
     lr_bwd_f32m<W, NKB, true><<<a.nblk, 512, 0, p.stream>>>((const float*)p.x, (const float*)p.z, U, sw,
                                                              (const float*)p.dy, (float*)p.dx, pdz, pdu, a);

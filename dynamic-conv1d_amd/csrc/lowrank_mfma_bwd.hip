@@ -990,6 +990,7 @@ __global__ __launch_bounds__(256) void lr_zpad(ZpadArgs a) {
 // lr_zpad over G problems: z_eff of group g into dst[g].
 template <typename T>
 hipError_t launch_zpad(const LrProblem* p, int G, void* const* dst) {
+  if (auditing()) return hipSuccess;  // plain pointers
   ZpadArgs za;
   const int64_t RP = zpad_ranks(p[0]);
   za.n = p[0].B * p[0].T * RP / 4;
@@ -1007,6 +1008,19 @@ hipError_t launch_zpad(const LrProblem* p, int G, void* const* dst) {
 }
 
 constexpr int kBwdTargetWaves = 2048;
+
+// The byte counts lr_bwd_mfma gives its buffer resources for pass b of wq taps
+// (the range audit; see the kernel): U, static_w and the dU partial per pass;
+// x, dy, dx, z and the dz partials for the longest run (from row 0).
+void audit_bwd_pass(const LrBwdArgs& b, int wq, bool f32) {
+  const int64_t D = b.D;
+  audit_range(lr_u_bytes(b.R, b.uld, b.kofs, D, 2), kOobLane);
+  audit_range(lr_sw_bytes(b.RK > b.R, wq, D, 2), kOobLane);
+  audit_range(lr_dupart_bytes(b.RK, b.uld, b.kofs, D), kOobLane);
+  const int64_t rows[5] = {(int64_t)b.xld * 2, (int64_t)b.yhd * 2, (int64_t)b.dxld * (f32 ? 4 : 2),
+                           (int64_t)b.zld * 2, (int64_t)b.dzld * 4};
+  for (int64_t rowb : rows) audit_range(run_rsrc_bytes(b.Tn, rowb), kOobTile - 15 * rowb);
+}
 
 // dx from the passes' fp32 accumulator (rows of D floats): each group's rows
 // rounded once to the output type, into dx rows dxld elements apart.
@@ -1038,6 +1052,7 @@ __global__ __launch_bounds__(256) void lr_dx_round(DxRoundArgs a) {
 
 template <typename T>
 hipError_t launch_dx_round(const LrProblem* p, int G, int64_t dxf_off) {
+  if (auditing()) return hipSuccess;  // plain pointers
   DxRoundArgs a;
   a.n4 = p[0].B * p[0].T * p[0].D / 4;
   a.dq = (int)(p[0].D / 4);
@@ -1197,6 +1212,10 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
       b.grp[g].sw = p[g].static_w && f.RK > f.R ? (const void*)((const T*)p[g].static_w + f.kofs * D) : nullptr;
       b.grp[g].part_dz = a.grp[g].part_dz + f.slot * dz_slot + f.rofs;
       b.grp[g].part_du = a.grp[g].part_du + f.rofs * WD + f.kofs * D;
+    }
+    if (auditing()) {
+      audit_bwd_pass(b, f.W, f32);
+      continue;
     }
     if ((e = dispatch_bwd_kernel<T>(b, f.W, rc, rc == 1 && p[0].W > 8, f32, p[0].stream)) != hipSuccess) return e;
   }

@@ -67,6 +67,20 @@ hipError_t launch_fwd(const LrProblem* p, int G) {
     a.grp[g] = LrFwdGroup{p[g].x, p[g].z, p[g].U, p[g].static_w, p[g].y, p[g].zeff};
     a.zvec = a.zvec && aligned_to(p[g].z, 8);
   }
+  if (auditing()) {
+    // the run resources of the longest run (from row 0): x, z, z_eff, and y
+    // over the head blocks of the widest 128-channel chunk (U is staged through
+    // plain pointers)
+    const int64_t rows[3] = {(int64_t)a.xld * 2, (int64_t)a.zld * 2, (int64_t)a.zrp * 2};
+    for (int64_t rowb : rows) audit_range(run_rsrc_bytes(a.Tn, rowb), kOobTile - 15 * rowb);
+    int heads = 0;
+    for (int c = 0; c < a.nch; ++c) {
+      const int yh0 = c * 128 / a.yhd, yhl = (c * 128 + 127 < a.D - 1 ? c * 128 + 127 : a.D - 1) / a.yhd;
+      heads = yhl - yh0 > heads ? yhl - yh0 : heads;
+    }
+    audit_range(run_rsrc_bytes((int64_t)heads * a.Tn + a.Tn, (int64_t)a.yhd * 2), kOobTile - 15 * (int64_t)a.yhd * 2);
+    return hipSuccess;
+  }
   if constexpr (ACC) {  // a later pass of taps (no z_eff writer)
     if (a.zvec)
       lr_fwd_mfma<T, W, RC, true, false, false, true><<<a.nblk, 256, 0, p[0].stream>>>(a);

@@ -80,7 +80,11 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(ReduceJobs jobs) {
   }
 }
 
+// The range audit's hook (dc_lowrank_plan_ranges installs it on its thread).
+thread_local RangeAudit* g_range_audit = nullptr;
+
 hipError_t reduce_partials_multi(const PartialReduce* r, int n, int dtype, hipStream_t stream) {
+  if (auditing()) return hipSuccess;  // plain pointers: no buffer resources to record
   ReduceJobs jobs{};
   int blocks = 0;
   for (int i = 0; i < n; ++i) {

@@ -14,7 +14,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdynconv.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
@@ -36,6 +36,7 @@ SIGNATURES = {
     "dc_lowrank_zeff_bytes": (_c_i64, [_c_i64] * 5 + [_c_int, _c_int]),
     "dc_lowrank_fwd": (_c_int, [_c_vp] * 6 + [_c_i64] + [_c_i64] * 5 + [_c_int, _c_int, _c_vp]),
     "dc_lowrank_bwd_ws_bytes": (_c_i64, [_c_i64] * 5 + [_c_int, _c_int]),
+    "dc_lowrank_plan_ranges": (_c_i64, [_c_i64] * 5 + [_c_int] * 3 + [ctypes.POINTER(_c_i64), _c_i64]),
     "dc_lowrank_bwd": (_c_int, [_c_vp] * 5 + [_c_i64] + [_c_vp] * 6 + [_c_i64] + [_c_i64] * 5
                        + [_c_int, _c_int, _c_vp]),
     "dc_lowrank_fwd_grouped": (_c_int, [_c_i64, _c_vp, _c_i64] + [_c_pp] * 5 + [_c_i64] * 7 + [_c_int, _c_int, _c_vp]),

@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define DC_ABI_VERSION 5
+#define DC_ABI_VERSION 6
 
 /* Largest convolution width and (kernel) rank accepted.  Every width up to 32
  * and kernel rank up to 256 runs on the vectorised / row-ring / matrix-core
@@ -167,6 +167,19 @@ int dc_lowrank_fwd(const void* x, const void* z, const void* U, const void* stat
  * dc_status.  No counterpart in the reference (lowrank.py:14-23, 75-85 and
  * 148-157 autotune tile sizes of one kernel each). */
 int dc_lowrank_path(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int has_static, int bwd);
+
+/* Test hook, no counterpart in the reference: the byte ranges that the
+ * matrix-core and fp32 lowrank kernels of dc_lowrank_fwd (bwd = 0) or
+ * dc_lowrank_bwd (bwd = 1) give their buffer resources for these sizes (with
+ * contiguous, 256-byte aligned tensors), over every pass of the launch plan,
+ * as the kernels compute them before clamping: per pass U, static_w and (in
+ * the backward) the dU partial; per tensor the range of the longest run.
+ * Writes up to max_pairs pairs (bytes, bound) to out, where each count must
+ * lie in [0, bound] for every out-of-range offset the kernel uses to stay out
+ * of range, and returns the number of pairs (0 for the generic kernels), or a
+ * negative dc_status.  Launches nothing and makes no HIP call. */
+int64_t dc_lowrank_plan_ranges(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W, int dtype, int has_static,
+                               int bwd, int64_t* out, int64_t max_pairs);
 
 /* Workspace bytes needed by dc_lowrank_bwd, or a negative dc_status. */
 int64_t dc_lowrank_bwd_ws_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_t W,

@@ -35,7 +35,7 @@ def header_functions():
 
 def test_exports_every_declared_symbol(lib):
     names = header_functions()
-    assert len(names) == 18, names
+    assert len(names) == 19, names
     raw = ctypes.CDLL(_capi.LIB_PATH)
     for n in names:
         assert hasattr(raw, n), f"{n} declared in dynconv.h but not exported"
@@ -43,7 +43,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_strings(lib):
-    assert lib.dc_abi_version() == 5
+    assert lib.dc_abi_version() == 6
     for s in (OK, E_NULL, E_SHAPE, E_DTYPE, E_UNSUP, E_WS, E_ALIGN, E_DEV, E_LAUNCH, E_SCRATCH):
         assert len(lib.dc_status_string(s)) > 0
     assert b"unknown" in lib.dc_status_string(-99)
@@ -348,3 +348,67 @@ def test_proj_in_validation(lib):
         assert fwd() == E_DEV
         assert fwd(G=1, z=arr(P), R=128) == E_DEV
         assert bwd() == E_DEV
+
+
+def _plan_ranges(lib, B, T, D, R, W, dt, st, bwd):
+    """(bytes, bound) pairs of dc_lowrank_plan_ranges for one shape."""
+    import ctypes
+
+    n = lib.dc_lowrank_plan_ranges(B, T, D, R, W, dt, st, bwd, None, 0)
+    assert n >= 0, (B, T, D, R, W, dt, st, bwd, n)
+    buf = (ctypes.c_int64 * (2 * max(n, 1)))()
+    assert lib.dc_lowrank_plan_ranges(B, T, D, R, W, dt, st, bwd, buf, n) == n
+    return [(buf[2 * i], buf[2 * i + 1]) for i in range(n)]
+
+
+def test_plan_buffer_ranges(lib):
+    """Every launch plan of the matrix-core and fp32 lowrank kernels, for every tap and rank pass split
+    at W <= 32 and kernel rank <= 256 (bf16, fp16; fp32 up to its kernel rank 64), forward and backward:
+    each buffer resource's byte count, as the kernels compute it before make_rsrc's clamp, lies in
+    [0, bound], where bound keeps the kernel's out-of-range offsets (a lane's 1 << 30, a tile's 1 << 29
+    less 15 rows of halo) out of range.  A negative count (a pass whose offsets run past its rows, as the
+    static-rank-only fp32 pass once did) or one that reaches an out-of-range offset fails here, on the
+    CPU, before any launch.  Host logic only: the audit launches nothing."""
+    dts = {0: 256, 1: 256, 2: 64}  # dtype: largest kernel rank to enumerate
+    n_pairs = n_plans = 0
+    for dt, rk_max in dts.items():
+        for W in range(1, 33):
+            for rk in list(range(1, 67)) + [95, 96, 97, 127, 128, 129, 160, 200, 255, 256]:
+                if rk > rk_max:
+                    continue
+                for st in (0, 1):
+                    R = rk - st
+                    if R < 1:
+                        continue
+                    for bwd in (0, 1):
+                        for B, T, D in ((2, 100, 256), (1, 50, 72)):
+                            pairs = _plan_ranges(lib, B, T, D, R, W, dt, st, bwd)
+                            n_plans += 1
+                            n_pairs += len(pairs)
+                            for i, (v, bound) in enumerate(pairs):
+                                assert 0 <= v <= bound, (dict(B=B, T=T, D=D, R=R, W=W, dtype=dt, static=st, bwd=bwd),
+                                                         i, v, bound)
+    assert n_plans > 10000 and n_pairs > 10 * n_plans
+
+
+def test_plan_buffer_ranges_long_sequences(lib):
+    """The per-run resources of sequences past 512 MiB of rows (capped runs) and the widest rows:
+    every count within its bound, for the BASELINE shapes at long T and the rank / tap pass splits."""
+    shapes = [(1, 131172, 2048, 15, 4, 1), (1, 131172, 2048, 16, 4, 0), (1, 1 << 20, 4096, 31, 8, 1),
+              (1, 65600, 2048, 127, 4, 1), (1, 32800, 4096, 63, 20, 1), (2, 8192, 4096, 255, 8, 1),
+              (1, 400000, 64, 31, 32, 1)]
+    for B, T, D, R, W, st in shapes:
+        for dt in (0, 1, 2):
+            for bwd in (0, 1):
+                for i, (v, bound) in enumerate(_plan_ranges(lib, B, T, D, R, W, dt, st, bwd)):
+                    assert 0 <= v <= bound, ((B, T, D, R, W, dt, st, bwd), i, v, bound)
+
+
+def test_plan_ranges_catch_a_negative_count(lib):
+    """The audit reports the pre-clamp counts: a plan whose U range would be negative shows up as
+    one.  Checked on the shared count function's arithmetic through a shape that has a static-rank-only
+    pass of ranks at a later pass of taps (fp32 kernel rank 33, W 12: rank pass 2 holds the static rank
+    alone, its tap passes start at kofs > 0) -- the count must be 0 there, not R * uld - kofs * D < 0."""
+    pairs = _plan_ranges(lib, 1, 60, 64, 32, 12, 2, 1, 0)
+    assert pairs and all(0 <= v <= b for v, b in pairs)
+    assert any(v == 0 for v, _ in pairs)  # the empty U range of the static-rank-only pass
