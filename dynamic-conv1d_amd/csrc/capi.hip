@@ -126,7 +126,7 @@ int dc_headwise_fwd(const void* x, const void* weight, const void* static_w, voi
 }
 
 static_assert(DC_PATH_GENERIC == 0 && DC_PATH_VECTOR == 1 && DC_PATH_MFMA == 2 && DC_PATH_F32_MFMA == 3 &&
-                  DC_PATH_F32_VALU == 4 && DC_PATH_WIDE == 5,
+                  DC_PATH_F32_VALU == 4 && DC_PATH_WIDE == 5 && DC_PATH_HEAD_MFMA == 6,
               "dc_path codes returned by hw_path / lr_path");
 
 int dc_headwise_path(int64_t B, int64_t T, int64_t D, int64_t H, int64_t W, int dtype, int has_static, int bwd) {

@@ -5,6 +5,7 @@
 // direction) in headwise_fast_*.hip / headwise_wide_*.hip so they compile in
 // parallel.
 #include "headwise_wide.h"
+#include "headwise_mma.h"
 
 namespace dc {
 
@@ -239,6 +240,62 @@ bool hw_wide_ok(const HwProblem& p, bool bwd) {
   return aligned(p.dy, ea) && aligned(p.dx, ea) && aligned(p.dweight, 16);
 }
 
+// ------------------------------------------------------- head-MFMA path
+// The matrix-core backward (headwise_mma.h): head sizes 16, 32, 64 at
+// 9 <= W <= 32 with whole 16-byte pieces of a wavefront's weight-row segment,
+// bf16 / fp16, D a multiple of 64.  Runs of 16-row tiles; each run's resources
+// reach 32 rows before it and 64 after it (the dy / weight look-ahead).
+int64_t mma_max_run_tiles(const HwProblem& p) {
+  const int64_t rowb = max_row_bytes(p);
+  const int64_t rows = kMaxSeqBytes / rowb - kSeqSlackRows - kRunHaloRows - 64;
+  return rows > 0 ? rows / 16 : 0;
+}
+
+bool hw_mma_ok(const HwProblem& p, bool bwd) {
+  if (!bwd) return false;  // the forward stays on the wide kernels
+  if (p.dtype != kBF16 && p.dtype != kFP16) return false;
+  const int64_t hs = p.D / p.H;
+  if (!hw_mma_width_ok((int)hs, (int)p.W) || p.D % 64 != 0) return false;
+  if (mma_max_run_tiles(p) < 1) return false;
+  // 16-byte pieces of x / dy rows and of the weight rows; dx a 16-bit element at a time
+  return aligned(p.x, 16) && aligned(p.dy, 16) && aligned(p.dx, 2) && aligned(p.weight, 16) &&
+         aligned(p.dweight, 16) && aligned(p.static_w, 2);
+}
+
+// Wavefronts per launch: about six per CU (the LDS of one, 16-36 KiB, allows
+// four to eight); runs of at least one tile.
+constexpr int kMmaTargetWaves = 1536;
+
+HwMmaArgs make_mma_args(const HwProblem& p) {
+  HwMmaArgs a;
+  a.Tn = (int)p.T;
+  a.D = (int)p.D;
+  a.H = (int)p.H;
+  a.nwc = (int)(p.D / 64);
+  const int64_t ntile = (p.T + 15) / 16;
+  int64_t seg = (p.B * ntile * a.nwc + kMmaTargetWaves - 1) / kMmaTargetWaves;
+  if (seg < 1) seg = 1;
+  if (seg > ntile) seg = ntile;
+  const int64_t cap = mma_max_run_tiles(p);  // >= 1 (hw_mma_ok)
+  if (seg > cap) seg = cap;
+  a.seg = (int)seg;
+  a.nspb = (int)((ntile + seg - 1) / seg);
+  a.nseg = (int)(p.B * a.nspb);
+  a.nblk = a.nseg * a.nwc;
+  a.residual = p.residual;
+  return a;
+}
+
+template <typename T>
+hipError_t bwd_mma(const HwProblem& p) {
+  const HwMmaArgs a = make_mma_args(p);
+  const int hs = (int)(p.D / p.H);
+  hipError_t e = p.static_w ? hw_bwd_mma_launch<T, true>(p, a, hs) : hw_bwd_mma_launch<T, false>(p, a, hs);
+  if (e != hipSuccess || !p.static_w) return e;
+  // one dstatic_w partial per run (row of wavefronts)
+  return reduce_partials(p.ws, p.W * p.D, a.nseg, p.W * p.D, p.dstatic_w, p.dtype, p.stream);
+}
+
 template <typename T>
 hipError_t fwd_wide(const HwProblem& p) {
   return dispatch_wide<T, false>(p, make_wide_args(p));
@@ -319,6 +376,8 @@ int64_t hw_bwd_ws_bytes(const HwProblem& p) {
   int P;
   if (hw_fast_ok(p, true))
     P = make_plan(p, true).P;
+  else if (hw_mma_ok(p, true))
+    P = make_mma_args(p).nseg;
   else if (hw_wide_ok(p, true))
     P = (make_wide_args(p).nseg + 3) / 4;
   else
@@ -327,7 +386,7 @@ int64_t hw_bwd_ws_bytes(const HwProblem& p) {
 }
 
 int hw_path(const HwProblem& p, bool bwd) {
-  return hw_fast_ok(p, bwd) ? 1 : hw_wide_ok(p, bwd) ? 5 : 0;
+  return hw_fast_ok(p, bwd) ? 1 : hw_mma_ok(p, bwd) ? 6 : hw_wide_ok(p, bwd) ? 5 : 0;
 }
 
 hipError_t hw_fwd(const HwProblem& p) {
@@ -362,6 +421,7 @@ hipError_t hw_bwd(const HwProblem& p) {
       default: return dispatch_fast<float, true>(p, pl);
     }
   }
+  if (hw_mma_ok(p, true)) return p.dtype == kBF16 ? bwd_mma<bf16>(p) : bwd_mma<fp16>(p);
   if (hw_wide_ok(p, true)) {
     switch (p.dtype) {
       case kBF16: return bwd_wide<bf16>(p);

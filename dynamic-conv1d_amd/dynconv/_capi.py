@@ -79,7 +79,7 @@ def load(path: str = LIB_PATH):
 
 
 # dc_path codes (include/dynconv.h): which kernel family a shape runs on
-PATHS = {0: "generic", 1: "vector", 2: "mfma", 3: "f32_mfma", 4: "f32_valu", 5: "wide"}
+PATHS = {0: "generic", 1: "vector", 2: "mfma", 3: "f32_mfma", 4: "f32_valu", 5: "wide", 6: "head_mfma"}
 
 
 def status_string(status: int) -> str:

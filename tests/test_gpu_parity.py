@@ -158,6 +158,20 @@ HW_EDGE = [
     (2, 200, 256, 32, 16, True, True, torch.float16),   # wide: hs 8, W 16
     (1, 1, 128, 64, 16, True, True, torch.bfloat16),    # wide: T 1
     (1, 50, 256, 2, 9, True, True, torch.bfloat16),     # hs 128 bf16 W 9: 18-byte weight segments, generic
+    # the head matrix-core backward (head sizes 16, 32, 64 at 9 <= W <= 32, whole 16-byte pieces of
+    # a wavefront's weight-row segment): dw on MFMA over the head's channels, the head weights' part
+    # of dx as a banded product, the static filter by row pairs; runs of 16-row tiles, T not a
+    # multiple of 16, T below one tile, runs ending at T
+    (2, 77, 256, 8, 24, True, True, torch.bfloat16),    # hs 32, W 24 (two look-back blocks)
+    (1, 100, 128, 4, 12, False, True, torch.float16),   # hs 32, W 12, no static filter
+    (1, 33, 128, 8, 10, True, False, torch.bfloat16),   # hs 16, W 10 (one look-back block)
+    (2, 50, 192, 12, 32, True, True, torch.float16),    # hs 16, W 32, three wavefront columns
+    (1, 70, 128, 2, 16, True, True, torch.bfloat16),    # hs 64, W 16
+    (1, 9, 64, 1, 24, True, True, torch.bfloat16),      # hs 64, W 24 > T
+    (1, 1, 128, 4, 28, True, False, torch.bfloat16),    # hs 32, T 1
+    (3, 300, 128, 8, 18, False, True, torch.bfloat16),  # hs 16, W 18: two look-ahead blocks, runs of tiles
+    (1, 1000, 64, 2, 32, True, True, torch.float16),    # hs 32, W 32, long runs
+    (2, 64, 128, 4, 20, True, True, torch.bfloat16),    # hs 32, W 20, T a multiple of 16
 ]
 
 
@@ -167,7 +181,8 @@ def test_edge_shapes_headwise(Bn, Tn, Dn, H, W, static, residual, dtype):
     want = ("vector" if W <= 8 and _hw_vector_shape(Dn, H, dtype)
             else "wide" if _hw_wide_shape(Dn, H, W, dtype) else "generic")
     for bwd in (0, 1):
-        assert _path("hw", Bn, Tn, Dn, H, W, dtype, static, bwd) == want
+        w_dir = "head_mfma" if bwd and want != "vector" and _hw_mma_shape(Dn, H, W, dtype) else want
+        assert _path("hw", Bn, Tn, Dn, H, W, dtype, static, bwd) == w_dir
     x = randn(g, Bn, Tn, Dn)
     dy = randn(g, Bn, Tn, Dn)
     w = randn(g, Bn, Tn, H, W, scale=1 / math.sqrt(W))
@@ -222,6 +237,15 @@ def _hw_vector_shape(Dn, H, dtype):
     vec = 16 // torch.tensor([], dtype=dtype).element_size()
     hs = Dn // H
     return Dn % vec == 0 and hs & (hs - 1) == 0 and hs <= 64 * vec
+
+
+def _hw_mma_shape(Dn, H, W, dtype):
+    """Shapes the head matrix-core backward takes (contiguous, aligned tensors): bf16 / fp16, head
+    sizes 16, 32, 64 at 9 <= W <= 32 with whole 16-byte pieces of a 64-channel wavefront's weight-row
+    segment ((64 / hs) * W a multiple of 8), D a multiple of 64."""
+    hs = Dn // H
+    return (dtype in (torch.bfloat16, torch.float16) and hs in (16, 32, 64) and 9 <= W <= 32
+            and (64 // hs) * W % 8 == 0 and Dn % 64 == 0)
 
 
 def _hw_wide_shape(Dn, H, W, dtype):
@@ -522,7 +546,7 @@ def test_long_sequence(kind):
     Bn = 1
     for bwd in (0, 1):
         if kind.startswith("hw"):
-            want = "vector" if W <= 8 else "wide"
+            want = "vector" if W <= 8 else "head_mfma" if bwd else "wide"
             assert _path("hw", Bn, Tn, Dn, Dn // 32, W, dtype, True, bwd) == want
         else:
             want = "f32_mfma" if dtype == torch.float32 else "mfma"
@@ -610,7 +634,8 @@ def test_lowrank_inference_forward(R, static, W, dtype):
 # ------------------------------------------------------------ determinism
 DET_CASES = [  # op, head size (headwise) or kernel rank with the static filter (lowrank), W
     ("hw", 1, 4), ("hw", 32, 4), ("lr", 16, 4),
-    ("hw", 32, 12), ("hw", 4, 24),  # the wide headwise kernels
+    ("hw", 32, 12), ("hw", 4, 24),  # the head matrix-core backward (hs 32), the wide kernels (hs 4)
+    ("hw", 16, 30),
     ("lr", 16, 20),                 # passes of taps into the fp32 dx accumulator
     ("lr", 128, 4), ("lr", 128, 8),  # passes of ranks (at W 8 into the fp32 dx accumulator)
 ]
@@ -629,7 +654,8 @@ def test_deterministic(op, n, W):
     if op == "hw":
         w = randn(g, Bn, Tn, Dn // n, W, scale=0.5).to(torch.bfloat16).to(DEV)
         src, fn = [x, w, sw], hw
-        assert _path("hw", Bn, Tn, Dn, Dn // n, W, torch.bfloat16, True, 1) == ("vector" if W <= 8 else "wide")
+        want = "vector" if W <= 8 else "head_mfma" if _hw_mma_shape(Dn, Dn // n, W, torch.bfloat16) else "wide"
+        assert _path("hw", Bn, Tn, Dn, Dn // n, W, torch.bfloat16, True, 1) == want
     else:
         R = n - 1  # dynamic ranks; the static filter is the last kernel rank
         z = randn(g, Bn, Tn, R).to(torch.bfloat16).to(DEV)
