@@ -241,7 +241,7 @@ bool hw_wide_ok(const HwProblem& p, bool bwd) {
 }
 
 // ------------------------------------------------------- head-MFMA path
-// The matrix-core backward (headwise_mma.h): head sizes 16, 32, 64 at
+// The matrix-core kernels (headwise_mma.h): head sizes 16, 32, 64 at
 // 9 <= W <= 32 with whole 16-byte pieces of a wavefront's weight-row segment,
 // bf16 / fp16, D a multiple of 64.  Runs of 16-row tiles; each run's resources
 // reach 32 rows before it and 64 after it (the dy / weight look-ahead).
@@ -252,14 +252,14 @@ int64_t mma_max_run_tiles(const HwProblem& p) {
 }
 
 bool hw_mma_ok(const HwProblem& p, bool bwd) {
-  if (!bwd) return false;  // the forward stays on the wide kernels
   if (p.dtype != kBF16 && p.dtype != kFP16) return false;
   const int64_t hs = p.D / p.H;
   if (!hw_mma_width_ok((int)hs, (int)p.W) || p.D % 64 != 0) return false;
   if (mma_max_run_tiles(p) < 1) return false;
-  // 16-byte pieces of x / dy rows and of the weight rows; dx a 16-bit element at a time
-  return aligned(p.x, 16) && aligned(p.dy, 16) && aligned(p.dx, 2) && aligned(p.weight, 16) &&
-         aligned(p.dweight, 16) && aligned(p.static_w, 2);
+  // 16-byte pieces of x / dy rows and of the weight rows; y / dx a 16-bit element at a time
+  if (!aligned(p.x, 16) || !aligned(p.weight, 16) || !aligned(p.static_w, 2)) return false;
+  if (!bwd) return aligned(p.y, 2);
+  return aligned(p.dy, 16) && aligned(p.dx, 2) && aligned(p.dweight, 16);
 }
 
 // Wavefronts per launch: about six per CU (the LDS of one, 16-36 KiB, allows
@@ -294,6 +294,13 @@ hipError_t bwd_mma(const HwProblem& p) {
   if (e != hipSuccess || !p.static_w) return e;
   // one dstatic_w partial per run (row of wavefronts)
   return reduce_partials(p.ws, p.W * p.D, a.nseg, p.W * p.D, p.dstatic_w, p.dtype, p.stream);
+}
+
+template <typename T>
+hipError_t fwd_mma(const HwProblem& p) {
+  const HwMmaArgs a = make_mma_args(p);
+  const int hs = (int)(p.D / p.H);
+  return p.static_w ? hw_fwd_mma_launch<T, true>(p, a, hs) : hw_fwd_mma_launch<T, false>(p, a, hs);
 }
 
 template <typename T>
@@ -398,6 +405,7 @@ hipError_t hw_fwd(const HwProblem& p) {
       default: return dispatch_fast<float, false>(p, pl);
     }
   }
+  if (hw_mma_ok(p, false)) return p.dtype == kBF16 ? fwd_mma<bf16>(p) : fwd_mma<fp16>(p);
   if (hw_wide_ok(p, false)) {
     switch (p.dtype) {
       case kBF16: return fwd_wide<bf16>(p);

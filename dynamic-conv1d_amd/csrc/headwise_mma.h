@@ -374,6 +374,219 @@ __global__ __launch_bounds__(64) void hw_bwd_mma(const T* __restrict__ x, const 
 
 namespace dc {
 
+// ------------------------------------------------------------------ forward
+//   y[t,d] = sum_k (w[t,h,k] + sw[k,d]) x[t-k,d]  (+ x[t,d])     headwise.py:24-91
+// Over a tile of 16 rows, per head: y = Wf x with the banded Wf[t][s] =
+// w[t,h,t-s] (0 <= t-s < W) from the tile's own weight rows, a 16x16x16 MFMA per
+// 16-row block of s and 16 channels (x by column from LDS: transposing reads);
+// the static filter and the residual by row pairs on v_dot2c, lane = channel,
+// after the MFMA sums pass through a transposed staging tile.  LDS: a ring of x
+// blocks (the tile and the NBF blocks before it, which hold row t0-W: the
+// padding tap of odd W), the tile's weight rows, the staging tile.
+template <typename T, int W, int HS>
+struct HwMmaFwdGeom {
+  static constexpr int NBF = (W + 15) / 16;         // x look-back blocks
+  static constexpr int NR = NBF + 1;
+  static constexpr int NHW = 64 / HS;
+  static constexpr int XP = 64 * 2 + 16;
+  static constexpr int WPB = NHW * W * 2;
+  static constexpr int BLK = 16 * XP;
+  static constexpr int DXP = 16 * 4 + 16;
+  static constexpr int X0 = 0;
+  static constexpr int W0 = X0 + NR * BLK;          // the tile's weight rows
+  static constexpr int Y0 = W0 + 16 * WPB;          // staging: 64 channels x 16 fp32 rows
+  static constexpr int Z0 = Y0 + 64 * DXP;          // 16 zero bytes
+  static constexpr int BYTES = Z0 + 16;
+  static_assert(WPB % 16 == 0, "whole 16-byte pieces of the heads' weight rows");
+};
+
+template <typename T, int W, int HS, bool STATIC>
+__global__ __launch_bounds__(64) void hw_fwd_mma(const T* __restrict__ x, const T* __restrict__ wt,
+                                                 const T* __restrict__ sw, T* __restrict__ y, HwMmaArgs a) {
+  typedef HwMmaFwdGeom<T, W, HS> G;
+  constexpr int NBF = G::NBF, NR = G::NR, NHW = G::NHW, XP = G::XP, WPB = G::WPB;
+  constexpr int NB = (W - 1 + 15) / 16;        // MFMA blocks of s before the tile's own
+  constexpr int NXQ = (W + 3) / 4;             // 4-row groups of the x columns before t0 (row t0-W included)
+  constexpr int NGX = NXQ + 4;                 // x column groups: rows t0-4*NXQ .. t0+15
+  constexpr int WP2 = (W + 1) / 2;
+  constexpr int WPC = WPB / 16;
+  constexpr int WPIECES = 16 * WPC;
+  constexpr int NWP = (WPIECES + 63) / 64;
+  static_assert(4 * NXQ <= 16 * NBF && NB <= NBF, "x look-back within the ring");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[G::BYTES];
+
+  const int lane = threadIdx.x;
+  const int q = lane >> 4, n = lane & 15;
+  const int lb = xcd_remap(blockIdx.x, a.nblk);
+  const int s = lb % a.nseg, wc = lb / a.nseg;  // consecutive blocks: consecutive runs of one slab
+  const int Tn = a.Tn, D = a.D;
+  const int b = s / a.nspb;
+  const int ntile = (Tn + 15) >> 4;
+  const int m0 = (s - b * a.nspb) * a.seg, m1 = min(m0 + a.seg, ntile);
+  const int c0 = wc * 64;
+  const int rb = run_base_row(m0);
+  const int64_t row0 = (int64_t)b * Tn;
+  const int rowb = D * 2, wrowb = a.H * W * 2;
+  const rsrc_t rx = run_rsrc(x + (row0 + rb) * D, Tn - rb, rowb);
+  const rsrc_t ry = run_rsrc(y + (row0 + rb) * D, Tn - rb, rowb);
+  const rsrc_t rw = run_rsrc(wt + (row0 + rb) * a.H * W, Tn - rb, wrowb);
+  const int wseg = (c0 / HS) * W * 2;
+
+  struct Blk {
+    u32x4 v[2];
+    u32x4 w[NWP];
+  };
+  const int prow = lane >> 3, pcol = (c0 + 8 * (lane & 7)) * 2;
+  auto load_x = [&](int blk, Blk& o) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) o.v[h] = bload128(rx, (16 * blk + prow + 8 * h - rb) * rowb + pcol);
+  };
+  auto load_w = [&](int blk, Blk& o) {
+#pragma unroll
+    for (int i = 0; i < NWP; ++i) {
+      const int p = i * 64 + lane, r = p / WPC, pc = p - r * WPC;
+      o.w[i] = bload128(rw, p < WPIECES ? (16 * blk + r - rb) * wrowb + wseg + pc * 16 : kOobLane);
+    }
+  };
+  auto xslot = [&](int blk) { return (blk + 4 * NR) % NR; };
+  auto store_x = [&](int blk, const Blk& o) {
+    uint8_t* p = lds + G::X0 + xslot(blk) * G::BLK;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) *reinterpret_cast<u32x4*>(p + (prow + 8 * h) * XP + 16 * (lane & 7)) = o.v[h];
+  };
+  auto store_w = [&](const Blk& o) {
+#pragma unroll
+    for (int i = 0; i < NWP; ++i) {
+      const int pi = i * 64 + lane;
+      if (pi < WPIECES) *reinterpret_cast<u32x4*>(lds + G::W0 + pi * 16) = o.w[i];
+    }
+  };
+  auto xa = [&](int r, int cb) { return G::X0 + xslot(r >> 4) * G::BLK + (r & 15) * XP + cb; };
+
+  // static filter of the lane's channel 16q+n as tap pairs in descending order:
+  // (sw[2p+1], sw[2p]) meets the ascending row pair (x[t-2p-1], x[t-2p])
+  const int cl = 16 * q + n;
+  uint32_t swr[STATIC ? WP2 : 1];
+  if constexpr (STATIC) {
+    const rsrc_t rs = make_rsrc(sw, (int64_t)W * D * 2);
+    uint32_t e[2 * WP2];
+#pragma unroll
+    for (int k = 0; k < 2 * WP2; ++k) e[k] = k < W ? bload16(rs, (k * D + c0 + cl) * 2) : 0u;
+#pragma unroll
+    for (int p = 0; p < WP2; ++p) swr[p] = (e[2 * p + 1] & 0xFFFFu) | (e[2 * p] << 16);
+  }
+
+  {
+    Blk t;
+#pragma unroll
+    for (int j = 0; j <= NBF; ++j) {
+      load_x(m0 - NBF + j, t);
+      store_x(m0 - NBF + j, t);
+    }
+    load_w(m0, t);
+    store_w(t);
+    if (lane < 4) *reinterpret_cast<uint32_t*>(lds + G::Z0 + 4 * lane) = 0u;
+  }
+  __syncthreads();
+
+  for (int m = m0; m < m1; ++m) {
+    const int t0 = 16 * m;
+    Blk nb;
+    load_x(m + 1, nb);
+    load_w(m + 1, nb);
+
+    // ---- y from the head weights: C = Wf x per head and 16 channels, K = s blocks
+    {
+      f32x4 c[NHW][HS / 16];
+#pragma unroll
+      for (int h = 0; h < NHW; ++h)
+#pragma unroll
+        for (int j = 0; j < HS / 16; ++j) c[h][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int be = 0; be <= NB; ++be) {
+#pragma unroll
+        for (int h = 0; h < NHW; ++h) {
+          // A[n][4q+e] = w[t0+n, h, t0+n-s] with s = t0-16be+4q+e (0 outside the band)
+          uint32_t e4[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int k = 16 * be + n - 4 * q - e;
+            const int addr = (k >= 0 && k < W) ? G::W0 + n * WPB + (h * W + k) * 2 : G::Z0;
+            e4[e] = *reinterpret_cast<const uint16_t*>(lds + addr);
+          }
+          const u32x2 av = {e4[0] | (e4[1] << 16), e4[2] | (e4[3] << 16)};
+#pragma unroll
+          for (int j = 0; j < HS / 16; ++j) {
+            const int L = lane & 15;
+            const u32x2 bv = lds_read_tr16(lds + xa(t0 - 16 * be + 4 * q + (L >> 2), (h * HS + 16 * j + 4 * (L & 3)) * 2));
+            c[h][j] = Mma16<T>::run(av, bv, c[h][j]);
+          }
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < NHW; ++h)
+#pragma unroll
+        for (int j = 0; j < HS / 16; ++j)
+          *reinterpret_cast<f32x4*>(lds + G::Y0 + (h * HS + 16 * j + n) * G::DXP + 16 * q) = c[h][j];
+    }
+    __syncthreads();
+
+    // ---- vector phase: lane = channel cl of the tile's rows
+    {
+      const int L = lane & 15;
+      const int cb = (16 * q + 4 * (L & 3)) * 2;
+      uint32_t xc[2 * NGX];
+#pragma unroll
+      for (int g = 0; g < NGX; ++g) {
+        const u32x2 v = lds_read_tr16(lds + xa(t0 - 4 * NXQ + 4 * g + (L >> 2), cb));
+        xc[2 * g] = v[0];
+        xc[2 * g + 1] = v[1];
+      }
+      const f32x4* yd = reinterpret_cast<const f32x4*>(lds + G::Y0 + cl * G::DXP);
+      float yv[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 v = yd[g];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) yv[4 * g + i] = v[i];
+      }
+      if (a.residual) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int j = r + 4 * NXQ;  // row t0+r in the column
+          yv[r] += Mma16<T>::to_f(j & 1 ? xc[j >> 1] >> 16 : xc[j >> 1] & 0xFFFFu);
+        }
+      }
+      if constexpr (STATIC) {
+        // y[t0+r] += sum_p (x[t-2p-1], x[t-2p]) . (sw[2p+1], sw[2p])
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+#pragma unroll
+          for (int p = 0; p < WP2; ++p) {
+            const int j = r - 2 * p - 1 + 4 * NXQ;  // first row of the pair in the column
+            const uint32_t xp = (j & 1) ? odd_pair(xc[j >> 1], xc[(j >> 1) + 1]) : xc[j >> 1];
+            yv[r] = Dot2<T>::run(xp, swr[p], yv[r]);
+          }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const T v = (T)yv[r];
+        uint16_t bits;
+        __builtin_memcpy(&bits, &v, 2);
+        __builtin_amdgcn_raw_buffer_store_b16(bits, ry, (t0 + r - rb) * rowb + (c0 + cl) * 2, 0, kNt);
+      }
+    }
+    __syncthreads();
+    store_x(m + 1, nb);
+    store_w(nb);
+    __syncthreads();
+  }
+}
+
+}  // namespace dc
+
+namespace dc {
+
 // Host side (headwise_mma_*.hip instantiate the kernels per dtype and static
 // filter; headwise.hip plans and dispatches).
 // Widths the kernels take at head size hs: a wavefront's weight-row segment,
@@ -384,5 +597,7 @@ constexpr bool hw_mma_width_ok(int hs, int W) {
 
 template <typename T, bool STATIC>
 hipError_t hw_bwd_mma_launch(const HwProblem& p, const HwMmaArgs& a, int hs);
+template <typename T, bool STATIC>
+hipError_t hw_fwd_mma_launch(const HwProblem& p, const HwMmaArgs& a, int hs);
 
 }  // namespace dc

@@ -1,4 +1,4 @@
-// hw_bwd_mma (headwise_mma.h) for bf16, without the static filter: one
+// hw_bwd_mma and hw_fwd_mma (headwise_mma.h) for bf16, without the static filter: one
 // translation unit per dtype and static filter, so the instantiations build in parallel.
 #include "headwise_mma.h"
 
@@ -16,6 +16,25 @@ hipError_t hw_bwd_mma_launch<bf16, false>(const HwProblem& p, const HwMmaArgs& a
   if (hs == HS && p.W == WW) {                                                                           \
     hw_bwd_mma<bf16, WW, HS, false><<<a.nblk, 64, 0, p.stream>>>(x, w, sw, dy, dx, dw, p.ws, a);       \
     return hipGetLastError();                                                                            \
+  }
+  DC_MMA(16, 10) DC_MMA(16, 12) DC_MMA(16, 14) DC_MMA(16, 16) DC_MMA(16, 18) DC_MMA(16, 20)
+  DC_MMA(16, 22) DC_MMA(16, 24) DC_MMA(16, 26) DC_MMA(16, 28) DC_MMA(16, 30) DC_MMA(16, 32)
+  DC_MMA(32, 12) DC_MMA(32, 16) DC_MMA(32, 20) DC_MMA(32, 24) DC_MMA(32, 28) DC_MMA(32, 32)
+  DC_MMA(64, 16) DC_MMA(64, 24) DC_MMA(64, 32)
+#undef DC_MMA
+  return hipErrorInvalidValue;
+}
+
+template <>
+hipError_t hw_fwd_mma_launch<bf16, false>(const HwProblem& p, const HwMmaArgs& a, int hs) {
+  const bf16* x = (const bf16*)p.x;
+  const bf16* w = (const bf16*)p.weight;
+  const bf16* sw = (const bf16*)p.static_w;
+  bf16* y = (bf16*)p.y;
+#define DC_MMA(HS, WW)                                                                  \
+  if (hs == HS && p.W == WW) {                                                          \
+    hw_fwd_mma<bf16, WW, HS, false><<<a.nblk, 64, 0, p.stream>>>(x, w, sw, y, a);      \
+    return hipGetLastError();                                                           \
   }
   DC_MMA(16, 10) DC_MMA(16, 12) DC_MMA(16, 14) DC_MMA(16, 16) DC_MMA(16, 18) DC_MMA(16, 20)
   DC_MMA(16, 22) DC_MMA(16, 24) DC_MMA(16, 26) DC_MMA(16, 28) DC_MMA(16, 30) DC_MMA(16, 32)

@@ -1,4 +1,4 @@
-// hw_bwd_mma (headwise_mma.h) for fp16, without the static filter: one
+// hw_bwd_mma and hw_fwd_mma (headwise_mma.h) for fp16, without the static filter: one
 // translation unit per dtype and static filter, so the instantiations build in parallel.
 #include "headwise_mma.h"
 
@@ -16,6 +16,25 @@ hipError_t hw_bwd_mma_launch<fp16, false>(const HwProblem& p, const HwMmaArgs& a
   if (hs == HS && p.W == WW) {                                                                           \
     hw_bwd_mma<fp16, WW, HS, false><<<a.nblk, 64, 0, p.stream>>>(x, w, sw, dy, dx, dw, p.ws, a);       \
     return hipGetLastError();                                                                            \
+  }
+  DC_MMA(16, 10) DC_MMA(16, 12) DC_MMA(16, 14) DC_MMA(16, 16) DC_MMA(16, 18) DC_MMA(16, 20)
+  DC_MMA(16, 22) DC_MMA(16, 24) DC_MMA(16, 26) DC_MMA(16, 28) DC_MMA(16, 30) DC_MMA(16, 32)
+  DC_MMA(32, 12) DC_MMA(32, 16) DC_MMA(32, 20) DC_MMA(32, 24) DC_MMA(32, 28) DC_MMA(32, 32)
+  DC_MMA(64, 16) DC_MMA(64, 24) DC_MMA(64, 32)
+#undef DC_MMA
+  return hipErrorInvalidValue;
+}
+
+template <>
+hipError_t hw_fwd_mma_launch<fp16, false>(const HwProblem& p, const HwMmaArgs& a, int hs) {
+  const fp16* x = (const fp16*)p.x;
+  const fp16* w = (const fp16*)p.weight;
+  const fp16* sw = (const fp16*)p.static_w;
+  fp16* y = (fp16*)p.y;
+#define DC_MMA(HS, WW)                                                                  \
+  if (hs == HS && p.W == WW) {                                                          \
+    hw_fwd_mma<fp16, WW, HS, false><<<a.nblk, 64, 0, p.stream>>>(x, w, sw, y, a);      \
+    return hipGetLastError();                                                           \
   }
   DC_MMA(16, 10) DC_MMA(16, 12) DC_MMA(16, 14) DC_MMA(16, 16) DC_MMA(16, 18) DC_MMA(16, 20)
   DC_MMA(16, 22) DC_MMA(16, 24) DC_MMA(16, 26) DC_MMA(16, 28) DC_MMA(16, 30) DC_MMA(16, 32)

@@ -254,7 +254,7 @@ def test_headwise_bwd_noalloc_validation(lib):
 def test_kernel_paths(lib):
     """dc_headwise_path / dc_lowrank_path: the kernel family each BASELINE shape and a few edge shapes
     take (0 generic, 1 vector, 2 matrix cores, 3 fp32 matrix cores, 4 fp32 VALU, 5 headwise wide,
-    6 headwise matrix-core backward);
+    6 headwise matrix cores);
     host logic only."""
     bf, f16, f32 = 0, 1, 2
     hp, lp = lib.dc_headwise_path, lib.dc_lowrank_path
@@ -269,8 +269,8 @@ def test_kernel_paths(lib):
         assert hp(1, 50, 64, 16, 12, bf, 1, bwd) == 0          # W 12, D 64: generic
         assert hp(4, 4096, 2048, 2048, 12, bf, 1, bwd) == 5    # W 12, head size 1: wide
         assert hp(4, 4096, 2048, 64, 16, f32, 0, bwd) == 5     # W 16, head size 32: wide
-        assert hp(4, 4096, 2048, 64, 24, bf, 1, bwd) == (6 if bwd else 5)  # W 24, hs 32: the backward on
-        assert hp(4, 4096, 2048, 128, 10, f16, 0, bwd) == (6 if bwd else 5)  # matrix cores (hs 16-64)
+        assert hp(4, 4096, 2048, 64, 24, bf, 1, bwd) == 6      # W 24, hs 32: matrix cores (hs 16-64)
+        assert hp(4, 4096, 2048, 128, 10, f16, 0, bwd) == 6    # W 10, hs 16
         assert hp(4, 4096, 2048, 256, 12, bf, 1, bwd) == 5     # hs 8: the wide kernels in both directions
         assert hp(4, 4096, 2048, 64, 9, bf, 1, bwd) == 0       # hs 32, W 9: segments not in 16-byte pieces
         assert hp(1, 50, 96, 96, 20, bf, 1, bwd) == 0          # W 20, D % 64 != 0: generic

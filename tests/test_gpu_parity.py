@@ -158,7 +158,7 @@ HW_EDGE = [
     (2, 200, 256, 32, 16, True, True, torch.float16),   # wide: hs 8, W 16
     (1, 1, 128, 64, 16, True, True, torch.bfloat16),    # wide: T 1
     (1, 50, 256, 2, 9, True, True, torch.bfloat16),     # hs 128 bf16 W 9: 18-byte weight segments, generic
-    # the head matrix-core backward (head sizes 16, 32, 64 at 9 <= W <= 32, whole 16-byte pieces of
+    # the head matrix-core kernels (head sizes 16, 32, 64 at 9 <= W <= 32, whole 16-byte pieces of
     # a wavefront's weight-row segment): dw on MFMA over the head's channels, the head weights' part
     # of dx as a banded product, the static filter by row pairs; runs of 16-row tiles, T not a
     # multiple of 16, T below one tile, runs ending at T
@@ -180,9 +180,10 @@ def test_edge_shapes_headwise(Bn, Tn, Dn, H, W, static, residual, dtype):
     g = gen(Bn * 1000003 + Tn * 1009 + Dn * 7 + H + W)
     want = ("vector" if W <= 8 and _hw_vector_shape(Dn, H, dtype)
             else "wide" if _hw_wide_shape(Dn, H, W, dtype) else "generic")
+    if want != "vector" and _hw_mma_shape(Dn, H, W, dtype):
+        want = "head_mfma"
     for bwd in (0, 1):
-        w_dir = "head_mfma" if bwd and want != "vector" and _hw_mma_shape(Dn, H, W, dtype) else want
-        assert _path("hw", Bn, Tn, Dn, H, W, dtype, static, bwd) == w_dir
+        assert _path("hw", Bn, Tn, Dn, H, W, dtype, static, bwd) == want
     x = randn(g, Bn, Tn, Dn)
     dy = randn(g, Bn, Tn, Dn)
     w = randn(g, Bn, Tn, H, W, scale=1 / math.sqrt(W))
@@ -240,7 +241,7 @@ def _hw_vector_shape(Dn, H, dtype):
 
 
 def _hw_mma_shape(Dn, H, W, dtype):
-    """Shapes the head matrix-core backward takes (contiguous, aligned tensors): bf16 / fp16, head
+    """Shapes the head matrix-core kernels take (contiguous, aligned tensors): bf16 / fp16, head
     sizes 16, 32, 64 at 9 <= W <= 32 with whole 16-byte pieces of a 64-channel wavefront's weight-row
     segment ((64 / hs) * W a multiple of 8), D a multiple of 64."""
     hs = Dn // H
@@ -546,7 +547,7 @@ def test_long_sequence(kind):
     Bn = 1
     for bwd in (0, 1):
         if kind.startswith("hw"):
-            want = "vector" if W <= 8 else "head_mfma" if bwd else "wide"
+            want = "vector" if W <= 8 else "head_mfma"
             assert _path("hw", Bn, Tn, Dn, Dn // 32, W, dtype, True, bwd) == want
         else:
             want = "f32_mfma" if dtype == torch.float32 else "mfma"
@@ -634,7 +635,7 @@ def test_lowrank_inference_forward(R, static, W, dtype):
 # ------------------------------------------------------------ determinism
 DET_CASES = [  # op, head size (headwise) or kernel rank with the static filter (lowrank), W
     ("hw", 1, 4), ("hw", 32, 4), ("lr", 16, 4),
-    ("hw", 32, 12), ("hw", 4, 24),  # the head matrix-core backward (hs 32), the wide kernels (hs 4)
+    ("hw", 32, 12), ("hw", 4, 24),  # the head matrix-core kernels (hs 32), the wide kernels (hs 4)
     ("hw", 16, 30),
     ("lr", 16, 20),                 # passes of taps into the fp32 dx accumulator
     ("lr", 128, 4), ("lr", 128, 8),  # passes of ranks (at W 8 into the fp32 dx accumulator)
