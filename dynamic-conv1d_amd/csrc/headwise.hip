@@ -262,24 +262,29 @@ bool hw_mma_ok(const HwProblem& p, bool bwd) {
   return aligned(p.dy, 16) && aligned(p.dx, 2) && aligned(p.dweight, 16);
 }
 
-// Wavefronts per launch: about six per CU (the LDS of one, 16-36 KiB, allows
-// four to eight); runs of at least one tile.
-constexpr int kMmaTargetWaves = 1536;
+// Wavefronts per launch, all resident at once (one LDS region of 13-36 KiB and
+// up to 256 VGPRs each): the backward one per SIMD, whose longer runs load
+// their look-back and look-ahead blocks less often, the forward two.  B4 T4096
+// D2048 head size 32 backward / forward: W 12 67 / 34 us, W 24 103 / 42 us;
+// 1536 backward wavefronts 84 / 107 us (runs of 22 and 14 tiles), 2048 backward
+// wavefronts at W 24 135 us (a second round: six fit per CU by LDS).
+constexpr int kMmaBwdWaves = 1024, kMmaFwdWaves = 2048;
 
-HwMmaArgs make_mma_args(const HwProblem& p) {
+HwMmaArgs make_mma_args(const HwProblem& p, bool bwd) {
   HwMmaArgs a;
   a.Tn = (int)p.T;
   a.D = (int)p.D;
   a.H = (int)p.H;
   a.nwc = (int)(p.D / 64);
   const int64_t ntile = (p.T + 15) / 16;
-  int64_t seg = (p.B * ntile * a.nwc + kMmaTargetWaves - 1) / kMmaTargetWaves;
-  if (seg < 1) seg = 1;
-  if (seg > ntile) seg = ntile;
+  // runs per sequence: as many as the target allows, each at least one tile and
+  // at most the resources' cap (tiles are split evenly among them)
+  int64_t nspb = (bwd ? kMmaBwdWaves : kMmaFwdWaves) / (p.B * a.nwc);
+  if (nspb > ntile) nspb = ntile;
   const int64_t cap = mma_max_run_tiles(p);  // >= 1 (hw_mma_ok)
-  if (seg > cap) seg = cap;
-  a.seg = (int)seg;
-  a.nspb = (int)((ntile + seg - 1) / seg);
+  if (nspb < (ntile + cap - 1) / cap) nspb = (ntile + cap - 1) / cap;
+  if (nspb < 1) nspb = 1;
+  a.nspb = (int)nspb;
   a.nseg = (int)(p.B * a.nspb);
   a.nblk = a.nseg * a.nwc;
   a.residual = p.residual;
@@ -288,7 +293,7 @@ HwMmaArgs make_mma_args(const HwProblem& p) {
 
 template <typename T>
 hipError_t bwd_mma(const HwProblem& p) {
-  const HwMmaArgs a = make_mma_args(p);
+  const HwMmaArgs a = make_mma_args(p, true);
   const int hs = (int)(p.D / p.H);
   hipError_t e = p.static_w ? hw_bwd_mma_launch<T, true>(p, a, hs) : hw_bwd_mma_launch<T, false>(p, a, hs);
   if (e != hipSuccess || !p.static_w) return e;
@@ -298,7 +303,7 @@ hipError_t bwd_mma(const HwProblem& p) {
 
 template <typename T>
 hipError_t fwd_mma(const HwProblem& p) {
-  const HwMmaArgs a = make_mma_args(p);
+  const HwMmaArgs a = make_mma_args(p, false);
   const int hs = (int)(p.D / p.H);
   return p.static_w ? hw_fwd_mma_launch<T, true>(p, a, hs) : hw_fwd_mma_launch<T, false>(p, a, hs);
 }
@@ -384,7 +389,7 @@ int64_t hw_bwd_ws_bytes(const HwProblem& p) {
   if (hw_fast_ok(p, true))
     P = make_plan(p, true).P;
   else if (hw_mma_ok(p, true))
-    P = make_mma_args(p).nseg;
+    P = make_mma_args(p, true).nseg;
   else if (hw_wide_ok(p, true))
     P = (make_wide_args(p).nseg + 3) / 4;
   else

@@ -47,8 +47,7 @@ struct HwMmaArgs {
   int D;        // channels (a multiple of 64)
   int H;        // heads
   int nwc;      // D / 64 wavefront columns
-  int seg;      // tiles per run
-  int nspb;     // runs per sequence
+  int nspb;     // runs per sequence: run i of a sequence holds tiles [i*ntile/nspb, (i+1)*ntile/nspb)
   int nseg;     // B * nspb
   int nblk;     // nseg * nwc (one wavefront per workgroup)
   int residual;
@@ -112,7 +111,8 @@ __global__ __launch_bounds__(64) void hw_bwd_mma(const T* __restrict__ x, const 
   const int Tn = a.Tn, D = a.D;
   const int b = s / a.nspb;
   const int ntile = (Tn + 15) >> 4;
-  const int m0 = (s - b * a.nspb) * a.seg, m1 = min(m0 + a.seg, ntile);
+  const int ri = s - b * a.nspb;  // runs split the sequence's tiles evenly (lengths differ by at most one)
+  const int m0 = (int)((int64_t)ri * ntile / a.nspb), m1 = (int)((int64_t)(ri + 1) * ntile / a.nspb);
   const int c0 = wc * 64;
   const int rb = run_base_row(m0);  // resources from the run's first tile less 32 rows
   const int64_t row0 = (int64_t)b * Tn;
@@ -422,7 +422,8 @@ __global__ __launch_bounds__(64) void hw_fwd_mma(const T* __restrict__ x, const 
   const int Tn = a.Tn, D = a.D;
   const int b = s / a.nspb;
   const int ntile = (Tn + 15) >> 4;
-  const int m0 = (s - b * a.nspb) * a.seg, m1 = min(m0 + a.seg, ntile);
+  const int ri = s - b * a.nspb;  // runs split the sequence's tiles evenly (lengths differ by at most one)
+  const int m0 = (int)((int64_t)ri * ntile / a.nspb), m1 = (int)((int64_t)(ri + 1) * ntile / a.nspb);
   const int c0 = wc * 64;
   const int rb = run_base_row(m0);
   const int64_t row0 = (int64_t)b * Tn;

@@ -170,7 +170,8 @@ HW_EDGE = [
     (1, 9, 64, 1, 24, True, True, torch.bfloat16),      # hs 64, W 24 > T
     (1, 1, 128, 4, 28, True, False, torch.bfloat16),    # hs 32, T 1
     (3, 300, 128, 8, 18, False, True, torch.bfloat16),  # hs 16, W 18: two look-ahead blocks, runs of tiles
-    (1, 1000, 64, 2, 32, True, True, torch.float16),    # hs 32, W 32, long runs
+    (1, 1000, 64, 2, 32, True, True, torch.float16),    # hs 32, W 32, runs of one tile
+    (2, 2000, 2048, 64, 32, True, True, torch.float16), # hs 32, W 32, runs of 7-8 tiles, 32 wavefront columns
     (2, 64, 128, 4, 20, True, True, torch.bfloat16),    # hs 32, W 20, T a multiple of 16
 ]
 
