@@ -39,9 +39,9 @@ Also reported:
                again right after the timed ones (an event record holds the GPU
                for ~5 us, so the timed steps carry no per-step events).  From
                profiles/roofline_trace.json (rocprofv3 kernel trace of this
-               command): the kernel alone and kernel start to reduce end.
-               `frac` uses the trace's kernel-only figure when the trace's span
-               is within 5% of the live events, else the live events;
+               command): the kernel alone and kernel start to reduce end,
+               reported beside the live figure (trace_* fields); `achieved`
+               and `frac` always come from this run's live events;
   cpu_baseline the CPU oracle (fp32 restatement of reference.py) on configs[0]
                on this host's cores.
 

@@ -43,6 +43,7 @@ int check_headwise(int64_t B, int64_t T, int64_t D, int64_t H, int64_t W, int dt
   int s = check_btd(B, T, D, W);
   if (s != DC_OK) return s;
   if (H <= 0 || D % H != 0) return DC_ERR_SHAPE;
+  if (W * D > kI32Max) return DC_ERR_SHAPE;  // static_w / dstatic_w columns
   return DC_OK;
 }
 

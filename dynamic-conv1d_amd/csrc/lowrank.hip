@@ -125,55 +125,70 @@ __global__ __launch_bounds__(256) void lr_fwd_generic(const T* __restrict__ x, c
   }
 }
 
-// dx[row, d] = sum_k dy[row+k, d] * Kw[row+k, k, d] (+ dy): the job's rows need
-// z of rows rb .. rb+kGenRows+W-2 (W <= 32).
+// dx[row, d] = sum_k dy[row+k, d] * Kw[row+k, k, d] (+ dy): the job's taps
+// k .. k+kGenTapChunk-1 need z of rows rb+k .. rb+k+kGenRows+kGenTapChunk-2.
+// Up to W = kGenTapChunk those rows are staged once per job; wider W stages
+// them per chunk of taps and per 256 channels, so the channel loop runs the
+// same trip count in every thread (its barriers) and out-of-range channels
+// only skip the arithmetic.
+constexpr int kGenTapChunk = 32;
 template <typename T>
 __global__ __launch_bounds__(256) void lr_bwd_dx_generic(const T* __restrict__ z, const T* __restrict__ U,
                                                          const T* __restrict__ sw, const T* __restrict__ dy,
                                                          T* __restrict__ dx, int64_t BT, int Tn, int D,
                                                          int64_t dxld, int hd, int R, int W, int residual) {
-  __shared__ __attribute__((aligned(16))) float zs[(kGenRows + 31) * kGenMaxR / 4 * 4];
+  __shared__ __attribute__((aligned(16))) float zs[(kGenRows + kGenTapChunk - 1) * kGenMaxR / 4 * 4];
   const int64_t WD = (int64_t)W * D;
   const int rp = (R + 3) / 4 * 4;
-  const int nz = kGenRows + W - 1;
+  const bool restage = W > kGenTapChunk;  // uniform: several chunks of taps
   const int64_t njobs = (BT + kGenRows - 1) / kGenRows;
   for (int64_t job = blockIdx.x; job < njobs; job += gridDim.x) {
     const int64_t rb = job * kGenRows;
-    __syncthreads();
-    stage_zrows(zs, z, rb, nz, R, rp, BT);
-    __syncthreads();
     int tpos[kGenRows];
 #pragma unroll
     for (int i = 0; i < kGenRows; ++i) tpos[i] = rb + i < BT ? (int)((rb + i) % Tn) : -1;
-    for (int d = threadIdx.x; d < D; d += 256) {
+    for (int d0 = 0; d0 < D; d0 += 256) {
+      const int d = d0 + (int)threadIdx.x;
+      const bool dv = d < D;
       float acc[kGenRows];
 #pragma unroll
       for (int i = 0; i < kGenRows; ++i) acc[i] = 0.f;
-      for (int k = 0; k < W; ++k) {
-        float kw[kGenRows];
+      for (int kc = 0; kc < W; kc += kGenTapChunk) {
+        const int kn = min(kGenTapChunk, W - kc);  // taps of this chunk
+        if (restage || d0 == 0) {
+          __syncthreads();  // earlier reads of zs are done
+          stage_zrows(zs, z, rb + kc, kGenRows + kn - 1, R, rp, BT);
+          __syncthreads();
+        }
+        if (!dv) continue;
+        for (int kk = 0; kk < kn; ++kk) {
+          const int k = kc + kk;
+          float kw[kGenRows];
 #pragma unroll
-        for (int i = 0; i < kGenRows; ++i) kw[i] = 0.f;
-        for (int r = 0; r < rp; r += 4) {
-          float u[4];
+          for (int i = 0; i < kGenRows; ++i) kw[i] = 0.f;
+          for (int r = 0; r < rp; r += 4) {
+            float u[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) u[q] = r + q < R ? (float)U[(int64_t)(r + q) * WD + (int64_t)k * D + d] : 0.f;
+            for (int q = 0; q < 4; ++q) u[q] = r + q < R ? (float)U[(int64_t)(r + q) * WD + (int64_t)k * D + d] : 0.f;
+#pragma unroll
+            for (int i = 0; i < kGenRows; ++i) {
+              const float4 zv = *reinterpret_cast<const float4*>(zs + (i + kk) * rp + r);  // row rb+i+k
+              kw[i] = fmaf(zv.x, u[0], kw[i]);
+              kw[i] = fmaf(zv.y, u[1], kw[i]);
+              kw[i] = fmaf(zv.z, u[2], kw[i]);
+              kw[i] = fmaf(zv.w, u[3], kw[i]);
+            }
+          }
+          const float st = sw ? (float)sw[(int64_t)k * D + d] : 0.f;
 #pragma unroll
           for (int i = 0; i < kGenRows; ++i) {
-            const float4 zv = *reinterpret_cast<const float4*>(zs + (i + k) * rp + r);  // row rb+i+k
-            kw[i] = fmaf(zv.x, u[0], kw[i]);
-            kw[i] = fmaf(zv.y, u[1], kw[i]);
-            kw[i] = fmaf(zv.z, u[2], kw[i]);
-            kw[i] = fmaf(zv.w, u[3], kw[i]);
+            const bool in = tpos[i] >= 0 && tpos[i] + k < Tn;  // row rb+i+k in the same sequence
+            const float dv2 = (float)dy[yoff(in ? rb + i + k : rb, d, Tn, D, hd)];
+            if (in) acc[i] = fmaf(dv2, sw ? kw[i] + st : kw[i], acc[i]);
           }
         }
-        const float st = sw ? (float)sw[(int64_t)k * D + d] : 0.f;
-#pragma unroll
-        for (int i = 0; i < kGenRows; ++i) {
-          const bool in = tpos[i] >= 0 && tpos[i] + k < Tn;  // row rb+i+k in the same sequence
-          const float dv = (float)dy[yoff(in ? rb + i + k : rb, d, Tn, D, hd)];
-          if (in) acc[i] = fmaf(dv, sw ? kw[i] + st : kw[i], acc[i]);
-        }
       }
+      if (!dv) continue;
 #pragma unroll
       for (int i = 0; i < kGenRows; ++i) {
         if (tpos[i] < 0) continue;

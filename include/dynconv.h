@@ -51,15 +51,16 @@
 extern "C" {
 #endif
 
-#define DC_ABI_VERSION 6
+#define DC_ABI_VERSION 7
 
 /* Largest convolution width and (kernel) rank accepted.  Every width up to 32
  * and kernel rank up to 256 runs on the vectorised / row-ring / matrix-core
  * kernels, subject to shape and alignment (dc_headwise_path, dc_lowrank_path
- * name the family); the rest take the generic kernels.  Above kernel rank 64
- * the lowrank kernels run as passes of ranks (the forward's at most four
- * passes of ranks x taps, since y is rounded after each). */
-#define DC_MAX_W 32
+ * name the family); the rest, and every width 33 .. DC_MAX_W, take the generic
+ * kernels.  Above kernel rank 64 the lowrank kernels run as passes of ranks
+ * (the forward's at most four passes of ranks x taps, since y is rounded after
+ * each). */
+#define DC_MAX_W 1024
 #define DC_MAX_R 256
 /* Largest number of problems in one grouped lowrank call. */
 #define DC_MAX_GROUPS 4

@@ -43,7 +43,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_strings(lib):
-    assert lib.dc_abi_version() == 6
+    assert lib.dc_abi_version() == 7
     for s in (OK, E_NULL, E_SHAPE, E_DTYPE, E_UNSUP, E_WS, E_ALIGN, E_DEV, E_LAUNCH, E_SCRATCH):
         assert len(lib.dc_status_string(s)) > 0
     assert b"unknown" in lib.dc_status_string(-99)
@@ -60,7 +60,8 @@ def test_headwise_fwd_validation(lib):
     assert hw_fwd(lib, T=-1) == E_SHAPE
     assert hw_fwd(lib, H=3) == E_SHAPE           # 16 % 3 != 0
     assert hw_fwd(lib, H=0) == E_SHAPE
-    assert hw_fwd(lib, W=33) == E_UNSUP          # > DC_MAX_W
+    assert hw_fwd(lib, W=1025) == E_UNSUP        # > DC_MAX_W
+    assert hw_fwd(lib, W=1024, D=1 << 21, H=1 << 21) == E_SHAPE  # W * D columns past int32
     assert hw_fwd(lib, T=1 << 31) == E_SHAPE     # int32 row indexing bound
     assert hw_fwd(lib, x=None) == E_NULL
     assert hw_fwd(lib, y=None) == E_NULL
@@ -104,7 +105,7 @@ def test_lowrank_validation(lib):
     assert lr_fwd(lib, R=0) == E_SHAPE
     assert lr_fwd(lib, R=256, sw=P) == E_UNSUP   # kernel rank 257 > DC_MAX_R
     assert lr_fwd(lib, R=257) == E_UNSUP
-    assert lr_fwd(lib, W=33) == E_UNSUP
+    assert lr_fwd(lib, W=1025) == E_UNSUP
     assert lr_fwd(lib, W=0) == E_SHAPE
     assert lr_fwd(lib, z=None) == E_NULL
     assert lr_fwd(lib, U=P + 1) == E_ALIGN
@@ -126,7 +127,7 @@ def test_lowrank_validation(lib):
     assert zb(2, 8, 16, 0, 4, 0, 1) == E_SHAPE
     need = lib.dc_lowrank_bwd_ws_bytes(2, 8, 16, 4, 4, 0, 1)
     assert need > 0
-    assert lib.dc_lowrank_bwd_ws_bytes(2, 8, 16, 4, 33, 0, 1) == E_UNSUP
+    assert lib.dc_lowrank_bwd_ws_bytes(2, 8, 16, 4, 1025, 0, 1) == E_UNSUP
     assert lib.dc_lowrank_bwd_ws_bytes(2, 8, 16, 127, 12, 0, 1) > 0   # generic kernels: W 12, kernel rank 128
 
     def bwd(zeff=None, nzeff=0, ws=P, nws=need, sw=P, R=4):
@@ -169,7 +170,7 @@ def test_lowrank_grouped_fwd_validation(lib):
     assert lr_fwd_g(lib, x_ld=47) == E_SHAPE               # rows narrower than G*D
     assert lr_fwd_g(lib, x_ld=1 << 31) == E_SHAPE
     assert lr_fwd_g(lib, dt=9) == E_DTYPE
-    assert lr_fwd_g(lib, W=33) == E_UNSUP
+    assert lr_fwd_g(lib, W=1025) == E_UNSUP
     assert lr_fwd_g(lib, x=None) == E_NULL
     assert lr_fwd_g(lib, z=None) == E_NULL
     assert lr_fwd_g(lib, y=arr(P, None, P)) == E_NULL      # a NULL entry
@@ -236,7 +237,7 @@ def test_headwise_bwd_noalloc_validation(lib):
 
     assert call(dt=5) == E_DTYPE
     assert call(H=3) == E_SHAPE
-    assert call(W=33) == E_UNSUP
+    assert call(W=1025) == E_UNSUP
     assert call(dy=None) == E_NULL
     assert call(sw=P, dsw=None) == E_NULL
     assert call(sw=P + 1, dsw=P) == E_ALIGN
@@ -275,6 +276,9 @@ def test_kernel_paths(lib):
         assert hp(4, 4096, 2048, 64, 9, bf, 1, bwd) == 0       # hs 32, W 9: segments not in 16-byte pieces
         assert hp(1, 50, 96, 96, 20, bf, 1, bwd) == 0          # W 20, D % 64 != 0: generic
         assert hp(1, 50, 256, 2, 9, bf, 1, bwd) == 0           # head size 128, W 9: 18-byte segments
+        assert hp(4, 4096, 2048, 64, 33, bf, 1, bwd) == 0      # W 33-1024: generic kernels
+        assert hp(1, 64, 256, 256, 1024, f32, 0, bwd) == 0
+        assert hp(1, 64, 256, 256, 1025, bf, 0, bwd) < 0       # above DC_MAX_W
         assert lp(1, 45, 64, 127, 12, bf, 1, bwd) == 2         # W 12, kernel rank 128: 2 x 2 forward passes
         assert lp(1, 70, 128, 64, 1, bf, 0, bwd) == 2          # kernel rank 64, W 1
         assert lp(1, 40, 128, 40, 2, f16, 0, bwd) == 2         # kernel rank 40, W 2
@@ -308,7 +312,8 @@ def test_kernel_paths(lib):
         assert lp(1, 64, 256, 40, 17, bf, 0, bwd) == 2         # W 17, kernel rank 40: passes of taps
         assert lp(1, 64, 256, 64, 32, bf, 0, bwd) == 2         # W 32, kernel rank 64
         assert lp(1, 64, 256, 65, 4, bf, 0, bwd) == 2          # kernel rank 65: passes of ranks
-        assert lp(1, 64, 256, 16, 33, bf, 0, bwd) < 0          # W 33: above DC_MAX_W
+        assert lp(1, 64, 256, 16, 33, bf, 0, bwd) == 0         # W 33-1024: generic kernels
+        assert lp(1, 64, 256, 16, 1025, bf, 0, bwd) < 0        # W 1025: above DC_MAX_W
     for bwd in (0, 1):                                         # kernel ranks 65-256 as passes of ranks
         assert lp(4, 4096, 2048, 127, 4, bf, 1, bwd) == 2      # (forward 64 per pass, backward 32)
         assert lp(1, 64, 256, 255, 8, f16, 1, bwd) == 2        # kernel rank 256, W 8: 4 forward passes
@@ -323,7 +328,7 @@ def test_kernel_paths(lib):
         assert lp(2, 100, 20, 16, 4, bf, 0, bwd) == 0          # D % 8 != 0: generic
     assert hp(2, 8, 16, 3, 4, bf, 0, 0) == E_SHAPE
     assert lp(2, 8, 16, 0, 4, bf, 0, 0) == E_SHAPE
-    assert lp(2, 8, 16, 4, 33, bf, 0, 1) == E_UNSUP
+    assert lp(2, 8, 16, 4, 1025, bf, 0, 1) == E_UNSUP
 
 
 def test_proj_in_validation(lib):

@@ -173,6 +173,11 @@ HW_EDGE = [
     (1, 1000, 64, 2, 32, True, True, torch.float16),    # hs 32, W 32, runs of one tile
     (2, 2000, 2048, 64, 32, True, True, torch.float16), # hs 32, W 32, runs of 7-8 tiles, 32 wavefront columns
     (2, 64, 128, 4, 20, True, True, torch.bfloat16),    # hs 32, W 20, T a multiple of 16
+    # W 33 .. DC_MAX_W (the reference takes any W, headwise.py:226): the generic kernels
+    (1, 70, 128, 128, 33, True, True, torch.bfloat16),  # hs 1, W 33
+    (2, 50, 128, 4, 48, True, False, torch.float16),    # hs 32, W 48
+    (1, 40, 64, 2, 64, False, True, torch.float32),     # hs 32 fp32, W 64 > T
+    (1, 300, 64, 16, 100, True, True, torch.bfloat16),  # hs 4, W 100
 ]
 
 
@@ -380,6 +385,13 @@ LR_EDGE = [
     # the forward past 4 passes takes the generic kernels (its y would be rounded more often)
     (1, 64, 256, 127, 20, True, True, torch.bfloat16, ("generic", "mfma")),   # 2 x 3 forward passes
     (1, 30, 32, 255, 3, True, False, torch.float32, ("generic", "generic")),  # fp32 kernel rank 256
+    # W 33 .. DC_MAX_W (the reference takes any W, lowrank.py:220): the generic kernels, whose dx
+    # stages z rows per chunk of 32 taps (and per 256 channels) above W 32
+    (1, 70, 128, 16, 33, False, True, torch.bfloat16, ("generic", "generic")),    # W 33: chunks 32 + 1
+    (2, 50, 64, 15, 48, True, True, torch.float16, ("generic", "generic")),       # W 48 > T
+    (1, 100, 128, 3, 64, True, False, torch.float32, ("generic", "generic")),     # fp32, W 64
+    (1, 300, 64, 8, 100, True, True, torch.bfloat16, ("generic", "generic")),     # W 100: 4 chunks
+    (1, 40, 320, 4, 70, False, True, torch.bfloat16, ("generic", "generic")),     # D 320: two channel steps
 ]
 
 
@@ -631,6 +643,49 @@ def test_lowrank_inference_forward(R, static, W, dtype):
                                                         [sw] * 3 if static else None, residual=True)
     for a, b in zip(ys_inf, ys_trn):
         assert torch.equal(a, b.detach())
+
+
+@pytest.mark.parametrize("R,static,W,dtype,passes", [(63, True, 32, torch.bfloat16, 4), (63, True, 32, torch.float16, 4),
+                                                     (64, False, 32, torch.bfloat16, 4), (31, True, 32, torch.bfloat16, 2),
+                                                     (127, True, 16, torch.bfloat16, 4), (127, True, 16, torch.float16, 4)])
+def test_lowrank_forward_pass_rounding(R, static, W, dtype, passes):
+    """The 16-bit forward above W 16 (kernel rank <= 32), above W 8 (ranks 33-64) and above kernel
+    rank 64 runs as `passes` launches, each adding to the y the previous one stored in x's type, so
+    y is rounded `passes` times where the reference rounds once.  Bound on |y - y64| against the
+    oracle's float64 result from the same inputs: u|y64| (the last rounding) + (passes - 1) u S
+    (each earlier rounding of a partial sum, |partial| <= S = |x| + sum_k |K[k]| |x[t-k]|) +
+    (W (R + 1) + 2) 2^-23 S' (fp32 sums, S' as S with |z| |U| for K); u = 2^-8 (bf16), 2^-11 (fp16)."""
+    from oracle.reference_cpu import lowrank_weights_ref
+
+    g = gen(97 + R + W)
+    Bn, Tn, Dn = 2, 256, 256
+    x = randn(g, Bn, Tn, Dn).to(dtype).to(DEV)
+    z = randn(g, Bn, Tn, R).to(dtype).to(DEV)
+    U = randn(g, R, W * Dn, scale=1 / math.sqrt((R + 1) * W)).to(dtype).to(DEV)
+    sw = uniform(g, W, Dn, lo=-1 / math.sqrt(W), hi=1 / math.sqrt(W)).to(dtype).to(DEV) if static else None
+    assert _path("lr", Bn, Tn, Dn, R, W, dtype, static, False) == "mfma"  # the matrix-core passes
+    with torch.no_grad():
+        y = lr_mod._LowrankDynamicConvolutionFn.apply(x, z, U, sw, True).double()
+    d = [None if t is None else t.double() for t in (x, z, U, sw)]
+    y64 = lr_ref(*d, residual=True)
+    K = lowrank_weights_ref(d[1], d[2], Dn) + (0 if sw is None else d[3])
+    Ka = lowrank_weights_ref(d[1].abs(), d[2].abs(), Dn) + (0 if sw is None else d[3].abs())
+    xa = d[0].abs()
+    S, S2 = xa.clone(), xa.clone()
+    for k in range(W):
+        xk = torch.zeros_like(xa)
+        xk[:, k:] = xa[:, :Tn - k]
+        S += K[:, :, k].abs() * xk
+        S2 += Ka[:, :, k] * xk
+    u = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    bound = u * y64.abs() + (passes - 1) * u * S + (W * (R + 1) + 2) * 2.0 ** -23 * S2
+    err = (y - y64).abs()
+    worst = (err / bound).max().item()
+    single = u * y64.abs() + (W * (R + 1) + 2) * 2.0 ** -23 * S2  # what one rounding allows
+    over = (err > single).double().mean().item()
+    print(f"R{R}{'+s' if static else ''} W{W} {dtype}: max err/bound {worst:.3f}, max err/(u S) "
+          f"{(err / (u * S)).max().item():.3f}, share past the one-rounding bound {over:.2e}")
+    assert worst <= 1.0
 
 
 # ------------------------------------------------------------ determinism
