@@ -13,7 +13,9 @@ import threading
 
 import torch
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdynconv.so")
+# DYNCONV_LIB selects another build of the library (the host-sanitizer build in
+# tests/test_host_sanitize.py); by default the in-tree libdynconv.so.
+LIB_PATH = os.environ.get("DYNCONV_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdynconv.so")
 ABI_VERSION = 7
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
