@@ -61,6 +61,7 @@ CASES = [
     (3, 2, 90, 128, 15, 20, True, 8, torch.bfloat16),   # W 20: two forward passes, five backward passes
     (3, 2, 70, 128, 127, 4, True, 8, torch.bfloat16),   # kernel rank 128: passes of ranks (2 forward, 4 backward)
     (2, 1, 50, 64, 63, 6, True, 0, torch.float16),      # kernel rank 64, W 6 (forward in one pass)
+    (2, 2, 40, 64, 15, 40, True, 8, torch.bfloat16),    # W 40: the generic kernels, group by group
 ]
 
 
@@ -325,6 +326,7 @@ HEAD_CASES = [
     (2, 1, 40, 128, 63, 12, True, 64, torch.float16, True),    # kernel rank 64, W 12: forward passes 4 + 8
     (3, 2, 60, 256, 127, 4, True, 64, torch.bfloat16, True),   # kernel rank 128: the second rank pass adds to y
     (2, 2, 45, 128, 15, 12, True, 64, torch.float32, True),    # fp32 W 12: forward passes 4 + 8
+    (2, 1, 40, 128, 15, 36, True, 64, torch.bfloat16, False),  # W 36: generic kernels, head-major y
 ]
 
 

@@ -5,7 +5,8 @@ dstatic_w partial sums) in a fixed device array of the library instead of a
 caller's allocation.  Through the C ABI, on consecutive calls whose second
 input is smaller than the first (the array keeps the last call's contents),
 its outputs must equal dc_headwise_bwd's bitwise: with and without static_w,
-on the vector kernels, the wide ones (W 9-16) and the generic ones (head size 3).
+on the vector kernels, the wide ones (W 9-32), the head matrix-core ones (head
+size 32 at W 12) and the generic ones (head size 3, W 48).
 """
 
 import pytest
@@ -25,6 +26,7 @@ SEQUENCES = [
     [(2, 256, 512, 16, 4, False, True), (1, 64, 256, 8, 2, False, False)],     # no static_w: no scratch
     [(2, 300, 512, 512, 12, True, True), (1, 70, 256, 8, 9, True, False),      # W 9-32: wide kernels
      (1, 50, 128, 32, 24, True, True)],
+    [(2, 300, 512, 16, 12, True, True), (1, 90, 256, 8, 48, True, False)],    # head matrix cores, then W 48: generic
 ]
 
 
