@@ -69,6 +69,9 @@ CASES = {
     "lr_grouped_hd64": _grouped_case(3, 2, 200, 128, 15, 4, 64, torch.bfloat16),
     "lr_r15s_w20": _lr_case(1, 200, 256, 15, 20, True, torch.bfloat16),     # forward passes, fp32 dx rounded once
     "hw_hs4_w24": _hw_case(1, 200, 256, 64, 24, True, torch.bfloat16),      # wide kernels, one channel per lane
+    "hw_hs32_w12": _hw_case(2, 300, 256, 8, 12, True, torch.bfloat16),      # head matrix-core kernels
+    "lr_r127s": _lr_case(1, 200, 256, 127, 4, True, torch.bfloat16),        # passes of kernel ranks
+    "lr_r16_w40": _lr_case(1, 100, 128, 16, 40, False, torch.float16),      # W 40: generic kernels
 }
 
 
