@@ -845,14 +845,14 @@ constexpr BwdShape bwd_shape(int W, int RC, bool wide = false) {
 
 // Taps per backward pass: what one pass's tap-weight and dz operands (registers
 // and LDS) and dU accumulators hold for RC rank chunks.  Wider problems run as
-// consecutive passes of taps kofs .. kofs+taps-1 (see the kernel's kofs): every
-// W <= 8 at every rank <= 64, and W <= 16 at one or two rank chunks, stays on
-// matrix cores, reading x and dy once per pass.  Every pass of a problem takes
-// the same launch shape (bwd_shape: the dU partial rows of all passes line up);
-// one rank chunk above W 8 runs passes of at most 4 taps on 32-channel tiles
-// (bwd_shape's WIDE: two wavefronts per SIMD; passes of 5-8 taps would hold one).
+// consecutive passes of taps kofs .. kofs+taps-1 (see the kernel's kofs),
+// reading x and dy once per pass.  Every pass of a problem takes the same
+// launch shape (bwd_shape: the dU partial rows of all passes line up); one rank
+// chunk above W 8 runs passes of at most 8 taps on 32-channel tiles (bwd_shape's
+// WIDE: 240-250 VGPRs at 8 taps, two wavefronts per SIMD; B4 T4096 D2048 R16
+// W16 backward 271 -> 207 us against passes of 4 taps, W32 670 -> 377 us).
 constexpr int pass_taps(int W, int RC) {
-  return RC == 1 ? (W <= 8 ? W : 4) : RC == 2 ? (W < 4 ? W : 4) : RC == 3 ? (W < 2 ? W : 2) : 1;
+  return RC == 1 ? (W <= 8 ? W : 8) : RC == 2 ? (W < 4 ? W : 4) : RC == 3 ? (W < 2 ? W : 2) : 1;
 }
 constexpr int npasses(int W, int RC) { return (W + pass_taps(W, RC) - 1) / pass_taps(W, RC); }
 
@@ -869,9 +869,9 @@ inline int bwd_rank_passes(const LrProblem& p) {
 }
 
 // More than four passes (ranks x taps) add dx into an fp32 accumulator in the
-// workspace, rounded to dx once by lr_dx_round (above W 16 at one or two rank
-// chunks, above W 8 at three, above W 4 at four; above kernel rank 64 past
-// four rank x tap passes).
+// workspace, rounded to dx once by lr_dx_round (above W 16 at two rank chunks,
+// above W 8 at three, above W 4 at four; above kernel rank 64 past four rank x
+// tap passes; one rank chunk takes at most four passes of 8 taps up to W 32).
 constexpr int kBwdMaxBf16DxPasses = 4;
 inline bool bwd_f32dx(const LrProblem& p) {
   return bwd_rank_passes(p) * npasses((int)p.W, bwd_rc(p)) > kBwdMaxBf16DxPasses;
@@ -1097,7 +1097,7 @@ hipError_t launch_bwd_kernel(const LrBwdArgs& a, hipStream_t stream) {
     return hipGetLastError();
   }
   // later passes of taps: problems of 2+ rank chunks, and one rank chunk at W > 8
-  // (WIDE: passes of at most 4 taps)
+  // (WIDE: passes of at most 8 taps)
   if constexpr (RC >= 2 || WIDE) {
     if (a.accdx) {
       lr_bwd_mfma<T, W, RC, NRW, CPW, true><<<a.nblk, NT, 0, stream>>>(a);
@@ -1113,12 +1113,8 @@ hipError_t launch_bwd_kernel(const LrBwdArgs& a, hipStream_t stream) {
 // problem above W 8.
 template <typename T>
 hipError_t dispatch_bwd_kernel(const LrBwdArgs& a, int wq, int rc, bool wide, bool f32, hipStream_t stream) {
-  if (f32) {  // more than four passes: one or two rank chunks above W 16, three or four above W 8 / 4
-    switch (wq * 4 + rc) {
-      case 5: return launch_bwd_kernel<T, 1, 1, true, true>(a, stream);
-      case 9: return launch_bwd_kernel<T, 2, 1, true, true>(a, stream);
-      case 13: return launch_bwd_kernel<T, 3, 1, true, true>(a, stream);
-      case 17: return launch_bwd_kernel<T, 4, 1, true, true>(a, stream);
+  if (f32) {  // more than four passes: two rank chunks above W 16, three or four above W 8 / 4
+    switch (wq * 4 + rc) {  // (one rank chunk never takes more than four passes)
       case 6: return launch_bwd_kernel<T, 1, 2, false, true>(a, stream);
       case 10: return launch_bwd_kernel<T, 2, 2, false, true>(a, stream);
       case 14: return launch_bwd_kernel<T, 3, 2, false, true>(a, stream);
@@ -1135,6 +1131,10 @@ hipError_t dispatch_bwd_kernel(const LrBwdArgs& a, int wq, int rc, bool wide, bo
       case 2: return launch_bwd_kernel<T, 2, 1, true>(a, stream);
       case 3: return launch_bwd_kernel<T, 3, 1, true>(a, stream);
       case 4: return launch_bwd_kernel<T, 4, 1, true>(a, stream);
+      case 5: return launch_bwd_kernel<T, 5, 1, true>(a, stream);
+      case 6: return launch_bwd_kernel<T, 6, 1, true>(a, stream);
+      case 7: return launch_bwd_kernel<T, 7, 1, true>(a, stream);
+      case 8: return launch_bwd_kernel<T, 8, 1, true>(a, stream);
       default: return hipErrorInvalidValue;
     }
   }

@@ -343,19 +343,20 @@ LR_EDGE = [
     (2, 33, 24, 7, 8, True, True, torch.bfloat16, ("mfma", "mfma")),          # W 8 gather form
     (1, 64, 72, 63, 2, False, True, torch.bfloat16, ("mfma", "mfma")),        # four rank chunks, tap passes
     # 9 <= W <= 16 at one or two rank chunks: the forward in one pass (x rows back to 4q-15), the
-    # backward as passes of at most 4 taps (x read 12 rows before each run in the last pass)
+    # backward as passes of at most 8 taps (one rank chunk) or 4 (two)
     (1, 9, 64, 8, 16, False, True, torch.bfloat16, ("mfma", "mfma")),          # W 16 > T
-    (2, 300, 256, 16, 12, False, True, torch.bfloat16, ("mfma", "mfma")),      # passes 4 + 4 + 4
-    (1, 520, 128, 15, 9, True, False, torch.float16, ("mfma", "mfma")),        # passes 4 + 4 + 1
+    (2, 300, 256, 16, 12, False, True, torch.bfloat16, ("mfma", "mfma")),      # passes 8 + 4
+    (1, 520, 128, 15, 9, True, False, torch.float16, ("mfma", "mfma")),        # passes 8 + 1
     (2, 77, 200, 31, 16, True, True, torch.bfloat16, ("mfma", "mfma")),        # two rank chunks: 4 x 4 taps
     (1, 3300, 256, 3, 13, False, True, torch.bfloat16, ("mfma", "mfma")),      # long runs, padded z
     (1, 64, 512, 20, 10, True, True, torch.float16, ("mfma", "mfma")),         # kernel rank 21: passes 4 + 4 + 2
     # 17 <= W <= 32 at one or two rank chunks: the forward as two passes (taps 0 .. W-17, then the
-    # last 16 added to the stored y, x read W-16 rows earlier), the backward as passes of 4 taps;
-    # long runs reach back up to 31 rows before their first tile (the runs' 32-row halo)
+    # last 16 added to the stored y, x read W-16 rows earlier), the backward as passes of 8 taps (one
+    # rank chunk: at most 4, dx rounded after each) or 4 (two: 5-8 passes into the fp32 dx
+    # accumulator); long runs reach back up to 31 rows before their first tile (the runs' 32-row halo)
     (1, 25, 64, 8, 20, False, True, torch.bfloat16, ("mfma", "mfma")),         # W 20 > T
     (2, 300, 256, 16, 17, True, True, torch.bfloat16, ("mfma", "mfma")),       # forward 1 + 16 taps
-    (1, 3300, 256, 15, 32, True, True, torch.bfloat16, ("mfma", "mfma")),      # W 32: backward 8 passes
+    (1, 3300, 256, 15, 32, True, True, torch.bfloat16, ("mfma", "mfma")),      # W 32: backward 4 passes of 8
     (2, 200, 128, 31, 24, True, False, torch.float16, ("mfma", "mfma")),       # two rank chunks, 8 + 16
     (1, 520, 200, 20, 28, False, True, torch.bfloat16, ("mfma", "mfma")),      # D % 16 != 0, 12 + 16
     (1, 3216, 64, 31, 25, True, True, torch.float16, ("mfma", "mfma")),        # long runs, two rank chunks
@@ -693,7 +694,8 @@ DET_CASES = [  # op, head size (headwise) or kernel rank with the static filter 
     ("hw", 1, 4), ("hw", 32, 4), ("lr", 16, 4),
     ("hw", 32, 12), ("hw", 4, 24),  # the head matrix-core kernels (hs 32), the wide kernels (hs 4)
     ("hw", 16, 30),
-    ("lr", 16, 20),                 # passes of taps into the fp32 dx accumulator
+    ("lr", 16, 20),                 # passes of 8 taps (one rank chunk)
+    ("lr", 32, 20),                 # passes of 4 taps (two rank chunks) into the fp32 dx accumulator
     ("lr", 128, 4), ("lr", 128, 8),  # passes of ranks (at W 8 into the fp32 dx accumulator)
 ]
 
@@ -701,8 +703,9 @@ DET_CASES = [  # op, head size (headwise) or kernel rank with the static filter 
 @pytest.mark.parametrize("op,n,W", DET_CASES, ids=[f"{o}{n}w{w}" for o, n, w in DET_CASES])
 def test_deterministic(op, n, W):
     """Two runs give bitwise equal outputs and gradients: no float atomics anywhere, partial sums in a
-    fixed order (W 12 / 24: the wide headwise kernels; lowrank W 20: passes of taps into the fp32 dx
-    accumulator; kernel rank 128: passes of ranks, at W 8 into the fp32 dx accumulator)."""
+    fixed order (W 12 / 24: the wide headwise kernels; lowrank W 20: passes of taps, at kernel rank 32
+    into the fp32 dx accumulator; kernel rank 128: passes of ranks, at W 8 into the fp32 dx
+    accumulator)."""
     g = gen(5)
     Bn, Tn, Dn = 2, 1024, 512
     x = randn(g, Bn, Tn, Dn).to(torch.bfloat16).to(DEV)
