@@ -275,7 +275,8 @@ template <int RC> struct ZOp<RC, true> { u32x4 v; };
 // group's dx pointer and dxld then address it), above W 16.
 template <typename T, int W, int RC, int NRW, int CPW, bool ACC, bool F32 = false>
 __global__ __launch_bounds__(64 * (256 / CPW) * NRW)
-__attribute__((amdgpu_waves_per_eu(W <= 4 && (RC == 1 || CPW == 32) ? 2 : 1, 8))) void lr_bwd_mfma(LrBwdArgs a) {
+__attribute__((amdgpu_waves_per_eu((W <= 4 && (RC == 1 || CPW == 32)) || (RC == 1 && CPW == 32) ? 2 : 1, 8))) void
+lr_bwd_mfma(LrBwdArgs a) {
   constexpr int NJ = CPW / 16;     // channels per lane
   constexpr int NS = CPW / 32;     // 32-channel K blocks of the dz MFMA
   constexpr int NCW = 256 / CPW;   // channel-chunk wavefronts per run: 256 channels per workgroup
@@ -848,9 +849,11 @@ constexpr BwdShape bwd_shape(int W, int RC, bool wide = false) {
 // consecutive passes of taps kofs .. kofs+taps-1 (see the kernel's kofs),
 // reading x and dy once per pass.  Every pass of a problem takes the same
 // launch shape (bwd_shape: the dU partial rows of all passes line up); one rank
-// chunk above W 8 runs passes of at most 8 taps on 32-channel tiles (bwd_shape's
+// chunk above W 4 runs passes of at most 8 taps on 32-channel tiles (bwd_shape's
 // WIDE: 240-250 VGPRs at 8 taps, two wavefronts per SIMD; B4 T4096 D2048 R16
-// W16 backward 271 -> 207 us against passes of 4 taps, W32 670 -> 377 us).
+// W16 backward 271 -> 207 us against passes of 4 taps, W32 670 -> 377 us; W 5-8
+// in one such pass 90-148 -> 66-103 us against one pass on 64-channel tiles at
+// one wavefront per SIMD).
 constexpr int pass_taps(int W, int RC) {
   return RC == 1 ? (W <= 8 ? W : 8) : RC == 2 ? (W < 4 ? W : 4) : RC == 3 ? (W < 2 ? W : 2) : 1;
 }
@@ -887,20 +890,24 @@ inline bool bwd_f32dx(const LrProblem& p) {
 int bwd_plan(const LrProblem& p, BwdPass* out) {
   const int RK = (int)(p.R + (p.static_w ? 1 : 0)), W = (int)p.W, rc = bwd_rc(p);
   const int nrp = bwd_rank_passes(p), step = nrp > 1 ? kBwdRankPass : RK;
-  const int wp = pass_taps(W, rc), ntp = npasses(W, rc);
+  const int ntp = npasses(W, rc);
   if (nrp * ntp > kBwdMaxPlan) return -1;
   int n = 0;
   for (int i = 0; i < nrp; ++i) {
     const int rofs = i * step, rk = RK - rofs < step ? RK - rofs : step;
     const int rd = (int)p.R - rofs < 0 ? 0 : ((int)p.R - rofs < rk ? (int)p.R - rofs : rk);
-    for (int t = 0; t < ntp; ++t) {
+    // taps split as evenly as the pass count allows, the longer passes first
+    // (each at most wp): a pass costs about one sweep of x, dy and dx plus its
+    // taps' products, so W 9 as 5 + 4 beats 8 + 1
+    for (int t = 0, kofs = 0; t < ntp; ++t) {
       BwdPass& b = out[n++];
       b.rofs = rofs;
       b.R = rd;
       b.RK = rk;
-      b.kofs = t * wp;
-      b.W = W - b.kofs < wp ? W - b.kofs : wp;
+      b.kofs = kofs;
+      b.W = W / ntp + (t < W % ntp ? 1 : 0);
       b.slot = t;
+      kofs += b.W;
     }
   }
   return n;
@@ -923,7 +930,7 @@ namespace {
 LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   LrBwdArgs a;
   const int rc = bwd_rc(p);
-  const BwdShape sh = bwd_shape(pass_taps((int)p.W, rc), rc, rc == 1 && p.W > 8);  // every pass has the same shape
+  const BwdShape sh = bwd_shape(pass_taps((int)p.W, rc), rc, rc == 1 && p.W > 4);  // every pass has the same shape
   const int ncw = 256 / sh.cpw;
   a.Tn = (int)p.T;
   a.D = (int)p.D;
@@ -1096,7 +1103,7 @@ hipError_t launch_bwd_kernel(const LrBwdArgs& a, hipStream_t stream) {
       lr_bwd_mfma<T, W, RC, NRW, CPW, false, true><<<a.nblk, NT, 0, stream>>>(a);
     return hipGetLastError();
   }
-  // later passes of taps: problems of 2+ rank chunks, and one rank chunk at W > 8
+  // later passes of taps: problems of 2+ rank chunks, and one rank chunk above W 8
   // (WIDE: passes of at most 8 taps)
   if constexpr (RC >= 2 || WIDE) {
     if (a.accdx) {
@@ -1108,9 +1115,9 @@ hipError_t launch_bwd_kernel(const LrBwdArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// One pass's kernel for wq taps and rc rank chunks (the instantiated pairs:
-// pass_taps(W, RC) and the last pass's remainder); wide: a one-rank-chunk
-// problem above W 8.
+// One pass's kernel for wq taps and rc rank chunks (the instantiated pairs: up
+// to pass_taps(W, RC) taps, as bwd_plan splits them); wide: a one-rank-chunk
+// problem above W 4.
 template <typename T>
 hipError_t dispatch_bwd_kernel(const LrBwdArgs& a, int wq, int rc, bool wide, bool f32, hipStream_t stream) {
   if (f32) {  // more than four passes: two rank chunks above W 16, three or four above W 8 / 4
@@ -1141,7 +1148,6 @@ hipError_t dispatch_bwd_kernel(const LrBwdArgs& a, int wq, int rc, bool wide, bo
 #define DC_LR_CASE(WW, CC) \
   if (wq == WW && rc == CC) return launch_bwd_kernel<T, WW, CC>(a, stream);
   DC_LR_CASE(1, 1) DC_LR_CASE(2, 1) DC_LR_CASE(3, 1) DC_LR_CASE(4, 1)
-  DC_LR_CASE(5, 1) DC_LR_CASE(6, 1) DC_LR_CASE(7, 1) DC_LR_CASE(8, 1)
   DC_LR_CASE(1, 2) DC_LR_CASE(2, 2) DC_LR_CASE(3, 2) DC_LR_CASE(4, 2)
   DC_LR_CASE(1, 3) DC_LR_CASE(2, 3)
   DC_LR_CASE(1, 4)
@@ -1217,7 +1223,7 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
       audit_bwd_pass(b, f.W, f32);
       continue;
     }
-    if ((e = dispatch_bwd_kernel<T>(b, f.W, rc, rc == 1 && p[0].W > 8, f32, p[0].stream)) != hipSuccess) return e;
+    if ((e = dispatch_bwd_kernel<T>(b, f.W, rc, rc == 1 && p[0].W > 4, f32, p[0].stream)) != hipSuccess) return e;
   }
   if (f32 && (e = launch_dx_round<T>(p, G, w.dxf_off)) != hipSuccess) return e;
   PartialReduce jobs[kMaxReduceJobs];
