@@ -132,6 +132,26 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)clamp_rsrc_bytes(bytes, MAX),
                                            0x00020000);
 }
+// make_rsrc for a base and count that are the same in every lane of the
+// wavefront (a row, run or tile of the wavefront), both passed through
+// readfirstlane.  The descriptor must sit in scalar registers.  When the
+// compiler computes a uniform count on the vector unit (64-bit clamps and
+// products do), it cannot prove the result uniform.  It then wraps every
+// access through the resource in a readfirstlane loop over the lanes' distinct
+// descriptors, and the register allocator has placed copies at the start of
+// such a loop's exit block, before exec is restored, where they run with no
+// lane enabled (lost values: the fp16 W 16 head-size-1 headwise backward lost
+// a dx ring slot that way).  Callers guarantee the uniformity.
+template <int64_t MAX = kRsrcMaxBytes>
+__device__ __forceinline__ rsrc_t make_rsrc_wave(const void* base, int64_t bytes) {
+  static_assert(MAX > 0 && MAX < (int64_t(1) << 31), "a range the 32-bit record count holds");
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+  const int n = __builtin_amdgcn_readfirstlane((int)clamp_rsrc_bytes(bytes, MAX));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0, n,
+                                           0x00020000);
+}
 template <int POL = 0>
 __device__ __forceinline__ u32x4 bload128(rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL); }
 template <int POL = 0>

@@ -93,7 +93,7 @@ struct WideRun {
 // row, so the unrolled row blocks hold no per-row offsets in vector registers.
 template <typename P>
 __device__ __forceinline__ rsrc_t row_rsrc(P* p0, int64_t row_elems, int t, bool live, int rowb) {
-  return make_rsrc(p0 + (live ? (int64_t)t * row_elems : 0), live ? rowb : 0);
+  return make_rsrc_wave(p0 + (live ? (int64_t)t * row_elems : 0), live ? rowb : 0);
 }
 
 // N consecutive elements of T from LDS, starting at element e0, as floats.

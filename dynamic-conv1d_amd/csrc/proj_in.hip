@@ -80,8 +80,8 @@ __global__ __launch_bounds__(256 * KS) void proj_fwd(ProjArgs a) {
   const int m0 = (blk * 4 + rt) * 16;
   const int rows = max(min(M - m0, 16), 0);
   // rows m0 .. m0+15 of pre_z: rows past M and K past the end read 0
-  const rsrc_t rp = make_rsrc<kProjOob>(a.pre + (int64_t)max(min(m0, M), 0) * K, (int64_t)rows * K * 2);
-  const rsrc_t rw = make_rsrc<kProjOob>(a.w, (int64_t)N * K * 2);
+  const rsrc_t rp = make_rsrc_wave<kProjOob>(a.pre + (int64_t)max(min(m0, M), 0) * K, (int64_t)rows * K * 2);
+  const rsrc_t rw = make_rsrc_wave<kProjOob>(a.w, (int64_t)N * K * 2);
   const int prow = n * K * 2;  // the lane's row in rp
 
   f32x4 acc[NB];
@@ -206,8 +206,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 6 ? 2
   const int tile0 = run * a.seg, tile1 = min(tile0 + a.seg, ntile);
   const int r0 = tile0 * 16;
   const int nrow = max(min(M - r0, (tile1 - tile0) * 16), 0);
-  const rsrc_t rp = make_rsrc<kProjOob>(a.pre + (int64_t)min(r0, M) * K, (int64_t)nrow * K * 2);
-  const rsrc_t rd = make_rsrc<kProjOob>(a.dpre + (int64_t)min(r0, M) * K, (int64_t)nrow * K * 2);
+  const rsrc_t rp = make_rsrc_wave<kProjOob>(a.pre + (int64_t)min(r0, M) * K, (int64_t)nrow * K * 2);
+  const rsrc_t rd = make_rsrc_wave<kProjOob>(a.dpre + (int64_t)min(r0, M) * K, (int64_t)nrow * K * 2);
   // the lane's row-4q channels in pre_z / dpre_z; lanes past K (chv false)
   // take kProjOob alone, never kProjOob plus a row offset (that sum would
   // overflow int32 and wrap back into the range)
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 6 ? 2
   // step s, channel j: ranks 32s + 8q .. +7 of channel col + j, packed.
   u32x4 wop[N32][4];
   {
-    const rsrc_t rw = make_rsrc<kProjOob>(a.w, (int64_t)N * K * 2);
+    const rsrc_t rw = make_rsrc_wave<kProjOob>(a.w, (int64_t)N * K * 2);
 #pragma unroll
     for (int s = 0; s < N32; ++s) {
       u32x2 rows8[8];
@@ -335,7 +335,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 6 ? 2
   }
 
   // dW_in partial of this run: rank 16c + 4q + i, channels col .. col+3
-  const rsrc_t rpart = make_rsrc<kProjOob>(a.part + (int64_t)run * N * K, (int64_t)N * K * 4);
+  const rsrc_t rpart = make_rsrc_wave<kProjOob>(a.part + (int64_t)run * N * K, (int64_t)N * K * 4);
 #pragma unroll
   for (int c = 0; c < NB; ++c)
 #pragma unroll

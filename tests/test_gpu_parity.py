@@ -158,6 +158,13 @@ HW_EDGE = [
     (2, 200, 256, 32, 16, True, True, torch.float16),   # wide: hs 8, W 16
     (1, 1, 128, 64, 16, True, True, torch.bfloat16),    # wide: T 1
     (1, 50, 256, 2, 9, True, True, torch.bfloat16),     # hs 128 bf16 W 9: 18-byte weight segments, generic
+    # fp16 W 16 head size 1 without a static filter: the dx of every row 16k + 15 came out wrong.
+    # The row resources were built from vector registers, every access went through a per-lane
+    # descriptor loop, and two register copies landed where no lane was enabled (found by a random
+    # sweep; resources now uniform by construction).  Also the same shape with the residual and in bf16.
+    (1, 40, 256, 256, 16, False, False, torch.float16),
+    (2, 64, 128, 128, 16, False, True, torch.float16),
+    (1, 40, 256, 256, 16, False, True, torch.bfloat16),
     # the head matrix-core kernels (head sizes 16, 32, 64 at 9 <= W <= 32, whole 16-byte pieces of
     # a wavefront's weight-row segment): dw on MFMA over the head's channels, the head weights' part
     # of dx as a banded product, the static filter by row pairs; runs of 16-row tiles, T not a
