@@ -696,6 +696,53 @@ def test_lowrank_forward_pass_rounding(R, static, W, dtype, passes):
     assert worst <= 1.0
 
 
+@pytest.mark.parametrize("R,static,W,dtype,passes", [(40, True, 5, torch.bfloat16, 3), (40, True, 7, torch.bfloat16, 4),
+                                                     (64, True, 1, torch.bfloat16, 3), (16, False, 16, torch.bfloat16, 2),
+                                                     (31, True, 8, torch.float16, 2), (40, True, 7, torch.float16, 4)])
+def test_lowrank_backward_pass_rounding(R, static, W, dtype, passes):
+    """The 16-bit backward of 2-4 passes (taps, or ranks above kernel rank 64) adds each pass's dx
+    to what the previous one stored in x's type (more passes go through an fp32 accumulator), so dx
+    is rounded `passes` times where the reference rounds once.  Bound on |dx - dx64| against the
+    oracle's float64 gradient from the same inputs: u|dx64| + (passes - 1) u S + (W (R + 1) + 2)
+    2^-23 S, with S = |dy| + sum_k |dy[t+k]| (|z| |U| + |static_w|)[t+k, k] (every partial sum of
+    ranks and taps is at most S); u = 2^-8 (bf16), 2^-11 (fp16).  A random sweep of large shapes
+    met single entries (of 10^6-10^7) just past the elementwise 2e-2 bar this way, where the exact
+    dx is near zero and the partials are several units: within this bound and the reference's own
+    bf16 tolerance (test.py:17)."""
+    from oracle.reference_cpu import lowrank_weights_ref
+
+    g = gen(193 + R + W)
+    Bn, Tn, Dn = 2, 256, 256
+    x = randn(g, Bn, Tn, Dn).to(dtype).to(DEV)
+    z = randn(g, Bn, Tn, R).to(dtype).to(DEV)
+    U = randn(g, R, W * Dn, scale=1 / math.sqrt((R + 1) * W)).to(dtype).to(DEV)
+    sw = uniform(g, W, Dn, lo=-1 / math.sqrt(W), hi=1 / math.sqrt(W)).to(dtype).to(DEV) if static else None
+    dy = randn(g, Bn, Tn, Dn).to(dtype).to(DEV)
+    for bwd in (0, 1):
+        assert _path("lr", Bn, Tn, Dn, R, W, dtype, static, bwd) == "mfma"
+    xk = x.clone().requires_grad_()
+    lr_mod._LowrankDynamicConvolutionFn.apply(xk, z, U, sw, True).backward(dy)
+    dx = xk.grad.double()
+    d = [None if t is None else t.double() for t in (x, z, U, sw)]
+    xr = d[0].clone().requires_grad_()
+    lr_ref(xr, *d[1:], residual=True).backward(dy.double())
+    dx64 = xr.grad
+    Ka = lowrank_weights_ref(d[1].abs(), d[2].abs(), Dn) + (0 if sw is None else d[3].abs())
+    dya = dy.double().abs()
+    S = dya.clone()  # the residual's term
+    for k in range(W):
+        t = torch.zeros_like(dya)
+        t[:, :Tn - k] = dya[:, k:] * Ka[:, k:, k]
+        S += t
+    u = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    bound = u * dx64.abs() + (passes - 1) * u * S + (W * (R + 1) + 2) * 2.0 ** -23 * S
+    err = (dx - dx64).abs()
+    worst = (err / bound).max().item()
+    print(f"R{R}{'+s' if static else ''} W{W} {dtype} ({passes} passes): max err/bound {worst:.3f}, "
+          f"max err/(u S) {(err / (u * S)).max().item():.3f}")
+    assert worst <= 1.0
+
+
 # ------------------------------------------------------------ determinism
 DET_CASES = [  # op, head size (headwise) or kernel rank with the static filter (lowrank), W
     ("hw", 1, 4), ("hw", 32, 4), ("lr", 16, 4),
