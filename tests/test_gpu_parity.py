@@ -597,6 +597,56 @@ def test_long_sequence(kind):
     check_reductions("hw" if kind.startswith("hw") else "lr", q, dyq, g_k, dtype)
 
 
+HUGE = {  # kind: T, D, heads (headwise) or rank (lowrank), W, static_w
+    "hw32": ((1 << 20) + 100, 2048, 64, 4, True),
+    "hw1": ((1 << 20) + 100, 2048, 2048, 4, True),   # weight and dweight of 2^33 + elements
+    "lr16": ((1 << 20) + 100, 2048, 16, 4, False),
+    "lr31s": ((1 << 19) + 50, 4096, 31, 4, True),    # the z_eff writer, two rank chunks
+}
+
+
+@pytest.mark.parametrize("kind", list(HUGE))
+def test_past_2_31_elements(kind):
+    """x (and y, dy, dx) past 2^31 elements, headwise weights past 2^33 (about 60 GB of device
+    memory at hs1): the vector and matrix-core kernels address every row through per-run buffer
+    resources whose bases are 64-bit.  Rows at both ends and around element 2^31 against the CPU
+    oracle on windows of the same inputs (with the W-1 rows of halo on each side)."""
+    dtype = torch.bfloat16
+    Tn, Dn, HR, W, static = HUGE[kind]
+    assert Tn * Dn > 1 << 31
+    g = torch.Generator(device=DEV).manual_seed(7)
+    x = torch.randn(1, Tn, Dn, device=DEV, generator=g, dtype=dtype)
+    dy = torch.randn(1, Tn, Dn, device=DEV, generator=g, dtype=dtype)
+    sw = ((torch.rand(W, Dn, device=DEV, generator=g) * 2 - 1) / math.sqrt(W)).to(dtype) if static else None
+    if kind.startswith("hw"):
+        mid = [(torch.randn(1, Tn, HR, W, device=DEV, generator=g) / math.sqrt(W)).to(dtype)]
+        fn, ref, per_row = hw, hw_ref, [True]
+        assert _path("hw", 1, Tn, Dn, HR, W, dtype, static, 1) == "vector"
+    else:
+        mid = [torch.randn(1, Tn, HR, device=DEV, generator=g, dtype=dtype),
+               (torch.randn(HR, W * Dn, device=DEV, generator=g) / math.sqrt((HR + 1) * W)).to(dtype)]
+        fn, ref, per_row = lr, lr_ref, [True, False]
+        assert _path("lr", 1, Tn, Dn, HR, W, dtype, static, 1) == "mfma"
+    src = [x] + mid + [sw]
+    leaves = [None if t is None else t.detach().requires_grad_() for t in src]
+    y = fn(*leaves, residual=True)
+    y.backward(dy)
+    torch.cuda.synchronize()
+    rows = [True] + per_row + [False]  # inputs cut to the window (z with x; U and static_w whole)
+    edge = (1 << 31) // Dn
+    for w0, w1 in [(0, 64), (edge - 40, edge + 40), (Tn - 64, Tn)]:
+        a, e = max(0, w0 - W + 1), min(Tn, w1 + W - 1)
+        win = [None if t is None else (t[:, a:e] if r else t).float().cpu() for t, r in zip(src, rows)]
+        y_w, g_w = run_fwd_bwd(ref, win, dy[:, a:e].float().cpu(), True)
+        sl = slice(w0 - a, w1 - a)
+        assert_ns(y[:, w0:w1], y_w[:, sl], dtype, f"{kind} y[{w0}:{w1}]")
+        assert_ns(leaves[0].grad[:, w0:w1], g_w[0][:, sl], dtype, f"{kind} dx[{w0}:{w1}]")
+        assert_ns(leaves[1].grad[:, w0:w1], g_w[1][:, sl], dtype, f"{kind} d1[{w0}:{w1}]",
+                  elementwise=kind.startswith("hw"))
+    del x, dy, sw, mid, src, leaves, y
+    torch.cuda.empty_cache()
+
+
 def test_generic_lowrank_rows_past_2_24():
     """The generic lowrank kernels (D = 4 is off the matrix-core paths, which take whole
     8-channel pieces) over more than 2^24 rows: the per-row dz launch loops over rows with a capped
