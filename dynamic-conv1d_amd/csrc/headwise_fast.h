@@ -534,9 +534,11 @@ __global__ __launch_bounds__(256) void hw_bwd_fast(const T* __restrict__ x, cons
     };
 
     if constexpr (HSV == 1) {
-      // Head size 1 carries W weights per channel: two chunks in flight would
-      // hold the kernel at one wavefront per SIMD.  One chunk per wavefront and
-      // two wavefronts per SIMD hide the loads better (hs1 backward 158 -> 155 us).
+      // Head size 1 carries W weights per channel: one chunk in flight per
+      // wavefront.  The launch has one wavefront per SIMD either way; the two
+      // alternating chunk buffers of larger heads take 256 VGPRs + 128 AGPRs
+      // here and measured slower (B4 T4096 D2048 W4 bf16 backward, static and
+      // residual: 143 -> 149.5 us; without both: 137.6 -> 142.2 us).
       for (int tc = t0; tc < tend; tc += U) {
         Chunk c;
         load_chunk(tc, c);
