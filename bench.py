@@ -112,6 +112,9 @@ EXTRA = {
     # its bytes per microsecond
     "lr_r128": dict(kind="lr", B=4, T=4096, D=2048, R=127, W=4, static=True, residual=True),
     "lr_r32_b4": dict(kind="lr", B=4, T=4096, D=2048, R=31, W=4, static=True, residual=True),
+    # kernel rank 64 (R 63 + static): the forward in one pass of four rank chunks, the backward as
+    # two passes of 32 ranks (four passes of one tap each before: 327 us)
+    "lr_r64_b4": dict(kind="lr", B=4, T=4096, D=2048, R=63, W=4, static=True, residual=True),
     # the reference bench.py's own shapes (bench.py:7-12): head sizes 1, 4, 16 and rank 16, no static_w, no residual
     "ref_hw_hs1": dict(kind="hw", B=4, T=4096, D=2048, H=2048, W=4, static=False, residual=False),
     "ref_hw_hs4": dict(kind="hw", B=4, T=4096, D=2048, H=512, W=4, static=False, residual=False),

@@ -422,7 +422,8 @@ bool lr_mfma_ok(const LrProblem& p, bool bwd) {
   // above kernel rank 64 (up to 256) as passes of ranks: the forward as passes of
   // 64 (each split into passes of at most 8 taps), at most kFwdMaxPasses of
   // them in all, since y is rounded after each; the backward as passes of 32
-  // (any number: past four its dx goes to an fp32 accumulator)
+  // (also at kernel ranks 49-64 from W 2 on, lr_bwd_rank_split; any number:
+  // past four its dx goes to an fp32 accumulator)
   const int64_t RK = p.R + (p.static_w ? 1 : 0);
   if (RK > kLrMfmaMaxRank) return false;
   if (!bwd && lr_fwd_npasses(p) > kFwdMaxPasses) return false;
@@ -451,8 +452,10 @@ int64_t lr_zeff_bytes(const LrProblem& p) {
   // z_eff: the backward pads z itself (one small launch next to its passes)
   if (rc > 4) return 0;
   // the backward reads z itself when its rows are what the kernel loads: R % 4
-  // == 0 (8-byte loads) or, for two rank chunks, exactly 32 dynamic ranks
-  const bool pad = rc == 2 ? !(p.R == 32 && !has_static) : p.R % 4 != 0;
+  // == 0 (8-byte loads) or, for two rank chunks and passes of 32 ranks, a
+  // multiple of 32 dynamic ranks (16-byte loads)
+  const bool k32 = rc == 2 || lr_bwd_rank_split(p.R + (has_static ? 1 : 0), p.W);
+  const bool pad = k32 ? !(p.R % 32 == 0 && !has_static) : p.R % 4 != 0;
   return pad ? p.B * p.T * lr_bwd_zrow(p.R, has_static) * 2 : 0;
 }
 

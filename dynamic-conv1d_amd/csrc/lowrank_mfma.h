@@ -205,12 +205,19 @@ inline int64_t run_tiles_cap(int64_t rowb) {
   return rows > 0 ? rows / 16 : 0;
 }
 
+// The backward runs passes of 32 kernel ranks on the two-rank-chunk kernels
+// above kernel rank 64, and from W 2 on at kernel ranks 49-64, where four rank
+// chunks hold the operands of one tap per pass: B4 T4096 D2048 R63 + static W4
+// then takes two passes (32 + 32 ranks, 4 taps each) instead of four.
+inline bool lr_bwd_rank_split(int64_t RK, int64_t W) { return RK > 64 || (RK > 48 && W >= 2); }
+
 // Ranks per row of the backward's padded z_eff copy: the kernel rank RK rounded
-// up to 4, or 32 for two rank chunks (17 <= RK <= 32), or above 64 up to 32.
+// up to 4, or 32 for two rank chunks (17 <= RK <= 32), or above 48 up to a
+// multiple of 32 (the passes of 32 ranks read 32 of a row's ranks, 16 bytes
+// per lane; four rank chunks in one pass read any multiple of 4).
 inline int64_t lr_bwd_zrow(int64_t R, bool has_static) {
   const int64_t rk = R + (has_static ? 1 : 0);
-  // above 64: passes of 32 ranks, each reading 32 of the row's ranks (16 bytes per lane)
-  if (rk > 64) return (rk + 31) / 32 * 32;
+  if (rk > 48) return (rk + 31) / 32 * 32;
   return rk > 16 && rk <= 32 ? 32 : (rk + 3) / 4 * 4;
 }
 
@@ -248,7 +255,7 @@ int lr_fwd_npasses(const LrProblem& p);
 
 // Passes of the matrix-core backward (lowrank_mfma_bwd.hip, bwd_plan): kernel
 // ranks rofs .. rofs+RK-1 (R dynamic) and taps kofs .. kofs+W-1, dz partials in
-// slot `slot`.  Above kernel rank 64 the ranks run as passes of 32.
+// slot `slot`.  Where lr_bwd_rank_split holds the ranks run as passes of 32.
 struct BwdPass {
   int rofs, R, RK, kofs, W, slot;
 };

@@ -859,16 +859,17 @@ constexpr int pass_taps(int W, int RC) {
 }
 constexpr int npasses(int W, int RC) { return (W + pass_taps(W, RC) - 1) / pass_taps(W, RC); }
 
-// Rank chunks of a problem's launch shape: up to kernel rank 64 its own
-// (one to four), above it passes of kBwdRankPass ranks on the two-chunk kernels.
+// Rank chunks of a problem's launch shape: its own (one to four), or passes of
+// kBwdRankPass ranks on the two-chunk kernels where lr_bwd_rank_split holds.
 constexpr int kBwdRankPass = 32;
+inline bool bwd_rank_split(const LrProblem& p) { return lr_bwd_rank_split(p.R + (p.static_w ? 1 : 0), p.W); }
 inline int bwd_rc(const LrProblem& p) {
   const int rk = (int)(p.R + (p.static_w ? 1 : 0));
-  return rk > 64 ? 2 : (rk + 15) / 16;
+  return bwd_rank_split(p) ? 2 : (rk + 15) / 16;
 }
 inline int bwd_rank_passes(const LrProblem& p) {
   const int rk = (int)(p.R + (p.static_w ? 1 : 0));
-  return rk > 64 ? (rk + kBwdRankPass - 1) / kBwdRankPass : 1;
+  return bwd_rank_split(p) ? (rk + kBwdRankPass - 1) / kBwdRankPass : 1;
 }
 
 // More than four passes (ranks x taps) add dx into an fp32 accumulator in the
@@ -1169,8 +1170,8 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
   a.dxld = (int)p[0].dxld();
   a.yhd = (int)p[0].yhd();
   // z itself when its rows are what the kernel reads: R % 4 == 0 and 8-byte
-  // aligned, or (two rank chunks, and passes of 32 ranks above 64) rows of a
-  // multiple of 32 dynamic ranks without the static one, 16-byte aligned.
+  // aligned, or (two rank chunks, and passes of 32 ranks) rows of a multiple
+  // of 32 dynamic ranks without the static one, 16-byte aligned.
   const bool K32 = rc == 2;
   bool zvec = K32 ? (p[0].R % 32 == 0 && p[0].static_w == nullptr) : p[0].R % 4 == 0;
   for (int g = 0; g < G; ++g) {

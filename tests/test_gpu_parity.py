@@ -329,11 +329,15 @@ LR_EDGE = [
     (1, 100, 128, 31, 20, True, True, torch.float32, ("f32_mfma", "f32_mfma")),   # 5 tap x 2 rank passes
     (1, 3300, 64, 7, 32, True, False, torch.float32, ("f32_mfma", "f32_mfma")),   # W 32, long runs
     (1, 5, 64, 3, 9, False, True, torch.float32, ("f32_mfma", "f32_mfma")),       # W 9 > T
-    # matrix-core plans with three and four rank chunks (kernel ranks 33-64 at W 1-2)
+    # matrix-core plans with three and four rank chunks (kernel ranks 33-64 at W 1-2); from W 2 on,
+    # kernel ranks 49-64 take the backward as passes of 32 ranks on the two-chunk kernels
     (1, 70, 128, 64, 1, False, True, torch.bfloat16, ("mfma", "mfma")),      # <W1, 4 chunks>
-    (2, 50, 256, 63, 2, True, True, torch.bfloat16, ("mfma", "mfma")),       # <W2, 4 chunks>: backward in 2 passes
+    (2, 50, 256, 63, 2, True, True, torch.bfloat16, ("mfma", "mfma")),       # <W2, kernel rank 64>: 2 rank passes
     (1, 40, 128, 40, 2, False, False, torch.float16, ("mfma", "mfma")),      # <W2, 3 chunks>
     (2, 60, 128, 40, 1, True, True, torch.bfloat16, ("mfma", "mfma")),       # <W1, 3 chunks>, kernel rank 41
+    (1, 90, 128, 48, 4, True, True, torch.bfloat16, ("mfma", "mfma")),       # kernel rank 49: 32 + 16 and the static
+    (2, 40, 256, 64, 3, False, False, torch.float16, ("mfma", "mfma")),      # 64 dynamic ranks: z itself, 2 passes
+    (1, 77, 128, 52, 6, False, True, torch.bfloat16, ("mfma", "mfma")),      # kernel rank 52, W 6: 2 x 2 passes
     # wide W x rank: the backward runs passes of taps (x shifted by each pass's first tap,
     # dx accumulated, dz partials per pass), the forward stages every tap's operands
     (2, 70, 128, 31, 8, True, True, torch.bfloat16, ("mfma", "mfma")),       # W 8, 2 chunks: 2 passes
@@ -859,14 +863,15 @@ def test_generic_matches_vector_path():
 # ------------------------------------------------- padded z copy from the forward
 @pytest.mark.parametrize("R,static,xoff,zoff", [(15, True, 0, 0), (31, True, 0, 0), (3, False, 0, 0), (28, False, 0, 0),
                                                 (15, True, 4, 0), (63, True, 0, 0), (37, False, 4, 0), (15, True, 0, 1),
-                                                (31, True, 4, 1)])
+                                                (31, True, 4, 1), (50, True, 0, 0), (52, False, 0, 1)])
 def test_lowrank_zeff_saved(R, static, xoff, zoff):
     """The forward's padded z copy (z, the static column as 1, zero ranks up to RP) feeds the
     backward exactly as the copy the backward builds itself: bitwise equal gradients.  xoff = 4
     puts x 8 bytes off 16-byte alignment: the forward takes its element-aligned kernels and
     fills the copy in a launch of its own (the padding kernel), the backward stays on matrix
     cores.  zoff = 1 starts z 2 bytes into its buffer (rows not 4-byte aligned); R 63 and 37
-    pad to 64 and 40 ranks."""
+    pad to 64 and 40 ranks; kernel ranks 51 and 52 to 64 (the backward's passes of 32 ranks read
+    16 bytes of a row per lane, so even R % 4 == 0 takes the copy)."""
     from dynconv import _capi
 
     lib = _capi.load()
@@ -881,7 +886,7 @@ def test_lowrank_zeff_saved(R, static, xoff, zoff):
     sw = uniform(g, W, Dn, lo=-0.5, hi=0.5).to(bf).to(DEV) if static else None
     dy = randn(g, Bn, Tn, Dn).to(bf).to(DEV)
     rk = R + (1 if static else 0)
-    rp = 32 if 16 < rk <= 32 else (rk + 3) // 4 * 4
+    rp = 32 if 16 < rk <= 32 else ((rk + 31) // 32 * 32 if rk > 48 else (rk + 3) // 4 * 4)
     nz = lib.dc_lowrank_zeff_bytes(Bn, Tn, Dn, R, W, 0, int(static))
     assert nz == Bn * Tn * rp * 2
     zeff = torch.full((nz,), 0xAB, dtype=torch.uint8, device=DEV)  # the forward overwrites all of it
