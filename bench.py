@@ -20,14 +20,14 @@ Also reported:
   breakdown    per configuration and direction, the average C-ABI launch
                sequence: back-to-back launches rotating over enough
                independent input sets that each launch's data is out of the
-               256 MB MALL, between one pair of HIP events; plus configs[4]
+               256 MB MALL, between one pair of HIP events (every set
+               launched once before; the median of three such averages); plus configs[4]
                (lowrank QKV) at its own shape, as 3 calls and as one grouped
                call reading x out of the fused [B, T, 3D] projection, the fp32
                tier, the reference bench.py's own shapes (ref_*: head
                sizes 1, 4, 16 and rank 16, no static_w, no residual), lowrank
-               W 16, W 20 and W 12 at rank 40 and headwise W 12 and W 24 on their wide
-               kernels, and one shape on the generic kernels (lowrank kernel
-               rank 128);
+               W 16, W 20 and W 12 at rank 40, kernel ranks 64 and 128 (passes of
+               ranks) and headwise W 12 and W 24 on their wide kernels;
   qkv          configs[4] end to end through autograd (forward + backward):
                the README's pattern (split the fused projection, .contiguous()
                each slice, three calls; autograd concatenates dq, dk, dv)
@@ -96,20 +96,20 @@ EXTRA = {
     # the fp32 tier (reference test.py's 1e-5 cases) at the B4 shapes
     "hw_hs32_fp32": dict(kind="hw", B=4, T=4096, D=2048, H=64, W=4, static=True, residual=True, dtype="fp32"),
     "lr_r16_fp32": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=4, static=False, residual=True, dtype="fp32"),
-    # W 16 at rank 16: the forward in one pass over the taps, the backward as four passes of 4 taps
+    # W 16 at rank 16: the forward in one pass over the taps, the backward as two passes of 8 taps
     "lr_W16": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=16, static=False, residual=True),
     # headwise above W 8: the wide row-ring kernels (head sizes 1 and 32, static filter, residual)
     "hw_W12_hs1": dict(kind="hw", B=4, T=4096, D=2048, H=2048, W=12, static=True, residual=True),
     "hw_W12_hs32": dict(kind="hw", B=4, T=4096, D=2048, H=64, W=12, static=True, residual=True),
     # above W 16 the wide kernels keep one channel per lane
     "hw_W24_hs32": dict(kind="hw", B=4, T=4096, D=2048, H=64, W=24, static=True, residual=True),
-    # W 20: the forward as two passes of taps (4 + 16), the backward as five passes of 4
+    # W 20: the forward as two passes of taps (4 + 16), the backward as three passes (7 + 7 + 6)
     "lr_W20": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=20, static=False, residual=True),
     # W 12 at kernel rank 40 (three rank chunks): the forward as passes of 4 + 8 taps, the backward as six of 2
     "lr_W12_r40": dict(kind="lr", B=4, T=4096, D=2048, R=40, W=12, static=False, residual=True),
     # kernel rank 128 (R 127 + static): the forward as two passes of 64 ranks, the backward as four
-    # passes of 32 (the generic kernels took 1.9 + 15.0 ms here), and rank 32 at the same shape for
-    # its bytes per microsecond
+    # passes of 32 (the generic kernels took 1.9 + 15.0 ms here), and kernel rank 32 at the same shape
+    # for its bytes per microsecond
     "lr_r128": dict(kind="lr", B=4, T=4096, D=2048, R=127, W=4, static=True, residual=True),
     "lr_r32_b4": dict(kind="lr", B=4, T=4096, D=2048, R=31, W=4, static=True, residual=True),
     # kernel rank 64 (R 63 + static): the forward in one pass of four rank chunks, the backward as
@@ -332,18 +332,25 @@ def abi_launchers(c, sets, torch):
     return fwd, bwd
 
 
-def time_launches(torch, launch, nsets, reps):
-    """Average duration of one launch sequence: `reps` back-to-back launches rotating over `nsets`
-    input sets between one pair of HIP events on torch's current stream (the launch stream)."""
-    launch(0)
+def time_launches(torch, launch, nsets, reps, rounds=3):
+    """Duration of one launch sequence: the median over `rounds` of the average of `reps`
+    back-to-back launches rotating over `nsets` input sets, between one pair of HIP events on
+    torch's current stream (the launch stream).  Every set is launched once first, so that no
+    timed launch is the first to touch its freshly allocated outputs and workspace (a configs[4]
+    backward call read 139 us that way against 130-132 us once warm)."""
+    for i in range(nsets):
+        launch(i)
     torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for i in range(reps):
-        launch(i % nsets)
-    e.record()
-    e.synchronize()
-    return s.elapsed_time(e) * 1e3 / reps  # us
+    avg = []
+    for _ in range(rounds):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for i in range(reps):
+            launch(i % nsets)
+        e.record()
+        e.synchronize()
+        avg.append(s.elapsed_time(e) * 1e3 / reps)  # us
+    return statistics.median(avg)
 
 
 def calibrate_copy(torch, dev, mib=256, reps=3):
