@@ -240,14 +240,16 @@ int64_t lr_bwd_max_run_tiles(const LrProblem& p);
 
 // Passes of the matrix-core forward (lowrank_mfma_fwd.hip, fwd_plan): kernel
 // ranks rofs .. rofs+RK-1 (R of them dynamic) and taps kofs .. kofs+W-1;
-// accy: add to the y the earlier passes stored.  Above kernel rank
-// kFwdRankPass the ranks run as passes of that many.  lr_mfma_ok admits at
+// accy: add to the y the earlier passes stored.  Above fwd_rank_pass(W)
+// kernel ranks the ranks run as passes of that many.  lr_mfma_ok admits at
 // most kFwdMaxPasses passes: y is rounded to the output type after each.
 struct FwdPass {
   int rofs, R, RK, kofs, W;
   bool accy;
 };
-constexpr int kFwdRankPass = 64;
+// Kernel ranks per forward pass: 128 up to W 4 (the W x 8 staged operand
+// chunks take up to 128 KiB of LDS, on 8-wavefront workgroups), else 64.
+constexpr int fwd_rank_pass(int W) { return W <= 4 ? 128 : 64; }
 constexpr int kFwdMaxPasses = 4;
 constexpr int kFwdMaxPlan = 64;  // room for every W <= 32, kernel rank <= 256 plan (rejected past kFwdMaxPasses)
 int fwd_plan(const LrProblem& p, FwdPass* out);  // number of passes, or -1

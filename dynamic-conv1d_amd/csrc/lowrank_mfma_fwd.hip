@@ -34,17 +34,17 @@ constexpr int fwd_pass_taps(int rc) { return rc <= 2 ? 16 : 8; }
 // above W 8 at three or four) run as passes of taps: taps 0 .. W0-1 as a
 // W0-tap problem (residual and z_eff included), then passes of P =
 // fwd_pass_taps taps, each on x read kofs rows earlier and added to the stored
-// y (accy).  Above kernel rank 64, passes of kFwdRankPass kernel ranks (z
+// y (accy).  Above fwd_rank_pass(W) kernel ranks, passes of that many (z
 // columns rofs .. of its rows, U rows rofs .., the static rank in the pass that
 // holds index R), each split into passes of at most 8 taps, every pass after
 // the first adding to the stored y.  y is rounded to the output type after
 // each pass; lr_mfma_ok admits at most kFwdMaxPasses of them.
 int fwd_plan(const LrProblem& p, FwdPass* out) {
-  const int RK = (int)(p.R + (p.static_w ? 1 : 0)), W = (int)p.W;
-  const bool ranks = RK > kFwdRankPass;
+  const int RK = (int)(p.R + (p.static_w ? 1 : 0)), W = (int)p.W, RP = fwd_rank_pass(W);
+  const bool ranks = RK > RP;
   int n = 0;
-  for (int rofs = 0; rofs < RK; rofs += kFwdRankPass) {
-    const int rk = RK - rofs < kFwdRankPass ? RK - rofs : kFwdRankPass;  // kernel ranks of the pass
+  for (int rofs = 0; rofs < RK; rofs += RP) {
+    const int rk = RK - rofs < RP ? RK - rofs : RP;  // kernel ranks of the pass
     const int rd = (int)p.R - rofs < 0 ? 0 : ((int)p.R - rofs < rk ? (int)p.R - rofs : rk);  // dynamic ones
     const int P = ranks ? 8 : fwd_pass_taps((rk + 15) / 16);
     const int nt = W <= P ? 1 : (W + P - 1) / P, w0 = W - (nt - 1) * P;
@@ -88,6 +88,11 @@ hipError_t dispatch_pass(const LrProblem* pp, int G) {
   DC_LR_CASE(6, 1) DC_LR_CASE(6, 2) DC_LR_CASE(6, 3) DC_LR_CASE(6, 4)
   DC_LR_CASE(7, 1) DC_LR_CASE(7, 2) DC_LR_CASE(7, 3) DC_LR_CASE(7, 4)
   DC_LR_CASE(8, 1) DC_LR_CASE(8, 2) DC_LR_CASE(8, 3) DC_LR_CASE(8, 4)
+  // kernel ranks 65-128 in one pass up to W 4 (fwd_rank_pass)
+  DC_LR_CASE(1, 5) DC_LR_CASE(1, 6) DC_LR_CASE(1, 7) DC_LR_CASE(1, 8)
+  DC_LR_CASE(2, 5) DC_LR_CASE(2, 6) DC_LR_CASE(2, 7) DC_LR_CASE(2, 8)
+  DC_LR_CASE(3, 5) DC_LR_CASE(3, 6) DC_LR_CASE(3, 7) DC_LR_CASE(3, 8)
+  DC_LR_CASE(4, 5) DC_LR_CASE(4, 6) DC_LR_CASE(4, 7) DC_LR_CASE(4, 8)
 #undef DC_LR_CASE
   if (p.W > 8) return lr_fwd_wide_dispatch<T>(pp, G);
   return hipErrorInvalidValue;

@@ -1,9 +1,10 @@
 // The lowrank forward (lowrank_mfma_fwd_kernel.h) as an accumulating pass
 // (ACC: the tile's y rows, as the earlier passes stored them, are added before
-// the store) at W <= 8 and one to four rank chunks: the passes of 8 taps of
-// problems above W 8 at three or four rank chunks, and every pass after the
-// first of a problem above kernel rank 64 (passes of 64 ranks).  Its own
-// translation unit, so these instantiations build in parallel with the rest.
+// the store) at W <= 8 and one to four rank chunks (up to eight at W <= 4):
+// the passes of 8 taps of problems above W 8 at three or four rank chunks, and
+// every pass after the first of a problem above fwd_rank_pass(W) kernel ranks
+// (passes of 128 ranks up to W 4, of 64 above).  Its own translation unit, so
+// these instantiations build in parallel with the rest.
 #include "lowrank_mfma_fwd_launch.h"
 
 namespace dc {
@@ -23,6 +24,10 @@ hipError_t lr_fwd_acc_dispatch(const LrProblem* pp, int G) {
   DC_LR_CASE(6, 1) DC_LR_CASE(6, 2) DC_LR_CASE(6, 3) DC_LR_CASE(6, 4)
   DC_LR_CASE(7, 1) DC_LR_CASE(7, 2) DC_LR_CASE(7, 3) DC_LR_CASE(7, 4)
   DC_LR_CASE(8, 1) DC_LR_CASE(8, 2) DC_LR_CASE(8, 3) DC_LR_CASE(8, 4)
+  DC_LR_CASE(1, 5) DC_LR_CASE(1, 6) DC_LR_CASE(1, 7) DC_LR_CASE(1, 8)
+  DC_LR_CASE(2, 5) DC_LR_CASE(2, 6) DC_LR_CASE(2, 7) DC_LR_CASE(2, 8)
+  DC_LR_CASE(3, 5) DC_LR_CASE(3, 6) DC_LR_CASE(3, 7) DC_LR_CASE(3, 8)
+  DC_LR_CASE(4, 5) DC_LR_CASE(4, 6) DC_LR_CASE(4, 7) DC_LR_CASE(4, 8)
 #undef DC_LR_CASE
   return hipErrorInvalidValue;
 }

@@ -63,13 +63,19 @@ struct LrArgs {
   LrFwdGroup grp[kMaxGroups];
 };
 
+// Wavefronts per forward workgroup: 4, or 8 where the staged operands (W x RC
+// x 4 KiB) exceed 80 KiB, so that the one workgroup a CU then holds still
+// keeps two wavefronts per SIMD (four would leave one).  Each wavefront runs
+// its own row run on the workgroup's 128-channel chunk.
+constexpr int fwd_wg_waves(int W, int RC) { return W * RC > 20 ? 8 : 4; }
+
 // Packed B operands of one 128-channel chunk, staged once per workgroup:
 // ub[(k*RC + c)*8 + j][lane] = U_eff[16c + 4q + kk, k*D + dl + j], kk = 0..3.
 template <int W, int RC>
 __device__ __forceinline__ void stage_u(u32x2* __restrict__ lds, const uint16_t* __restrict__ U,
                                         const uint16_t* __restrict__ sw, int R, int RK, int D, int64_t WD, int dl,
                                         bool chv, int q, int lane, int wave) {
-  for (int kc = wave; kc < W * RC; kc += 4) {
+  for (int kc = wave; kc < W * RC; kc += fwd_wg_waves(W, RC)) {
     const int k = kc / RC, c = kc - k * RC;
     u32x4 rows[4];
 #pragma unroll
@@ -107,9 +113,11 @@ __device__ __forceinline__ void stage_u(u32x2* __restrict__ lds, const uint16_t*
 // pass of kernel ranks (above 64: z columns and U rows from the pass's first
 // rank, kofs 0 unless taps are split as well).
 template <typename T, int W, int RC, bool ZV, bool ZE, bool ILP = false, bool ACC = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZE && W <= 4 && RC <= 2 ? 4 : 1, 8)))
+__global__ __launch_bounds__(64 * fwd_wg_waves(W, RC))
+__attribute__((amdgpu_waves_per_eu(ZE && W <= 4 && RC <= 2 ? 4 : 1, 8)))
 void lr_fwd_mfma(LrArgs a) {
   constexpr int NR = W + 3;  // x rows 4q-W+1 .. 4q+3 of a lane
+  constexpr int NWV = fwd_wg_waves(W, RC);
   typedef ZRaw<T, RC, ZV> ZR;
   __shared__ u32x2 ub[W * RC * 8 * 64];
 
@@ -123,14 +131,14 @@ void lr_fwd_mfma(LrArgs a) {
   const uint16_t* __restrict__ U = reinterpret_cast<const uint16_t*>(pick(a.grp, g, &LrFwdGroup::U));
   const uint16_t* __restrict__ sw = reinterpret_cast<const uint16_t*>(pick(a.grp, g, &LrFwdGroup::sw));
   uint16_t* __restrict__ y = reinterpret_cast<uint16_t*>(pick(a.grp, g, &LrFwdGroup::y));
-  const int chunk = lb % a.nch, sgp = lb / a.nch;  // 4 wavefronts: one chunk, 4 consecutive runs
+  const int chunk = lb % a.nch, sgp = lb / a.nch;  // NWV wavefronts: one chunk, NWV consecutive runs
   const int D = a.D, Tn = a.Tn, R = a.R, RK = a.RK;
   const int dl = chunk * 128 + 8 * n;  // first channel of the lane's octet
   const bool chv = dl < D;             // D % 8 == 0: octets are whole
   stage_u<W, RC>(ub, U, sw, R, RK, D, a.uld, dl, chv, q, lane, wave);
   __syncthreads();
 
-  const int sg = sgp * 4 + wave;
+  const int sg = sgp * NWV + wave;
   if (sg >= a.nseg) return;
   const int b = sg / a.nspb;
   const int ntile = (Tn + 15) >> 4;

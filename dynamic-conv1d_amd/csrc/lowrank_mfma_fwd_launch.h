@@ -25,7 +25,7 @@ inline int fwd_target_waves(const LrProblem& p) {
 // launches (B2 T8192 D4096 R31 + static: 61.5 us at 4096, 72 us at 2048).
 constexpr int kFwdIlpWaves = 2 * 4 * 256;
 
-inline LrArgs make_args(const LrProblem& p, int target_waves) {
+inline LrArgs make_args(const LrProblem& p, int target_waves, int wg_waves) {
   LrArgs a;
   a.Tn = (int)p.T;
   a.D = (int)p.D;
@@ -47,7 +47,7 @@ inline LrArgs make_args(const LrProblem& p, int target_waves) {
   a.seg = (int)seg;
   a.nspb = (int)((ntile + seg - 1) / seg);
   a.nseg = (int)(p.B * a.nspb);
-  a.nblk = ((a.nseg + 3) / 4) * a.nch;
+  a.nblk = ((a.nseg + wg_waves - 1) / wg_waves) * a.nch;
   a.uld = p.uld();
   a.kofs = p.kofs;
   return a;
@@ -55,9 +55,10 @@ inline LrArgs make_args(const LrProblem& p, int target_waves) {
 
 template <typename T, int W, int RC, bool ACC = false>
 hipError_t launch_fwd(const LrProblem* p, int G) {
+  constexpr int NWV = fwd_wg_waves(W, RC), NT = 64 * NWV;
   int waves = fwd_target_waves(p[0]);
   if (RC == 1 && W <= 8 && !p[0].zeff && waves > kFwdIlpWaves) waves = kFwdIlpWaves;
-  LrArgs a = make_args(p[0], waves);
+  LrArgs a = make_args(p[0], waves, NWV);
   a.nblk1 = a.nblk;
   a.nblk = G * a.nblk1;
   a.xld = (int)p[0].xld();
@@ -83,27 +84,31 @@ hipError_t launch_fwd(const LrProblem* p, int G) {
   }
   if constexpr (ACC) {  // a later pass of taps (no z_eff writer)
     if (a.zvec)
-      lr_fwd_mfma<T, W, RC, true, false, false, true><<<a.nblk, 256, 0, p[0].stream>>>(a);
+      lr_fwd_mfma<T, W, RC, true, false, false, true><<<a.nblk, NT, 0, p[0].stream>>>(a);
     else
-      lr_fwd_mfma<T, W, RC, false, false, false, true><<<a.nblk, 256, 0, p[0].stream>>>(a);
+      lr_fwd_mfma<T, W, RC, false, false, false, true><<<a.nblk, NT, 0, p[0].stream>>>(a);
     return hipGetLastError();
   }
   if constexpr (RC == 1 && W <= 8) {
     // all wavefronts resident at the ILP build's three per SIMD (see lowrank_mfma_fwd_ilp.hip);
     // more only where the run length cap forces them
+    static_assert(NWV == 4, "the ILP build launches 4-wavefront workgroups");
     if (a.zrp == 0 && a.nblk * 4 <= kFwdIlpMaxWaves) return lr_fwd_ilp_launch<T, W>(a, p[0].stream);
   }
-  if (a.zrp > 0) {
-    if (a.zvec)
-      lr_fwd_mfma<T, W, RC, true, true><<<a.nblk, 256, 0, p[0].stream>>>(a);
-    else
-      lr_fwd_mfma<T, W, RC, false, true><<<a.nblk, 256, 0, p[0].stream>>>(a);
-  } else {
-    if (a.zvec)
-      lr_fwd_mfma<T, W, RC, true, false><<<a.nblk, 256, 0, p[0].stream>>>(a);
-    else
-      lr_fwd_mfma<T, W, RC, false, false><<<a.nblk, 256, 0, p[0].stream>>>(a);
+  if constexpr (RC <= 4) {  // z_eff writer: kernel ranks up to 64 (above, lr_zeff_bytes is 0)
+    if (a.zrp > 0) {
+      if (a.zvec)
+        lr_fwd_mfma<T, W, RC, true, true><<<a.nblk, NT, 0, p[0].stream>>>(a);
+      else
+        lr_fwd_mfma<T, W, RC, false, true><<<a.nblk, NT, 0, p[0].stream>>>(a);
+      return hipGetLastError();
+    }
   }
+  if (a.zrp > 0) return hipErrorInvalidValue;
+  if (a.zvec)
+    lr_fwd_mfma<T, W, RC, true, false><<<a.nblk, NT, 0, p[0].stream>>>(a);
+  else
+    lr_fwd_mfma<T, W, RC, false, false><<<a.nblk, NT, 0, p[0].stream>>>(a);
   return hipGetLastError();
 }
 

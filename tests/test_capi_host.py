@@ -323,7 +323,7 @@ def test_kernel_paths(lib):
         assert lp(1, 64, 256, 16, 33, bf, 0, bwd) == 0         # W 33-1024: generic kernels
         assert lp(1, 64, 256, 16, 1025, bf, 0, bwd) < 0        # W 1025: above DC_MAX_W
     for bwd in (0, 1):                                         # kernel ranks 65-256 as passes of ranks
-        assert lp(4, 4096, 2048, 127, 4, bf, 1, bwd) == 2      # (forward 64 per pass, backward 32)
+        assert lp(4, 4096, 2048, 127, 4, bf, 1, bwd) == 2      # (forward 128 per pass up to W 4, 64 above; backward 32)
         assert lp(1, 64, 256, 255, 8, f16, 1, bwd) == 2        # kernel rank 256, W 8: 4 forward passes
         assert lp(1, 64, 256, 100, 16, bf, 0, bwd) == 2        # 2 x 2 forward passes
     assert lp(1, 64, 256, 127, 20, bf, 1, 0) == 0              # 2 x 3 forward passes (y rounded 6 times):

@@ -381,16 +381,19 @@ LR_EDGE = [
     (1, 25, 64, 40, 20, False, True, torch.bfloat16, ("mfma", "mfma")),        # W 20 > T
     (1, 50, 64, 64, 32, False, True, torch.bfloat16, ("mfma", "mfma")),        # W 32: forward 4 x 8, 32 passes
     # kernel ranks 65-256 (the reference takes any power-of-two rank, lowrank.py:331-333): the forward
-    # as passes of 64 ranks (z columns and U rows from the pass's first rank, the static rank in the pass
+    # as passes of 128 ranks up to W 4 (8-wavefront workgroups), of 64 above (z columns and U rows from
+    # the pass's first rank, the static rank in the pass
     # that holds index R, each pass split into passes of at most 8 taps, every pass after the first added
     # to the stored y; at most 4 passes), the backward as passes of 32 ranks on the two-chunk kernels
     # (dz partial columns and dU partial rows of the whole problem, dx accumulated; past 4 rank x tap
     # passes in fp32)
-    (2, 300, 256, 127, 4, True, True, torch.bfloat16, ("mfma", "mfma")),      # kernel rank 128: 2 + 4 passes
-    (1, 100, 128, 64, 3, True, False, torch.float16, ("mfma", "mfma")),       # rank 65: the static rank alone
+    (2, 300, 256, 127, 4, True, True, torch.bfloat16, ("mfma", "mfma")),      # kernel rank 128: 1 + 4 passes
+    (1, 100, 128, 64, 3, True, False, torch.float16, ("mfma", "mfma")),       # rank 65: static alone in bwd pass 3
+    (1, 60, 128, 64, 6, True, True, torch.bfloat16, ("mfma", "mfma")),        # W 6, rank 65: fwd 64 + static alone
+    (1, 80, 128, 255, 4, True, True, torch.bfloat16, ("mfma", "mfma")),       # rank 256, W 4: forward 128 + 128
     (1, 3216, 256, 96, 2, False, True, torch.bfloat16, ("mfma", "mfma")),     # rank 96: z itself, long runs
     (2, 64, 128, 255, 8, True, True, torch.float16, ("mfma", "mfma")),        # rank 256, W 8: 4 + 8 x 2 passes
-    (1, 50, 64, 200, 1, False, True, torch.bfloat16, ("mfma", "mfma")),       # rank 200, W 1: padded z
+    (1, 50, 64, 200, 1, False, True, torch.bfloat16, ("mfma", "mfma")),       # rank 200, W 1: fwd 128 + 72
     (1, 37, 64, 100, 16, True, True, torch.bfloat16, ("mfma", "mfma")),       # rank 101, W 16: 2 x 2, 4 x 4
     (1, 45, 64, 127, 12, True, True, torch.bfloat16, ("mfma", "mfma")),       # W 12: forward 2 x (4 + 8)
     (1, 520, 200, 70, 5, False, False, torch.float16, ("mfma", "mfma")),      # D % 16 != 0, rank 70, W 5
