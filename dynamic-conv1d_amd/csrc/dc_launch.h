@@ -73,6 +73,9 @@ struct LrProblem {
   // z's row stride in elements (0: R): a pass over kernel ranks rofs .. of a
   // wider problem reads z from column rofs of rows z_ld apart (fp32 forward)
   int64_t z_ld;
+  // Ranks per row of zeff (0: those of this problem, lr_zeff_rows): a forward
+  // pass over some of a wider problem's taps writes the whole problem's rows.
+  int64_t zeff_rp;
   int64_t xld() const { return x_ld > 0 ? x_ld : D; }
   int64_t uld() const { return u_ld > 0 ? u_ld : W * D; }
   int64_t zld() const { return z_ld > 0 ? z_ld : R; }

@@ -456,7 +456,7 @@ int64_t lr_zeff_bytes(const LrProblem& p) {
   // multiple of 32 dynamic ranks (16-byte loads)
   const bool k32 = rc == 2 || lr_bwd_rank_split(p.R + (has_static ? 1 : 0), p.W);
   const bool pad = k32 ? !(p.R % 32 == 0 && !has_static) : p.R % 4 != 0;
-  return pad ? p.B * p.T * lr_bwd_zrow(p.R, has_static) * 2 : 0;
+  return pad ? p.B * p.T * lr_bwd_zrow(p.R, has_static, p.W) * 2 : 0;
 }
 
 int64_t lr_bwd_ws_bytes(const LrProblem& p) {

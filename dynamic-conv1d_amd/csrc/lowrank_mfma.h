@@ -206,19 +206,27 @@ inline int64_t run_tiles_cap(int64_t rowb) {
 }
 
 // The backward runs passes of 32 kernel ranks on the two-rank-chunk kernels
-// above kernel rank 64, and from W 2 on at kernel ranks 49-64, where four rank
-// chunks hold the operands of one tap per pass: B4 T4096 D2048 R63 + static W4
-// then takes two passes (32 + 32 ranks, 4 taps each) instead of four.
-inline bool lr_bwd_rank_split(int64_t RK, int64_t W) { return RK > 64 || (RK > 48 && W >= 2); }
+// above kernel rank 64, from W 2 on at kernel ranks 49-64 (four rank chunks
+// hold the operands of one tap per pass) and from W 3 on at 33-48 (three rank
+// chunks hold two taps per pass, at one wavefront per SIMD): B4 T4096 D2048
+// backward R63 + static W4 327 -> 160 us (two passes of 32 + 32 ranks, 4 taps
+// each, instead of four), R47 + static W4 171 -> 146 us, W8 369 -> 296 us.  At
+// W 2 the one three-chunk pass stays (R47 + static: 78 us against 130 us).
+inline bool lr_bwd_rank_split(int64_t RK, int64_t W) {
+  return RK > 64 || (RK > 48 && W >= 2) || (RK > 32 && W >= 3);
+}
 
-// Ranks per row of the backward's padded z_eff copy: the kernel rank RK rounded
-// up to 4, or 32 for two rank chunks (17 <= RK <= 32), or above 48 up to a
-// multiple of 32 (the passes of 32 ranks read 32 of a row's ranks, 16 bytes
-// per lane; four rank chunks in one pass read any multiple of 4).
-inline int64_t lr_bwd_zrow(int64_t R, bool has_static) {
+// Ranks per row of the backward's padded z_eff copy: with passes of 32 ranks
+// a multiple of 32 (each pass reads 32 of a row's ranks, 16 bytes per lane),
+// else 32 for two rank chunks (17 <= RK <= 32) or RK rounded up to 4.
+inline int64_t lr_bwd_zrow(int64_t R, bool has_static, int64_t W) {
   const int64_t rk = R + (has_static ? 1 : 0);
-  if (rk > 48) return (rk + 31) / 32 * 32;
+  if (lr_bwd_rank_split(rk, W)) return (rk + 31) / 32 * 32;
   return rk > 16 && rk <= 32 ? 32 : (rk + 3) / 4 * 4;
+}
+// Ranks per row of a problem's z_eff (a forward pass of taps: the whole problem's).
+inline int64_t lr_zeff_rows(const LrProblem& p) {
+  return p.zeff_rp > 0 ? p.zeff_rp : lr_bwd_zrow(p.R, p.static_w != nullptr, p.W);
 }
 
 // Largest kernel rank (R + static) of the matrix-core kernels: above 64 they

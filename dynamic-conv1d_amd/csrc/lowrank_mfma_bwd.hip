@@ -921,7 +921,7 @@ int64_t lr_bwd_max_run_tiles(const LrProblem& p) {
   int64_t rowb = p.xld() * 2;
   // past four passes of taps the passes' dx rows are the fp32 accumulator (D floats each)
   const int64_t dxb = bwd_f32dx(p) ? p.D * 4 : p.dxld() * 2;
-  const int64_t others[4] = {dxb, p.yhd() * 2, lr_bwd_zrow(p.R, p.static_w != nullptr) * 2, p.R * 4};
+  const int64_t others[4] = {dxb, p.yhd() * 2, lr_bwd_zrow(p.R, p.static_w != nullptr, p.W) * 2, p.R * 4};
   for (int64_t v : others) rowb = rowb > v ? rowb : v;
   return run_tiles_cap(rowb);
 }
@@ -964,7 +964,7 @@ LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
 
 // Ranks of the padded z_eff copy: RK rounded up to a multiple of 4, or 32 for
 // two rank chunks (their 16x16x32 operands read ranks 8q..8q+7 of every row).
-inline int64_t zpad_ranks(const LrProblem& p) { return lr_bwd_zrow(p.R, p.static_w != nullptr); }
+inline int64_t zpad_ranks(const LrProblem& p) { return lr_bwd_zrow(p.R, p.static_w != nullptr, p.W); }
 
 // z_eff[t, r] = z[t, r] (r < R), 1 (r == R, static_w given), 0 up to RP: the
 // backward's z operand when z cannot be read 8 bytes at a time.

@@ -13,7 +13,7 @@ int64_t lr_fwd_max_run_tiles(const LrProblem& p) {
   int64_t rowb = p.xld() * 2;
   rowb = rowb > hd * 2 ? rowb : hd * 2;
   rowb = rowb > p.zld() * 2 ? rowb : p.zld() * 2;  // z rows (a pass of ranks: the whole problem's)
-  const int64_t zrp = p.zeff ? lr_bwd_zrow(p.R, p.static_w != nullptr) : 0;
+  const int64_t zrp = p.zeff ? lr_zeff_rows(p) : 0;
   rowb = rowb > zrp * 2 ? rowb : zrp * 2;
   int64_t tiles = run_tiles_cap(rowb);
   if (hd != p.D) {
@@ -127,6 +127,7 @@ hipError_t dispatch_fwd(const LrProblem* pp, int G) {
       a[g].accy = f.accy;
       a[g].residual = i == 0 ? p.residual : 0;
       a[g].zeff = i == 0 ? p.zeff : nullptr;  // null above kernel rank 64 (lr_zeff_bytes is 0)
+      a[g].zeff_rp = lr_zeff_rows(p);          // the whole problem's rows (its W decides)
     }
     e = dispatch_pass<T>(a, G);
   }

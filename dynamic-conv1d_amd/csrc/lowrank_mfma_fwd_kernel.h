@@ -202,6 +202,12 @@ void lr_fwd_mfma(LrArgs a) {
         bstore64<false>(zc[c], rze,
                         zrow_mine && tile * 16 + n < Tn && r0 < zrp ? ((tile * 16 + n - rb) * zrp + r0) * 2 : kOobTile);
       }
+      if constexpr (RC == 3) {
+        // rows of 64 ranks for the backward's passes of 32 (lr_bwd_zrow): ranks 48-63 are zeros
+        const int r0 = 48 + 4 * q;
+        bstore64<false>(u32x2{0u, 0u}, rze,
+                        zrow_mine && tile * 16 + n < Tn && r0 < zrp ? ((tile * 16 + n - rb) * zrp + r0) * 2 : kOobTile);
+      }
     }
     if constexpr (HX) {
       // row 4q-W+1+m is own row 5-W+m (slot m+4) of the group above

@@ -63,7 +63,7 @@ hipError_t launch_fwd(const LrProblem* p, int G) {
   a.nblk = G * a.nblk1;
   a.xld = (int)p[0].xld();
   a.yhd = (int)p[0].yhd();
-  a.zrp = p[0].zeff ? (int)lr_bwd_zrow(p[0].R, p[0].static_w != nullptr) : 0;
+  a.zrp = p[0].zeff ? (int)lr_zeff_rows(p[0]) : 0;
   for (int g = 0; g < G; ++g) {
     a.grp[g] = LrFwdGroup{p[g].x, p[g].z, p[g].U, p[g].static_w, p[g].y, p[g].zeff};
     a.zvec = a.zvec && aligned_to(p[g].z, 8);

@@ -121,14 +121,19 @@ def test_lowrank_validation(lib):
     assert zb(2, 8, 16, 31, 4, 0, 1) == 2 * 8 * 32 * 2
     assert zb(2, 8, 16, 32, 4, 0, 0) == 0
     assert zb(2, 8, 16, 28, 4, 0, 0) == 2 * 8 * 32 * 2
-    # kernel ranks 49-64 from W 2 on: passes of 32 ranks, rows of 64 unless z holds 64 dynamic ranks;
-    # at W 1 one pass of four rank chunks (8-byte loads: R % 4 == 0 reads z itself)
+    # kernel ranks 49-64 from W 2 on and 33-48 from W 3 on: passes of 32 ranks, rows of 64 unless z
+    # holds a multiple of 32 dynamic ranks; below those widths one pass of three or four rank chunks
+    # (8-byte loads: R % 4 == 0 reads z itself, else rows of RK rounded up to 4)
     assert zb(2, 8, 16, 63, 4, 0, 1) == 2 * 8 * 64 * 2
     assert zb(2, 8, 16, 60, 2, 0, 0) == 2 * 8 * 64 * 2
     assert zb(2, 8, 16, 64, 4, 0, 0) == 0
     assert zb(2, 8, 16, 60, 1, 0, 0) == 0
     assert zb(2, 8, 16, 63, 1, 0, 1) == 2 * 8 * 64 * 2
-    assert zb(2, 8, 16, 47, 4, 0, 1) == 2 * 8 * 48 * 2  # three rank chunks: one pass, rows of 48
+    assert zb(2, 8, 16, 47, 4, 0, 1) == 2 * 8 * 64 * 2
+    assert zb(2, 8, 16, 40, 3, 0, 0) == 2 * 8 * 64 * 2
+    assert zb(2, 8, 16, 47, 2, 0, 1) == 2 * 8 * 48 * 2  # W 2: one pass of three rank chunks
+    assert zb(2, 8, 16, 40, 2, 0, 0) == 0
+    assert zb(2, 8, 16, 37, 9, 0, 0) == 2 * 8 * 64 * 2  # W 9: the forward's first pass of taps holds 1
     assert zb(2, 8, 16, 3, 4, 2, 1) == 0              # fp32: the backward reads z itself
     assert zb(2, 8, 20, 3, 4, 0, 1) == 0              # D % 8 != 0: no matrix-core backward
     assert zb(2, 8, 24, 3, 4, 0, 1) == 2 * 8 * 4 * 2  # D % 8 == 0 suffices

@@ -372,10 +372,10 @@ LR_EDGE = [
     (1, 520, 200, 20, 28, False, True, torch.bfloat16, ("mfma", "mfma")),      # D % 16 != 0, 12 + 16
     (1, 3216, 64, 31, 25, True, True, torch.float16, ("mfma", "mfma")),        # long runs, two rank chunks
     # kernel ranks 33-64 above W 8: the forward as passes of 8 taps (the first W - 8(n-1), each later
-    # one added to the stored y), the backward as passes of 2 (three rank chunks) or 1 (four) taps
-    # into the fp32 dx accumulator
-    (1, 40, 64, 40, 9, False, True, torch.bfloat16, ("mfma", "mfma")),         # forward 1 + 8, 5 passes
-    (1, 100, 128, 40, 12, False, True, torch.bfloat16, ("mfma", "mfma")),      # forward 4 + 8, 6 passes
+    # one added to the stored y), the backward as passes of 32 ranks x passes of up to 4 taps into
+    # the fp32 dx accumulator (the forward's z_eff rows of 64 ranks even where its first pass holds 1 tap)
+    (1, 40, 64, 40, 9, False, True, torch.bfloat16, ("mfma", "mfma")),         # forward 1 + 8, 2 x 3 passes
+    (1, 100, 128, 40, 12, False, True, torch.bfloat16, ("mfma", "mfma")),      # forward 4 + 8, 2 x 3 passes
     (2, 70, 256, 63, 9, True, True, torch.float16, ("mfma", "mfma")),          # four chunks: 9 passes of 1
     (1, 300, 64, 47, 20, True, False, torch.bfloat16, ("mfma", "mfma")),       # forward 4 + 8 + 8
     (1, 25, 64, 40, 20, False, True, torch.bfloat16, ("mfma", "mfma")),        # W 20 > T
@@ -872,9 +872,9 @@ def test_lowrank_zeff_saved(R, static, xoff, zoff):
     backward exactly as the copy the backward builds itself: bitwise equal gradients.  xoff = 4
     puts x 8 bytes off 16-byte alignment: the forward takes its element-aligned kernels and
     fills the copy in a launch of its own (the padding kernel), the backward stays on matrix
-    cores.  zoff = 1 starts z 2 bytes into its buffer (rows not 4-byte aligned); R 63 and 37
-    pad to 64 and 40 ranks; kernel ranks 51 and 52 to 64 (the backward's passes of 32 ranks read
-    16 bytes of a row per lane, so even R % 4 == 0 takes the copy)."""
+    cores.  zoff = 1 starts z 2 bytes into its buffer (rows not 4-byte aligned); at W 4 every
+    kernel rank above 32 pads to a multiple of 32 (the backward's passes of 32 ranks read 16
+    bytes of a row per lane, so even R % 4 == 0 takes the copy): R 63, 37, 50 + static, 52."""
     from dynconv import _capi
 
     lib = _capi.load()
@@ -889,7 +889,7 @@ def test_lowrank_zeff_saved(R, static, xoff, zoff):
     sw = uniform(g, W, Dn, lo=-0.5, hi=0.5).to(bf).to(DEV) if static else None
     dy = randn(g, Bn, Tn, Dn).to(bf).to(DEV)
     rk = R + (1 if static else 0)
-    rp = 32 if 16 < rk <= 32 else ((rk + 31) // 32 * 32 if rk > 48 else (rk + 3) // 4 * 4)
+    rp = 32 if 16 < rk <= 32 else ((rk + 31) // 32 * 32 if rk > 32 else (rk + 3) // 4 * 4)  # W 4
     nz = lib.dc_lowrank_zeff_bytes(Bn, Tn, Dn, R, W, 0, int(static))
     assert nz == Bn * Tn * rp * 2
     zeff = torch.full((nz,), 0xAB, dtype=torch.uint8, device=DEV)  # the forward overwrites all of it
