@@ -3,7 +3,8 @@
 Each case draws B, T, D, the head size (headwise) or rank (lowrank), W,
 static_w, residual and dtype from a fixed seed, so every dispatch path meets
 shapes nobody picked by hand: the vector / MFMA kernels with partial channel
-chunks and tiles, the lowrank passes of taps (kernel ranks 33-64, and W 9-32), the headwise wide
+chunks and tiles, the lowrank passes of taps and of ranks (kernel ranks 33-256, and W 9-32), the
+8-wavefront forward workgroups, the headwise wide
 kernels (W 9-16), the fp32 matrix-core and VALU kernels, and the generic
 kernels (D not a multiple of the vector width, head sizes that are not a power
 of two, ranks and W outside the fast plans).  Criterion: the north-star
@@ -66,8 +67,9 @@ def _headwise_case(i):
 
 def _lowrank_wide_case(i):
     """Kernel ranks 33-64 (3-4 rank chunks) at W 1-12 in 16-bit types: the matrix-core backward's
-    passes of taps (each pass's dx added to the earlier passes', its dz in slots of its own; past
-    four passes in fp32), above W 8 the forward's passes of 8 taps."""
+    passes of 32 ranks (49-64 from W 2 on, 33-48 from W 3 on) or its one pass of three or four
+    rank chunks, with passes of taps (each pass's dx added to the earlier passes', its dz in slots
+    of its own; past four passes in fp32), above W 8 the forward's passes of 8 taps."""
     rnd = random.Random(6113 * i + 29)
     dtype = rnd.choice([torch.bfloat16, torch.float16])
     Bn = rnd.randint(1, 2)
@@ -112,8 +114,30 @@ def _headwise_wide_case(i):
     return Bn, Tn, Dn, Dn // hs, W, static, residual, dtype
 
 
+def _lowrank_big_lds_case(i):
+    """Forward shapes whose staged operands exceed 80 KiB (8-wavefront workgroups): W 5-8 at three
+    or four rank chunks, W 11-16 at two, and kernel ranks 65-256 at W 1-4 (one pass of up to 128
+    ranks, or two); their backward as passes of 32 ranks or of taps."""
+    rnd = random.Random(27644437 * i + 1)
+    dtype = rnd.choice([torch.bfloat16, torch.float16])
+    Bn = rnd.randint(1, 2)
+    Tn = rnd.choice([1, 16, 33, 100, 129])
+    Dn = rnd.choice([8, 64, 128, 136, 256])
+    static = rnd.random() < 0.5
+    residual = rnd.random() < 0.5
+    k = rnd.randint(0, 2)
+    if k == 0:
+        W, R = rnd.randint(5, 8), rnd.randint(33, 64)
+    elif k == 1:
+        W, R = rnd.randint(11, 16), rnd.randint(17, 32)
+    else:
+        W, R = rnd.randint(1, 4), rnd.randint(65, 256)
+    R = max(1, min(R - (1 if static else 0), 255 if static else 256))
+    return Bn, Tn, Dn, R, W, static, residual, dtype
+
+
 LR_CASES = ([_lowrank_case(i) for i in range(64)] + [_lowrank_wide_case(i) for i in range(24)]
-            + [_lowrank_widew_case(i) for i in range(24)])
+            + [_lowrank_widew_case(i) for i in range(24)] + [_lowrank_big_lds_case(i) for i in range(24)])
 HW_CASES = [_headwise_case(i) for i in range(64)] + [_headwise_wide_case(i) for i in range(32)]
 
 
