@@ -145,7 +145,8 @@ int dc_headwise_bwd_noalloc(const void* x, const void* weight, const void* stati
                             int dtype, int residual, void* stream);
 
 /* Bytes of the padded z_eff (z with the static column and zero ranks, rows of
- * 4*k or 32 ranks) that dc_lowrank_bwd builds before its main kernel for this
+ * 4*k ranks, or of a multiple of 32 where the backward reads 32 ranks of a row
+ * at a time: two rank chunks, passes of 32 ranks) that dc_lowrank_bwd builds before its main kernel for this
  * shape, or 0 when it reads z itself, or a negative dc_status.  A caller that
  * keeps such a buffer from the forward to the backward saves that pass: the
  * forward writes it as a by-product (z_eff of dc_lowrank_fwd) and the backward
