@@ -241,7 +241,7 @@ bool hw_wide_ok(const HwProblem& p, bool bwd) {
 }
 
 // ------------------------------------------------------- head-MFMA path
-// The matrix-core kernels (headwise_mma.h): head sizes 16, 32, 64 at
+// The matrix-core kernels (headwise_mma.h): head sizes 8, 16, 32, 64 at
 // 9 <= W <= 32 with whole 16-byte pieces of a wavefront's weight-row segment,
 // bf16 / fp16, D a multiple of 64.  Runs of 16-row tiles; each run's resources
 // reach 32 rows before it and 64 after it (the dy / weight look-ahead).
@@ -279,7 +279,14 @@ HwMmaArgs make_mma_args(const HwProblem& p, bool bwd) {
   const int64_t ntile = (p.T + 15) / 16;
   // runs per sequence: as many as the target allows, each at least one tile and
   // at most the resources' cap (tiles are split evenly among them)
-  int64_t nspb = (bwd ? kMmaBwdWaves : kMmaFwdWaves) / (p.B * a.nwc);
+  // the backward's wavefronts all resident: four per CU, or as many as fit by
+  // LDS (head size 8 above W 20: three)
+  int target = kMmaFwdWaves;
+  if (bwd) {
+    const int per = (160 * 1024) / ((hw_mma_bwd_lds_bytes((int)p.W, (int)(p.D / p.H)) + 1023) / 1024 * 1024);
+    target = per >= 4 ? kMmaBwdWaves : 256 * per;
+  }
+  int64_t nspb = target / (p.B * a.nwc);
   if (nspb > ntile) nspb = ntile;
   const int64_t cap = mma_max_run_tiles(p);  // >= 1 (hw_mma_ok)
   if (nspb < (ntile + cap - 1) / cap) nspb = (ntile + cap - 1) / cap;

@@ -1,5 +1,5 @@
 // Headwise dynamic convolution backward on gfx950 matrix cores, for head
-// sizes 16, 32 and 64 at 9 <= W <= 32 (bf16 / fp16).
+// sizes 8, 16, 32 and 64 at 9 <= W <= 32 (bf16 / fp16).
 //
 // Reference: headwise.py:105-215 (causal_conv1d_bwd_kernel), any W
 // (headwise.py:226).  With h the head of channel d, hs its size:
@@ -17,6 +17,12 @@
 //   * the head weights' part of dx: dx[t,d] = sum_s Wm[t][s] dy[s,d] with the
 //     banded Wm[t][s] = w[s,h,s-t] (0 <= s-t < W): a 16x16x16 MFMA per 16-row
 //     block of s and 16 channels, dy by column from LDS (transposing reads).
+// Head size 8: a 16-channel block holds two heads.  In the dw product lane
+// quarter q's channels 4q..4q+3 lie in head 4q/8 of the block, so each head's
+// product takes A with the other head's quarters zeroed; in the dx (and the
+// forward's y) product the output column is the channel, so each head adds its
+// banded Wm times dy with the other head's columns zeroed.  Twice the products
+// of head size 16, on a pipe these kernels leave mostly idle.
 // The static filter is per channel: dx[t,d] += sum_k dy[t+k,d] sw[k,d] and
 // dsw[k,d] += sum_t dy[t,d] x[t-k,d] stay on the vector units, two products
 // per instruction (v_dot2c_f32_bf16 / _f16 on row pairs of one channel, which
@@ -53,6 +59,14 @@ struct HwMmaArgs {
   int residual;
 };
 
+// LDS bytes of one backward wavefront (HwMmaGeom::BYTES), for the host's launch size.
+constexpr int hw_mma_bwd_lds_bytes(int W, int HS) {
+  const int NB = (W - 1 + 15) / 16, WP2 = (W + 1) / 2, NGY = (WP2 + 9) / 2;
+  const int NBY = (4 * NGY - 16 + 15) / 16, NR = NB + 1, NRY = NBY + 1;
+  const int WPB = (64 / HS) * W * 2, BLK = 16 * (64 * 2 + 16);
+  return NR * BLK + NRY * BLK + NRY * 16 * WPB + 16 * WPB + 16 + 64 * (16 * 4 + 16) + 16;
+}
+
 // LDS geometry of one wavefront (bytes): row blocks of 16 rows.
 template <typename T, int W, int HS>
 struct HwMmaGeom {
@@ -79,6 +93,7 @@ struct HwMmaGeom {
   static constexpr int BYTES = Z0 + 16;
   static_assert(WPB % 16 == 0, "whole 16-byte pieces of the heads' weight rows");
   static_assert(NBY >= NB && 4 * NGY <= 16 * NRY, "the dy ring holds the look-ahead rows");
+  static_assert(BYTES == hw_mma_bwd_lds_bytes(W, HS), "the host's LDS size of the backward");
 };
 
 // The pair of 16-bit elements (2i+1, 2i+2) of a packed row sequence v (pair i
@@ -212,6 +227,21 @@ __global__ __launch_bounds__(64) void hw_bwd_mma(const T* __restrict__ x, const 
     // ---- dw: C[t][s] over K = the head's channels; dw[t,h,k] = C[t][t-k]
     {
       f32x4 c[NHW][NB + 1];
+      if constexpr (HS < 16) {
+        constexpr int HPG = 16 / HS;  // heads per 16-channel block
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int be = 0; be <= NB; ++be) {
+            const u32x2 av = *reinterpret_cast<const u32x2*>(lds + ya(t0 + n, (g * 16 + 4 * q) * 2));
+            const u32x2 bv = *reinterpret_cast<const u32x2*>(lds + xa(t0 - 16 * be + n, (g * 16 + 4 * q) * 2));
+#pragma unroll
+            for (int hh = 0; hh < HPG; ++hh) {
+              const u32x2 am = (4 * q) / HS == hh ? av : u32x2{0u, 0u};  // K = channels 4q..4q+3
+              c[g * HPG + hh][be] = Mma16<T>::run(am, bv, f32x4{0.f, 0.f, 0.f, 0.f});
+            }
+          }
+      } else {
 #pragma unroll
       for (int h = 0; h < NHW; ++h) {
 #pragma unroll
@@ -232,6 +262,7 @@ __global__ __launch_bounds__(64) void hw_bwd_mma(const T* __restrict__ x, const 
           }
           c[h][be] = acc;
         }
+      }
       }
       // lane (q, n) holds C[4q+i][n] of block be: t = t0+4q+i, s = t0-16be+n, k = 4q+i-n+16be
 #pragma unroll
@@ -255,7 +286,36 @@ __global__ __launch_bounds__(64) void hw_bwd_mma(const T* __restrict__ x, const 
     }
 
     // ---- dx from the head weights: C = Wm dy per head and 16 channels, K = s blocks
-    {
+    if constexpr (HS < 16) {
+      constexpr int HPG = 16 / HS;
+      f32x4 c[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) c[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int be = 0; be <= NB; ++be) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int L = lane & 15;
+          const u32x2 bv0 = lds_read_tr16(lds + ya(t0 + 16 * be + 4 * q + (L >> 2), (g * 16 + 4 * (L & 3)) * 2));
+#pragma unroll
+          for (int hh = 0; hh < HPG; ++hh) {
+            const int h = g * HPG + hh;
+            uint32_t e4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int k = 16 * be + 4 * q + e - n;
+              const int addr = (k >= 0 && k < W) ? wa(t0 + 16 * be + 4 * q + e, h * W + k) : G::Z0;
+              e4[e] = *reinterpret_cast<const uint16_t*>(lds + addr);
+            }
+            const u32x2 av = {e4[0] | (e4[1] << 16), e4[2] | (e4[3] << 16)};
+            const u32x2 bv = n / HS == hh ? bv0 : u32x2{0u, 0u};  // column n = channel g*16+n
+            c[g] = Mma16<T>::run(av, bv, c[g]);
+          }
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *reinterpret_cast<f32x4*>(lds + G::DX0 + (g * 16 + n) * G::DXP + 16 * q) = c[g];
+    } else {
       f32x4 c[NHW][HS / 16];
 #pragma unroll
       for (int h = 0; h < NHW; ++h)
@@ -497,7 +557,36 @@ __global__ __launch_bounds__(64) void hw_fwd_mma(const T* __restrict__ x, const 
     load_w(m + 1, nb);
 
     // ---- y from the head weights: C = Wf x per head and 16 channels, K = s blocks
-    {
+    if constexpr (HS < 16) {
+      constexpr int HPG = 16 / HS;
+      f32x4 c[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) c[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int be = 0; be <= NB; ++be) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int L = lane & 15;
+          const u32x2 bv0 = lds_read_tr16(lds + xa(t0 - 16 * be + 4 * q + (L >> 2), (g * 16 + 4 * (L & 3)) * 2));
+#pragma unroll
+          for (int hh = 0; hh < HPG; ++hh) {
+            const int h = g * HPG + hh;
+            uint32_t e4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int k = 16 * be + n - 4 * q - e;
+              const int addr = (k >= 0 && k < W) ? G::W0 + n * WPB + (h * W + k) * 2 : G::Z0;
+              e4[e] = *reinterpret_cast<const uint16_t*>(lds + addr);
+            }
+            const u32x2 av = {e4[0] | (e4[1] << 16), e4[2] | (e4[3] << 16)};
+            const u32x2 bv = n / HS == hh ? bv0 : u32x2{0u, 0u};  // column n = channel g*16+n
+            c[g] = Mma16<T>::run(av, bv, c[g]);
+          }
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *reinterpret_cast<f32x4*>(lds + G::Y0 + (g * 16 + n) * G::DXP + 16 * q) = c[g];
+    } else {
       f32x4 c[NHW][HS / 16];
 #pragma unroll
       for (int h = 0; h < NHW; ++h)
@@ -593,7 +682,7 @@ namespace dc {
 // Widths the kernels take at head size hs: a wavefront's weight-row segment,
 // (64 / hs) * W 16-bit elements, in whole 16-byte pieces.
 constexpr bool hw_mma_width_ok(int hs, int W) {
-  return W >= kHwMmaMinW && W <= kHwMmaMaxW && (hs == 16 || hs == 32 || hs == 64) && ((64 / hs) * W) % 8 == 0;
+  return W >= kHwMmaMinW && W <= kHwMmaMaxW && (hs == 8 || hs == 16 || hs == 32 || hs == 64) && ((64 / hs) * W) % 8 == 0;
 }
 
 template <typename T, bool STATIC>

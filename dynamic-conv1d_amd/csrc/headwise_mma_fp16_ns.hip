@@ -21,6 +21,8 @@ hipError_t hw_bwd_mma_launch<fp16, false>(const HwProblem& p, const HwMmaArgs& a
   DC_MMA(16, 22) DC_MMA(16, 24) DC_MMA(16, 26) DC_MMA(16, 28) DC_MMA(16, 30) DC_MMA(16, 32)
   DC_MMA(32, 12) DC_MMA(32, 16) DC_MMA(32, 20) DC_MMA(32, 24) DC_MMA(32, 28) DC_MMA(32, 32)
   DC_MMA(64, 16) DC_MMA(64, 24) DC_MMA(64, 32)
+  DC_MMA(8, 9) DC_MMA(8, 10) DC_MMA(8, 11) DC_MMA(8, 12) DC_MMA(8, 13) DC_MMA(8, 14) DC_MMA(8, 15) DC_MMA(8, 16) DC_MMA(8, 17) DC_MMA(8, 18) DC_MMA(8, 19) DC_MMA(8, 20)
+  DC_MMA(8, 21) DC_MMA(8, 22) DC_MMA(8, 23) DC_MMA(8, 24) DC_MMA(8, 25) DC_MMA(8, 26) DC_MMA(8, 27) DC_MMA(8, 28) DC_MMA(8, 29) DC_MMA(8, 30) DC_MMA(8, 31) DC_MMA(8, 32)
 #undef DC_MMA
   return hipErrorInvalidValue;
 }
@@ -40,6 +42,8 @@ hipError_t hw_fwd_mma_launch<fp16, false>(const HwProblem& p, const HwMmaArgs& a
   DC_MMA(16, 22) DC_MMA(16, 24) DC_MMA(16, 26) DC_MMA(16, 28) DC_MMA(16, 30) DC_MMA(16, 32)
   DC_MMA(32, 12) DC_MMA(32, 16) DC_MMA(32, 20) DC_MMA(32, 24) DC_MMA(32, 28) DC_MMA(32, 32)
   DC_MMA(64, 16) DC_MMA(64, 24) DC_MMA(64, 32)
+  DC_MMA(8, 9) DC_MMA(8, 10) DC_MMA(8, 11) DC_MMA(8, 12) DC_MMA(8, 13) DC_MMA(8, 14) DC_MMA(8, 15) DC_MMA(8, 16) DC_MMA(8, 17) DC_MMA(8, 18) DC_MMA(8, 19) DC_MMA(8, 20)
+  DC_MMA(8, 21) DC_MMA(8, 22) DC_MMA(8, 23) DC_MMA(8, 24) DC_MMA(8, 25) DC_MMA(8, 26) DC_MMA(8, 27) DC_MMA(8, 28) DC_MMA(8, 29) DC_MMA(8, 30) DC_MMA(8, 31) DC_MMA(8, 32)
 #undef DC_MMA
   return hipErrorInvalidValue;
 }

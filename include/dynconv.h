@@ -92,7 +92,7 @@ typedef enum dc_path {
   DC_PATH_F32_MFMA = 3,  /* lowrank fp32: fp32 matrix-core kernels                  */
   DC_PATH_F32_VALU = 4,  /* lowrank fp32: vector-ALU kernels                        */
   DC_PATH_WIDE = 5,      /* headwise 9 <= W <= 32: row-ring kernels, staged weights */
-  DC_PATH_HEAD_MFMA = 6  /* headwise, head sizes 16-64 at 9 <= W <= 32: matrix cores */
+  DC_PATH_HEAD_MFMA = 6  /* headwise, head sizes 8-64 at 9 <= W <= 32: matrix cores */
 } dc_path;
 
 /* DC_ABI_VERSION of the loaded library. */

@@ -283,9 +283,11 @@ def test_kernel_paths(lib):
         assert hp(1, 50, 64, 16, 12, bf, 1, bwd) == 0          # W 12, D 64: generic
         assert hp(4, 4096, 2048, 2048, 12, bf, 1, bwd) == 5    # W 12, head size 1: wide
         assert hp(4, 4096, 2048, 64, 16, f32, 0, bwd) == 5     # W 16, head size 32: wide
-        assert hp(4, 4096, 2048, 64, 24, bf, 1, bwd) == 6      # W 24, hs 32: matrix cores (hs 16-64)
+        assert hp(4, 4096, 2048, 64, 24, bf, 1, bwd) == 6      # W 24, hs 32: matrix cores (hs 8-64)
         assert hp(4, 4096, 2048, 128, 10, f16, 0, bwd) == 6    # W 10, hs 16
-        assert hp(4, 4096, 2048, 256, 12, bf, 1, bwd) == 5     # hs 8: the wide kernels in both directions
+        assert hp(4, 4096, 2048, 256, 12, bf, 1, bwd) == 6     # hs 8: matrix cores (two heads per 16 channels)
+        assert hp(4, 4096, 2048, 256, 9, f16, 0, bwd) == 6     # hs 8 at every W 9-32
+        assert hp(4, 4096, 2048, 512, 12, bf, 1, bwd) == 5     # hs 4: the wide kernels in both directions
         assert hp(4, 4096, 2048, 64, 9, bf, 1, bwd) == 0       # hs 32, W 9: segments not in 16-byte pieces
         assert hp(1, 50, 96, 96, 20, bf, 1, bwd) == 0          # W 20, D % 64 != 0: generic
         assert hp(1, 50, 256, 2, 9, bf, 1, bwd) == 0           # head size 128, W 9: 18-byte segments

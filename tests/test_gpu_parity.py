@@ -153,9 +153,9 @@ HW_EDGE = [
     (2, 61, 384, 96, 11, True, False, torch.float32),   # wide: hs 4, three wavefront columns
     (1, 130, 256, 8, 12, True, True, torch.bfloat16),   # wide: hs 32
     (2, 45, 256, 2, 13, True, True, torch.float32),     # wide: hs 128 (a head is a whole wavefront)
-    (1, 90, 128, 16, 14, False, False, torch.bfloat16), # wide: hs 8
+    (1, 90, 128, 16, 14, False, False, torch.float32),  # wide: hs 8 (16-bit types: matrix cores)
     (1, 7, 128, 128, 15, True, True, torch.float16),    # wide: T < W
-    (2, 200, 256, 32, 16, True, True, torch.float16),   # wide: hs 8, W 16
+    (2, 200, 256, 32, 16, True, True, torch.float32),   # wide: hs 8, W 16
     (1, 1, 128, 64, 16, True, True, torch.bfloat16),    # wide: T 1
     (1, 50, 256, 2, 9, True, True, torch.bfloat16),     # hs 128 bf16 W 9: 18-byte weight segments, generic
     # fp16 W 16 head size 1 without a static filter: the dx of every row 16k + 15 came out wrong.
@@ -165,7 +165,7 @@ HW_EDGE = [
     (1, 40, 256, 256, 16, False, False, torch.float16),
     (2, 64, 128, 128, 16, False, True, torch.float16),
     (1, 40, 256, 256, 16, False, True, torch.bfloat16),
-    # the head matrix-core kernels (head sizes 16, 32, 64 at 9 <= W <= 32, whole 16-byte pieces of
+    # the head matrix-core kernels (head sizes 8, 16, 32, 64 at 9 <= W <= 32, whole 16-byte pieces of
     # a wavefront's weight-row segment): dw on MFMA over the head's channels, the head weights' part
     # of dx as a banded product, the static filter by row pairs; runs of 16-row tiles, T not a
     # multiple of 16, T below one tile, runs ending at T
@@ -173,6 +173,14 @@ HW_EDGE = [
     (1, 100, 128, 4, 12, False, True, torch.float16),   # hs 32, W 12, no static filter
     (1, 33, 128, 8, 10, True, False, torch.bfloat16),   # hs 16, W 10 (one look-back block)
     (2, 50, 192, 12, 32, True, True, torch.float16),    # hs 16, W 32, three wavefront columns
+    # head size 8: two heads per 16-channel block, one product per head with the other head's
+    # channels zeroed (dw: its K quarters, dx / y: its output columns)
+    (1, 90, 128, 16, 14, False, False, torch.bfloat16), # hs 8, W 14
+    (2, 200, 256, 32, 16, True, True, torch.float16),   # hs 8, W 16
+    (1, 77, 256, 32, 9, True, True, torch.bfloat16),    # hs 8, W 9 (odd)
+    (2, 61, 192, 24, 17, True, False, torch.float16),   # hs 8, W 17: two look-back blocks, three columns
+    (1, 130, 256, 32, 24, False, True, torch.bfloat16), # hs 8, W 24: three wavefronts per CU by LDS
+    (1, 10, 128, 16, 32, True, True, torch.bfloat16),   # hs 8, W 32 > T
     (1, 70, 128, 2, 16, True, True, torch.bfloat16),    # hs 64, W 16
     (1, 9, 64, 1, 24, True, True, torch.bfloat16),      # hs 64, W 24 > T
     (1, 1, 128, 4, 28, True, False, torch.bfloat16),    # hs 32, T 1
@@ -255,10 +263,10 @@ def _hw_vector_shape(Dn, H, dtype):
 
 def _hw_mma_shape(Dn, H, W, dtype):
     """Shapes the head matrix-core kernels take (contiguous, aligned tensors): bf16 / fp16, head
-    sizes 16, 32, 64 at 9 <= W <= 32 with whole 16-byte pieces of a 64-channel wavefront's weight-row
-    segment ((64 / hs) * W a multiple of 8), D a multiple of 64."""
+    sizes 8, 16, 32, 64 at 9 <= W <= 32 with whole 16-byte pieces of a 64-channel wavefront's
+    weight-row segment ((64 / hs) * W a multiple of 8), D a multiple of 64."""
     hs = Dn // H
-    return (dtype in (torch.bfloat16, torch.float16) and hs in (16, 32, 64) and 9 <= W <= 32
+    return (dtype in (torch.bfloat16, torch.float16) and hs in (8, 16, 32, 64) and 9 <= W <= 32
             and (64 // hs) * W % 8 == 0 and Dn % 64 == 0)
 
 
