@@ -26,12 +26,14 @@ int64_t lr_fwd_max_run_tiles(const LrProblem& p) {
   return tiles;
 }
 
-// Taps per forward pass: what one launch stages (W x RC operand chunks in LDS).
-constexpr int fwd_pass_taps(int rc) { return rc <= 2 ? 16 : 8; }
+// Taps per forward pass: what one launch stages (W x RC operand chunks in LDS,
+// up to 128 KiB on 8-wavefront workgroups): one rank chunk up to W 32 in one
+// pass, two up to 16, three or four up to 8.
+constexpr int fwd_pass_taps(int rc) { return rc == 1 ? 32 : rc == 2 ? 16 : 8; }
 
 // The passes of a forward launch sequence (fwd_plan).  Up to kernel rank 64
-// one pass of ranks; wider problems (above W 16 at one or two rank chunks,
-// above W 8 at three or four) run as passes of taps: taps 0 .. W0-1 as a
+// one pass of ranks; wider problems (above W 32 at one rank chunk, above
+// W 16 at two, above W 8 at three or four) run as passes of taps: taps 0 .. W0-1 as a
 // W0-tap problem (residual and z_eff included), then passes of P =
 // fwd_pass_taps taps, each on x read kofs rows earlier and added to the stored
 // y (accy).  Above fwd_rank_pass(W) kernel ranks, passes of that many (z
@@ -70,7 +72,7 @@ int lr_fwd_npasses(const LrProblem& p) {
 namespace {
 
 // The kernel of one pass: the plain kernels up to W 8 (this unit) and at
-// 9 <= W <= 16 (lowrank_mfma_fwd_wide.hip, which also holds the 16-tap
+// 9 <= W <= 32 (lowrank_mfma_fwd_wide.hip, which also holds the 16-tap
 // accumulating pass above W 16), the accumulating ones up to W 8
 // (lowrank_mfma_fwd_acc.hip).
 template <typename T>

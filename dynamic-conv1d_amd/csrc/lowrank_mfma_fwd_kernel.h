@@ -108,8 +108,9 @@ __device__ __forceinline__ void stage_u(u32x2* __restrict__ lds, const uint16_t*
 //
 // ACC: a later pass of a wider problem, whose y rows, as the earlier passes
 // stored them, are added before the store (each lane loads and stores only its
-// own rows): a pass of taps kofs .. kofs+W-1 (above W 16 the host runs taps
-// 0 .. W-17 first, then the last 16), whose x is read kofs rows earlier, or a
+// own rows): a pass of taps kofs .. kofs+W-1 (above W 16 at two rank chunks
+// the host runs taps 0 .. W-17 first, then the last 16), whose x is read kofs
+// rows earlier, or a
 // pass of kernel ranks (above 64: z columns and U rows from the pass's first
 // rank, kofs 0 unless taps are split as well).
 template <typename T, int W, int RC, bool ZV, bool ZE, bool ILP = false, bool ACC = false>

@@ -1,8 +1,9 @@
 // The lowrank forward (lowrank_mfma_fwd_kernel.h) at 9 <= W <= 16 taps with one
-// or two rank chunks, and the accumulating pass over the last 16 taps of wider
-// problems: the same kernel in one pass over the taps, a lane's x
-// rows 4q-W+1 .. 4q+3 loaded directly (up to 19 rows) and the U operands of
-// W x RC chunks staged in LDS (up to 128 KiB at W 16 with two chunks).  Its own
+// or two rank chunks and 17 <= W <= 32 with one, and the accumulating pass over
+// the last 16 taps of wider problems at two rank chunks: the same kernel in one
+// pass over the taps, a lane's x rows 4q-W+1 .. 4q+3 loaded directly (up to 35
+// rows) and the U operands of W x RC chunks staged in LDS (up to 128 KiB at W
+// 16 with two chunks or W 32 with one, on 8-wavefront workgroups).  Its own
 // translation unit, so these instantiations build in parallel with the rest.
 #include "lowrank_mfma_fwd_launch.h"
 
@@ -23,6 +24,10 @@ hipError_t lr_fwd_wide_dispatch(const LrProblem* pp, int G) {
   DC_LR_CASE(13, 1) DC_LR_CASE(14, 1) DC_LR_CASE(15, 1) DC_LR_CASE(16, 1)
   DC_LR_CASE(9, 2) DC_LR_CASE(10, 2) DC_LR_CASE(11, 2) DC_LR_CASE(12, 2)
   DC_LR_CASE(13, 2) DC_LR_CASE(14, 2) DC_LR_CASE(15, 2) DC_LR_CASE(16, 2)
+  DC_LR_CASE(17, 1) DC_LR_CASE(18, 1) DC_LR_CASE(19, 1) DC_LR_CASE(20, 1)
+  DC_LR_CASE(21, 1) DC_LR_CASE(22, 1) DC_LR_CASE(23, 1) DC_LR_CASE(24, 1)
+  DC_LR_CASE(25, 1) DC_LR_CASE(26, 1) DC_LR_CASE(27, 1) DC_LR_CASE(28, 1)
+  DC_LR_CASE(29, 1) DC_LR_CASE(30, 1) DC_LR_CASE(31, 1) DC_LR_CASE(32, 1)
 #undef DC_LR_CASE
   return hipErrorInvalidValue;
 }

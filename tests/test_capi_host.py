@@ -322,8 +322,8 @@ def test_kernel_paths(lib):
         assert lp(2, 300, 256, 16, 12, bf, 0, bwd) == 2        # W 9-16 at kernel ranks <= 32
         assert lp(2, 77, 200, 31, 16, bf, 1, bwd) == 2
         assert lp(1, 64, 256, 40, 9, f16, 0, bwd) == 2         # W 9, kernel rank 40: passes of taps
-        assert lp(1, 64, 256, 16, 17, bf, 0, bwd) == 2         # W 17-32 at kernel ranks <= 32: two forward
-        assert lp(4, 4096, 2048, 31, 32, f16, 1, bwd) == 2     # passes, backward passes of 4 taps
+        assert lp(1, 64, 256, 16, 17, bf, 0, bwd) == 2         # W 17-32 at kernel ranks <= 32: the forward in
+        assert lp(4, 4096, 2048, 31, 32, f16, 1, bwd) == 2     # one or two passes, backward tap passes
         assert lp(1, 64, 256, 40, 17, bf, 0, bwd) == 2         # W 17, kernel rank 40: passes of taps
         assert lp(1, 64, 256, 64, 32, bf, 0, bwd) == 2         # W 32, kernel rank 64
         assert lp(1, 64, 256, 65, 4, bf, 0, bwd) == 2          # kernel rank 65: passes of ranks

@@ -58,7 +58,7 @@ CASES = [
     (2, 2, 24, 40, 3, 3, True, 12, torch.float32),      # fp32
     (3, 2, 50, 64, 15, 12, True, 8, torch.bfloat16),    # W 12: backward as three passes of 4 taps
     (2, 1, 70, 128, 31, 10, True, 0, torch.float16),    # W 10, two rank chunks
-    (3, 2, 90, 128, 15, 20, True, 8, torch.bfloat16),   # W 20: two forward passes, five backward passes
+    (3, 2, 90, 128, 15, 20, True, 8, torch.bfloat16),   # W 20: one forward pass, three backward passes
     (3, 2, 70, 128, 127, 4, True, 8, torch.bfloat16),   # kernel rank 128: passes of ranks (2 forward, 4 backward)
     (2, 1, 50, 64, 63, 6, True, 0, torch.float16),      # kernel rank 64, W 6 (forward in one pass)
     (2, 2, 40, 64, 15, 40, True, 8, torch.bfloat16),    # W 40: the generic kernels, group by group
@@ -322,7 +322,8 @@ HEAD_CASES = [
     (3, 2, 40, 128, 15, 4, True, 32, torch.bfloat16, False),   # head dim 32: generic backward
     (2, 1, 33, 64, 7, 2, True, 16, torch.float32, False),      # fp32 head dim 16: generic kernels
     (3, 2, 60, 256, 15, 14, True, 64, torch.bfloat16, True),   # W 14: forward in one pass over the taps
-    (3, 2, 60, 256, 15, 20, True, 64, torch.bfloat16, True),   # W 20: the second forward pass adds to y
+    (3, 2, 60, 256, 15, 20, True, 64, torch.bfloat16, True),   # W 20, one rank chunk: forward in one pass
+    (3, 2, 60, 256, 16, 20, True, 64, torch.bfloat16, True),   # W 20, two chunks: the second forward pass adds to y
     (2, 1, 40, 128, 63, 12, True, 64, torch.float16, True),    # kernel rank 64, W 12: forward passes 4 + 8
     (3, 2, 60, 256, 127, 4, True, 64, torch.bfloat16, True),   # kernel rank 128: the second rank pass adds to y
     (2, 2, 45, 128, 15, 12, True, 64, torch.float32, True),    # fp32 W 12: forward passes 4 + 8

@@ -369,13 +369,14 @@ LR_EDGE = [
     (2, 77, 200, 31, 16, True, True, torch.bfloat16, ("mfma", "mfma")),        # two rank chunks: 4 x 4 taps
     (1, 3300, 256, 3, 13, False, True, torch.bfloat16, ("mfma", "mfma")),      # long runs, padded z
     (1, 64, 512, 20, 10, True, True, torch.float16, ("mfma", "mfma")),         # kernel rank 21: passes 4 + 4 + 2
-    # 17 <= W <= 32 at one or two rank chunks: the forward as two passes (taps 0 .. W-17, then the
-    # last 16 added to the stored y, x read W-16 rows earlier), the backward as passes of 8 taps (one
+    # 17 <= W <= 32 at one or two rank chunks: the forward in one pass at one chunk (x rows up to
+    # 4q-31, U chunks of all W taps in LDS), as two at two (taps 0 .. W-17, then the last 16 added
+    # to the stored y, x read W-16 rows earlier), the backward as passes of 8 taps (one
     # rank chunk: at most 4, dx rounded after each) or 4 (two: 5-8 passes into the fp32 dx
     # accumulator); long runs reach back up to 31 rows before their first tile (the runs' 32-row halo)
     (1, 25, 64, 8, 20, False, True, torch.bfloat16, ("mfma", "mfma")),         # W 20 > T
     (2, 300, 256, 16, 17, True, True, torch.bfloat16, ("mfma", "mfma")),       # forward 1 + 16 taps
-    (1, 3300, 256, 15, 32, True, True, torch.bfloat16, ("mfma", "mfma")),      # W 32: backward 4 passes of 8
+    (1, 3300, 256, 15, 32, True, True, torch.bfloat16, ("mfma", "mfma")),      # W 32: forward one pass, backward 4 x 8
     (2, 200, 128, 31, 24, True, False, torch.float16, ("mfma", "mfma")),       # two rank chunks, 8 + 16
     (1, 520, 200, 20, 28, False, True, torch.bfloat16, ("mfma", "mfma")),      # D % 16 != 0, 12 + 16
     (1, 3216, 64, 31, 25, True, True, torch.float16, ("mfma", "mfma")),        # long runs, two rank chunks
