@@ -105,7 +105,7 @@ EXTRA = {
     "hw_W24_hs32": dict(kind="hw", B=4, T=4096, D=2048, H=64, W=24, static=True, residual=True),
     # head size 8 at W 24 on the head matrix-core kernels (two heads per 16-channel block)
     "hw_W24_hs8": dict(kind="hw", B=4, T=4096, D=2048, H=256, W=24, static=True, residual=True),
-    # W 20: the forward as two passes of taps (4 + 16), the backward as three passes (7 + 7 + 6)
+    # W 20: the forward in one pass over the taps, the backward as three passes (7 + 7 + 6)
     "lr_W20": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=20, static=False, residual=True),
     # W 12 at kernel rank 40 (three rank chunks): the forward as passes of 4 + 8 taps, the backward as six of 2
     "lr_W12_r40": dict(kind="lr", B=4, T=4096, D=2048, R=40, W=12, static=False, residual=True),

@@ -150,14 +150,26 @@ __device__ __forceinline__ rsrc_t run_rsrc(const void* p, int64_t nrows, int64_t
 // results (vmcnt retires in order, so any use of a just-loaded value would also
 // wait for every load issued before it), ZRaw::finish forms the operands once
 // they are needed.  ZV (R % 4 == 0, z 8-byte aligned): one 8-byte load per rank
-// chunk, whose four ranks are all dynamic or all not; otherwise 2-byte element
-// loads (the forward only: the backward reads a padded z_eff copy instead).  Ranks >= R load nothing (out-of-range offset); finish sets the static
-// rank R (inside the sequence) to 1 and ranks beyond to 0.  `base` is the z
-// byte offset of row t, or kOobTile for a tile that does not exist.
+// chunk, whose four ranks are all dynamic or all not.  Otherwise (the forward
+// only: the backward reads a padded z_eff copy instead), at two or five to
+// eight rank chunks (ZW), one 8-byte load per rank chunk at the row's own
+// 2-byte alignment (gfx950 under HSA serves unaligned vector memory accesses)
+// that ends at rank min(r0 + 4, R), so it never reads past the row's R ranks,
+// shifted into place by finish; else 2-byte element loads.  B4 T4096 D2048 W4
+// forward against 2-byte loads: R31 + static without z_eff 33.6 -> 31.6 us,
+// configs[4] 60.4 -> 59.5 us per call (58.8 -> 57.2 without z_eff), R95 +
+// static 58.7 -> 50.7 us, R127 + static 73.8 -> 68.4 us; slower at one rank
+// chunk (R15 + static 30.4 -> 33.3 us), three (R47 + static 40.9 -> 41.8 us)
+// and four (R63 + static 45.4 -> 48.9 us), which keep the 2-byte loads.
+// Ranks >= R load nothing (out-of-range offset); finish sets the static rank R
+// (inside the sequence) to 1 and ranks beyond to 0.  `base` is the z byte
+// offset of row t, or kOobTile for a tile that does not exist.
 template <typename T, int RC, bool ZV>
 struct ZRaw {
+  // unaligned 8-byte windows (two, or five to eight, rank chunks) or 2-byte elements
+  static constexpr bool ZW = RC == 2 || RC > 4;
   u32x2 v[ZV ? RC : 1];
-  uint32_t e[ZV ? 1 : RC][4];
+  uint32_t e[ZV ? 1 : RC][ZV ? 1 : (ZW ? 2 : 4)];
 
   __device__ __forceinline__ void load(rsrc_t rz, int base, int R, int q) {
 #pragma unroll
@@ -165,6 +177,12 @@ struct ZRaw {
       const int r0 = 16 * c + 4 * q;
       if constexpr (ZV) {
         v[c] = bload64(rz, r0 < R ? base + r0 * 2 : kOobTile);
+      } else if constexpr (ZW) {
+        // R >= 16 (RC - 1): every chunk but the last holds dynamic ranks only
+        const int s = c < RC - 1 || r0 + 4 <= R ? r0 : R - 4;  // the 4 ranks ending at min(r0 + 4, R)
+        const u32x2 w = bload64(rz, c < RC - 1 || r0 < R ? base + s * 2 : kOobTile);
+        e[c][0] = w[0];
+        e[c][1] = w[1];
       } else {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) e[c][kk] = bload16(rz, r0 + kk < R ? base + (r0 + kk) * 2 : kOobTile);
@@ -181,6 +199,22 @@ struct ZRaw {
         const uint32_t s = (r0 == R && R < RK && t < Tn) ? one : 0u;
         za[c][0] = r0 < R ? v[c][0] : s;
         za[c][1] = r0 < R ? v[c][1] : 0u;
+      } else if constexpr (ZW) {
+        // m dynamic ranks in the group: when 0 < m < 4 the load holds ranks
+        // R-4 .. R-1, so ranks r0 .. R-1 are its last m elements; they move to
+        // the front, the static rank takes element m, zeros follow
+        const int m = c < RC - 1 ? 4 : R - r0;
+        const uint32_t e0 = e[c][0], e1 = e[c][1];
+        const uint32_t st = (R < RK && t < Tn) ? one : 0u;
+        const uint32_t mid = __builtin_amdgcn_alignbit(e1, e0, 16);  // elements 1, 2
+        const uint32_t top = (e1 >> 16) | (st << 16);                // element 3, static
+        uint32_t lo = e0, hi = e1;
+        if (m < 4) {
+          lo = m == 3 ? mid : m == 2 ? e1 : m == 1 ? top : m == 0 ? st : 0u;
+          hi = m == 3 ? top : m == 2 ? st : 0u;
+        }
+        za[c][0] = lo;
+        za[c][1] = hi;
       } else {
         uint32_t w[4];
 #pragma unroll

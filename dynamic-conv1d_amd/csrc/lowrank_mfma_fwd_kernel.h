@@ -110,12 +110,15 @@ __device__ __forceinline__ void stage_u(u32x2* __restrict__ lds, const uint16_t*
 // stored them, are added before the store (each lane loads and stores only its
 // own rows): a pass of taps kofs .. kofs+W-1 (above W 16 at two rank chunks
 // the host runs taps 0 .. W-17 first, then the last 16), whose x is read kofs
-// rows earlier, or a
-// pass of kernel ranks (above 64: z columns and U rows from the pass's first
-// rank, kofs 0 unless taps are split as well).
+// rows earlier, or a pass of kernel ranks (above 64: z columns and U rows from
+// the pass's first rank, kofs 0 unless taps are split as well).
+//
+// Up to W 4 with one or two rank chunks the kernels are held to 4 wavefronts
+// per SIMD (128 VGPRs): the z_eff writer, and the unaligned z loads of two
+// rank chunks (ZRaw), would otherwise take 138-140.
 template <typename T, int W, int RC, bool ZV, bool ZE, bool ILP = false, bool ACC = false>
 __global__ __launch_bounds__(64 * fwd_wg_waves(W, RC))
-__attribute__((amdgpu_waves_per_eu(ZE && W <= 4 && RC <= 2 ? 4 : 1, 8)))
+__attribute__((amdgpu_waves_per_eu((ZE || !ZV) && W <= 4 && RC <= 2 ? 4 : 1, 8)))
 void lr_fwd_mfma(LrArgs a) {
   constexpr int NR = W + 3;  // x rows 4q-W+1 .. 4q+3 of a lane
   constexpr int NWV = fwd_wg_waves(W, RC);

@@ -323,7 +323,7 @@ HEAD_CASES = [
     (2, 1, 33, 64, 7, 2, True, 16, torch.float32, False),      # fp32 head dim 16: generic kernels
     (3, 2, 60, 256, 15, 14, True, 64, torch.bfloat16, True),   # W 14: forward in one pass over the taps
     (3, 2, 60, 256, 15, 20, True, 64, torch.bfloat16, True),   # W 20, one rank chunk: forward in one pass
-    (3, 2, 60, 256, 16, 20, True, 64, torch.bfloat16, True),   # W 20, two chunks: the second forward pass adds to y
+    (3, 2, 60, 256, 31, 20, True, 64, torch.bfloat16, True),   # W 20, two chunks: the second forward pass adds to y
     (2, 1, 40, 128, 63, 12, True, 64, torch.float16, True),    # kernel rank 64, W 12: forward passes 4 + 8
     (3, 2, 60, 256, 127, 4, True, 64, torch.bfloat16, True),   # kernel rank 128: the second rank pass adds to y
     (2, 2, 45, 128, 15, 12, True, 64, torch.float32, True),    # fp32 W 12: forward passes 4 + 8

@@ -406,6 +406,15 @@ LR_EDGE = [
     (1, 37, 64, 100, 16, True, True, torch.bfloat16, ("mfma", "mfma")),       # rank 101, W 16: 2 x 2, 4 x 4
     (1, 45, 64, 127, 12, True, True, torch.bfloat16, ("mfma", "mfma")),       # W 12: forward 2 x (4 + 8)
     (1, 520, 200, 70, 5, False, False, torch.float16, ("mfma", "mfma")),      # D % 16 != 0, rank 70, W 5
+    # z rows of R % 4 != 0 ranks at two or five to eight rank chunks: 8-byte loads at the rows'
+    # 2-byte alignment, the last chunk's boundary group loaded as the 4 ranks that end at R (m = R -
+    # 4q - 16(RC-1) dynamic ranks in it, then the static rank, then zeros)
+    (2, 70, 64, 17, 4, False, True, torch.bfloat16, ("mfma", "mfma")),        # m = 1
+    (1, 90, 128, 18, 3, True, False, torch.bfloat16, ("mfma", "mfma")),       # m = 2, static after
+    (1, 61, 64, 19, 2, True, True, torch.float16, ("mfma", "mfma")),          # m = 3, static after
+    (1, 50, 128, 29, 4, False, True, torch.bfloat16, ("mfma", "mfma")),       # m = 1 in group 3
+    (1, 45, 64, 93, 4, True, True, torch.bfloat16, ("mfma", "mfma")),         # six chunks, m = 1
+    (1, 40, 64, 118, 3, False, False, torch.float16, ("mfma", "mfma")),       # eight chunks, m = 2
     # the forward past 4 passes takes the generic kernels (its y would be rounded more often)
     (1, 64, 256, 127, 20, True, True, torch.bfloat16, ("generic", "mfma")),   # 2 x 3 forward passes
     (1, 30, 32, 255, 3, True, False, torch.float32, ("generic", "generic")),  # fp32 kernel rank 256
