@@ -107,11 +107,12 @@ EXTRA = {
     "hw_W24_hs8": dict(kind="hw", B=4, T=4096, D=2048, H=256, W=24, static=True, residual=True),
     # W 20: the forward in one pass over the taps, the backward as three passes (7 + 7 + 6)
     "lr_W20": dict(kind="lr", B=4, T=4096, D=2048, R=16, W=20, static=False, residual=True),
-    # W 12 at kernel rank 40 (three rank chunks): the forward as passes of 4 + 8 taps, the backward as six of 2
+    # W 12 at kernel rank 40 (three rank chunks): the forward as passes of 4 + 8 taps, the backward as
+    # two passes of 32 + 8 ranks x three of 4 taps
     "lr_W12_r40": dict(kind="lr", B=4, T=4096, D=2048, R=40, W=12, static=False, residual=True),
     # kernel rank 128 (R 127 + static): the forward in one pass of 128 ranks, the backward as four
-    # passes of 32 (the generic kernels took 1.9 + 15.0 ms here), and kernel rank 32 at the same shape
-    # for its bytes per microsecond
+    # passes of 32 into the fp32 dx accumulator (the generic kernels took 1.9 + 15.0 ms here), and
+    # kernel rank 32 at the same shape for its bytes per microsecond
     "lr_r128": dict(kind="lr", B=4, T=4096, D=2048, R=127, W=4, static=True, residual=True),
     "lr_r32_b4": dict(kind="lr", B=4, T=4096, D=2048, R=31, W=4, static=True, residual=True),
     # kernel rank 64 (R 63 + static): the forward in one pass of four rank chunks, the backward as

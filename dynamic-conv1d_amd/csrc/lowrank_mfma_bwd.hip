@@ -874,11 +874,18 @@ inline int bwd_rank_passes(const LrProblem& p) {
 
 // More than four passes (ranks x taps) add dx into an fp32 accumulator in the
 // workspace, rounded to dx once by lr_dx_round (above W 16 at two rank chunks,
-// above W 8 at three, above W 4 at four; above kernel rank 64 past four rank x
-// tap passes; one rank chunk takes at most four passes of 8 taps up to W 32).
+// above W 8 at three, above W 4 at four; one rank chunk takes at most four
+// passes of 8 taps up to W 32), and so do more than two where the passes split
+// the ranks: each rank pass adds a partial tap weight whose terms can cancel
+// (dx near zero from partials of several units), and three or four roundings
+// of such partials left single entries past the elementwise bar in a random
+// sweep (|dx - dx_oracle| 0.0217 at R104 + static W1, 4 passes, and 0.0219 at
+// R73 + static W2, 3 passes, against 0.02 + 2%).
 constexpr int kBwdMaxBf16DxPasses = 4;
+constexpr int kBwdMaxBf16DxRankPasses = 2;
 inline bool bwd_f32dx(const LrProblem& p) {
-  return bwd_rank_passes(p) * npasses((int)p.W, bwd_rc(p)) > kBwdMaxBf16DxPasses;
+  const int np = bwd_rank_passes(p) * npasses((int)p.W, bwd_rc(p));
+  return np > kBwdMaxBf16DxPasses || (bwd_rank_passes(p) > 1 && np > kBwdMaxBf16DxRankPasses);
 }
 
 }  // namespace
