@@ -70,6 +70,7 @@ struct LrBwdGroup {
   void* dx;        // this group's first channel; rows dxld elements apart
   float* part_dz;
   float* part_du;
+  void* dxs;       // the last pass over the fp32 accumulator (DXM 2): dx itself, rows dxsld apart
 };
 
 struct LrBwdArgs {
@@ -83,7 +84,8 @@ struct LrBwdArgs {
   int nblk;   // ncg * npair * groups
   int nblk1;  // ncg * npair: blocks per group
   int xld;    // row stride of x (elements)
-  int dxld;   // row stride of dx (elements)
+  int dxld;   // row stride of dx (elements; the fp32 accumulator's D past four passes)
+  int dxsld;  // row stride of dx for the last pass over the accumulator (DXM 2)
   // z rows: zld elements apart, ranks < zr loaded, ranks zr .. zrk-1 of z_eff
   // added as the static rank (ZRaw).  z itself (zld = zr = R, zrk = RK) when
   // R % 4 == 0 and z is 8-byte aligned, else the padded z_eff copy in the
@@ -230,10 +232,11 @@ __device__ __forceinline__ void stage_uw32(u32x4 (&uw)[W * NJ], const uint16_t* 
     }
 }
 
-// A lane's NJ channels of one dx row as the passes of taps keep them: the
-// output type (DxVec<T, NJ, false>), or above W 16 an fp32 accumulator in the
-// workspace (DxVec<T, NJ, true>), rounded to dx once after the last pass (more
-// passes than 4 rounded in 16 bits each drift past the north-star bar).
+// A lane's NJ channels of one dx row as the passes keep them: the output type
+// (DxVec<T, NJ, false>), or past four passes (two that split the ranks) an
+// fp32 accumulator in the workspace (DxVec<T, NJ, true>), which the last pass
+// rounds to dx once (more passes rounded in 16 bits each drift past the
+// north-star bar).
 template <typename T, int NJ, bool F32> struct DxVec {
   typedef LaneVec<NJ> LV;
   typedef typename LV::type type;
@@ -271,9 +274,11 @@ template <int RC> struct ZOp<RC, true> { u32x4 v; };
 
 // ACC: a later pass of taps (the host splits wide W), which adds its dx to
 // what the earlier passes stored; a separate instantiation, so single-pass
-// launches carry none of it.  F32: dx rows are the fp32 accumulator (the
-// group's dx pointer and dxld then address it), above W 16.
-template <typename T, int W, int RC, int NRW, int CPW, bool ACC, bool F32 = false>
+// launches carry none of it.  DXM 1: dx rows are the fp32 accumulator (the
+// group's dx pointer and dxld then address it), past four passes (or two that
+// split the ranks); DXM 2: the last such pass, which adds to the accumulator's
+// rows and stores dx itself (dxs, dxsld) rounded once.
+template <typename T, int W, int RC, int NRW, int CPW, bool ACC, int DXM = 0>
 __global__ __launch_bounds__(64 * (256 / CPW) * NRW)
 __attribute__((amdgpu_waves_per_eu((W <= 4 && (RC == 1 || CPW == 32)) || (RC == 1 && CPW == 32) ? 2 : 1, 8))) void
 lr_bwd_mfma(LrBwdArgs a) {
@@ -284,7 +289,11 @@ lr_bwd_mfma(LrBwdArgs a) {
   static_assert(CPW == 64 || CPW == 32, "64- or 32-channel tiles");
   static_assert(NRW == 1 || (RC == 1 && W <= 4 && CPW == 64), "two runs per workgroup: one rank chunk, W <= 4");
   typedef LaneVec<NJ> LV;
-  typedef DxVec<T, NJ, F32> DV;
+  // dx rows: loaded as DV, stored as DVS (DXM 0: the output type; 1: the fp32
+  // accumulator; 2: the last pass, which adds to the accumulator's rows and
+  // stores dx itself, rounded once)
+  typedef DxVec<T, NJ, DXM != 0> DV;
+  typedef DxVec<T, NJ, DXM == 1> DVS;
   // dx in scatter form for 2 <= W <= 4 (SC): tap weights of the lane's own rows
   // only, partial sums for the rows of the group above passed across lanes.
   // Otherwise (gather form) NB row blocks of tap weights cover the look-ahead.
@@ -393,16 +402,20 @@ lr_bwd_mfma(LrBwdArgs a) {
   // stay out of range either way).
   const int yhd = a.yhd, head = d0 / yhd;
   const int rowb = yhd * 2, xrowb = a.xld * 2, dxrowb = a.dxld * DV::ES;
+  const int dxsld = DXM == 2 ? a.dxsld : a.dxld, dxsrowb = dxsld * DVS::ES;
   // resources of the run's rows from rb (offsets below are relative to row rb)
   const rsrc_t rx = run_rsrc(x + rrow * a.xld, Tn - rb, xrowb);
   const rsrc_t rdy = run_rsrc(dy + row0 * D + ((int64_t)head * Tn + rb) * yhd, Tn - rb, rowb);
   const rsrc_t rdx = run_rsrc(dx + rrow * a.dxld * DV::ES, Tn - rb, dxrowb);
+  char* __restrict__ dxs = DXM == 2 ? reinterpret_cast<char*>(pick(a.grp, g, &LrBwdGroup::dxs)) : dx;
+  const rsrc_t rdxs = DXM == 2 ? run_rsrc(dxs + rrow * dxsld * DVS::ES, Tn - rb, dxsrowb) : rdx;
   const int zld = a.zld, zr = a.zr, zrk = a.zrk;
   const rsrc_t rz = run_rsrc(z + rrow * zld, Tn - rb, zld * 2);
   // byte offsets of the lane's row-4q channels in dy, x and dx
   const int lane_off = chv ? (4 * q * yhd + col - head * yhd) * 2 : kOobLane;
   const int xlane_off = chv ? (4 * q * a.xld + col) * 2 : kOobLane;
   const int dxlane_off = chv ? (4 * q * a.dxld + col) * DV::ES : kOobLane;
+  const int dxslane_off = chv ? (4 * q * dxsld + col) * DVS::ES : kOobLane;  // the stores
 
   u32x2 uw_reg[UWREG && !K32 ? NUW : 1];  // staged below, after the first tile's loads are issued
   u32x4 uw32[K32 ? W * NJ : 1];
@@ -510,8 +523,8 @@ lr_bwd_mfma(LrBwdArgs a) {
     const bool top = q == 3;
     const bool cur_live = tile < tile1;
     const bool prev_live = tile > tile0 && tile <= tile1;
-    const int cur_off = cur_live ? dxlane_off + (tile * 16 - rb - kofs) * dxrowb : kOobTile;
-    const int prev_off = prev_live ? dxlane_off + ((tile - 1) * 16 - rb - kofs) * dxrowb : kOobTile;
+    const int cur_off = cur_live ? dxslane_off + (tile * 16 - rb - kofs) * dxsrowb : kOobTile;
+    const int prev_off = prev_live ? dxslane_off + ((tile - 1) * 16 - rb - kofs) * dxsrowb : kOobTile;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       constexpr int kFirstOpen = 4 - NOPEN;
@@ -523,14 +536,14 @@ lr_bwd_mfma(LrBwdArgs a) {
         if (open) b = (top ? carry[i - kFirstOpen][j] : b) + recv[3 - i][j];
         v[j] = b;
       }
-      const int off = (top && open ? prev_off : cur_off) + i * dxrowb;
+      const int off = (top && open ? prev_off : cur_off) + i * dxsrowb;
       if constexpr (ACC) {  // a later pass of taps adds to the stored rows
         typename DV::type o = dxo[ACC ? i : 0];
         if (open) o = top ? dxo_carry[ACC ? i - kFirstOpen : 0] : o;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) v[j] += DV::get(o, j);
       }
-      DV::store(DV::make(v), rdx, off);
+      DVS::store(DVS::make(v), rdxs, off);
     }
 #pragma unroll
     for (int i = 0; i < NOPEN; ++i)
@@ -572,7 +585,7 @@ lr_bwd_mfma(LrBwdArgs a) {
     const int tile = tile0 + it;
     const bool live = tile < tile1;
     const int t0 = tile * 16;
-    const int dxtoff = live ? (t0 - rb - kofs) * dxrowb : kOobTile;  // tiles past the run store nothing
+    const int dxtoff = live ? (t0 - rb - kofs) * dxsrowb : kOobTile;  // tiles past the run store nothing
     const typename LV::type(&xr)[NR] = in.xr;
     const typename LV::type(&dyr)[NDY] = in.dyr;
     ZO zA[NB];
@@ -669,12 +682,12 @@ lr_bwd_mfma(LrBwdArgs a) {
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int off = dxlane_off + dxtoff + i * dxrowb;
+        const int off = dxslane_off + dxtoff + i * dxsrowb;
         if constexpr (ACC) {  // a later pass of taps adds to the stored rows (loaded with the tile)
 #pragma unroll
           for (int j = 0; j < NJ; ++j) dxa[i][j] += DV::get(in.dxo[ACC ? i : 0], j);
         }
-        DV::store(DV::make(dxa[i]), rdx, off);
+        DVS::store(DVS::make(dxa[i]), rdxs, off);
       }
     }
     // ---- dz: gather this wavefront's tile sums; every DZB iterations (and at the
@@ -873,7 +886,9 @@ inline int bwd_rank_passes(const LrProblem& p) {
 }
 
 // More than four passes (ranks x taps) add dx into an fp32 accumulator in the
-// workspace, rounded to dx once by lr_dx_round (above W 16 at two rank chunks,
+// workspace, whose last pass stores dx itself, rounded once (DXM 2; a launch
+// that rounded the whole accumulator after the passes took 55 us more at B4
+// T4096 D2048 R127 + static W4: 456 -> 400 us) (above W 16 at two rank chunks,
 // above W 8 at three, above W 4 at four; one rank chunk takes at most four
 // passes of 8 taps up to W 32), and so do more than two where the passes split
 // the ranks: each rank pass adds a partial tap weight whose terms can cancel
@@ -928,7 +943,9 @@ int64_t lr_bwd_max_run_tiles(const LrProblem& p) {
   int64_t rowb = p.xld() * 2;
   // past four passes of taps the passes' dx rows are the fp32 accumulator (D floats each)
   const int64_t dxb = bwd_f32dx(p) ? p.D * 4 : p.dxld() * 2;
-  const int64_t others[4] = {dxb, p.yhd() * 2, lr_bwd_zrow(p.R, p.static_w != nullptr, p.W) * 2, p.R * 4};
+  // (the last pass over the accumulator also stores dx rows of dxld elements)
+  const int64_t others[5] = {dxb, p.dxld() * 2, p.yhd() * 2, lr_bwd_zrow(p.R, p.static_w != nullptr, p.W) * 2,
+                             p.R * 4};
   for (int64_t v : others) rowb = rowb > v ? rowb : v;
   return run_tiles_cap(rowb);
 }
@@ -964,6 +981,7 @@ LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   a.uld = (int)(p.W * p.D);
   a.kofs = 0;
   a.accdx = 0;
+  a.dxsld = 0;
   a.dzld = a.R;
   a.dupr = a.RK;
   return a;
@@ -1032,32 +1050,39 @@ void audit_bwd_pass(const LrBwdArgs& b, int wq, bool f32) {
   audit_range(lr_u_bytes(b.R, b.uld, b.kofs, D, 2), kOobLane);
   audit_range(lr_sw_bytes(b.RK > b.R, wq, D, 2), kOobLane);
   audit_range(lr_dupart_bytes(b.RK, b.uld, b.kofs, D), kOobLane);
-  const int64_t rows[5] = {(int64_t)b.xld * 2, (int64_t)b.yhd * 2, (int64_t)b.dxld * (f32 ? 4 : 2),
-                           (int64_t)b.zld * 2, (int64_t)b.dzld * 4};
+  const int64_t rows[6] = {(int64_t)b.xld * 2, (int64_t)b.yhd * 2, (int64_t)b.dxld * (f32 ? 4 : 2),
+                           (int64_t)b.zld * 2, (int64_t)b.dzld * 4, (int64_t)b.dxsld * 2};
   for (int64_t rowb : rows) audit_range(run_rsrc_bytes(b.Tn, rowb), kOobTile - 15 * rowb);
 }
 
-// dx from the passes' fp32 accumulator (rows of D floats): each group's rows
-// rounded once to the output type, into dx rows dxld elements apart.
+// dx rows T-kt .. T-1 of every sequence from the passes' fp32 accumulator
+// (rows of D floats), rounded to the output type into dx rows dxld elements
+// apart: the rows that the last pass over the accumulator, whose taps start at
+// kt, does not store.
 struct DxRoundGroup {
   const float* src;
   uint16_t* dst;
 };
 struct DxRoundArgs {
-  int64_t n4;   // BT * D / 4 quads per group
+  int64_t n4;   // B * kt * D / 4 quads per group
   int dq;       // D / 4 quads per row
+  int kt;       // rows per sequence
+  int Tn;
   int64_t dld;  // row stride of dx (elements, a multiple of 4)
   DxRoundGroup grp[kMaxGroups];
 };
 
 template <typename T>
-__global__ __launch_bounds__(256) void lr_dx_round(DxRoundArgs a) {
+__global__ __launch_bounds__(256) void lr_dx_round_tail(DxRoundArgs a) {
   const int g = blockIdx.y;
   const float* __restrict__ src = pick(a.grp, g, &DxRoundGroup::src);
   uint16_t* __restrict__ dst = pick(a.grp, g, &DxRoundGroup::dst);
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < a.n4; e += (int64_t)gridDim.x * 256) {
-    const int64_t row = e / a.dq, c = (e - row * a.dq) * 4;
-    const float4 v = *reinterpret_cast<const float4*>(src + e * 4);
+    const int64_t rl = e / a.dq;  // the tail row of the sequences, in order
+    const int c = (int)(e - rl * a.dq) * 4;
+    const int64_t b = rl / a.kt;
+    const int64_t row = b * a.Tn + a.Tn - a.kt + (rl - b * a.kt);
+    const float4 v = *reinterpret_cast<const float4*>(src + row * a.dq * 4 + c);
     u32x2 o;
     o[0] = pack2<T>(v.x, v.y);
     o[1] = pack2<T>(v.z, v.w);
@@ -1066,24 +1091,26 @@ __global__ __launch_bounds__(256) void lr_dx_round(DxRoundArgs a) {
 }
 
 template <typename T>
-hipError_t launch_dx_round(const LrProblem* p, int G, int64_t dxf_off) {
+hipError_t launch_dx_round_tail(const LrProblem* p, int G, int64_t dxf_off, int kofs) {
   if (auditing()) return hipSuccess;  // plain pointers
   DxRoundArgs a;
-  a.n4 = p[0].B * p[0].T * p[0].D / 4;
+  a.kt = (int)(kofs < p[0].T ? kofs : p[0].T);
+  a.Tn = (int)p[0].T;
   a.dq = (int)(p[0].D / 4);
+  a.n4 = p[0].B * a.kt * a.dq;
   a.dld = p[0].dxld();
   for (int g = 0; g < kMaxGroups; ++g) {
     const LrProblem& q = p[g < G ? g : 0];
     a.grp[g] = DxRoundGroup{(const float*)((const char*)q.ws + dxf_off), (uint16_t*)q.dx};
   }
   const int64_t blocks = (a.n4 + 255) / 256;
-  lr_dx_round<T><<<dim3((unsigned)(blocks < 8192 ? blocks : 8192), G), 256, 0, p[0].stream>>>(a);
+  lr_dx_round_tail<T><<<dim3((unsigned)(blocks < 8192 ? blocks : 8192), G), 256, 0, p[0].stream>>>(a);
   return hipGetLastError();
 }
 
 // Workspace: [dz partials: passes x ncg x BT x R fp32][dU partials: npair x RK
-// x W*D fp32][padded z_eff: BT x RP of z's type][above W 16: the fp32 dx
-// accumulator, BT x D], each 256-byte aligned.  The z_eff part is reserved
+// x W*D fp32][padded z_eff: BT x RP of z's type][past four passes, or two
+// that split the ranks: the fp32 dx accumulator, BT x D], each 256-byte aligned.  The z_eff part is reserved
 // whatever the pointers' alignment (the size query has none).
 struct BwdWs {
   int64_t dz_off, du_off, zp_off, dxf_off, total;
@@ -1104,11 +1131,13 @@ template <typename T, int W, int RC, bool WIDE = false, bool F32 = false>
 hipError_t launch_bwd_kernel(const LrBwdArgs& a, hipStream_t stream) {
   constexpr BwdShape SH = bwd_shape(W, RC, WIDE);  // as make_bwd_args
   constexpr int NRW = SH.nrw, CPW = SH.cpw, NT = 64 * (256 / CPW) * NRW;
-  if constexpr (F32) {  // above W 16: every pass on the fp32 dx accumulator
-    if (a.accdx)
-      lr_bwd_mfma<T, W, RC, NRW, CPW, true, true><<<a.nblk, NT, 0, stream>>>(a);
+  if constexpr (F32) {  // every pass on the fp32 dx accumulator; the last one stores dx itself
+    if (a.accdx && a.dxsld > 0)
+      lr_bwd_mfma<T, W, RC, NRW, CPW, true, 2><<<a.nblk, NT, 0, stream>>>(a);
+    else if (a.accdx)
+      lr_bwd_mfma<T, W, RC, NRW, CPW, true, 1><<<a.nblk, NT, 0, stream>>>(a);
     else
-      lr_bwd_mfma<T, W, RC, NRW, CPW, false, true><<<a.nblk, NT, 0, stream>>>(a);
+      lr_bwd_mfma<T, W, RC, NRW, CPW, false, 1><<<a.nblk, NT, 0, stream>>>(a);
     return hipGetLastError();
   }
   // later passes of taps: problems of 2+ rank chunks, and one rank chunk above W 8
@@ -1207,6 +1236,7 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
     a.dxld = (int)D;
     for (int g = 0; g < G; ++g) a.grp[g].dx = (char*)p[g].ws + w.dxf_off;
   }
+  a.dxsld = 0;
   for (int i = 0; i < np; ++i) {
     // pass i: ranks rofs .. (z from column rofs, U and the dU partial rows from
     // row rofs, dz partial columns from rofs, static_w in the pass that holds
@@ -1220,6 +1250,10 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
     b.kofs = f.kofs;
     b.accdx = i > 0;
     b.residual = a.residual && i == 0;
+    if (f32 && i == np - 1) {  // the last pass adds to the accumulator and stores dx, rounded once
+      b.dxsld = (int)p[0].dxld();
+      for (int g = 0; g < G; ++g) b.grp[g].dxs = p[g].dx;
+    }
     for (int g = 0; g < G; ++g) {
       b.grp[g].z = static_cast<const T*>(a.grp[g].z) + f.rofs;
       b.grp[g].U = (const T*)p[g].U + f.rofs * WD + f.kofs * D;
@@ -1233,7 +1267,11 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
     }
     if ((e = dispatch_bwd_kernel<T>(b, f.W, rc, rc == 1 && p[0].W > 4, f32, p[0].stream)) != hipSuccess) return e;
   }
-  if (f32 && (e = launch_dx_round<T>(p, G, w.dxf_off)) != hipSuccess) return e;
+  // The last pass stores dx rows 0 .. T-1-kofs of its taps kofs ..; the rows
+  // after those (no terms of its taps) are rounded from the accumulator here
+  // (passes that split only the ranks have kofs 0: nothing left).
+  if (f32 && ps[np - 1].kofs > 0 && (e = launch_dx_round_tail<T>(p, G, w.dxf_off, ps[np - 1].kofs)) != hipSuccess)
+    return e;
   PartialReduce jobs[kMaxReduceJobs];
   int nj = 0;
   const int nslot = npasses((int)p[0].W, rc);
