@@ -111,7 +111,7 @@ EXTRA = {
     # two passes of 32 + 8 ranks x three of 4 taps
     "lr_W12_r40": dict(kind="lr", B=4, T=4096, D=2048, R=40, W=12, static=False, residual=True),
     # kernel rank 128 (R 127 + static): the forward in one pass of 128 ranks, the backward as four
-    # passes of 32 into the fp32 dx accumulator (the generic kernels took 1.9 + 15.0 ms here), and
+    # passes of 32 for dz / dU and one launch for dx (the generic kernels took 1.9 + 15.0 ms here), and
     # kernel rank 32 at the same shape for its bytes per microsecond
     "lr_r128": dict(kind="lr", B=4, T=4096, D=2048, R=127, W=4, static=True, residual=True),
     "lr_r32_b4": dict(kind="lr", B=4, T=4096, D=2048, R=31, W=4, static=True, residual=True),

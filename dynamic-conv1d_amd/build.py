@@ -51,6 +51,7 @@ COMMON = [
 # for instruction-level parallelism (see that file).
 PER_FILE = {"lowrank_mfma_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
             "lowrank_mfma_fwd_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+            "lowrank_mfma_dx.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
             "lowrank_mfma_fwd_ilp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-sched-strategy=max-ilp"],
             "lowrank_f32_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 

@@ -229,6 +229,11 @@ struct ZRaw {
   }
 };
 
+// dx of the backward over all kernel ranks in one launch (lowrank_mfma_dx.hip;
+// the passes of ranks then form dz and dU only).
+template <typename T>
+hipError_t lr_dx_mfma_launch(const LrProblem* p, int G);
+
 inline bool aligned_to(const void* p, int a) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 // Longest run (in 16-row tiles) whose rows fit the resource cap when rows are

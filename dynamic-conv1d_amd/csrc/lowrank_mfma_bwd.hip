@@ -86,6 +86,7 @@ struct LrBwdArgs {
   int xld;    // row stride of x (elements)
   int dxld;   // row stride of dx (elements; the fp32 accumulator's D past four passes)
   int dxsld;  // row stride of dx for the last pass over the accumulator (DXM 2)
+  int nodx;   // dz and dU only (DXM 3): a separate launch (lr_dx_mfma) forms dx over all ranks
   // z rows: zld elements apart, ranks < zr loaded, ranks zr .. zrk-1 of z_eff
   // added as the static rank (ZRaw).  z itself (zld = zr = R, zrk = RK) when
   // R % 4 == 0 and z is 8-byte aligned, else the padded z_eff copy in the
@@ -277,7 +278,8 @@ template <int RC> struct ZOp<RC, true> { u32x4 v; };
 // launches carry none of it.  DXM 1: dx rows are the fp32 accumulator (the
 // group's dx pointer and dxld then address it), past four passes (or two that
 // split the ranks); DXM 2: the last such pass, which adds to the accumulator's
-// rows and stores dx itself (dxs, dxsld) rounded once.
+// rows and stores dx itself (dxs, dxsld) rounded once; DXM 3: no dx at all
+// (the passes of ranks when lr_dx_mfma forms dx in one launch over all ranks).
 template <typename T, int W, int RC, int NRW, int CPW, bool ACC, int DXM = 0>
 __global__ __launch_bounds__(64 * (256 / CPW) * NRW)
 __attribute__((amdgpu_waves_per_eu((W <= 4 && (RC == 1 || CPW == 32)) || (RC == 1 && CPW == 32) ? 2 : 1, 8))) void
@@ -292,7 +294,8 @@ lr_bwd_mfma(LrBwdArgs a) {
   // dx rows: loaded as DV, stored as DVS (DXM 0: the output type; 1: the fp32
   // accumulator; 2: the last pass, which adds to the accumulator's rows and
   // stores dx itself, rounded once)
-  typedef DxVec<T, NJ, DXM != 0> DV;
+  constexpr bool NODX = DXM == 3;
+  typedef DxVec<T, NJ, DXM == 1 || DXM == 2> DV;
   typedef DxVec<T, NJ, DXM == 1> DVS;
   // dx in scatter form for 2 <= W <= 4 (SC): tap weights of the lane's own rows
   // only, partial sums for the rows of the group above passed across lanes.
@@ -643,10 +646,10 @@ lr_bwd_mfma(LrBwdArgs a) {
         for (int j = 0; j < NJ; ++j) gf[i][j] = dyf[i][j] * Mma16<T>::to_f(LV::elem(xr[i - k + W - 1], j));
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        if constexpr (SC) scatter_taps(zA[0], dyf, k, j, dxa, S);
+        if constexpr (SC && !NODX) scatter_taps(zA[0], dyf, k, j, dxa, S);
         // Gather form: dx += dy[4q+i+k] * Kw[4q+i+k, k] from the row blocks that hold rows k..k+3.
 #pragma unroll
-        for (int bb = 0; bb < (SC ? 0 : NB); ++bb) {
+        for (int bb = 0; bb < (SC || NODX ? 0 : NB); ++bb) {
           if (4 * bb > 3 + k || 4 * bb + 3 < k) continue;
           const f32x4 wk = tap_w(zA[bb], k, j, k == 0 ? res : 0.f);  // k = 0 uses block 0 only
 #pragma unroll
@@ -677,7 +680,8 @@ lr_bwd_mfma(LrBwdArgs a) {
     }
 
     // ---- dx rows (the residual dy rides on tap 0's weight); out-of-range stores are dropped
-    if constexpr (SC) {
+    if constexpr (NODX) {
+    } else if constexpr (SC) {
       close_rows(dxa, S, tile, in.dxo);
     } else {
 #pragma unroll
@@ -751,7 +755,7 @@ lr_bwd_mfma(LrBwdArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     if (it + 1 < nit) compute_tile(it + 1, tb);
   }
-  if constexpr (SC) {
+  if constexpr (SC && !NODX) {
     // The tile after the longest run (loaded into the buffer that is next in
     // turn) closes that run's last rows; in shorter runs it lies past tile1
     // and stores nothing.
@@ -898,10 +902,20 @@ inline int bwd_rank_passes(const LrProblem& p) {
 // R73 + static W2, 3 passes, against 0.02 + 2%).
 constexpr int kBwdMaxBf16DxPasses = 4;
 constexpr int kBwdMaxBf16DxRankPasses = 2;
-inline bool bwd_f32dx(const LrProblem& p) {
+// Passes of ranks at W <= 4 up to kernel rank 128 with dy in [B, T, D]: the
+// passes form dz and dU only (DXM 3) and lr_dx_mfma forms dx over all ranks in
+// one launch, rounded once (no fp32 accumulator).
+inline bool bwd_dx_split(const LrProblem& p) {
+  const int64_t rk = p.R + (p.static_w ? 1 : 0);
+  return bwd_rank_split(p) && p.W <= 4 && rk <= 128 && p.yhd() == p.D;
+}
+// The workspace keeps room for the accumulator whether or not dx is split off:
+// the size queries do not see dy's layout, on which the split depends.
+inline bool bwd_f32dx_room(const LrProblem& p) {
   const int np = bwd_rank_passes(p) * npasses((int)p.W, bwd_rc(p));
   return np > kBwdMaxBf16DxPasses || (bwd_rank_passes(p) > 1 && np > kBwdMaxBf16DxRankPasses);
 }
+inline bool bwd_f32dx(const LrProblem& p) { return !bwd_dx_split(p) && bwd_f32dx_room(p); }
 
 }  // namespace
 
@@ -942,7 +956,7 @@ int bwd_plan(const LrProblem& p, BwdPass* out) {
 int64_t lr_bwd_max_run_tiles(const LrProblem& p) {
   int64_t rowb = p.xld() * 2;
   // past four passes of taps the passes' dx rows are the fp32 accumulator (D floats each)
-  const int64_t dxb = bwd_f32dx(p) ? p.D * 4 : p.dxld() * 2;
+  const int64_t dxb = bwd_f32dx_room(p) ? p.D * 4 : p.dxld() * 2;
   // (the last pass over the accumulator also stores dx rows of dxld elements)
   const int64_t others[5] = {dxb, p.dxld() * 2, p.yhd() * 2, lr_bwd_zrow(p.R, p.static_w != nullptr, p.W) * 2,
                              p.R * 4};
@@ -982,6 +996,7 @@ LrBwdArgs make_bwd_args(const LrProblem& p, int target_waves) {
   a.kofs = 0;
   a.accdx = 0;
   a.dxsld = 0;
+  a.nodx = 0;
   a.dzld = a.R;
   a.dupr = a.RK;
   return a;
@@ -1123,7 +1138,7 @@ BwdWs bwd_ws(const LrProblem& p, const LrBwdArgs& a) {
   w.du_off = (dz + 255) / 256 * 256;
   w.zp_off = (w.du_off + (int64_t)a.npair * a.RK * p.W * p.D * 4 + 255) / 256 * 256;
   w.dxf_off = (w.zp_off + a.BT * zpad_ranks(p) * 2 + 255) / 256 * 256;
-  w.total = w.dxf_off + (bwd_f32dx(p) ? a.BT * p.D * 4 : 0);
+  w.total = w.dxf_off + (bwd_f32dx_room(p) ? a.BT * p.D * 4 : 0);
   return w;
 }
 
@@ -1142,6 +1157,12 @@ hipError_t launch_bwd_kernel(const LrBwdArgs& a, hipStream_t stream) {
   }
   // later passes of taps: problems of 2+ rank chunks, and one rank chunk above W 8
   // (WIDE: passes of at most 8 taps)
+  if constexpr (RC == 2 && !WIDE) {  // passes of ranks without dx (lr_dx_mfma forms it)
+    if (a.nodx) {
+      lr_bwd_mfma<T, W, RC, NRW, CPW, false, 3><<<a.nblk, NT, 0, stream>>>(a);
+      return hipGetLastError();
+    }
+  }
   if constexpr (RC >= 2 || WIDE) {
     if (a.accdx) {
       lr_bwd_mfma<T, W, RC, NRW, CPW, true><<<a.nblk, NT, 0, stream>>>(a);
@@ -1231,7 +1252,8 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
   const int64_t D = p[0].D, WD = p[0].W * D, RKWD = (int64_t)a.RK * WD, R = p[0].R;
   const int64_t dz_slot = (int64_t)a.ncg * a.BT * R;  // one pass of taps' dz partials
   // past four passes every pass works on the fp32 accumulator (rows of D floats)
-  const bool f32 = bwd_f32dx(p[0]);
+  const bool f32 = bwd_f32dx(p[0]), dxs = bwd_dx_split(p[0]);
+  a.nodx = dxs ? 1 : 0;
   if (f32) {
     a.dxld = (int)D;
     for (int g = 0; g < G; ++g) a.grp[g].dx = (char*)p[g].ws + w.dxf_off;
@@ -1267,6 +1289,7 @@ hipError_t launch_bwd(const LrProblem* p, int G) {
     }
     if ((e = dispatch_bwd_kernel<T>(b, f.W, rc, rc == 1 && p[0].W > 4, f32, p[0].stream)) != hipSuccess) return e;
   }
+  if (dxs && (e = lr_dx_mfma_launch<T>(p, G)) != hipSuccess) return e;
   // The last pass stores dx rows 0 .. T-1-kofs of its taps kofs ..; the rows
   // after those (no terms of its taps) are rounded from the accumulator here
   // (passes that split only the ranks have kofs 0: nothing left).

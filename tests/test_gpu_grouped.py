@@ -325,7 +325,9 @@ HEAD_CASES = [
     (3, 2, 60, 256, 15, 20, True, 64, torch.bfloat16, True),   # W 20, one rank chunk: forward in one pass
     (3, 2, 60, 256, 31, 20, True, 64, torch.bfloat16, True),   # W 20, two chunks: the second forward pass adds to y
     (2, 1, 40, 128, 63, 12, True, 64, torch.float16, True),    # kernel rank 64, W 12: forward passes 4 + 8
-    (3, 2, 60, 256, 127, 4, True, 64, torch.bfloat16, True),   # kernel rank 128: the second rank pass adds to y
+    # kernel rank 128: the second rank pass adds to y; head-major dy takes the backward's fp32 dx
+    # accumulator, [B, T, D] dy the one-launch dx over all ranks (both round dx once: not bitwise)
+    (3, 2, 60, 256, 127, 4, True, 64, torch.bfloat16, False),
     (2, 2, 45, 128, 15, 12, True, 64, torch.float32, True),    # fp32 W 12: forward passes 4 + 8
     (2, 1, 40, 128, 15, 36, True, 64, torch.bfloat16, False),  # W 36: generic kernels, head-major y
 ]
